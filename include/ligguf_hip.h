@@ -1,0 +1,196 @@
+/* ligguf_hip.h -- C-ABI of the gfx950 (MI355X) decode path of LiGGUF FAST.
+ *
+ * libligguf_hip.so replaces the hot paths of the reference's math layer
+ * (fast/lil_math.h:5-39, fast/lil_math.cpp, fast/arch_avx2.h) and the inline
+ * per-token sequence of inference() (fast/ligguf_fast_qk.cpp:24-144).  The
+ * reference's host code -- GGUF loader, tokenizer, samplers, chat and state
+ * save -- keeps running on the CPU and calls this layer; the maintainer-side
+ * binding is shown in INTEGRATION.md.
+ *
+ * Conventions
+ *   - Every entry point returns LG_OK (0) or a negative LG_ERR_* code and
+ *     never aborts (the reference aborts on unsupported types,
+ *     fast/lil_math.cpp:313-315,771-773, and asserts shapes, :360,752,903).
+ *     The message of the last failure is lg_last_error(ctx), or
+ *     lg_last_error(NULL) for the per-op calls, which keep it per host thread.
+ *   - Weight type codes are the reference's gguf_type values
+ *     (fast/lil_gguf.h:26-43).  Block layouts are the GGUF ones
+ *     (fast/lil_gguf.h:64-119): weights are consumed as stored, rows of rsz
+ *     bytes (wtensor, fast/lil_gguf.h:126-130).
+ *   - Per-op calls take device pointers and a HIP stream passed as void*
+ *     (NULL = the default stream); they are asynchronous.
+ *   - A context owns one device, one stream and the uploaded model; it is not
+ *     thread-safe (the reference's op layer is not reentrant either: global
+ *     g_m and the static m_xq8, fast/lil_math.cpp:13).
+ */
+#ifndef LIGGUF_HIP_H
+#define LIGGUF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define LG_OK 0
+#define LG_ERR_ARG (-1)      /* bad argument, shape or size */
+#define LG_ERR_TYPE (-2)     /* unsupported tensor type */
+#define LG_ERR_HIP (-3)      /* HIP runtime error */
+#define LG_ERR_STATE (-4)    /* call out of order (no model, context full ...) */
+#define LG_ERR_NOMEM (-5)    /* device allocation failed */
+
+/* ---- tensor types: gguf_type (fast/lil_gguf.h:26-43) ---- */
+enum lg_type {
+    LG_F32 = 0, LG_F16 = 1, LG_Q8_0 = 8, LG_Q2_K = 10, LG_Q3_K = 11, LG_Q4_K = 12,
+    LG_Q5_K = 13, LG_Q6_K = 14, LG_Q8_K = 15, LG_Q1_0 = 40, LG_Q1_G = 41
+};
+
+enum lg_arch { LG_ARCH_LLAMA = 0, LG_ARCH_QWEN3 = 1 };
+
+/* Bytes of one row of n values of type t (row_size, fast/lil_gguf.cpp:190-225),
+ * or -1 when n does not fit the block size.  Q8_K is the activation format
+ * (block_q8_K, fast/lil_gguf.h:115-119). */
+int64_t lg_row_size(int type, int64_t n);
+
+/* ===================================================================== */
+/* Context and model                                                      */
+/* ===================================================================== */
+typedef struct lg_ctx lg_ctx;
+
+/* Open device `device` (HIP ordinal).  Replaces nothing in the reference,
+ * whose state is the global model_state g_m (fast/common.h:33-72). */
+int lg_create(int device, lg_ctx** out);
+int lg_destroy(lg_ctx* ctx);
+const char* lg_last_error(const lg_ctx* ctx);
+
+/* One weight matrix in host memory: the reference's wtensor
+ * {ptr, type, rsz} (fast/lil_gguf.h:126-130) plus its shape. */
+typedef struct {
+    const void* data;   /* host pointer to rows * rsz bytes */
+    int32_t type;       /* lg_type */
+    uint32_t rsz;       /* bytes per row */
+    int32_t rows;       /* output width d */
+    int32_t cols;       /* input width n */
+} lg_weight;
+
+/* One transformer block: trans_block (fast/lil_gguf.h:132-144).  Norm
+ * vectors are F32 host arrays (n_embed, or head_dim for the Qwen3 QK norms). */
+typedef struct {
+    const float* att_norm;
+    lg_weight att_q, att_k, att_v, att_out;
+    const float* att_q_norm;    /* qwen3 only */
+    const float* att_k_norm;    /* qwen3 only */
+    const float* ffn_norm;
+    lg_weight ffn_up, ffn_down, ffn_gate;
+} lg_layer_desc;
+
+/* The model: the fields of gguf_model the decode path reads
+ * (fast/lil_gguf.h:161-219) plus the host RoPE table of
+ * model_state::allocate (fast/common.cpp:38-39), uploaded as is so the
+ * device uses bit-identical frequencies. */
+typedef struct {
+    int32_t arch;               /* lg_arch */
+    int32_t n_layers, n_embed, n_heads, n_kv_heads, head_dim, kv_dim, n_ff, vocab_size, n_context, rope_dim;
+    float rms_epsilon;
+    const float* rope_freq;     /* rope_dim/2 floats */
+    lg_weight token_embd, output;
+    const float* output_norm;
+    const lg_layer_desc* layers;  /* n_layers entries */
+} lg_model_desc;
+
+/* Copy the model into HBM (weights, norms, RoPE table) and allocate the fp16
+ * KV cache [n_layers][n_context][kv_dim] (fast/common.cpp:31-32) plus the
+ * activation buffers.  The host memory can be released afterwards. */
+int lg_load_model(lg_ctx* ctx, const lg_model_desc* desc);
+
+/* inference(tok) at position pos (fast/ligguf_fast_qk.cpp:24-144): the whole
+ * layer loop on the device, KV row pos written, logits[vocab] copied to
+ * logits_host when it is not NULL.  Synchronous on return. */
+int lg_decode_step(lg_ctx* ctx, int tok, int pos, float* logits_host);
+
+/* Same as lg_decode_step but leaves the logits on the device (returned via
+ * lg_logits_device) and does not wait: the caller synchronises with
+ * lg_sync.  Lets a driver keep the decode loop free of host round trips. */
+int lg_decode_step_async(lg_ctx* ctx, int tok, int pos);
+int lg_sync(lg_ctx* ctx);
+const float* lg_logits_device(lg_ctx* ctx);
+
+/* Greedy argmax of the current device logits, first index wins ties
+ * (sampler_greedy, fast/ligguf_fast_qk.cpp:146-160). */
+int lg_argmax(lg_ctx* ctx, int* tok_out);
+
+/* feed_text's prompt loop (fast/ligguf_fast_qk.cpp:340-356): n tokens at
+ * positions pos0..pos0+n-1, equal to n sequential lg_decode_step calls;
+ * logits of the last token to logits_host (NULL allowed). */
+int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* logits_host);
+
+/* fp16 KV rows [pos0, pos0+npos) of layers [layer0, layer0+nlayers) to/from
+ * host arrays laid out [nlayers][npos][kv_dim] -- the per-layer blocks of the
+ * reference's state file (save/load_model_state,
+ * fast/ligguf_fast_qk.cpp:216-302). */
+int lg_kv_read(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, uint16_t* k_host, uint16_t* v_host);
+int lg_kv_write(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, const uint16_t* k_host,
+                const uint16_t* v_host);
+
+/* ===================================================================== */
+/* Per-op entry points (device pointers, asynchronous on `stream`)        */
+/* ===================================================================== */
+
+/* dequantize_row (fast/lil_math.cpp:300-317): n values of `type` at x to
+ * fp32 y; bit-identical to the reference. */
+int lg_dequantize_row(int type, const void* x, float* y, int64_t n, void* stream);
+
+/* quantize_q8_0 (fast/lil_math.cpp:329-351): n % 32 == 0, y gets n/32 blocks
+ * of 34 B; bit-identical to the reference as compiled. */
+int lg_quantize_q8_0(const float* x, int64_t n, void* y, void* stream);
+
+/* quantize_q8_K (fast/lil_math.cpp:358-394): n % 256 == 0, y gets n/256
+ * blocks of 292 B; bit-identical to the reference as compiled. */
+int lg_quantize_q8_K(const float* x, int64_t n, void* y, void* stream);
+
+/* matmul (fast/lil_math.cpp:748-776) on a pre-quantized activation:
+ * out[r] = row r of w . x for r < d, n = input width.  xq holds Q8_0 blocks
+ * for Q8_0/Q1_0/Q1_G weights, Q8_K blocks for Q2_K..Q6_K, and n fp32 values
+ * for F32/F16 weights.  accumulate != 0 adds into out (the residual adds of
+ * fast/ligguf_fast_qk.cpp:111,131). */
+int lg_matvec(int type, const void* w, uint32_t rsz, int n, int d, const void* xq, float* out, int accumulate,
+              void* stream);
+
+/* rmsnorm (fast/lil_math.cpp:922-929) fused with the activation quantizer
+ * that follows it in inference() (:37-39): out_q gets Q8_K (qtype LG_Q8_K),
+ * Q8_0 (LG_Q8_0) blocks, or with qtype LG_F32 the fp32 normalised vector.
+ * out_f (optional) also receives the fp32 normalised vector. */
+int lg_rmsnorm_quant(const float* x, const float* w, int n, float eps, int qtype, void* out_q, float* out_f,
+                     void* stream);
+
+/* Qwen3 per-head QK RMSNorm (fast/ligguf_fast_qk.cpp:42-51, qw/kw may be
+ * NULL to skip), adjacent-pair RoPE (fast/lil_math.cpp:901-920) at `pos`,
+ * and the fp16 KV write of the new row (fast/ligguf_fast_qk.cpp:57-62).
+ * q [n_heads*head_dim] and k [kv_dim] are updated in place; kc_row/vc_row
+ * (may be NULL) receive fp16(k), fp16(v). */
+int lg_qk_norm_rope_kv(float* q, float* k, const float* v, const float* qw, const float* kw, int n_heads,
+                       int n_kv_heads, int head_dim, int rope_dim, int pos, const float* freq, float eps,
+                       uint16_t* kc_row, uint16_t* vc_row, void* stream);
+
+/* GQA decode attention (fast/ligguf_fast_qk.cpp:64-105), split over the
+ * sequence: out[n_heads*head_dim] = softmax(q.K^T/sqrt(hd)) V for t <= pos,
+ * rows t < pos from the fp16 caches kc/vc ([pos][kv_dim] rows of this
+ * layer), row pos from the fp32 k/v.  workspace must hold
+ * lg_attn_workspace_size(...) bytes. */
+size_t lg_attn_workspace_size(int n_heads, int head_dim, int pos);
+int lg_attn_decode(const float* q, const float* k, const float* v, const uint16_t* kc, const uint16_t* vc,
+                   int n_heads, int n_kv_heads, int head_dim, int pos, float* out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* SwiGLU of fast/ligguf_fast_qk.cpp:119-123, hb[i] = silu(hb2[i]) * hb[i],
+ * fused with the activation quantizer of :126 (qtype as lg_rmsnorm_quant;
+ * out_q may be NULL when only hb is wanted). */
+int lg_swiglu_quant(float* hb, const float* hb2, int n, int qtype, void* out_q, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIGGUF_HIP_H */

@@ -1,0 +1,634 @@
+/* lg_engine.hip -- context, model upload, the per-token decode step and the
+ * C-ABI entry points of include/ligguf_hip.h.
+ *
+ * The step is the sequence of inference() (fast/ligguf_fast_qk.cpp:24-144)
+ * with the math on the device:
+ *   embed -> per layer { rmsnorm+quant -> QKV matvec -> QK-norm/RoPE/KV write
+ *   -> split-K attention -> quant -> att_out matvec (+residual) ->
+ *   rmsnorm+quant -> up|gate matvec -> SwiGLU+quant -> down matvec
+ *   (+residual) } -> rmsnorm+quant -> output matvec.
+ * Q|K|V and up|gate are uploaded as one matrix each when their types agree
+ * (the fused row loops of matmul3/matmul2, fast/lil_math.cpp:779-899).
+ *
+ * Device layout (HBM): weights as stored in GGUF rows; the fp16 KV cache
+ * [n_layers][n_context][kv_dim] as model_state (fast/common.cpp:31-32);
+ * fp32 activations x, q|k|v, att, hb|hb2, logits; quantized activations
+ * in Q8_K and/or Q8_0 form.
+ */
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "lg_common.h"
+
+/* ------------------------------------------------------------------ */
+/* errors                                                               */
+/* ------------------------------------------------------------------ */
+static thread_local char g_err[1024];
+
+void lg_set_error(const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+const char* lg_get_thread_error(void) { return g_err; }
+
+int lg_check_launch(const char* what)
+{
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        lg_set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+        return LG_ERR_HIP;
+    }
+    return LG_OK;
+}
+
+extern "C" int64_t lg_row_size(int type, int64_t n)
+{
+    if (n < 0) return -1;
+    switch (type) {
+    case LG_F32: return 4 * n;
+    case LG_F16: return 2 * n;
+    case LG_Q8_0: return n % 32 ? -1 : n / 32 * LG_BS_Q8_0;
+    case LG_Q1_0: return n % 32 ? -1 : n / 32 * LG_BS_Q1_0;
+    case LG_Q1_G: return n % 128 ? -1 : n / 128 * LG_BS_Q1_G;
+    case LG_Q2_K: return n % 256 ? -1 : n / 256 * LG_BS_Q2_K;
+    case LG_Q3_K: return n % 256 ? -1 : n / 256 * LG_BS_Q3_K;
+    case LG_Q4_K: return n % 256 ? -1 : n / 256 * LG_BS_Q4_K;
+    case LG_Q5_K: return n % 256 ? -1 : n / 256 * LG_BS_Q5_K;
+    case LG_Q6_K: return n % 256 ? -1 : n / 256 * LG_BS_Q6_K;
+    case LG_Q8_K: return n % 256 ? -1 : n / 256 * LG_BS_Q8_K;
+    default: return -1;
+    }
+}
+
+/* activation family a weight type consumes */
+enum { ACT_K = 1, ACT_80 = 2, ACT_F = 4 };
+static int act_family(int type)
+{
+    switch (type) {
+    case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: return ACT_K;
+    case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: return ACT_80;
+    case LG_F32: case LG_F16: return ACT_F;
+    default: return 0;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* context                                                              */
+/* ------------------------------------------------------------------ */
+struct dweight {
+    uint8_t* data = nullptr;
+    int type = -1;
+    uint32_t rsz = 0;
+    int rows = 0, cols = 0;
+};
+
+struct dlayer {
+    float *att_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
+    dweight q, k, v;        /* views into qkv when fused */
+    bool qkv_fused = false;
+    dweight qkv;
+    dweight att_out;
+    dweight up, gate;
+    bool ug_fused = false;
+    dweight ug;
+    dweight down;
+};
+
+struct lg_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    char err[1024] = {0};
+    std::vector<void*> allocs;
+
+    bool loaded = false;
+    int arch = 0, n_layers = 0, n_embed = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, kv_dim = 0, n_ff = 0;
+    int vocab = 0, n_context = 0, rope_dim = 0;
+    float eps = 0.0f;
+    std::vector<dlayer> layers;
+    dweight embd, output;
+    float* out_norm = nullptr;
+    float* rope_freq = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *hb = nullptr, *logits = nullptr, *xf = nullptr;
+    uint8_t *xqk = nullptr, *xq0 = nullptr;
+    float* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    int* argmax_dev = nullptr;
+};
+
+static int ctx_fail(lg_ctx* ctx, int rc)
+{
+    if (ctx && rc != LG_OK) snprintf(ctx->err, sizeof(ctx->err), "%s", g_err);
+    return rc;
+}
+
+static int dalloc(lg_ctx* ctx, void** p, size_t bytes)
+{
+    const hipError_t e = hipMalloc(p, bytes ? bytes : 16);
+    if (e != hipSuccess) {
+        lg_set_error("hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+        return LG_ERR_NOMEM;
+    }
+    ctx->allocs.push_back(*p);
+    return LG_OK;
+}
+
+static void free_model(lg_ctx* ctx)
+{
+    for (void* p : ctx->allocs) hipFree(p);
+    ctx->allocs.clear();
+    ctx->layers.clear();
+    ctx->loaded = false;
+}
+
+extern "C" int lg_create(int device, lg_ctx** out)
+{
+    if (!out) { lg_set_error("lg_create: null output"); return LG_ERR_ARG; }
+    *out = nullptr;
+    int n = 0;
+    LG_HIP_CHECK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) { lg_set_error("lg_create: device %d of %d", device, n); return LG_ERR_ARG; }
+    LG_HIP_CHECK(hipSetDevice(device));
+    lg_ctx* ctx = new lg_ctx();
+    ctx->device = device;
+    const hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        lg_set_error("hipStreamCreate failed: %s", hipGetErrorString(e));
+        delete ctx;
+        return LG_ERR_HIP;
+    }
+    *out = ctx;
+    return LG_OK;
+}
+
+extern "C" int lg_destroy(lg_ctx* ctx)
+{
+    if (!ctx) return LG_OK;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    free_model(ctx);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return LG_OK;
+}
+
+extern "C" const char* lg_last_error(const lg_ctx* ctx) { return ctx ? ctx->err : g_err; }
+
+/* ------------------------------------------------------------------ */
+/* model upload                                                         */
+/* ------------------------------------------------------------------ */
+static int check_weight(const lg_weight& w, int rows, int cols, const char* name)
+{
+    if (!w.data) { lg_set_error("load_model: %s missing", name); return LG_ERR_ARG; }
+    if (w.rows != rows || w.cols != cols) {
+        lg_set_error("load_model: %s is %dx%d, expected %dx%d", name, w.rows, w.cols, rows, cols);
+        return LG_ERR_ARG;
+    }
+    if (!act_family(w.type)) { lg_set_error("load_model: %s has unsupported type %d", name, w.type); return LG_ERR_TYPE; }
+    const int64_t need = lg_row_size(w.type, cols);
+    if (need < 0 || (int64_t)w.rsz < need) { lg_set_error("load_model: %s row size %u (type %d needs %lld)", name, w.rsz, w.type, (long long)need); return LG_ERR_ARG; }
+    return LG_OK;
+}
+
+static int upload_weight(lg_ctx* ctx, const lg_weight& w, dweight& d)
+{
+    const size_t bytes = (size_t)w.rows * w.rsz;
+    int rc = dalloc(ctx, (void**)&d.data, bytes);
+    if (rc) return rc;
+    LG_HIP_CHECK(hipMemcpy(d.data, w.data, bytes, hipMemcpyHostToDevice));
+    d.type = w.type; d.rsz = w.rsz; d.rows = w.rows; d.cols = w.cols;
+    return LG_OK;
+}
+
+/* stack matrices of one type and row size into one device matrix */
+static int upload_stacked(lg_ctx* ctx, const lg_weight* const* ws, int n, dweight& out, dweight* views)
+{
+    size_t bytes = 0;
+    int rows = 0;
+    for (int i = 0; i < n; i++) { bytes += (size_t)ws[i]->rows * ws[i]->rsz; rows += ws[i]->rows; }
+    int rc = dalloc(ctx, (void**)&out.data, bytes);
+    if (rc) return rc;
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        const size_t b = (size_t)ws[i]->rows * ws[i]->rsz;
+        LG_HIP_CHECK(hipMemcpy(out.data + off, ws[i]->data, b, hipMemcpyHostToDevice));
+        views[i].data = out.data + off;
+        views[i].type = ws[i]->type; views[i].rsz = ws[i]->rsz; views[i].rows = ws[i]->rows; views[i].cols = ws[i]->cols;
+        off += b;
+    }
+    out.type = ws[0]->type; out.rsz = ws[0]->rsz; out.rows = rows; out.cols = ws[0]->cols;
+    return LG_OK;
+}
+
+static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const char* name)
+{
+    if (!h) { lg_set_error("load_model: %s missing", name); return LG_ERR_ARG; }
+    int rc = dalloc(ctx, (void**)d, n * sizeof(float));
+    if (rc) return rc;
+    LG_HIP_CHECK(hipMemcpy(*d, h, n * sizeof(float), hipMemcpyHostToDevice));
+    return LG_OK;
+}
+
+static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
+{
+    if (!m || !m->layers) { lg_set_error("load_model: null descriptor"); return LG_ERR_ARG; }
+    if (m->arch != LG_ARCH_LLAMA && m->arch != LG_ARCH_QWEN3) { lg_set_error("load_model: arch %d unsupported", m->arch); return LG_ERR_ARG; }
+    if (m->n_layers <= 0 || m->n_embed <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 || m->head_dim <= 0 ||
+        m->n_ff <= 0 || m->vocab_size <= 0 || m->n_context <= 0 || m->n_heads % m->n_kv_heads ||
+        m->kv_dim != m->n_kv_heads * m->head_dim || m->n_heads * m->head_dim != m->n_embed) {
+        /* q and the attention output are n_embed wide in the reference
+         * (fast/common.cpp:28, fast/ligguf_fast_qk.cpp:40,109) */
+        lg_set_error("load_model: inconsistent dimensions");
+        return LG_ERR_ARG;
+    }
+    if (m->n_embed % 32 || m->n_ff % 32 || m->head_dim % 4 || m->head_dim > 256) {
+        lg_set_error("load_model: n_embed/n_ff must be multiples of 32 and head_dim a multiple of 4 up to 256");
+        return LG_ERR_ARG;
+    }
+    if (m->rope_dim > 0 && !m->rope_freq) { lg_set_error("load_model: rope_freq missing"); return LG_ERR_ARG; }
+    int rc;
+    if ((rc = check_weight(m->token_embd, m->token_embd.rows, m->n_embed, "token_embd"))) return rc;
+    if ((rc = check_weight(m->output, m->vocab_size, m->n_embed, "output"))) return rc;
+    for (int l = 0; l < m->n_layers; l++) {
+        const lg_layer_desc& L = m->layers[l];
+        if ((rc = check_weight(L.att_q, m->n_embed, m->n_embed, "attn_q"))) return rc;
+        if ((rc = check_weight(L.att_k, m->kv_dim, m->n_embed, "attn_k"))) return rc;
+        if ((rc = check_weight(L.att_v, m->kv_dim, m->n_embed, "attn_v"))) return rc;
+        if ((rc = check_weight(L.att_out, m->n_embed, m->n_embed, "attn_output"))) return rc;
+        if ((rc = check_weight(L.ffn_up, m->n_ff, m->n_embed, "ffn_up"))) return rc;
+        if ((rc = check_weight(L.ffn_gate, m->n_ff, m->n_embed, "ffn_gate"))) return rc;
+        if ((rc = check_weight(L.ffn_down, m->n_embed, m->n_ff, "ffn_down"))) return rc;
+        if (!L.att_norm || !L.ffn_norm) { lg_set_error("load_model: layer %d norms missing", l); return LG_ERR_ARG; }
+        if (m->arch == LG_ARCH_QWEN3 && (!L.att_q_norm || !L.att_k_norm)) { lg_set_error("load_model: layer %d QK norms missing", l); return LG_ERR_ARG; }
+    }
+    /* K-quant activations need 256-wide blocks (quantize_q8_K asserts it,
+     * fast/lil_math.cpp:360) */
+    auto needs_k = [&](int n, int t) { return act_family(t) == ACT_K && n % 256; };
+    for (int l = 0; l < m->n_layers; l++) {
+        const lg_layer_desc& L = m->layers[l];
+        if (needs_k(m->n_embed, L.att_q.type) || needs_k(m->n_embed, L.att_k.type) || needs_k(m->n_embed, L.att_v.type) ||
+            needs_k(m->n_embed, L.att_out.type) || needs_k(m->n_embed, L.ffn_up.type) ||
+            needs_k(m->n_embed, L.ffn_gate.type) || needs_k(m->n_ff, L.ffn_down.type)) {
+            lg_set_error("load_model: K-quant weights need widths that are multiples of 256");
+            return LG_ERR_ARG;
+        }
+    }
+
+    free_model(ctx);
+    ctx->arch = m->arch; ctx->n_layers = m->n_layers; ctx->n_embed = m->n_embed; ctx->n_heads = m->n_heads;
+    ctx->n_kv_heads = m->n_kv_heads; ctx->head_dim = m->head_dim; ctx->kv_dim = m->kv_dim; ctx->n_ff = m->n_ff;
+    ctx->vocab = m->vocab_size; ctx->n_context = m->n_context; ctx->rope_dim = m->rope_dim; ctx->eps = m->rms_epsilon;
+
+    if ((rc = upload_weight(ctx, m->token_embd, ctx->embd))) return rc;
+    if ((rc = upload_weight(ctx, m->output, ctx->output))) return rc;
+    if ((rc = upload_floats(ctx, m->output_norm, m->n_embed, &ctx->out_norm, "output_norm"))) return rc;
+    const int nfreq = m->rope_dim / 2 > 0 ? m->rope_dim / 2 : 1;
+    if (m->rope_dim > 0) {
+        if ((rc = upload_floats(ctx, m->rope_freq, nfreq, &ctx->rope_freq, "rope_freq"))) return rc;
+    }
+    ctx->layers.resize(m->n_layers);
+    for (int l = 0; l < m->n_layers; l++) {
+        const lg_layer_desc& L = m->layers[l];
+        dlayer& D = ctx->layers[l];
+        if ((rc = upload_floats(ctx, L.att_norm, m->n_embed, &D.att_norm, "attn_norm"))) return rc;
+        if ((rc = upload_floats(ctx, L.ffn_norm, m->n_embed, &D.ffn_norm, "ffn_norm"))) return rc;
+        if (m->arch == LG_ARCH_QWEN3) {
+            if ((rc = upload_floats(ctx, L.att_q_norm, m->head_dim, &D.q_norm, "attn_q_norm"))) return rc;
+            if ((rc = upload_floats(ctx, L.att_k_norm, m->head_dim, &D.k_norm, "attn_k_norm"))) return rc;
+        }
+        if (L.att_q.type == L.att_k.type && L.att_q.type == L.att_v.type && L.att_q.rsz == L.att_k.rsz &&
+            L.att_q.rsz == L.att_v.rsz) {
+            const lg_weight* ws[3] = {&L.att_q, &L.att_k, &L.att_v};
+            dweight views[3];
+            if ((rc = upload_stacked(ctx, ws, 3, D.qkv, views))) return rc;
+            D.q = views[0]; D.k = views[1]; D.v = views[2];
+            D.qkv_fused = true;
+        } else {
+            if ((rc = upload_weight(ctx, L.att_q, D.q))) return rc;
+            if ((rc = upload_weight(ctx, L.att_k, D.k))) return rc;
+            if ((rc = upload_weight(ctx, L.att_v, D.v))) return rc;
+        }
+        if ((rc = upload_weight(ctx, L.att_out, D.att_out))) return rc;
+        if (L.ffn_up.type == L.ffn_gate.type && L.ffn_up.rsz == L.ffn_gate.rsz) {
+            const lg_weight* ws[2] = {&L.ffn_up, &L.ffn_gate};
+            dweight views[2];
+            if ((rc = upload_stacked(ctx, ws, 2, D.ug, views))) return rc;
+            D.up = views[0]; D.gate = views[1];
+            D.ug_fused = true;
+        } else {
+            if ((rc = upload_weight(ctx, L.ffn_up, D.up))) return rc;
+            if ((rc = upload_weight(ctx, L.ffn_gate, D.gate))) return rc;
+        }
+        if ((rc = upload_weight(ctx, L.ffn_down, D.down))) return rc;
+    }
+
+    const size_t kvn = (size_t)m->n_layers * m->n_context * m->kv_dim;
+    if ((rc = dalloc(ctx, (void**)&ctx->kc, kvn * 2))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->vc, kvn * 2))) return rc;
+    LG_HIP_CHECK(hipMemset(ctx->kc, 0, kvn * 2));
+    LG_HIP_CHECK(hipMemset(ctx->vc, 0, kvn * 2));
+
+    const int wide = m->n_ff > m->n_embed ? m->n_ff : m->n_embed;
+    if ((rc = dalloc(ctx, (void**)&ctx->x, (size_t)m->n_embed * 4))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->qkv, (size_t)(m->n_embed + 2 * m->kv_dim) * 4))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->att, (size_t)m->n_embed * 4))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->hb, (size_t)2 * m->n_ff * 4))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->logits, (size_t)m->vocab_size * 4))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->xf, (size_t)wide * 4))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->xqk, (size_t)(wide / 256 + 1) * LG_BS_Q8_K))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->xq0, (size_t)(wide / 32 + 8) * LG_BS_Q8_0))) return rc;
+    ctx->attn_ws_bytes = lg_attn_ws_bytes(m->n_heads, m->head_dim, m->n_context - 1);
+    if ((rc = dalloc(ctx, (void**)&ctx->attn_ws, ctx->attn_ws_bytes))) return rc;
+    if ((rc = dalloc(ctx, (void**)&ctx->argmax_dev, 16))) return rc;
+    LG_HIP_CHECK(hipDeviceSynchronize());
+    ctx->loaded = true;
+    return LG_OK;
+}
+
+extern "C" int lg_load_model(lg_ctx* ctx, const lg_model_desc* desc)
+{
+    if (!ctx) { lg_set_error("lg_load_model: null context"); return LG_ERR_ARG; }
+    hipSetDevice(ctx->device);
+    const int rc = load_model_impl(ctx, desc);
+    if (rc) free_model(ctx);
+    return ctx_fail(ctx, rc);
+}
+
+/* ------------------------------------------------------------------ */
+/* the step                                                             */
+/* ------------------------------------------------------------------ */
+
+/* quantized forms of the activation for the weights in `fam` */
+struct actbufs {
+    const void* k;
+    const void* q0;
+    const float* f;
+};
+
+static int prep_norm(lg_ctx* c, const float* x, const float* w, int n, int fam, actbufs& a)
+{
+    int rc;
+    a.k = c->xqk; a.q0 = c->xq0; a.f = c->xf;
+    if (fam & ACT_K) if ((rc = lg_launch_rmsnorm_quant(x, w, n, c->eps, LG_Q8_K, c->xqk, (fam & ACT_F) ? c->xf : nullptr, c->stream))) return rc;
+    if (fam & ACT_80) if ((rc = lg_launch_rmsnorm_quant(x, w, n, c->eps, LG_Q8_0, c->xq0, (fam & ACT_F) && !(fam & ACT_K) ? c->xf : nullptr, c->stream))) return rc;
+    if (fam == ACT_F) if ((rc = lg_launch_rmsnorm_quant(x, w, n, c->eps, LG_F32, nullptr, c->xf, c->stream))) return rc;
+    return LG_OK;
+}
+
+static int prep_plain(lg_ctx* c, const float* x, int n, int fam, actbufs& a)
+{
+    int rc;
+    a.k = c->xqk; a.q0 = c->xq0; a.f = x;
+    if (fam & ACT_K) if ((rc = lg_launch_quantize_q8_K(x, n, c->xqk, c->stream))) return rc;
+    if (fam & ACT_80) if ((rc = lg_launch_quantize_q8_0(x, n, c->xq0, c->stream))) return rc;
+    return LG_OK;
+}
+
+static const void* act_for(const actbufs& a, int type)
+{
+    const int f = act_family(type);
+    return f == ACT_K ? a.k : (f == ACT_80 ? a.q0 : (const void*)a.f);
+}
+
+static int mv(lg_ctx* c, const dweight& w, const actbufs& a, float* out, int acc)
+{
+    return lg_launch_matvec(w.type, w.data, w.rsz, w.cols, w.rows, act_for(a, w.type), out, acc, c->stream);
+}
+
+static int enqueue_step(lg_ctx* c, int tok, int pos)
+{
+    int rc;
+    const int ne = c->n_embed, kvd = c->kv_dim;
+    float* q = c->qkv;
+    float* k = c->qkv + ne;
+    float* v = c->qkv + ne + kvd;
+    if ((rc = lg_launch_embed(c->embd.type, c->embd.data, c->embd.rsz, nullptr, tok, ne, c->x, c->stream))) return rc;
+    for (int l = 0; l < c->n_layers; l++) {
+        const dlayer& L = c->layers[l];
+        actbufs a;
+        /* attention branch */
+        const int fam_qkv = act_family(L.q.type) | act_family(L.k.type) | act_family(L.v.type);
+        if ((rc = prep_norm(c, c->x, L.att_norm, ne, fam_qkv, a))) return rc;
+        if (L.qkv_fused) {
+            if ((rc = mv(c, L.qkv, a, c->qkv, 0))) return rc;
+        } else {
+            if ((rc = mv(c, L.q, a, q, 0))) return rc;
+            if ((rc = mv(c, L.k, a, k, 0))) return rc;
+            if ((rc = mv(c, L.v, a, v, 0))) return rc;
+        }
+        const size_t loff = (size_t)l * c->n_context * kvd;
+        uint16_t* kc = c->kc + loff;
+        uint16_t* vc = c->vc + loff;
+        if ((rc = lg_launch_qk_norm_rope_kv(q, k, v, L.q_norm, L.k_norm, c->n_heads, c->n_kv_heads, c->head_dim,
+                                            c->rope_dim, pos, c->rope_freq, c->eps, kc + (size_t)pos * kvd,
+                                            vc + (size_t)pos * kvd, c->stream)))
+            return rc;
+        if ((rc = lg_launch_attn(q, k, v, kc, vc, c->n_heads, c->n_kv_heads, c->head_dim, pos, c->att, c->attn_ws,
+                                 c->attn_ws_bytes, c->stream)))
+            return rc;
+        if ((rc = prep_plain(c, c->att, ne, act_family(L.att_out.type), a))) return rc;
+        if ((rc = mv(c, L.att_out, a, c->x, 1))) return rc;
+        /* FFN branch */
+        const int fam_ug = act_family(L.up.type) | act_family(L.gate.type);
+        if ((rc = prep_norm(c, c->x, L.ffn_norm, ne, fam_ug, a))) return rc;
+        float* hb = c->hb;
+        float* hb2 = c->hb + c->n_ff;
+        if (L.ug_fused) {
+            if ((rc = mv(c, L.ug, a, hb, 0))) return rc;
+        } else {
+            if ((rc = mv(c, L.up, a, hb, 0))) return rc;
+            if ((rc = mv(c, L.gate, a, hb2, 0))) return rc;
+        }
+        const int fam_d = act_family(L.down.type);
+        if (fam_d == ACT_K) {
+            if ((rc = lg_launch_swiglu_quant(hb, hb2, c->n_ff, LG_Q8_K, c->xqk, c->stream))) return rc;
+        } else if (fam_d == ACT_80) {
+            if ((rc = lg_launch_swiglu_quant(hb, hb2, c->n_ff, LG_Q8_0, c->xq0, c->stream))) return rc;
+        } else {
+            if ((rc = lg_launch_swiglu_quant(hb, hb2, c->n_ff, LG_F32, nullptr, c->stream))) return rc;
+        }
+        a.k = c->xqk; a.q0 = c->xq0; a.f = hb;
+        if ((rc = mv(c, L.down, a, c->x, 1))) return rc;
+    }
+    actbufs a;
+    if ((rc = prep_norm(c, c->x, c->out_norm, ne, act_family(c->output.type), a))) return rc;
+    if ((rc = mv(c, c->output, a, c->logits, 0))) return rc;
+    return LG_OK;
+}
+
+static int step_checks(lg_ctx* ctx, int tok, int pos)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return LG_ERR_STATE; }
+    if (pos < 0 || pos >= ctx->n_context) { lg_set_error("position %d outside the context of %d", pos, ctx->n_context); return LG_ERR_STATE; }
+    if (tok < 0 || tok >= ctx->embd.rows) { lg_set_error("token %d outside the vocabulary of %d", tok, ctx->embd.rows); return LG_ERR_ARG; }
+    return LG_OK;
+}
+
+extern "C" int lg_decode_step_async(lg_ctx* ctx, int tok, int pos)
+{
+    int rc = step_checks(ctx, tok, pos);
+    if (rc) return ctx_fail(ctx, rc);
+    hipSetDevice(ctx->device);
+    return ctx_fail(ctx, enqueue_step(ctx, tok, pos));
+}
+
+extern "C" int lg_sync(lg_ctx* ctx)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        lg_set_error("stream synchronize: %s", hipGetErrorString(e));
+        return ctx_fail(ctx, LG_ERR_HIP);
+    }
+    return LG_OK;
+}
+
+extern "C" const float* lg_logits_device(lg_ctx* ctx) { return ctx && ctx->loaded ? ctx->logits : nullptr; }
+
+extern "C" int lg_decode_step(lg_ctx* ctx, int tok, int pos, float* logits_host)
+{
+    int rc = lg_decode_step_async(ctx, tok, pos);
+    if (rc) return rc;
+    if (logits_host) {
+        const hipError_t e = hipMemcpyAsync(logits_host, ctx->logits, (size_t)ctx->vocab * 4, hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) { lg_set_error("logits copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
+    }
+    return lg_sync(ctx);
+}
+
+extern "C" int lg_argmax(lg_ctx* ctx, int* tok_out)
+{
+    if (!ctx || !tok_out) { lg_set_error("lg_argmax: null argument"); return LG_ERR_ARG; }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    int rc = lg_launch_argmax(ctx->logits, ctx->vocab, ctx->argmax_dev, ctx->stream);
+    if (rc) return ctx_fail(ctx, rc);
+    const hipError_t e = hipMemcpyAsync(tok_out, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) { lg_set_error("argmax copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
+    return lg_sync(ctx);
+}
+
+extern "C" int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* logits_host)
+{
+    if (!ctx || !toks || n <= 0) { lg_set_error("lg_prefill: bad arguments"); return ctx_fail(ctx, LG_ERR_ARG); }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    if (pos0 < 0 || pos0 + n > ctx->n_context) { lg_set_error("prefill of %d tokens at %d exceeds the context of %d", n, pos0, ctx->n_context); return ctx_fail(ctx, LG_ERR_STATE); }
+    for (int i = 0; i < n; i++) {
+        int rc = step_checks(ctx, toks[i], pos0 + i);
+        if (rc) return ctx_fail(ctx, rc);
+    }
+    hipSetDevice(ctx->device);
+    for (int i = 0; i < n; i++) {
+        int rc = enqueue_step(ctx, toks[i], pos0 + i);
+        if (rc) return ctx_fail(ctx, rc);
+    }
+    if (logits_host) {
+        const hipError_t e = hipMemcpyAsync(logits_host, ctx->logits, (size_t)ctx->vocab * 4, hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) { lg_set_error("logits copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
+    }
+    return lg_sync(ctx);
+}
+
+static int kv_io(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, uint16_t* kh, uint16_t* vh, bool write)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    if (layer0 < 0 || nlayers < 0 || layer0 + nlayers > ctx->n_layers || pos0 < 0 || npos < 0 ||
+        pos0 + npos > ctx->n_context) {
+        lg_set_error("kv range outside the cache");
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    hipSetDevice(ctx->device);
+    const size_t row = (size_t)ctx->kv_dim * 2;
+    for (int l = 0; l < nlayers; l++) {
+        const size_t doff = ((size_t)(layer0 + l) * ctx->n_context + pos0) * ctx->kv_dim;
+        const size_t hoff = (size_t)l * npos * ctx->kv_dim;
+        for (int q = 0; q < 2; q++) {
+            uint16_t* dev = (q ? ctx->vc : ctx->kc) + doff;
+            uint16_t* host = (q ? vh : kh);
+            if (!host) continue;
+            const hipError_t e = write ? hipMemcpyAsync(dev, host + hoff, row * npos, hipMemcpyHostToDevice, ctx->stream)
+                                       : hipMemcpyAsync(host + hoff, dev, row * npos, hipMemcpyDeviceToHost, ctx->stream);
+            if (e != hipSuccess) { lg_set_error("kv copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
+        }
+    }
+    return lg_sync(ctx);
+}
+
+extern "C" int lg_kv_read(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, uint16_t* k_host, uint16_t* v_host)
+{
+    return kv_io(ctx, layer0, nlayers, pos0, npos, k_host, v_host, false);
+}
+
+extern "C" int lg_kv_write(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, const uint16_t* k_host,
+                           const uint16_t* v_host)
+{
+    return kv_io(ctx, layer0, nlayers, pos0, npos, (uint16_t*)k_host, (uint16_t*)v_host, true);
+}
+
+/* ------------------------------------------------------------------ */
+/* per-op entry points                                                  */
+/* ------------------------------------------------------------------ */
+#define S(stream) ((hipStream_t)(stream))
+
+extern "C" int lg_dequantize_row(int type, const void* x, float* y, int64_t n, void* stream)
+{
+    return lg_launch_dequantize(type, x, y, n, S(stream));
+}
+
+extern "C" int lg_quantize_q8_0(const float* x, int64_t n, void* y, void* stream)
+{
+    return lg_launch_quantize_q8_0(x, n, y, S(stream));
+}
+
+extern "C" int lg_quantize_q8_K(const float* x, int64_t n, void* y, void* stream)
+{
+    return lg_launch_quantize_q8_K(x, n, y, S(stream));
+}
+
+extern "C" int lg_matvec(int type, const void* w, uint32_t rsz, int n, int d, const void* xq, float* out, int accumulate,
+                         void* stream)
+{
+    return lg_launch_matvec(type, w, rsz, n, d, xq, out, accumulate, S(stream));
+}
+
+extern "C" int lg_rmsnorm_quant(const float* x, const float* w, int n, float eps, int qtype, void* out_q, float* out_f,
+                                void* stream)
+{
+    return lg_launch_rmsnorm_quant(x, w, n, eps, qtype, out_q, out_f, S(stream));
+}
+
+extern "C" int lg_qk_norm_rope_kv(float* q, float* k, const float* v, const float* qw, const float* kw, int n_heads,
+                                  int n_kv_heads, int head_dim, int rope_dim, int pos, const float* freq, float eps,
+                                  uint16_t* kc_row, uint16_t* vc_row, void* stream)
+{
+    return lg_launch_qk_norm_rope_kv(q, k, v, qw, kw, n_heads, n_kv_heads, head_dim, rope_dim, pos, freq, eps, kc_row,
+                                     vc_row, S(stream));
+}
+
+extern "C" size_t lg_attn_workspace_size(int n_heads, int head_dim, int pos)
+{
+    return lg_attn_ws_bytes(n_heads, head_dim, pos);
+}
+
+extern "C" int lg_attn_decode(const float* q, const float* k, const float* v, const uint16_t* kc, const uint16_t* vc,
+                              int n_heads, int n_kv_heads, int head_dim, int pos, float* out, void* workspace,
+                              size_t workspace_bytes, void* stream)
+{
+    return lg_launch_attn(q, k, v, kc, vc, n_heads, n_kv_heads, head_dim, pos, out, workspace, workspace_bytes,
+                          S(stream));
+}
+
+extern "C" int lg_swiglu_quant(float* hb, const float* hb2, int n, int qtype, void* out_q, void* stream)
+{
+    return lg_launch_swiglu_quant(hb, hb2, n, qtype, out_q, S(stream));
+}

