@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Batch-1 decode throughput of a Qwen3-8B-shaped Q4_K model on one MI355X.
+
+Workload (one "step" = one greedy decode token, batch 1):
+  Qwen3-8B shape -- 36 layers, dim 4096, 32 query / 8 KV heads of 128,
+  per-head QK RMSNorm, SwiGLU FFN 12288, vocab 151936, RoPE theta 1e6 --
+  with synthetic N(0, 0.02) weights encoded to Q4_K (attention, FFN,
+  embedding) and Q6_K (output head), norms 1.0.  A 512-token random-id
+  prompt is prefilled first, then W warm-up and K timed greedy tokens run
+  through lg_decode_step + lg_argmax (the reference's inference() +
+  sampler_greedy loop, fast/ligguf_fast_qk.cpp:368-382).
+
+Prints one JSON line.  `value` is decode tokens/s with weights and KV
+resident in HBM.  `roofline` is for the dominant kernel (the fused up|gate
+Q4_K matvec, 24576 x 4096) timed with HIP events on its stream over
+rotating buffers larger than the 256 MB Infinity Cache; `cpu_baseline` is
+the reference FAST engine (built from its own sources, AVX2) decoding the
+same model on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def dominant_kernel_roofline(torch, rows: int, cols: int, reps: int = 200):
+    """Average duration of the Q4_K matvec at the fused up|gate shape, over
+    distinct weight buffers totalling > 512 MB, timed with HIP events on the
+    stream the kernel runs on."""
+    from ligguf_amd import ops
+    from ligguf_amd.lib import Q4_K, row_size
+    rsz = row_size(Q4_K, cols)
+    wbytes = rows * rsz
+    nbuf = max(2, (600 << 20) // wbytes + 1)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    bufs = [torch.randint(0, 256, (wbytes,), dtype=torch.uint8, device=dev, generator=g) for _ in range(nbuf)]
+    for b in bufs:     # finite fp16 scales: d, dmin = 2^-10 in every block header
+        v = b.view(-1, 144)
+        v[:, 0] = 0; v[:, 1] = 0x14; v[:, 2] = 0; v[:, 3] = 0x14
+    x = torch.randn(cols, device=dev)
+    xq = ops.quantize_q8_K(x)
+    out = torch.empty(rows, device=dev)
+    for i in range(10):
+        ops.matvec(Q4_K, bufs[i % nbuf], rsz, cols, rows, xq, out=out)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(reps):
+        ops.matvec(Q4_K, bufs[i % nbuf], rsz, cols, rows, xq, out=out)
+    e1.record(s)
+    torch.cuda.synchronize()
+    avg_s = e0.elapsed_time(e1) / 1e3 / reps
+    alg = wbytes + (cols // 256) * 292 + rows * 4      # weights + Q8_K activation + fp32 output
+    del bufs
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "achieved": round(alg / avg_s / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": round(alg / avg_s / HBM_PEAK, 4), "traffic": None,
+            "kernel": f"k_matvec<Q4_K> {rows}x{cols}", "avg_us": round(avg_s * 1e6, 3), "bytes_per_launch": alg,
+            "buffers_mb": round(nbuf * wbytes / 2 ** 20)}
+
+
+def cpu_baseline(hm, seconds: float, max_tokens: int = 64):
+    """The reference FAST engine (oracle/_ref, AVX2, OpenMP) decoding the same
+    host model from position 0 for about `seconds`."""
+    import ctypes as C
+    import numpy as np
+    from oracle import binding
+    if not binding.reference_available():
+        return None
+    R = binding.load_reference()
+    c = hm.cfg
+    layers = (binding.RefLayer * c.n_layers)()
+
+    def w(name):
+        t, rows, cols, data = hm.weights[name]
+        from ligguf_amd.lib import row_size
+        return binding.RefWeight(np.asarray(data).ctypes.data, t, row_size(t, cols))
+
+    def f(name):
+        return np.asarray(hm.norms[name]).ctypes.data
+
+    for l in range(c.n_layers):
+        b = f"blk.{l}."
+        L = layers[l]
+        L.att_norm, L.ffn_norm = f(b + "attn_norm.weight"), f(b + "ffn_norm.weight")
+        L.att_q, L.att_k, L.att_v = w(b + "attn_q.weight"), w(b + "attn_k.weight"), w(b + "attn_v.weight")
+        L.att_out = w(b + "attn_output.weight")
+        L.att_q_norm, L.att_k_norm = f(b + "attn_q_norm.weight"), f(b + "attn_k_norm.weight")
+        L.ffn_up, L.ffn_down, L.ffn_gate = w(b + "ffn_up.weight"), w(b + "ffn_down.weight"), w(b + "ffn_gate.weight")
+    m = binding.RefModel(c.arch, c.n_layers, c.n_embed, c.n_heads, c.n_kv_heads, c.head_dim, c.kv_dim, c.n_ff,
+                         c.vocab, c.n_context, c.rope_dim, c.rms_eps, c.rope_theta, w("token_embd.weight"),
+                         w("output.weight"), f("output_norm.weight"), C.cast(layers, C.c_void_p))
+    R.model_bind(m)
+    rng = np.random.default_rng(1)
+    R.inference(int(rng.integers(1, c.vocab)), c.vocab)      # untimed: faults pages in, warms caches
+    n, t0 = 0, time.perf_counter()
+    tok = 1
+    while n < max_tokens and (time.perf_counter() - t0 < seconds or n < 2):
+        logits = R.inference(tok, c.vocab)
+        tok = int(np.argmax(logits))
+        n += 1
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} greedy decode tokens at positions 1..{n} of the same model (reference FAST engine, "
+                      f"AVX2 build, {threads} OpenMP threads)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prefill", type=int, default=512)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernel", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: the decode path here is single-GPU (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from ligguf_amd.model import QWEN3_8B_Q4K, Engine, HostModel
+
+    cfg = QWEN3_8B_Q4K.with_(n_context=max(1024, args.prefill + args.warmup + args.steps + 1))
+    t0 = time.perf_counter()
+    hm = HostModel.synthetic(cfg)
+    log(f"synthetic {cfg.name}: {cfg.weight_bytes() / 1e9:.3f} GB of weights read per token, "
+        f"built in {time.perf_counter() - t0:.1f}s")
+    eng = Engine(0)
+    t0 = time.perf_counter()
+    eng.load(hm)
+    log(f"uploaded in {time.perf_counter() - t0:.1f}s")
+
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(1, cfg.vocab, args.prefill).astype(np.int32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = eng.prefill(prompt, 0)
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {args.prefill} tokens: {args.prefill / prefill_s:.1f} tok/s")
+
+    pos = args.prefill
+    tok = int(np.argmax(logits))
+    for _ in range(args.warmup):
+        eng.decode_async(tok, pos)
+        tok = eng.argmax()
+        pos += 1
+    torch.cuda.synchronize()
+    p_first = pos
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.decode_async(tok, pos)
+        tok = eng.argmax()
+        pos += 1
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt / args.steps * 1e3
+    tps = args.steps / dt
+    mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
+    log(f"decode: {tps:.1f} tok/s, {ms:.3f} ms/token, {mean_bytes / (dt / args.steps) / 1e9:.0f} GB/s per token")
+
+    roof = None
+    if not args.no_kernel:
+        roof = dominant_kernel_roofline(torch, 2 * cfg.n_ff, cfg.n_embed)
+        log(f"dominant kernel: {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of HBM peak)")
+    eng.close()
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(hm, args.cpu_seconds)
+        log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f}s)")
+
+    out = {
+        "metric": "batch-1 decode tok/s (Qwen3-8B-shape Q4_K) + % of HBM roofline",
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3-8b-shape Q4_K/Q6_K batch-1 greedy decode after a 512-token prefill",
+            "layers": cfg.n_layers, "dim": cfg.n_embed, "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}x{cfg.head_dim}",
+            "ffn": cfg.n_ff, "vocab": cfg.vocab, "weights": "Q4_K layers+embedding, Q6_K output",
+            "prefill_tokens": args.prefill, "positions": [p_first, pos - 1],
+            "bytes_per_token": int(mean_bytes),
+        },
+        "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) / HBM_PEAK, 4),
+        "prefill_tok_s": round(args.prefill / prefill_s, 1),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

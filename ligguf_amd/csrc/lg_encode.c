@@ -14,6 +14,7 @@
  * Random tensors come from a counter-based generator keyed on (seed, stream,
  * element index), so a tensor is identical for any thread count.
  */
+#define _GNU_SOURCE
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -68,17 +69,38 @@ static inline uint64_t mix64(uint64_t z)
     return z ^ (z >> 31);
 }
 
-static inline double u01(uint64_t k) { return ((double)(mix64(k) >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+/* uniform in (0,1) from 24 random bits */
+static inline float u01f(uint64_t k) { return ((float)(mix64(k) >> 40) + 0.5f) * 5.9604644775390625e-8f; }
 
-/* element i of stream `stream` under `seed`: N(0,1) by Box-Muller over a
- * pair of counters */
-static inline float gauss(uint64_t seed, uint64_t stream, uint64_t i)
+static inline uint64_t stream_key(uint64_t seed, uint64_t stream) { return mix64(seed * 0x9E3779B97F4A7C15ull + stream); }
+
+/* N(0,1) pair number `pair` of a stream: Box-Muller on two counters; element
+ * 2*pair takes the cosine branch, 2*pair+1 the sine branch */
+static inline void gauss_pair(uint64_t key, uint64_t pair, float* z0, float* z1)
 {
-    const uint64_t base = mix64(seed * 0x9E3779B97F4A7C15ull + stream) ^ (i >> 1) * 0xD1B54A32D192ED03ull;
-    const double u1 = u01(base * 2 + 1), u2 = u01(base * 2 + 2);
-    const double r = sqrt(-2.0 * log(u1));
-    const double a = 6.283185307179586 * u2;
-    return (float)((i & 1) ? r * sin(a) : r * cos(a));
+    const uint64_t base = key ^ (pair * 0xD1B54A32D192ED03ull);
+    const float u1 = u01f(base * 2 + 1), u2 = u01f(base * 2 + 2);
+    const float r = sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.28318530717958648f * u2, &sn, &cs);
+    *z0 = r * cs;
+    *z1 = r * sn;
+}
+
+/* n values of a stream starting at element `first` (even) */
+static void gauss_run(uint64_t key, uint64_t first, float* out, int64_t n, float sigma)
+{
+    for (int64_t j = 0; j + 1 < n; j += 2) {
+        float z0, z1;
+        gauss_pair(key, (first + (uint64_t)j) >> 1, &z0, &z1);
+        out[j] = sigma * z0;
+        out[j + 1] = sigma * z1;
+    }
+    if (n & 1) {
+        float z0, z1;
+        gauss_pair(key, (first + (uint64_t)n - 1) >> 1, &z0, &z1);
+        out[n - 1] = sigma * z0;
+    }
 }
 
 static inline uint32_t ubits(uint64_t seed, uint64_t stream, uint64_t i)
@@ -88,8 +110,13 @@ static inline uint32_t ubits(uint64_t seed, uint64_t stream, uint64_t i)
 
 void lge_fill_normal(uint64_t seed, uint64_t stream, float* out, int64_t n, float sigma)
 {
+    const uint64_t key = stream_key(seed, stream);
+    const int64_t chunk = 1 << 16;
     #pragma omp parallel for schedule(static)
-    for (int64_t i = 0; i < n; i++) out[i] = sigma * gauss(seed, stream, (uint64_t)i);
+    for (int64_t c = 0; c < (n + chunk - 1) / chunk; c++) {
+        const int64_t b = c * chunk, e = b + chunk < n ? b + chunk : n;
+        gauss_run(key, (uint64_t)b, out + b, e - b, sigma);
+    }
 }
 
 /* ---- block encoders (x: 32/128/256 floats -> one block) ---- */
@@ -330,13 +357,14 @@ int lge_quantize(int type, const float* x, int64_t rows, int64_t cols, void* out
 int lge_random_tensor(int type, uint64_t seed, uint64_t stream, int64_t rows, int64_t cols, float sigma, void* out)
 {
     const int64_t rsz = lge_row_size(type, cols);
-    if (rsz < 0 || rows < 0 || block_len(type) <= 0) return -1;
+    if (rsz < 0 || rows < 0 || block_len(type) <= 0 || (cols & 1)) return -1;
+    const uint64_t key = stream_key(seed, stream);
     #pragma omp parallel
     {
         float* buf = (float*)malloc((size_t)cols * sizeof(float));
         #pragma omp for schedule(static)
         for (int64_t r = 0; r < rows; r++) {
-            for (int64_t j = 0; j < cols; j++) buf[j] = sigma * gauss(seed, stream, (uint64_t)(r * cols + j));
+            gauss_run(key, (uint64_t)(r * cols), buf, cols, sigma);
             enc_row(type, buf, cols, (uint8_t*)out + r * rsz);
         }
         free(buf);
@@ -352,10 +380,13 @@ int lge_random_q1(int type, uint64_t seed, uint64_t stream, int64_t rows, int64_
     const int bs = g == 32 ? 6 : 18;
     if (!g || cols % g) return -1;
     const int64_t nb = rows * (cols / g);
+    const uint64_t key = stream_key(seed, stream);
     #pragma omp parallel for schedule(static)
     for (int64_t b = 0; b < nb; b++) {
         uint8_t* blk = (uint8_t*)out + b * bs;
-        put16(blk, h16(fabsf(sigma * gauss(seed, stream, (uint64_t)b))));
+        float z0, z1;
+        gauss_pair(key, (uint64_t)b, &z0, &z1);
+        put16(blk, h16(fabsf(sigma * z0)));
         for (int k = 0; k < g / 32; k++) {
             const uint32_t w = ubits(seed, stream, (uint64_t)(b * 4 + k));
             memcpy(blk + 2 + 4 * k, &w, 4);

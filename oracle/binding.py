@@ -88,6 +88,7 @@ class Oracle:
         L.or_state_set_pos.argtypes = [_vp, C.c_int]
         L.or_inference.argtypes = [_vp, C.c_int, _fp]
         L.or_state_kv.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
+        L.or_state_kv_write.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_argmax.argtypes = [_fp, C.c_int]
 
     # --- scalar helpers
@@ -189,6 +190,11 @@ class Oracle:
         rc = self.L.or_inference(st, tok, out.ctypes.data_as(_fp))
         assert rc == 0
         return out
+
+    def state_kv_write(self, st, layer, p0, np_, k, v):
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        self.L.or_state_kv_write(st, layer, p0, np_, k.ctypes.data, v.ctypes.data)
 
     def state_kv(self, st, layer, p0, np_, kv_dim):
         k = np.empty(np_ * kv_dim, np.uint16)

@@ -394,17 +394,23 @@ static double row_dot(int type, const uint8_t* w, int n, const void* xq, double*
         for (b = 0; b < n / 256; b++) {
             kview_of(type, w + b * bb, &v);
             int64_t S = 0, M = 0;
-            for (i = 0; i < 256; i++) S += (int64_t)v.sc[i] * v.q[i] * a[b].qs[i];
-            if (v.has_min) {
-                /* min of group i/16 (Q2_K) or sub-block i/32 (Q4_K/Q5_K) times
+            const double da = a[b].d;
+            for (int g = 0; g < 16; g++) {
+                int64_t Sg = 0;
+                for (i = 16 * g; i < 16 * g + 16; i++) Sg += (int64_t)v.sc[i] * v.q[i] * a[b].qs[i];
+                S += Sg;
+                /* min of group g (Q2_K) or of sub-block g/2 (Q4_K/Q5_K) times
                  * the activation sum over those values: the reference uses the
                  * Q8_K bsums, which are exactly these sums */
-                for (int g = 0; g < 16; g++) M += (int64_t)v.mn[16 * g] * a[b].bsums[g];
+                const int64_t Mg = v.has_min ? (int64_t)v.mn[16 * g] * a[b].bsums[g] : 0;
+                M += Mg;
+                /* tolerance scale: magnitudes per 16-value group, the finest
+                 * unit any summation order combines */
+                aacc += fabs(da * (double)v.d * (double)Sg) + fabs(da * (double)v.dmin * (double)Mg);
             }
-            const double da = a[b].d;
             const double t1 = da * (double)v.d * (double)S;
             const double t2 = v.has_min ? da * (double)v.dmin * (double)M : 0.0;
-            acc += t1 - t2; aacc += fabs(t1) + fabs(t2);
+            acc += t1 - t2;
         }
     }
     if (abs_out) *abs_out = aacc;
@@ -625,6 +631,14 @@ int or_inference(or_state* s, int tok, float* logits)
     mv(&m->output, s->x, s->logits);
     if (logits) memcpy(logits, s->logits, (size_t)m->vocab_size * 4);
     return 0;
+}
+
+void or_state_kv_write(or_state* s, int layer, int p0, int np, const uint16_t* k, const uint16_t* v)
+{
+    const size_t off = (size_t)layer * s->m.n_context * s->m.kv_dim + (size_t)p0 * s->m.kv_dim;
+    const size_t cnt = (size_t)np * s->m.kv_dim;
+    if (k) memcpy(s->kc + off, k, cnt * 2);
+    if (v) memcpy(s->vc + off, v, cnt * 2);
 }
 
 void or_state_kv(const or_state* s, int layer, int p0, int np, uint16_t* k, uint16_t* v)

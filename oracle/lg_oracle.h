@@ -109,6 +109,7 @@ void or_state_set_pos(or_state* s, int pos);
 int or_inference(or_state* s, int tok, float* logits);
 /* fp16 KV rows of one layer for positions [p0, p0+np) */
 void or_state_kv(const or_state* s, int layer, int p0, int np, uint16_t* k, uint16_t* v);
+void or_state_kv_write(or_state* s, int layer, int p0, int np, const uint16_t* k, const uint16_t* v);
 /* greedy argmax, first index wins ties (fast/ligguf_fast_qk.cpp:146-160) */
 int or_argmax(const float* x, int n);
 
