@@ -18,6 +18,7 @@
  */
 #include <stdint.h>
 #include <string.h>
+#include <algorithm>
 #include <vector>
 #include <string>
 #include "common.h"
@@ -177,6 +178,16 @@ void ref_attention(const float* q, const float* k, const float* v, const uint16_
  * does (fast/ligguf_fast_qk.cpp:572-575). n_ctx > 0 overrides the context. */
 int ref_model_open(const char* path, int n_ctx)
 {
+    /* read_gguf() adds to the tensor and metadata maps without clearing them
+     * (fast/lil_gguf.cpp:357-372): a second open in one process must start
+     * from empty maps, as the reference's single-model process does, or
+     * read_llama would bind the previous file's stale tensors.  The KV cache
+     * is cleared for the same reason (allocate() keeps old contents). */
+    g_m.m.close_mmap();
+    g_m.m.tensors.clear();
+    g_m.m.meta_kv.clear();
+    std::fill(g_m.kc.begin(), g_m.kc.end(), (uint16_t)0);
+    std::fill(g_m.vc.begin(), g_m.vc.end(), (uint16_t)0);
     g_m.pos = 0;
     g_m.u_context = n_ctx;
     if (!g_m.m.open_mmap(path)) return -1;
