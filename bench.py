@@ -68,10 +68,44 @@ def dominant_kernel_roofline(torch, rows: int, cols: int, reps: int = 200):
     alg = wbytes + (cols // 256) * 292 + rows * 4      # weights + Q8_K activation + fp32 output
     del bufs
     torch.cuda.empty_cache()
+    name = f"k_matvec Q4_K {rows}x{cols}"
     return {"bound": "hbm", "achieved": round(alg / avg_s / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(alg / avg_s / HBM_PEAK, 4), "traffic": None,
-            "kernel": f"k_matvec<Q4_K> {rows}x{cols}", "avg_us": round(avg_s * 1e6, 3), "bytes_per_launch": alg,
+            "frac": round(alg / avg_s / HBM_PEAK, 4), "traffic": measured_traffic(name),
+            "kernel": name, "avg_us": round(avg_s * 1e6, 3), "bytes_per_launch": alg,
             "buffers_mb": round(nbuf * wbytes / 2 ** 20)}
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's
+    reading for a copy of known size), or None when no summary covers it."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return int(rec["traffic_bytes"]) if rec else None
+
+
+def plain_copy(torch, nbytes: int = 256 << 20, reps: int = 20):
+    """A plain device copy of a known size (read nbytes, write nbytes): the
+    calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record(s)
+    torch.cuda.synchronize()
+    avg_s = e0.elapsed_time(e1) / 1e3 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes_each_way": nbytes, "avg_us": round(avg_s * 1e6, 2), "GB/s": round(2 * nbytes / avg_s / 1e9, 1)}
 
 
 def cpu_baseline(hm, seconds: float, max_tokens: int = 64):
@@ -130,6 +164,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the decode path here is single-GPU (asked for --gpus {args.gpus}).",
@@ -139,6 +175,13 @@ def main() -> int:
     import numpy as np
     import torch
     from ligguf_amd.model import QWEN3_8B_Q4K, Engine, HostModel
+
+    if args.kernel_only:
+        cfg = QWEN3_8B_Q4K
+        copy_gbs = plain_copy(torch)
+        roof = dominant_kernel_roofline(torch, 2 * cfg.n_ff, cfg.n_embed)
+        print(json.dumps({"roofline": roof, "copy": copy_gbs}), flush=True)
+        return 0
 
     cfg = QWEN3_8B_Q4K.with_(n_context=max(1024, args.prefill + args.warmup + args.steps + 1))
     t0 = time.perf_counter()
