@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "lg_common.h"
+#include "lg_persist.h"
 
 /* ------------------------------------------------------------------ */
 /* errors                                                               */
@@ -123,6 +124,18 @@ struct lg_ctx {
     float* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     int* argmax_dev = nullptr;
+
+    /* persistent one-launch-per-token path (lg_persist.hip) */
+    bool pk_ok = false;          /* the loaded model fits it */
+    int path = LG_PATH_AUTO;
+    int pk_nwg = 0;
+    PkParams pk = {};
+    PkParams* pk_dev = nullptr;      /* device copy of pk */
+    const void* pk_kernel = nullptr; /* the instantiation for this model */
+    uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
+    uint64_t pk_base = 0;
+    int* pk_status_host = nullptr;   /* pinned {token, error} of the last persistent step */
+    bool last_was_pk = false;
 };
 
 static int ctx_fail(lg_ctx* ctx, int rc)
@@ -148,6 +161,9 @@ static void free_model(lg_ctx* ctx)
     ctx->allocs.clear();
     ctx->layers.clear();
     ctx->loaded = false;
+    ctx->pk_ok = false;
+    ctx->last_was_pk = false;
+    ctx->pk_base = 0;
 }
 
 extern "C" int lg_create(int device, lg_ctx** out)
@@ -176,6 +192,7 @@ extern "C" int lg_destroy(lg_ctx* ctx)
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     free_model(ctx);
+    if (ctx->pk_status_host) hipHostFree(ctx->pk_status_host);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return LG_OK;
@@ -236,6 +253,187 @@ static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const
     if (rc) return rc;
     LG_HIP_CHECK(hipMemcpy(*d, h, n * sizeof(float), hipMemcpyHostToDevice));
     return LG_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* persistent path set-up                                               */
+/* ------------------------------------------------------------------ */
+/* the persistent kernel reads every layer matrix at width n_embed = 4096
+ * (n_ff = 12288 for down), one type for all layer matrices */
+static bool pk_shape_ok(const dweight& w, int type, int rows, int cols)
+{
+    return w.type == type && w.rows == rows && w.cols == cols;
+}
+
+static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
+{
+    ctx->pk_ok = false;
+    ctx->pk_kernel = nullptr;
+    const int nrep = m->n_heads / m->n_kv_heads;
+    const int lt = ctx->layers.empty() ? -1 : ctx->layers[0].q.type;
+    bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && m->n_context <= PK_MAX_CHUNK * PK_MAX_UNITS_PER_HEAD &&
+              m->n_kv_heads <= 32 && ctx->output.cols == m->n_embed;
+    for (int l = 0; ok && l < m->n_layers; l++) {
+        const dlayer& D = ctx->layers[l];
+        ok = D.qkv_fused && D.ug_fused && pk_shape_ok(D.qkv, lt, m->n_embed + 2 * m->kv_dim, m->n_embed) &&
+             pk_shape_ok(D.att_out, lt, m->n_embed, m->n_embed) && pk_shape_ok(D.ug, lt, 2 * m->n_ff, m->n_embed) &&
+             pk_shape_ok(D.down, lt, m->n_embed, m->n_ff);
+    }
+    const void* kern = ok ? lg_persist_kernel(lt, ctx->output.type, m->head_dim, nrep) : nullptr;
+    if (!kern) return LG_OK;   /* the multi-kernel path serves this model */
+    int rc;
+    if ((rc = lg_persist_grid(kern, &ctx->pk_nwg))) return rc;
+    std::vector<PkLayer> hl(m->n_layers);
+    for (int l = 0; l < m->n_layers; l++) {
+        const dlayer& D = ctx->layers[l];
+        PkLayer& P = hl[l];
+        P.qkv = D.qkv.data; P.qkv_rsz = D.qkv.rsz; P.qkv_t = D.qkv.type;
+        P.ao = D.att_out.data; P.ao_rsz = D.att_out.rsz; P.ao_t = D.att_out.type;
+        P.ug = D.ug.data; P.ug_rsz = D.ug.rsz; P.ug_t = D.ug.type;
+        P.down = D.down.data; P.down_rsz = D.down.rsz; P.down_t = D.down.type;
+        P.att_norm = D.att_norm; P.ffn_norm = D.ffn_norm; P.q_norm = D.q_norm; P.k_norm = D.k_norm;
+    }
+    PkLayer* dl = nullptr;
+    if ((rc = dalloc(ctx, (void**)&dl, hl.size() * sizeof(PkLayer)))) return rc;
+    LG_HIP_CHECK(hipMemcpy(dl, hl.data(), hl.size() * sizeof(PkLayer), hipMemcpyHostToDevice));
+    PkParams& P = ctx->pk;
+    P = PkParams{};
+    P.layers = dl;
+    P.n_layers = m->n_layers; P.n_embed = m->n_embed; P.n_heads = m->n_heads; P.n_kv = m->n_kv_heads;
+    P.head_dim = m->head_dim; P.kv_dim = m->kv_dim; P.n_ff = m->n_ff; P.vocab = m->vocab_size;
+    P.n_ctx = m->n_context; P.rope_dim = m->rope_dim; P.eps = m->rms_epsilon;
+    P.embd = ctx->embd.data; P.embd_rsz = ctx->embd.rsz; P.embd_t = ctx->embd.type;
+    P.out_w = ctx->output.data; P.out_rsz = ctx->output.rsz; P.out_t = ctx->output.type;
+    P.out_norm = ctx->out_norm; P.rope_freq = ctx->rope_freq;
+    P.kc = ctx->kc; P.vc = ctx->vc;
+    P.logits = ctx->logits;
+    {
+        /* per-layer activation buffers, each written once per step */
+        const size_t L = (size_t)m->n_layers, ne = m->n_embed, qs = ne + 2 * m->kv_dim, ff = m->n_ff;
+        const size_t floats = (L + 1) * ne + L * ne + L * qs + L * ne + L * ff;
+        float* arena = nullptr;
+        if ((rc = dalloc(ctx, (void**)&arena, floats * sizeof(float)))) return rc;
+        P.xs = arena;
+        P.xm = P.xs + (L + 1) * ne;
+        P.qkv = P.xm + L * ne;
+        P.att = P.qkv + L * qs;
+        P.hb = P.att + L * ne;
+    }
+    const size_t ws = (size_t)m->n_kv_heads * PK_MAX_UNITS_PER_HEAD * nrep * (m->head_dim + 2) * sizeof(float);
+    if ((rc = dalloc(ctx, (void**)&P.attn_ws, ws))) return rc;
+    /* one zeroed block for the counters and flags */
+    const int nwg = ctx->pk_nwg;
+    const size_t cnt_bytes = 256 + (size_t)nwg * (8 + 4 + 4) + 64;
+    uint8_t* blk = nullptr;
+    if ((rc = dalloc(ctx, (void**)&blk, cnt_bytes))) return rc;
+    LG_HIP_CHECK(hipMemset(blk, 0, cnt_bytes));
+    P.progress = (uint64_t*)blk;                                   /* nwg x 8 B */
+    P.amax_v = (float*)(blk + (size_t)nwg * 8);                    /* nwg x 4 B */
+    P.amax_i = (int*)(blk + (size_t)nwg * 12);                     /* nwg x 4 B */
+    uint8_t* tail = blk + (size_t)nwg * 16;
+    P.attn_cnt = (uint32_t*)tail;                                  /* up to 32 heads */
+    P.amax_cnt = (uint32_t*)(tail + 128);
+    P.tok_out = (int*)(tail + 192);                                /* {token, error} */
+    P.err = (uint32_t*)(tail + 196);
+    P.spin_cap = 1 << 20;
+    if ((rc = dalloc(ctx, (void**)&ctx->pk_dev, sizeof(PkParams)))) return rc;
+    LG_HIP_CHECK(hipMemcpy(ctx->pk_dev, &P, sizeof(PkParams), hipMemcpyHostToDevice));
+    if (!ctx->pk_status_host) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->pk_status_host, 2 * sizeof(int), 0));
+    ctx->pk_base = 0;
+    ctx->pk_kernel = kern;
+    ctx->pk_ok = true;
+    return LG_OK;
+}
+
+/* the persistent kernel's counters after an expired wait: back to zero */
+static void pk_reset(lg_ctx* c)
+{
+    const size_t bytes = 256 + (size_t)c->pk_nwg * 16 + 64;
+    hipMemsetAsync(c->pk.progress, 0, bytes, c->stream);
+    hipStreamSynchronize(c->stream);
+    c->pk_base = 0;
+}
+
+/* AUTO takes the multi-kernel path until the persistent kernel measures
+ * faster on the headline workload; PERSISTENT selects it explicitly */
+static bool use_pk(const lg_ctx* c) { return c->pk_ok && c->path == LG_PATH_PERSISTENT; }
+
+static int enqueue_pk(lg_ctx* c, int tok, int pos)
+{
+    PkParams& P = c->pk;
+    const int ctx_len = pos + 1;
+    /* attention units of (kv head, chunk): about one per workgroup, but no
+     * shorter than 64 positions (a short unit is all fixed latency) and no
+     * longer than PK_MAX_CHUNK */
+    int chunk = (int)(((int64_t)ctx_len * c->n_kv_heads + c->pk_nwg - 1) / c->pk_nwg);
+    chunk = (chunk + 31) / 32 * 32;
+    if (chunk < 64) chunk = 64;
+    if (chunk > PK_MAX_CHUNK) chunk = PK_MAX_CHUNK;
+    /* up to PK_ONE_UNIT positions one unit per head streams the whole
+     * context and writes att itself: no partials, no merge */
+    if (ctx_len <= PK_ONE_UNIT) chunk = ctx_len;
+    const int nch = (ctx_len + chunk - 1) / chunk;
+    if (nch > PK_MAX_UNITS_PER_HEAD) { lg_set_error("persistent decode: context %d too long", ctx_len); return LG_ERR_STATE; }
+    PkStep S;
+    S.tok = tok; S.pos = pos; S.chunk = chunk; S.nch = nch; S.base = c->pk_base;
+    S.trace = c->pk_trace;
+    c->pk_trace = nullptr;   /* one step only */
+    int rc = lg_persist_launch(c->pk_kernel, c->pk_dev, &S, c->pk_nwg, c->stream);
+    if (rc) return rc;
+    c->pk_base += 5ull * c->n_layers + 1;
+    LG_HIP_CHECK(hipMemcpyAsync(c->pk_status_host, P.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    c->last_was_pk = true;
+    return LG_OK;
+}
+
+/* after a synchronize: turn an expired wait of the last persistent step
+ * into an error (and reset the counters for the next step) */
+static int pk_check(lg_ctx* c)
+{
+    if (!c->last_was_pk || !c->pk_status_host) return LG_OK;
+    if (c->pk_status_host[1]) {
+        const int code = c->pk_status_host[1];
+        pk_reset(c);
+        c->pk_status_host[1] = 0;
+        lg_set_error(code == 1 ? "persistent decode: a workgroup sync wait expired"
+                               : "persistent decode: unsupported phase configuration");
+        return LG_ERR_STATE;
+    }
+    return LG_OK;
+}
+
+extern "C" int lg_set_decode_path(lg_ctx* ctx, int path)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    if (path != LG_PATH_AUTO && path != LG_PATH_PERSISTENT && path != LG_PATH_MULTI) {
+        lg_set_error("lg_set_decode_path: unknown path %d", path);
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    if (path == LG_PATH_PERSISTENT && !ctx->pk_ok) {
+        lg_set_error("lg_set_decode_path: the loaded model is not supported by the persistent kernel");
+        return ctx_fail(ctx, LG_ERR_STATE);
+    }
+    ctx->path = path;
+    return LG_OK;
+}
+
+extern "C" int lg_trace_next_step(lg_ctx* ctx, uint64_t* trace_dev)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    ctx->pk_trace = trace_dev;
+    return LG_OK;
+}
+
+extern "C" size_t lg_trace_size(const lg_ctx* ctx)
+{
+    if (!ctx || !ctx->pk_ok) return 0;
+    return (size_t)(5 * ctx->n_layers + 1) * ctx->pk_nwg * 4 * sizeof(uint64_t);
+}
+
+extern "C" int lg_decode_path(const lg_ctx* ctx)
+{
+    if (!ctx || !ctx->loaded) return -1;
+    return use_pk(ctx) ? LG_PATH_PERSISTENT : LG_PATH_MULTI;
 }
 
 static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
@@ -349,6 +547,7 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
     ctx->attn_ws_bytes = lg_attn_ws_bytes(m->n_heads, m->head_dim, m->n_context - 1);
     if ((rc = dalloc(ctx, (void**)&ctx->attn_ws, ctx->attn_ws_bytes))) return rc;
     if ((rc = dalloc(ctx, (void**)&ctx->argmax_dev, 16))) return rc;
+    if ((rc = setup_persistent(ctx, m))) return rc;
     LG_HIP_CHECK(hipDeviceSynchronize());
     ctx->loaded = true;
     return LG_OK;
@@ -406,6 +605,8 @@ static int mv(lg_ctx* c, const dweight& w, const actbufs& a, float* out, int acc
 
 static int enqueue_step(lg_ctx* c, int tok, int pos)
 {
+    if (use_pk(c)) return enqueue_pk(c, tok, pos);
+    c->last_was_pk = false;
     int rc;
     const int ne = c->n_embed, kvd = c->kv_dim;
     float* q = c->qkv;
@@ -490,7 +691,7 @@ extern "C" int lg_sync(lg_ctx* ctx)
         lg_set_error("stream synchronize: %s", hipGetErrorString(e));
         return ctx_fail(ctx, LG_ERR_HIP);
     }
-    return LG_OK;
+    return ctx_fail(ctx, pk_check(ctx));
 }
 
 extern "C" const float* lg_logits_device(lg_ctx* ctx) { return ctx && ctx->loaded ? ctx->logits : nullptr; }
@@ -510,6 +711,14 @@ extern "C" int lg_argmax(lg_ctx* ctx, int* tok_out)
 {
     if (!ctx || !tok_out) { lg_set_error("lg_argmax: null argument"); return LG_ERR_ARG; }
     if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    if (ctx->last_was_pk) {
+        /* the persistent step reduced the argmax already and its status
+         * copy is queued behind it */
+        const int rc = lg_sync(ctx);
+        if (rc) return rc;
+        *tok_out = ctx->pk_status_host[0];
+        return LG_OK;
+    }
     int rc = lg_launch_argmax(ctx->logits, ctx->vocab, ctx->argmax_dev, ctx->stream);
     if (rc) return ctx_fail(ctx, rc);
     const hipError_t e = hipMemcpyAsync(tok_out, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);

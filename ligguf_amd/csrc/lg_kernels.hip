@@ -8,91 +8,7 @@
 #include <math.h>
 
 #include "lg_common.h"
-
-/* ------------------------------------------------------------------ */
-/* Dequantization of one value (closed forms of fast/lil_math.cpp:93-298;*/
-/* every product is exact in fp32, so the result is bit-identical).     */
-/* ------------------------------------------------------------------ */
-__device__ __forceinline__ int k4_sc(const uint8_t* s, int j)
-{
-    return j < 4 ? (s[j] & 63) : ((s[j + 4] & 15) | ((s[j - 4] >> 6) << 4));
-}
-
-__device__ __forceinline__ int k4_mn(const uint8_t* s, int j)
-{
-    return j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
-}
-
-__device__ __forceinline__ int k3_sc(const uint8_t* s, int g)
-{
-    const int lo = g < 8 ? (s[g] & 15) : (s[g - 8] >> 4);
-    const int hi = (s[8 + (g & 3)] >> (2 * (g >> 2))) & 3;
-    return lo | (hi << 4);
-}
-
-__device__ float lg_dq_value(int type, const uint8_t* row, int64_t i)
-{
-#pragma clang fp contract(off)
-    switch (type) {
-    case LG_F32: return lg_ld<float>(row + 4 * i);
-    case LG_F16: return lg_h2f(lg_ld16(row + 2 * i));
-    case LG_Q8_0: {
-        const uint8_t* b = row + (i >> 5) * LG_BS_Q8_0;
-        return (float)(int8_t)b[2 + (i & 31)] * lg_h2f(lg_ld16(b));
-    }
-    case LG_Q1_0: {
-        const uint8_t* b = row + (i >> 5) * LG_BS_Q1_0;
-        const float d = lg_h2f(lg_ld16(b));
-        const int j = (int)(i & 31);
-        return ((b[2 + (j >> 3)] >> (j & 7)) & 1) ? d : -d;
-    }
-    case LG_Q1_G: {
-        const uint8_t* b = row + (i >> 7) * LG_BS_Q1_G;
-        const float d = lg_h2f(lg_ld16(b));
-        const int j = (int)(i & 127);
-        return ((b[2 + (j >> 3)] >> (j & 7)) & 1) ? d : -d;
-    }
-    case LG_Q2_K: {
-        const uint8_t* b = row + (i >> 8) * LG_BS_Q2_K;
-        const int k = (int)(i & 255), n = k >> 7, j = (k >> 5) & 3, h = (k >> 4) & 1, l = k & 15;
-        const int q = (b[16 + 32 * n + 16 * h + l] >> (2 * j)) & 3;
-        const uint8_t s = b[k >> 4];
-        const float d = lg_h2f(lg_ld16(b + 80)), dm = lg_h2f(lg_ld16(b + 82));
-        return d * (float)(s & 15) * (float)q - dm * (float)(s >> 4);
-    }
-    case LG_Q3_K: {
-        const uint8_t* b = row + (i >> 8) * LG_BS_Q3_K;
-        const int k = (int)(i & 255), n = k >> 7, j = (k >> 5) & 3, h = (k >> 4) & 1, l = k & 15;
-        const int lo = (b[32 + 32 * n + 16 * h + l] >> (2 * j)) & 3;
-        const int hb = (b[16 * h + l] >> (4 * n + j)) & 1;
-        const float d = lg_h2f(lg_ld16(b + 108));
-        return d * (float)(k3_sc(b + 96, k >> 4) - 32) * (float)(lo - (hb ? 0 : 4));
-    }
-    case LG_Q4_K: {
-        const uint8_t* b = row + (i >> 8) * LG_BS_Q4_K;
-        const int k = (int)(i & 255), c = k >> 6, h = (k >> 5) & 1, l = k & 31;
-        const int q = (b[16 + 32 * c + l] >> (4 * h)) & 15;
-        const float d = lg_h2f(lg_ld16(b)), dm = lg_h2f(lg_ld16(b + 2));
-        return d * (float)k4_sc(b + 4, 2 * c + h) * (float)q - dm * (float)k4_mn(b + 4, 2 * c + h);
-    }
-    case LG_Q5_K: {
-        const uint8_t* b = row + (i >> 8) * LG_BS_Q5_K;
-        const int k = (int)(i & 255), c = k >> 6, h = (k >> 5) & 1, l = k & 31;
-        const int q = ((b[48 + 32 * c + l] >> (4 * h)) & 15) + 16 * ((b[16 + l] >> (2 * c + h)) & 1);
-        const float d = lg_h2f(lg_ld16(b)), dm = lg_h2f(lg_ld16(b + 2));
-        return d * (float)k4_sc(b + 4, 2 * c + h) * (float)q - dm * (float)k4_mn(b + 4, 2 * c + h);
-    }
-    case LG_Q6_K: {
-        const uint8_t* b = row + (i >> 8) * LG_BS_Q6_K;
-        const int k = (int)(i & 255), n = k >> 7, g = (k >> 5) & 3, l = k & 31;
-        const int lo = (b[64 * n + l + 32 * (g & 1)] >> (4 * (g >> 1))) & 15;
-        const int hi = (b[128 + 32 * n + l] >> (2 * g)) & 3;
-        const float d = lg_h2f(lg_ld16(b + 208));
-        return d * (float)(int8_t)b[192 + (k >> 4)] * (float)((lo | (hi << 4)) - 32);
-    }
-    default: return 0.0f;
-    }
-}
+#include "lg_quant.h"
 
 __global__ void k_dequantize(int type, const uint8_t* __restrict__ x, float* __restrict__ y, int64_t n)
 {
@@ -108,100 +24,6 @@ __global__ void k_embed(int type, const uint8_t* __restrict__ table, uint32_t rs
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     const int t = tok_dev ? *tok_dev : tok;
     if (i < n) x[i] = lg_dq_value(type, table + (size_t)t * rsz, i);
-}
-
-/* ------------------------------------------------------------------ */
-/* Activation quantizers from registers.                               */
-/* ------------------------------------------------------------------ */
-
-/* Q8_K block from the wave's 256 values (lane l holds v[0..3] = values
- * 4l..4l+3; inactive values must be 0).  quantize_q8_K as the reference
- * compiles it (fast/lil_math.cpp:358-394 under -Ofast): first-index signed
- * max of |x|, iscale = -127/max, q = min(127, trunc(iscale*x -+ 0.5)),
- * 16-value bsums, d = max * (-1/127). */
-__device__ void lg_q8k_block(const float v[4], uint8_t* __restrict__ out)
-{
-#pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float a = fabsf(v[j]);
-        if (a > amax) { amax = a; mx = v[j]; idx = 4 * lane + j; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float oa = __shfl_xor(amax, o, 64);
-        const float om = __shfl_xor(mx, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
-    uint32_t packed = 0;
-    int s = 0;
-    if (amax != 0.0f) {
-        const float iscale = -127.0f / mx;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float f = iscale * v[j];
-            int t = f < 0.0f ? (int)(f - 0.5f) : (int)(f + 0.5f);
-            t = t < 127 ? t : 127;
-            s += t;
-            packed |= (uint32_t)(t & 255) << (8 * j);
-        }
-    }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    *(uint32_t*)(out + 4 + 4 * lane) = packed;
-    if ((lane & 3) == 0) *(int16_t*)(out + 260 + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *(float*)out = amax != 0.0f ? mx * (-1.0f / 127.0f) : 0.0f;
-}
-
-/* Eight Q8_0 blocks from the wave's 256 values (block = lane/8), or fewer
- * when nvalid < 256.  quantize_q8_0 as compiled (fast/lil_math.cpp:329-351
- * under -Ofast): d = amax * (1/127), id = 127/amax, q = roundf(x*id). */
-__device__ void lg_q8_0_blocks(const float v[4], uint8_t* __restrict__ out, int nvalid)
-{
-#pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float a = fabsf(v[j]);
-        if (amax < a) amax = a;
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-    const int blk = lane >> 3;
-    if (32 * blk >= nvalid) return;
-    const float d = amax * (1.0f / 127.0f);
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    uint8_t* b = out + LG_BS_Q8_0 * blk;
-    uint32_t packed = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int q = (int)roundf(v[j] * id);
-        packed |= (uint32_t)(q & 255) << (8 * j);
-    }
-    __builtin_memcpy(b + 2 + 4 * (lane & 7), &packed, 4);
-    if ((lane & 7) == 0) {
-        const uint16_t dh = lg_f2h(d);
-        __builtin_memcpy(b, &dh, 2);
-    }
-}
-
-/* store the wave's 256 values in the requested activation format */
-__device__ __forceinline__ void lg_emit(const float v[4], int qtype, uint8_t* out_q, int64_t chunk, int nvalid)
-{
-    const int lane = threadIdx.x & 63;
-    if (qtype == LG_Q8_K) {
-        lg_q8k_block(v, out_q + chunk * LG_BS_Q8_K);
-    } else if (qtype == LG_Q8_0) {
-        lg_q8_0_blocks(v, out_q + chunk * 8 * LG_BS_Q8_0, nvalid);
-    } else if (qtype == LG_F32) {
-        if (4 * lane < nvalid) *(float4*)((float*)out_q + chunk * 256 + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
-    }
 }
 
 /* one wave per 256 values */

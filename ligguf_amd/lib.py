@@ -22,6 +22,7 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q1_0: (32, 6), Q1_G: (128, 18
          Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
 
 ARCH_LLAMA, ARCH_QWEN3 = 0, 1
+PATH_AUTO, PATH_PERSISTENT, PATH_MULTI = 0, 1, 2
 
 _vp = C.c_void_p
 
@@ -60,6 +61,10 @@ SIGNATURES = {
     "lg_sync": (C.c_int, [_vp]),
     "lg_logits_device": (_vp, [_vp]),
     "lg_argmax": (C.c_int, [_vp, C.POINTER(C.c_int)]),
+    "lg_set_decode_path": (C.c_int, [_vp, C.c_int]),
+    "lg_decode_path": (C.c_int, [_vp]),
+    "lg_trace_next_step": (C.c_int, [_vp, _vp]),
+    "lg_trace_size": (C.c_size_t, [_vp]),
     "lg_prefill": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),
     "lg_kv_read": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "lg_kv_write": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),

@@ -276,6 +276,14 @@ class Engine:
         self.vocab = hm.cfg.vocab
         self.cfg = hm.cfg
 
+    def set_path(self, path: int) -> None:
+        """lg_set_decode_path: PATH_AUTO, PATH_PERSISTENT or PATH_MULTI."""
+        check(self.lib.lg_set_decode_path(self.ctx, path), self.ctx)
+
+    def path(self) -> int:
+        """The decode path the next step takes (PATH_PERSISTENT / PATH_MULTI)."""
+        return int(self.lib.lg_decode_path(self.ctx))
+
     def decode(self, tok: int, pos: int, want_logits: bool = True):
         if want_logits:
             out = np.empty(self.vocab, np.float32)
