@@ -191,7 +191,8 @@ def main() -> int:
     eng = Engine(0)
     t0 = time.perf_counter()
     eng.load(hm)
-    log(f"uploaded in {time.perf_counter() - t0:.1f}s")
+    path_name = {1: "persistent", 2: "multi-kernel", 3: "fused-graph"}.get(eng.path(), "?")
+    log(f"uploaded in {time.perf_counter() - t0:.1f}s; decode path {path_name}")
 
     rng = np.random.default_rng(0)
     prompt = rng.integers(1, cfg.vocab, args.prefill).astype(np.int32)
@@ -251,7 +252,7 @@ def main() -> int:
             "layers": cfg.n_layers, "dim": cfg.n_embed, "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}x{cfg.head_dim}",
             "ffn": cfg.n_ff, "vocab": cfg.vocab, "weights": "Q4_K layers+embedding, Q6_K output",
             "prefill_tokens": args.prefill, "positions": [p_first, pos - 1],
-            "bytes_per_token": int(mean_bytes),
+            "bytes_per_token": int(mean_bytes), "decode_path": path_name,
         },
         "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) / HBM_PEAK, 4),
         "prefill_tok_s": round(args.prefill / prefill_s, 1),

@@ -117,11 +117,17 @@ int lg_decode_step_async(lg_ctx* ctx, int tok, int pos);
 int lg_sync(lg_ctx* ctx);
 const float* lg_logits_device(lg_ctx* ctx);
 
-/* Which implementation runs the decode step.  LG_PATH_PERSISTENT is one
- * cooperative kernel per token (one workgroup per CU walking all layers with
- * flag syncs between phases); LG_PATH_MULTI is one kernel per operation.
- * AUTO (the default) is currently the multi-kernel path.  PERSISTENT
- * needs a model with an instantiation: n_embed 4096, n_ff 12288, one layer type for all
+/* Which implementation runs the decode step.  LG_PATH_FUSED is five fused
+ * kernels per layer (rmsnorm+QKV, attention with its merge, att_out +
+ * residual, rmsnorm + up|gate + SwiGLU, down + residual) and one for the
+ * output head and greedy argmax, replayed from a HIP graph captured on first
+ * use (set LG_NO_GRAPH=1 in the environment before lg_create to launch them
+ * directly); token and position live in device memory, so consecutive greedy
+ * steps need no host-to-device copy.  LG_PATH_PERSISTENT is the same phases in
+ * one cooperative kernel per token with flag syncs between them.
+ * LG_PATH_MULTI is one kernel per operation and serves every model.  AUTO
+ * (the default) takes FUSED when the model has an instantiation, else MULTI.
+ * FUSED and PERSISTENT need: n_embed 4096, n_ff 12288, one layer type for all
  * layer matrices (Q4_K, Q5_K, Q6_K, Q1_G or Q8_0) with a matching output
  * type, head_dim 128 and 1, 4 or 8 query heads per KV head.  Both compute the
  * reference's inference() sequence with the same quantizers and dot
@@ -129,16 +135,18 @@ const float* lg_logits_device(lg_ctx* ctx);
 #define LG_PATH_AUTO 0
 #define LG_PATH_PERSISTENT 1
 #define LG_PATH_MULTI 2
+#define LG_PATH_FUSED 3
 int lg_set_decode_path(lg_ctx* ctx, int path);
 /* the path the next step takes (LG_PATH_PERSISTENT or LG_PATH_MULTI), -1 without a model */
 int lg_decode_path(const lg_ctx* ctx);
 
-/* Phase tracing of the persistent kernel (no counterpart in the reference,
+/* Phase tracing of the fused and persistent steps (no counterpart in the reference,
  * whose only instrumentation is wall-clock per token,
  * fast/ligguf_fast_qk.cpp:316-331).  lg_trace_size(ctx) bytes of device
- * memory at trace_dev receive, for the NEXT persistent step only, four
+ * memory at trace_dev receive, for the NEXT fused or persistent step only, four
  * 100 MHz timestamps per phase and workgroup -- [5*n_layers+1][nwg][4]:
  * phase entry, dependency wait over, activation built, phase published.
+ * (for the fused kernels: entry, loads issued, activation built, done).
  * lg_trace_size is 0 when the model runs on the multi-kernel path. */
 int lg_trace_next_step(lg_ctx* ctx, uint64_t* trace_dev);
 size_t lg_trace_size(const lg_ctx* ctx);

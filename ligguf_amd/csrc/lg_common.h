@@ -65,28 +65,74 @@ __device__ __forceinline__ int lg_dot4(int a, int b, int c)
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+/* Cross-lane butterfly.  Step K pairs every lane with a partner so that
+ * after steps 0..log2(G)-1 each aligned group of G lanes has combined all of
+ * its members: steps 0-3 are DPP permutes inside 16-lane rows (quad_perm
+ * [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror -- each pairs
+ * two already-combined halves), steps 4-5 cross rows (ds_bpermute).  Every
+ * lane ends with the same bits: each pairwise op sees the same two operands. */
+#define LG_DPP_XOR1 0xB1
+#define LG_DPP_XOR2 0x4E
+#define LG_DPP_HALF_MIRROR 0x141
+#define LG_DPP_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ int lg_dpp(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int K>
+__device__ __forceinline__ int lg_partner(int v)
+{
+    if constexpr (K == 0) return lg_dpp<LG_DPP_XOR1>(v);
+    else if constexpr (K == 1) return lg_dpp<LG_DPP_XOR2>(v);
+    else if constexpr (K == 2) return lg_dpp<LG_DPP_HALF_MIRROR>(v);
+    else if constexpr (K == 3) return lg_dpp<LG_DPP_MIRROR>(v);
+    else if constexpr (K == 4) return __shfl_xor(v, 16, LG_WAVE);
+    else return __shfl_xor(v, 32, LG_WAVE);
+}
+
+template <int K>
+__device__ __forceinline__ float lg_partner(float v)
+{
+    return __int_as_float(lg_partner<K>(__float_as_int(v)));
+}
+
 /* sum over aligned groups of G lanes (G a power of two <= 64) */
 template <int G>
 __device__ __forceinline__ float lg_group_sum(float v)
 {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LG_WAVE);
+    if constexpr (G >= 2) v += lg_partner<0>(v);
+    if constexpr (G >= 4) v += lg_partner<1>(v);
+    if constexpr (G >= 8) v += lg_partner<2>(v);
+    if constexpr (G >= 16) v += lg_partner<3>(v);
+    if constexpr (G >= 32) v += lg_partner<4>(v);
+    if constexpr (G >= 64) v += lg_partner<5>(v);
     return v;
 }
 
 template <int G>
 __device__ __forceinline__ float lg_group_max(float v)
 {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, LG_WAVE));
+    if constexpr (G >= 2) v = fmaxf(v, lg_partner<0>(v));
+    if constexpr (G >= 4) v = fmaxf(v, lg_partner<1>(v));
+    if constexpr (G >= 8) v = fmaxf(v, lg_partner<2>(v));
+    if constexpr (G >= 16) v = fmaxf(v, lg_partner<3>(v));
+    if constexpr (G >= 32) v = fmaxf(v, lg_partner<4>(v));
+    if constexpr (G >= 64) v = fmaxf(v, lg_partner<5>(v));
     return v;
 }
 
 template <int G>
 __device__ __forceinline__ int lg_group_isum(int v)
 {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LG_WAVE);
+    if constexpr (G >= 2) v += lg_partner<0>(v);
+    if constexpr (G >= 4) v += lg_partner<1>(v);
+    if constexpr (G >= 8) v += lg_partner<2>(v);
+    if constexpr (G >= 16) v += lg_partner<3>(v);
+    if constexpr (G >= 32) v += lg_partner<4>(v);
+    if constexpr (G >= 64) v += lg_partner<5>(v);
     return v;
 }
 

@@ -17,6 +17,7 @@
  */
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -134,8 +135,20 @@ struct lg_ctx {
     const void* pk_kernel = nullptr; /* the instantiation for this model */
     uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
     uint64_t pk_base = 0;
-    int* pk_status_host = nullptr;   /* pinned {token, error} of the last persistent step */
-    bool last_was_pk = false;
+    int* pk_status_host = nullptr;   /* pinned {token, error} of the last persistent / fused step */
+    bool last_was_pk = false;        /* the last step left its greedy token in pk_status_host */
+
+    /* fused per-phase kernels replayed from a HIP graph (lg_fused.hip) */
+    const void* fused_fn = nullptr;
+    PkStep* step_dev = nullptr;      /* {tok, pos, feed_end} the next fused step reads */
+    PkStep* step_ring = nullptr;     /* pinned slots for host updates of step_dev */
+    int ring_next = 0, ring_pending = 0;
+    int* feed_dev = nullptr;         /* [n_context] prompt tokens */
+    int* feed_host = nullptr;        /* pinned staging of the same */
+    bool dev_known = false;          /* step_dev holds {dev_tok, dev_pos} (read back after a sync) */
+    int dev_tok = 0, dev_pos = 0, dev_feed_end = 0, last_pos = 0;
+    bool use_graph = true;
+    hipGraphExec_t graph = nullptr;
 };
 
 static int ctx_fail(lg_ctx* ctx, int rc)
@@ -164,6 +177,13 @@ static void free_model(lg_ctx* ctx)
     ctx->pk_ok = false;
     ctx->last_was_pk = false;
     ctx->pk_base = 0;
+    ctx->fused_fn = nullptr;
+    ctx->dev_known = false;
+    ctx->dev_feed_end = 0;
+    if (ctx->graph) {
+        hipGraphExecDestroy(ctx->graph);
+        ctx->graph = nullptr;
+    }
 }
 
 extern "C" int lg_create(int device, lg_ctx** out)
@@ -176,6 +196,8 @@ extern "C" int lg_create(int device, lg_ctx** out)
     LG_HIP_CHECK(hipSetDevice(device));
     lg_ctx* ctx = new lg_ctx();
     ctx->device = device;
+    const char* ng = getenv("LG_NO_GRAPH");
+    ctx->use_graph = !(ng && ng[0] == '1');
     const hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         lg_set_error("hipStreamCreate failed: %s", hipGetErrorString(e));
@@ -193,6 +215,8 @@ extern "C" int lg_destroy(lg_ctx* ctx)
     hipStreamSynchronize(ctx->stream);
     free_model(ctx);
     if (ctx->pk_status_host) hipHostFree(ctx->pk_status_host);
+    if (ctx->step_ring) hipHostFree(ctx->step_ring);
+    if (ctx->feed_host) hipHostFree(ctx->feed_host);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return LG_OK;
@@ -258,6 +282,7 @@ static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const
 /* ------------------------------------------------------------------ */
 /* persistent path set-up                                               */
 /* ------------------------------------------------------------------ */
+#define LG_STEP_RING 64   /* pinned step records in flight before a forced sync */
 /* the persistent kernel reads every layer matrix at width n_embed = 4096
  * (n_ff = 12288 for down), one type for all layer matrices */
 static bool pk_shape_ok(const dweight& w, int type, int rows, int cols)
@@ -336,6 +361,17 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.tok_out = (int*)(tail + 192);                                /* {token, error} */
     P.err = (uint32_t*)(tail + 196);
     P.spin_cap = 1 << 20;
+    /* fused path: device step record, prompt feed, pinned staging */
+    if ((rc = dalloc(ctx, (void**)&ctx->step_dev, sizeof(PkStep)))) return rc;
+    LG_HIP_CHECK(hipMemset(ctx->step_dev, 0, sizeof(PkStep)));
+    if ((rc = dalloc(ctx, (void**)&ctx->feed_dev, (size_t)m->n_context * sizeof(int)))) return rc;
+    LG_HIP_CHECK(hipMemset(ctx->feed_dev, 0, (size_t)m->n_context * sizeof(int)));
+    P.feed = ctx->feed_dev;
+    if (ctx->feed_host) { hipHostFree(ctx->feed_host); ctx->feed_host = nullptr; }
+    LG_HIP_CHECK(hipHostMalloc((void**)&ctx->feed_host, (size_t)m->n_context * sizeof(int), 0));
+    if (!ctx->step_ring) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->step_ring, LG_STEP_RING * sizeof(PkStep), 0));
+    ctx->ring_next = ctx->ring_pending = 0;
+    ctx->fused_fn = lg_fused_variant(lt, ctx->output.type, m->head_dim, nrep);
     if ((rc = dalloc(ctx, (void**)&ctx->pk_dev, sizeof(PkParams)))) return rc;
     LG_HIP_CHECK(hipMemcpy(ctx->pk_dev, &P, sizeof(PkParams), hipMemcpyHostToDevice));
     if (!ctx->pk_status_host) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->pk_status_host, 2 * sizeof(int), 0));
@@ -357,22 +393,77 @@ static void pk_reset(lg_ctx* c)
 /* AUTO takes the multi-kernel path until the persistent kernel measures
  * faster on the headline workload; PERSISTENT selects it explicitly */
 static bool use_pk(const lg_ctx* c) { return c->pk_ok && c->path == LG_PATH_PERSISTENT; }
+static bool use_fused(const lg_ctx* c)
+{
+    return c->pk_ok && c->fused_fn && (c->path == LG_PATH_FUSED || c->path == LG_PATH_AUTO);
+}
+
+/* write {tok, pos, feed_end} into the device step record through a pinned slot */
+static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* trace = nullptr)
+{
+    if (c->ring_pending >= LG_STEP_RING) {
+        LG_HIP_CHECK(hipStreamSynchronize(c->stream));
+        c->ring_pending = 0;
+    }
+    PkStep* s = &c->step_ring[c->ring_next];
+    c->ring_next = (c->ring_next + 1) % LG_STEP_RING;
+    c->ring_pending++;
+    memset(s, 0, sizeof(*s));
+    s->tok = tok; s->pos = pos; s->feed_end = feed_end; s->trace = trace;
+    LG_HIP_CHECK(hipMemcpyAsync(c->step_dev, s, sizeof(PkStep), hipMemcpyHostToDevice, c->stream));
+    c->dev_feed_end = feed_end;
+    return LG_OK;
+}
+
+/* one fused step on the stream: the graph (captured on first use) or the
+ * same launches issued directly */
+static int fused_launch(lg_ctx* c)
+{
+    if (c->use_graph && !c->graph) {
+        hipGraph_t g = nullptr;
+        LG_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = lg_fused_enqueue(c->fused_fn, c->pk_dev, c->step_dev, c->n_layers, c->pk_nwg, c->stream);
+        const hipError_t ec = hipStreamEndCapture(c->stream, &g);
+        if (rc || ec != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            lg_set_error("graph capture of the fused step failed: %s", hipGetErrorString(ec));
+            return rc ? rc : LG_ERR_HIP;
+        }
+        const hipError_t ei = hipGraphInstantiate(&c->graph, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ei != hipSuccess) {
+            c->graph = nullptr;
+            lg_set_error("graph instantiate: %s", hipGetErrorString(ei));
+            return LG_ERR_HIP;
+        }
+    }
+    if (c->use_graph) {
+        LG_HIP_CHECK(hipGraphLaunch(c->graph, c->stream));
+        return LG_OK;
+    }
+    return lg_fused_enqueue(c->fused_fn, c->pk_dev, c->step_dev, c->n_layers, c->pk_nwg, c->stream);
+}
+
+static int enqueue_fused(lg_ctx* c, int tok, int pos)
+{
+    int rc;
+    if (c->pk_trace || !(c->dev_known && c->dev_tok == tok && c->dev_pos == pos && pos >= c->dev_feed_end))
+        if ((rc = fused_set_step(c, tok, pos, 0, c->pk_trace))) return rc;
+    c->pk_trace = nullptr;
+    c->dev_known = false;
+    if ((rc = fused_launch(c))) return rc;
+    LG_HIP_CHECK(hipMemcpyAsync(c->pk_status_host, c->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    c->last_was_pk = true;
+    c->last_pos = pos;
+    return LG_OK;
+}
 
 static int enqueue_pk(lg_ctx* c, int tok, int pos)
 {
     PkParams& P = c->pk;
     const int ctx_len = pos + 1;
-    /* attention units of (kv head, chunk): about one per workgroup, but no
-     * shorter than 64 positions (a short unit is all fixed latency) and no
-     * longer than PK_MAX_CHUNK */
-    int chunk = (int)(((int64_t)ctx_len * c->n_kv_heads + c->pk_nwg - 1) / c->pk_nwg);
-    chunk = (chunk + 31) / 32 * 32;
-    if (chunk < 64) chunk = 64;
-    if (chunk > PK_MAX_CHUNK) chunk = PK_MAX_CHUNK;
-    /* up to PK_ONE_UNIT positions one unit per head streams the whole
-     * context and writes att itself: no partials, no merge */
-    if (ctx_len <= PK_ONE_UNIT) chunk = ctx_len;
-    const int nch = (ctx_len + chunk - 1) / chunk;
+    int chunk, nch;
+    pk_attn_split(ctx_len, c->n_kv_heads, c->pk_nwg, &chunk, &nch);
     if (nch > PK_MAX_UNITS_PER_HEAD) { lg_set_error("persistent decode: context %d too long", ctx_len); return LG_ERR_STATE; }
     PkStep S;
     S.tok = tok; S.pos = pos; S.chunk = chunk; S.nch = nch; S.base = c->pk_base;
@@ -390,7 +481,14 @@ static int enqueue_pk(lg_ctx* c, int tok, int pos)
  * into an error (and reset the counters for the next step) */
 static int pk_check(lg_ctx* c)
 {
+    c->ring_pending = 0;
     if (!c->last_was_pk || !c->pk_status_host) return LG_OK;
+    if (use_fused(c)) {
+        /* the output kernel advanced the step record to {token, pos + 1} */
+        c->dev_tok = c->pk_status_host[0];
+        c->dev_pos = c->last_pos + 1;
+        c->dev_known = true;
+    }
     if (c->pk_status_host[1]) {
         const int code = c->pk_status_host[1];
         pk_reset(c);
@@ -405,9 +503,13 @@ static int pk_check(lg_ctx* c)
 extern "C" int lg_set_decode_path(lg_ctx* ctx, int path)
 {
     if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
-    if (path != LG_PATH_AUTO && path != LG_PATH_PERSISTENT && path != LG_PATH_MULTI) {
+    if (path != LG_PATH_AUTO && path != LG_PATH_PERSISTENT && path != LG_PATH_MULTI && path != LG_PATH_FUSED) {
         lg_set_error("lg_set_decode_path: unknown path %d", path);
         return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    if (path == LG_PATH_FUSED && !(ctx->pk_ok && ctx->fused_fn)) {
+        lg_set_error("lg_set_decode_path: the loaded model is not supported by the fused kernels");
+        return ctx_fail(ctx, LG_ERR_STATE);
     }
     if (path == LG_PATH_PERSISTENT && !ctx->pk_ok) {
         lg_set_error("lg_set_decode_path: the loaded model is not supported by the persistent kernel");
@@ -433,7 +535,7 @@ extern "C" size_t lg_trace_size(const lg_ctx* ctx)
 extern "C" int lg_decode_path(const lg_ctx* ctx)
 {
     if (!ctx || !ctx->loaded) return -1;
-    return use_pk(ctx) ? LG_PATH_PERSISTENT : LG_PATH_MULTI;
+    return use_pk(ctx) ? LG_PATH_PERSISTENT : (use_fused(ctx) ? LG_PATH_FUSED : LG_PATH_MULTI);
 }
 
 static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
@@ -606,6 +708,7 @@ static int mv(lg_ctx* c, const dweight& w, const actbufs& a, float* out, int acc
 static int enqueue_step(lg_ctx* c, int tok, int pos)
 {
     if (use_pk(c)) return enqueue_pk(c, tok, pos);
+    if (use_fused(c)) return enqueue_fused(c, tok, pos);
     c->last_was_pk = false;
     int rc;
     const int ne = c->n_embed, kvd = c->kv_dim;
@@ -736,9 +839,27 @@ extern "C" int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* 
         if (rc) return ctx_fail(ctx, rc);
     }
     hipSetDevice(ctx->device);
-    for (int i = 0; i < n; i++) {
-        int rc = enqueue_step(ctx, toks[i], pos0 + i);
+    if (use_fused(ctx)) {
+        /* the prompt goes to the device once; every replay of the step graph
+         * takes its token from it (PkStep.feed_end) */
+        LG_HIP_CHECK(hipStreamSynchronize(ctx->stream));   /* feed_host may back an earlier copy */
+        ctx->ring_pending = 0;
+        memcpy(ctx->feed_host + pos0, toks, (size_t)n * sizeof(int));
+        LG_HIP_CHECK(hipMemcpyAsync(ctx->feed_dev + pos0, ctx->feed_host + pos0, (size_t)n * sizeof(int),
+                                    hipMemcpyHostToDevice, ctx->stream));
+        int rc = fused_set_step(ctx, toks[0], pos0, pos0 + n);
+        for (int i = 0; !rc && i < n; i++) rc = fused_launch(ctx);
         if (rc) return ctx_fail(ctx, rc);
+        LG_HIP_CHECK(hipMemcpyAsync(ctx->pk_status_host, ctx->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost,
+                                    ctx->stream));
+        ctx->dev_known = false;
+        ctx->last_was_pk = true;
+        ctx->last_pos = pos0 + n - 1;
+    } else {
+        for (int i = 0; i < n; i++) {
+            int rc = enqueue_step(ctx, toks[i], pos0 + i);
+            if (rc) return ctx_fail(ctx, rc);
+        }
     }
     if (logits_host) {
         const hipError_t e = hipMemcpyAsync(logits_host, ctx->logits, (size_t)ctx->vocab * 4, hipMemcpyDeviceToHost, ctx->stream);

@@ -106,20 +106,29 @@ __device__ __forceinline__ void lg_q8k_block(const float v[4], uint8_t* __restri
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 0x7fffffff;
+    /* The first-index signed max of |x| as one 64-bit key: |x| bits (a
+     * non-negative float orders as an unsigned integer) above (255 - index)
+     * and the sign bit, so an unsigned max keeps the largest |x| and, among
+     * equal ones, the first index -- the strict '>' scan of the reference. */
+    float la = 0.0f;
+    uint32_t lo = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const float a = fabsf(v[j]);
-        if (a > amax) { amax = a; mx = v[j]; idx = 4 * lane + j; }
+        const bool take = a > la;
+        la = take ? a : la;
+        lo = take ? ((uint32_t)(255 - (4 * lane + j)) << 1) | (uint32_t)(v[j] < 0.0f) : lo;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float oa = __shfl_xor(amax, o, 64);
-        const float om = __shfl_xor(mx, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
+    uint64_t key = ((uint64_t)__float_as_uint(la) << 32) | lo;
+    auto step = [&](uint64_t o) { key = o > key ? o : key; };
+    step(((uint64_t)(uint32_t)lg_partner<0>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<0>((int)key));
+    step(((uint64_t)(uint32_t)lg_partner<1>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<1>((int)key));
+    step(((uint64_t)(uint32_t)lg_partner<2>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<2>((int)key));
+    step(((uint64_t)(uint32_t)lg_partner<3>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<3>((int)key));
+    step(((uint64_t)(uint32_t)lg_partner<4>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<4>((int)key));
+    step(((uint64_t)(uint32_t)lg_partner<5>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<5>((int)key));
+    const float amax = __uint_as_float((uint32_t)(key >> 32));
+    const float mx = (key & 1u) ? -amax : amax;
     uint32_t packed = 0;
     int s = 0;
     if (amax != 0.0f) {
@@ -133,8 +142,7 @@ __device__ __forceinline__ void lg_q8k_block(const float v[4], uint8_t* __restri
             packed |= (uint32_t)(t & 255) << (8 * j);
         }
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s = lg_group_isum<4>(s);
     *(uint32_t*)(out + 4 + 4 * lane) = packed;
     if ((lane & 3) == 0) *(int16_t*)(out + 260 + 2 * (lane >> 2)) = (int16_t)s;
     if (lane == 0) *(float*)out = amax != 0.0f ? mx * (-1.0f / 127.0f) : 0.0f;
@@ -153,9 +161,7 @@ __device__ __forceinline__ void lg_q8_0_blocks(const float v[4], uint8_t* __rest
         const float a = fabsf(v[j]);
         if (amax < a) amax = a;
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = lg_group_max<8>(amax);
     const int blk = lane >> 3;
     if (32 * blk >= nvalid) return;
     const float d = amax * (1.0f / 127.0f);

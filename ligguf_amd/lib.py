@@ -22,7 +22,7 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q1_0: (32, 6), Q1_G: (128, 18
          Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
 
 ARCH_LLAMA, ARCH_QWEN3 = 0, 1
-PATH_AUTO, PATH_PERSISTENT, PATH_MULTI = 0, 1, 2
+PATH_AUTO, PATH_PERSISTENT, PATH_MULTI, PATH_FUSED = 0, 1, 2, 3
 
 _vp = C.c_void_p
 

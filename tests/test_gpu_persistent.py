@@ -1,29 +1,35 @@
-"""The persistent one-launch-per-token decode kernel (LG_PATH_PERSISTENT)
-against the oracle and against the multi-kernel path.
+"""The whole-step decode kernels for n_embed 4096 models -- the fused
+per-phase kernels replayed from a HIP graph (LG_PATH_FUSED) and the
+persistent one-launch kernel (LG_PATH_PERSISTENT) -- against the oracle and
+against the multi-kernel path.
 
-Both GPU paths compute the matvecs, norms and quantizers with the same slot
-order and lane reductions; attention differs in fp32 order only (the
-persistent kernel runs one online-softmax pass per unit, the multi-kernel
-path a three-pass softmax per chunk).  So on the same KV state their logits
+All GPU paths compute the matvecs, norms and quantizers with the same slot
+order and lane reductions.  FUSED and PERSISTENT share their phase code and
+attention split, so they agree bit for bit; against the multi-kernel path
+attention differs in fp32 order only (one online-softmax pass per unit
+against a three-pass softmax per chunk).  On the same KV state logits then
 agree to ~1e-7 except where that rounding moves one activation across an
-int8 rounding boundary (see test_gpu_decode.py): the bounds below are the
-one-step parity bounds used against the oracle."""
+int8 rounding boundary (see test_gpu_decode.py): the cross-path bounds below
+are the one-step parity bounds used against the oracle."""
+import os
+
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import PATH_MULTI, PATH_PERSISTENT, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0
+from ligguf_amd.lib import PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0
 from ligguf_amd.model import Engine, HostModel, ModelConfig
 from test_gpu_decode import one_step_errors, rel
 
 pytestmark = pytest.mark.gpu
 
-# two-layer models at the Qwen3-8B widths the persistent kernel is built for
+# two-layer models at the Qwen3-8B widths the whole-step kernels are built for
 PK_MODELS = [
     ModelConfig("qwen3-w4096-q4k", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
     ModelConfig("qwen3-w4096-q1g", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q1_G, Q8_0, Q8_0,
                 q1_direct=True),
     ModelConfig("llama-w4096-q5k", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q5_K, Q8_0, Q4_K),
 ]
+WHOLE = [PATH_FUSED, PATH_PERSISTENT]
 
 
 @pytest.fixture(scope="module", params=PK_MODELS, ids=lambda c: c.name)
@@ -36,47 +42,54 @@ def pk_model(request, gpu):
     eng.close()
 
 
-def test_persistent_path_available(pk_model):
+def test_paths_available(pk_model):
     hm, eng = pk_model
-    eng.set_path(PATH_PERSISTENT)
-    assert eng.path() == PATH_PERSISTENT
-    eng.set_path(PATH_MULTI)
-    assert eng.path() == PATH_MULTI
+    eng.set_path(0)
+    assert eng.path() == PATH_FUSED          # AUTO picks the fused graph for these models
+    for p in (PATH_PERSISTENT, PATH_MULTI, PATH_FUSED):
+        eng.set_path(p)
+        assert eng.path() == p
 
 
-def test_persistent_one_step_parity_with_oracle(pk_model, oracle):
+@pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
+def test_one_step_parity_with_oracle(pk_model, oracle, path):
     hm, eng = pk_model
-    eng.set_path(PATH_PERSISTENT)
+    eng.set_path(path)
     toks = np.random.default_rng(5).integers(1, hm.cfg.vocab, 6)
     errs, agree = one_step_errors(eng, oracle, hm, toks)
-    print(f"\n{hm.cfg.name}: median {np.median(errs):.2e} max {errs.max():.2e}")
+    print(f"\n{hm.cfg.name} path {path}: median {np.median(errs):.2e} max {errs.max():.2e}")
     assert np.median(errs) <= 1e-5
     assert errs.max() <= 2e-2
     assert agree.mean() >= 0.8
 
 
-def run_both(eng, toks, pos0=0):
-    """Greedy-free replay of toks on each path from a zeroed cache: logits of
-    every step and the in-kernel argmax."""
-    out = {}
-    for path in (PATH_MULTI, PATH_PERSISTENT):
-        eng.set_path(path)
-        logits, am = [], []
-        for i, t in enumerate(toks):
-            logits.append(eng.decode(int(t), pos0 + i))
-            am.append(eng.argmax())
-        out[path] = (np.array(logits), am)
-    return out
+def replay(eng, path, toks, pos0=0):
+    """toks fed one synchronous step at a time (lg_decode_step + lg_argmax)."""
+    eng.set_path(path)
+    logits, am = [], []
+    for i, t in enumerate(toks):
+        logits.append(eng.decode(int(t), pos0 + i))
+        am.append(eng.argmax())
+    return np.array(logits), am
 
 
-def test_persistent_matches_multikernel(pk_model):
+def test_fused_equals_persistent_bitwise(pk_model):
+    hm, eng = pk_model
+    toks = np.random.default_rng(11).integers(1, hm.cfg.vocab, 10)
+    lf, af = replay(eng, PATH_FUSED, toks)
+    lp, ap = replay(eng, PATH_PERSISTENT, toks)
+    assert np.array_equal(lf.view(np.uint32), lp.view(np.uint32))
+    assert af == ap
+
+
+@pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
+def test_matches_multikernel(pk_model, path):
     hm, eng = pk_model
     toks = np.random.default_rng(11).integers(1, hm.cfg.vocab, 12)
-    out = run_both(eng, toks)
-    lm, am = out[PATH_MULTI]
-    lp, ap = out[PATH_PERSISTENT]
+    lm, am = replay(eng, PATH_MULTI, toks)
+    lp, ap = replay(eng, path, toks)
     errs = np.array([rel(a, b) for a, b in zip(lp, lm)])
-    print(f"\n{hm.cfg.name}: persistent vs multi median {np.median(errs):.2e} max {errs.max():.2e}")
+    print(f"\n{hm.cfg.name} path {path} vs multi: median {np.median(errs):.2e} max {errs.max():.2e}")
     assert np.median(errs) <= 1e-6
     assert errs.max() <= 2e-2
     assert np.mean(np.array(ap) == np.array(am)) >= 0.9
@@ -84,10 +97,11 @@ def test_persistent_matches_multikernel(pk_model):
     assert ap == [int(np.argmax(v)) for v in lp]
 
 
-def test_persistent_long_context_attention(pk_model):
-    """Decode at a long position over a random fp16 cache: the persistent
-    split (one unit per workgroup, chunks up to 512) against the multi-kernel
-    split (about 64 chunks), from the same cache rows."""
+@pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
+def test_long_context_attention(pk_model, path):
+    """Decode at a long position over a random fp16 cache: the whole-step
+    split (about one (kv head, chunk) unit per workgroup, merged by the last
+    unit) against the multi-kernel split, from the same cache rows."""
     hm, eng = pk_model
     cfg = hm.cfg
     pos = min(cfg.n_context - 1, 3001)
@@ -97,22 +111,22 @@ def test_persistent_long_context_attention(pk_model):
         v = rng.standard_normal(pos * cfg.kv_dim).astype(np.float16).view(np.uint16)
         eng.kv_write(l, 1, 0, pos, k, v)
     res = {}
-    for path in (PATH_MULTI, PATH_PERSISTENT):
-        eng.set_path(path)
-        res[path] = eng.decode(7, pos)
-        eng.set_path(PATH_MULTI)
-    e = rel(res[PATH_PERSISTENT], res[PATH_MULTI])
-    print(f"\n{cfg.name}: pos {pos} persistent vs multi {e:.2e}")
+    for p in (PATH_MULTI, path):
+        eng.set_path(p)
+        res[p] = eng.decode(7, pos)
+    e = rel(res[path], res[PATH_MULTI])
+    print(f"\n{cfg.name} path {path}: pos {pos} vs multi {e:.2e}")
     assert e <= 2e-2
 
 
-def test_persistent_prefill_equals_sequential_and_greedy(pk_model):
-    """lg_prefill on the persistent path equals the same tokens fed one
-    lg_decode_step at a time, bit for bit (feed_text's prompt loop,
-    fast/ligguf_fast_qk.cpp:340-356), and the in-kernel greedy token of every
-    step of a free-running loop is sampler_greedy of that step's logits."""
+@pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
+def test_prefill_equals_sequential_and_greedy(pk_model, path):
+    """lg_prefill equals the same tokens fed one lg_decode_step at a time, bit
+    for bit (feed_text's prompt loop, fast/ligguf_fast_qk.cpp:340-356), and the
+    in-kernel greedy token of every step of a free-running loop is
+    sampler_greedy of that step's logits."""
     hm, eng = pk_model
-    eng.set_path(PATH_PERSISTENT)
+    eng.set_path(path)
     prompt = np.random.default_rng(9).integers(1, hm.cfg.vocab, 20)
     lg_prefill = eng.prefill(prompt, 0)
     for i, t in enumerate(prompt):
@@ -124,3 +138,34 @@ def test_persistent_prefill_equals_sequential_and_greedy(pk_model):
         nxt = eng.argmax()
         assert nxt == int(np.argmax(lg))
         tok, pos = nxt, pos + 1
+
+
+def test_graph_replays_equal_direct_launches(pk_model):
+    """The captured step graph, replayed over several tokens with host work
+    and synchronisations between replays (and a host-chosen token that forces
+    a step-record update), gives every replay the bits of the same kernels
+    launched directly."""
+    hm, eng = pk_model
+    os.environ["LG_NO_GRAPH"] = "1"
+    try:
+        direct = Engine(0)
+        direct.load(hm)
+    finally:
+        del os.environ["LG_NO_GRAPH"]
+    eng.set_path(PATH_FUSED)
+    direct.set_path(PATH_FUSED)
+    outs = {}
+    for name, e in (("graph", eng), ("direct", direct)):
+        seq, tok = [], 5
+        for pos in range(14):
+            if pos == 7:
+                tok = 3                      # host-chosen token mid-run
+            e.decode_async(tok, pos)
+            tok = e.argmax()
+            seq.append((tok, e.decode(tok, pos + 1) if pos == 13 else None))
+        outs[name] = seq
+    direct.close()
+    for (ta, la), (tb, lb) in zip(outs["graph"], outs["direct"]):
+        assert ta == tb
+        if la is not None:
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
