@@ -4,8 +4,8 @@
  * (fast/lil_math.h:5-39, fast/lil_math.cpp, fast/arch_avx2.h) and the inline
  * per-token sequence of inference() (fast/ligguf_fast_qk.cpp:24-144).  The
  * reference's host code -- GGUF loader, tokenizer, samplers, chat and state
- * save -- keeps running on the CPU and calls this layer; the maintainer-side
- * binding is shown in INTEGRATION.md.
+ * save -- keeps running on the CPU and calls this layer at model upload, per
+ * step and for KV state I/O.
  *
  * Conventions
  *   - Every entry point returns LG_OK (0) or a negative LG_ERR_* code and

@@ -15,6 +15,7 @@
  * fp32 activations x, q|k|v, att, hb|hb2, logits; quantized activations
  * in Q8_K and/or Q8_0 form.
  */
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -131,7 +132,6 @@ struct lg_ctx {
     int path = LG_PATH_AUTO;
     int pk_nwg = 0;
     PkParams pk = {};
-    PkParams* pk_dev = nullptr;      /* device copy of pk */
     const void* pk_kernel = nullptr; /* the instantiation for this model */
     uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
     uint64_t pk_base = 0;
@@ -140,6 +140,7 @@ struct lg_ctx {
 
     /* fused per-phase kernels replayed from a HIP graph (lg_fused.hip) */
     const void* fused_fn = nullptr;
+    std::vector<PkLayer> pk_layers;  /* host copy: the fused kernels take their layer by value */
     PkStep* step_dev = nullptr;      /* {tok, pos, feed_end} the next fused step reads */
     PkStep* step_ring = nullptr;     /* pinned slots for host updates of step_dev */
     int ring_next = 0, ring_pending = 0;
@@ -296,7 +297,13 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     ctx->pk_kernel = nullptr;
     const int nrep = m->n_heads / m->n_kv_heads;
     const int lt = ctx->layers.empty() ? -1 : ctx->layers[0].q.type;
-    bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && m->n_context <= PK_MAX_CHUNK * PK_MAX_UNITS_PER_HEAD &&
+    /* attention partials per head and layer: PK_ATT_MERGE chunks, or full
+     * units (pk_attn_split) at the longest context */
+    int att_chunk = 0, att_nch = 0;
+    if (m->head_dim > 0 && m->head_dim <= 128 && nrep >= 1 && nrep <= PK_MAX_NREP)
+        pk_attn_split(m->n_context, m->head_dim, nrep, &att_chunk, &att_nch);
+    att_nch = std::max(att_nch, PK_ATT_MERGE);
+    bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
               m->n_kv_heads <= 32 && ctx->output.cols == m->n_embed;
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
@@ -321,6 +328,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     PkLayer* dl = nullptr;
     if ((rc = dalloc(ctx, (void**)&dl, hl.size() * sizeof(PkLayer)))) return rc;
     LG_HIP_CHECK(hipMemcpy(dl, hl.data(), hl.size() * sizeof(PkLayer), hipMemcpyHostToDevice));
+    ctx->pk_layers = hl;
     PkParams& P = ctx->pk;
     P = PkParams{};
     P.layers = dl;
@@ -335,17 +343,25 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     {
         /* per-layer activation buffers, each written once per step */
         const size_t L = (size_t)m->n_layers, ne = m->n_embed, qs = ne + 2 * m->kv_dim, ff = m->n_ff;
-        const size_t floats = (L + 1) * ne + L * ne + L * qs + L * ne + L * ff;
+        const size_t floats = (L + 1) * ne + L * ne + L * qs + L * ff;
         float* arena = nullptr;
         if ((rc = dalloc(ctx, (void**)&arena, floats * sizeof(float)))) return rc;
         P.xs = arena;
         P.xm = P.xs + (L + 1) * ne;
         P.qkv = P.xm + L * ne;
-        P.att = P.qkv + L * qs;
-        P.hb = P.att + L * ne;
+        P.hb = P.qkv + L * qs;
     }
-    const size_t ws = (size_t)m->n_kv_heads * PK_MAX_UNITS_PER_HEAD * nrep * (m->head_dim + 2) * sizeof(float);
-    if ((rc = dalloc(ctx, (void**)&P.attn_ws, ws))) return rc;
+    {
+        /* per-layer attention partials, each written once per step */
+        const size_t L = (size_t)m->n_layers;
+        float* ws = nullptr;
+        const size_t slots = (size_t)att_nch + 1;
+        if ((rc = dalloc(ctx, (void**)&ws, L * slots * ((size_t)m->n_embed + 2 * m->n_heads) * sizeof(float))))
+            return rc;
+        P.att_slots = (int)slots;
+        P.att_po = ws;
+        P.att_pml = ws + L * slots * m->n_embed;
+    }
     /* one zeroed block for the counters and flags */
     const int nwg = ctx->pk_nwg;
     const size_t cnt_bytes = 256 + (size_t)nwg * (8 + 4 + 4) + 64;
@@ -372,8 +388,6 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     if (!ctx->step_ring) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->step_ring, LG_STEP_RING * sizeof(PkStep), 0));
     ctx->ring_next = ctx->ring_pending = 0;
     ctx->fused_fn = lg_fused_variant(lt, ctx->output.type, m->head_dim, nrep);
-    if ((rc = dalloc(ctx, (void**)&ctx->pk_dev, sizeof(PkParams)))) return rc;
-    LG_HIP_CHECK(hipMemcpy(ctx->pk_dev, &P, sizeof(PkParams), hipMemcpyHostToDevice));
     if (!ctx->pk_status_host) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->pk_status_host, 2 * sizeof(int), 0));
     ctx->pk_base = 0;
     ctx->pk_kernel = kern;
@@ -422,7 +436,7 @@ static int fused_launch(lg_ctx* c)
     if (c->use_graph && !c->graph) {
         hipGraph_t g = nullptr;
         LG_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = lg_fused_enqueue(c->fused_fn, c->pk_dev, c->step_dev, c->n_layers, c->pk_nwg, c->stream);
+        const int rc = lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg, c->stream);
         const hipError_t ec = hipStreamEndCapture(c->stream, &g);
         if (rc || ec != hipSuccess) {
             if (g) hipGraphDestroy(g);
@@ -441,7 +455,7 @@ static int fused_launch(lg_ctx* c)
         LG_HIP_CHECK(hipGraphLaunch(c->graph, c->stream));
         return LG_OK;
     }
-    return lg_fused_enqueue(c->fused_fn, c->pk_dev, c->step_dev, c->n_layers, c->pk_nwg, c->stream);
+    return lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg, c->stream);
 }
 
 static int enqueue_fused(lg_ctx* c, int tok, int pos)
@@ -461,15 +475,11 @@ static int enqueue_fused(lg_ctx* c, int tok, int pos)
 static int enqueue_pk(lg_ctx* c, int tok, int pos)
 {
     PkParams& P = c->pk;
-    const int ctx_len = pos + 1;
-    int chunk, nch;
-    pk_attn_split(ctx_len, c->n_kv_heads, c->pk_nwg, &chunk, &nch);
-    if (nch > PK_MAX_UNITS_PER_HEAD) { lg_set_error("persistent decode: context %d too long", ctx_len); return LG_ERR_STATE; }
-    PkStep S;
-    S.tok = tok; S.pos = pos; S.chunk = chunk; S.nch = nch; S.base = c->pk_base;
+    PkStep S = {};
+    S.tok = tok; S.pos = pos; S.base = c->pk_base;
     S.trace = c->pk_trace;
     c->pk_trace = nullptr;   /* one step only */
-    int rc = lg_persist_launch(c->pk_kernel, c->pk_dev, &S, c->pk_nwg, c->stream);
+    int rc = lg_persist_launch(c->pk_kernel, c->pk, &S, c->pk_nwg, c->stream);
     if (rc) return rc;
     c->pk_base += 5ull * c->n_layers + 1;
     LG_HIP_CHECK(hipMemcpyAsync(c->pk_status_host, P.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
@@ -591,9 +601,14 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
     if ((rc = upload_weight(ctx, m->token_embd, ctx->embd))) return rc;
     if ((rc = upload_weight(ctx, m->output, ctx->output))) return rc;
     if ((rc = upload_floats(ctx, m->output_norm, m->n_embed, &ctx->out_norm, "output_norm"))) return rc;
-    const int nfreq = m->rope_dim / 2 > 0 ? m->rope_dim / 2 : 1;
-    if (m->rope_dim > 0) {
-        if ((rc = upload_floats(ctx, m->rope_freq, nfreq, &ctx->rope_freq, "rope_freq"))) return rc;
+    {
+        /* rope table padded with zeros to at least head_dim floats: the
+         * whole-step attention loads a fixed slice per lane */
+        const int nfreq = m->rope_dim / 2 > 0 ? m->rope_dim / 2 : 0;
+        const size_t nalloc = std::max<size_t>((size_t)std::max(nfreq, m->head_dim), 1);
+        std::vector<float> tab(nalloc, 0.0f);
+        if (nfreq) std::copy(m->rope_freq, m->rope_freq + nfreq, tab.begin());
+        if ((rc = upload_floats(ctx, tab.data(), nalloc, &ctx->rope_freq, "rope_freq"))) return rc;
     }
     ctx->layers.resize(m->n_layers);
     for (int l = 0; l < m->n_layers; l++) {

@@ -5,15 +5,20 @@
  * Per layer l (one workgroup of 8 waves per CU in every kernel):
  *   qkv   rmsnorm(x)->Q8 in LDS (every workgroup), Q|K|V rows      -> qkv[l]
  *   attn  QK-norm + RoPE + fp16 KV write of row pos, one-pass online
- *         softmax over (kv head, chunk) units, last unit of a head
- *         merges the partials (atomic counter)                   -> att[l]
- *   ao    Q8(att) in LDS, att_out rows + residual                 -> xm[l]
+ *         softmax over (kv head, chunk) units               -> partials
+ *   ao    merge of the partials, Q8(att) in LDS, att_out rows
+ *         + residual                                              -> xm[l]
  *   ug    rmsnorm(xm)->Q8, up|gate row pairs + SwiGLU             -> hb[l]
  *   down  Q8(hb) in LDS, down rows + residual                     -> xs[l+1]
  * then out: rmsnorm -> output rows -> logits, per-WG argmax, the last
  * workgroup reduces it (sampler_greedy, fast/ligguf_fast_qk.cpp:146-160) and
  * advances the device step record to {token, pos + 1}.
  *
+ * The parameter block and the layer's weights are kernel arguments (by
+ * value): pointers read from them are known to be global, so every access
+ * is a global_load/store -- a
+ * flat access would also count against lgkmcnt, and each LDS wait of a
+ * build would then wait for all of the wave's outstanding weight loads.
  * Every kernel issues its weight loads first and builds its activation
  * while they are in flight; the kernel boundary is the only sync (a graph
  * replays 5*n_layers + 1 kernels at ~1.6 us of fixed cost each, cheaper than
@@ -30,74 +35,62 @@ __device__ __forceinline__ uint64_t* f_tr(const PkStep* Sd, int l, int k)
     return t ? t + ((size_t)(5 * l + k) * gridDim.x + blockIdx.x) * 4 : nullptr;
 }
 
-template <int LT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams* __restrict__ Pp, const PkStep* __restrict__ Sd,
+/* EMB: layer 0, whose input is the embedding row of the step's token */
+template <int LT, bool EMB>
+__global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                       int l)
 {
-    const PkParams& P = *Pp;
-    const PkLayer& L = P.layers[l];
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
     float* xin = P.xs + (size_t)l * ne;
     const int pos = Sd->pos;
     const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
-    phase_mv<LT, NE, Batch<LT, NE, 1, 4, 288>::value, 1, EPI_STORE, BLD_RMS, 2, true>(
-        P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, l == 0 ? nullptr : xin, nullptr, P.qkv + (size_t)l * qs, xin,
-        0, 0, f_tr(Sd, l, 0));
+    phase_mv<LT, NE, Batch<LT, NE, 1, 3, 512>::value, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, 2, false>(
+        P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, P.qkv + (size_t)l * qs, xin, 0, 0,
+        f_tr(Sd, l, 0));
 }
 
 template <int HD, int NREP>
-__global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams* __restrict__ Pp, const PkStep* __restrict__ Sd,
+__global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                        int l)
 {
-    const PkParams& P = *Pp;
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
-    const int pos = Sd->pos;
-    int chunk, nch;
-    pk_attn_split(pos + 1, P.n_kv, gridDim.x, &chunk, &nch);
-    phase_attn<HD, NREP>(P, l, pos, chunk, nch, P.qkv + (size_t)l * qs, P.att + (size_t)l * ne, 0, 0, f_tr(Sd, l, 1));
+    phase_attn<HD, NREP>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
 }
 
-template <int LT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams* __restrict__ Pp, const PkStep* __restrict__ Sd, int l)
+template <int LT, int HD, int NREP>
+__global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
 {
-    const PkParams& P = *Pp;
-    const PkLayer& L = P.layers[l];
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed;
-    phase_mv<LT, NE, Batch<LT, NE, 1, 4, 288>::value, 1, EPI_RESID, BLD_PLAIN, 2, true>(
-        P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, P.att + (size_t)l * ne, P.xs + (size_t)l * ne, P.xm + (size_t)l * ne,
-        nullptr, 0, 0, f_tr(Sd, l, 2));
+    phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_RESID, BLD_MERGE, 2, false>(
+        P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, P.xs + (size_t)l * ne, P.xm + (size_t)l * ne, nullptr, 0, 0,
+        f_tr(Sd, l, 2), att_partials<HD, NREP>(P, l, Sd->pos));
 }
 
 template <int LT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams* __restrict__ Pp, const PkStep* __restrict__ Sd, int l)
+__global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
 {
-    const PkParams& P = *Pp;
-    const PkLayer& L = P.layers[l];
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NE, Batch<LT, NE, 2, 6, 288>::value, 2, EPI_SWIGLU, BLD_RMS, 2, true>(
+    phase_mv<LT, NE, Batch<LT, NE, 2, 6, 512>::value, 2, EPI_SWIGLU, BLD_RMS, 2, false>(
         P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, P.xm + (size_t)l * ne, nullptr, P.hb + (size_t)l * nff, nullptr, 0,
         0, f_tr(Sd, l, 3));
 }
 
 template <int LT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams* __restrict__ Pp, const PkStep* __restrict__ Sd, int l)
+__global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
 {
-    const PkParams& P = *Pp;
-    const PkLayer& L = P.layers[l];
     constexpr int NF = 3 * NsE<LT>::value;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NF, Batch<LT, NF, 1, 4, 288>::value, 1, EPI_RESID, BLD_PLAIN, 6, true>(
+    phase_mv<LT, NF, Batch<LT, NF, 1, 2, 512>::value, 1, EPI_RESID, BLD_PLAIN, 6, false>(
         P, 0, L.down, L.down_rsz, ne, 0, nullptr, P.hb + (size_t)l * nff, P.xm + (size_t)l * ne,
         P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4));
 }
 
 template <int OT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams* __restrict__ Pp, PkStep* __restrict__ Sd)
+__global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* __restrict__ Sd)
 {
-    const PkParams& P = *Pp;
     constexpr int NO = NsE<OT>::value;
     const int pos = Sd->pos;
     phase_mv<OT, NO, Batch<OT, NO, 1, 4, 288>::value, 1, EPI_LOGITS, BLD_RMS, 2, true>(
@@ -114,18 +107,19 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams* __restrict
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-typedef void (*fused_enqueue_t)(const PkParams*, PkStep*, int, int, hipStream_t);
+typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, hipStream_t);
 
 template <int LT, int OT, int HD, int NREP>
-static void fused_enqueue(const PkParams* P, PkStep* S, int n_layers, int nwg, hipStream_t st)
+static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n_layers, int nwg, hipStream_t st)
 {
     const dim3 g(nwg), b(PK_THREADS);
     for (int l = 0; l < n_layers; l++) {
-        hipLaunchKernelGGL((k_f_qkv<LT>), g, b, 0, st, P, S, l);
-        hipLaunchKernelGGL((k_f_attn<HD, NREP>), g, b, 0, st, P, S, l);
-        hipLaunchKernelGGL((k_f_ao<LT>), g, b, 0, st, P, S, l);
-        hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, S, l);
-        hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, S, l);
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l);
+        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l);
+        hipLaunchKernelGGL((k_f_attn<HD, NREP>), g, b, 0, st, P, Lh[l], S, l);
+        hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l);
+        hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l);
+        hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l);
     }
     hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S);
 }
@@ -152,8 +146,9 @@ const void* lg_fused_variant(int lt, int ot, int hd, int nrep)
     return nullptr;
 }
 
-int lg_fused_enqueue(const void* variant, const PkParams* P_dev, PkStep* S_dev, int n_layers, int nwg, hipStream_t s)
+int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
+                     hipStream_t s)
 {
-    ((fused_enqueue_t)variant)(P_dev, S_dev, n_layers, nwg, s);
+    ((fused_enqueue_t)variant)(P, layers, S_dev, n_layers, nwg, s);
     return lg_check_launch("fused decode step");
 }

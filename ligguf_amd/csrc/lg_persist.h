@@ -9,8 +9,8 @@
 #define PK_MAX_EMBED 8192   /* n_embed limit (fp32 staging of x in LDS) */
 #define PK_MAX_FF 16384     /* n_ff limit (quantized activation in LDS) */
 #define PK_MAX_NREP 8       /* query heads per KV head */
-#define PK_MAX_CHUNK 512    /* attention positions per unit */
-#define PK_MAX_UNITS_PER_HEAD 64
+#define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
+#define PK_ATT_MAX_NCH 160  /* attention partials per head at most (n_ctx <= 160 full units) */
 
 /* one layer as the kernel reads it: fused Q|K|V and up|gate matrices */
 struct PkLayer {
@@ -43,10 +43,11 @@ struct PkParams {
     float* xs;               /* [n_layers+1][n_embed] residual stream entering each layer */
     float* xm;               /* [n_layers][n_embed] after the attention residual */
     float* qkv;              /* [n_layers][n_embed + 2*kv_dim] */
-    float* att;              /* [n_layers][n_embed] */
     float* hb;               /* [n_layers][n_ff] */
     float* logits;
-    float* attn_ws;          /* n_kv * PK_MAX_UNITS_PER_HEAD partials of NREP*(head_dim+2) floats */
+    float* att_po;           /* [n_layers][att_slots][n_embed] unnormalised attention partials */
+    float* att_pml;          /* [n_layers][att_slots][n_heads][2] their (max, sum), log2 units */
+    int att_slots;           /* per layer: one per chunk, then one for the vector merged in-kernel */
     uint32_t* attn_cnt;      /* n_kv counters, zero between launches */
     uint64_t* progress;      /* one word per workgroup */
     float* amax_v;           /* per-workgroup argmax partials */
@@ -58,10 +59,10 @@ struct PkParams {
     int spin_cap;
 };
 
-/* what changes from token to token (a kernel argument; PkParams lives in
- * device memory, uploaded once per model) */
+/* what changes from token to token (PkParams, fixed per model, and PkStep
+ * are kernel arguments; the fused kernels read PkStep from device memory) */
 struct PkStep {
-    int tok, pos, nch, chunk;
+    int tok, pos;
     int feed_end;            /* fused path: positions below this take their token from PkParams.feed */
     int pad_;
     uint64_t base;           /* progress value at launch; the launch adds 5*n_layers + 1 */
@@ -69,14 +70,23 @@ struct PkStep {
                                 phase entry, wait done, activation built, phase published */
 };
 
-/* attention work split for a context of ctx_len positions: units of
- * (kv head, chunk) of about one per workgroup, 64..PK_MAX_CHUNK positions */
-__host__ __device__ inline void pk_attn_split(int ctx_len, int n_kv, int nwg, int* chunk_out, int* nch_out)
+/* attention work split.  A workgroup step covers ppb = PK_THREADS * 8 /
+ * head_dim positions (one 16-byte slice of a cache row per lane) and a unit
+ * (kv head, chunk) holds at most pk_att_steps(nrep) steps of K and V in
+ * registers.  Contexts up to PK_ATT_MERGE full units are cut into at most
+ * PK_ATT_MERGE chunks per head, whose partials the att_out build merges;
+ * longer ones into full units merged by the last unit of each head. */
+__host__ __device__ constexpr int pk_att_steps(int nrep)
 {
-    int chunk = (int)(((long long)ctx_len * n_kv + nwg - 1) / nwg);
-    chunk = (chunk + 31) / 32 * 32;
-    if (chunk < 64) chunk = 64;
-    if (chunk > PK_MAX_CHUNK) chunk = PK_MAX_CHUNK;
+    return nrep > 4 ? 4 : 8;
+}
+
+__host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nrep, int* chunk_out, int* nch_out)
+{
+    const int ppb = PK_THREADS * 8 / head_dim;
+    int chunk = (ctx_len + PK_ATT_MERGE - 1) / PK_ATT_MERGE;
+    chunk = (chunk + ppb - 1) / ppb * ppb;
+    if (chunk > pk_att_steps(nrep) * ppb) chunk = pk_att_steps(nrep) * ppb;
     *chunk_out = chunk;
     *nch_out = (ctx_len + chunk - 1) / chunk;
 }
@@ -85,11 +95,12 @@ __host__ __device__ inline void pk_attn_split(int ctx_len, int n_kv, int nwg, in
  * per KV head), or NULL: the model then runs on the multi-kernel path */
 const void* lg_persist_kernel(int layer_type, int out_type, int head_dim, int nrep);
 int lg_persist_grid(const void* kernel, int* nwg);
-int lg_persist_launch(const void* kernel, const PkParams* P_dev, const PkStep* S, int nwg, hipStream_t s);
+int lg_persist_launch(const void* kernel, const PkParams& P, const PkStep* S, int nwg, hipStream_t s);
 
 /* the fused per-phase kernels of one step (lg_fused.hip): 5*n_layers + 1
  * launches on stream s reading {tok, pos} from S_dev; the last one writes the
  * greedy token to P->tok_out and advances S_dev to {token, pos + 1}.  NULL
  * when the variant is not instantiated. */
 const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep);
-int lg_fused_enqueue(const void* variant, const PkParams* P_dev, PkStep* S_dev, int n_layers, int nwg, hipStream_t s);
+int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
+                     hipStream_t s);

@@ -46,11 +46,11 @@
  * KV head): every phase body is inlined, so no call saves registers.
  * Activation buffers (each written once per launch): xs[l] = residual stream
  * entering layer l (xs[0] the embedding row, xs[L] the output of the last
- * layer), xm[l] = after attention, qkv[l], att[l], hb[l]. */
+ * layer), xm[l] = after attention, qkv[l], hb[l]; the attention partials
+ * (att_po/att_pml) are per layer too. */
 template <int LT, int OT, int HD, int NREP>
-__global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams* __restrict__ Pp, PkStep S)
+__global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams P, PkStep S)
 {
-    const PkParams& P = *Pp;
     const int ne = P.n_embed, kvd = P.kv_dim, nff = P.n_ff;
     const int qs = ne + 2 * kvd;
     const uint64_t B = S.base;
@@ -64,17 +64,20 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
         float* xmid = P.xm + (size_t)l * ne;
         float* xout = P.xs + (size_t)(l + 1) * ne;
         float* qkv = P.qkv + (size_t)l * qs;
-        float* att = P.att + (size_t)l * ne;
         float* hb = P.hb + (size_t)l * nff;
         /* A: rmsnorm + QKV (layer 0 takes x from the embedding row, no wait) */
-        phase_mv<LT, NE, Batch<LT, NE, 1, 4>::value, 1, EPI_STORE, BLD_RMS, 2, false>(
-            P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, l == 0 ? nullptr : xin, nullptr, qkv, xin,
-            l == 0 ? 0 : p0, p0 + 1, TR(5 * l));
+        if (l == 0)
+            phase_mv<LT, NE, Batch<LT, NE, 1, 4>::value, 1, EPI_STORE, BLD_EMB, 2, false>(
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l));
+        else
+            phase_mv<LT, NE, Batch<LT, NE, 1, 4>::value, 1, EPI_STORE, BLD_RMS, 2, false>(
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l));
         /* B: attention */
-        phase_attn<HD, NREP>(P, l, S.pos, S.chunk, S.nch, qkv, att, p0 + 1, p0 + 2, TR(5 * l + 1));
-        /* C: att_out + residual */
-        phase_mv<LT, NE, Batch<LT, NE, 1, 4>::value, 1, EPI_RESID, BLD_PLAIN, 2, false>(
-            P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, att, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2));
+        phase_attn<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
+        /* C: merge of the attention partials, att_out + residual */
+        phase_mv<LT, NE, Batch<LT, NE, 1, 4>::value, 1, EPI_RESID, BLD_MERGE, 2, false>(
+            P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2),
+            att_partials<HD, NREP>(P, l, S.pos));
         /* D: rmsnorm + up|gate + SwiGLU */
         phase_mv<LT, NE, Batch<LT, NE, 2, 6>::value, 2, EPI_SWIGLU, BLD_RMS, 2, false>(
             P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, xmid, nullptr, hb, nullptr, p0 + 3, p0 + 4, TR(5 * l + 3));
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-typedef void (*pk_kernel_t)(const PkParams*, PkStep);
+typedef void (*pk_kernel_t)(const PkParams, PkStep);
 
 struct PkVariant {
     int lt, ot, hd, nrep;
@@ -132,9 +135,9 @@ int lg_persist_grid(const void* kernel, int* nwg)
     return LG_OK;
 }
 
-int lg_persist_launch(const void* kernel, const PkParams* P_dev, const PkStep* S, int nwg, hipStream_t s)
+int lg_persist_launch(const void* kernel, const PkParams& P, const PkStep* S, int nwg, hipStream_t s)
 {
-    const PkParams* p = P_dev;
+    PkParams p = P;
     PkStep st = *S;
     void* args[] = {&p, &st};
     LG_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(nwg), dim3(PK_THREADS), args, 0, s));

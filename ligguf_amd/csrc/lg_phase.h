@@ -26,7 +26,7 @@ __shared__ int s_int[8];
 /* attention */
 __shared__ __attribute__((aligned(16))) float s_q[PK_MAX_NREP * 128];
 __shared__ __attribute__((aligned(16))) float s_kv[2 * 128];
-__shared__ __attribute__((aligned(16))) float s_sc[PK_MAX_NREP * PK_MAX_CHUNK];
+__shared__ __attribute__((aligned(16))) float s_sc[3 * PK_ATT_MAX_NCH * PK_MAX_NREP];
 __shared__ __attribute__((aligned(16))) float s_o[PK_WAVES * PK_MAX_NREP * 128];
 __shared__ float s_m[PK_WAVES * PK_MAX_NREP];
 
@@ -50,6 +50,14 @@ __device__ __forceinline__ float2 cld2(const float* p)
 {
     const uint64_t u = cld((const uint64_t*)p);
     return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
+
+/* keeps the loads before it ahead of the loads after it in issue order (a
+ * wave's loads return in issue order, so what is needed first is issued
+ * first); no wait is implied */
+__device__ __forceinline__ void lg_issue_order()
+{
+    asm volatile("" ::: "memory");
 }
 
 /* workgroup barrier that orders LDS but leaves global loads in flight */
@@ -98,10 +106,18 @@ __device__ __forceinline__ void pk_wait(const PkParams& P, uint64_t target)
     bar();
 }
 
-/* phase timestamps (lane 0 of wave 0 of every WG; nothing when tr is NULL) */
+/* 2^x (v_exp_f32): attention scores are kept in log2 units */
+__device__ __forceinline__ float lg_exp2(float x)
+{
+    return __builtin_amdgcn_exp2f(x);
+}
+
+/* phase timestamps (lane 0 of wave 0 of every WG; nothing when tr is NULL).
+ * The store goes through the global address space: a flat store would also
+ * count against lgkmcnt and make the next LDS wait wait for it. */
 __device__ __forceinline__ void stamp(uint64_t* tr, int k)
 {
-    if (tr && threadIdx.x == 0) tr[k] = wall_clock64();
+    if (tr && threadIdx.x == 0) *(__attribute__((address_space(1))) uint64_t*)(tr + k) = wall_clock64();
 }
 
 /* ------------------------------------------------------------------ */
@@ -114,7 +130,10 @@ __device__ __forceinline__ void stamp(uint64_t* tr, int k)
  * read with plain (L2-cached) loads: every activation buffer of a launch is
  * written exactly once, before anyone reads it, so no L2 holds a stale copy
  * (the launch starts with invalidated caches). */
-enum { BLD_RMS = 0, BLD_PLAIN = 1 };
+/* BLD_RMS: rmsnorm of the source vector; BLD_EMB: rmsnorm of the embedding
+ * row; BLD_PLAIN: the source vector as it is; BLD_MERGE: the attention
+ * partials merged (MergeSrc) */
+enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3 };
 
 __device__ __forceinline__ int chunk_base(int c)
 {
@@ -145,12 +164,75 @@ struct ActSrc {
     }
 };
 
+/* attention partials of one layer, merged by the att_out build (BLD_MERGE):
+ * the source vector is sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c,
+ * M = max_c m_c, over the nch chunks in ascending order */
+struct MergeSrc {
+    const float* po;     /* [nch][n_embed] */
+    const float* pml;    /* [nch][n_heads][2] */
+    int nch;             /* 1..PK_ATT_MERGE */
+    int head_dim;
+};
+
+template <int CPW>
+struct MergeAct {
+    float4 o[PK_ATT_MERGE][CPW];
+    float2 ml[PK_ATT_MERGE][CPW];
+
+    __device__ __forceinline__ void load(const MergeSrc& ms, int ne, int nh)
+    {
+#pragma unroll
+        for (int c = 0; c < PK_ATT_MERGE; c++) {
+            const int cc = min(c, ms.nch - 1);   /* unconditional loads (see Rows) */
+#pragma unroll
+            for (int k = 0; k < CPW; k++) {
+                const int b = chunk_base(k);
+                o[c][k] = *(const float4*)(ms.po + (size_t)cc * ne + b);
+                ml[c][k] = *(const float2*)(ms.pml + ((size_t)cc * nh + b / ms.head_dim) * 2);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void merge(int nch, ActSrc<CPW>& a) const
+    {
+#pragma unroll
+        for (int k = 0; k < CPW; k++) {
+            float M = ml[0][k].x;
+#pragma unroll
+            for (int c = 1; c < PK_ATT_MERGE; c++)
+                if (c < nch) M = fmaxf(M, ml[c][k].x);
+            float Ls = 0.0f;
+            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int c = 0; c < PK_ATT_MERGE; c++) {
+                if (c < nch) {
+                    const float w = lg_exp2(ml[c][k].x - M);
+                    Ls += ml[c][k].y * w;
+                    O.x += o[c][k].x * w; O.y += o[c][k].y * w; O.z += o[c][k].z * w; O.w += o[c][k].w * w;
+                }
+            }
+            a.v[k] = make_float4(O.x / Ls, O.y / Ls, O.z / Ls, O.w / Ls);
+        }
+    }
+};
+
+/* the attention partials of layer l at position pos as the att_out build
+ * reads them: the chunks (pk_attn_split), or the merged slot */
+template <int HD, int NREP>
+__device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int pos)
+{
+    int chunk, nch;
+    pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
+    const size_t slot = (size_t)l * P.att_slots + (nch > PK_ATT_MERGE ? P.att_slots - 1 : 0);
+    return MergeSrc{P.att_po + slot * P.n_embed, P.att_pml + slot * P.n_heads * 2, nch > PK_ATT_MERGE ? 1 : nch, HD};
+}
+
 /* rmsnorm(x) * w quantized into s_act (fast/lil_math.cpp:922-929 and
  * quantize_q8_K / quantize_q8_0, :329-394).  The sum of squares is taken by
  * one wave in the per-lane order of k_rmsnorm_quant, so both paths agree bit
- * for bit.  x is `src` or, for layer 0 (src == NULL), the embedding row of
- * tok, dequantized here; WG 0 also stores that row as the residual stream
- * `emb_out`. */
+ * for bit.  x is the source vector (BLD_RMS) or, for layer 0 (BLD_EMB), the
+ * embedding row of tok, dequantized here; WG 0 also stores that row as the
+ * residual stream `emb_out`. */
 template <int QT, int CPW>
 __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const NormW<CPW>& nw, const ActSrc<CPW>& xsrc,
                                           bool from_embed, float* __restrict__ emb_out)
@@ -221,23 +303,29 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 /* Items of one phase are split evenly over all waves of the grid in
  * contiguous runs; an item is K rows (K = 2 for up|gate: rows i and i+kstride)
- * each dotted by the whole wave (lane j owns slots j, j+64, ...). */
+ * each dotted by the whole wave (lane j owns slots j, j+64, ...).
+ *
+ * Every load of the hot path is unconditional (indices clamped to a valid
+ * item instead of a branch around the load): the compiler counts the loads
+ * still in flight with vmcnt, and where a load sits under a branch it must
+ * assume the shorter path and wait for every later load as well -- the
+ * activation build would then wait for all the wave's weights. */
 template <int FMT, int NS, int MAXB, int K>
 struct Rows {
     typename Fmt<FMT>::W w[MAXB][K][NS];
 
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, uint32_t rsz, int i0, int nb, int kstride,
+    /* items i0 .. i0+MAXB-1, those past `wlast` replaced by wlast */
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, uint32_t rsz, int i0, int wlast, int kstride,
                                          int lane)
     {
 #pragma unroll
         for (int b = 0; b < MAXB; b++) {
-            if (b < nb) {
+            const int i = min(i0 + b, wlast);
 #pragma unroll
-                for (int k = 0; k < K; k++) {
-                    const uint8_t* row = W + (size_t)(i0 + b + k * kstride) * rsz;
+            for (int k = 0; k < K; k++) {
+                const uint8_t* row = W + (size_t)(i + k * kstride) * rsz;
 #pragma unroll
-                    for (int s = 0; s < NS; s++) Fmt<FMT>::load_w(w[b][k][s], row, lane + 64 * s);
-                }
+                for (int s = 0; s < NS; s++) Fmt<FMT>::load_w(w[b][k][s], row, lane + 64 * s);
             }
         }
     }
@@ -256,7 +344,8 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                                          int items, int kstride, const float* __restrict__ normw,
                                          const float* __restrict__ src, const float* __restrict__ res_src,
                                          float* __restrict__ out, float* __restrict__ emb_out,
-                                         uint64_t wait_target, uint64_t sig, uint64_t* tr)
+                                         uint64_t wait_target, uint64_t sig, uint64_t* tr,
+                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0})
 {
     using F = Fmt<FMT>;
     constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q1_0 || FMT == LG_Q1_G) ? LG_Q8_0 : LG_Q8_K;
@@ -266,37 +355,50 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     const int ipw = (items + nwv - 1) / nwv;
     const int i0 = gw * ipw;
     const int my = max(0, min(items, i0 + ipw) - i0);
+    const int wlast = my > 0 ? i0 + my - 1 : items - 1;   /* clamp for the loads */
 
     stamp(tr, 0);
     Rows<FMT, NS, MAXB, K> R0;
     NormW<CPW> nw;
     ActSrc<CPW> as;
+    MergeAct<CPW> mg;
     float res[MAXB];
-    const bool from_embed = BLD == BLD_RMS && !src;
-    const int first = DB ? 1 : MAXB;
-    auto prefetch = [&]() {
-        R0.load(W, rsz, i0, min(my, first), kstride, lane);
+    constexpr bool from_embed = BLD == BLD_EMB;
+    constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
+    auto load_src = [&]() {
+        if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
+        else if (!from_embed) as.load(src);
+    };
+    auto load_res = [&](float* r, int b0) {
         if (EPI == EPI_RESID) {
 #pragma unroll
-            for (int b = 0; b < MAXB; b++) res[b] = b < min(my, first) ? res_src[i0 + b] : 0.0f;
+            for (int b = 0; b < MAXB; b++) r[b] = res_src[min(i0 + b0 + b, wlast)];
         }
+    };
+    auto prefetch = [&]() {
+        R0.load(W, rsz, i0, wlast, kstride, lane);
+        load_res(res, 0);
     };
     if (!wait_target) {
         /* no dependency wait (fused kernels): the activation and the norm
          * weights go first, the rows after them */
-        if (!from_embed) as.load(src);
-        if (BLD == BLD_RMS) nw.load(normw);
+        load_src();
+        if (rms) nw.load(normw);
+        lg_issue_order();   /* activation first */
         prefetch();
     } else {
-        if (BLD == BLD_RMS) nw.load(normw);
+        if (rms) nw.load(normw);
         if (wave != 0) prefetch();
         pk_wait(P, wait_target);
-        if (!from_embed) as.load(src);
+        load_src();
         if (wave == 0) prefetch();
     }
     stamp(tr, 1);
-    if (BLD == BLD_RMS) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out);
-    else build_plain<QT, CPW>(as);
+    if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out);
+    else {
+        if (BLD == BLD_MERGE) mg.merge(ms.nch, as);
+        build_plain<QT, CPW>(as);
+    }
     stamp(tr, 2);
 
     typename F::Act act[NS];
@@ -334,46 +436,24 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     };
     if (!DB) {
         for (int b0 = 0; b0 < my; b0 += MAXB) {
-            const int nb = min(MAXB, my - b0);
             if (b0 > 0) {
-                R0.load(W, rsz, i0 + b0, nb, kstride, lane);
-                if (EPI == EPI_RESID) {
-#pragma unroll
-                    for (int b = 0; b < MAXB; b++) res[b] = b < nb ? res_src[i0 + b0 + b] : 0.0f;
-                }
+                R0.load(W, rsz, i0 + b0, wlast, kstride, lane);
+                load_res(res, b0);
             }
-            process(R0, res, b0, nb);
+            process(R0, res, b0, min(MAXB, my - b0));
         }
     } else {
-        /* R0 holds the first FIRST items (issued before the build, so the
-         * activation loads are not queued behind a flood of rows); then
-         * two batches in flight: the next loads while this one computes */
+        /* two batches in flight: the next one loads while this one computes
+         * (the last iteration loads clamped duplicates it does not use) */
         Rows<FMT, NS, MAXB, K> R1;
         float res1[MAXB];
-        auto load_res = [&](float* r, int b0, int nb) {
-            if (EPI == EPI_RESID) {
-#pragma unroll
-                for (int b = 0; b < MAXB; b++) r[b] = b < nb ? res_src[i0 + b0 + b] : 0.0f;
-            }
-        };
-        int c0 = 0, n0 = min(my, first);
-        while (n0 > 0) {
-            const int c1 = c0 + n0;
-            const int n1 = min(MAXB, my - c1);
-            if (n1 > 0) {
-                R1.load(W, rsz, i0 + c1, n1, kstride, lane);
-                load_res(res1, c1, n1);
-            }
-            process(R0, res, c0, n0);
-            const int c2 = c1 + max(n1, 0);
-            const int n2 = n1 > 0 ? min(MAXB, my - c2) : 0;
-            if (n2 > 0) {
-                R0.load(W, rsz, i0 + c2, n2, kstride, lane);
-                load_res(res, c2, n2);
-            }
-            if (n1 > 0) process(R1, res1, c1, n1);
-            c0 = c2;
-            n0 = n2;
+        for (int b0 = 0; b0 < my; b0 += 2 * MAXB) {
+            R1.load(W, rsz, i0 + b0 + MAXB, wlast, kstride, lane);
+            load_res(res1, b0 + MAXB);
+            process(R0, res, b0, min(MAXB, my - b0));
+            R0.load(W, rsz, i0 + b0 + 2 * MAXB, wlast, kstride, lane);
+            load_res(res, b0 + 2 * MAXB);
+            process(R1, res1, b0 + MAXB, min(MAXB, my - b0 - MAXB));
         }
     }
     if (EPI == EPI_LOGITS) {
@@ -420,21 +500,26 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
 /* attention phase                                                      */
 /* ------------------------------------------------------------------ */
 /* One head of HD values held 4 per lane (lanes 4l < HD): Qwen3 QK RMSNorm
- * (when nw) and adjacent-pair RoPE, exactly as k_qk_norm_rope_kv. */
+ * (when has_norm, weights g of the lane's 4 values) and adjacent-pair RoPE
+ * (fr = the frequencies of the lane's two pairs), exactly as
+ * k_qk_norm_rope_kv. */
 template <int HD>
-__device__ __forceinline__ void norm_rope_head(float e[4], const float* __restrict__ nw, float eps, int rope_dim,
-                                               int pos, const float* __restrict__ freq)
+__device__ __forceinline__ void norm_rope_head(float e[4], bool has_norm, float4 g, float eps, int rope_dim, int pos,
+                                               float2 fr)
 {
     const int lane = threadIdx.x & 63;
     const bool act = 4 * lane < HD;
-    if (nw) {
-        float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
+    {
+        /* computed whether or not the model has QK norms, and selected: the
+         * weights' load is used unconditionally and stays where it is issued */
+        float ss = act ? e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3] : 0.0f;
         ss = lg_group_sum<64>(ss);
         const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-        if (act) {
-            const float4 g = *(const float4*)(nw + 4 * lane);
-            e[0] = e[0] * sc * g.x; e[1] = e[1] * sc * g.y; e[2] = e[2] * sc * g.z; e[3] = e[3] * sc * g.w;
-        }
+        const bool nrm = has_norm && act;
+        e[0] = nrm ? e[0] * sc * g.x : e[0];
+        e[1] = nrm ? e[1] * sc * g.y : e[1];
+        e[2] = nrm ? e[2] * sc * g.z : e[2];
+        e[3] = nrm ? e[3] * sc * g.w : e[3];
     }
     int rd = rope_dim < HD ? rope_dim : HD;
     rd &= ~1;
@@ -443,7 +528,7 @@ __device__ __forceinline__ void norm_rope_head(float e[4], const float* __restri
         for (int j = 0; j < 4; j += 2) {
             const int i = 4 * lane + j;
             if (i < rd) {
-                const float ang = (float)pos * freq[i >> 1];
+                const float ang = (float)pos * (j == 0 ? fr.x : fr.y);
                 float s, c;
                 sincosf(ang, &s, &c);
                 const float x0 = e[j], x1 = e[j + 1];
@@ -465,100 +550,144 @@ __device__ __forceinline__ void h8(const uint4& v, float f[8])
     }
 }
 
-/* combine two online-softmax states (running max m, sum l, weighted o) */
+/* combine two online-softmax states (max m and sum l in log2 units, weighted
+ * sum o); a state with m = -inf is empty */
 __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2, float l2, const float* o2, int n)
 {
     const float mn = fmaxf(m, m2);
-    const float a = m == -INFINITY ? 0.0f : expf(m - mn);
-    const float b = m2 == -INFINITY ? 0.0f : expf(m2 - mn);
+    const float a = m == -INFINITY ? 0.0f : lg_exp2(m - mn);
+    const float b = m2 == -INFINITY ? 0.0f : lg_exp2(m2 - mn);
     l = l * a + l2 * b;
     for (int i = 0; i < n; i++) o[i] = o[i] * a + o2[i] * b;
     m = mn;
 }
 
-/* Attention units (kv head g, chunk c of positions [c*chunk, ...) <= pos):
- * one pass over K and V with an online softmax per lane group; LPP lanes
- * hold one position (8 dims each), the step of a workgroup covers
- * PK_WAVES * 64/LPP positions, and the K/V loads of step s+1 are in flight
- * while step s computes (the first step's before the dependency wait: the
- * cache rows < pos do not depend on this token).  With one chunk per head
- * the unit writes att directly; otherwise it writes its (m, l, o) partial
- * and the last unit of the head (atomic counter) merges the partials. */
+/* Attention units (kv head g, chunk c of positions [c*chunk, ...) <= pos),
+ * split by pk_attn_split.  A unit issues all its loads at once -- the q/k/v
+ * heads of g and every K and V slice of its (at most pk_att_steps) steps,
+ * held in registers -- so it costs one memory round trip (with a dependency
+ * wait, the loads follow it).  Then QK-norm +
+ * RoPE of the heads into LDS, and one pass over the positions with an
+ * online softmax per lane group in log2 units (LPP lanes hold one position,
+ * 8 dims each); the lane groups of a wave combine by shuffles, the waves in
+ * LDS.  Output: the unit's unnormalised partial (o, and (m, l) per head),
+ * merged by the consumer's build (MergeSrc); past PK_ATT_MERGE chunks per
+ * head the last unit of the head (atomic counter) merges them into the
+ * layer's merged slot.  The unit of the head's last chunk also writes the fp16 cache
+ * row pos. */
 template <int HD, int NREP>
-__device__ __forceinline__ void phase_attn(const PkParams& P, int layer, int pos, int chunk, int nch,
-                                           const float* __restrict__ qkv, float* __restrict__ att,
-                                           uint64_t wait_target, uint64_t sig, uint64_t* tr)
+__device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
+                                           const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
+                                           uint64_t* tr)
 {
     constexpr int LPP = HD / 8;            /* lanes per position */
     constexpr int PPW = 64 / LPP;          /* positions per wave step */
     constexpr int PPB = PK_WAVES * PPW;    /* positions per WG step */
-    const PkLayer& L = P.layers[layer];
+    constexpr int MAXST = pk_att_steps(NREP);
+    constexpr int NH = (NREP + PK_WAVES) / PK_WAVES;   /* heads normed per wave: NREP q + 1 k */
+    static_assert(PPB == PK_THREADS * 8 / HD, "step geometry of pk_attn_split");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gl = lane & (LPP - 1), grp = lane / LPP;
     const int kvd = P.kv_dim;
+    int chunk, nch;
+    pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
     const int nunits = P.n_kv * nch;
     const size_t loff = (size_t)layer * P.n_ctx * kvd;
-    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale2 = 1.44269504088896341f / sqrtf((float)HD);   /* log2(e) / sqrt(head_dim) */
+    float* po = P.att_po + (size_t)layer * P.att_slots * P.n_embed;
+    float* pml = P.att_pml + (size_t)layer * P.att_slots * P.n_heads * 2;
+    /* the merged slot: written by nobody else in a launch, so no cache
+     * holds a stale copy of it */
+    float* po_m = po + (size_t)(P.att_slots - 1) * P.n_embed;
+    float* pml_m = pml + (size_t)(P.att_slots - 1) * P.n_heads * 2;
 
     stamp(tr, 0);
-    uint4 kb0, vb0, kb1, vb1;   /* K/V of two steps: static names, no indexed registers */
-    auto load_step = [&](int u, int st, uint4& kb, uint4& vb) {
+    uint4 kb[MAXST], vb[MAXST];   /* K/V slices of the unit's steps (static indices only) */
+    float4 hx[NH], hv;            /* this wave's heads h = wave + PK_WAVES*j: q (h < NREP) or k, and v */
+    /* unconditional loads (see Rows): positions outside the unit and the
+     * row pos itself (not in the cache yet) load the unit's first row */
+    auto load_kv = [&](int u) {
         const int g = u / nch, c = u % nch;
-        const int t = c * chunk + st * PPB + wave * PPW + grp;
-        const int t1 = min(c * chunk + chunk, pos + 1);
-        if (t < t1 && t != pos) {
+        const int t0 = c * chunk, t1 = min(t0 + chunk, pos + 1);
+#pragma unroll
+        for (int st = 0; st < MAXST; st++) {
+            int t = t0 + st * PPB + wave * PPW + grp;
+            t = t < t1 && t != pos ? t : t0;
             const size_t o = loff + (size_t)t * kvd + (size_t)g * HD + gl * 8;
-            kb = *(const uint4*)(P.kc + o);
-            vb = *(const uint4*)(P.vc + o);
+            kb[st] = *(const uint4*)(P.kc + o);
+            vb[st] = *(const uint4*)(P.vc + o);
         }
     };
+    /* q/k norm weights (a dummy slice of the rope table when the model has
+     * none) and the rope frequencies of the lane's two pairs */
+    const bool has_norm = L.q_norm != nullptr;
+    const int l4 = 4 * (lane & (HD / 4 - 1));
+    float4 ng[NH];
+    float2 fr;
+    auto load_heads = [&](int u) {
+        const int g = u / nch;
+#pragma unroll
+        for (int j = 0; j < NH; j++) {
+            const int h = min(wave + PK_WAVES * j, NREP);
+            const float* srcp = h < NREP ? qkv + (size_t)(g * NREP + h) * HD : qkv + P.n_embed + (size_t)g * HD;
+            hx[j] = *(const float4*)(srcp + l4);
+            const float* nwp = has_norm ? (h < NREP ? L.q_norm : L.k_norm) : P.rope_freq;
+            ng[j] = *(const float4*)(nwp + l4);
+        }
+        hv = *(const float4*)(qkv + P.n_embed + kvd + (size_t)g * HD + l4);
+        fr = *(const float2*)(P.rope_freq + l4 / 2);
+    };
     const bool has = (int)blockIdx.x < nunits;
-    if (has && (wave != 0 || !wait_target)) load_step(blockIdx.x, 0, kb0, vb0);
-    if (wait_target) {
-        pk_wait(P, wait_target);
-        if (has && wave == 0) load_step(blockIdx.x, 0, kb0, vb0);
-    }
-    stamp(tr, 1);
+    if (wait_target) pk_wait(P, wait_target);
+    if (!has) stamp(tr, 1);
 
     for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
         const int g = u / nch, c = u % nch;
         const int t0 = c * chunk;
         const int t1 = min(t0 + chunk, pos + 1);
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
-        if (u != (int)blockIdx.x) load_step(u, 0, kb0, vb0);
-        /* q heads g*NREP.., then k and v of g: normed/roped into LDS */
-        for (int h = wave; h <= NREP; h += PK_WAVES) {
+        load_heads(u);
+        lg_issue_order();   /* heads first, then K/V */
+        load_kv(u);
+        /* v of g into LDS, by every wave (the same values): an unconditional
+         * use keeps its load ahead of the K/V loads */
+        *(float4*)(s_kv + HD + l4) = hv;
+        /* q heads g*NREP.., then k of g: normed/roped into LDS (waves past
+         * the last head compute a copy and store nothing: the operands' loads
+         * are used unconditionally and stay where they are issued) */
+#pragma unroll
+        for (int j = 0; j < NH; j++) {
+            const int h = wave + PK_WAVES * j;
             const bool is_q = h < NREP;
-            const float* srcp = is_q ? qkv + (size_t)(g * NREP + h) * HD : qkv + P.n_embed + (size_t)g * HD;
-            float e[4] = {0.f, 0.f, 0.f, 0.f};
-            if (4 * lane < HD) {
-                const float4 t = *(const float4*)(srcp + 4 * lane);
-                e[0] = t.x; e[1] = t.y; e[2] = t.z; e[3] = t.w;
-            }
-            norm_rope_head<HD>(e, is_q ? L.q_norm : L.k_norm, P.eps, P.rope_dim, pos, P.rope_freq);
-            if (4 * lane < HD) {
-                float* dst = is_q ? s_q + h * HD : s_kv;
-                *(float4*)(dst + 4 * lane) = make_float4(e[0], e[1], e[2], e[3]);
-                if (!is_q) {
-                    const float4 vv = *(const float4*)(qkv + P.n_embed + kvd + (size_t)g * HD + 4 * lane);
-                    *(float4*)(s_kv + HD + 4 * lane) = vv;
-                    if (c == nch - 1) {
-                        /* fp16 KV row pos (fast/ligguf_fast_qk.cpp:57-62), read from the next token on */
-                        const size_t o = loff + (size_t)pos * kvd + (size_t)g * HD + 4 * lane;
-                        const uint32_t klo = (uint32_t)lg_f2h(e[0]) | ((uint32_t)lg_f2h(e[1]) << 16);
-                        const uint32_t khi = (uint32_t)lg_f2h(e[2]) | ((uint32_t)lg_f2h(e[3]) << 16);
-                        const uint32_t vlo = (uint32_t)lg_f2h(vv.x) | ((uint32_t)lg_f2h(vv.y) << 16);
-                        const uint32_t vhi = (uint32_t)lg_f2h(vv.z) | ((uint32_t)lg_f2h(vv.w) << 16);
-                        *(uint2*)(P.kc + o) = make_uint2(klo, khi);
-                        *(uint2*)(P.vc + o) = make_uint2(vlo, vhi);
+            float e[4] = {hx[j].x, hx[j].y, hx[j].z, hx[j].w};
+            norm_rope_head<HD>(e, has_norm, ng[j], P.eps, P.rope_dim, pos, fr);
+            if (h <= NREP) {
+                if (4 * lane < HD) {
+                    float* dst = is_q ? s_q + h * HD : s_kv;
+                    *(float4*)(dst + 4 * lane) = make_float4(e[0], e[1], e[2], e[3]);
+                    if (!is_q) {
+                        if (c == nch - 1) {
+                            /* fp16 KV row pos (fast/ligguf_fast_qk.cpp:57-62), read from the next token on */
+                            const size_t o = loff + (size_t)pos * kvd + (size_t)g * HD + 4 * lane;
+                            const uint32_t klo = (uint32_t)lg_f2h(e[0]) | ((uint32_t)lg_f2h(e[1]) << 16);
+                            const uint32_t khi = (uint32_t)lg_f2h(e[2]) | ((uint32_t)lg_f2h(e[3]) << 16);
+                            const uint32_t vlo = (uint32_t)lg_f2h(hv.x) | ((uint32_t)lg_f2h(hv.y) << 16);
+                            const uint32_t vhi = (uint32_t)lg_f2h(hv.z) | ((uint32_t)lg_f2h(hv.w) << 16);
+                            *(uint2*)(P.kc + o) = make_uint2(klo, khi);
+                            *(uint2*)(P.vc + o) = make_uint2(vlo, vhi);
+                        }
                     }
                 }
             }
         }
         bar();
-        float qr[NREP][8];
+        if (u == (int)blockIdx.x) stamp(tr, 1);
+        /* q in registers; with 8 query heads per KV head it is re-read from
+         * LDS each step (registers go to K/V and the accumulators) */
+        constexpr int QREG = NREP <= 4 ? NREP : 1;
+        float qr[QREG][8];
 #pragma unroll
-        for (int r = 0; r < NREP; r++)
+        for (int r = 0; r < QREG; r++)
 #pragma unroll
             for (int i = 0; i < 8; i++) qr[r][i] = s_q[r * HD + gl * 8 + i];
 
@@ -572,39 +701,36 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, int layer, int pos
 #pragma unroll
             for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
         }
-        auto step = [&](int st, const uint4& kb, const uint4& vb) {
+#pragma unroll
+        for (int st = 0; st < MAXST; st++) {
             const int t = t0 + st * PPB + wave * PPW + grp;
-            if (t < t1) {
+            if (st < nsteps && t < t1) {
                 float kf[8], vf[8];
                 if (t != pos) {
-                    h8(kb, kf);
-                    h8(vb, vf);
+                    h8(kb[st], kf);
+                    h8(vb[st], vf);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
                 }
 #pragma unroll
                 for (int r = 0; r < NREP; r++) {
+                    float qv[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) qv[i] = NREP <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HD + gl * 8 + i];
                     float sc = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) sc += qr[r][i] * kf[i];
-                    sc = lg_group_sum<LPP>(sc) * scale;
+                    for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];
+                    sc = lg_group_sum<LPP>(sc) * scale2;
                     const float mn = fmaxf(m[r], sc);
-                    const float a = expf(m[r] - mn);     /* 0 while m = -inf */
-                    const float pw = expf(sc - mn);
+                    const float a = lg_exp2(m[r] - mn);     /* 0 while m = -inf */
+                    const float pw = lg_exp2(sc - mn);
                     l[r] = l[r] * a + pw;
 #pragma unroll
                     for (int i = 0; i < 8; i++) o[r][i] = o[r][i] * a + pw * vf[i];
                     m[r] = mn;
                 }
             }
-        };
-        /* two steps per iteration, the loads of the next step in flight */
-        for (int st = 0; st < nsteps; st += 2) {
-            if (st + 1 < nsteps) load_step(u, st + 1, kb1, vb1);
-            step(st, kb0, vb0);
-            if (st + 2 < nsteps) load_step(u, st + 2, kb0, vb0);
-            if (st + 1 < nsteps) step(st + 1, kb1, vb1);
         }
         /* combine the position groups of the wave, then the waves (LDS) */
 #pragma unroll
@@ -627,22 +753,24 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, int layer, int pos
             }
         }
         bar();
-        const bool direct = nch == 1;
-        float* part = P.attn_ws + (size_t)u * NREP * (HD + 2);
         for (int i = threadIdx.x; i < NREP * HD; i += PK_THREADS) {
-            const int r = i / HD;
-            float M = s_m[r], Ls = s_sc[r], O = s_o[r * HD + i % HD];
-            for (int w = 1; w < PK_WAVES; w++) {
-                const float o2 = s_o[(w * NREP + r) * HD + i % HD];
-                osm_merge(M, Ls, &O, s_m[w * NREP + r], s_sc[w * NREP + r], &o2, 1);
+            const int r = i / HD, d = i % HD, q = g * NREP + r;
+            float M = -INFINITY;
+            for (int w = 0; w < PK_WAVES; w++) M = fmaxf(M, s_m[w * NREP + r]);
+            float O = 0.0f, Ls = 0.0f;
+            for (int w = 0; w < PK_WAVES; w++) {
+                const float mw = s_m[w * NREP + r];
+                const float wt = mw == -INFINITY ? 0.0f : lg_exp2(mw - M);
+                O += s_o[(w * NREP + r) * HD + d] * wt;
+                Ls += s_sc[w * NREP + r] * wt;
             }
-            if (direct) cst(&att[(size_t)g * NREP * HD + i], O / Ls);
-            else {
-                cst(&part[2 * NREP + i], O);
-                if (i % HD == 0) { cst(&part[r], M); cst(&part[NREP + r], Ls); }
+            cst(&po[(size_t)c * P.n_embed + (size_t)q * HD + d], O);
+            if (d == 0) {
+                cst(&pml[((size_t)c * P.n_heads + q) * 2], M);
+                cst(&pml[((size_t)c * P.n_heads + q) * 2 + 1], Ls);
             }
         }
-        if (!direct) {
+        if (nch > PK_ATT_MERGE) {
             wait_stores();
             bar();
             if (threadIdx.x == 0) {
@@ -651,42 +779,48 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, int layer, int pos
             }
             bar();
             if (s_int[0]) {
-                /* last unit of head group g: merge its nch partials.  (m, l)
-                 * of all chunks go through LDS; each thread then sums one
-                 * output value over the chunks with 8 loads in flight. */
-                constexpr int ST = NREP * (HD + 2);
-                const float* base = P.attn_ws + (size_t)g * nch * ST;
-                float* s_ml = s_sc;                                   /* [nch][2*NREP]: m then l */
-                float* s_w = s_sc + PK_MAX_UNITS_PER_HEAD * 2 * NREP; /* [nch][NREP] weights */
-                for (int i = threadIdx.x; i < nch * 2 * NREP; i += PK_THREADS)
-                    s_ml[i] = cld(&base[(size_t)(i / (2 * NREP)) * ST + i % (2 * NREP)]);
+                /* last unit of head group g: merge its nch partials, weights
+                 * through LDS, each thread one output value over the chunks
+                 * with 8 loads in flight (the consumer's formula) */
+                float* s_ml = s_sc;                                   /* [nch][NREP][2] */
+                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NREP] */
+                for (int i = threadIdx.x; i < nch * NREP; i += PK_THREADS) {
+                    const float2 v = cld2(&pml[((size_t)(i / NREP) * P.n_heads + g * NREP + i % NREP) * 2]);
+                    s_ml[2 * i] = v.x;
+                    s_ml[2 * i + 1] = v.y;
+                }
                 bar();
                 if (threadIdx.x < NREP) {
                     const int r = threadIdx.x;
                     float M = -INFINITY;
-                    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_ml[cc * 2 * NREP + r]);
+                    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NREP + r) * 2]);
                     float Ls = 0.0f;
                     for (int cc = 0; cc < nch; cc++) {
-                        const float wgt = expf(s_ml[cc * 2 * NREP + r] - M);
+                        const float wgt = lg_exp2(s_ml[(cc * NREP + r) * 2] - M);
                         s_w[cc * NREP + r] = wgt;
-                        Ls += s_ml[cc * 2 * NREP + NREP + r] * wgt;
+                        Ls += s_ml[(cc * NREP + r) * 2 + 1] * wgt;
                     }
                     s_red[r] = Ls;
                 }
                 bar();
                 for (int i = threadIdx.x; i < NREP * HD; i += PK_THREADS) {
                     const int r = i / HD;
+                    const float* col = po + (size_t)g * NREP * HD + i;
                     float acc = 0.0f;
                     for (int c0 = 0; c0 < nch; c0 += 8) {
                         float v[8];
 #pragma unroll
-                        for (int k = 0; k < 8; k++)
-                            v[k] = c0 + k < nch ? cld(&base[(size_t)(c0 + k) * ST + 2 * NREP + i]) : 0.0f;
+                        for (int k = 0; k < 8; k++) v[k] = c0 + k < nch ? cld(col + (size_t)(c0 + k) * P.n_embed) : 0.0f;
 #pragma unroll
                         for (int k = 0; k < 8; k++)
                             if (c0 + k < nch) acc += v[k] * s_w[(c0 + k) * NREP + r];
                     }
-                    cst(&att[(size_t)g * NREP * HD + i], acc / s_red[r]);
+                    /* the merged vector as a one-chunk partial (m 0, l 1) */
+                    cst(&po_m[(size_t)g * NREP * HD + i], acc / s_red[r]);
+                }
+                if (threadIdx.x < NREP) {
+                    cst(&pml_m[(size_t)(g * NREP + threadIdx.x) * 2], 0.0f);
+                    cst(&pml_m[(size_t)(g * NREP + threadIdx.x) * 2 + 1], 1.0f);
                 }
                 if (threadIdx.x == 0) cst(&P.attn_cnt[g], 0u);
             }
