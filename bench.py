@@ -11,11 +11,13 @@ Workload (one "step" = one greedy decode token, batch 1):
   sampler_greedy loop, fast/ligguf_fast_qk.cpp:368-382).
 
 Prints one JSON line.  `value` is decode tokens/s with weights and KV
-resident in HBM.  `roofline` is for the dominant kernel (the fused up|gate
-Q4_K matvec, 24576 x 4096) timed with HIP events on its stream over
-rotating buffers larger than the 256 MB Infinity Cache; `cpu_baseline` is
-the reference FAST engine (built from its own sources, AVX2) decoding the
-same model on this host's cores.
+resident in HBM.  `roofline` is for the dominant kernel of the step, the
+fused rmsnorm + up|gate (2 x 12288 x 4096 Q4_K) + SwiGLU kernel, launched
+on its own through lg_time_fused_phase over all 36 layers in turn (2 GB of
+distinct weights, far above the 256 MB Infinity Cache) and timed with HIP
+events on the stream it runs on; `cpu_baseline` is the reference FAST engine
+(built from its own sources, AVX2) decoding the same model on this host's
+cores.
 """
 from __future__ import annotations
 
@@ -35,44 +37,23 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def dominant_kernel_roofline(torch, rows: int, cols: int, reps: int = 200):
-    """Average duration of the Q4_K matvec at the fused up|gate shape, over
-    distinct weight buffers totalling > 512 MB, timed with HIP events on the
-    stream the kernel runs on."""
-    from ligguf_amd import ops
+UG_KERNEL = "k_f_ug Q4_K (rmsnorm + up|gate 24576x4096 + SwiGLU)"
+
+
+def dominant_kernel_roofline(eng, cfg, passes: int = 5):
+    """Mean duration of the fused up|gate kernel over `passes` sweeps of all
+    layers (lg_time_fused_phase: HIP events on the engine's stream), against
+    its algorithmic bytes: the two Q4_K matrices, the fp32 input vector and
+    rmsnorm weights it reads and the fp32 SwiGLU output it writes."""
     from ligguf_amd.lib import Q4_K, row_size
-    rsz = row_size(Q4_K, cols)
-    wbytes = rows * rsz
-    nbuf = max(2, (600 << 20) // wbytes + 1)
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(7)
-    bufs = [torch.randint(0, 256, (wbytes,), dtype=torch.uint8, device=dev, generator=g) for _ in range(nbuf)]
-    for b in bufs:     # finite fp16 scales: d, dmin = 2^-10 in every block header
-        v = b.view(-1, 144)
-        v[:, 0] = 0; v[:, 1] = 0x14; v[:, 2] = 0; v[:, 3] = 0x14
-    x = torch.randn(cols, device=dev)
-    xq = ops.quantize_q8_K(x)
-    out = torch.empty(rows, device=dev)
-    for i in range(10):
-        ops.matvec(Q4_K, bufs[i % nbuf], rsz, cols, rows, xq, out=out)
-    torch.cuda.synchronize()
-    s = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for i in range(reps):
-        ops.matvec(Q4_K, bufs[i % nbuf], rsz, cols, rows, xq, out=out)
-    e1.record(s)
-    torch.cuda.synchronize()
-    avg_s = e0.elapsed_time(e1) / 1e3 / reps
-    alg = wbytes + (cols // 256) * 292 + rows * 4      # weights + Q8_K activation + fp32 output
-    del bufs
-    torch.cuda.empty_cache()
-    name = f"k_matvec Q4_K {rows}x{cols}"
+    iters = passes * cfg.n_layers
+    eng.time_phase(3, 0, cfg.n_layers)             # warm-up sweep
+    avg_us = eng.time_phase(3, 0, iters)
+    alg = 2 * cfg.n_ff * row_size(Q4_K, cfg.n_embed) + 2 * cfg.n_embed * 4 + cfg.n_ff * 4
+    avg_s = avg_us * 1e-6
     return {"bound": "hbm", "achieved": round(alg / avg_s / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(alg / avg_s / HBM_PEAK, 4), "traffic": measured_traffic(name),
-            "kernel": name, "avg_us": round(avg_s * 1e6, 3), "bytes_per_launch": alg,
-            "buffers_mb": round(nbuf * wbytes / 2 ** 20)}
+            "frac": round(alg / avg_s / HBM_PEAK, 4), "traffic": measured_traffic(UG_KERNEL),
+            "kernel": UG_KERNEL, "avg_us": round(avg_us, 3), "bytes_per_launch": alg, "launches": iters}
 
 
 def measured_traffic(kernel: str):
@@ -108,7 +89,7 @@ def plain_copy(torch, nbytes: int = 256 << 20, reps: int = 20):
     return {"bytes_each_way": nbytes, "avg_us": round(avg_s * 1e6, 2), "GB/s": round(2 * nbytes / avg_s / 1e9, 1)}
 
 
-def cpu_baseline(hm, seconds: float, max_tokens: int = 64):
+def cpu_baseline(hm, seconds: float, max_tokens: int = 4000):
     """The reference FAST engine (oracle/_ref, AVX2, OpenMP) decoding the same
     host model from position 0 for about `seconds`."""
     import ctypes as C
@@ -142,6 +123,7 @@ def cpu_baseline(hm, seconds: float, max_tokens: int = 64):
     R.model_bind(m)
     rng = np.random.default_rng(1)
     R.inference(int(rng.integers(1, c.vocab)), c.vocab)      # untimed: faults pages in, warms caches
+    max_tokens = min(max_tokens, c.n_context - 2)          # positions 1..n stay inside the context
     n, t0 = 0, time.perf_counter()
     tok = 1
     while n < max_tokens and (time.perf_counter() - t0 < seconds or n < 2):
@@ -176,14 +158,18 @@ def main() -> int:
     import torch
     from ligguf_amd.model import QWEN3_8B_Q4K, Engine, HostModel
 
+    cfg = QWEN3_8B_Q4K.with_(n_context=max(1024, args.prefill + args.warmup + args.steps + 1))
     if args.kernel_only:
-        cfg = QWEN3_8B_Q4K
+        hm = HostModel.synthetic(cfg)
+        eng = Engine(0)
+        eng.load(hm)
+        eng.decode(1, 0, want_logits=False)           # a known device step record
         copy_gbs = plain_copy(torch)
-        roof = dominant_kernel_roofline(torch, 2 * cfg.n_ff, cfg.n_embed)
+        roof = dominant_kernel_roofline(eng, cfg)
+        eng.close()
         print(json.dumps({"roofline": roof, "copy": copy_gbs}), flush=True)
         return 0
 
-    cfg = QWEN3_8B_Q4K.with_(n_context=max(1024, args.prefill + args.warmup + args.steps + 1))
     t0 = time.perf_counter()
     hm = HostModel.synthetic(cfg)
     log(f"synthetic {cfg.name}: {cfg.weight_bytes() / 1e9:.3f} GB of weights read per token, "
@@ -223,8 +209,8 @@ def main() -> int:
     log(f"decode: {tps:.1f} tok/s, {ms:.3f} ms/token, {mean_bytes / (dt / args.steps) / 1e9:.0f} GB/s per token")
 
     roof = None
-    if not args.no_kernel:
-        roof = dominant_kernel_roofline(torch, 2 * cfg.n_ff, cfg.n_embed)
+    if not args.no_kernel and path_name == "fused-graph":
+        roof = dominant_kernel_roofline(eng, cfg)
         log(f"dominant kernel: {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of HBM peak)")
     eng.close()
 

@@ -137,7 +137,7 @@ const float* lg_logits_device(lg_ctx* ctx);
 #define LG_PATH_MULTI 2
 #define LG_PATH_FUSED 3
 int lg_set_decode_path(lg_ctx* ctx, int path);
-/* the path the next step takes (LG_PATH_PERSISTENT or LG_PATH_MULTI), -1 without a model */
+/* the path the next step takes (LG_PATH_FUSED, LG_PATH_PERSISTENT or LG_PATH_MULTI), -1 without a model */
 int lg_decode_path(const lg_ctx* ctx);
 
 /* Phase tracing of the fused and persistent steps (no counterpart in the reference,
@@ -150,6 +150,16 @@ int lg_decode_path(const lg_ctx* ctx);
  * lg_trace_size is 0 when the model runs on the multi-kernel path. */
 int lg_trace_next_step(lg_ctx* ctx, uint64_t* trace_dev);
 size_t lg_trace_size(const lg_ctx* ctx);
+
+/* Times one kernel of the fused step (no counterpart in the reference; for
+ * benchmarks and profiles): phase 0 rmsnorm + QKV, 1 attention, 2 att_out,
+ * 3 rmsnorm + up|gate + SwiGLU, 4 down, 5 output head + argmax, launched
+ * `iters` times directly on the context's stream at layers layer0,
+ * layer0 + 1, ... (mod n_layers), between two HIP events; *avg_us receives
+ * the mean time per launch.  The kernels work on the device state of the
+ * last step (run and synchronize one first); the next step rewrites
+ * everything they touch.  LG_ERR_STATE unless the fused path is in use. */
+int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters, float* avg_us);
 
 /* Greedy argmax of the current device logits, first index wins ties
  * (sampler_greedy, fast/ligguf_fast_qk.cpp:146-160). */

@@ -542,6 +542,42 @@ extern "C" size_t lg_trace_size(const lg_ctx* ctx)
     return (size_t)(5 * ctx->n_layers + 1) * ctx->pk_nwg * 4 * sizeof(uint64_t);
 }
 
+extern "C" int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters, float* avg_us)
+{
+    if (!ctx || !avg_us || iters <= 0 || phase < 0 || phase > 5 || layer0 < 0) {
+        lg_set_error("time_fused_phase: bad argument");
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    if (!ctx->loaded || !use_fused(ctx)) {
+        lg_set_error("time_fused_phase: the fused decode path is not in use");
+        return ctx_fail(ctx, LG_ERR_STATE);
+    }
+    /* the kernels read the device step record: it must hold a known position */
+    if (!ctx->dev_known || ctx->dev_pos >= ctx->n_context) {
+        lg_set_error("time_fused_phase: run and synchronize a decode step first");
+        return ctx_fail(ctx, LG_ERR_STATE);
+    }
+    hipEvent_t e0, e1;
+    LG_HIP_CHECK(hipEventCreate(&e0));
+    LG_HIP_CHECK(hipEventCreate(&e1));
+    LG_HIP_CHECK(hipEventRecord(e0, ctx->stream));
+    int rc = LG_OK;
+    for (int i = 0; i < iters && rc == LG_OK; i++)
+        rc = lg_fused_phase(ctx->fused_fn, ctx->pk, ctx->pk_layers.data(), ctx->step_dev, phase,
+                            (layer0 + i) % ctx->n_layers, ctx->pk_nwg, ctx->stream);
+    LG_HIP_CHECK(hipEventRecord(e1, ctx->stream));
+    LG_HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    LG_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    /* the output-head kernel advances the step record: rewrite it before the next step */
+    if (phase == 5) ctx->dev_known = false;
+    if (rc) return ctx_fail(ctx, rc);
+    *avg_us = ms * 1000.0f / (float)iters;
+    return LG_OK;
+}
+
 extern "C" int lg_decode_path(const lg_ctx* ctx)
 {
     if (!ctx || !ctx->loaded) return -1;

@@ -124,12 +124,33 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
     hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S);
 }
 
+typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, hipStream_t);
+
+/* one kernel of the step: phase 0..4 of layer l, 5 = output head */
+template <int LT, int OT, int HD, int NREP>
+static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int phase, int l, int nwg, hipStream_t st)
+{
+    const dim3 g(nwg), b(PK_THREADS);
+    switch (phase) {
+    case 0:
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l);
+        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l);
+        break;
+    case 1: hipLaunchKernelGGL((k_f_attn<HD, NREP>), g, b, 0, st, P, Lh[l], S, l); break;
+    case 2: hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l); break;
+    case 3: hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l); break;
+    case 4: hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l); break;
+    default: hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S); break;
+    }
+}
+
 struct FusedVariant {
     int lt, ot, hd, nrep;
     fused_enqueue_t fn;
+    fused_phase_t phase;
 };
 
-#define FV(LT, OT, HD, NR) {LT, OT, HD, NR, fused_enqueue<LT, OT, HD, NR>}
+#define FV(LT, OT, HD, NR) {LT, OT, HD, NR, fused_enqueue<LT, OT, HD, NR>, fused_phase<LT, OT, HD, NR>}
 static const FusedVariant f_variants[] = {
     FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
     FV(LG_Q5_K, LG_Q6_K, 128, 4), FV(LG_Q6_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q8_0, 128, 4),
@@ -142,13 +163,20 @@ static const FusedVariant f_variants[] = {
 const void* lg_fused_variant(int lt, int ot, int hd, int nrep)
 {
     for (const FusedVariant& v : f_variants)
-        if (v.lt == lt && v.ot == ot && v.hd == hd && v.nrep == nrep) return (const void*)v.fn;
+        if (v.lt == lt && v.ot == ot && v.hd == hd && v.nrep == nrep) return (const void*)&v;
     return nullptr;
 }
 
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
                      hipStream_t s)
 {
-    ((fused_enqueue_t)variant)(P, layers, S_dev, n_layers, nwg, s);
+    ((const FusedVariant*)variant)->fn(P, layers, S_dev, n_layers, nwg, s);
     return lg_check_launch("fused decode step");
+}
+
+int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int phase, int layer,
+                   int nwg, hipStream_t s)
+{
+    ((const FusedVariant*)variant)->phase(P, layers, S_dev, phase, layer, nwg, s);
+    return lg_check_launch("fused decode phase");
 }

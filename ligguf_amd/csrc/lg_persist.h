@@ -104,3 +104,7 @@ int lg_persist_launch(const void* kernel, const PkParams& P, const PkStep* S, in
 const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep);
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
                      hipStream_t s);
+/* one kernel of the fused step: phase 0 rmsnorm+QKV, 1 attention, 2 att_out,
+ * 3 up|gate, 4 down (of `layer`), 5 output head */
+int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int phase, int layer,
+                   int nwg, hipStream_t s);

@@ -277,12 +277,20 @@ class Engine:
         self.cfg = hm.cfg
 
     def set_path(self, path: int) -> None:
-        """lg_set_decode_path: PATH_AUTO, PATH_PERSISTENT or PATH_MULTI."""
+        """lg_set_decode_path: PATH_AUTO, PATH_FUSED, PATH_PERSISTENT or PATH_MULTI."""
         check(self.lib.lg_set_decode_path(self.ctx, path), self.ctx)
 
     def path(self) -> int:
-        """The decode path the next step takes (PATH_PERSISTENT / PATH_MULTI)."""
+        """The decode path the next step takes (PATH_FUSED / PATH_PERSISTENT / PATH_MULTI)."""
         return int(self.lib.lg_decode_path(self.ctx))
+
+    def time_phase(self, phase: int, layer0: int = 0, iters: int = 100) -> float:
+        """lg_time_fused_phase: mean microseconds per launch of one fused-step
+        kernel (0 QKV, 1 attention, 2 att_out, 3 up|gate, 4 down, 5 output),
+        at layers layer0, layer0+1, ... (mod n_layers)."""
+        us = C.c_float()
+        check(self.lib.lg_time_fused_phase(self.ctx, phase, layer0, iters, C.byref(us)), self.ctx)
+        return float(us.value)
 
     def decode(self, tok: int, pos: int, want_logits: bool = True):
         if want_logits:

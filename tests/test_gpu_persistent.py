@@ -16,7 +16,7 @@ import os
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0
+from ligguf_amd.lib import PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0, LgError
 from ligguf_amd.model import Engine, HostModel, ModelConfig
 from test_gpu_decode import one_step_errors, rel
 
@@ -179,3 +179,22 @@ def test_graph_replays_equal_direct_launches(pk_model):
         assert ta == tb
         if la is not None:
             assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+def test_time_fused_phase_leaves_the_next_step_unchanged(pk_model):
+    """lg_time_fused_phase launches single kernels of the step on the device
+    state of the last step; the next step rewrites all of it, so its logits
+    are those of the same two steps without the timing in between."""
+    hm, eng = pk_model
+    eng.set_path(PATH_FUSED)
+    eng.decode(5, 0)
+    ref = eng.decode(6, 1)
+    eng.decode(5, 0)
+    for phase in range(6):
+        us = eng.time_phase(phase, 0, 3)
+        assert 0.0 < us < 1e5
+    got = eng.decode(6, 1)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    eng.set_path(PATH_MULTI)
+    with pytest.raises(LgError):
+        eng.time_phase(3, 0, 1)
