@@ -170,6 +170,23 @@ int lg_argmax(lg_ctx* ctx, int* tok_out);
  * logits of the last token to logits_host (NULL allowed). */
 int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* logits_host);
 
+/* How lg_prefill runs a prompt (no counterpart in the reference, which
+ * feeds it token by token).  BATCHED: layer passes over up to 512 tokens,
+ * each weight matrix read once per pass and multiplied by all of them with
+ * int8 MFMA GEMMs, the tokens' integer sub-block sums and quantizers those
+ * of the step; the logits then match n sequential steps to fp32 rounding (an
+ * int8 rounding of an activation may differ in rare tokens).  Needs Q4_K
+ * layer matrices (Q|K|V and up|gate stackable) and head_dim 128.  STEPS: one
+ * decode step per token, bit-equal to n lg_decode_step calls.  AUTO (the
+ * default): BATCHED when the model allows it and n >= 2, else STEPS.
+ * lg_prefill_path reports what a prompt of 2+ tokens takes (-1 without a
+ * model). */
+#define LG_PREFILL_AUTO 0
+#define LG_PREFILL_STEPS 1
+#define LG_PREFILL_BATCHED 2
+int lg_set_prefill_path(lg_ctx* ctx, int path);
+int lg_prefill_path(const lg_ctx* ctx);
+
 /* fp16 KV rows [pos0, pos0+npos) of layers [layer0, layer0+nlayers) to/from
  * host arrays laid out [nlayers][npos][kv_dim] -- the per-layer blocks of the
  * reference's state file (save/load_model_state,
@@ -201,6 +218,16 @@ int lg_quantize_q8_K(const float* x, int64_t n, void* y, void* stream);
  * fast/ligguf_fast_qk.cpp:111,131). */
 int lg_matvec(int type, const void* w, uint32_t rsz, int n, int d, const void* xq, float* out, int accumulate,
               void* stream);
+
+/* The matvec of T tokens at once on int8 MFMA (the batched prefill's GEMM):
+ * out[t*d + r] = row r of w . Q8_K(x[t*n ..]) for t < T, r < d, each fp32 row
+ * of x quantized as quantize_q8_K does.  Q4_K weights only, n % 256 == 0.
+ * The integer sub-block sums are those of lg_matvec (fast/lil_math.cpp:
+ * 582-616); only the fp32 accumulation order differs.  Allocates and frees a
+ * workspace of about 1.1*T*n bytes and synchronizes `stream` (tests and
+ * benches).  No counterpart in the reference, which calls matmul per token. */
+int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, int d, const float* x, int T, float* out,
+                     void* stream);
 
 /* rmsnorm (fast/lil_math.cpp:922-929) fused with the activation quantizer
  * that follows it in inference() (:37-39): out_q gets Q8_K (qtype LG_Q8_K),

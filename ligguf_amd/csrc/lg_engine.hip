@@ -26,6 +26,7 @@
 
 #include "lg_common.h"
 #include "lg_persist.h"
+#include "lg_prefill.h"
 
 /* ------------------------------------------------------------------ */
 /* errors                                                               */
@@ -141,6 +142,12 @@ struct lg_ctx {
     /* fused per-phase kernels replayed from a HIP graph (lg_fused.hip) */
     const void* fused_fn = nullptr;
     std::vector<PkLayer> pk_layers;  /* host copy: the fused kernels take their layer by value */
+    /* batched prefill */
+    bool pf_ok = false;
+    int prefill_path = LG_PREFILL_AUTO;
+    std::vector<PfLayer> pf_layers;
+    PfModel pf_model = {};
+    PfBuffers pf = {};
     PkStep* step_dev = nullptr;      /* {tok, pos, feed_end} the next fused step reads */
     PkStep* step_ring = nullptr;     /* pinned slots for host updates of step_dev */
     int ring_next = 0, ring_pending = 0;
@@ -181,6 +188,9 @@ static void free_model(lg_ctx* ctx)
     ctx->fused_fn = nullptr;
     ctx->dev_known = false;
     ctx->dev_feed_end = 0;
+    ctx->pf_ok = false;
+    ctx->pf_layers.clear();
+    ctx->pf = PfBuffers{};
     if (ctx->graph) {
         hipGraphExecDestroy(ctx->graph);
         ctx->graph = nullptr;
@@ -584,6 +594,65 @@ extern "C" int lg_decode_path(const lg_ctx* ctx)
     return use_pk(ctx) ? LG_PATH_PERSISTENT : (use_fused(ctx) ? LG_PATH_FUSED : LG_PATH_MULTI);
 }
 
+/* ------------------------------------------------------------------ */
+/* batched prefill set-up                                               */
+/* ------------------------------------------------------------------ */
+#define LG_PF_TMAX 512   /* tokens per layer pass */
+
+/* the batched prefill serves models whose layer matrices are all Q4_K (Q|K|V
+ * and up|gate stacked), widths multiples of 256, head_dim 128 */
+static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
+{
+    ctx->pf_ok = false;
+    const int nrep = m->n_heads / m->n_kv_heads;
+    bool ok = m->n_embed % 256 == 0 && m->n_ff % 256 == 0 && m->head_dim == 128 &&
+              (nrep == 1 || nrep == 2 || nrep == 4 || nrep == 8) && !ctx->layers.empty();
+    for (int l = 0; ok && l < m->n_layers; l++) {
+        const dlayer& D = ctx->layers[l];
+        ok = D.qkv_fused && D.ug_fused && D.qkv.type == LG_Q4_K && D.att_out.type == LG_Q4_K && D.ug.type == LG_Q4_K &&
+             D.down.type == LG_Q4_K && D.down.cols == m->n_ff;
+    }
+    if (!ok) return;
+    ctx->pf_layers.resize(m->n_layers);
+    for (int l = 0; l < m->n_layers; l++) {
+        const dlayer& D = ctx->layers[l];
+        PfLayer& L = ctx->pf_layers[l];
+        L.qkv = D.qkv.data; L.ao = D.att_out.data; L.ug = D.ug.data; L.down = D.down.data;
+        L.qkv_rsz = D.qkv.rsz; L.ao_rsz = D.att_out.rsz; L.ug_rsz = D.ug.rsz; L.down_rsz = D.down.rsz;
+        L.att_norm = D.att_norm; L.ffn_norm = D.ffn_norm; L.q_norm = D.q_norm; L.k_norm = D.k_norm;
+    }
+    PfModel& M = ctx->pf_model;
+    M.layers = ctx->pf_layers.data();
+    M.n_layers = m->n_layers; M.n_embed = m->n_embed; M.n_heads = m->n_heads; M.n_kv = m->n_kv_heads;
+    M.head_dim = m->head_dim; M.kv_dim = m->kv_dim; M.n_ff = m->n_ff; M.n_ctx = m->n_context;
+    M.rope_dim = m->rope_dim; M.eps = m->rms_epsilon;
+    M.embd = ctx->embd.data; M.embd_rsz = ctx->embd.rsz; M.embd_t = ctx->embd.type;
+    M.rope_freq = ctx->rope_freq; M.kc = ctx->kc; M.vc = ctx->vc;
+    ctx->pf_ok = true;
+}
+
+/* buffers for LG_PF_TMAX tokens, allocated at the first batched prefill */
+static int prefill_buffers(lg_ctx* c)
+{
+    if (c->pf.tmax) return LG_OK;
+    PfBuffers B = {};
+    const int tmax = std::min(LG_PF_TMAX, (c->n_context + 3) / 4 * 4);
+    const size_t ne = c->n_embed, qs = ne + 2 * (size_t)c->kv_dim, nff = c->n_ff, nbm = nff / 256;
+    int rc;
+    if ((rc = dalloc(c, (void**)&B.toks, (size_t)tmax * sizeof(int)))) return rc;
+    if ((rc = dalloc(c, (void**)&B.x, (size_t)tmax * ne * 4))) return rc;
+    if ((rc = dalloc(c, (void**)&B.qkv, (size_t)tmax * qs * 4))) return rc;
+    if ((rc = dalloc(c, (void**)&B.att, (size_t)tmax * ne * 4))) return rc;
+    if ((rc = dalloc(c, (void**)&B.ug, (size_t)tmax * 2 * nff * 4))) return rc;
+    if ((rc = dalloc(c, (void**)&B.q.qs, (size_t)tmax * nff))) return rc;
+    if ((rc = dalloc(c, (void**)&B.q.d, nbm * tmax * 4))) return rc;
+    if ((rc = dalloc(c, (void**)&B.q.bs, (size_t)tmax * nbm * 16 * 2))) return rc;
+    B.q.tld = tmax;
+    B.tmax = tmax;
+    c->pf = B;
+    return LG_OK;
+}
+
 static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
 {
     if (!m || !m->layers) { lg_set_error("load_model: null descriptor"); return LG_ERR_ARG; }
@@ -701,6 +770,7 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
     if ((rc = dalloc(ctx, (void**)&ctx->attn_ws, ctx->attn_ws_bytes))) return rc;
     if ((rc = dalloc(ctx, (void**)&ctx->argmax_dev, 16))) return rc;
     if ((rc = setup_persistent(ctx, m))) return rc;
+    setup_prefill(ctx, m);
     LG_HIP_CHECK(hipDeviceSynchronize());
     ctx->loaded = true;
     return LG_OK;
@@ -880,6 +950,76 @@ extern "C" int lg_argmax(lg_ctx* ctx, int* tok_out)
     return lg_sync(ctx);
 }
 
+/* the prompt in layer passes of up to LG_PF_TMAX tokens (lg_prefill.hip),
+ * then the output head on the last token's residual stream */
+static int prefill_batched(lg_ctx* c, const int* toks, int n, int pos0)
+{
+    int rc;
+    if ((rc = prefill_buffers(c))) return rc;
+    LG_HIP_CHECK(hipStreamSynchronize(c->stream));   /* the token staging below reuses one buffer */
+    int T = 0;
+    for (int off = 0; off < n; off += T) {
+        T = std::min(c->pf.tmax, n - off);
+        LG_HIP_CHECK(hipMemcpyAsync(c->pf.toks, toks + off, (size_t)T * sizeof(int), hipMemcpyHostToDevice, c->stream));
+        if ((rc = lg_prefill_layers(c->pf_model, c->pf, T, pos0 + off, c->stream))) return rc;
+        if (off + T < n) LG_HIP_CHECK(hipStreamSynchronize(c->stream));
+    }
+    LG_HIP_CHECK(hipMemcpyAsync(c->x, c->pf.x + (size_t)(T - 1) * c->n_embed, (size_t)c->n_embed * 4,
+                                hipMemcpyDeviceToDevice, c->stream));
+    actbufs a;
+    if ((rc = prep_norm(c, c->x, c->out_norm, c->n_embed, act_family(c->output.type), a))) return rc;
+    if ((rc = mv(c, c->output, a, c->logits, 0))) return rc;
+    c->last_was_pk = false;
+    c->dev_known = false;
+    return LG_OK;
+}
+
+extern "C" int lg_set_prefill_path(lg_ctx* ctx, int path)
+{
+    if (!ctx || path < LG_PREFILL_AUTO || path > LG_PREFILL_BATCHED) {
+        lg_set_error("set_prefill_path: bad argument");
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    if (path == LG_PREFILL_BATCHED && ctx->loaded && !ctx->pf_ok) {
+        lg_set_error("set_prefill_path: the batched prefill needs Q4_K layer matrices and head_dim 128");
+        return ctx_fail(ctx, LG_ERR_TYPE);
+    }
+    ctx->prefill_path = path;
+    return LG_OK;
+}
+
+extern "C" int lg_prefill_path(const lg_ctx* ctx)
+{
+    if (!ctx || !ctx->loaded) return -1;
+    return ctx->pf_ok && ctx->prefill_path != LG_PREFILL_STEPS ? LG_PREFILL_BATCHED : LG_PREFILL_STEPS;
+}
+
+extern "C" int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, int d, const float* x, int T, float* out,
+                                void* stream)
+{
+    if (type != LG_Q4_K) { lg_set_error("matmul_tokens: type %d (Q4_K only)", type); return LG_ERR_TYPE; }
+    if (!w || !x || !out || n <= 0 || n % 256 || d <= 0 || T <= 0) {
+        lg_set_error("matmul_tokens: bad arguments (n %d, d %d, T %d)", n, d, T);
+        return LG_ERR_ARG;
+    }
+    const int tld = (T + 3) / 4 * 4, nb = n / 256;
+    PfQ8K q = {};
+    q.tld = tld;
+    const size_t bytes = (size_t)tld * n + (size_t)nb * tld * 4 + (size_t)tld * nb * 32;
+    uint8_t* ws = nullptr;
+    const hipError_t e = hipMalloc((void**)&ws, bytes);
+    if (e != hipSuccess) { lg_set_error("matmul_tokens: hipMalloc(%zu): %s", bytes, hipGetErrorString(e)); return LG_ERR_NOMEM; }
+    q.qs = (int8_t*)ws;
+    q.d = (float*)(ws + (size_t)tld * n);
+    q.bs = (int16_t*)(ws + (size_t)tld * n + (size_t)nb * tld * 4);
+    int rc = lg_prefill_quantize(x, n, nullptr, 0.0f, n, T, q, (hipStream_t)stream);
+    if (!rc) rc = lg_prefill_gemm_q4k((const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream);
+    const hipError_t e2 = hipStreamSynchronize((hipStream_t)stream);
+    hipFree(ws);
+    if (!rc && e2 != hipSuccess) { lg_set_error("matmul_tokens: %s", hipGetErrorString(e2)); rc = LG_ERR_HIP; }
+    return rc;
+}
+
 extern "C" int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* logits_host)
 {
     if (!ctx || !toks || n <= 0) { lg_set_error("lg_prefill: bad arguments"); return ctx_fail(ctx, LG_ERR_ARG); }
@@ -890,7 +1030,12 @@ extern "C" int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* 
         if (rc) return ctx_fail(ctx, rc);
     }
     hipSetDevice(ctx->device);
-    if (use_fused(ctx)) {
+    const bool batched = ctx->pf_ok && (ctx->prefill_path == LG_PREFILL_BATCHED ||
+                                        (ctx->prefill_path == LG_PREFILL_AUTO && n >= 2));
+    if (batched) {
+        int rc = prefill_batched(ctx, toks, n, pos0);
+        if (rc) return ctx_fail(ctx, rc);
+    } else if (use_fused(ctx)) {
         /* the prompt goes to the device once; every replay of the step graph
          * takes its token from it (PkStep.feed_end) */
         LG_HIP_CHECK(hipStreamSynchronize(ctx->stream));   /* feed_host may back an earlier copy */

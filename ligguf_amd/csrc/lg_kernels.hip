@@ -9,6 +9,7 @@
 
 #include "lg_common.h"
 #include "lg_quant.h"
+#include "lg_rope.h"
 
 __global__ void k_dequantize(int type, const uint8_t* __restrict__ x, float* __restrict__ y, int64_t n)
 {
@@ -109,58 +110,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope_kv(float* __restrict__ q, 
                                                          uint16_t* __restrict__ kc_row, uint16_t* __restrict__ vc_row)
 {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int lane = threadIdx.x & 63;
-    if (wave >= n_heads + n_kv_heads) return;
-    const bool is_q = wave < n_heads;
-    const int h = is_q ? wave : wave - n_heads;
-    float* p = (is_q ? q : k) + (size_t)h * hd;
-    const float* nw = is_q ? qw : kw;
-    const bool act = 4 * lane < hd;
-    float e[4] = {0.f, 0.f, 0.f, 0.f};
-    if (act) {
-        const float4 t = *(const float4*)(p + 4 * lane);
-        e[0] = t.x; e[1] = t.y; e[2] = t.z; e[3] = t.w;
-    }
-    if (nw) {
-        float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
-        ss = lg_group_sum<64>(ss);
-        const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
-        if (act) {
-            const float4 g = *(const float4*)(nw + 4 * lane);
-            e[0] = e[0] * sc * g.x; e[1] = e[1] * sc * g.y; e[2] = e[2] * sc * g.z; e[3] = e[3] * sc * g.w;
-        }
-    }
-    int rd = rope_dim < hd ? rope_dim : hd;
-    rd &= ~1;
-    if (act) {
-#pragma unroll
-        for (int j = 0; j < 4; j += 2) {
-            const int i = 4 * lane + j;
-            if (i < rd) {
-                const float ang = (float)pos * freq[i >> 1];
-                float s, c;
-                sincosf(ang, &s, &c);
-                const float x0 = e[j], x1 = e[j + 1];
-                e[j] = x0 * c - x1 * s;
-                e[j + 1] = x0 * s + x1 * c;
-            }
-        }
-        *(float4*)(p + 4 * lane) = make_float4(e[0], e[1], e[2], e[3]);
-        if (!is_q) {
-            const size_t o = (size_t)h * hd + 4 * lane;
-            if (kc_row) {
-                const uint32_t lo = (uint32_t)lg_f2h(e[0]) | ((uint32_t)lg_f2h(e[1]) << 16);
-                const uint32_t hi = (uint32_t)lg_f2h(e[2]) | ((uint32_t)lg_f2h(e[3]) << 16);
-                *(uint2*)(kc_row + o) = make_uint2(lo, hi);
-            }
-            if (vc_row) {
-                const float4 t = *(const float4*)(v + o);
-                const uint32_t lo = (uint32_t)lg_f2h(t.x) | ((uint32_t)lg_f2h(t.y) << 16);
-                const uint32_t hi = (uint32_t)lg_f2h(t.z) | ((uint32_t)lg_f2h(t.w) << 16);
-                *(uint2*)(vc_row + o) = make_uint2(lo, hi);
-            }
-        }
-    }
+    lg_qk_norm_rope_kv_wave(wave, q, k, v, qw, kw, n_heads, n_kv_heads, hd, rope_dim, pos, freq, eps, kc_row, vc_row);
 }
 
 /* ------------------------------------------------------------------ */

@@ -1,0 +1,476 @@
+/* lg_prefill.hip -- feed_text's prompt loop (fast/ligguf_fast_qk.cpp:340-356)
+ * as layer passes over T tokens at once.  Each token's arithmetic is that of
+ * inference() (:24-144); what changes is that every weight matrix is read
+ * once per pass and multiplied by the T quantized activations with int8
+ * MFMA:
+ *   - activations are quantized per token as the decode step does (same
+ *     rmsnorm lane order, same Q8_K quantizer, lg_q8k_lane);
+ *   - Q4_K x Q8_K (fast/lil_math.cpp:582-616): the integer sum of q*a of
+ *     each 32-value sub-block is one v_mfma_i32_16x16x32_i8 (K = 32), exact;
+ *     S = sum_j sc_j * isum_j in int32, exact; the mins term
+ *     M = sum_j m_j * (bsums[2j] + bsums[2j+1]) is a K = 8 product on
+ *     v_mfma_f32_16x16x4f32, exact (every partial sum is an integer below
+ *     2^24); then out += d_a * (d_w * S - dmin_w * M) per 256-value block;
+ *   - attention per query token over the fp16 cache rows before it and its
+ *     own fp32 k/v (:64-105), after the pass has written the KV rows of all
+ *     its tokens;
+ * so every integer of the reference's decomposition is reproduced and only
+ * the fp32 accumulation order differs from T sequential steps. */
+#include <math.h>
+
+#include "lg_common.h"
+#include "lg_prefill.h"
+#include "lg_quant.h"
+#include "lg_rope.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+/* ------------------------------------------------------------------ */
+/* embedding rows, quantizers                                           */
+/* ------------------------------------------------------------------ */
+__global__ __launch_bounds__(256) void k_pf_embed(int type, const uint8_t* __restrict__ table, uint32_t rsz,
+                                                  const int* __restrict__ toks, int n, float* __restrict__ x)
+{
+    const int t = blockIdx.x;
+    const uint8_t* row = table + (size_t)toks[t] * rsz;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[(size_t)t * n + i] = lg_dq_value(type, row, i);
+}
+
+/* one 256-value block of one token into the SoA Q8_K form */
+__device__ __forceinline__ void pf_store_q8k(const float v[4], const PfQ8K& q, int n, int t, int b)
+{
+    const int lane = threadIdx.x & 63;
+    const Q8KLane r = lg_q8k_lane(v);
+    *(uint32_t*)(q.qs + (size_t)t * n + b * 256 + 4 * lane) = r.packed;
+    if ((lane & 3) == 0) q.bs[((size_t)t * (n >> 8) + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+    if (lane == 0) q.d[(size_t)b * q.tld + t] = r.d;
+}
+
+/* block b of token t: rmsnorm(x_t) * w (w != NULL) or x_t, quantized; the
+ * sum of squares in k_rmsnorm_quant's lane order (fast/lil_math.cpp:922-929) */
+__global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, int ldx, const float* __restrict__ w,
+                                                 float eps, int n, PfQ8K q)
+{
+    const int lane = threadIdx.x, b = blockIdx.x, t = blockIdx.y;
+    const float* xr = x + (size_t)t * ldx;
+    float scale = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int i = 4 * lane; i < n; i += 256) {
+            const float4 v = *(const float4*)(xr + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = lg_group_sum<64>(ss);
+        scale = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    const int base = b * 256 + 4 * lane;
+    const float4 tv = *(const float4*)(xr + base);
+    float v[4] = {tv.x, tv.y, tv.z, tv.w};
+    if (w) {
+        const float4 g = *(const float4*)(w + base);
+        v[0] = tv.x * scale * g.x; v[1] = tv.y * scale * g.y; v[2] = tv.z * scale * g.z; v[3] = tv.w * scale * g.w;
+    }
+    pf_store_q8k(v, q, n, t, b);
+}
+
+/* hb = silu(gate) * up of token t (fast/ligguf_fast_qk.cpp:119-123), block b,
+ * quantized; ug row = [up | gate] */
+__global__ __launch_bounds__(64) void k_pf_swiglu_quant(const float* __restrict__ ug, int nff, PfQ8K q)
+{
+    const int lane = threadIdx.x, b = blockIdx.x, t = blockIdx.y;
+    const float* ur = ug + (size_t)t * 2 * nff;
+    const int base = b * 256 + 4 * lane;
+    const float4 u = *(const float4*)(ur + base);
+    const float4 g = *(const float4*)(ur + nff + base);
+    float v[4];
+    v[0] = (g.x / (1.0f + expf(-g.x))) * u.x;
+    v[1] = (g.y / (1.0f + expf(-g.y))) * u.y;
+    v[2] = (g.z / (1.0f + expf(-g.z))) * u.z;
+    v[3] = (g.w / (1.0f + expf(-g.w))) * u.w;
+    pf_store_q8k(v, q, nff, t, b);
+}
+
+/* QK-norm + RoPE + KV rows of token t at position pos0 + t */
+__global__ __launch_bounds__(256) void k_pf_qk_rope_kv(float* __restrict__ qkv, int qstride, int n_embed, int kv_dim,
+                                                       const float* __restrict__ qw, const float* __restrict__ kw,
+                                                       int n_heads, int n_kv, int hd, int rope_dim, int pos0,
+                                                       const float* __restrict__ freq, float eps,
+                                                       uint16_t* __restrict__ kc, uint16_t* __restrict__ vc)
+{
+    const int t = blockIdx.y;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int pos = pos0 + t;
+    float* q = qkv + (size_t)t * qstride;
+    lg_qk_norm_rope_kv_wave(wave, q, q + n_embed, q + n_embed + kv_dim, qw, kw, n_heads, n_kv, hd, rope_dim, pos,
+                            freq, eps, kc + (size_t)pos * kv_dim, vc + (size_t)pos * kv_dim);
+}
+
+/* ------------------------------------------------------------------ */
+/* causal attention: query token t, kv head g                           */
+/* ------------------------------------------------------------------ */
+/* 4 waves; LPP lanes hold one key (8 dims each), 16 keys per workgroup step;
+ * an online softmax per lane group in log2 units, groups combined by
+ * shuffles and waves in LDS, as the decode step's attention phase. */
+template <int HD, int NREP>
+__global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, int qstride, int n_embed, int kv_dim,
+                                                 const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+                                                 int pos0, float* __restrict__ att)
+{
+    constexpr int LPP = HD / 8, PPW = 64 / LPP, WV = 4, PPB = WV * PPW;
+    __shared__ __attribute__((aligned(16))) float s_q[NREP * HD];
+    __shared__ __attribute__((aligned(16))) float s_kv[2 * HD];
+    __shared__ __attribute__((aligned(16))) float s_o[WV * NREP * HD];
+    __shared__ float s_m[WV * NREP], s_l[WV * NREP];
+    const int t = blockIdx.x, g = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gl = lane & (LPP - 1), grp = lane / LPP;
+    const int pos = pos0 + t;
+    const float* row = qkv + (size_t)t * qstride;
+    for (int i = threadIdx.x; i < NREP * HD; i += 256) s_q[i] = row[(size_t)g * NREP * HD + i];
+    for (int i = threadIdx.x; i < HD; i += 256) {
+        s_kv[i] = row[n_embed + g * HD + i];
+        s_kv[HD + i] = row[n_embed + kv_dim + g * HD + i];
+    }
+    __syncthreads();
+    const float scale2 = 1.44269504088896341f / sqrtf((float)HD);
+    float qr[NREP][8];
+#pragma unroll
+    for (int r = 0; r < NREP; r++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) qr[r][i] = s_q[r * HD + gl * 8 + i];
+    float m[NREP], l[NREP], o[NREP][8];
+#pragma unroll
+    for (int r = 0; r < NREP; r++) {
+        m[r] = -INFINITY;
+        l[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
+    }
+    for (int j0 = 0; j0 <= pos; j0 += PPB) {
+        const int j = j0 + wave * PPW + grp;
+        if (j <= pos) {
+            float kf[8], vf[8];
+            if (j < pos) {
+                const size_t off = (size_t)j * kv_dim + (size_t)g * HD + gl * 8;
+                const uint4 kb = *(const uint4*)(kc + off);
+                const uint4 vb = *(const uint4*)(vc + off);
+                const uint32_t ku[4] = {kb.x, kb.y, kb.z, kb.w}, vu[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kf[2 * i] = lg_h2f((uint16_t)(ku[i] & 0xffffu));
+                    kf[2 * i + 1] = lg_h2f((uint16_t)(ku[i] >> 16));
+                    vf[2 * i] = lg_h2f((uint16_t)(vu[i] & 0xffffu));
+                    vf[2 * i + 1] = lg_h2f((uint16_t)(vu[i] >> 16));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
+            }
+#pragma unroll
+            for (int r = 0; r < NREP; r++) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) sc += qr[r][i] * kf[i];
+                sc = lg_group_sum<LPP>(sc) * scale2;
+                const float mn = fmaxf(m[r], sc);
+                const float a = __builtin_amdgcn_exp2f(m[r] - mn);
+                const float pw = __builtin_amdgcn_exp2f(sc - mn);
+                l[r] = l[r] * a + pw;
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[r][i] = o[r][i] * a + pw * vf[i];
+                m[r] = mn;
+            }
+        }
+    }
+    /* lane groups of the wave, then the waves */
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < NREP; r++) {
+            const float m2 = __shfl_xor(m[r], off, 64), l2 = __shfl_xor(l[r], off, 64);
+            const float mn = fmaxf(m[r], m2);
+            const float a = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - mn);
+            const float bb = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
+            l[r] = l[r] * a + l2 * bb;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float o2 = __shfl_xor(o[r][i], off, 64);
+                o[r][i] = o[r][i] * a + o2 * bb;
+            }
+            m[r] = mn;
+        }
+    }
+    if (grp == 0) {
+#pragma unroll
+        for (int r = 0; r < NREP; r++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) s_o[(wave * NREP + r) * HD + gl * 8 + i] = o[r][i];
+            if (gl == 0) { s_m[wave * NREP + r] = m[r]; s_l[wave * NREP + r] = l[r]; }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NREP * HD; i += 256) {
+        const int r = i / HD, d = i % HD;
+        float M = -INFINITY;
+        for (int w = 0; w < WV; w++) M = fmaxf(M, s_m[w * NREP + r]);
+        float O = 0.0f, L = 0.0f;
+        for (int w = 0; w < WV; w++) {
+            const float mw = s_m[w * NREP + r];
+            const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            O += s_o[(w * NREP + r) * HD + d] * wt;
+            L += s_l[w * NREP + r] * wt;
+        }
+        att[(size_t)t * n_embed + (size_t)g * NREP * HD + i] = O / L;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Q4_K x Q8_K GEMM on int8 MFMA                                        */
+/* ------------------------------------------------------------------ */
+/* Workgroup tile: 32 tokens x 128 rows, 4 waves of 32 x 32 (2 x 2 MFMA
+ * tiles of 16 x 16).  v_mfma_i32_16x16x32_i8 (layout checked on the part):
+ * lane l holds A[token l%16][k 8(l/16)..+7], B[k 8(l/16)..+7][row l%16],
+ * D[token 4(l/16)+i][row l%16] in register i.  In a Q4_K block, byte 32c+i
+ * of qs holds value 64c+i (low nibble) and 64c+32+i (high nibble), so lane
+ * group g takes bytes 32c+8g..+7 of its row: the low nibbles are its 8
+ * values of sub-block 2c, the high ones of sub-block 2c+1; the activation
+ * bytes 64c+8g and 64c+32+8g match them.  The token tile of each block is
+ * staged in LDS (16-byte loads, double-buffered) and shared by the 4 waves;
+ * each wave reads its rows' bytes straight from the GGUF rows.  Rows and
+ * tokens past the ends are clamped for the loads and not stored. */
+template <int ACC>
+__global__ __launch_bounds__(256) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
+                                                     PfQ8K x, int T, float* __restrict__ out, int ldo)
+{
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][32 * 256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int nb = K >> 8;
+    const int t0 = blockIdx.y * 32;
+    const int r0 = blockIdx.x * 128 + wave * 32;
+    const uint8_t* wr[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) wr[ni] = W + (size_t)min(r0 + 16 * ni + l16, R - 1) * rsz;
+    int ta[2];   /* the lane's A tokens (M-term operand): t0 + 16 mi + l16 */
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++) ta[mi] = min(t0 + 16 * mi + l16, T - 1);
+    /* staging: thread -> (token 16k + tid/16, 16-byte chunk tid%16) */
+    const int st_tok = threadIdx.x >> 4, st_ch = threadIdx.x & 15;
+    const int8_t* st_src[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) st_src[k] = x.qs + (size_t)min(t0 + st_tok + 16 * k, T - 1) * K + st_ch * 16;
+
+    uint4 st[2];
+    auto stage_load = [&](int b) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) st[k] = *(const uint4*)(st_src[k] + (size_t)b * 256);
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) *(uint4*)(s_a[buf] + (st_tok + 16 * k) * 256 + st_ch * 16) = st[k];
+    };
+    /* per-block operands of the wave, loaded one block ahead */
+    struct Blk {
+        uint4 hdr[2];
+        uint2 wq[2][4];
+        int bsp[2][2];    /* bsums of the M-term A operand: [mi][kc] two int16 */
+        float4 dx[2];     /* d of the 4 output tokens 4g..4g+3 of tile mi */
+    };
+    auto blk_load = [&](Blk& B, int b) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            const uint8_t* p = wr[ni] + (size_t)b * LG_BS_Q4_K;
+            B.hdr[ni] = *(const uint4*)p;
+#pragma unroll
+            for (int c = 0; c < 4; c++) B.wq[ni][c] = *(const uint2*)(p + 16 + 32 * c + 8 * g);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const int16_t* bs = x.bs + ((size_t)ta[mi] * nb + b) * 16;
+#pragma unroll
+            for (int kc = 0; kc < 2; kc++) B.bsp[mi][kc] = *(const int*)(bs + 2 * (g + 4 * kc));
+            B.dx[mi] = *(const float4*)(x.d + (size_t)b * x.tld + min(t0 + 16 * mi + 4 * g, x.tld - 4));
+        }
+    };
+
+    v4f acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) acc[mi][ni] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    Blk cur, nxt;
+    stage_load(0);
+    blk_load(cur, 0);
+    stage_store(0);
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        const int bn = min(b + 1, nb - 1);
+        stage_load(bn);
+        blk_load(nxt, bn);
+        const int8_t* sa = s_a[b & 1];
+
+        /* scales of the lane's two rows (get_scale_min_k4, fast/lil_math.cpp:129-138) */
+        uint32_t scq[2][2];   /* [ni][lo/hi]: sc_j of sub-blocks 0-3 / 4-7, one per byte */
+        float mb[2][2], dw[2], dmw[2];
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            const uint4 h = cur.hdr[ni];
+            scq[ni][0] = h.y & 0x3F3F3F3Fu;
+            scq[ni][1] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+            const uint32_t mlo = h.z & 0x3F3F3F3Fu;
+            const uint32_t mhi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+            mb[ni][0] = (float)((mlo >> (8 * g)) & 0xFFu);   /* m_j, j = g */
+            mb[ni][1] = (float)((mhi >> (8 * g)) & 0xFFu);   /* m_j, j = g + 4 */
+            dw[ni] = lg_h2f((uint16_t)(h.x & 0xffffu));
+            dmw[ni] = lg_h2f((uint16_t)(h.x >> 16));
+        }
+        v4i S[2][2];
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) S[mi][ni] = (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int j = 2 * c + h;
+                long bf[2], af[2];
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++) {
+                    const uint2 q = cur.wq[ni][c];
+                    const uint32_t lo = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+                    const uint32_t hi = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+                    bf[ni] = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                }
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++) af[mi] = *(const long*)(sa + (16 * mi + l16) * 256 + 64 * c + 32 * h + 8 * g);
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                    for (int ni = 0; ni < 2; ni++) {
+                        const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[mi], bf[ni], (v4i){0, 0, 0, 0}, 0, 0, 0);
+                        const int sc = (int)((scq[ni][j >> 2] >> (8 * (j & 3))) & 0xFFu);
+                        S[mi][ni] += sc * is;
+                    }
+            }
+        }
+        /* mins term and the block's fp32 contribution */
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            float bpa[2];
+#pragma unroll
+            for (int kc = 0; kc < 2; kc++) {
+                const int v = cur.bsp[mi][kc];
+                bpa[kc] = (float)((int)(int16_t)(v & 0xffff) + (int)(int16_t)(v >> 16));
+            }
+            const float dx[4] = {cur.dx[mi].x, cur.dx[mi].y, cur.dx[mi].z, cur.dx[mi].w};
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                v4f M = __builtin_amdgcn_mfma_f32_16x16x4f32(bpa[0], mb[ni][0], (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                M = __builtin_amdgcn_mfma_f32_16x16x4f32(bpa[1], mb[ni][1], M, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[mi][ni][i] += dx[i] * (dw[ni] * (float)S[mi][ni][i] - dmw[ni] * M[i]);
+            }
+        }
+        stage_store((b + 1) & 1);
+        cur = nxt;
+        __syncthreads();
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            const int r = r0 + 16 * ni + l16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = t0 + 16 * mi + 4 * g + i;
+                if (t < T && r < R) {
+                    float* o = out + (size_t)t * ldo + r;
+                    *o = ACC ? *o + acc[mi][ni][i] : acc[mi][ni][i];
+                }
+            }
+        }
+}
+
+/* ------------------------------------------------------------------ */
+/* host side                                                            */
+/* ------------------------------------------------------------------ */
+int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                        int accumulate, hipStream_t s)
+{
+    if (!W || !out || rows <= 0 || cols <= 0 || cols % 256 || T <= 0 || T > x.tld || x.tld % 4 ||
+        rsz != (uint32_t)(cols / 256) * LG_BS_Q4_K || ldo < rows) {
+        lg_set_error("prefill gemm: bad arguments (rows %d, cols %d, T %d)", rows, cols, T);
+        return LG_ERR_ARG;
+    }
+    const dim3 grid((rows + 127) / 128, (T + 31) / 32), blk(256);
+    if (accumulate) hipLaunchKernelGGL(k_pf_gemm_q4k<1>, grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    else hipLaunchKernelGGL(k_pf_gemm_q4k<0>, grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    return lg_check_launch("prefill gemm");
+}
+
+int lg_prefill_quantize(const float* x, int ldx, const float* norm_w, float eps, int n, int T, const PfQ8K& q,
+                        hipStream_t s)
+{
+    if (!x || n <= 0 || n % 256 || T <= 0 || T > q.tld || ldx < n) {
+        lg_set_error("prefill quantize: bad arguments (n %d, T %d)", n, T);
+        return LG_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_pf_quant, dim3(n / 256, T), dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    return lg_check_launch("prefill quantize");
+}
+
+typedef void (*pf_attn_t)(const float*, int, int, int, const uint16_t*, const uint16_t*, int, float*);
+
+static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_t* kc, const uint16_t* vc, int T,
+                       int pos0, float* att, hipStream_t s)
+{
+    const int nrep = M.n_heads / M.n_kv;
+    const dim3 grid(T, M.n_kv), blk(256);
+    if (M.head_dim != 128) { lg_set_error("prefill attention: head_dim %d", M.head_dim); return LG_ERR_TYPE; }
+    switch (nrep) {
+    case 1: hipLaunchKernelGGL((k_pf_attn<128, 1>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
+    case 2: hipLaunchKernelGGL((k_pf_attn<128, 2>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
+    case 4: hipLaunchKernelGGL((k_pf_attn<128, 4>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
+    case 8: hipLaunchKernelGGL((k_pf_attn<128, 8>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
+    default: lg_set_error("prefill attention: %d query heads per KV head", nrep); return LG_ERR_TYPE;
+    }
+    return lg_check_launch("prefill attention");
+}
+
+int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream_t s)
+{
+    if (T <= 0 || T > B.tmax || pos0 < 0 || pos0 + T > M.n_ctx) {
+        lg_set_error("prefill: %d tokens at %d (buffers for %d, context %d)", T, pos0, B.tmax, M.n_ctx);
+        return LG_ERR_STATE;
+    }
+    const int ne = M.n_embed, kvd = M.kv_dim, qs = ne + 2 * kvd, nff = M.n_ff;
+    int rc;
+    hipLaunchKernelGGL(k_pf_embed, dim3(T), dim3(256), 0, s, M.embd_t, M.embd, M.embd_rsz, B.toks, ne, B.x);
+    if ((rc = lg_check_launch("prefill embedding"))) return rc;
+    for (int l = 0; l < M.n_layers; l++) {
+        const PfLayer& L = M.layers[l];
+        uint16_t* kc = M.kc + (size_t)l * M.n_ctx * kvd;
+        uint16_t* vc = M.vc + (size_t)l * M.n_ctx * kvd;
+        /* attention branch */
+        if ((rc = lg_prefill_quantize(B.x, ne, L.att_norm, M.eps, ne, T, B.q, s))) return rc;
+        if ((rc = lg_prefill_gemm_q4k(L.qkv, L.qkv_rsz, qs, ne, B.q, T, B.qkv, qs, 0, s))) return rc;
+        const int waves = M.n_heads + M.n_kv;
+        hipLaunchKernelGGL(k_pf_qk_rope_kv, dim3((waves + 3) / 4, T), dim3(256), 0, s, B.qkv, qs, ne, kvd, L.q_norm,
+                           L.k_norm, M.n_heads, M.n_kv, M.head_dim, M.rope_dim, pos0, M.rope_freq, M.eps, kc, vc);
+        if ((rc = lg_check_launch("prefill qk-norm/rope/kv"))) return rc;
+        if ((rc = launch_attn(M, B.qkv, qs, kc, vc, T, pos0, B.att, s))) return rc;
+        if ((rc = lg_prefill_quantize(B.att, ne, nullptr, M.eps, ne, T, B.q, s))) return rc;
+        if ((rc = lg_prefill_gemm_q4k(L.ao, L.ao_rsz, ne, ne, B.q, T, B.x, ne, 1, s))) return rc;
+        /* FFN branch */
+        if ((rc = lg_prefill_quantize(B.x, ne, L.ffn_norm, M.eps, ne, T, B.q, s))) return rc;
+        if ((rc = lg_prefill_gemm_q4k(L.ug, L.ug_rsz, 2 * nff, ne, B.q, T, B.ug, 2 * nff, 0, s))) return rc;
+        hipLaunchKernelGGL(k_pf_swiglu_quant, dim3(nff / 256, T), dim3(64), 0, s, B.ug, nff, B.q);
+        if ((rc = lg_check_launch("prefill swiglu"))) return rc;
+        if ((rc = lg_prefill_gemm_q4k(L.down, L.down_rsz, ne, nff, B.q, T, B.x, ne, 1, s))) return rc;
+    }
+    return LG_OK;
+}

@@ -102,7 +102,16 @@ __device__ __forceinline__ float lg_dq_value(int type, const uint8_t* row, int64
  * compiles it (fast/lil_math.cpp:358-394 under -Ofast): first-index signed
  * max of |x|, iscale = -127/max, q = min(127, trunc(iscale*x -+ 0.5)),
  * 16-value bsums, d = max * (-1/127). */
-__device__ __forceinline__ void lg_q8k_block(const float v[4], uint8_t* __restrict__ out)
+/* one lane's share of a Q8_K block: its 4 quants packed, the 16-value sum
+ * of its lane quad (bsums entry, in every lane of the quad) and the block
+ * scale d */
+struct Q8KLane {
+    uint32_t packed;
+    int bsum;
+    float d;
+};
+
+__device__ __forceinline__ Q8KLane lg_q8k_lane(const float v[4])
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -143,9 +152,21 @@ __device__ __forceinline__ void lg_q8k_block(const float v[4], uint8_t* __restri
         }
     }
     s = lg_group_isum<4>(s);
-    *(uint32_t*)(out + 4 + 4 * lane) = packed;
-    if ((lane & 3) == 0) *(int16_t*)(out + 260 + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *(float*)out = amax != 0.0f ? mx * (-1.0f / 127.0f) : 0.0f;
+    Q8KLane r;
+    r.packed = packed;
+    r.bsum = s;
+    r.d = amax != 0.0f ? mx * (-1.0f / 127.0f) : 0.0f;
+    return r;
+}
+
+/* the block as quantize_q8_K lays it out: d, qs[256], bsums[16] */
+__device__ __forceinline__ void lg_q8k_block(const float v[4], uint8_t* __restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    const Q8KLane q = lg_q8k_lane(v);
+    *(uint32_t*)(out + 4 + 4 * lane) = q.packed;
+    if ((lane & 3) == 0) *(int16_t*)(out + 260 + 2 * (lane >> 2)) = (int16_t)q.bsum;
+    if (lane == 0) *(float*)out = q.d;
 }
 
 /* Eight Q8_0 blocks from the wave's 256 values (block = lane/8), or fewer

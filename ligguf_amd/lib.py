@@ -23,6 +23,7 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q1_0: (32, 6), Q1_G: (128, 18
 
 ARCH_LLAMA, ARCH_QWEN3 = 0, 1
 PATH_AUTO, PATH_PERSISTENT, PATH_MULTI, PATH_FUSED = 0, 1, 2, 3
+PREFILL_AUTO, PREFILL_STEPS, PREFILL_BATCHED = 0, 1, 2
 
 _vp = C.c_void_p
 
@@ -67,12 +68,15 @@ SIGNATURES = {
     "lg_trace_size": (C.c_size_t, [_vp]),
     "lg_time_fused_phase": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "lg_prefill": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),
+    "lg_set_prefill_path": (C.c_int, [_vp, C.c_int]),
+    "lg_prefill_path": (C.c_int, [_vp]),
     "lg_kv_read": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "lg_kv_write": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "lg_dequantize_row": (C.c_int, [C.c_int, _vp, _vp, C.c_int64, _vp]),
     "lg_quantize_q8_0": (C.c_int, [_vp, C.c_int64, _vp, _vp]),
     "lg_quantize_q8_K": (C.c_int, [_vp, C.c_int64, _vp, _vp]),
     "lg_matvec": (C.c_int, [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp]),
+    "lg_matmul_tokens": (C.c_int, [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
     "lg_rmsnorm_quant": (C.c_int, [_vp, _vp, C.c_int, C.c_float, C.c_int, _vp, _vp, _vp]),
     "lg_qk_norm_rope_kv": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp,
                                      C.c_float, _vp, _vp, _vp]),

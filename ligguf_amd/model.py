@@ -311,6 +311,13 @@ class Engine:
         check(self.lib.lg_argmax(self.ctx, C.byref(t)), self.ctx)
         return int(t.value)
 
+    def set_prefill_path(self, path: int) -> None:
+        """lg_set_prefill_path: PREFILL_AUTO, PREFILL_STEPS or PREFILL_BATCHED."""
+        check(self.lib.lg_set_prefill_path(self.ctx, path), self.ctx)
+
+    def prefill_path(self) -> int:
+        return int(self.lib.lg_prefill_path(self.ctx))
+
     def prefill(self, toks, pos0: int, want_logits: bool = True):
         arr = np.ascontiguousarray(toks, dtype=np.int32)
         out = np.empty(self.vocab, np.float32) if want_logits else None

@@ -50,6 +50,14 @@ def matvec(t: int, w: torch.Tensor, rsz: int, n: int, d: int, xq: torch.Tensor, 
     return out
 
 
+def matmul_tokens(t: int, w: torch.Tensor, rsz: int, n: int, d: int, x: torch.Tensor) -> torch.Tensor:
+    """lg_matmul_tokens: x [T, n] fp32 -> [T, d], each row quantized to Q8_K."""
+    T = x.shape[0]
+    out = torch.empty((T, d), dtype=torch.float32, device=w.device)
+    check(load().lg_matmul_tokens(t, _p(w), rsz, n, d, _p(x), T, _p(out), _stream()))
+    return out
+
+
 def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, qtype: int, want_float: bool = False):
     n = x.numel()
     if qtype == F32:

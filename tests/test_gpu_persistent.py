@@ -16,7 +16,8 @@ import os
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0, LgError
+from ligguf_amd.lib import (PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q1_G, Q4_K, Q5_K, Q6_K,
+                            Q8_0, LgError)
 from ligguf_amd.model import Engine, HostModel, ModelConfig
 from test_gpu_decode import one_step_errors, rel
 
@@ -137,8 +138,10 @@ def test_prefill_equals_sequential_and_greedy(pk_model, path):
     sampler_greedy of that step's logits."""
     hm, eng = pk_model
     eng.set_path(path)
+    eng.set_prefill_path(PREFILL_STEPS)
     prompt = np.random.default_rng(9).integers(1, hm.cfg.vocab, 20)
     lg_prefill = eng.prefill(prompt, 0)
+    eng.set_prefill_path(PREFILL_AUTO)
     for i, t in enumerate(prompt):
         lg_seq = eng.decode(int(t), i)
     assert np.array_equal(lg_prefill.view(np.uint32), lg_seq.view(np.uint32))

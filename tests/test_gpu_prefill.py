@@ -1,0 +1,174 @@
+"""The batched prefill: lg_matmul_tokens (the int8 MFMA GEMM of T tokens)
+against the oracle's matvec of every token, and lg_prefill with
+LG_PREFILL_BATCHED against the token-by-token prefill (LG_PREFILL_STEPS,
+itself bit-equal to sequential decode steps) and against the oracle.
+
+The GEMM reproduces the integer sub-block sums of the reference's Q4_K x Q8_K
+dot exactly (fast/lil_math.cpp:582-616) and combines them in fp32 per
+256-value block, so each output is held to the matvec bar: within 2e-6 of the
+row's sum of |terms|.  Whole prompts accumulate fp32 order differences over
+their tokens; an activation that lands on the other side of an int8 rounding
+boundary moves later logits by up to ~2e-2 (the same effect the decode tests
+document), so the prompt checks bound the logits and the KV cache loosely and
+require the greedy next token to agree."""
+import numpy as np
+import pytest
+
+from ligguf_amd import encode, ops
+from ligguf_amd.lib import (PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS, Q4_K, Q5_K, Q6_K, Q8_0, LgError,
+                            row_size)
+from ligguf_amd.model import Engine, HostModel, ModelConfig
+from test_gpu_decode import oracle_state, rel
+from test_gpu_ops import MATVEC_TOL, dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("d,n,T", [(200, 512, 37), (130, 256, 1), (384, 12288, 5), (4096, 4096, 64),
+                                   (6144, 4096, 100)])
+def test_matmul_tokens_vs_oracle(gpu, oracle, d, n, T):
+    rng = np.random.default_rng(d + T)
+    w = encode.random_tensor(Q4_K, d + n, Q4_K, d, n)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    rsz = row_size(Q4_K, n)
+    y = host(ops.matmul_tokens(Q4_K, dev(w, gpu), rsz, n, d, dev(x, gpu)))
+    toks = range(T) if T <= 40 else rng.choice(T, 12, replace=False)
+    for t in toks:
+        ref, ab = oracle.matvec_q(Q4_K, w, rsz, n, d, oracle.quantize_q8_K(x[t]), want_abs=True)
+        err = np.abs(y[t] - ref) / np.maximum(ab, 1e-30)
+        assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
+
+
+def test_matmul_tokens_rejects_other_types(gpu):
+    x = dev(np.zeros((2, 256), np.float32), gpu)
+    w = dev(np.zeros(row_size(Q6_K, 256) * 4, np.uint8), gpu)
+    with pytest.raises(LgError):
+        ops.matmul_tokens(Q6_K, w, row_size(Q6_K, 256), 256, 4, x)
+
+
+Q4K_MODELS = [
+    ModelConfig("qwen3-w4096-q4k", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
+    ModelConfig("llama-w4096-q4k-nrep1", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q8_0, Q4_K),
+]
+
+
+@pytest.fixture(scope="module", params=Q4K_MODELS, ids=lambda c: c.name)
+def q4k_model(request, gpu):
+    cfg = request.param
+    hm = HostModel.synthetic(cfg)
+    eng = Engine(0)
+    eng.load(hm)
+    yield hm, eng
+    eng.close()
+
+
+def run_prefill(eng, path, prompt, pos0=0):
+    eng.set_prefill_path(path)
+    lg = eng.prefill(prompt, pos0)
+    return lg, eng.argmax()
+
+
+def test_prefill_path_selection(q4k_model):
+    hm, eng = q4k_model
+    eng.set_prefill_path(PREFILL_AUTO)
+    assert eng.prefill_path() == PREFILL_BATCHED
+    eng.set_prefill_path(PREFILL_STEPS)
+    assert eng.prefill_path() == PREFILL_STEPS
+    eng.set_prefill_path(PREFILL_AUTO)
+
+
+def near_best(lg, tok, tol=3e-2):
+    """tok is the argmax of lg, or within the flip tolerance of it (a near tie)"""
+    return tok == int(np.argmax(lg)) or lg[tok] >= lg.max() - tol * np.abs(lg).max()
+
+
+@pytest.mark.parametrize("n", [2, 33, 200])
+def test_batched_equals_steps(q4k_model, n):
+    """Against the token-by-token prefill, beside the distance between the two
+    token-by-token paths (fused kernels and one kernel per op) on the same
+    prompt: an int8 flip moves a whole later-layer KV row, for every path
+    pair alike.  Layer 0's K/V depend on their own token only, so they agree
+    to fp16 rounding."""
+    hm, eng = q4k_model
+    cfg = hm.cfg
+    prompt = np.random.default_rng(n).integers(1, cfg.vocab, n)
+    lg_s, tok_s = run_prefill(eng, PREFILL_STEPS, prompt)
+    k_s, v_s = eng.kv_read(0, cfg.n_layers, 0, n)
+    eng.set_path(PATH_MULTI)
+    lg_m, _ = run_prefill(eng, PREFILL_STEPS, prompt)
+    eng.set_path(PATH_AUTO)
+    lg_b, tok_b = run_prefill(eng, PREFILL_BATCHED, prompt)
+    k_b, v_b = eng.kv_read(0, cfg.n_layers, 0, n)
+    e, e_paths = rel(lg_b, lg_s), rel(lg_m, lg_s)
+    L, kvd = cfg.n_layers, cfg.kv_dim
+    k_s, k_b, v_s, v_b = (a.reshape(L, n, kvd) for a in (k_s, k_b, v_s, v_b))
+    eq0 = min(np.mean(k_s[0] == k_b[0]), np.mean(v_s[0] == v_b[0]))
+
+    def maxrel(a, b):
+        fa, fb = a.view(np.float16).astype(np.float32), b.view(np.float16).astype(np.float32)
+        return float(np.max(np.abs(fa - fb)) / np.max(np.abs(fa)))
+    kv_err = max(maxrel(k_s, k_b), maxrel(v_s, v_b))
+    print(f"\n{cfg.name} n={n}: logits batched-vs-steps {e:.2e} (multi-vs-fused steps {e_paths:.2e}); "
+          f"layer-0 KV equal {eq0:.4f}; KV max rel diff {kv_err:.1e}")
+    assert e <= 3e-2
+    assert eq0 >= 0.99
+    assert kv_err <= 5e-2
+    assert near_best(lg_s, tok_b)
+    # the next step reads the batched KV state as it reads the sequential one
+    a = eng.decode(int(tok_s), n)
+    assert np.array_equal(a, eng.decode(int(tok_s), n))
+
+
+def test_batched_prefill_vs_oracle(q4k_model, oracle):
+    """The last token's logits of a 24-token prompt against the oracle's
+    sequential inference() over the same prompt."""
+    hm, eng = q4k_model
+    cfg = hm.cfg
+    prompt = np.random.default_rng(77).integers(1, cfg.vocab, 24)
+    st = oracle_state(oracle, hm)
+    for t in prompt:
+        ref = oracle.inference(st, int(t), cfg.vocab)
+    oracle.free_state(st)
+    lg_b, tok_b = run_prefill(eng, PREFILL_BATCHED, prompt)
+    e = rel(lg_b, ref)
+    print(f"\n{cfg.name}: batched prefill vs oracle {e:.2e}")
+    assert e <= 3e-2
+    assert near_best(ref, tok_b)
+
+
+def test_batched_prefill_in_several_passes(q4k_model):
+    """A prompt longer than one pass (512 tokens) continues the KV cache across
+    passes; at pos0 > 0 the pass reads the rows before it."""
+    hm, eng = q4k_model
+    cfg = hm.cfg
+    n = min(600, cfg.n_context - 8)
+    prompt = np.random.default_rng(5).integers(1, cfg.vocab, n)
+    lg_s, tok_s = run_prefill(eng, PREFILL_STEPS, prompt)
+    lg_b, tok_b = run_prefill(eng, PREFILL_BATCHED, prompt)
+    e = rel(lg_b, lg_s)
+    # a second prompt appended at pos0 = n on top of each state
+    more = np.random.default_rng(6).integers(1, cfg.vocab, 5)
+    run_prefill(eng, PREFILL_STEPS, prompt)
+    lg_s2, _ = run_prefill(eng, PREFILL_STEPS, more, n)
+    run_prefill(eng, PREFILL_BATCHED, prompt)
+    lg_b2, _ = run_prefill(eng, PREFILL_BATCHED, more, n)
+    e2 = rel(lg_b2, lg_s2)
+    print(f"\n{cfg.name}: n={n} rel {e:.2e}; +5 at pos {n} rel {e2:.2e}")
+    assert e <= 3e-2 and e2 <= 3e-2
+    assert near_best(lg_s, tok_b)
+
+
+def test_batched_prefill_unavailable_for_other_types(gpu):
+    cfg = ModelConfig("llama-w4096-q5k", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q5_K, Q8_0, Q4_K)
+    hm = HostModel.synthetic(cfg)
+    eng = Engine(0)
+    eng.load(hm)
+    try:
+        assert eng.prefill_path() == PREFILL_STEPS
+        with pytest.raises(LgError):
+            eng.set_prefill_path(PREFILL_BATCHED)
+        eng.set_path(PATH_FUSED)
+        lg = eng.prefill(np.arange(1, 9), 0)       # AUTO falls back to steps
+        assert np.all(np.isfinite(lg))
+    finally:
+        eng.close()
