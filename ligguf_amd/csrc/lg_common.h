@@ -112,6 +112,20 @@ __device__ __forceinline__ float lg_group_sum(float v)
     return v;
 }
 
+/* sum over the 64 lanes of a wave, returned as a wave-uniform value: the
+ * 16-lane rows by the butterfly, then DPP row_bcast:15 / row_bcast:31 carry
+ * the row sums up to lane 63 ((r3 + r2) + (r1 + r0)), read back as a scalar
+ * -- no cross-row permute through LDS */
+#define LG_DPP_ROW_BCAST15 0x142
+#define LG_DPP_ROW_BCAST31 0x143
+__device__ __forceinline__ float lg_wave_sum(float v)
+{
+    v = lg_group_sum<16>(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), LG_DPP_ROW_BCAST15, 0xA, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), LG_DPP_ROW_BCAST31, 0xC, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 template <int G>
 __device__ __forceinline__ float lg_group_max(float v)
 {

@@ -124,18 +124,20 @@ struct Fmt<LG_Q4_K> {
             dl = lg_dot4((int)(q[i] & 0x0F0F0F0Fu), A.a[i], dl);
             dh = lg_dot4((int)((q[i] >> 4) & 0x0F0F0F0Fu), A.a[8 + i], dh);
         }
-        /* scales[12] = bytes 4..15 of the header */
-        const int j0 = 2 * c, j1 = 2 * c + 1;
-        int sc0, m0, sc1, m1;
-        if (c < 2) {
-            sc0 = byte16(w.h, 4 + j0) & 63; m0 = byte16(w.h, 8 + j0) & 63;
-            sc1 = byte16(w.h, 4 + j1) & 63; m1 = byte16(w.h, 8 + j1) & 63;
-        } else {
-            sc0 = (byte16(w.h, 8 + j0) & 15) | ((byte16(w.h, j0) >> 6) << 4);
-            m0 = (byte16(w.h, 8 + j0) >> 4) | ((byte16(w.h, 4 + j0) >> 6) << 4);
-            sc1 = (byte16(w.h, 8 + j1) & 15) | ((byte16(w.h, j1) >> 6) << 4);
-            m1 = (byte16(w.h, 8 + j1) >> 4) | ((byte16(w.h, 4 + j1) >> 6) << 4);
-        }
+        /* get_scale_min_k4 (fast/lil_math.cpp:129-138) of sub-blocks 2c and
+         * 2c+1 without a branch: the header's scales[12] are bytes 4..15
+         * (y, z, w); v_perm_b32 gathers, at lane-constant positions e,
+         * A4 = {y.e, y.e+1, z.e, z.e+1} and B4 = {w.e, w.e+1, w.e, w.e+1};
+         * sub-blocks 0..3 take A4 & 63, sub-blocks 4..7 the low (sc) or high
+         * (m) nibble of B4 with the top two bits of A4 above it */
+        const uint32_t e = (uint32_t)(c & 1) * 2u;
+        const uint32_t A4 = __builtin_amdgcn_perm(w.h.z, w.h.y, e | ((e + 1) << 8) | ((e + 4) << 16) | ((e + 5) << 24));
+        const uint32_t B4 = __builtin_amdgcn_perm(w.h.w, w.h.w, e | ((e + 1) << 8) | (e << 16) | ((e + 1) << 24));
+        const uint32_t lo = A4 & 0x3F3F3F3Fu;
+        const uint32_t hi = ((A4 >> 2) & 0x30303030u) | (B4 & 0x00000F0Fu) | ((B4 >> 4) & 0x0F0F0000u);
+        const uint32_t r = c < 2 ? lo : hi;
+        const int sc0 = (int)(r & 0xFFu), sc1 = (int)((r >> 8) & 0xFFu);
+        const int m0 = (int)((r >> 16) & 0xFFu), m1 = (int)(r >> 24);
         const float d = lg_h2f((uint16_t)(w.h.x & 0xffffu)), dmin = lg_h2f((uint16_t)(w.h.x >> 16));
         const int S = sc0 * dl + sc1 * dh;
         const int M = m0 * (A.bs[0] + A.bs[1]) + m1 * (A.bs[2] + A.bs[3]);

@@ -417,7 +417,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                     float a = 0.0f;
 #pragma unroll
                     for (int s = 0; s < NS; s++) a += F::dot(R.w[b][k][s], act[s], lane + 64 * s);
-                    acc[k] = lg_group_sum<64>(a);
+                    acc[k] = lg_wave_sum(a);
                 }
                 const int i = i0 + b0 + b;
                 if (EPI == EPI_LOGITS) {
