@@ -126,6 +126,19 @@ __device__ __forceinline__ float lg_wave_sum(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+/* the value of the 16-lane row above (row r+1 for even r; odd rows get their
+ * own) and of the lane 32 above (lanes 0..31): v_permlane16_swap /
+ * v_permlane32_swap, VALU with no LDS round trip */
+__device__ __forceinline__ float lg_from_row_above(float x)
+{
+    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+}
+
+__device__ __forceinline__ float lg_from_half_above(float x)
+{
+    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+}
+
 template <int G>
 __device__ __forceinline__ float lg_group_max(float v)
 {

@@ -732,15 +732,19 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                 }
             }
         }
-        /* combine the position groups of the wave, then the waves (LDS) */
+        /* combine the position groups of the wave into group 0 (16-lane
+         * rows: row 1 -> 0 and 3 -> 2, then 2 -> 0, by lane permutes), then
+         * the waves (LDS) */
+        static_assert(LPP == 16, "position groups are 16-lane rows");
 #pragma unroll
-        for (int off = LPP; off < 64; off <<= 1) {
+        for (int step = 0; step < 2; step++) {
 #pragma unroll
             for (int r = 0; r < NREP; r++) {
                 float o2[8];
 #pragma unroll
-                for (int i = 0; i < 8; i++) o2[i] = __shfl_xor(o[r][i], off, 64);
-                const float m2 = __shfl_xor(m[r], off, 64), l2 = __shfl_xor(l[r], off, 64);
+                for (int i = 0; i < 8; i++) o2[i] = step ? lg_from_half_above(o[r][i]) : lg_from_row_above(o[r][i]);
+                const float m2 = step ? lg_from_half_above(m[r]) : lg_from_row_above(m[r]);
+                const float l2 = step ? lg_from_half_above(l[r]) : lg_from_row_above(l[r]);
                 osm_merge(m[r], l[r], o[r], m2, l2, o2, 8);
             }
         }

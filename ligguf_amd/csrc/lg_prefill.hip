@@ -110,8 +110,8 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope_kv(float* __restrict__ qkv, 
 /* causal attention: query token t, kv head g                           */
 /* ------------------------------------------------------------------ */
 /* 4 waves; LPP lanes hold one key (8 dims each), 16 keys per workgroup step;
- * an online softmax per lane group in log2 units, groups combined by
- * shuffles and waves in LDS, as the decode step's attention phase. */
+ * an online softmax per lane group in log2 units, groups combined by lane
+ * permutes and waves in LDS, as the decode step's attention phase. */
 template <int HD, int NREP>
 __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, int qstride, int n_embed, int kv_dim,
                                                  const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
@@ -183,19 +183,22 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
             }
         }
     }
-    /* lane groups of the wave, then the waves */
+    /* lane groups (16-lane rows) of the wave into group 0 by lane permutes,
+     * then the waves */
+    static_assert(LPP == 16, "key groups are 16-lane rows");
 #pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) {
+    for (int step = 0; step < 2; step++) {
 #pragma unroll
         for (int r = 0; r < NREP; r++) {
-            const float m2 = __shfl_xor(m[r], off, 64), l2 = __shfl_xor(l[r], off, 64);
+            const float m2 = step ? lg_from_half_above(m[r]) : lg_from_row_above(m[r]);
+            const float l2 = step ? lg_from_half_above(l[r]) : lg_from_row_above(l[r]);
             const float mn = fmaxf(m[r], m2);
             const float a = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - mn);
             const float bb = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
             l[r] = l[r] * a + l2 * bb;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float o2 = __shfl_xor(o[r][i], off, 64);
+                const float o2 = step ? lg_from_half_above(o[r][i]) : lg_from_row_above(o[r][i]);
                 o[r][i] = o[r][i] * a + o2 * bb;
             }
             m[r] = mn;
