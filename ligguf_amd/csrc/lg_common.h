@@ -69,7 +69,8 @@ __device__ __forceinline__ int lg_dot4(int a, int b, int c)
  * after steps 0..log2(G)-1 each aligned group of G lanes has combined all of
  * its members: steps 0-3 are DPP permutes inside 16-lane rows (quad_perm
  * [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror -- each pairs
- * two already-combined halves), steps 4-5 cross rows (ds_bpermute).  Every
+ * two already-combined halves), steps 4-5 cross rows (v_permlane16_swap,
+ * v_permlane32_swap: VALU, no LDS round trip).  Every
  * lane ends with the same bits: each pairwise op sees the same two operands. */
 #define LG_DPP_XOR1 0xB1
 #define LG_DPP_XOR2 0x4E
@@ -89,14 +90,37 @@ __device__ __forceinline__ int lg_partner(int v)
     else if constexpr (K == 1) return lg_dpp<LG_DPP_XOR2>(v);
     else if constexpr (K == 2) return lg_dpp<LG_DPP_HALF_MIRROR>(v);
     else if constexpr (K == 3) return lg_dpp<LG_DPP_MIRROR>(v);
-    else if constexpr (K == 4) return __shfl_xor(v, 16, LG_WAVE);
-    else return __shfl_xor(v, 32, LG_WAVE);
+    else if constexpr (K == 4) {
+        /* lane ^ 16: v_permlane16_swap gives even rows the row above ([1])
+         * and odd rows the row below ([0]) */
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)((__lane_id() & 16) ? r[0] : r[1]);
+    } else {
+        /* lane ^ 32: v_permlane32_swap, lanes 0..31 get [1], 32..63 [0] */
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)((__lane_id() & 32) ? r[0] : r[1]);
+    }
 }
 
 template <int K>
 __device__ __forceinline__ float lg_partner(float v)
 {
     return __int_as_float(lg_partner<K>(__float_as_int(v)));
+}
+
+/* a*b + c*d rounded one fixed way, fma(c, d, a*b): in an expression of two
+ * products the compiler picks which product it fuses into the add, and may
+ * pick differently in different kernels -- the paths would then disagree in
+ * the last bit */
+__device__ __forceinline__ float lg_fma2(float a, float b, float c, float d)
+{
+    return __builtin_fmaf(c, d, a * b);
+}
+
+/* x^2 + y^2 + z^2 + w^2 in one fixed order */
+__device__ __forceinline__ float lg_sq4(float4 t)
+{
+    return __builtin_fmaf(t.w, t.w, __builtin_fmaf(t.z, t.z, __builtin_fmaf(t.y, t.y, t.x * t.x)));
 }
 
 /* sum over aligned groups of G lanes (G a power of two <= 64) */
@@ -124,6 +148,21 @@ __device__ __forceinline__ float lg_wave_sum(float v)
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), LG_DPP_ROW_BCAST15, 0xA, 0xF, false));
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), LG_DPP_ROW_BCAST31, 0xC, 0xF, false));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+/* sum of x[0..n)^2 by one wave (n a multiple of 256), in the order of the
+ * whole-step kernels' rmsnorm build: the 256-value chunks in 8 interleaved
+ * groups (chunk % 8), lane partials in chunk order, one lg_wave_sum per
+ * group, the group sums added in group order */
+__device__ __forceinline__ float lg_sumsq_chunked(const float* __restrict__ x, int n, int lane)
+{
+    float ss = 0.0f;
+    for (int w = 0; w < 8; w++) {
+        float p = 0.0f;
+        for (int i = 256 * w + 4 * lane; i < n; i += 2048) p += lg_sq4(*(const float4*)(x + i));
+        ss += lg_wave_sum(p);
+    }
+    return ss;
 }
 
 /* the value of the 16-lane row above (row r+1 for even r; odd rows get their

@@ -136,12 +136,23 @@ struct lg_ctx {
     const void* pk_kernel = nullptr; /* the instantiation for this model */
     uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
     uint64_t pk_base = 0;
+    uint32_t pk_tag = 0;             /* tag of the last persistent launch (tagged activations) */
+    uint64_t* pk_tagged = nullptr;   /* the tagged activation arena and its size in words */
+    size_t pk_tagged_n = 0;
     int* pk_status_host = nullptr;   /* pinned {token, error} of the last persistent / fused step */
     bool last_was_pk = false;        /* the last step left its greedy token in pk_status_host */
 
     /* fused per-phase kernels replayed from a HIP graph (lg_fused.hip) */
     const void* fused_fn = nullptr;
     std::vector<PkLayer> pk_layers;  /* host copy: the fused kernels take their layer by value */
+    /* layer matrices and norms of models with one shape and type per matrix
+     * kind: one allocation per kind, layer l at l * stride */
+    struct {
+        bool ok;
+        uint8_t *qkv, *ao, *ug, *down;
+        size_t qkv_b, ao_b, ug_b, down_b;
+        float *att_norm, *ffn_norm, *q_norm, *k_norm;
+    } arena = {};
     /* batched prefill */
     bool pf_ok = false;
     int prefill_path = LG_PREFILL_AUTO;
@@ -189,6 +200,7 @@ static void free_model(lg_ctx* ctx)
     ctx->dev_known = false;
     ctx->dev_feed_end = 0;
     ctx->pf_ok = false;
+    ctx->arena = {};
     ctx->pf_layers.clear();
     ctx->pf = PfBuffers{};
     if (ctx->graph) {
@@ -251,10 +263,10 @@ static int check_weight(const lg_weight& w, int rows, int cols, const char* name
     return LG_OK;
 }
 
-static int upload_weight(lg_ctx* ctx, const lg_weight& w, dweight& d)
+static int upload_weight(lg_ctx* ctx, const lg_weight& w, dweight& d, uint8_t* dst = nullptr)
 {
     const size_t bytes = (size_t)w.rows * w.rsz;
-    int rc = dalloc(ctx, (void**)&d.data, bytes);
+    int rc = dst ? (d.data = dst, LG_OK) : dalloc(ctx, (void**)&d.data, bytes);
     if (rc) return rc;
     LG_HIP_CHECK(hipMemcpy(d.data, w.data, bytes, hipMemcpyHostToDevice));
     d.type = w.type; d.rsz = w.rsz; d.rows = w.rows; d.cols = w.cols;
@@ -262,12 +274,13 @@ static int upload_weight(lg_ctx* ctx, const lg_weight& w, dweight& d)
 }
 
 /* stack matrices of one type and row size into one device matrix */
-static int upload_stacked(lg_ctx* ctx, const lg_weight* const* ws, int n, dweight& out, dweight* views)
+static int upload_stacked(lg_ctx* ctx, const lg_weight* const* ws, int n, dweight& out, dweight* views,
+                          uint8_t* dst = nullptr)
 {
     size_t bytes = 0;
     int rows = 0;
     for (int i = 0; i < n; i++) { bytes += (size_t)ws[i]->rows * ws[i]->rsz; rows += ws[i]->rows; }
-    int rc = dalloc(ctx, (void**)&out.data, bytes);
+    int rc = dst ? (out.data = dst, LG_OK) : dalloc(ctx, (void**)&out.data, bytes);
     if (rc) return rc;
     size_t off = 0;
     for (int i = 0; i < n; i++) {
@@ -281,10 +294,10 @@ static int upload_stacked(lg_ctx* ctx, const lg_weight* const* ws, int n, dweigh
     return LG_OK;
 }
 
-static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const char* name)
+static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const char* name, float* dst = nullptr)
 {
     if (!h) { lg_set_error("load_model: %s missing", name); return LG_ERR_ARG; }
-    int rc = dalloc(ctx, (void**)d, n * sizeof(float));
+    int rc = dst ? (*d = dst, LG_OK) : dalloc(ctx, (void**)d, n * sizeof(float));
     if (rc) return rc;
     LG_HIP_CHECK(hipMemcpy(*d, h, n * sizeof(float), hipMemcpyHostToDevice));
     return LG_OK;
@@ -314,7 +327,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         pk_attn_split(m->n_context, m->head_dim, nrep, &att_chunk, &att_nch);
     att_nch = std::max(att_nch, PK_ATT_MERGE);
     bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
-              m->n_kv_heads <= 32 && ctx->output.cols == m->n_embed;
+              m->n_kv_heads <= 32 && ctx->output.cols == m->n_embed && ctx->arena.ok;
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
         ok = D.qkv_fused && D.ug_fused && pk_shape_ok(D.qkv, lt, m->n_embed + 2 * m->kv_dim, m->n_embed) &&
@@ -342,6 +355,9 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     PkParams& P = ctx->pk;
     P = PkParams{};
     P.layers = dl;
+    P.w_qkv = ctx->arena.qkv; P.w_ao = ctx->arena.ao; P.w_ug = ctx->arena.ug; P.w_down = ctx->arena.down;
+    P.s_qkv = ctx->arena.qkv_b; P.s_ao = ctx->arena.ao_b; P.s_ug = ctx->arena.ug_b; P.s_down = ctx->arena.down_b;
+    P.n_att = ctx->arena.att_norm; P.n_ffn = ctx->arena.ffn_norm; P.n_q = ctx->arena.q_norm; P.n_k = ctx->arena.k_norm;
     P.n_layers = m->n_layers; P.n_embed = m->n_embed; P.n_heads = m->n_heads; P.n_kv = m->n_kv_heads;
     P.head_dim = m->head_dim; P.kv_dim = m->kv_dim; P.n_ff = m->n_ff; P.vocab = m->vocab_size;
     P.n_ctx = m->n_context; P.rope_dim = m->rope_dim; P.eps = m->rms_epsilon;
@@ -360,6 +376,24 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.xm = P.xs + (L + 1) * ne;
         P.qkv = P.xm + L * ne;
         P.hb = P.qkv + L * qs;
+    }
+    {
+        /* the persistent kernel's tagged activations (zero: no tag yet) */
+        const size_t L = (size_t)m->n_layers, ne = m->n_embed, qs = ne + 2 * m->kv_dim, ff = m->n_ff;
+        const size_t slots = (size_t)att_nch + 1;
+        const size_t words = (L + 1) * ne + L * ne + L * qs + L * ff + L * ne + L * slots * ne + L * slots * m->n_heads * 2;
+        uint64_t* t = nullptr;
+        if ((rc = dalloc(ctx, (void**)&t, words * sizeof(uint64_t)))) return rc;
+        LG_HIP_CHECK(hipMemset(t, 0, words * sizeof(uint64_t)));
+        ctx->pk_tagged = t;
+        ctx->pk_tagged_n = words;
+        P.t_xs = t;
+        P.t_xm = P.t_xs + (L + 1) * ne;
+        P.t_qkv = P.t_xm + L * ne;
+        P.t_hb = P.t_qkv + L * qs;
+        P.t_att = P.t_hb + L * ff;
+        P.t_po = P.t_att + L * ne;
+        P.t_pml = P.t_po + L * slots * ne;
     }
     {
         /* per-layer attention partials, each written once per step */
@@ -486,7 +520,12 @@ static int enqueue_pk(lg_ctx* c, int tok, int pos)
 {
     PkParams& P = c->pk;
     PkStep S = {};
-    S.tok = tok; S.pos = pos; S.base = c->pk_base;
+    if (++c->pk_tag == 0) {
+        /* the tag wrapped: no word may still carry a tag of this new cycle */
+        LG_HIP_CHECK(hipMemsetAsync(c->pk_tagged, 0, c->pk_tagged_n * sizeof(uint64_t), c->stream));
+        c->pk_tag = 1;
+    }
+    S.tok = tok; S.pos = pos; S.base = c->pk_base; S.tag = c->pk_tag;
     S.trace = c->pk_trace;
     c->pk_trace = nullptr;   /* one step only */
     int rc = lg_persist_launch(c->pk_kernel, c->pk, &S, c->pk_nwg, c->stream);
@@ -715,21 +754,66 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
         if (nfreq) std::copy(m->rope_freq, m->rope_freq + nfreq, tab.begin());
         if ((rc = upload_floats(ctx, tab.data(), nalloc, &ctx->rope_freq, "rope_freq"))) return rc;
     }
+    {
+        /* one shape and type per matrix kind over all layers, Q|K|V and
+         * up|gate stackable: one allocation per kind */
+        const lg_layer_desc& L0 = m->layers[0];
+        auto same = [](const lg_weight& a, const lg_weight& b) {
+            return a.type == b.type && a.rsz == b.rsz && a.rows == b.rows && a.cols == b.cols;
+        };
+        bool uni = L0.att_q.type == L0.att_k.type && L0.att_q.type == L0.att_v.type && L0.att_q.rsz == L0.att_k.rsz &&
+                   L0.att_q.rsz == L0.att_v.rsz && L0.ffn_up.type == L0.ffn_gate.type && L0.ffn_up.rsz == L0.ffn_gate.rsz;
+        for (int l = 1; uni && l < m->n_layers; l++) {
+            const lg_layer_desc& L = m->layers[l];
+            uni = same(L.att_q, L0.att_q) && same(L.att_k, L0.att_k) && same(L.att_v, L0.att_v) &&
+                  same(L.att_out, L0.att_out) && same(L.ffn_up, L0.ffn_up) && same(L.ffn_gate, L0.ffn_gate) &&
+                  same(L.ffn_down, L0.ffn_down);
+        }
+        auto& A = ctx->arena;
+        A = {};
+        if (uni) {
+            const size_t nl = m->n_layers;
+            A.qkv_b = (size_t)(L0.att_q.rows + L0.att_k.rows + L0.att_v.rows) * L0.att_q.rsz;
+            A.ao_b = (size_t)L0.att_out.rows * L0.att_out.rsz;
+            A.ug_b = (size_t)(L0.ffn_up.rows + L0.ffn_gate.rows) * L0.ffn_up.rsz;
+            A.down_b = (size_t)L0.ffn_down.rows * L0.ffn_down.rsz;
+            if ((rc = dalloc(ctx, (void**)&A.qkv, nl * A.qkv_b))) return rc;
+            if ((rc = dalloc(ctx, (void**)&A.ao, nl * A.ao_b))) return rc;
+            if ((rc = dalloc(ctx, (void**)&A.ug, nl * A.ug_b))) return rc;
+            if ((rc = dalloc(ctx, (void**)&A.down, nl * A.down_b))) return rc;
+            if ((rc = dalloc(ctx, (void**)&A.att_norm, nl * m->n_embed * 4))) return rc;
+            if ((rc = dalloc(ctx, (void**)&A.ffn_norm, nl * m->n_embed * 4))) return rc;
+            if (m->arch == LG_ARCH_QWEN3) {
+                if ((rc = dalloc(ctx, (void**)&A.q_norm, nl * m->head_dim * 4))) return rc;
+                if ((rc = dalloc(ctx, (void**)&A.k_norm, nl * m->head_dim * 4))) return rc;
+            }
+            A.ok = true;
+        }
+    }
+    const auto& AR = ctx->arena;
+    auto slot = [&](uint8_t* base, size_t stride, int l) { return base ? base + (size_t)l * stride : nullptr; };
+    auto fslot = [&](float* base, size_t stride, int l) { return base ? base + (size_t)l * stride : nullptr; };
     ctx->layers.resize(m->n_layers);
     for (int l = 0; l < m->n_layers; l++) {
         const lg_layer_desc& L = m->layers[l];
         dlayer& D = ctx->layers[l];
-        if ((rc = upload_floats(ctx, L.att_norm, m->n_embed, &D.att_norm, "attn_norm"))) return rc;
-        if ((rc = upload_floats(ctx, L.ffn_norm, m->n_embed, &D.ffn_norm, "ffn_norm"))) return rc;
+        if ((rc = upload_floats(ctx, L.att_norm, m->n_embed, &D.att_norm, "attn_norm", fslot(AR.att_norm, m->n_embed, l))))
+            return rc;
+        if ((rc = upload_floats(ctx, L.ffn_norm, m->n_embed, &D.ffn_norm, "ffn_norm", fslot(AR.ffn_norm, m->n_embed, l))))
+            return rc;
         if (m->arch == LG_ARCH_QWEN3) {
-            if ((rc = upload_floats(ctx, L.att_q_norm, m->head_dim, &D.q_norm, "attn_q_norm"))) return rc;
-            if ((rc = upload_floats(ctx, L.att_k_norm, m->head_dim, &D.k_norm, "attn_k_norm"))) return rc;
+            if ((rc = upload_floats(ctx, L.att_q_norm, m->head_dim, &D.q_norm, "attn_q_norm",
+                                    fslot(AR.q_norm, m->head_dim, l))))
+                return rc;
+            if ((rc = upload_floats(ctx, L.att_k_norm, m->head_dim, &D.k_norm, "attn_k_norm",
+                                    fslot(AR.k_norm, m->head_dim, l))))
+                return rc;
         }
         if (L.att_q.type == L.att_k.type && L.att_q.type == L.att_v.type && L.att_q.rsz == L.att_k.rsz &&
             L.att_q.rsz == L.att_v.rsz) {
             const lg_weight* ws[3] = {&L.att_q, &L.att_k, &L.att_v};
             dweight views[3];
-            if ((rc = upload_stacked(ctx, ws, 3, D.qkv, views))) return rc;
+            if ((rc = upload_stacked(ctx, ws, 3, D.qkv, views, slot(AR.qkv, AR.qkv_b, l)))) return rc;
             D.q = views[0]; D.k = views[1]; D.v = views[2];
             D.qkv_fused = true;
         } else {
@@ -737,18 +821,18 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
             if ((rc = upload_weight(ctx, L.att_k, D.k))) return rc;
             if ((rc = upload_weight(ctx, L.att_v, D.v))) return rc;
         }
-        if ((rc = upload_weight(ctx, L.att_out, D.att_out))) return rc;
+        if ((rc = upload_weight(ctx, L.att_out, D.att_out, slot(AR.ao, AR.ao_b, l)))) return rc;
         if (L.ffn_up.type == L.ffn_gate.type && L.ffn_up.rsz == L.ffn_gate.rsz) {
             const lg_weight* ws[2] = {&L.ffn_up, &L.ffn_gate};
             dweight views[2];
-            if ((rc = upload_stacked(ctx, ws, 2, D.ug, views))) return rc;
+            if ((rc = upload_stacked(ctx, ws, 2, D.ug, views, slot(AR.ug, AR.ug_b, l)))) return rc;
             D.up = views[0]; D.gate = views[1];
             D.ug_fused = true;
         } else {
             if ((rc = upload_weight(ctx, L.ffn_up, D.up))) return rc;
             if ((rc = upload_weight(ctx, L.ffn_gate, D.gate))) return rc;
         }
-        if ((rc = upload_weight(ctx, L.ffn_down, D.down))) return rc;
+        if ((rc = upload_weight(ctx, L.ffn_down, D.down, slot(AR.down, AR.down_b, l)))) return rc;
     }
 
     const size_t kvn = (size_t)m->n_layers * m->n_context * m->kv_dim;

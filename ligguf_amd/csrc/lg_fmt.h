@@ -141,7 +141,7 @@ struct Fmt<LG_Q4_K> {
         const float d = lg_h2f((uint16_t)(w.h.x & 0xffffu)), dmin = lg_h2f((uint16_t)(w.h.x >> 16));
         const int S = sc0 * dl + sc1 * dh;
         const int M = m0 * (A.bs[0] + A.bs[1]) + m1 * (A.bs[2] + A.bs[3]);
-        return A.d * (d * (float)S - dmin * (float)M);
+        return A.d * lg_fma2(d, (float)S, -dmin, (float)M);
     }
 };
 
@@ -191,7 +191,7 @@ struct Fmt<LG_Q5_K> {
         const float d = lg_h2f((uint16_t)(w.h.x & 0xffffu)), dmin = lg_h2f((uint16_t)(w.h.x >> 16));
         const int S = sc0 * dl + sc1 * dh;
         const int M = m0 * (A.bs[0] + A.bs[1]) + m1 * (A.bs[2] + A.bs[3]);
-        return A.d * (d * (float)S - dmin * (float)M);
+        return A.d * lg_fma2(d, (float)S, -dmin, (float)M);
     }
 };
 
@@ -272,7 +272,7 @@ struct Fmt<LG_Q2_K> {
             M += (sb >> 4) * A.bs[j];
         }
         const float d = lg_h2f((uint16_t)(w.dd & 0xffffu)), dmin = lg_h2f((uint16_t)(w.dd >> 16));
-        return A.d * (d * (float)S - dmin * (float)M);
+        return A.d * lg_fma2(d, (float)S, -dmin, (float)M);
     }
 };
 
@@ -406,7 +406,7 @@ struct Fmt<LG_Q1_G> {
             s0 = lg_dot4(bits4_to_bytes((w.bits.x >> (4 * i)) & 15u), A.b[0].a[i], s0);
             s1 = lg_dot4(bits4_to_bytes((w.bits.y >> (4 * i)) & 15u), A.b[1].a[i], s1);
         }
-        const float sumi = A.b[0].d * (float)(2 * s0 - A.b[0].asum) + A.b[1].d * (float)(2 * s1 - A.b[1].asum);
+        const float sumi = lg_fma2(A.b[0].d, (float)(2 * s0 - A.b[0].asum), A.b[1].d, (float)(2 * s1 - A.b[1].asum));
         return lg_h2f((uint16_t)w.d) * sumi;
     }
 };
@@ -456,7 +456,9 @@ struct Fmt<LG_F32> {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            acc += w.v[i].x * A.a[4 * i] + w.v[i].y * A.a[4 * i + 1] + w.v[i].z * A.a[4 * i + 2] + w.v[i].w * A.a[4 * i + 3];
+            acc += __builtin_fmaf(w.v[i].w, A.a[4 * i + 3],
+                                  __builtin_fmaf(w.v[i].z, A.a[4 * i + 2],
+                                                 lg_fma2(w.v[i].x, A.a[4 * i], w.v[i].y, A.a[4 * i + 1])));
         return acc;
     }
 };

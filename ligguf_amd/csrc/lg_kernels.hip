@@ -47,7 +47,10 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
 /* RMSNorm fused with the quantizer (fast/lil_math.cpp:922-929 then the */
 /* quantize_q8_K/q8_0 of fast/ligguf_fast_qk.cpp:39,116,140).  Each     */
 /* wave recomputes sum(x^2) over the whole vector (16 KB at dim 4096,   */
-/* L2-resident) so that no second launch or grid sync is needed.        */
+/* L2-resident) so that no second launch or grid sync is needed, in the */
+/* order of the whole-step kernels' build: the 256-value chunks in 8    */
+/* interleaved groups (chunk % 8), lane partials in chunk order, one    */
+/* lg_wave_sum per group, the group sums added in group order.          */
 /* ------------------------------------------------------------------ */
 __global__ __launch_bounds__(64) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                       float eps, int qtype, uint8_t* __restrict__ out_q,
@@ -55,12 +58,7 @@ __global__ __launch_bounds__(64) void k_rmsnorm_quant(const float* __restrict__ 
 {
     const int lane = threadIdx.x;
     const int chunk = blockIdx.x;
-    float ss = 0.0f;
-    for (int i = 4 * lane; i < n; i += 256) {
-        const float4 t = *(const float4*)(x + i);
-        ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-    }
-    ss = lg_group_sum<64>(ss);
+    const float ss = lg_sumsq_chunked(x, n, lane);
     const float scale = 1.0f / sqrtf(ss / (float)n + eps);
     const int base = chunk * 256 + 4 * lane;
     float v[4] = {0.f, 0.f, 0.f, 0.f};

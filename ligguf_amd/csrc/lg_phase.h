@@ -15,6 +15,15 @@
 
 #define PK_WAVES (PK_THREADS / 64)
 
+/* thread index in the workgroup as the phases read it.  A kernel that walks
+ * all layers with every phase inlined defines LG_TID before including this
+ * header as an index the compiler cannot see through: otherwise it hoists the
+ * per-lane address arithmetic of every phase out of the layer loop and keeps
+ * it live (spilled) across the whole loop. */
+#ifndef LG_TID
+#define LG_TID ((int)threadIdx.x)
+#endif
+
 /* ------------------------------------------------------------------ */
 /* LDS                                                                  */
 /* ------------------------------------------------------------------ */
@@ -29,6 +38,7 @@ __shared__ __attribute__((aligned(16))) float s_kv[2 * 128];
 __shared__ __attribute__((aligned(16))) float s_sc[3 * PK_ATT_MAX_NCH * PK_MAX_NREP];
 __shared__ __attribute__((aligned(16))) float s_o[PK_WAVES * PK_MAX_NREP * 128];
 __shared__ float s_m[PK_WAVES * PK_MAX_NREP];
+__shared__ float s_own[2 * PK_MAX_NREP];
 
 /* ------------------------------------------------------------------ */
 /* coherent memory helpers                                              */
@@ -51,6 +61,74 @@ __device__ __forceinline__ float2 cld2(const float* p)
     const uint64_t u = cld((const uint64_t*)p);
     return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
 }
+
+/* tagged values: {fp32 bits, tag} in one 64-bit word, written with a
+ * single-copy-atomic coherent store.  A tagged buffer is written once per
+ * launch, with the launch's tag.  Its writers publish their progress word
+ * without waiting for the acknowledgement of their data stores, so a reader
+ * past the progress wait may still find a word that is not there yet: it
+ * reads with plain (L2-cached) 16-byte loads -- two words, each written
+ * whole -- and loads every word without the tag again, coherently, until it
+ * carries it.  (A word read too early can leave a stale line in an L2; the
+ * coherent reloads do not use it, and the launch's end discards it.) */
+__device__ __forceinline__ float tg_val(uint64_t u)
+{
+    return __uint_as_float((uint32_t)u);
+}
+
+__device__ __forceinline__ bool tg_is(uint64_t u, uint32_t tag)
+{
+    return (uint32_t)(u >> 32) == tag;
+}
+
+__device__ __forceinline__ void tg_st(uint64_t* p, float v, uint32_t tag)
+{
+    cst(p, ((uint64_t)tag << 32) | __float_as_uint(v));
+}
+
+/* u[i] = the word at p + off(i), i < N, for words already loaded into u:
+ * loads again the ones without `tag` until all carry it.  Bounded: past
+ * spin_cap rounds, or once another wait has expired (the error flag), it
+ * sets the error flag and returns what it has. */
+template <int N, typename Off>
+__device__ __forceinline__ void tg_settle(uint64_t (&u)[N], const uint64_t* p, Off off, uint32_t tag,
+                                          const PkParams& P)
+{
+    uint32_t e = 0;
+    for (int it = 0;; it++) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok = ok && tg_is(u[i], tag);
+        if (ok) break;
+        if (e || it >= P.spin_cap) {
+            cst(P.err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if (!tg_is(u[i], tag)) u[i] = cld(p + off(i));
+        e = cld(P.err);
+    }
+}
+
+template <int N, typename Off>
+__device__ __forceinline__ void tg_poll(uint64_t (&u)[N], const uint64_t* p, Off off, uint32_t tag, const PkParams& P)
+{
+#pragma unroll
+    for (int i = 0; i < N; i++) u[i] = cld(p + off(i));
+    tg_settle(u, p, off, tag, P);
+}
+
+/* element type of an activation buffer: fp32, or tagged words */
+template <bool TG>
+struct ActT {
+    using type = float;
+};
+template <>
+struct ActT<true> {
+    using type = uint64_t;
+};
 
 /* keeps the loads before it ahead of the loads after it in issue order (a
  * wave's loads return in issue order, so what is needed first is issued
@@ -76,20 +154,27 @@ __device__ __forceinline__ void pk_signal(const PkParams& P, uint64_t val)
 {
     wait_stores();
     bar();
-    if (threadIdx.x == 0) cst(&P.progress[blockIdx.x], val);
+    if (LG_TID == 0) cst(&P.progress[blockIdx.x], val);
+}
+
+/* publish without waiting for the data stores (their values are tagged) */
+__device__ __forceinline__ void pk_publish(const PkParams& P, uint64_t val)
+{
+    bar();
+    if (LG_TID == 0) cst(&P.progress[blockIdx.x], val);
 }
 
 /* wait until every WG's progress word reaches `target` (wave 0 polls) */
 __device__ __forceinline__ void pk_wait(const PkParams& P, uint64_t target)
 {
-    if (threadIdx.x < 64) {
+    if (LG_TID < 64) {
         if (!cld(P.err)) {
             const int nwg = gridDim.x;
             bool ok = false;
             int it = 0;
             do {
                 uint64_t mn = ~0ull;
-                for (int i = threadIdx.x; i < nwg; i += 64) {
+                for (int i = LG_TID; i < nwg; i += 64) {
                     const uint64_t v = cld(&P.progress[i]);
                     mn = v < mn ? v : mn;
                 }
@@ -100,7 +185,7 @@ __device__ __forceinline__ void pk_wait(const PkParams& P, uint64_t target)
                 }
                 ok = mn >= target;
             } while (!ok && ++it < P.spin_cap);
-            if (!ok && threadIdx.x == 0) cst(P.err, 1u);
+            if (!ok && LG_TID == 0) cst(P.err, 1u);
         }
     }
     bar();
@@ -117,7 +202,7 @@ __device__ __forceinline__ float lg_exp2(float x)
  * count against lgkmcnt and make the next LDS wait wait for it. */
 __device__ __forceinline__ void stamp(uint64_t* tr, int k)
 {
-    if (tr && threadIdx.x == 0) *(__attribute__((address_space(1))) uint64_t*)(tr + k) = wall_clock64();
+    if (tr && LG_TID == 0) *(__attribute__((address_space(1))) uint64_t*)(tr + k) = wall_clock64();
 }
 
 /* ------------------------------------------------------------------ */
@@ -137,7 +222,7 @@ enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3 };
 
 __device__ __forceinline__ int chunk_base(int c)
 {
-    return ((threadIdx.x >> 6) + PK_WAVES * c) * 256 + 4 * (threadIdx.x & 63);
+    return ((LG_TID >> 6) + PK_WAVES * c) * 256 + 4 * (LG_TID & 63);
 }
 
 /* rmsnorm weights of this wave's chunks: constants, loaded before the wait */
@@ -161,6 +246,30 @@ struct ActSrc {
     {
 #pragma unroll
         for (int c = 0; c < CPW; c++) v[c] = *(const float4*)(src + chunk_base(c));
+    }
+};
+
+/* the same chunks of a tagged vector: issue() the plain loads, settle()
+ * into an ActSrc once every word carries the tag */
+template <int CPW>
+struct TgSrc {
+    uint64_t u[CPW * 4];
+    __device__ __forceinline__ void issue(const uint64_t* __restrict__ src)
+    {
+#pragma unroll
+        for (int c = 0; c < CPW; c++) {
+            const ulonglong2* p = (const ulonglong2*)(src + chunk_base(c));
+            const ulonglong2 a = p[0], b = p[1];
+            u[4 * c] = a.x; u[4 * c + 1] = a.y; u[4 * c + 2] = b.x; u[4 * c + 3] = b.y;
+        }
+    }
+    __device__ __forceinline__ void settle(const uint64_t* __restrict__ src, uint32_t tag, const PkParams& P,
+                                           ActSrc<CPW>& a)
+    {
+        tg_settle(u, src, [](int i) { return chunk_base(i >> 2) + (i & 3); }, tag, P);
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+            a.v[c] = make_float4(tg_val(u[4 * c]), tg_val(u[4 * c + 1]), tg_val(u[4 * c + 2]), tg_val(u[4 * c + 3]));
     }
 };
 
@@ -228,52 +337,54 @@ __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int p
 }
 
 /* rmsnorm(x) * w quantized into s_act (fast/lil_math.cpp:922-929 and
- * quantize_q8_K / quantize_q8_0, :329-394).  The sum of squares is taken by
- * one wave in the per-lane order of k_rmsnorm_quant, so both paths agree bit
- * for bit.  x is the source vector (BLD_RMS) or, for layer 0 (BLD_EMB), the
- * embedding row of tok, dequantized here; WG 0 also stores that row as the
- * residual stream `emb_out`. */
-template <int QT, int CPW>
+ * quantize_q8_K / quantize_q8_0, :329-394).  The sum of squares is taken in
+ * the order of k_rmsnorm_quant: per wave over its chunks (lane partials in
+ * chunk order, then lg_wave_sum), the wave sums added in wave order -- so
+ * both paths agree bit for bit.  x is the source vector (BLD_RMS) or, for
+ * layer 0 (BLD_EMB), the embedding row of tok, dequantized here; WG 0 also
+ * stores that row as the residual stream `emb_out`. */
+template <int QT, int CPW, bool TG = false>
 __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const NormW<CPW>& nw, const ActSrc<CPW>& xsrc,
-                                          bool from_embed, float* __restrict__ emb_out)
+                                          bool from_embed, typename ActT<TG>::type* __restrict__ emb_out,
+                                          uint32_t tag = 0)
 {
     constexpr int n = CPW * 256 * PK_WAVES;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = LG_TID & 63, wave = LG_TID >> 6;
     float4 xv[CPW];
     if (from_embed) {
         /* one dequantization loop (the switch over types stays out of the
          * unrolled chunk code), staged through s_x */
         const uint8_t* row = P.embd + (size_t)tok * P.embd_rsz;
-        for (int i = threadIdx.x; i < n; i += PK_THREADS) s_x[i] = lg_dq_value(P.embd_t, row, i);
+        for (int i = LG_TID; i < n; i += PK_THREADS) s_x[i] = lg_dq_value(P.embd_t, row, i);
         bar();
 #pragma unroll
         for (int c = 0; c < CPW; c++) {
             const int b = chunk_base(c);
             xv[c] = *(const float4*)(s_x + b);
             if (blockIdx.x == 0) {
-                cst(&emb_out[b], xv[c].x); cst(&emb_out[b + 1], xv[c].y);
-                cst(&emb_out[b + 2], xv[c].z); cst(&emb_out[b + 3], xv[c].w);
+                if constexpr (TG) {
+                    tg_st(&emb_out[b], xv[c].x, tag); tg_st(&emb_out[b + 1], xv[c].y, tag);
+                    tg_st(&emb_out[b + 2], xv[c].z, tag); tg_st(&emb_out[b + 3], xv[c].w, tag);
+                } else {
+                    cst(&emb_out[b], xv[c].x); cst(&emb_out[b + 1], xv[c].y);
+                    cst(&emb_out[b + 2], xv[c].z); cst(&emb_out[b + 3], xv[c].w);
+                }
             }
         }
     } else {
 #pragma unroll
-        for (int c = 0; c < CPW; c++) {
-            xv[c] = xsrc.v[c];
-            *(float4*)(s_x + chunk_base(c)) = xv[c];
-        }
+        for (int c = 0; c < CPW; c++) xv[c] = xsrc.v[c];
     }
+    float p = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPW; c++) p += lg_sq4(xv[c]);
+    p = lg_wave_sum(p);
+    if (lane == 0) s_red[wave] = p;
     bar();
-    if (wave == 0) {
-        float ss = 0.0f;
-        for (int i = 4 * lane; i < n; i += 256) {
-            const float4 t = *(const float4*)(s_x + i);
-            ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-        }
-        ss = lg_group_sum<64>(ss);
-        if (lane == 0) s_red[0] = 1.0f / sqrtf(ss / (float)n + P.eps);
-    }
-    bar();
-    const float scale = s_red[0];
+    float ss = 0.0f;
+#pragma unroll
+    for (int w = 0; w < PK_WAVES; w++) ss += s_red[w];
+    const float scale = 1.0f / sqrtf(ss / (float)n + P.eps);
 #pragma unroll
     for (int c = 0; c < CPW; c++) {
         const float4 t = xv[c], g = nw.g[c];
@@ -287,7 +398,7 @@ __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const Norm
 template <int QT, int CPW>
 __device__ __forceinline__ void build_plain(const ActSrc<CPW>& a)
 {
-    const int wave = threadIdx.x >> 6;
+    const int wave = LG_TID >> 6;
 #pragma unroll
     for (int c = 0; c < CPW; c++) {
         const float v[4] = {a.v[c].x, a.v[c].y, a.v[c].z, a.v[c].w};
@@ -338,18 +449,28 @@ struct Rows {
  * words; its own loads go after the wait, since a wave's loads return in
  * order and would hold the poll back.  Then: build the activation, compute,
  * store, publish.  CPW = 256-value activation chunks per wave; DB =
- * double-buffer the items (long phases: the output head). */
-template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, bool DB>
+ * double-buffer the items (long phases: the output head).
+ *
+ * TG (tagged activations): src, res_src, out (except logits) and emb_out are
+ * tagged buffers of launch tag `tag`, and the phase publishes without
+ * waiting for its stores.  The source chunks are settled after the wait;
+ * the residual rows were settled by this workgroup's own earlier build of
+ * the same vector, and are read coherently (RESPOLL: not so -- they are
+ * polled at phase entry). */
+template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, bool DB, bool TG = false, bool RESPOLL = false>
 __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8_t* __restrict__ W, uint32_t rsz,
                                          int items, int kstride, const float* __restrict__ normw,
-                                         const float* __restrict__ src, const float* __restrict__ res_src,
-                                         float* __restrict__ out, float* __restrict__ emb_out,
+                                         const typename ActT<TG>::type* __restrict__ src,
+                                         const typename ActT<TG>::type* __restrict__ res_src,
+                                         typename ActT<TG && EPI != EPI_LOGITS>::type* __restrict__ out,
+                                         typename ActT<TG>::type* __restrict__ emb_out,
                                          uint64_t wait_target, uint64_t sig, uint64_t* tr,
-                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0})
+                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0}, uint32_t tag = 0)
 {
+    static_assert(!TG || BLD != BLD_MERGE, "tagged phases read the merged attention vector");
     using F = Fmt<FMT>;
     constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q1_0 || FMT == LG_Q1_G) ? LG_Q8_0 : LG_Q8_K;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int nwv = gridDim.x * PK_WAVES;
     const int gw = blockIdx.x * PK_WAVES + wave;
     const int ipw = (items + nwv - 1) / nwv;
@@ -365,21 +486,43 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     float res[MAXB];
     constexpr bool from_embed = BLD == BLD_EMB;
     constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
+    TgSrc<CPW> ts;
     auto load_src = [&]() {
-        if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
-        else if (!from_embed) as.load(src);
+        if constexpr (TG) {
+            if (!from_embed) ts.issue(src);
+        } else {
+            if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
+            else if (!from_embed) as.load(src);
+        }
     };
     auto load_res = [&](float* r, int b0) {
         if (EPI == EPI_RESID) {
 #pragma unroll
-            for (int b = 0; b < MAXB; b++) r[b] = res_src[min(i0 + b0 + b, wlast)];
+            for (int b = 0; b < MAXB; b++) {
+                const int i = min(i0 + b0 + b, wlast);
+                if constexpr (TG) r[b] = tg_val(cld(res_src + i));
+                else r[b] = res_src[i];
+            }
         }
     };
     auto prefetch = [&]() {
         R0.load(W, rsz, i0, wlast, kstride, lane);
         load_res(res, 0);
     };
-    if (!wait_target) {
+    if constexpr (TG) {
+        if constexpr (RESPOLL && EPI == EPI_RESID) {
+            for (int j = lane; j < my; j += 64) {
+                uint64_t u[1];
+                tg_poll(u, res_src + i0 + j, [](int) { return 0; }, tag, P);
+            }
+        }
+        if (rms) nw.load(normw);
+        if (wave != 0) prefetch();
+        if (wait_target) pk_wait(P, wait_target);
+        load_src();
+        if (wave == 0) prefetch();
+        if (!from_embed) ts.settle(src, tag, P, as);
+    } else if (!wait_target) {
         /* no dependency wait (fused kernels): the activation and the norm
          * weights go first, the rows after them */
         load_src();
@@ -394,7 +537,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         if (wave == 0) prefetch();
     }
     stamp(tr, 1);
-    if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out);
+    if (rms) build_rms<QT, CPW, TG>(P, tok, nw, as, from_embed, emb_out, tag);
     else {
         if (BLD == BLD_MERGE) mg.merge(ms.nch, as);
         build_plain<QT, CPW>(as);
@@ -424,12 +567,15 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                     if (acc[0] > best) { best = acc[0]; besti = i; }
                 }
                 if (lane == 0) {
-                    if (EPI == EPI_STORE) cst(&out[i], acc[0]);
-                    else if (EPI == EPI_RESID) cst(&out[i], rs[b] + acc[0]);
+                    float v = acc[0];
+                    if (EPI == EPI_RESID) v = rs[b] + acc[0];
                     else if (EPI == EPI_SWIGLU) {
                         const float u = acc[0], g = acc[1];
-                        cst(&out[i], (g / (1.0f + expf(-g))) * u);
-                    } else out[i] = acc[0];
+                        v = (g / (1.0f + expf(-g))) * u;
+                    }
+                    if constexpr (EPI == EPI_LOGITS) out[i] = v;
+                    else if constexpr (TG) tg_st(&out[i], v, tag);
+                    else cst(&out[i], v);
                 }
             }
         }
@@ -461,7 +607,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
          * wave, waves and WGs own increasing row ranges */
         if (lane == 0) { s_red[wave] = best; s_int[wave] = besti; }
         bar();
-        if (threadIdx.x == 0) {
+        if (LG_TID == 0) {
             float bv = s_red[0];
             int bi = s_int[0];
             for (int w = 1; w < PK_WAVES; w++)
@@ -470,19 +616,23 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
             cst(&P.amax_i[blockIdx.x], bi);
         }
     }
-    if (sig) pk_signal(P, sig);
-    else if (EPI == EPI_LOGITS) {
+    if constexpr (EPI == EPI_LOGITS) {
+        /* the argmax partials are read by the last workgroup: stores acknowledged first */
         wait_stores();
         bar();
+        if (sig && LG_TID == 0) cst(&P.progress[blockIdx.x], sig);
+    } else if (sig) {
+        if constexpr (TG) pk_publish(P, sig);
+        else pk_signal(P, sig);
     }
     stamp(tr, 3);
     if (EPI == EPI_LOGITS) {
-        if (threadIdx.x == 0) {
+        if (LG_TID == 0) {
             const uint32_t old = __hip_atomic_fetch_add(P.amax_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_int[0] = old == gridDim.x - 1;
         }
         bar();
-        if (s_int[0] && threadIdx.x == 0) {
+        if (s_int[0] && LG_TID == 0) {
             float bv = -INFINITY;
             int bi = 0x7fffffff;
             for (int w = 0; w < (int)gridDim.x; w++) {
@@ -507,12 +657,12 @@ template <int HD>
 __device__ __forceinline__ void norm_rope_head(float e[4], bool has_norm, float4 g, float eps, int rope_dim, int pos,
                                                float2 fr)
 {
-    const int lane = threadIdx.x & 63;
+    const int lane = LG_TID & 63;
     const bool act = 4 * lane < HD;
     {
         /* computed whether or not the model has QK norms, and selected: the
          * weights' load is used unconditionally and stays where it is issued */
-        float ss = act ? e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3] : 0.0f;
+        float ss = act ? lg_sq4(make_float4(e[0], e[1], e[2], e[3])) : 0.0f;
         ss = lg_group_sum<64>(ss);
         const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
         const bool nrm = has_norm && act;
@@ -532,8 +682,8 @@ __device__ __forceinline__ void norm_rope_head(float e[4], bool has_norm, float4
                 float s, c;
                 sincosf(ang, &s, &c);
                 const float x0 = e[j], x1 = e[j + 1];
-                e[j] = x0 * c - x1 * s;
-                e[j + 1] = x0 * s + x1 * c;
+                e[j] = lg_fma2(x0, c, -x1, s);
+                e[j + 1] = lg_fma2(x0, s, x1, c);
             }
         }
     }
@@ -557,8 +707,8 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
     const float mn = fmaxf(m, m2);
     const float a = m == -INFINITY ? 0.0f : lg_exp2(m - mn);
     const float b = m2 == -INFINITY ? 0.0f : lg_exp2(m2 - mn);
-    l = l * a + l2 * b;
-    for (int i = 0; i < n; i++) o[i] = o[i] * a + o2[i] * b;
+    l = lg_fma2(l, a, l2, b);
+    for (int i = 0; i < n; i++) o[i] = lg_fma2(o[i], a, o2[i], b);
     m = mn;
 }
 
@@ -575,10 +725,16 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * head the last unit of the head (atomic counter) merges them into the
  * layer's merged slot.  The unit of the head's last chunk also writes the fp16 cache
  * row pos. */
-template <int HD, int NREP>
+/* TG (tagged activations): a unit issues its K/V loads before the wait,
+ * then settles the heads from the tagged qkv of the layer; the partials are
+ * tagged, and the unit of the head group's last chunk merges them
+ * (MergeAct's formula and order, polling the other chunks' words) into the
+ * tagged attention vector t_att.  Workgroups without a unit publish at
+ * once. */
+template <int HD, int NREP, bool TG = false>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
-                                           uint64_t* tr)
+                                           uint64_t* tr, uint32_t tag = 0)
 {
     constexpr int LPP = HD / 8;            /* lanes per position */
     constexpr int PPW = 64 / LPP;          /* positions per wave step */
@@ -586,7 +742,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     constexpr int MAXST = pk_att_steps(NREP);
     constexpr int NH = (NREP + PK_WAVES) / PK_WAVES;   /* heads normed per wave: NREP q + 1 k */
     static_assert(PPB == PK_THREADS * 8 / HD, "step geometry of pk_attn_split");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int gl = lane & (LPP - 1), grp = lane / LPP;
     const int kvd = P.kv_dim;
     int chunk, nch;
@@ -600,6 +756,8 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
      * holds a stale copy of it */
     float* po_m = po + (size_t)(P.att_slots - 1) * P.n_embed;
     float* pml_m = pml + (size_t)(P.att_slots - 1) * P.n_heads * 2;
+    uint64_t* tpo = TG ? P.t_po + (size_t)layer * P.att_slots * P.n_embed : nullptr;
+    uint64_t* tpml = TG ? P.t_pml + (size_t)layer * P.att_slots * P.n_heads * 2 : nullptr;
 
     stamp(tr, 0);
     uint4 kb[MAXST], vb[MAXST];   /* K/V slices of the unit's steps (static indices only) */
@@ -637,8 +795,43 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         hv = *(const float4*)(qkv + P.n_embed + kvd + (size_t)g * HD + l4);
         fr = *(const float2*)(P.rope_freq + l4 / 2);
     };
+    const uint64_t* tqkv = TG ? P.t_qkv + (size_t)layer * (P.n_embed + 2 * kvd) : nullptr;
+    auto poll_heads = [&](int u) {
+        const int g = u / nch;
+#pragma unroll
+        for (int j = 0; j < NH; j++) {
+            const int h = min(wave + PK_WAVES * j, NREP);
+            const float* nwp = has_norm ? (h < NREP ? L.q_norm : L.k_norm) : P.rope_freq;
+            ng[j] = *(const float4*)(nwp + l4);
+        }
+        fr = *(const float2*)(P.rope_freq + l4 / 2);
+        auto off = [&](int i) {
+            const int j = i >> 2;
+            const int h = min(wave + PK_WAVES * j, NREP);
+            const int base = j == NH ? P.n_embed + kvd + g * HD
+                                     : (h < NREP ? (g * NREP + h) * HD : P.n_embed + g * HD);
+            return base + l4 + (i & 3);
+        };
+        uint64_t w[(NH + 1) * 4];
+#pragma unroll
+        for (int j = 0; j <= NH; j++) {
+            const ulonglong2* p = (const ulonglong2*)(tqkv + off(4 * j));
+            const ulonglong2 a = p[0], b = p[1];
+            w[4 * j] = a.x; w[4 * j + 1] = a.y; w[4 * j + 2] = b.x; w[4 * j + 3] = b.y;
+        }
+        tg_settle(w, tqkv, off, tag, P);
+#pragma unroll
+        for (int j = 0; j < NH; j++)
+            hx[j] = make_float4(tg_val(w[4 * j]), tg_val(w[4 * j + 1]), tg_val(w[4 * j + 2]), tg_val(w[4 * j + 3]));
+        hv = make_float4(tg_val(w[4 * NH]), tg_val(w[4 * NH + 1]), tg_val(w[4 * NH + 2]), tg_val(w[4 * NH + 3]));
+    };
     const bool has = (int)blockIdx.x < nunits;
-    if (wait_target) pk_wait(P, wait_target);
+    if constexpr (TG) {
+        if (has) {
+            load_kv(blockIdx.x);
+            if (wait_target) pk_wait(P, wait_target);
+        }
+    } else if (wait_target) pk_wait(P, wait_target);
     if (!has) stamp(tr, 1);
 
     for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
@@ -646,9 +839,15 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int t0 = c * chunk;
         const int t1 = min(t0 + chunk, pos + 1);
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
-        load_heads(u);
-        lg_issue_order();   /* heads first, then K/V */
-        load_kv(u);
+        if constexpr (TG) {
+            /* K/V first: they do not wait for this token */
+            if (u != (int)blockIdx.x) load_kv(u);
+            poll_heads(u);
+        } else {
+            load_heads(u);
+            lg_issue_order();   /* heads first, then K/V */
+            load_kv(u);
+        }
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
         *(float4*)(s_kv + HD + l4) = hv;
@@ -727,7 +926,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     const float pw = lg_exp2(sc - mn);
                     l[r] = l[r] * a + pw;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) o[r][i] = o[r][i] * a + pw * vf[i];
+                    for (int i = 0; i < 8; i++) o[r][i] = lg_fma2(o[r][i], a, pw, vf[i]);
                     m[r] = mn;
                 }
             }
@@ -757,7 +956,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
             }
         }
         bar();
-        for (int i = threadIdx.x; i < NREP * HD; i += PK_THREADS) {
+        for (int i = LG_TID; i < NREP * HD; i += PK_THREADS) {
             const int r = i / HD, d = i % HD, q = g * NREP + r;
             float M = -INFINITY;
             for (int w = 0; w < PK_WAVES; w++) M = fmaxf(M, s_m[w * NREP + r]);
@@ -768,16 +967,89 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                 O += s_o[(w * NREP + r) * HD + d] * wt;
                 Ls += s_sc[w * NREP + r] * wt;
             }
-            cst(&po[(size_t)c * P.n_embed + (size_t)q * HD + d], O);
-            if (d == 0) {
-                cst(&pml[((size_t)c * P.n_heads + q) * 2], M);
-                cst(&pml[((size_t)c * P.n_heads + q) * 2 + 1], Ls);
+            if constexpr (TG) {
+                if (c == nch - 1) {
+                    s_q[i] = O;   /* q is no longer read: the merging unit keeps its own partial here */
+                    if (d == 0) { s_own[2 * r] = M; s_own[2 * r + 1] = Ls; }
+                } else {
+                    tg_st(&tpo[(size_t)c * P.n_embed + (size_t)q * HD + d], O, tag);
+                    if (d == 0) {
+                        tg_st(&tpml[((size_t)c * P.n_heads + q) * 2], M, tag);
+                        tg_st(&tpml[((size_t)c * P.n_heads + q) * 2 + 1], Ls, tag);
+                    }
+                }
+            } else {
+                cst(&po[(size_t)c * P.n_embed + (size_t)q * HD + d], O);
+                if (d == 0) {
+                    cst(&pml[((size_t)c * P.n_heads + q) * 2], M);
+                    cst(&pml[((size_t)c * P.n_heads + q) * 2 + 1], Ls);
+                }
             }
         }
-        if (nch > PK_ATT_MERGE) {
+        if constexpr (TG) {
+            if (c == nch - 1) {
+                /* merge the head group's chunks in ascending order, as
+                 * MergeAct::merge does: M = max m_c, w_c = 2^(m_c - M),
+                 * out = sum o_c w_c / sum l_c w_c */
+                float* s_ml = s_sc;                                   /* [nch][NREP][2] */
+                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NREP] */
+                bar();
+                for (int i = LG_TID; i < nch * NREP; i += PK_THREADS) {
+                    const int cc = i / NREP, r = i % NREP;
+                    if (cc == c) {
+                        s_ml[2 * i] = s_own[2 * r];
+                        s_ml[2 * i + 1] = s_own[2 * r + 1];
+                    } else {
+                        uint64_t w[2];
+                        tg_poll(w, tpml + ((size_t)cc * P.n_heads + g * NREP + r) * 2, [](int k) { return k; }, tag,
+                                P);
+                        s_ml[2 * i] = tg_val(w[0]);
+                        s_ml[2 * i + 1] = tg_val(w[1]);
+                    }
+                }
+                bar();
+                if (LG_TID < NREP) {
+                    const int r = LG_TID;
+                    float M = s_ml[r * 2];
+                    for (int cc = 1; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NREP + r) * 2]);
+                    float Ls = 0.0f;
+                    for (int cc = 0; cc < nch; cc++) {
+                        const float wgt = lg_exp2(s_ml[(cc * NREP + r) * 2] - M);
+                        s_w[cc * NREP + r] = wgt;
+                        Ls += s_ml[(cc * NREP + r) * 2 + 1] * wgt;
+                    }
+                    s_red[r] = Ls;
+                }
+                bar();
+                uint64_t* tatt = P.t_att + (size_t)layer * P.n_embed + (size_t)g * NREP * HD;
+                for (int i = LG_TID; i < NREP * HD; i += PK_THREADS) {
+                    const int r = i / HD;
+                    const uint64_t* col = tpo + (size_t)g * NREP * HD + i;
+                    float acc = 0.0f;
+                    for (int c0 = 0; c0 < nch; c0 += 8) {
+                        /* 8 chunks in flight; the own chunk (c, the last)
+                         * and those past nch read chunk 0's word, unused */
+                        uint64_t w[8] = {};
+                        if (nch > 1) {
+                            auto off = [&](int k) {
+                                const int cc = c0 + k;
+                                return (size_t)(cc < nch && cc != c ? cc : 0) * P.n_embed;
+                            };
+                            tg_poll(w, col, off, tag, P);
+                        }
+#pragma unroll
+                        for (int k = 0; k < 8; k++) {
+                            const int cc = c0 + k;
+                            if (cc < nch) acc += (cc == c ? s_q[i] : tg_val(w[k])) * s_w[cc * NREP + r];
+                        }
+                    }
+                    tg_st(&tatt[i], acc / s_red[r], tag);
+                }
+            }
+        } else if (nch > PK_ATT_MERGE) {
             wait_stores();
             bar();
-            if (threadIdx.x == 0) {
+            if (LG_TID == 0) {
                 const uint32_t old = __hip_atomic_fetch_add(&P.attn_cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 s_int[0] = old == (uint32_t)(nch - 1);
             }
@@ -788,14 +1060,14 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                  * with 8 loads in flight (the consumer's formula) */
                 float* s_ml = s_sc;                                   /* [nch][NREP][2] */
                 float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NREP] */
-                for (int i = threadIdx.x; i < nch * NREP; i += PK_THREADS) {
+                for (int i = LG_TID; i < nch * NREP; i += PK_THREADS) {
                     const float2 v = cld2(&pml[((size_t)(i / NREP) * P.n_heads + g * NREP + i % NREP) * 2]);
                     s_ml[2 * i] = v.x;
                     s_ml[2 * i + 1] = v.y;
                 }
                 bar();
-                if (threadIdx.x < NREP) {
-                    const int r = threadIdx.x;
+                if (LG_TID < NREP) {
+                    const int r = LG_TID;
                     float M = -INFINITY;
                     for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NREP + r) * 2]);
                     float Ls = 0.0f;
@@ -807,7 +1079,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     s_red[r] = Ls;
                 }
                 bar();
-                for (int i = threadIdx.x; i < NREP * HD; i += PK_THREADS) {
+                for (int i = LG_TID; i < NREP * HD; i += PK_THREADS) {
                     const int r = i / HD;
                     const float* col = po + (size_t)g * NREP * HD + i;
                     float acc = 0.0f;
@@ -822,17 +1094,20 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     /* the merged vector as a one-chunk partial (m 0, l 1) */
                     cst(&po_m[(size_t)g * NREP * HD + i], acc / s_red[r]);
                 }
-                if (threadIdx.x < NREP) {
-                    cst(&pml_m[(size_t)(g * NREP + threadIdx.x) * 2], 0.0f);
-                    cst(&pml_m[(size_t)(g * NREP + threadIdx.x) * 2 + 1], 1.0f);
+                if (LG_TID < NREP) {
+                    cst(&pml_m[(size_t)(g * NREP + LG_TID) * 2], 0.0f);
+                    cst(&pml_m[(size_t)(g * NREP + LG_TID) * 2 + 1], 1.0f);
                 }
-                if (threadIdx.x == 0) cst(&P.attn_cnt[g], 0u);
+                if (LG_TID == 0) cst(&P.attn_cnt[g], 0u);
             }
         }
         bar();
     }
     stamp(tr, 2);
-    if (sig) pk_signal(P, sig);
+    if (sig) {
+        if constexpr (TG) pk_publish(P, sig);
+        else pk_signal(P, sig);
+    }
     stamp(tr, 3);
 }
 

@@ -48,7 +48,7 @@ __device__ __forceinline__ void pf_store_q8k(const float v[4], const PfQ8K& q, i
 }
 
 /* block b of token t: rmsnorm(x_t) * w (w != NULL) or x_t, quantized; the
- * sum of squares in k_rmsnorm_quant's lane order (fast/lil_math.cpp:922-929) */
+ * sum of squares in the decode kernels' order (fast/lil_math.cpp:922-929) */
 __global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, int ldx, const float* __restrict__ w,
                                                  float eps, int n, PfQ8K q)
 {
@@ -56,12 +56,7 @@ __global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, in
     const float* xr = x + (size_t)t * ldx;
     float scale = 1.0f;
     if (w) {
-        float ss = 0.0f;
-        for (int i = 4 * lane; i < n; i += 256) {
-            const float4 v = *(const float4*)(xr + i);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        ss = lg_group_sum<64>(ss);
+        const float ss = lg_sumsq_chunked(xr, n, lane);
         scale = 1.0f / sqrtf(ss / (float)n + eps);
     }
     const int base = b * 256 + 4 * lane;
@@ -178,7 +173,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
                 const float pw = __builtin_amdgcn_exp2f(sc - mn);
                 l[r] = l[r] * a + pw;
 #pragma unroll
-                for (int i = 0; i < 8; i++) o[r][i] = o[r][i] * a + pw * vf[i];
+                for (int i = 0; i < 8; i++) o[r][i] = lg_fma2(o[r][i], a, pw, vf[i]);
                 m[r] = mn;
             }
         }
@@ -195,11 +190,11 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
             const float mn = fmaxf(m[r], m2);
             const float a = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - mn);
             const float bb = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
-            l[r] = l[r] * a + l2 * bb;
+            l[r] = lg_fma2(l[r], a, l2, bb);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float o2 = step ? lg_from_half_above(o[r][i]) : lg_from_row_above(o[r][i]);
-                o[r][i] = o[r][i] * a + o2 * bb;
+                o[r][i] = lg_fma2(o[r][i], a, o2, bb);
             }
             m[r] = mn;
         }

@@ -32,7 +32,7 @@ __device__ __forceinline__ void lg_qk_norm_rope_kv_wave(int wave, float* __restr
         e[0] = t.x; e[1] = t.y; e[2] = t.z; e[3] = t.w;
     }
     if (nw) {
-        float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
+        float ss = lg_sq4(make_float4(e[0], e[1], e[2], e[3]));
         ss = lg_group_sum<64>(ss);
         const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
         if (act) {
@@ -51,8 +51,8 @@ __device__ __forceinline__ void lg_qk_norm_rope_kv_wave(int wave, float* __restr
                 float s, c;
                 sincosf(ang, &s, &c);
                 const float x0 = e[j], x1 = e[j + 1];
-                e[j] = x0 * c - x1 * s;
-                e[j + 1] = x0 * s + x1 * c;
+                e[j] = lg_fma2(x0, c, -x1, s);
+                e[j + 1] = lg_fma2(x0, s, x1, c);
             }
         }
         *(float4*)(p + 4 * lane) = make_float4(e[0], e[1], e[2], e[3]);
