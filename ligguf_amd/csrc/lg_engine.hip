@@ -136,9 +136,6 @@ struct lg_ctx {
     const void* pk_kernel = nullptr; /* the instantiation for this model */
     uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
     uint64_t pk_base = 0;
-    uint32_t pk_tag = 0;             /* tag of the last persistent launch (tagged activations) */
-    uint64_t* pk_tagged = nullptr;   /* the tagged activation arena and its size in words */
-    size_t pk_tagged_n = 0;
     int* pk_status_host = nullptr;   /* pinned {token, error} of the last persistent / fused step */
     bool last_was_pk = false;        /* the last step left its greedy token in pk_status_host */
 
@@ -378,24 +375,6 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.hb = P.qkv + L * qs;
     }
     {
-        /* the persistent kernel's tagged activations (zero: no tag yet) */
-        const size_t L = (size_t)m->n_layers, ne = m->n_embed, qs = ne + 2 * m->kv_dim, ff = m->n_ff;
-        const size_t slots = (size_t)att_nch + 1;
-        const size_t words = (L + 1) * ne + L * ne + L * qs + L * ff + L * ne + L * slots * ne + L * slots * m->n_heads * 2;
-        uint64_t* t = nullptr;
-        if ((rc = dalloc(ctx, (void**)&t, words * sizeof(uint64_t)))) return rc;
-        LG_HIP_CHECK(hipMemset(t, 0, words * sizeof(uint64_t)));
-        ctx->pk_tagged = t;
-        ctx->pk_tagged_n = words;
-        P.t_xs = t;
-        P.t_xm = P.t_xs + (L + 1) * ne;
-        P.t_qkv = P.t_xm + L * ne;
-        P.t_hb = P.t_qkv + L * qs;
-        P.t_att = P.t_hb + L * ff;
-        P.t_po = P.t_att + L * ne;
-        P.t_pml = P.t_po + L * slots * ne;
-    }
-    {
         /* per-layer attention partials, each written once per step */
         const size_t L = (size_t)m->n_layers;
         float* ws = nullptr;
@@ -520,12 +499,7 @@ static int enqueue_pk(lg_ctx* c, int tok, int pos)
 {
     PkParams& P = c->pk;
     PkStep S = {};
-    if (++c->pk_tag == 0) {
-        /* the tag wrapped: no word may still carry a tag of this new cycle */
-        LG_HIP_CHECK(hipMemsetAsync(c->pk_tagged, 0, c->pk_tagged_n * sizeof(uint64_t), c->stream));
-        c->pk_tag = 1;
-    }
-    S.tok = tok; S.pos = pos; S.base = c->pk_base; S.tag = c->pk_tag;
+    S.tok = tok; S.pos = pos; S.base = c->pk_base;
     S.trace = c->pk_trace;
     c->pk_trace = nullptr;   /* one step only */
     int rc = lg_persist_launch(c->pk_kernel, c->pk, &S, c->pk_nwg, c->stream);

@@ -61,16 +61,6 @@ struct PkParams {
     uint32_t* amax_cnt;      /* zero between launches */
     int* tok_out;            /* greedy token of this step */
     uint32_t* err;           /* nonzero: a sync wait expired (or an unsupported phase) */
-    /* the persistent kernel's activations, tagged: each value stored with
-     * the launch's tag as one 64-bit word {fp32 bits, tag}, so a reader
-     * polls the values themselves instead of a completion flag */
-    uint64_t* t_xs;          /* [n_layers+1][n_embed] */
-    uint64_t* t_xm;          /* [n_layers][n_embed] */
-    uint64_t* t_qkv;         /* [n_layers][n_embed + 2*kv_dim] */
-    uint64_t* t_hb;          /* [n_layers][n_ff] */
-    uint64_t* t_att;         /* [n_layers][n_embed] attention output, chunks merged */
-    uint64_t* t_po;          /* [n_layers][att_slots][n_embed] unnormalised partials */
-    uint64_t* t_pml;         /* [n_layers][att_slots][n_heads][2] */
     const int* feed;         /* [n_ctx] prompt tokens for positions < PkStep.feed_end (fused path) */
     int spin_cap;
 };
@@ -80,7 +70,7 @@ struct PkParams {
 struct PkStep {
     int tok, pos;
     int feed_end;            /* fused path: positions below this take their token from PkParams.feed */
-    uint32_t tag;            /* persistent kernel: this launch's tag (nonzero, new per launch) */
+    int pad_;
     uint64_t base;           /* progress value at launch; the launch adds 5*n_layers + 1 */
     uint64_t* trace;         /* NULL, or [5*n_layers+1][gridDim][4] timestamps (100 MHz clock):
                                 phase entry, wait done, activation built, phase published */

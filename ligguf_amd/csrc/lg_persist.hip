@@ -52,12 +52,6 @@ static __device__ __forceinline__ int pk_tid()
 /* ------------------------------------------------------------------ */
 /* the kernel                                                           */
 /* ------------------------------------------------------------------ */
-/* One instantiation per (layer type, output type, head_dim, query heads per
- * KV head): every phase body is inlined, so no call saves registers.
- * Activation buffers (each written once per launch): xs[l] = residual stream
- * entering layer l (xs[0] the embedding row, xs[L] the output of the last
- * layer), xm[l] = after attention, qkv[l], hb[l]; the attention partials
- * (att_po/att_pml) are per layer too. */
 /* layer l from the per-kind arenas: pointers computed from kernel
  * arguments, so the weight loads stay global (not flat) loads */
 __device__ __forceinline__ PkLayer pk_layer(const PkParams& P, int l)
@@ -79,61 +73,50 @@ __device__ __forceinline__ PkLayer pk_layer(const PkParams& P, int l)
     return L;
 }
 
+/* One instantiation per (layer type, output type, head_dim, query heads per
+ * KV head): every phase body is inlined, so no call saves registers, and the
+ * phases use the matvec batch sizes of the fused kernels (no spills: the
+ * opaque thread index above keeps per-phase address arithmetic inside the
+ * layer loop).  Activation buffers (each written once per launch): xs[l] =
+ * residual stream entering layer l (xs[0] the embedding row, xs[L] the output
+ * of the last layer), xm[l] = after attention, qkv[l], hb[l]; the attention
+ * partials (att_po/att_pml) are per layer too. */
 template <int LT, int OT, int HD, int NREP>
 __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams P, PkStep S)
 {
     const int ne = P.n_embed, kvd = P.kv_dim, nff = P.n_ff;
     const int qs = ne + 2 * kvd;
-    const uint32_t tag = S.tag;
     const uint64_t B = S.base;
     constexpr int NE = NsE<LT>::value, NF = 3 * NE;
-    /* trace slot of phase p for this WG */
 #define TR(p) (S.trace ? S.trace + ((size_t)(p) * gridDim.x + blockIdx.x) * 4 : nullptr)
     for (int l = 0; l < P.n_layers; l++) {
         const PkLayer L = pk_layer(P, l);
-        uint64_t* xin = P.t_xs + (size_t)l * ne;
-        uint64_t* xmid = P.t_xm + (size_t)l * ne;
-        uint64_t* xout = P.t_xs + (size_t)(l + 1) * ne;
-        uint64_t* qkv = P.t_qkv + (size_t)l * qs;
-        uint64_t* hb = P.t_hb + (size_t)l * nff;
-        const uint64_t* att = P.t_att + (size_t)l * ne;
-        const uint64_t p0 = B + 5ull * l;   /* progress after phase A of layer l is p0 + 1 */
-        /* A: rmsnorm + QKV (layer 0 takes x from the embedding row) */
+        const uint64_t p0 = B + 5ull * l;
+        float* xin = P.xs + (size_t)l * ne;
+        float* xmid = P.xm + (size_t)l * ne;
+        float* xout = P.xs + (size_t)(l + 1) * ne;
+        float* qkv = P.qkv + (size_t)l * qs;
+        float* hb = P.hb + (size_t)l * nff;
         if (l == 0)
-            phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_STORE, BLD_EMB, 2, true, true>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l), MergeSrc{},
-                tag);
+            phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_STORE, BLD_EMB, 2, true>(
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l));
         else
-            phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_STORE, BLD_RMS, 2, true, true>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, nullptr, p0, p0 + 1, TR(5 * l),
-                MergeSrc{}, tag);
-        /* B: attention, the chunks of each head group merged by its last unit */
-        phase_attn<HD, NREP, true>(P, L, l, S.pos, nullptr, p0 + 1, p0 + 2, TR(5 * l + 1), tag);
-        /* C: att_out + residual (layer 0: the residual rows are the
-         * embedding row stored by workgroup 0, polled) */
-        if (l == 0)
-            phase_mv<LT, NE, Batch<LT, NE, 1, 1, 512>::value, 1, EPI_RESID, BLD_PLAIN, 2, true, true, true>(
-                P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, att, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2), MergeSrc{},
-                tag);
-        else
-            phase_mv<LT, NE, Batch<LT, NE, 1, 1, 512>::value, 1, EPI_RESID, BLD_PLAIN, 2, true, true>(
-                P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, att, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2), MergeSrc{},
-                tag);
-        /* D: rmsnorm + up|gate + SwiGLU */
-        phase_mv<LT, NE, Batch<LT, NE, 2, 2, 512>::value, 2, EPI_SWIGLU, BLD_RMS, 2, true, true>(
-            P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, xmid, nullptr, hb, nullptr, p0 + 3, p0 + 4, TR(5 * l + 3), MergeSrc{},
-            tag);
-        /* E: down + residual */
-        phase_mv<LT, NF, Batch<LT, NF, 1, 1, 512>::value, 1, EPI_RESID, BLD_PLAIN, 6, true, true>(
-            P, 0, L.down, L.down_rsz, ne, 0, nullptr, hb, xmid, xout, nullptr, p0 + 4, p0 + 5, TR(5 * l + 4), MergeSrc{},
-            tag);
+            phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_STORE, BLD_RMS, 2, true>(
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l));
+        phase_attn<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
+        phase_mv<LT, NE, Batch<LT, NE, 1, 1, 512>::value, 1, EPI_RESID, BLD_MERGE, 2, true>(
+            P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2),
+            att_partials<HD, NREP>(P, l, S.pos));
+        phase_mv<LT, NE, Batch<LT, NE, 2, 2, 512>::value, 2, EPI_SWIGLU, BLD_RMS, 2, true>(
+            P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, xmid, nullptr, hb, nullptr, p0 + 3, p0 + 4, TR(5 * l + 3));
+        phase_mv<LT, NF, Batch<LT, NF, 1, 1, 512>::value, 1, EPI_RESID, BLD_PLAIN, 6, true>(
+            P, 0, L.down, L.down_rsz, ne, 0, nullptr, hb, xmid, xout, nullptr, p0 + 4, p0 + 5, TR(5 * l + 4));
     }
-    /* F: final norm, output head, argmax */
     const uint64_t pf = B + 5ull * P.n_layers;
     constexpr int NO = NsE<OT>::value;
-    phase_mv<OT, NO, Batch<OT, NO, 1, 4, 288>::value, 1, EPI_LOGITS, BLD_RMS, 2, true, true>(
-        P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.t_xs + (size_t)P.n_layers * ne, nullptr, P.logits,
-        nullptr, pf, pf + 1, TR(5 * P.n_layers), MergeSrc{}, tag);
+    phase_mv<OT, NO, Batch<OT, NO, 1, 4, 288>::value, 1, EPI_LOGITS, BLD_RMS, 2, true>(
+        P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * ne, nullptr, P.logits, nullptr,
+        pf, pf + 1, TR(5 * P.n_layers));
 #undef TR
 }
 

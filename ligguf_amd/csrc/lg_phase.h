@@ -38,7 +38,6 @@ __shared__ __attribute__((aligned(16))) float s_kv[2 * 128];
 __shared__ __attribute__((aligned(16))) float s_sc[3 * PK_ATT_MAX_NCH * PK_MAX_NREP];
 __shared__ __attribute__((aligned(16))) float s_o[PK_WAVES * PK_MAX_NREP * 128];
 __shared__ float s_m[PK_WAVES * PK_MAX_NREP];
-__shared__ float s_own[2 * PK_MAX_NREP];
 
 /* ------------------------------------------------------------------ */
 /* coherent memory helpers                                              */
@@ -61,74 +60,6 @@ __device__ __forceinline__ float2 cld2(const float* p)
     const uint64_t u = cld((const uint64_t*)p);
     return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
 }
-
-/* tagged values: {fp32 bits, tag} in one 64-bit word, written with a
- * single-copy-atomic coherent store.  A tagged buffer is written once per
- * launch, with the launch's tag.  Its writers publish their progress word
- * without waiting for the acknowledgement of their data stores, so a reader
- * past the progress wait may still find a word that is not there yet: it
- * reads with plain (L2-cached) 16-byte loads -- two words, each written
- * whole -- and loads every word without the tag again, coherently, until it
- * carries it.  (A word read too early can leave a stale line in an L2; the
- * coherent reloads do not use it, and the launch's end discards it.) */
-__device__ __forceinline__ float tg_val(uint64_t u)
-{
-    return __uint_as_float((uint32_t)u);
-}
-
-__device__ __forceinline__ bool tg_is(uint64_t u, uint32_t tag)
-{
-    return (uint32_t)(u >> 32) == tag;
-}
-
-__device__ __forceinline__ void tg_st(uint64_t* p, float v, uint32_t tag)
-{
-    cst(p, ((uint64_t)tag << 32) | __float_as_uint(v));
-}
-
-/* u[i] = the word at p + off(i), i < N, for words already loaded into u:
- * loads again the ones without `tag` until all carry it.  Bounded: past
- * spin_cap rounds, or once another wait has expired (the error flag), it
- * sets the error flag and returns what it has. */
-template <int N, typename Off>
-__device__ __forceinline__ void tg_settle(uint64_t (&u)[N], const uint64_t* p, Off off, uint32_t tag,
-                                          const PkParams& P)
-{
-    uint32_t e = 0;
-    for (int it = 0;; it++) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < N; i++) ok = ok && tg_is(u[i], tag);
-        if (ok) break;
-        if (e || it >= P.spin_cap) {
-            cst(P.err, 1u);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-        for (int i = 0; i < N; i++)
-            if (!tg_is(u[i], tag)) u[i] = cld(p + off(i));
-        e = cld(P.err);
-    }
-}
-
-template <int N, typename Off>
-__device__ __forceinline__ void tg_poll(uint64_t (&u)[N], const uint64_t* p, Off off, uint32_t tag, const PkParams& P)
-{
-#pragma unroll
-    for (int i = 0; i < N; i++) u[i] = cld(p + off(i));
-    tg_settle(u, p, off, tag, P);
-}
-
-/* element type of an activation buffer: fp32, or tagged words */
-template <bool TG>
-struct ActT {
-    using type = float;
-};
-template <>
-struct ActT<true> {
-    using type = uint64_t;
-};
 
 /* keeps the loads before it ahead of the loads after it in issue order (a
  * wave's loads return in issue order, so what is needed first is issued
@@ -153,13 +84,6 @@ __device__ __forceinline__ void wait_stores()
 __device__ __forceinline__ void pk_signal(const PkParams& P, uint64_t val)
 {
     wait_stores();
-    bar();
-    if (LG_TID == 0) cst(&P.progress[blockIdx.x], val);
-}
-
-/* publish without waiting for the data stores (their values are tagged) */
-__device__ __forceinline__ void pk_publish(const PkParams& P, uint64_t val)
-{
     bar();
     if (LG_TID == 0) cst(&P.progress[blockIdx.x], val);
 }
@@ -249,30 +173,6 @@ struct ActSrc {
     }
 };
 
-/* the same chunks of a tagged vector: issue() the plain loads, settle()
- * into an ActSrc once every word carries the tag */
-template <int CPW>
-struct TgSrc {
-    uint64_t u[CPW * 4];
-    __device__ __forceinline__ void issue(const uint64_t* __restrict__ src)
-    {
-#pragma unroll
-        for (int c = 0; c < CPW; c++) {
-            const ulonglong2* p = (const ulonglong2*)(src + chunk_base(c));
-            const ulonglong2 a = p[0], b = p[1];
-            u[4 * c] = a.x; u[4 * c + 1] = a.y; u[4 * c + 2] = b.x; u[4 * c + 3] = b.y;
-        }
-    }
-    __device__ __forceinline__ void settle(const uint64_t* __restrict__ src, uint32_t tag, const PkParams& P,
-                                           ActSrc<CPW>& a)
-    {
-        tg_settle(u, src, [](int i) { return chunk_base(i >> 2) + (i & 3); }, tag, P);
-#pragma unroll
-        for (int c = 0; c < CPW; c++)
-            a.v[c] = make_float4(tg_val(u[4 * c]), tg_val(u[4 * c + 1]), tg_val(u[4 * c + 2]), tg_val(u[4 * c + 3]));
-    }
-};
-
 /* attention partials of one layer, merged by the att_out build (BLD_MERGE):
  * the source vector is sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c,
  * M = max_c m_c, over the nch chunks in ascending order */
@@ -343,10 +243,9 @@ __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int p
  * both paths agree bit for bit.  x is the source vector (BLD_RMS) or, for
  * layer 0 (BLD_EMB), the embedding row of tok, dequantized here; WG 0 also
  * stores that row as the residual stream `emb_out`. */
-template <int QT, int CPW, bool TG = false>
+template <int QT, int CPW>
 __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const NormW<CPW>& nw, const ActSrc<CPW>& xsrc,
-                                          bool from_embed, typename ActT<TG>::type* __restrict__ emb_out,
-                                          uint32_t tag = 0)
+                                          bool from_embed, float* __restrict__ emb_out)
 {
     constexpr int n = CPW * 256 * PK_WAVES;
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
@@ -362,13 +261,8 @@ __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const Norm
             const int b = chunk_base(c);
             xv[c] = *(const float4*)(s_x + b);
             if (blockIdx.x == 0) {
-                if constexpr (TG) {
-                    tg_st(&emb_out[b], xv[c].x, tag); tg_st(&emb_out[b + 1], xv[c].y, tag);
-                    tg_st(&emb_out[b + 2], xv[c].z, tag); tg_st(&emb_out[b + 3], xv[c].w, tag);
-                } else {
-                    cst(&emb_out[b], xv[c].x); cst(&emb_out[b + 1], xv[c].y);
-                    cst(&emb_out[b + 2], xv[c].z); cst(&emb_out[b + 3], xv[c].w);
-                }
+                cst(&emb_out[b], xv[c].x); cst(&emb_out[b + 1], xv[c].y);
+                cst(&emb_out[b + 2], xv[c].z); cst(&emb_out[b + 3], xv[c].w);
             }
         }
     } else {
@@ -449,25 +343,15 @@ struct Rows {
  * words; its own loads go after the wait, since a wave's loads return in
  * order and would hold the poll back.  Then: build the activation, compute,
  * store, publish.  CPW = 256-value activation chunks per wave; DB =
- * double-buffer the items (long phases: the output head).
- *
- * TG (tagged activations): src, res_src, out (except logits) and emb_out are
- * tagged buffers of launch tag `tag`, and the phase publishes without
- * waiting for its stores.  The source chunks are settled after the wait;
- * the residual rows were settled by this workgroup's own earlier build of
- * the same vector, and are read coherently (RESPOLL: not so -- they are
- * polled at phase entry). */
-template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, bool DB, bool TG = false, bool RESPOLL = false>
+ * double-buffer the items (long phases: the output head). */
+template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, bool DB>
 __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8_t* __restrict__ W, uint32_t rsz,
                                          int items, int kstride, const float* __restrict__ normw,
-                                         const typename ActT<TG>::type* __restrict__ src,
-                                         const typename ActT<TG>::type* __restrict__ res_src,
-                                         typename ActT<TG && EPI != EPI_LOGITS>::type* __restrict__ out,
-                                         typename ActT<TG>::type* __restrict__ emb_out,
+                                         const float* __restrict__ src, const float* __restrict__ res_src,
+                                         float* __restrict__ out, float* __restrict__ emb_out,
                                          uint64_t wait_target, uint64_t sig, uint64_t* tr,
-                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0}, uint32_t tag = 0)
+                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0})
 {
-    static_assert(!TG || BLD != BLD_MERGE, "tagged phases read the merged attention vector");
     using F = Fmt<FMT>;
     constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q1_0 || FMT == LG_Q1_G) ? LG_Q8_0 : LG_Q8_K;
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
@@ -486,43 +370,21 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     float res[MAXB];
     constexpr bool from_embed = BLD == BLD_EMB;
     constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
-    TgSrc<CPW> ts;
     auto load_src = [&]() {
-        if constexpr (TG) {
-            if (!from_embed) ts.issue(src);
-        } else {
-            if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
-            else if (!from_embed) as.load(src);
-        }
+        if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
+        else if (!from_embed) as.load(src);
     };
     auto load_res = [&](float* r, int b0) {
         if (EPI == EPI_RESID) {
 #pragma unroll
-            for (int b = 0; b < MAXB; b++) {
-                const int i = min(i0 + b0 + b, wlast);
-                if constexpr (TG) r[b] = tg_val(cld(res_src + i));
-                else r[b] = res_src[i];
-            }
+            for (int b = 0; b < MAXB; b++) r[b] = res_src[min(i0 + b0 + b, wlast)];
         }
     };
     auto prefetch = [&]() {
         R0.load(W, rsz, i0, wlast, kstride, lane);
         load_res(res, 0);
     };
-    if constexpr (TG) {
-        if constexpr (RESPOLL && EPI == EPI_RESID) {
-            for (int j = lane; j < my; j += 64) {
-                uint64_t u[1];
-                tg_poll(u, res_src + i0 + j, [](int) { return 0; }, tag, P);
-            }
-        }
-        if (rms) nw.load(normw);
-        if (wave != 0) prefetch();
-        if (wait_target) pk_wait(P, wait_target);
-        load_src();
-        if (wave == 0) prefetch();
-        if (!from_embed) ts.settle(src, tag, P, as);
-    } else if (!wait_target) {
+    if (!wait_target) {
         /* no dependency wait (fused kernels): the activation and the norm
          * weights go first, the rows after them */
         load_src();
@@ -537,7 +399,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         if (wave == 0) prefetch();
     }
     stamp(tr, 1);
-    if (rms) build_rms<QT, CPW, TG>(P, tok, nw, as, from_embed, emb_out, tag);
+    if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out);
     else {
         if (BLD == BLD_MERGE) mg.merge(ms.nch, as);
         build_plain<QT, CPW>(as);
@@ -573,8 +435,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                         const float u = acc[0], g = acc[1];
                         v = (g / (1.0f + expf(-g))) * u;
                     }
-                    if constexpr (EPI == EPI_LOGITS) out[i] = v;
-                    else if constexpr (TG) tg_st(&out[i], v, tag);
+                    if (EPI == EPI_LOGITS) out[i] = v;
                     else cst(&out[i], v);
                 }
             }
@@ -621,10 +482,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         wait_stores();
         bar();
         if (sig && LG_TID == 0) cst(&P.progress[blockIdx.x], sig);
-    } else if (sig) {
-        if constexpr (TG) pk_publish(P, sig);
-        else pk_signal(P, sig);
-    }
+    } else if (sig) pk_signal(P, sig);
     stamp(tr, 3);
     if (EPI == EPI_LOGITS) {
         if (LG_TID == 0) {
@@ -725,16 +583,10 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * head the last unit of the head (atomic counter) merges them into the
  * layer's merged slot.  The unit of the head's last chunk also writes the fp16 cache
  * row pos. */
-/* TG (tagged activations): a unit issues its K/V loads before the wait,
- * then settles the heads from the tagged qkv of the layer; the partials are
- * tagged, and the unit of the head group's last chunk merges them
- * (MergeAct's formula and order, polling the other chunks' words) into the
- * tagged attention vector t_att.  Workgroups without a unit publish at
- * once. */
-template <int HD, int NREP, bool TG = false>
+template <int HD, int NREP>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
-                                           uint64_t* tr, uint32_t tag = 0)
+                                           uint64_t* tr)
 {
     constexpr int LPP = HD / 8;            /* lanes per position */
     constexpr int PPW = 64 / LPP;          /* positions per wave step */
@@ -756,8 +608,6 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
      * holds a stale copy of it */
     float* po_m = po + (size_t)(P.att_slots - 1) * P.n_embed;
     float* pml_m = pml + (size_t)(P.att_slots - 1) * P.n_heads * 2;
-    uint64_t* tpo = TG ? P.t_po + (size_t)layer * P.att_slots * P.n_embed : nullptr;
-    uint64_t* tpml = TG ? P.t_pml + (size_t)layer * P.att_slots * P.n_heads * 2 : nullptr;
 
     stamp(tr, 0);
     uint4 kb[MAXST], vb[MAXST];   /* K/V slices of the unit's steps (static indices only) */
@@ -795,43 +645,8 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         hv = *(const float4*)(qkv + P.n_embed + kvd + (size_t)g * HD + l4);
         fr = *(const float2*)(P.rope_freq + l4 / 2);
     };
-    const uint64_t* tqkv = TG ? P.t_qkv + (size_t)layer * (P.n_embed + 2 * kvd) : nullptr;
-    auto poll_heads = [&](int u) {
-        const int g = u / nch;
-#pragma unroll
-        for (int j = 0; j < NH; j++) {
-            const int h = min(wave + PK_WAVES * j, NREP);
-            const float* nwp = has_norm ? (h < NREP ? L.q_norm : L.k_norm) : P.rope_freq;
-            ng[j] = *(const float4*)(nwp + l4);
-        }
-        fr = *(const float2*)(P.rope_freq + l4 / 2);
-        auto off = [&](int i) {
-            const int j = i >> 2;
-            const int h = min(wave + PK_WAVES * j, NREP);
-            const int base = j == NH ? P.n_embed + kvd + g * HD
-                                     : (h < NREP ? (g * NREP + h) * HD : P.n_embed + g * HD);
-            return base + l4 + (i & 3);
-        };
-        uint64_t w[(NH + 1) * 4];
-#pragma unroll
-        for (int j = 0; j <= NH; j++) {
-            const ulonglong2* p = (const ulonglong2*)(tqkv + off(4 * j));
-            const ulonglong2 a = p[0], b = p[1];
-            w[4 * j] = a.x; w[4 * j + 1] = a.y; w[4 * j + 2] = b.x; w[4 * j + 3] = b.y;
-        }
-        tg_settle(w, tqkv, off, tag, P);
-#pragma unroll
-        for (int j = 0; j < NH; j++)
-            hx[j] = make_float4(tg_val(w[4 * j]), tg_val(w[4 * j + 1]), tg_val(w[4 * j + 2]), tg_val(w[4 * j + 3]));
-        hv = make_float4(tg_val(w[4 * NH]), tg_val(w[4 * NH + 1]), tg_val(w[4 * NH + 2]), tg_val(w[4 * NH + 3]));
-    };
     const bool has = (int)blockIdx.x < nunits;
-    if constexpr (TG) {
-        if (has) {
-            load_kv(blockIdx.x);
-            if (wait_target) pk_wait(P, wait_target);
-        }
-    } else if (wait_target) pk_wait(P, wait_target);
+    if (wait_target) pk_wait(P, wait_target);
     if (!has) stamp(tr, 1);
 
     for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
@@ -839,15 +654,9 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int t0 = c * chunk;
         const int t1 = min(t0 + chunk, pos + 1);
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
-        if constexpr (TG) {
-            /* K/V first: they do not wait for this token */
-            if (u != (int)blockIdx.x) load_kv(u);
-            poll_heads(u);
-        } else {
-            load_heads(u);
-            lg_issue_order();   /* heads first, then K/V */
-            load_kv(u);
-        }
+        load_heads(u);
+        lg_issue_order();   /* heads first, then K/V */
+        load_kv(u);
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
         *(float4*)(s_kv + HD + l4) = hv;
@@ -967,86 +776,13 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                 O += s_o[(w * NREP + r) * HD + d] * wt;
                 Ls += s_sc[w * NREP + r] * wt;
             }
-            if constexpr (TG) {
-                if (c == nch - 1) {
-                    s_q[i] = O;   /* q is no longer read: the merging unit keeps its own partial here */
-                    if (d == 0) { s_own[2 * r] = M; s_own[2 * r + 1] = Ls; }
-                } else {
-                    tg_st(&tpo[(size_t)c * P.n_embed + (size_t)q * HD + d], O, tag);
-                    if (d == 0) {
-                        tg_st(&tpml[((size_t)c * P.n_heads + q) * 2], M, tag);
-                        tg_st(&tpml[((size_t)c * P.n_heads + q) * 2 + 1], Ls, tag);
-                    }
-                }
-            } else {
-                cst(&po[(size_t)c * P.n_embed + (size_t)q * HD + d], O);
-                if (d == 0) {
-                    cst(&pml[((size_t)c * P.n_heads + q) * 2], M);
-                    cst(&pml[((size_t)c * P.n_heads + q) * 2 + 1], Ls);
-                }
+            cst(&po[(size_t)c * P.n_embed + (size_t)q * HD + d], O);
+            if (d == 0) {
+                cst(&pml[((size_t)c * P.n_heads + q) * 2], M);
+                cst(&pml[((size_t)c * P.n_heads + q) * 2 + 1], Ls);
             }
         }
-        if constexpr (TG) {
-            if (c == nch - 1) {
-                /* merge the head group's chunks in ascending order, as
-                 * MergeAct::merge does: M = max m_c, w_c = 2^(m_c - M),
-                 * out = sum o_c w_c / sum l_c w_c */
-                float* s_ml = s_sc;                                   /* [nch][NREP][2] */
-                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NREP] */
-                bar();
-                for (int i = LG_TID; i < nch * NREP; i += PK_THREADS) {
-                    const int cc = i / NREP, r = i % NREP;
-                    if (cc == c) {
-                        s_ml[2 * i] = s_own[2 * r];
-                        s_ml[2 * i + 1] = s_own[2 * r + 1];
-                    } else {
-                        uint64_t w[2];
-                        tg_poll(w, tpml + ((size_t)cc * P.n_heads + g * NREP + r) * 2, [](int k) { return k; }, tag,
-                                P);
-                        s_ml[2 * i] = tg_val(w[0]);
-                        s_ml[2 * i + 1] = tg_val(w[1]);
-                    }
-                }
-                bar();
-                if (LG_TID < NREP) {
-                    const int r = LG_TID;
-                    float M = s_ml[r * 2];
-                    for (int cc = 1; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NREP + r) * 2]);
-                    float Ls = 0.0f;
-                    for (int cc = 0; cc < nch; cc++) {
-                        const float wgt = lg_exp2(s_ml[(cc * NREP + r) * 2] - M);
-                        s_w[cc * NREP + r] = wgt;
-                        Ls += s_ml[(cc * NREP + r) * 2 + 1] * wgt;
-                    }
-                    s_red[r] = Ls;
-                }
-                bar();
-                uint64_t* tatt = P.t_att + (size_t)layer * P.n_embed + (size_t)g * NREP * HD;
-                for (int i = LG_TID; i < NREP * HD; i += PK_THREADS) {
-                    const int r = i / HD;
-                    const uint64_t* col = tpo + (size_t)g * NREP * HD + i;
-                    float acc = 0.0f;
-                    for (int c0 = 0; c0 < nch; c0 += 8) {
-                        /* 8 chunks in flight; the own chunk (c, the last)
-                         * and those past nch read chunk 0's word, unused */
-                        uint64_t w[8] = {};
-                        if (nch > 1) {
-                            auto off = [&](int k) {
-                                const int cc = c0 + k;
-                                return (size_t)(cc < nch && cc != c ? cc : 0) * P.n_embed;
-                            };
-                            tg_poll(w, col, off, tag, P);
-                        }
-#pragma unroll
-                        for (int k = 0; k < 8; k++) {
-                            const int cc = c0 + k;
-                            if (cc < nch) acc += (cc == c ? s_q[i] : tg_val(w[k])) * s_w[cc * NREP + r];
-                        }
-                    }
-                    tg_st(&tatt[i], acc / s_red[r], tag);
-                }
-            }
-        } else if (nch > PK_ATT_MERGE) {
+        if (nch > PK_ATT_MERGE) {
             wait_stores();
             bar();
             if (LG_TID == 0) {
@@ -1104,10 +840,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         bar();
     }
     stamp(tr, 2);
-    if (sig) {
-        if constexpr (TG) pk_publish(P, sig);
-        else pk_signal(P, sig);
-    }
+    if (sig) pk_signal(P, sig);
     stamp(tr, 3);
 }
 
