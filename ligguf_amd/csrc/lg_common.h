@@ -77,10 +77,13 @@ __device__ __forceinline__ int lg_dot4(int a, int b, int c)
 #define LG_DPP_HALF_MIRROR 0x141
 #define LG_DPP_MIRROR 0x140
 
+/* every lane of these permutes reads a valid lane of its row, so bound_ctrl
+ * changes nothing; with it the compiler folds the move into the consuming
+ * add/max (v_add_f32_dpp ...) */
 template <int CTRL>
 __device__ __forceinline__ int lg_dpp(int v)
 {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 
 template <int K>
@@ -188,6 +191,33 @@ __device__ __forceinline__ float lg_group_max(float v)
     if constexpr (G >= 32) v = fmaxf(v, lg_partner<4>(v));
     if constexpr (G >= 64) v = fmaxf(v, lg_partner<5>(v));
     return v;
+}
+
+/* max over aligned groups of G lanes of non-negative floats (|x| values),
+ * taken on their bits as unsigned integers -- the same order for
+ * non-negative floats; an integer max folds into the DPP move and needs no
+ * NaN canonicalization */
+template <int G>
+__device__ __forceinline__ float lg_group_max_nn(float v)
+{
+    uint32_t u = __float_as_uint(v);
+    if constexpr (G >= 2) u = max(u, (uint32_t)lg_partner<0>((int)u));
+    if constexpr (G >= 4) u = max(u, (uint32_t)lg_partner<1>((int)u));
+    if constexpr (G >= 8) u = max(u, (uint32_t)lg_partner<2>((int)u));
+    if constexpr (G >= 16) u = max(u, (uint32_t)lg_partner<3>((int)u));
+    if constexpr (G >= 32) u = max(u, (uint32_t)lg_partner<4>((int)u));
+    if constexpr (G >= 64) u = max(u, (uint32_t)lg_partner<5>((int)u));
+    return __uint_as_float(u);
+}
+
+/* wave max of non-negative floats, wave-uniform: the row maxima, then
+ * row_bcast:15 / row_bcast:31 up to lane 63 (as lg_wave_sum) */
+__device__ __forceinline__ float lg_wave_max_nn(float v)
+{
+    uint32_t u = __float_as_uint(lg_group_max_nn<16>(v));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, LG_DPP_ROW_BCAST15, 0xA, 0xF, false));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, LG_DPP_ROW_BCAST31, 0xC, 0xF, false));
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)u, 63));
 }
 
 template <int G>

@@ -114,42 +114,31 @@ struct Q8KLane {
 __device__ __forceinline__ Q8KLane lg_q8k_lane(const float v[4])
 {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    /* The first-index signed max of |x| as one 64-bit key: |x| bits (a
-     * non-negative float orders as an unsigned integer) above (255 - index)
-     * and the sign bit, so an unsigned max keeps the largest |x| and, among
-     * equal ones, the first index -- the strict '>' scan of the reference. */
-    float la = 0.0f;
-    uint32_t lo = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float a = fabsf(v[j]);
-        const bool take = a > la;
-        la = take ? a : la;
-        lo = take ? ((uint32_t)(255 - (4 * lane + j)) << 1) | (uint32_t)(v[j] < 0.0f) : lo;
-    }
-    uint64_t key = ((uint64_t)__float_as_uint(la) << 32) | lo;
-    auto step = [&](uint64_t o) { key = o > key ? o : key; };
-    step(((uint64_t)(uint32_t)lg_partner<0>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<0>((int)key));
-    step(((uint64_t)(uint32_t)lg_partner<1>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<1>((int)key));
-    step(((uint64_t)(uint32_t)lg_partner<2>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<2>((int)key));
-    step(((uint64_t)(uint32_t)lg_partner<3>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<3>((int)key));
-    step(((uint64_t)(uint32_t)lg_partner<4>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<4>((int)key));
-    step(((uint64_t)(uint32_t)lg_partner<5>((int)(key >> 32)) << 32) | (uint32_t)lg_partner<5>((int)key));
-    const float amax = __uint_as_float((uint32_t)(key >> 32));
-    const float mx = (key & 1u) ? -amax : amax;
+    /* The signed value of the first element with the largest |x| -- the
+     * strict '>' scan of the reference: amax by a wave max (exact), then
+     * the lowest lane holding an element equal to it (ballot) and, within
+     * that lane, the lowest such element; its value is read back from that
+     * lane. */
+    const float a0 = fabsf(v[0]), a1 = fabsf(v[1]), a2 = fabsf(v[2]), a3 = fabsf(v[3]);
+    const float amax = lg_wave_max_nn(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+    const bool h0 = a0 == amax, h1 = a1 == amax, h2 = a2 == amax, h3 = a3 == amax;
+    const float first = h0 ? v[0] : h1 ? v[1] : h2 ? v[2] : v[3];
+    const unsigned long long hits = __ballot(h0 || h1 || h2 || h3);
+    const int src = __builtin_ffsll((long long)hits) - 1;
+    const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(first), src));
+    /* amax == 0: every quant 0 and d = 0, as the reference's early out */
+    const float iscale = amax != 0.0f ? -127.0f / mx : 0.0f;
     uint32_t packed = 0;
     int s = 0;
-    if (amax != 0.0f) {
-        const float iscale = -127.0f / mx;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float f = iscale * v[j];
-            int t = f < 0.0f ? (int)(f - 0.5f) : (int)(f + 0.5f);
-            t = t < 127 ? t : 127;
-            s += t;
-            packed |= (uint32_t)(t & 255) << (8 * j);
-        }
+    for (int j = 0; j < 4; j++) {
+        const float f = iscale * v[j];
+        /* round half away from zero: f - 0.5 below zero, f + 0.5 otherwise
+         * (-0 takes +0.5; both give 0) */
+        int t = (int)(f + __builtin_copysignf(0.5f, f));
+        t = t < 127 ? t : 127;
+        s += t;
+        packed |= (uint32_t)(t & 255) << (8 * j);
     }
     s = lg_group_isum<4>(s);
     Q8KLane r;
@@ -182,7 +171,7 @@ __device__ __forceinline__ void lg_q8_0_blocks(const float v[4], uint8_t* __rest
         const float a = fabsf(v[j]);
         if (amax < a) amax = a;
     }
-    amax = lg_group_max<8>(amax);
+    amax = lg_group_max_nn<8>(amax);
     const int blk = lane >> 3;
     if (32 * blk >= nvalid) return;
     const float d = amax * (1.0f / 127.0f);
