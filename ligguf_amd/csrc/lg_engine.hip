@@ -324,7 +324,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         pk_attn_split(m->n_context, m->head_dim, nrep, &att_chunk, &att_nch);
     att_nch = std::max(att_nch, PK_ATT_MERGE);
     bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
-              m->n_kv_heads <= 32 && ctx->output.cols == m->n_embed && ctx->arena.ok;
+              m->n_kv_heads <= 32 && m->n_heads <= 32 && ctx->output.cols == m->n_embed && ctx->arena.ok;
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
         ok = D.qkv_fused && D.ug_fused && pk_shape_ok(D.qkv, lt, m->n_embed + 2 * m->kv_dim, m->n_embed) &&

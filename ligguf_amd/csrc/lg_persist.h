@@ -54,7 +54,7 @@ struct PkParams {
     float* att_po;           /* [n_layers][att_slots][n_embed] unnormalised attention partials */
     float* att_pml;          /* [n_layers][att_slots][n_heads][2] their (max, sum), log2 units */
     int att_slots;           /* per layer: one per chunk, then one for the vector merged in-kernel */
-    uint32_t* attn_cnt;      /* n_kv counters, zero between launches */
+    uint32_t* attn_cnt;      /* one per unit head set (n_kv * NREP / NQ <= 32), zero between launches */
     uint64_t* progress;      /* one word per workgroup */
     float* amax_v;           /* per-workgroup argmax partials */
     int* amax_i;
@@ -85,6 +85,16 @@ struct PkStep {
 __host__ __device__ constexpr int pk_att_steps(int nrep)
 {
     return nrep > 4 ? 4 : 8;
+}
+
+/* query heads per attention unit: one.  A unit (query head, kv head,
+ * chunk) carries 1/NREP of the group's arithmetic (the work of a unit is
+ * lane arithmetic, not memory), so NREP times as many workgroups share the
+ * phase; the NREP units that read the same K/V rows are ordered onto the
+ * same XCD, whose L2 serves the repeats. */
+__host__ __device__ constexpr int pk_att_nq(int)
+{
+    return 1;
 }
 
 __host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nrep, int* chunk_out, int* nch_out)

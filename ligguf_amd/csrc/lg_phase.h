@@ -570,20 +570,20 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
     m = mn;
 }
 
-/* Attention units (kv head g, chunk c of positions [c*chunk, ...) <= pos),
- * split by pk_attn_split.  A unit issues all its loads at once -- the q/k/v
- * heads of g and every K and V slice of its (at most pk_att_steps) steps,
- * held in registers -- so it costs one memory round trip (with a dependency
- * wait, the loads follow it).  Then QK-norm +
+/* Attention units (NQ query heads of kv head g, chunk c of positions
+ * [c*chunk, ...) <= pos), split by pk_attn_split.  A unit issues all its
+ * loads at once -- its q heads, k and v of g, and every K and V slice of its
+ * (at most pk_att_steps) steps, held in registers -- so it costs one memory
+ * round trip (with a dependency wait, the loads follow it).  Then QK-norm +
  * RoPE of the heads into LDS, and one pass over the positions with an
  * online softmax per lane group in log2 units (LPP lanes hold one position,
- * 8 dims each); the lane groups of a wave combine by shuffles, the waves in
- * LDS.  Output: the unit's unnormalised partial (o, and (m, l) per head),
- * merged by the consumer's build (MergeSrc); past PK_ATT_MERGE chunks per
- * head the last unit of the head (atomic counter) merges them into the
- * layer's merged slot.  The unit of the head's last chunk also writes the fp16 cache
+ * 8 dims each); the lane groups of a wave combine by lane permutes, the
+ * waves in LDS.  Output: the unit's unnormalised partial (o, and (m, l) per
+ * head), merged by the consumer's build (MergeSrc); past PK_ATT_MERGE chunks
+ * the last unit of the heads (atomic counter) merges them into the layer's
+ * merged slot.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
-template <int HD, int NREP>
+template <int HD, int NREP, int NQ = pk_att_nq(NREP)>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
                                            uint64_t* tr)
@@ -592,14 +592,17 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     constexpr int PPW = 64 / LPP;          /* positions per wave step */
     constexpr int PPB = PK_WAVES * PPW;    /* positions per WG step */
     constexpr int MAXST = pk_att_steps(NREP);
-    constexpr int NH = (NREP + PK_WAVES) / PK_WAVES;   /* heads normed per wave: NREP q + 1 k */
+    constexpr int NSUB = NREP / NQ;       /* units per (kv head, chunk) */
+    constexpr int NH = (NQ + PK_WAVES) / PK_WAVES;     /* heads normed per wave: NQ q + 1 k */
     static_assert(PPB == PK_THREADS * 8 / HD, "step geometry of pk_attn_split");
+    static_assert(NREP % NQ == 0, "query heads per unit divide the group");
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int gl = lane & (LPP - 1), grp = lane / LPP;
     const int kvd = P.kv_dim;
     int chunk, nch;
     pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
-    const int nunits = P.n_kv * nch;
+    const int ngc = P.n_kv * nch;           /* (kv head, chunk) pairs */
+    const int nunits = ngc * NSUB;
     const size_t loff = (size_t)layer * P.n_ctx * kvd;
     const float scale2 = 1.44269504088896341f / sqrtf((float)HD);   /* log2(e) / sqrt(head_dim) */
     float* po = P.att_po + (size_t)layer * P.att_slots * P.n_embed;
@@ -611,11 +614,11 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 
     stamp(tr, 0);
     uint4 kb[MAXST], vb[MAXST];   /* K/V slices of the unit's steps (static indices only) */
-    float4 hx[NH], hv;            /* this wave's heads h = wave + PK_WAVES*j: q (h < NREP) or k, and v */
+    float4 hx[NH], hv;            /* this wave's heads h = wave + PK_WAVES*j: q (h < NQ) or k, and v */
     /* unconditional loads (see Rows): positions outside the unit and the
      * row pos itself (not in the cache yet) load the unit's first row */
     auto load_kv = [&](int u) {
-        const int g = u / nch, c = u % nch;
+        const int g = (u % ngc) / nch, c = (u % ngc) % nch;
         const int t0 = c * chunk, t1 = min(t0 + chunk, pos + 1);
 #pragma unroll
         for (int st = 0; st < MAXST; st++) {
@@ -633,13 +636,13 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     float4 ng[NH];
     float2 fr;
     auto load_heads = [&](int u) {
-        const int g = u / nch;
+        const int g = (u % ngc) / nch, q0 = g * NREP + (u / ngc) * NQ;
 #pragma unroll
         for (int j = 0; j < NH; j++) {
-            const int h = min(wave + PK_WAVES * j, NREP);
-            const float* srcp = h < NREP ? qkv + (size_t)(g * NREP + h) * HD : qkv + P.n_embed + (size_t)g * HD;
+            const int h = min(wave + PK_WAVES * j, NQ);
+            const float* srcp = h < NQ ? qkv + (size_t)(q0 + h) * HD : qkv + P.n_embed + (size_t)g * HD;
             hx[j] = *(const float4*)(srcp + l4);
-            const float* nwp = has_norm ? (h < NREP ? L.q_norm : L.k_norm) : P.rope_freq;
+            const float* nwp = has_norm ? (h < NQ ? L.q_norm : L.k_norm) : P.rope_freq;
             ng[j] = *(const float4*)(nwp + l4);
         }
         hv = *(const float4*)(qkv + P.n_embed + kvd + (size_t)g * HD + l4);
@@ -650,7 +653,11 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     if (!has) stamp(tr, 1);
 
     for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
-        const int g = u / nch, c = u % nch;
+        /* units ordered (q-head subset, kv head, chunk): the NSUB units that
+         * read the same K/V rows sit ngc apart, on the same XCD (and L2)
+         * when ngc is a multiple of 8 */
+        const int g = (u % ngc) / nch, c = (u % ngc) % nch, qsub = u / ngc;
+        const int q0 = g * NREP + qsub * NQ;   /* first query head of the unit */
         const int t0 = c * chunk;
         const int t1 = min(t0 + chunk, pos + 1);
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
@@ -660,21 +667,21 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
         *(float4*)(s_kv + HD + l4) = hv;
-        /* q heads g*NREP.., then k of g: normed/roped into LDS (waves past
+        /* q heads q0.., then k of g: normed/roped into LDS (waves past
          * the last head compute a copy and store nothing: the operands' loads
          * are used unconditionally and stay where they are issued) */
 #pragma unroll
         for (int j = 0; j < NH; j++) {
             const int h = wave + PK_WAVES * j;
-            const bool is_q = h < NREP;
+            const bool is_q = h < NQ;
             float e[4] = {hx[j].x, hx[j].y, hx[j].z, hx[j].w};
             norm_rope_head<HD>(e, has_norm, ng[j], P.eps, P.rope_dim, pos, fr);
-            if (h <= NREP) {
+            if (h <= NQ) {
                 if (4 * lane < HD) {
                     float* dst = is_q ? s_q + h * HD : s_kv;
                     *(float4*)(dst + 4 * lane) = make_float4(e[0], e[1], e[2], e[3]);
                     if (!is_q) {
-                        if (c == nch - 1) {
+                        if (c == nch - 1 && qsub == 0) {
                             /* fp16 KV row pos (fast/ligguf_fast_qk.cpp:57-62), read from the next token on */
                             const size_t o = loff + (size_t)pos * kvd + (size_t)g * HD + 4 * lane;
                             const uint32_t klo = (uint32_t)lg_f2h(e[0]) | ((uint32_t)lg_f2h(e[1]) << 16);
@@ -692,7 +699,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         if (u == (int)blockIdx.x) stamp(tr, 1);
         /* q in registers; with 8 query heads per KV head it is re-read from
          * LDS each step (registers go to K/V and the accumulators) */
-        constexpr int QREG = NREP <= 4 ? NREP : 1;
+        constexpr int QREG = NQ <= 4 ? NQ : 1;
         float qr[QREG][8];
 #pragma unroll
         for (int r = 0; r < QREG; r++)
@@ -701,9 +708,9 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 
         /* one pass: scores, online softmax, p.V (t == pos uses the fp32 k/v
          * of this step, fast/ligguf_fast_qk.cpp:77-79,98-99) */
-        float m[NREP], l[NREP], o[NREP][8];
+        float m[NQ], l[NQ], o[NQ][8];
 #pragma unroll
-        for (int r = 0; r < NREP; r++) {
+        for (int r = 0; r < NQ; r++) {
             m[r] = -INFINITY;
             l[r] = 0.0f;
 #pragma unroll
@@ -722,10 +729,10 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
                 }
 #pragma unroll
-                for (int r = 0; r < NREP; r++) {
+                for (int r = 0; r < NQ; r++) {
                     float qv[8];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) qv[i] = NREP <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HD + gl * 8 + i];
+                    for (int i = 0; i < 8; i++) qv[i] = NQ <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HD + gl * 8 + i];
                     float sc = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];
@@ -747,7 +754,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 #pragma unroll
         for (int step = 0; step < 2; step++) {
 #pragma unroll
-            for (int r = 0; r < NREP; r++) {
+            for (int r = 0; r < NQ; r++) {
                 float o2[8];
 #pragma unroll
                 for (int i = 0; i < 8; i++) o2[i] = step ? lg_from_half_above(o[r][i]) : lg_from_row_above(o[r][i]);
@@ -758,23 +765,23 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         }
         if (grp == 0) {
 #pragma unroll
-            for (int r = 0; r < NREP; r++) {
+            for (int r = 0; r < NQ; r++) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) s_o[(wave * NREP + r) * HD + gl * 8 + i] = o[r][i];
-                if (gl == 0) { s_m[wave * NREP + r] = m[r]; s_sc[wave * NREP + r] = l[r]; }
+                for (int i = 0; i < 8; i++) s_o[(wave * NQ + r) * HD + gl * 8 + i] = o[r][i];
+                if (gl == 0) { s_m[wave * NQ + r] = m[r]; s_sc[wave * NQ + r] = l[r]; }
             }
         }
         bar();
-        for (int i = LG_TID; i < NREP * HD; i += PK_THREADS) {
-            const int r = i / HD, d = i % HD, q = g * NREP + r;
+        for (int i = LG_TID; i < NQ * HD; i += PK_THREADS) {
+            const int r = i / HD, d = i % HD, q = q0 + r;
             float M = -INFINITY;
-            for (int w = 0; w < PK_WAVES; w++) M = fmaxf(M, s_m[w * NREP + r]);
+            for (int w = 0; w < PK_WAVES; w++) M = fmaxf(M, s_m[w * NQ + r]);
             float O = 0.0f, Ls = 0.0f;
             for (int w = 0; w < PK_WAVES; w++) {
-                const float mw = s_m[w * NREP + r];
+                const float mw = s_m[w * NQ + r];
                 const float wt = mw == -INFINITY ? 0.0f : lg_exp2(mw - M);
-                O += s_o[(w * NREP + r) * HD + d] * wt;
-                Ls += s_sc[w * NREP + r] * wt;
+                O += s_o[(w * NQ + r) * HD + d] * wt;
+                Ls += s_sc[w * NQ + r] * wt;
             }
             cst(&po[(size_t)c * P.n_embed + (size_t)q * HD + d], O);
             if (d == 0) {
@@ -786,38 +793,38 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
             wait_stores();
             bar();
             if (LG_TID == 0) {
-                const uint32_t old = __hip_atomic_fetch_add(&P.attn_cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t old = __hip_atomic_fetch_add(&P.attn_cnt[g * NSUB + qsub], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 s_int[0] = old == (uint32_t)(nch - 1);
             }
             bar();
             if (s_int[0]) {
-                /* last unit of head group g: merge its nch partials, weights
+                /* last unit of these heads: merge their nch partials, weights
                  * through LDS, each thread one output value over the chunks
                  * with 8 loads in flight (the consumer's formula) */
-                float* s_ml = s_sc;                                   /* [nch][NREP][2] */
-                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NREP] */
-                for (int i = LG_TID; i < nch * NREP; i += PK_THREADS) {
-                    const float2 v = cld2(&pml[((size_t)(i / NREP) * P.n_heads + g * NREP + i % NREP) * 2]);
+                float* s_ml = s_sc;                                   /* [nch][NQ][2] */
+                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NQ] */
+                for (int i = LG_TID; i < nch * NQ; i += PK_THREADS) {
+                    const float2 v = cld2(&pml[((size_t)(i / NQ) * P.n_heads + q0 + i % NQ) * 2]);
                     s_ml[2 * i] = v.x;
                     s_ml[2 * i + 1] = v.y;
                 }
                 bar();
-                if (LG_TID < NREP) {
+                if (LG_TID < NQ) {
                     const int r = LG_TID;
                     float M = -INFINITY;
-                    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NREP + r) * 2]);
+                    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NQ + r) * 2]);
                     float Ls = 0.0f;
                     for (int cc = 0; cc < nch; cc++) {
-                        const float wgt = lg_exp2(s_ml[(cc * NREP + r) * 2] - M);
-                        s_w[cc * NREP + r] = wgt;
-                        Ls += s_ml[(cc * NREP + r) * 2 + 1] * wgt;
+                        const float wgt = lg_exp2(s_ml[(cc * NQ + r) * 2] - M);
+                        s_w[cc * NQ + r] = wgt;
+                        Ls += s_ml[(cc * NQ + r) * 2 + 1] * wgt;
                     }
                     s_red[r] = Ls;
                 }
                 bar();
-                for (int i = LG_TID; i < NREP * HD; i += PK_THREADS) {
+                for (int i = LG_TID; i < NQ * HD; i += PK_THREADS) {
                     const int r = i / HD;
-                    const float* col = po + (size_t)g * NREP * HD + i;
+                    const float* col = po + (size_t)q0 * HD + i;
                     float acc = 0.0f;
                     for (int c0 = 0; c0 < nch; c0 += 8) {
                         float v[8];
@@ -825,16 +832,16 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                         for (int k = 0; k < 8; k++) v[k] = c0 + k < nch ? cld(col + (size_t)(c0 + k) * P.n_embed) : 0.0f;
 #pragma unroll
                         for (int k = 0; k < 8; k++)
-                            if (c0 + k < nch) acc += v[k] * s_w[(c0 + k) * NREP + r];
+                            if (c0 + k < nch) acc += v[k] * s_w[(c0 + k) * NQ + r];
                     }
                     /* the merged vector as a one-chunk partial (m 0, l 1) */
-                    cst(&po_m[(size_t)g * NREP * HD + i], acc / s_red[r]);
+                    cst(&po_m[(size_t)q0 * HD + i], acc / s_red[r]);
                 }
-                if (LG_TID < NREP) {
-                    cst(&pml_m[(size_t)(g * NREP + LG_TID) * 2], 0.0f);
-                    cst(&pml_m[(size_t)(g * NREP + LG_TID) * 2 + 1], 1.0f);
+                if (LG_TID < NQ) {
+                    cst(&pml_m[(size_t)(q0 + LG_TID) * 2], 0.0f);
+                    cst(&pml_m[(size_t)(q0 + LG_TID) * 2 + 1], 1.0f);
                 }
-                if (LG_TID == 0) cst(&P.attn_cnt[g], 0u);
+                if (LG_TID == 0) cst(&P.attn_cnt[g * NSUB + qsub], 0u);
             }
         }
         bar();
