@@ -220,7 +220,8 @@ struct MergeAct {
                     O.x += o[c][k].x * w; O.y += o[c][k].y * w; O.z += o[c][k].z * w; O.w += o[c][k].w * w;
                 }
             }
-            a.v[k] = make_float4(O.x / Ls, O.y / Ls, O.z / Ls, O.w / Ls);
+            const float inv = 1.0f / Ls;
+            a.v[k] = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
         }
     }
 };
