@@ -25,6 +25,16 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+
+template <typename To, typename From>
+__device__ __forceinline__ To lg_bits(From v)
+{
+    static_assert(sizeof(To) == sizeof(From), "same size");
+    To t;
+    __builtin_memcpy(&t, &v, sizeof(To));
+    return t;
+}
 
 /* ------------------------------------------------------------------ */
 /* embedding rows, quantizers                                           */
@@ -226,171 +236,182 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
 /* ------------------------------------------------------------------ */
 /* Q4_K x Q8_K GEMM on int8 MFMA                                        */
 /* ------------------------------------------------------------------ */
-/* Workgroup tile: 32 tokens x 128 rows, 4 waves of 32 x 32 (2 x 2 MFMA
- * tiles of 16 x 16).  v_mfma_i32_16x16x32_i8 (layout checked on the part):
- * lane l holds A[token l%16][k 8(l/16)..+7], B[k 8(l/16)..+7][row l%16],
- * D[token 4(l/16)+i][row l%16] in register i.  In a Q4_K block, byte 32c+i
- * of qs holds value 64c+i (low nibble) and 64c+32+i (high nibble), so lane
- * group g takes bytes 32c+8g..+7 of its row: the low nibbles are its 8
- * values of sub-block 2c, the high ones of sub-block 2c+1; the activation
- * bytes 64c+8g and 64c+32+8g match them.  The token tile of each block is
- * staged in LDS (16-byte loads, double-buffered) and shared by the 4 waves;
- * each wave reads its rows' bytes straight from the GGUF rows.  Rows and
- * tokens past the ends are clamped for the loads and not stored. */
+/* Workgroup tile: 128 tokens x 128 rows, 8 waves of 128 tokens x 16 rows
+ * (8 MFMA tiles of 16 x 16 per wave: a wave's weight operands, unpacked
+ * once per sub-block, feed 16 MFMAs).  v_mfma_i32_16x16x32_i8 (layout
+ * checked on the part): lane l holds A[token l%16][k 8(l/16)..+7],
+ * B[k 8(l/16)..+7][row l%16], D[token 4(l/16)+i][row l%16] in register i.
+ * In a Q4_K block, byte 32c+i of qs holds value 64c+i (low nibble) and
+ * 64c+32+i (high nibble), so lane group g takes bytes 32c+8g..+7 of its
+ * row: the low nibbles are its 8 values of sub-block 2c, the high ones of
+ * sub-block 2c+1; the activation bytes 64c+8g and 64c+32+8g match them.
+ *
+ * S = sum_j sc_j isum_j over the 8 sub-blocks with sc_j = 8 h_j + l_j
+ * (h, l < 8): the weights scaled by h_j and by l_j still fit int8
+ * (q h <= 105), so both sums accumulate inside the MFMA over the whole
+ * block and S = 8 S_h + S_l exactly, with no per-sub-block readback.  A
+ * packed 16-bit multiply scales four q bytes at once (every product is
+ * below 256, so no carry crosses a byte).
+ *
+ * Per 256-value block the token tile's quants, bsums and block scales are
+ * staged in LDS (double-buffered, rows padded to 272 B against bank
+ * conflicts) and shared by the 4 waves; each wave reads its rows' bytes
+ * straight from the GGUF rows, one block ahead.  Rows and tokens past the
+ * ends are clamped for the loads and not stored.  The grid is one
+ * dimension: (row block, token tile) from the index, XCD-aware. */
+#define PF_TT 128              /* tokens per workgroup */
+#define PF_RB 128              /* rows per workgroup: 8 waves of 16 */
+#define PF_AST 272             /* LDS row stride of the staged quants */
 template <int ACC>
-__global__ __launch_bounds__(256) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
+__global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
                                                      PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    __shared__ __attribute__((aligned(16))) int8_t s_a[2][32 * 256];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][PF_TT * PF_AST];
+    __shared__ __attribute__((aligned(16))) int16_t s_bs[2][PF_TT * 16];
+    __shared__ __attribute__((aligned(16))) float s_d[2][PF_TT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, l16 = lane & 15;
     const int nb = K >> 8;
-    const int t0 = blockIdx.y * 32;
-    const int r0 = blockIdx.x * 128 + wave * 32;
-    const uint8_t* wr[2];
-#pragma unroll
-    for (int ni = 0; ni < 2; ni++) wr[ni] = W + (size_t)min(r0 + 16 * ni + l16, R - 1) * rsz;
-    int ta[2];   /* the lane's A tokens (M-term operand): t0 + 16 mi + l16 */
-#pragma unroll
-    for (int mi = 0; mi < 2; mi++) ta[mi] = min(t0 + 16 * mi + l16, T - 1);
-    /* staging: thread -> (token 16k + tid/16, 16-byte chunk tid%16) */
-    const int st_tok = threadIdx.x >> 4, st_ch = threadIdx.x & 15;
-    const int8_t* st_src[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) st_src[k] = x.qs + (size_t)min(t0 + st_tok + 16 * k, T - 1) * K + st_ch * 16;
+    /* tile of this workgroup: workgroups go to the 8 XCDs round-robin by
+     * index, so the token tiles of one row block get indices 8 apart -- one
+     * XCD, dispatched together -- and its weight bytes come from HBM once
+     * and from that XCD's L2 for the other token tiles */
+    const int nt = (T + PF_TT - 1) / PF_TT;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int rb = (slot / nt) * 8 + xcd;
+    if (rb * PF_RB >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
+    const int t0 = (slot % nt) * PF_TT;
+    const int r0 = rb * PF_RB + wave * 16;
+    const uint8_t* wr = W + (size_t)min(r0 + l16, R - 1) * rsz;
 
-    uint4 st[2];
-    auto stage_load = [&](int b) {
-#pragma unroll
-        for (int k = 0; k < 2; k++) st[k] = *(const uint4*)(st_src[k] + (size_t)b * 256);
+    /* staging, per block: thread tid takes quant chunks tid + 512 i (token
+     * chunk/16, 16-byte piece chunk%16), one 8-byte quarter of a token's
+     * bsums (token tid/4) and, threads < 32, four block scales */
+    struct Stg {
+        uint4 a[4];
+        uint2 bs;
+        uint4 d;
     };
-    auto stage_store = [&](int buf) {
+    auto stage_load = [&](Stg& st, int b) {
 #pragma unroll
-        for (int k = 0; k < 2; k++) *(uint4*)(s_a[buf] + (st_tok + 16 * k) * 256 + st_ch * 16) = st[k];
+        for (int i = 0; i < 4; i++) {
+            const int q = tid + 512 * i, tok = min(t0 + (q >> 4), T - 1);
+            st.a[i] = *(const uint4*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
+        }
+        const int tb = min(t0 + (tid >> 2), T - 1);
+        st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
+        st.d = *(const uint4*)(x.d + (size_t)b * x.tld + min(t0 + 4 * (tid & 31), x.tld - 4));
     };
-    /* per-block operands of the wave, loaded one block ahead */
+    auto stage_store = [&](const Stg& st, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = tid + 512 * i;
+            *(uint4*)(s_a[buf] + (q >> 4) * PF_AST + (q & 15) * 16) = st.a[i];
+        }
+        *(uint2*)(s_bs[buf] + (tid >> 2) * 16 + (tid & 3) * 4) = st.bs;
+        if (tid < 32) *(uint4*)(s_d[buf] + 4 * tid) = st.d;
+    };
+    /* the wave's weight operands of one block */
     struct Blk {
-        uint4 hdr[2];
-        uint2 wq[2][4];
-        int bsp[2][2];    /* bsums of the M-term A operand: [mi][kc] two int16 */
-        float4 dx[2];     /* d of the 4 output tokens 4g..4g+3 of tile mi */
+        uint4 hdr;
+        uint2 wq[4];
     };
     auto blk_load = [&](Blk& B, int b) {
+        const uint8_t* p = wr + (size_t)b * LG_BS_Q4_K;
+        B.hdr = *(const uint4*)p;
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const uint8_t* p = wr[ni] + (size_t)b * LG_BS_Q4_K;
-            B.hdr[ni] = *(const uint4*)p;
-#pragma unroll
-            for (int c = 0; c < 4; c++) B.wq[ni][c] = *(const uint2*)(p + 16 + 32 * c + 8 * g);
-        }
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const int16_t* bs = x.bs + ((size_t)ta[mi] * nb + b) * 16;
-#pragma unroll
-            for (int kc = 0; kc < 2; kc++) B.bsp[mi][kc] = *(const int*)(bs + 2 * (g + 4 * kc));
-            B.dx[mi] = *(const float4*)(x.d + (size_t)b * x.tld + min(t0 + 16 * mi + 4 * g, x.tld - 4));
-        }
+        for (int c = 0; c < 4; c++) B.wq[c] = *(const uint2*)(p + 16 + 32 * c + 8 * g);
     };
 
-    v4f acc[2][2];
+    v4f acc[8];
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 2; ni++) acc[mi][ni] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int mi = 0; mi < 8; mi++) acc[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    Blk cur, nxt;
-    stage_load(0);
-    blk_load(cur, 0);
-    stage_store(0);
-    __syncthreads();
-    for (int b = 0; b < nb; b++) {
-        const int bn = min(b + 1, nb - 1);
-        stage_load(bn);
-        blk_load(nxt, bn);
-        const int8_t* sa = s_a[b & 1];
-
-        /* scales of the lane's two rows (get_scale_min_k4, fast/lil_math.cpp:129-138) */
-        uint32_t scq[2][2];   /* [ni][lo/hi]: sc_j of sub-blocks 0-3 / 4-7, one per byte */
-        float mb[2][2], dw[2], dmw[2];
+    auto compute = [&](int b, const Blk& cur) {
+        const int buf = b & 1;
+        /* scales of the lane's row (get_scale_min_k4, fast/lil_math.cpp:129-138) */
+        const uint4 h4 = cur.hdr;
+        const uint32_t scq[2] = {h4.y & 0x3F3F3F3Fu, (h4.w & 0x0F0F0F0Fu) | ((h4.y >> 2) & 0x30303030u)};
+        const uint32_t mlo = h4.z & 0x3F3F3F3Fu;
+        const uint32_t mhi = ((h4.w >> 4) & 0x0F0F0F0Fu) | ((h4.z >> 2) & 0x30303030u);
+        const float mb0 = (float)((mlo >> (8 * g)) & 0xFFu);   /* m_j, j = g */
+        const float mb1 = (float)((mhi >> (8 * g)) & 0xFFu);   /* m_j, j = g + 4 */
+        const float dw = lg_h2f((uint16_t)(h4.x & 0xffffu));
+        const float dmw = lg_h2f((uint16_t)(h4.x >> 16));
+        v4i Sh[8], Sl[8];
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const uint4 h = cur.hdr[ni];
-            scq[ni][0] = h.y & 0x3F3F3F3Fu;
-            scq[ni][1] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
-            const uint32_t mlo = h.z & 0x3F3F3F3Fu;
-            const uint32_t mhi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
-            mb[ni][0] = (float)((mlo >> (8 * g)) & 0xFFu);   /* m_j, j = g */
-            mb[ni][1] = (float)((mhi >> (8 * g)) & 0xFFu);   /* m_j, j = g + 4 */
-            dw[ni] = lg_h2f((uint16_t)(h.x & 0xffffu));
-            dmw[ni] = lg_h2f((uint16_t)(h.x >> 16));
-        }
-        v4i S[2][2];
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-            for (int ni = 0; ni < 2; ni++) S[mi][ni] = (v4i){0, 0, 0, 0};
+        for (int mi = 0; mi < 8; mi++) Sh[mi] = Sl[mi] = (v4i){0, 0, 0, 0};
+        const int8_t* sa = s_a[buf] + l16 * PF_AST + 8 * g;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int j = 2 * c + h;
-                long bf[2], af[2];
+                const uint2 q = cur.wq[c];
+                const uint32_t lo = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+                const uint32_t hi = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+                const uint32_t sc = (scq[j >> 2] >> (8 * (j & 3))) & 0x3Fu;
+                const v2u16 sh = (v2u16)(uint16_t)(sc >> 3), sl = (v2u16)(uint16_t)(sc & 7u);
+                const long bh = (long)((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sh) |
+                                       ((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sh) << 32));
+                const long bl = (long)((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sl) |
+                                       ((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sl) << 32));
 #pragma unroll
-                for (int ni = 0; ni < 2; ni++) {
-                    const uint2 q = cur.wq[ni][c];
-                    const uint32_t lo = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
-                    const uint32_t hi = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-                    bf[ni] = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                for (int mi = 0; mi < 8; mi++) {
+                    const long af = *(const long*)(sa + 16 * mi * PF_AST + 64 * c + 32 * h);
+                    Sh[mi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bh, Sh[mi], 0, 0, 0);
+                    Sl[mi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bl, Sl[mi], 0, 0, 0);
                 }
-#pragma unroll
-                for (int mi = 0; mi < 2; mi++) af[mi] = *(const long*)(sa + (16 * mi + l16) * 256 + 64 * c + 32 * h + 8 * g);
-#pragma unroll
-                for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-                    for (int ni = 0; ni < 2; ni++) {
-                        const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[mi], bf[ni], (v4i){0, 0, 0, 0}, 0, 0, 0);
-                        const int sc = (int)((scq[ni][j >> 2] >> (8 * (j & 3))) & 0xFFu);
-                        S[mi][ni] += sc * is;
-                    }
             }
         }
-        /* mins term and the block's fp32 contribution */
+        /* mins term M[token][row] = sum_j m_j (bsums_2j + bsums_2j+1) on the
+         * fp32 MFMA (k = g: sub-blocks g and g + 4), and the block's fp32
+         * contribution acc += d_a (d_w S - dmin_w M) */
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            float bpa[2];
+        for (int mi = 0; mi < 8; mi++) {
+            const int16_t* bsr = s_bs[buf] + (16 * mi + l16) * 16;
+            const int v0 = *(const int*)(bsr + 2 * g), v1 = *(const int*)(bsr + 2 * (g + 4));
+            const float bpa0 = (float)((int)(int16_t)(v0 & 0xffff) + (int)(int16_t)(v0 >> 16));
+            const float bpa1 = (float)((int)(int16_t)(v1 & 0xffff) + (int)(int16_t)(v1 >> 16));
+            v4f M = __builtin_amdgcn_mfma_f32_16x16x4f32(bpa0, mb0, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            M = __builtin_amdgcn_mfma_f32_16x16x4f32(bpa1, mb1, M, 0, 0, 0);
+            const float4 dx = *(const float4*)(s_d[buf] + 16 * mi + 4 * g);
+            const v4i S = Sh[mi] * 8 + Sl[mi];
+            const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-            for (int kc = 0; kc < 2; kc++) {
-                const int v = cur.bsp[mi][kc];
-                bpa[kc] = (float)((int)(int16_t)(v & 0xffff) + (int)(int16_t)(v >> 16));
-            }
-            const float dx[4] = {cur.dx[mi].x, cur.dx[mi].y, cur.dx[mi].z, cur.dx[mi].w};
-#pragma unroll
-            for (int ni = 0; ni < 2; ni++) {
-                v4f M = __builtin_amdgcn_mfma_f32_16x16x4f32(bpa[0], mb[ni][0], (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                M = __builtin_amdgcn_mfma_f32_16x16x4f32(bpa[1], mb[ni][1], M, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[mi][ni][i] += dx[i] * (dw[ni] * (float)S[mi][ni][i] - dmw[ni] * M[i]);
-            }
+            for (int i = 0; i < 4; i++)
+                acc[mi][i] = __builtin_fmaf(dxs[i], lg_fma2(dw, (float)S[i], -dmw, M[i]), acc[mi][i]);
         }
-        stage_store((b + 1) & 1);
+    };
+
+    /* one block ahead: block b+1's operands load while block b computes */
+    Blk cur, nxt;
+    Stg st;
+    stage_load(st, 0);
+    blk_load(cur, 0);
+    stage_store(st, 0);
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        const int bn = min(b + 1, nb - 1);
+        stage_load(st, bn);
+        blk_load(nxt, bn);
+        compute(b, cur);
+        stage_store(st, (b + 1) & 1);
         cur = nxt;
         __syncthreads();
     }
+    const int r = r0 + l16;
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
+    for (int mi = 0; mi < 8; mi++) {
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const int r = r0 + 16 * ni + l16;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = t0 + 16 * mi + 4 * g + i;
-                if (t < T && r < R) {
-                    float* o = out + (size_t)t * ldo + r;
-                    *o = ACC ? *o + acc[mi][ni][i] : acc[mi][ni][i];
-                }
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 16 * mi + 4 * g + i;
+            if (t < T && r < R) {
+                float* o = out + (size_t)t * ldo + r;
+                *o = ACC ? *o + acc[mi][i] : acc[mi][i];
             }
         }
+    }
 }
 
 /* ------------------------------------------------------------------ */
@@ -404,7 +425,8 @@ int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
         lg_set_error("prefill gemm: bad arguments (rows %d, cols %d, T %d)", rows, cols, T);
         return LG_ERR_ARG;
     }
-    const dim3 grid((rows + 127) / 128, (T + 31) / 32), blk(256);
+    const int nrb = (rows + PF_RB - 1) / PF_RB, nt = (T + PF_TT - 1) / PF_TT;
+    const dim3 grid((unsigned)((nrb + 7) / 8 * 8 * nt)), blk(512);
     if (accumulate) hipLaunchKernelGGL(k_pf_gemm_q4k<1>, grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     else hipLaunchKernelGGL(k_pf_gemm_q4k<0>, grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     return lg_check_launch("prefill gemm");
