@@ -236,9 +236,9 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
 /* ------------------------------------------------------------------ */
 /* Q4_K x Q8_K GEMM on int8 MFMA                                        */
 /* ------------------------------------------------------------------ */
-/* Workgroup tile: 128 tokens x 128 rows, 8 waves of 128 tokens x 16 rows
- * (8 MFMA tiles of 16 x 16 per wave: a wave's weight operands, unpacked
- * once per sub-block, feed 16 MFMAs).  v_mfma_i32_16x16x32_i8 (layout
+/* Workgroup tile: 16 MI tokens x 128 rows, 8 waves of 16 MI tokens x 16
+ * rows (MI MFMA tiles of 16 x 16 per wave: a wave's weight operands,
+ * unpacked once per sub-block, feed 2 MI MFMAs).  v_mfma_i32_16x16x32_i8 (layout
  * checked on the part): lane l holds A[token l%16][k 8(l/16)..+7],
  * B[k 8(l/16)..+7][row l%16], D[token 4(l/16)+i][row l%16] in register i.
  * In a Q4_K block, byte 32c+i of qs holds value 64c+i (low nibble) and
@@ -259,16 +259,16 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
  * straight from the GGUF rows, one block ahead.  Rows and tokens past the
  * ends are clamped for the loads and not stored.  The grid is one
  * dimension: (row block, token tile) from the index, XCD-aware. */
-#define PF_TT 128              /* tokens per workgroup */
 #define PF_RB 128              /* rows per workgroup: 8 waves of 16 */
 #define PF_AST 272             /* LDS row stride of the staged quants */
-template <int ACC>
+/* MI token tiles of 16 per workgroup */
+template <int ACC, int MI>
 __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
                                                      PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    __shared__ __attribute__((aligned(16))) int8_t s_a[2][PF_TT * PF_AST];
-    __shared__ __attribute__((aligned(16))) int16_t s_bs[2][PF_TT * 16];
-    __shared__ __attribute__((aligned(16))) float s_d[2][PF_TT];
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][(16 * MI) * PF_AST];
+    __shared__ __attribute__((aligned(16))) int16_t s_bs[2][(16 * MI) * 16];
+    __shared__ __attribute__((aligned(16))) float s_d[2][(16 * MI)];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, l16 = lane & 15;
     const int nb = K >> 8;
@@ -276,40 +276,42 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
      * index, so the token tiles of one row block get indices 8 apart -- one
      * XCD, dispatched together -- and its weight bytes come from HBM once
      * and from that XCD's L2 for the other token tiles */
-    const int nt = (T + PF_TT - 1) / PF_TT;
+    const int nt = (T + (16 * MI) - 1) / (16 * MI);
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int rb = (slot / nt) * 8 + xcd;
     if (rb * PF_RB >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
-    const int t0 = (slot % nt) * PF_TT;
+    const int t0 = (slot % nt) * (16 * MI);
     const int r0 = rb * PF_RB + wave * 16;
     const uint8_t* wr = W + (size_t)min(r0 + l16, R - 1) * rsz;
 
     /* staging, per block: thread tid takes quant chunks tid + 512 i (token
      * chunk/16, 16-byte piece chunk%16), one 8-byte quarter of a token's
-     * bsums (token tid/4) and, threads < 32, four block scales */
+     * bsums (token tid/4, threads < 64 MI) and, threads < 4 MI, four block
+     * scales */
+    constexpr int NA = MI / 2;   /* quant chunks per thread: 16 MI tokens x 16 / 512 */
     struct Stg {
-        uint4 a[4];
+        uint4 a[NA];
         uint2 bs;
         uint4 d;
     };
     auto stage_load = [&](Stg& st, int b) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NA; i++) {
             const int q = tid + 512 * i, tok = min(t0 + (q >> 4), T - 1);
             st.a[i] = *(const uint4*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
         }
-        const int tb = min(t0 + (tid >> 2), T - 1);
+        const int tb = min(t0 + ((tid >> 2) & (16 * MI - 1)), T - 1);
         st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
-        st.d = *(const uint4*)(x.d + (size_t)b * x.tld + min(t0 + 4 * (tid & 31), x.tld - 4));
+        st.d = *(const uint4*)(x.d + (size_t)b * x.tld + min(t0 + 4 * (tid & (4 * MI - 1)), x.tld - 4));
     };
     auto stage_store = [&](const Stg& st, int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NA; i++) {
             const int q = tid + 512 * i;
             *(uint4*)(s_a[buf] + (q >> 4) * PF_AST + (q & 15) * 16) = st.a[i];
         }
-        *(uint2*)(s_bs[buf] + (tid >> 2) * 16 + (tid & 3) * 4) = st.bs;
-        if (tid < 32) *(uint4*)(s_d[buf] + 4 * tid) = st.d;
+        if (tid < 64 * MI) *(uint2*)(s_bs[buf] + (tid >> 2) * 16 + (tid & 3) * 4) = st.bs;
+        if (tid < 4 * MI) *(uint4*)(s_d[buf] + 4 * tid) = st.d;
     };
     /* the wave's weight operands of one block */
     struct Blk {
@@ -323,9 +325,9 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
         for (int c = 0; c < 4; c++) B.wq[c] = *(const uint2*)(p + 16 + 32 * c + 8 * g);
     };
 
-    v4f acc[8];
+    v4f acc[MI];
 #pragma unroll
-    for (int mi = 0; mi < 8; mi++) acc[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int mi = 0; mi < MI; mi++) acc[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](int b, const Blk& cur) {
         const int buf = b & 1;
@@ -338,9 +340,9 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
         const float mb1 = (float)((mhi >> (8 * g)) & 0xFFu);   /* m_j, j = g + 4 */
         const float dw = lg_h2f((uint16_t)(h4.x & 0xffffu));
         const float dmw = lg_h2f((uint16_t)(h4.x >> 16));
-        v4i Sh[8], Sl[8];
+        v4i Sh[MI], Sl[MI];
 #pragma unroll
-        for (int mi = 0; mi < 8; mi++) Sh[mi] = Sl[mi] = (v4i){0, 0, 0, 0};
+        for (int mi = 0; mi < MI; mi++) Sh[mi] = Sl[mi] = (v4i){0, 0, 0, 0};
         const int8_t* sa = s_a[buf] + l16 * PF_AST + 8 * g;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -357,7 +359,7 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
                 const long bl = (long)((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sl) |
                                        ((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sl) << 32));
 #pragma unroll
-                for (int mi = 0; mi < 8; mi++) {
+                for (int mi = 0; mi < MI; mi++) {
                     const long af = *(const long*)(sa + 16 * mi * PF_AST + 64 * c + 32 * h);
                     Sh[mi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bh, Sh[mi], 0, 0, 0);
                     Sl[mi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bl, Sl[mi], 0, 0, 0);
@@ -368,7 +370,7 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
          * fp32 MFMA (k = g: sub-blocks g and g + 4), and the block's fp32
          * contribution acc += d_a (d_w S - dmin_w M) */
 #pragma unroll
-        for (int mi = 0; mi < 8; mi++) {
+        for (int mi = 0; mi < MI; mi++) {
             const int16_t* bsr = s_bs[buf] + (16 * mi + l16) * 16;
             const int v0 = *(const int*)(bsr + 2 * g), v1 = *(const int*)(bsr + 2 * (g + 4));
             const float bpa0 = (float)((int)(int16_t)(v0 & 0xffff) + (int)(int16_t)(v0 >> 16));
@@ -402,7 +404,7 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
     }
     const int r = r0 + l16;
 #pragma unroll
-    for (int mi = 0; mi < 8; mi++) {
+    for (int mi = 0; mi < MI; mi++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = t0 + 16 * mi + 4 * g + i;
@@ -425,10 +427,13 @@ int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
         lg_set_error("prefill gemm: bad arguments (rows %d, cols %d, T %d)", rows, cols, T);
         return LG_ERR_ARG;
     }
-    const int nrb = (rows + PF_RB - 1) / PF_RB, nt = (T + PF_TT - 1) / PF_TT;
-    const dim3 grid((unsigned)((nrb + 7) / 8 * 8 * nt)), blk(512);
-    if (accumulate) hipLaunchKernelGGL(k_pf_gemm_q4k<1>, grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
-    else hipLaunchKernelGGL(k_pf_gemm_q4k<0>, grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    /* 64-token tiles: 128 VGPRs, so up to four workgroups share a CU (at
+     * 128 tokens a workgroup needs 220 and the 512-token up|gate GEMM ran 10%
+     * slower) */
+    const int nrb8 = (rows + PF_RB - 1) / PF_RB + 7 & ~7;
+    const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
+    if (accumulate) hipLaunchKernelGGL((k_pf_gemm_q4k<1, 4>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    else hipLaunchKernelGGL((k_pf_gemm_q4k<0, 4>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     return lg_check_launch("prefill gemm");
 }
 
