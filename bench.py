@@ -89,6 +89,96 @@ def plain_copy(torch, nbytes: int = 256 << 20, reps: int = 20):
     return {"bytes_each_way": nbytes, "avg_us": round(avg_s * 1e6, 2), "GB/s": round(2 * nbytes / avg_s / 1e9, 1)}
 
 
+MFMA_INT8_PEAK = 5.0e15    # MI355X dense int8, ops/s
+
+
+def prefill_report(cfg, tokens: int, seconds: float, path: int):
+    """Prefill throughput against two bounds: the HBM roofline of one pass
+    (every layer matrix read once per pass of <= 512 tokens) and the int8
+    MFMA peak for the pass's GEMM work (2 ops per weight x token)."""
+    from ligguf_amd.lib import PREFILL_BATCHED, row_size
+    passes = (tokens + 511) // 512
+    head = cfg.vocab * row_size(cfg.out_type, cfg.n_embed)      # the output head, once (last token)
+    hbm = passes * (cfg.weight_bytes() - head) + head
+    macs = cfg.n_layers * (cfg.n_embed + 2 * cfg.kv_dim + cfg.n_embed + 2 * cfg.n_ff + cfg.n_ff) * cfg.n_embed
+    ops = 2.0 * macs * tokens
+    return {"tok_s": round(tokens / seconds, 1), "tokens": tokens, "ms": round(seconds * 1e3, 2),
+            "path": "batched" if path == PREFILL_BATCHED else "steps",
+            "hbm_roofline_frac": round(hbm / seconds / HBM_PEAK, 4),
+            "gemm_int8_tops": round(ops / seconds / 1e12, 1),
+            "mfma_frac": round(ops / seconds / MFMA_INT8_PEAK, 4)}
+
+
+def _time_launches(torch, fn, reps: int) -> float:
+    """Mean wall time of fn() over reps launches (HIP events on the current stream), microseconds."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def isolated_kernels(torch, np):
+    """The isolated-kernel workloads: batch-1 quantized matvec (k_matvec)
+    for Q4_K 4096x4096, Q4_K 14336x4096 and Q6_K 128256x4096 (weights N(0,
+    0.02) through the reference quantizers, activation N(0,1) as Q8_K), each
+    cycled over enough distinct copies to exceed the 256 MB Infinity Cache;
+    and GQA decode attention (lg_attn_decode: 32 query / 8 KV heads of 128,
+    fp16 cache, the reference's KV format) at 512, 4096 and 32768 positions.
+    Rates are algorithmic bytes (weights + activation + output; K and V rows
+    read) per launch over the launch time."""
+    from ligguf_amd import ops
+    from ligguf_amd.encode import random_tensor
+    from ligguf_amd.lib import Q4_K, Q6_K, row_size
+    dev = "cuda:0"
+    out = {"matvec": [], "attention": []}
+    for t, name, rows, cols in ((Q4_K, "Q4_K", 4096, 4096), (Q4_K, "Q4_K", 14336, 4096), (Q6_K, "Q6_K", 128256, 4096)):
+        rsz = row_size(t, cols)
+        mbytes = rows * rsz
+        copies = max(1, -(-300_000_000 // mbytes))
+        w0 = torch.from_numpy(random_tensor(t, 7, 0, rows, cols)).to(dev)
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        x = torch.from_numpy(np.random.default_rng(3).standard_normal(cols).astype(np.float32)).to(dev)
+        xq = ops.quantize_q8_K(x)
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        k = [0]
+
+        def mv():
+            ops.matvec(t, ws[k[0] % copies], rsz, cols, rows, xq, y)
+            k[0] += 1
+        us = _time_launches(torch, mv, 10 * copies)
+        alg = mbytes + xq.numel() + 4 * rows
+        out["matvec"].append({"type": name, "shape": [rows, cols], "us": round(us, 2),
+                              "GB/s": round(alg / us / 1e3, 1), "frac": round(alg / (us * 1e-6) / HBM_PEAK, 4),
+                              "copies": copies})
+        del ws, w0
+    torch.cuda.empty_cache()
+    nh, nkv, hd = 32, 8, 128
+    rng = np.random.default_rng(5)
+    for ctx in (512, 4096, 32768):
+        kvd = nkv * hd
+        kc = torch.from_numpy(rng.standard_normal(ctx * kvd).astype(np.float16).view(np.uint16)).to(dev)
+        vc = torch.from_numpy(rng.standard_normal(ctx * kvd).astype(np.float16).view(np.uint16)).to(dev)
+        q = torch.from_numpy(rng.standard_normal(nh * hd).astype(np.float32)).to(dev)
+        kk = torch.from_numpy(rng.standard_normal(kvd).astype(np.float32)).to(dev)
+        vv = torch.from_numpy(rng.standard_normal(kvd).astype(np.float32)).to(dev)
+        pos = ctx - 1
+        wsz = max(16, ops.load().lg_attn_workspace_size(nh, hd, pos))
+        ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
+        us = _time_launches(torch, lambda: ops.attention(q, kk, vv, kc, vc, nh, nkv, hd, pos, ws), 50)
+        alg = pos * kvd * 2 * 2 + (nh * hd + 2 * kvd) * 4 + nh * hd * 4
+        out["attention"].append({"ctx": ctx, "us": round(us, 2), "GB/s": round(alg / us / 1e3, 1),
+                                 "frac": round(alg / (us * 1e-6) / HBM_PEAK, 4)})
+        del kc, vc
+    torch.cuda.empty_cache()
+    log(f"isolated: {out}")
+    return out
+
+
 def cpu_baseline(hm, seconds: float, max_tokens: int = 4000):
     """The reference FAST engine (oracle/_ref, AVX2, OpenMP) decoding the same
     host model from position 0 for about `seconds`."""
@@ -146,6 +236,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
+    ap.add_argument("--no-isolated", action="store_true", help="skip the isolated matvec/attention lines")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
     args = ap.parse_args()
@@ -182,11 +273,13 @@ def main() -> int:
 
     rng = np.random.default_rng(0)
     prompt = rng.integers(1, cfg.vocab, args.prefill).astype(np.int32)
+    eng.prefill(prompt, 0)                         # warm-up: first-use buffers and code objects
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    logits = eng.prefill(prompt, 0)
+    logits = eng.prefill(prompt, 0)                # the same rows again (KV positions 0.. rewritten)
     prefill_s = time.perf_counter() - t0
     log(f"prefill {args.prefill} tokens: {args.prefill / prefill_s:.1f} tok/s")
+    prefill = prefill_report(cfg, args.prefill, prefill_s, eng.prefill_path())
 
     pos = args.prefill
     tok = int(np.argmax(logits))
@@ -207,6 +300,8 @@ def main() -> int:
     tps = args.steps / dt
     mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
     log(f"decode: {tps:.1f} tok/s, {ms:.3f} ms/token, {mean_bytes / (dt / args.steps) / 1e9:.0f} GB/s per token")
+
+    isolated = None if args.no_isolated else isolated_kernels(torch, np)
 
     roof = None
     if not args.no_kernel and path_name == "fused-graph":
@@ -242,8 +337,10 @@ def main() -> int:
         },
         "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) / HBM_PEAK, 4),
         "prefill_tok_s": round(args.prefill / prefill_s, 1),
+        "prefill": prefill,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "isolated": isolated,
     }
     print(json.dumps(out), flush=True)
     return 0
