@@ -21,11 +21,12 @@
 
 #define LG_ATTN_MAX_CHUNK 1024
 
-/* chunk length for a context of ctx positions: about 64 chunks, between 64
- * and LG_ATTN_MAX_CHUNK positions, multiple of 64 */
+/* chunk length for a context of ctx positions: about 128 chunks (with 8 KV
+ * heads, 1024 workgroups: four per CU), between 64 and LG_ATTN_MAX_CHUNK
+ * positions, multiple of 64 */
 static int attn_chunk(int ctx)
 {
-    int c = (ctx + 63) / 64;
+    int c = (ctx + 127) / 128;
     c = (c + 63) / 64 * 64;
     if (c < 64) c = 64;
     if (c > LG_ATTN_MAX_CHUNK) c = LG_ATTN_MAX_CHUNK;
@@ -94,25 +95,29 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
 #pragma unroll
         for (int i = 0; i < DPL; i++) qr[r][i] = q[(size_t)(kh * NREP + r) * HD + gl * DPL + i];
 
-    /* pass 1: scores */
-    for (int tb = 0; tb < nt; tb += PPB) {
-        const int tl = tb + wave * PPW + grp;
-        const int t = t0 + tl;
-        float kv[DPL];
-        if (tl < nt) {
-            if (t == pos) load_f32_row<DPL>(kcur + kh * HD + gl * DPL, kv);
-            else load_half_row<DPL>(kc + (size_t)t * kv_dim + kh * HD + gl * DPL, kv);
-        } else {
+    /* pass 1: scores, U steps of rows loaded before any is used (positions
+     * past the chunk load its first row and are not stored) */
+    constexpr int U = 4;
+    for (int tb = 0; tb < nt; tb += U * PPB) {
+        float kv[U][DPL];
 #pragma unroll
-            for (int i = 0; i < DPL; i++) kv[i] = 0.0f;
+        for (int u = 0; u < U; u++) {
+            const int tl = tb + u * PPB + wave * PPW + grp;
+            const int t = tl < nt ? t0 + tl : t0;
+            if (t == pos) load_f32_row<DPL>(kcur + kh * HD + gl * DPL, kv[u]);
+            else load_half_row<DPL>(kc + (size_t)t * kv_dim + kh * HD + gl * DPL, kv[u]);
         }
 #pragma unroll
-        for (int r = 0; r < NREP; r++) {
-            float s = 0.0f;
+        for (int u = 0; u < U; u++) {
+            const int tl = tb + u * PPB + wave * PPW + grp;
 #pragma unroll
-            for (int i = 0; i < DPL; i++) s += qr[r][i] * kv[i];
-            s = lg_group_sum<LPP>(s);
-            if (gl == 0 && tl < nt) s_sc[r * LG_ATTN_MAX_CHUNK + tl] = s * scale;
+            for (int r = 0; r < NREP; r++) {
+                float s = 0.0f;
+#pragma unroll
+                for (int i = 0; i < DPL; i++) s += qr[r][i] * kv[u][i];
+                s = lg_group_sum<LPP>(s);
+                if (gl == 0 && tl < nt) s_sc[r * LG_ATTN_MAX_CHUNK + tl] = s * scale;
+            }
         }
     }
     __syncthreads();
@@ -146,18 +151,25 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
     for (int r = 0; r < NREP; r++)
 #pragma unroll
         for (int i = 0; i < DPL; i++) o[r][i] = 0.0f;
-    for (int tb = 0; tb < nt; tb += PPB) {
-        const int tl = tb + wave * PPW + grp;
-        const int t = t0 + tl;
-        if (tl < nt) {
-            float vv[DPL];
-            if (t == pos) load_f32_row<DPL>(vcur + kh * HD + gl * DPL, vv);
-            else load_half_row<DPL>(vc + (size_t)t * kv_dim + kh * HD + gl * DPL, vv);
+    for (int tb = 0; tb < nt; tb += U * PPB) {
+        float vv[U][DPL];
 #pragma unroll
-            for (int r = 0; r < NREP; r++) {
-                const float p = s_sc[r * LG_ATTN_MAX_CHUNK + tl];
+        for (int u = 0; u < U; u++) {
+            const int tl = tb + u * PPB + wave * PPW + grp;
+            const int t = tl < nt ? t0 + tl : t0;
+            if (t == pos) load_f32_row<DPL>(vcur + kh * HD + gl * DPL, vv[u]);
+            else load_half_row<DPL>(vc + (size_t)t * kv_dim + kh * HD + gl * DPL, vv[u]);
+        }
 #pragma unroll
-                for (int i = 0; i < DPL; i++) o[r][i] += p * vv[i];
+        for (int u = 0; u < U; u++) {
+            const int tl = tb + u * PPB + wave * PPW + grp;
+            if (tl < nt) {
+#pragma unroll
+                for (int r = 0; r < NREP; r++) {
+                    const float p = s_sc[r * LG_ATTN_MAX_CHUNK + tl];
+#pragma unroll
+                    for (int i = 0; i < DPL; i++) o[r][i] += p * vv[u][i];
+                }
             }
         }
     }
@@ -209,9 +221,11 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
     const int h = blockIdx.x;
     const int kh = h / NREP, r = h % NREP;
     float M = -INFINITY;
+#pragma unroll 8
     for (int c = 0; c < nch; c++) M = fmaxf(M, ws[((size_t)kh * nch + c) * NREP * (HD + 2) + r]);
     for (int dd = threadIdx.x; dd < HD; dd += blockDim.x) {
         float L = 0.0f, acc = 0.0f;
+#pragma unroll 8
         for (int c = 0; c < nch; c++) {
             const float* p = ws + ((size_t)kh * nch + c) * NREP * (HD + 2);
             const float w = expf(p[r] - M);
