@@ -179,6 +179,51 @@ def isolated_kernels(torch, np):
     return out
 
 
+def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
+    """The 1-bit workload: Qwen3-8B shape with Q1_G layers (group 128, sign
+    bits, fp16 group scales |N(0,0.02)|) and Q8_0 embedding/output, an
+    8192-token prompt of random ids fed through lg_prefill (token by token:
+    the batched prefill takes Q4_K layers only), then greedy decode at
+    positions 8192.. .  Reports prefill and decode tok/s and the decode
+    token roofline (weight + KV bytes per token over the time)."""
+    from ligguf_amd.model import QWEN3_8B_Q1G, Engine, HostModel
+    cfg = QWEN3_8B_Q1G.with_(n_context=ctx + warmup + steps + 1)
+    t0 = time.perf_counter()
+    hm = HostModel.synthetic(cfg)
+    log(f"synthetic {cfg.name} built in {time.perf_counter() - t0:.1f}s")
+    eng = Engine(0)
+    eng.load(hm)
+    prompt = np.random.default_rng(1).integers(1, cfg.vocab, ctx).astype(np.int32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = eng.prefill(prompt, 0)
+    pf_s = time.perf_counter() - t0
+    tok, pos = int(np.argmax(logits)), ctx
+    for _ in range(warmup):
+        eng.decode_async(tok, pos)
+        tok = eng.argmax()
+        pos += 1
+    torch.cuda.synchronize()
+    p_first = pos
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.decode_async(tok, pos)
+        tok = eng.argmax()
+        pos += 1
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    path = {1: "persistent", 2: "multi-kernel", 3: "fused-graph"}.get(eng.path(), "?")
+    eng.close()
+    mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
+    out = {"workload": "qwen3-8b-shape Q1_G layers, Q8_0 embedding/output, 8192-token prompt then greedy decode",
+           "prefill_tok_s": round(ctx / pf_s, 1), "decode_tok_s": round(steps / dt, 1),
+           "ms_per_token": round(dt / steps * 1e3, 4), "positions": [p_first, pos - 1],
+           "bytes_per_token": int(mean_bytes), "hbm_roofline_frac_token": round(mean_bytes / (dt / steps) / HBM_PEAK, 4),
+           "decode_path": path}
+    log(f"q1g: {out}")
+    return out
+
+
 def cpu_baseline(hm, seconds: float, max_tokens: int = 4000):
     """The reference FAST engine (oracle/_ref, AVX2, OpenMP) decoding the same
     host model from position 0 for about `seconds`."""
@@ -237,6 +282,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated matvec/attention lines")
+    ap.add_argument("--no-q1g", action="store_true", help="skip the Q1_G 8192-context workload")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
     args = ap.parse_args()
@@ -309,6 +355,8 @@ def main() -> int:
         log(f"dominant kernel: {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of HBM peak)")
     eng.close()
 
+    q1g = None if args.no_q1g else q1g_context(torch, np)
+
     cpu = None
     if not args.no_cpu:
         t0 = time.perf_counter()
@@ -341,6 +389,7 @@ def main() -> int:
         "roofline": roof,
         "cpu_baseline": cpu,
         "isolated": isolated,
+        "q1g_8k": q1g,
     }
     print(json.dumps(out), flush=True)
     return 0

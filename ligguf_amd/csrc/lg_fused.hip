@@ -55,7 +55,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const P
                                                        int l)
 {
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
-    phase_attn<HD, NREP>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
+    phase_attn_any<HD, NREP>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
 }
 
 template <int LT, int HD, int NREP>

@@ -87,14 +87,16 @@ __host__ __device__ constexpr int pk_att_steps(int nrep)
     return nrep > 4 ? 4 : 8;
 }
 
-/* query heads per attention unit: one.  A unit (query head, kv head,
- * chunk) carries 1/NREP of the group's arithmetic (the work of a unit is
- * lane arithmetic, not memory), so NREP times as many workgroups share the
- * phase; the NREP units that read the same K/V rows are ordered onto the
- * same XCD, whose L2 serves the repeats. */
-__host__ __device__ constexpr int pk_att_nq(int)
+/* query heads per attention unit.  One, while every unit of the phase gets a
+ * workgroup of its own (n_kv x NREP x chunks <= grid): a unit carries 1/NREP
+ * of the group's arithmetic (its work is lane arithmetic, not memory), so
+ * NREP times as many workgroups share the phase, and the NREP units that read
+ * the same K/V rows run at the same time on one XCD, whose L2 serves the
+ * repeats.  Past that (long contexts) a unit takes all NREP query heads, so
+ * every K/V row is read from HBM once. */
+__host__ __device__ inline bool pk_att_one_head(int n_kv, int nrep, int nch, int nwg)
 {
-    return 1;
+    return n_kv * nrep * nch <= nwg;
 }
 
 __host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nrep, int* chunk_out, int* nch_out)

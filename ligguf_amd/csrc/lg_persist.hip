@@ -103,7 +103,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
         else
             phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_STORE, BLD_RMS, 2, true>(
                 P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l));
-        phase_attn<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
+        phase_attn_any<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
         phase_mv<LT, NE, Batch<LT, NE, 1, 1, 512>::value, 1, EPI_RESID, BLD_MERGE, 2, true>(
             P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2),
             att_partials<HD, NREP>(P, l, S.pos));

@@ -584,7 +584,7 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * the last unit of the heads (atomic counter) merges them into the layer's
  * merged slot.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
-template <int HD, int NREP, int NQ = pk_att_nq(NREP)>
+template <int HD, int NREP, int NQ>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
                                            uint64_t* tr)
@@ -850,6 +850,21 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     stamp(tr, 2);
     if (sig) pk_signal(P, sig);
     stamp(tr, 3);
+}
+
+/* the attention phase with the unit size pk_att_one_head picks for this
+ * context (both bodies inlined; the choice is uniform over the grid) */
+template <int HD, int NREP>
+__device__ __forceinline__ void phase_attn_any(const PkParams& P, const PkLayer& L, int layer, int pos,
+                                               const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
+                                               uint64_t* tr)
+{
+    int chunk, nch;
+    pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
+    if (NREP > 1 && pk_att_one_head(P.n_kv, NREP, nch, gridDim.x))
+        phase_attn<HD, NREP, 1>(P, L, layer, pos, qkv, wait_target, sig, tr);
+    else
+        phase_attn<HD, NREP, NREP>(P, L, layer, pos, qkv, wait_target, sig, tr);
 }
 
 
