@@ -164,7 +164,7 @@ struct lg_ctx {
     bool dev_known = false;          /* step_dev holds {dev_tok, dev_pos} (read back after a sync) */
     int dev_tok = 0, dev_pos = 0, dev_feed_end = 0, last_pos = 0;
     bool use_graph = true;
-    hipGraphExec_t graph = nullptr;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};   /* the step with short / long-context attention */
 };
 
 static int ctx_fail(lg_ctx* ctx, int rc)
@@ -200,9 +200,9 @@ static void free_model(lg_ctx* ctx)
     ctx->arena = {};
     ctx->pf_layers.clear();
     ctx->pf = PfBuffers{};
-    if (ctx->graph) {
-        hipGraphExecDestroy(ctx->graph);
-        ctx->graph = nullptr;
+    for (auto& gr : ctx->graph) {
+        if (gr) hipGraphExecDestroy(gr);
+        gr = nullptr;
     }
 }
 
@@ -317,11 +317,15 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     ctx->pk_kernel = nullptr;
     const int nrep = m->n_heads / m->n_kv_heads;
     const int lt = ctx->layers.empty() ? -1 : ctx->layers[0].q.type;
-    /* attention partials per head and layer: PK_ATT_MERGE chunks, or full
-     * units (pk_attn_split) at the longest context */
+    /* attention partials per head and layer: PK_ATT_MERGE chunks, or the
+     * long-context chunk count of pk_attn_split (one grid of one workgroup
+     * per CU) at the longest context */
+    int dev = 0, ncu = 0;
+    LG_HIP_CHECK(hipGetDevice(&dev));
+    LG_HIP_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
     int att_chunk = 0, att_nch = 0;
-    if (m->head_dim > 0 && m->head_dim <= 128 && nrep >= 1 && nrep <= PK_MAX_NREP)
-        pk_attn_split(m->n_context, m->head_dim, nrep, &att_chunk, &att_nch);
+    if (m->head_dim > 0 && m->head_dim <= 128 && nrep >= 1 && nrep <= PK_MAX_NREP && m->n_kv_heads > 0)
+        pk_attn_split(m->n_context, m->head_dim, nrep, ncu / m->n_kv_heads, &att_chunk, &att_nch);
     att_nch = std::max(att_nch, PK_ATT_MERGE);
     bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
               m->n_kv_heads <= 32 && m->n_heads <= 32 && ctx->output.cols == m->n_embed && ctx->arena.ok;
@@ -452,33 +456,42 @@ static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* t
     return LG_OK;
 }
 
-/* one fused step on the stream: the graph (captured on first use) or the
- * same launches issued directly */
-static int fused_launch(lg_ctx* c)
+/* attention at position pos takes the long-context kernel */
+static bool att_long(const lg_ctx* c, int pos)
 {
-    if (c->use_graph && !c->graph) {
+    return pk_att_long(pos, c->pk.head_dim, c->pk.n_heads / c->pk.n_kv, c->pk.n_kv, c->pk_nwg);
+}
+
+/* one fused step at position pos on the stream: its graph (captured on first
+ * use; one per attention kernel) or the same launches issued directly */
+static int fused_launch(lg_ctx* c, int pos)
+{
+    const bool lc = att_long(c, pos);
+    hipGraphExec_t& graph = c->graph[lc ? 1 : 0];
+    if (c->use_graph && !graph) {
         hipGraph_t g = nullptr;
         LG_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg, c->stream);
+        const int rc = lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg,
+                                        lc, c->stream);
         const hipError_t ec = hipStreamEndCapture(c->stream, &g);
         if (rc || ec != hipSuccess) {
             if (g) hipGraphDestroy(g);
             lg_set_error("graph capture of the fused step failed: %s", hipGetErrorString(ec));
             return rc ? rc : LG_ERR_HIP;
         }
-        const hipError_t ei = hipGraphInstantiate(&c->graph, g, nullptr, nullptr, 0);
+        const hipError_t ei = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (ei != hipSuccess) {
-            c->graph = nullptr;
+            graph = nullptr;
             lg_set_error("graph instantiate: %s", hipGetErrorString(ei));
             return LG_ERR_HIP;
         }
     }
     if (c->use_graph) {
-        LG_HIP_CHECK(hipGraphLaunch(c->graph, c->stream));
+        LG_HIP_CHECK(hipGraphLaunch(graph, c->stream));
         return LG_OK;
     }
-    return lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg, c->stream);
+    return lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg, lc, c->stream);
 }
 
 static int enqueue_fused(lg_ctx* c, int tok, int pos)
@@ -488,7 +501,7 @@ static int enqueue_fused(lg_ctx* c, int tok, int pos)
         if ((rc = fused_set_step(c, tok, pos, 0, c->pk_trace))) return rc;
     c->pk_trace = nullptr;
     c->dev_known = false;
-    if ((rc = fused_launch(c))) return rc;
+    if ((rc = fused_launch(c, pos))) return rc;
     LG_HIP_CHECK(hipMemcpyAsync(c->pk_status_host, c->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
     c->last_was_pk = true;
     c->last_pos = pos;
@@ -587,7 +600,7 @@ extern "C" int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters
     int rc = LG_OK;
     for (int i = 0; i < iters && rc == LG_OK; i++)
         rc = lg_fused_phase(ctx->fused_fn, ctx->pk, ctx->pk_layers.data(), ctx->step_dev, phase,
-                            (layer0 + i) % ctx->n_layers, ctx->pk_nwg, ctx->stream);
+                            (layer0 + i) % ctx->n_layers, ctx->pk_nwg, att_long(ctx, ctx->dev_pos), ctx->stream);
     LG_HIP_CHECK(hipEventRecord(e1, ctx->stream));
     LG_HIP_CHECK(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -1102,7 +1115,7 @@ extern "C" int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* 
         LG_HIP_CHECK(hipMemcpyAsync(ctx->feed_dev + pos0, ctx->feed_host + pos0, (size_t)n * sizeof(int),
                                     hipMemcpyHostToDevice, ctx->stream));
         int rc = fused_set_step(ctx, toks[0], pos0, pos0 + n);
-        for (int i = 0; !rc && i < n; i++) rc = fused_launch(ctx);
+        for (int i = 0; !rc && i < n; i++) rc = fused_launch(ctx, pos0 + i);
         if (rc) return ctx_fail(ctx, rc);
         LG_HIP_CHECK(hipMemcpyAsync(ctx->pk_status_host, ctx->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost,
                                     ctx->stream));

@@ -50,12 +50,16 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const Pk
         f_tr(Sd, l, 0));
 }
 
-template <int HD, int NREP>
+/* LONG: the long-context units (the host picks by pk_att_long of the step's
+ * position); otherwise one-head single-batch units.  Two kernels, so the
+ * short-context one carries no long-context code or registers. */
+template <int HD, int NREP, bool LONG>
 __global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                        int l)
 {
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
-    phase_attn_any<HD, NREP>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
+    if constexpr (LONG) phase_attn<HD, NREP, NREP, true>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
+    else phase_attn<HD, NREP, 1, false>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
 }
 
 template <int LT, int HD, int NREP>
@@ -107,16 +111,18 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, hipStream_t);
+typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t);
 
 template <int LT, int OT, int HD, int NREP>
-static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n_layers, int nwg, hipStream_t st)
+static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n_layers, int nwg, bool long_ctx,
+                          hipStream_t st)
 {
     const dim3 g(nwg), b(PK_THREADS);
     for (int l = 0; l < n_layers; l++) {
         if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l);
-        hipLaunchKernelGGL((k_f_attn<HD, NREP>), g, b, 0, st, P, Lh[l], S, l);
+        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
+        else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l);
         hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l);
         hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l);
@@ -124,11 +130,12 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
     hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S);
 }
 
-typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, hipStream_t);
+typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, bool, hipStream_t);
 
 /* one kernel of the step: phase 0..4 of layer l, 5 = output head */
 template <int LT, int OT, int HD, int NREP>
-static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int phase, int l, int nwg, hipStream_t st)
+static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int phase, int l, int nwg, bool long_ctx,
+                        hipStream_t st)
 {
     const dim3 g(nwg), b(PK_THREADS);
     switch (phase) {
@@ -136,7 +143,10 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
         if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l);
         break;
-    case 1: hipLaunchKernelGGL((k_f_attn<HD, NREP>), g, b, 0, st, P, Lh[l], S, l); break;
+    case 1:
+        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
+        else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
+        break;
     case 2: hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l); break;
     case 3: hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l); break;
     case 4: hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l); break;
@@ -168,15 +178,15 @@ const void* lg_fused_variant(int lt, int ot, int hd, int nrep)
 }
 
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
-                     hipStream_t s)
+                     bool long_ctx, hipStream_t s)
 {
-    ((const FusedVariant*)variant)->fn(P, layers, S_dev, n_layers, nwg, s);
+    ((const FusedVariant*)variant)->fn(P, layers, S_dev, n_layers, nwg, long_ctx, s);
     return lg_check_launch("fused decode step");
 }
 
 int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int phase, int layer,
-                   int nwg, hipStream_t s)
+                   int nwg, bool long_ctx, hipStream_t s)
 {
-    ((const FusedVariant*)variant)->phase(P, layers, S_dev, phase, layer, nwg, s);
+    ((const FusedVariant*)variant)->phase(P, layers, S_dev, phase, layer, nwg, long_ctx, s);
     return lg_check_launch("fused decode phase");
 }

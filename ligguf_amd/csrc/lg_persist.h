@@ -10,7 +10,7 @@
 #define PK_MAX_FF 16384     /* n_ff limit (quantized activation in LDS) */
 #define PK_MAX_NREP 8       /* query heads per KV head */
 #define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
-#define PK_ATT_MAX_NCH 160  /* attention partials per head at most (n_ctx <= 160 full units) */
+#define PK_ATT_MAX_NCH 160  /* attention chunks per head at most */
 
 /* one layer as the kernel reads it: fused Q|K|V and up|gate matrices */
 struct PkLayer {
@@ -78,10 +78,12 @@ struct PkStep {
 
 /* attention work split.  A workgroup step covers ppb = PK_THREADS * 8 /
  * head_dim positions (one 16-byte slice of a cache row per lane) and a unit
- * (kv head, chunk) holds at most pk_att_steps(nrep) steps of K and V in
- * registers.  Contexts up to PK_ATT_MERGE full units are cut into at most
- * PK_ATT_MERGE chunks per head, whose partials the att_out build merges;
- * longer ones into full units merged by the last unit of each head. */
+ * (kv head, chunk) holds pk_att_steps(nrep) steps of K and V in registers at
+ * a time -- one register batch.  Contexts up to PK_ATT_MERGE batches are cut
+ * into at most PK_ATT_MERGE chunks per head, whose partials the att_out build
+ * merges; longer ones into max_nch chunks (the grid's workgroups per head
+ * group, clamped to [PK_ATT_MERGE, PK_ATT_MAX_NCH]) of one or more batches,
+ * merged by the last unit of each head. */
 __host__ __device__ constexpr int pk_att_steps(int nrep)
 {
     return nrep > 4 ? 4 : 8;
@@ -99,12 +101,17 @@ __host__ __device__ inline bool pk_att_one_head(int n_kv, int nrep, int nch, int
     return n_kv * nrep * nch <= nwg;
 }
 
-__host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nrep, int* chunk_out, int* nch_out)
+__host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nrep, int max_nch, int* chunk_out,
+                                              int* nch_out)
 {
     const int ppb = PK_THREADS * 8 / head_dim;
     int chunk = (ctx_len + PK_ATT_MERGE - 1) / PK_ATT_MERGE;
     chunk = (chunk + ppb - 1) / ppb * ppb;
-    if (chunk > pk_att_steps(nrep) * ppb) chunk = pk_att_steps(nrep) * ppb;
+    if (chunk > pk_att_steps(nrep) * ppb) {
+        const int n = max_nch < PK_ATT_MERGE ? PK_ATT_MERGE : (max_nch > PK_ATT_MAX_NCH ? PK_ATT_MAX_NCH : max_nch);
+        chunk = (ctx_len + n - 1) / n;
+        chunk = (chunk + ppb - 1) / ppb * ppb;
+    }
     *chunk_out = chunk;
     *nch_out = (ctx_len + chunk - 1) / chunk;
 }
@@ -115,14 +122,26 @@ const void* lg_persist_kernel(int layer_type, int out_type, int head_dim, int nr
 int lg_persist_grid(const void* kernel, int* nwg);
 int lg_persist_launch(const void* kernel, const PkParams& P, const PkStep* S, int nwg, hipStream_t s);
 
+/* attention at position pos takes the long-context units (whole query-head
+ * groups, register batches) unless every unit is one batch of one query
+ * head with a workgroup of its own */
+__host__ __device__ inline bool pk_att_long(int pos, int head_dim, int nrep, int n_kv, int nwg)
+{
+    int chunk, nch;
+    pk_attn_split(pos + 1, head_dim, nrep, nwg / n_kv, &chunk, &nch);
+    const bool single = chunk <= pk_att_steps(nrep) * (PK_THREADS * 8 / head_dim);
+    return !(single && pk_att_one_head(n_kv, nrep, nch, nwg));
+}
+
 /* the fused per-phase kernels of one step (lg_fused.hip): 5*n_layers + 1
  * launches on stream s reading {tok, pos} from S_dev; the last one writes the
  * greedy token to P->tok_out and advances S_dev to {token, pos + 1}.  NULL
- * when the variant is not instantiated. */
+ * when the variant is not instantiated.  long_ctx = pk_att_long(pos, ...) of
+ * the step's position selects the attention kernel. */
 const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep);
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
-                     hipStream_t s);
+                     bool long_ctx, hipStream_t s);
 /* one kernel of the fused step: phase 0 rmsnorm+QKV, 1 attention, 2 att_out,
  * 3 up|gate, 4 down (of `layer`), 5 output head */
 int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int phase, int layer,
-                   int nwg, hipStream_t s);
+                   int nwg, bool long_ctx, hipStream_t s);

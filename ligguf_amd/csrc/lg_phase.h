@@ -226,13 +226,19 @@ struct MergeAct {
     }
 };
 
+/* long-context chunks per head: the grid's workgroups per head group */
+__device__ __forceinline__ int pk_att_max_nch(const PkParams& P)
+{
+    return (int)gridDim.x / P.n_kv;
+}
+
 /* the attention partials of layer l at position pos as the att_out build
  * reads them: the chunks (pk_attn_split), or the merged slot */
 template <int HD, int NREP>
 __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int pos)
 {
     int chunk, nch;
-    pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
+    pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
     const size_t slot = (size_t)l * P.att_slots + (nch > PK_ATT_MERGE ? P.att_slots - 1 : 0);
     return MergeSrc{P.att_po + slot * P.n_embed, P.att_pml + slot * P.n_heads * 2, nch > PK_ATT_MERGE ? 1 : nch, HD};
 }
@@ -584,7 +590,7 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * the last unit of the heads (atomic counter) merges them into the layer's
  * merged slot.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
-template <int HD, int NREP, int NQ>
+template <int HD, int NREP, int NQ, bool BATCHES>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
                                            uint64_t* tr)
@@ -601,7 +607,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     const int gl = lane & (LPP - 1), grp = lane / LPP;
     const int kvd = P.kv_dim;
     int chunk, nch;
-    pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
+    pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
     const int ngc = P.n_kv * nch;           /* (kv head, chunk) pairs */
     const int nunits = ngc * NSUB;
     const size_t loff = (size_t)layer * P.n_ctx * kvd;
@@ -618,12 +624,12 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     float4 hx[NH], hv;            /* this wave's heads h = wave + PK_WAVES*j: q (h < NQ) or k, and v */
     /* unconditional loads (see Rows): positions outside the unit and the
      * row pos itself (not in the cache yet) load the unit's first row */
-    auto load_kv = [&](int u) {
+    auto load_kv = [&](int u, int sb) {   /* the register batch of steps sb.. */
         const int g = (u % ngc) / nch, c = (u % ngc) % nch;
         const int t0 = c * chunk, t1 = min(t0 + chunk, pos + 1);
 #pragma unroll
         for (int st = 0; st < MAXST; st++) {
-            int t = t0 + st * PPB + wave * PPW + grp;
+            int t = t0 + (sb + st) * PPB + wave * PPW + grp;
             t = t < t1 && t != pos ? t : t0;
             const size_t o = loff + (size_t)t * kvd + (size_t)g * HD + gl * 8;
             kb[st] = *(const uint4*)(P.kc + o);
@@ -664,7 +670,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
         load_heads(u);
         lg_issue_order();   /* heads first, then K/V */
-        load_kv(u);
+        load_kv(u, 0);
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
         *(float4*)(s_kv + HD + l4) = hv;
@@ -717,36 +723,43 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 #pragma unroll
             for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
         }
+        /* register batches of MAXST steps; the next batch's loads follow
+         * the current batch's use (one round trip per batch) */
+        for (int sb = 0;;) {
 #pragma unroll
-        for (int st = 0; st < MAXST; st++) {
-            const int t = t0 + st * PPB + wave * PPW + grp;
-            if (st < nsteps && t < t1) {
-                float kf[8], vf[8];
-                if (t != pos) {
-                    h8(kb[st], kf);
-                    h8(vb[st], vf);
-                } else {
+            for (int st = 0; st < MAXST; st++) {
+                const int t = t0 + (sb + st) * PPB + wave * PPW + grp;
+                if (sb + st < nsteps && t < t1) {
+                    float kf[8], vf[8];
+                    if (t != pos) {
+                        h8(kb[st], kf);
+                        h8(vb[st], vf);
+                    } else {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
-                }
+                        for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
+                    }
 #pragma unroll
-                for (int r = 0; r < NQ; r++) {
-                    float qv[8];
+                    for (int r = 0; r < NQ; r++) {
+                        float qv[8];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) qv[i] = NQ <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HD + gl * 8 + i];
-                    float sc = 0.0f;
+                        for (int i = 0; i < 8; i++) qv[i] = NQ <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HD + gl * 8 + i];
+                        float sc = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];
-                    sc = lg_group_sum<LPP>(sc) * scale2;
-                    const float mn = fmaxf(m[r], sc);
-                    const float a = lg_exp2(m[r] - mn);     /* 0 while m = -inf */
-                    const float pw = lg_exp2(sc - mn);
-                    l[r] = l[r] * a + pw;
+                        for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];
+                        sc = lg_group_sum<LPP>(sc) * scale2;
+                        const float mn = fmaxf(m[r], sc);
+                        const float a = lg_exp2(m[r] - mn);     /* 0 while m = -inf */
+                        const float pw = lg_exp2(sc - mn);
+                        l[r] = l[r] * a + pw;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) o[r][i] = lg_fma2(o[r][i], a, pw, vf[i]);
-                    m[r] = mn;
+                        for (int i = 0; i < 8; i++) o[r][i] = lg_fma2(o[r][i], a, pw, vf[i]);
+                        m[r] = mn;
+                    }
                 }
             }
+            sb += MAXST;
+            if (!BATCHES || sb >= nsteps) break;   /* one batch: chunks of <= MAXST steps */
+            load_kv(u, sb);
         }
         /* combine the position groups of the wave into group 0 (16-lane
          * rows: row 1 -> 0 and 3 -> 2, then 2 -> 0, by lane permutes), then
@@ -852,19 +865,17 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     stamp(tr, 3);
 }
 
-/* the attention phase with the unit size pk_att_one_head picks for this
- * context (both bodies inlined; the choice is uniform over the grid) */
+/* the attention phase with the units pk_att_long picks for this context
+ * (both bodies inlined; the choice is uniform over the grid) */
 template <int HD, int NREP>
 __device__ __forceinline__ void phase_attn_any(const PkParams& P, const PkLayer& L, int layer, int pos,
                                                const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
                                                uint64_t* tr)
 {
-    int chunk, nch;
-    pk_attn_split(pos + 1, HD, NREP, &chunk, &nch);
-    if (NREP > 1 && pk_att_one_head(P.n_kv, NREP, nch, gridDim.x))
-        phase_attn<HD, NREP, 1>(P, L, layer, pos, qkv, wait_target, sig, tr);
+    if (!pk_att_long(pos, HD, NREP, P.n_kv, gridDim.x))
+        phase_attn<HD, NREP, 1, false>(P, L, layer, pos, qkv, wait_target, sig, tr);
     else
-        phase_attn<HD, NREP, NREP>(P, L, layer, pos, qkv, wait_target, sig, tr);
+        phase_attn<HD, NREP, NREP, true>(P, L, layer, pos, qkv, wait_target, sig, tr);
 }
 
 
