@@ -285,6 +285,8 @@ def main() -> int:
     ap.add_argument("--no-q1g", action="store_true", help="skip the Q1_G 8192-context workload")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill: the prompt twice, the second timed (for MFMA counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the decode path here is single-GPU (asked for --gpus {args.gpus}).",
@@ -305,6 +307,21 @@ def main() -> int:
         roof = dominant_kernel_roofline(eng, cfg)
         eng.close()
         print(json.dumps({"roofline": roof, "copy": copy_gbs}), flush=True)
+        return 0
+
+    if args.prefill_only:
+        hm = HostModel.synthetic(cfg)
+        eng = Engine(0)
+        eng.load(hm)
+        prompt = np.random.default_rng(0).integers(1, cfg.vocab, args.prefill).astype(np.int32)
+        eng.prefill(prompt, 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.prefill(prompt, 0)
+        seconds = time.perf_counter() - t0
+        rep = prefill_report(cfg, args.prefill, seconds, eng.prefill_path())
+        eng.close()
+        print(json.dumps({"prefill": rep}), flush=True)
         return 0
 
     t0 = time.perf_counter()
