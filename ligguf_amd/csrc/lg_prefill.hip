@@ -152,14 +152,25 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
 #pragma unroll
         for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
     }
-    for (int j0 = 0; j0 <= pos; j0 += PPB) {
-        const int j = j0 + wave * PPW + grp;
+    /* U steps of K/V rows loaded before any is used (positions past pos
+     * load row 0 and are skipped) */
+    constexpr int U = 4;
+    for (int j00 = 0; j00 <= pos; j00 += U * PPB) {
+        uint4 kbu[U], vbu[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = j00 + u * PPB + wave * PPW + grp;
+            const size_t off = (size_t)(j < pos ? j : 0) * kv_dim + (size_t)g * HD + gl * 8;
+            kbu[u] = *(const uint4*)(kc + off);
+            vbu[u] = *(const uint4*)(vc + off);
+        }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int j = j00 + u * PPB + wave * PPW + grp;
         if (j <= pos) {
             float kf[8], vf[8];
             if (j < pos) {
-                const size_t off = (size_t)j * kv_dim + (size_t)g * HD + gl * 8;
-                const uint4 kb = *(const uint4*)(kc + off);
-                const uint4 vb = *(const uint4*)(vc + off);
+                const uint4 kb = kbu[u], vb = vbu[u];
                 const uint32_t ku[4] = {kb.x, kb.y, kb.z, kb.w}, vu[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -187,6 +198,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
                 m[r] = mn;
             }
         }
+    }
     }
     /* lane groups (16-lane rows) of the wave into group 0 by lane permutes,
      * then the waves */
