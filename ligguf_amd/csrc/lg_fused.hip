@@ -45,7 +45,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const Pk
     float* xin = P.xs + (size_t)l * ne;
     const int pos = Sd->pos;
     const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
-    phase_mv<LT, NE, Batch<LT, NE, 1, 2, 512>::value, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, 2, true>(
+    phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, 2, LG_QKV_R>(
         P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, P.qkv + (size_t)l * qs, xin, 0, 0,
         f_tr(Sd, l, 0));
 }
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkL
 {
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed;
-    phase_mv<LT, NE, Batch<LT, NE, 1, 1, 512>::value, 1, EPI_RESID, BLD_MERGE, 2, true>(
+    phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
         P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, P.xs + (size_t)l * ne, P.xm + (size_t)l * ne, nullptr, 0, 0,
         f_tr(Sd, l, 2), att_partials<HD, NREP>(P, l, Sd->pos));
 }
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkL
 {
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NE, Batch<LT, NE, 2, 2, 512>::value, 2, EPI_SWIGLU, BLD_RMS, 2, true>(
+    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, 2, LG_UG_R>(
         P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, P.xm + (size_t)l * ne, nullptr, P.hb + (size_t)l * nff, nullptr, 0,
         0, f_tr(Sd, l, 3));
 }
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const P
 {
     constexpr int NF = 3 * NsE<LT>::value;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NF, Batch<LT, NF, 1, 1, 512>::value, 1, EPI_RESID, BLD_PLAIN, 6, true>(
+    phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, 6, LG_DN_R>(
         P, 0, L.down, L.down_rsz, ne, 0, nullptr, P.hb + (size_t)l * nff, P.xm + (size_t)l * ne,
         P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4));
 }
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 {
     constexpr int NO = NsE<OT>::value;
     const int pos = Sd->pos;
-    phase_mv<OT, NO, Batch<OT, NO, 1, 4, 288>::value, 1, EPI_LOGITS, BLD_RMS, 2, true>(
+        phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
         nullptr, 0, 0, f_tr(Sd, P.n_layers, 0));
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */

@@ -24,6 +24,13 @@
 #define LG_TID ((int)threadIdx.x)
 #endif
 
+/* matvec phases: wave w of the grid takes items w, w + waves, w + 2 waves, ...
+ * so that all waves sweep each window of consecutive rows together (DRAM
+ * pages and channels see one moving window); 0 = a contiguous range per wave */
+#ifndef LG_MV_SPREAD
+#define LG_MV_SPREAD 1
+#endif
+
 /* ------------------------------------------------------------------ */
 /* LDS                                                                  */
 /* ------------------------------------------------------------------ */
@@ -326,13 +333,13 @@ template <int FMT, int NS, int MAXB, int K>
 struct Rows {
     typename Fmt<FMT>::W w[MAXB][K][NS];
 
-    /* items i0 .. i0+MAXB-1, those past `wlast` replaced by wlast */
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, uint32_t rsz, int i0, int wlast, int kstride,
-                                         int lane)
+    /* items i0, i0+ist, ... (MAXB of them), those past `wlast` replaced by wlast */
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, uint32_t rsz, int i0, int ist, int wlast,
+                                         int kstride, int lane)
     {
 #pragma unroll
         for (int b = 0; b < MAXB; b++) {
-            const int i = min(i0 + b, wlast);
+            const int i = min(i0 + b * ist, wlast);
 #pragma unroll
             for (int k = 0; k < K; k++) {
                 const uint8_t* row = W + (size_t)(i + k * kstride) * rsz;
@@ -349,9 +356,11 @@ struct Rows {
  * phase that wrote it being two syncs back.  Wave 0 polls the progress
  * words; its own loads go after the wait, since a wave's loads return in
  * order and would hold the poll back.  Then: build the activation, compute,
- * store, publish.  CPW = 256-value activation chunks per wave; DB =
- * double-buffer the items (long phases: the output head). */
-template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, bool DB>
+ * store, publish.  CPW = 256-value activation chunks per wave; NR = batches
+ * of MAXB items held at once: 1 = load a batch, then compute it; NR >= 2 = a
+ * ring in which NR - 1 batches load while one computes (the first NR - 1
+ * batches load before the build). */
+template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, int NR>
 __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8_t* __restrict__ W, uint32_t rsz,
                                          int items, int kstride, const float* __restrict__ normw,
                                          const float* __restrict__ src, const float* __restrict__ res_src,
@@ -364,17 +373,23 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int nwv = gridDim.x * PK_WAVES;
     const int gw = blockIdx.x * PK_WAVES + wave;
+#if LG_MV_SPREAD
+    const int ist = nwv, i0 = gw;
+    const int my = gw < items ? (items - gw + nwv - 1) / nwv : 0;
+#else
     const int ipw = (items + nwv - 1) / nwv;
-    const int i0 = gw * ipw;
+    const int ist = 1, i0 = gw * ipw;
     const int my = max(0, min(items, i0 + ipw) - i0);
-    const int wlast = my > 0 ? i0 + my - 1 : items - 1;   /* clamp for the loads */
+#endif
+    const int wlast = my > 0 ? i0 + (my - 1) * ist : items - 1;   /* clamp for the loads */
 
     stamp(tr, 0);
-    Rows<FMT, NS, MAXB, K> R0;
+    static_assert(NR >= 1 && NR <= 4, "ring depth");
+    Rows<FMT, NS, MAXB, K> R[NR];
+    float res[NR][MAXB];
     NormW<CPW> nw;
     ActSrc<CPW> as;
     MergeAct<CPW> mg;
-    float res[MAXB];
     constexpr bool from_embed = BLD == BLD_EMB;
     constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
     auto load_src = [&]() {
@@ -384,12 +399,15 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     auto load_res = [&](float* r, int b0) {
         if (EPI == EPI_RESID) {
 #pragma unroll
-            for (int b = 0; b < MAXB; b++) r[b] = res_src[min(i0 + b0 + b, wlast)];
+            for (int b = 0; b < MAXB; b++) r[b] = res_src[min(i0 + (b0 + b) * ist, wlast)];
         }
     };
     auto prefetch = [&]() {
-        R0.load(W, rsz, i0, wlast, kstride, lane);
-        load_res(res, 0);
+#pragma unroll
+        for (int k = 0; k < (NR > 1 ? NR - 1 : 1); k++) {
+            R[k].load(W, rsz, i0 + k * MAXB * ist, ist, wlast, kstride, lane);
+            load_res(res[k], k * MAXB);
+        }
     };
     if (!wait_target) {
         /* no dependency wait (fused kernels): the activation and the norm
@@ -431,7 +449,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                     for (int s = 0; s < NS; s++) a += F::dot(R.w[b][k][s], act[s], lane + 64 * s);
                     acc[k] = lg_wave_sum(a);
                 }
-                const int i = i0 + b0 + b;
+                const int i = i0 + (b0 + b) * ist;
                 if (EPI == EPI_LOGITS) {
                     if (acc[0] > best) { best = acc[0]; besti = i; }
                 }
@@ -448,26 +466,26 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
             }
         }
     };
-    if (!DB) {
+    if (NR == 1) {
         for (int b0 = 0; b0 < my; b0 += MAXB) {
             if (b0 > 0) {
-                R0.load(W, rsz, i0 + b0, wlast, kstride, lane);
-                load_res(res, b0);
+                R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane);
+                load_res(res[0], b0);
             }
-            process(R0, res, b0, min(MAXB, my - b0));
+            process(R[0], res[0], b0, min(MAXB, my - b0));
         }
     } else {
-        /* two batches in flight: the next one loads while this one computes
-         * (the last iteration loads clamped duplicates it does not use) */
-        Rows<FMT, NS, MAXB, K> R1;
-        float res1[MAXB];
-        for (int b0 = 0; b0 < my; b0 += 2 * MAXB) {
-            R1.load(W, rsz, i0 + b0 + MAXB, wlast, kstride, lane);
-            load_res(res1, b0 + MAXB);
-            process(R0, res, b0, min(MAXB, my - b0));
-            R0.load(W, rsz, i0 + b0 + 2 * MAXB, wlast, kstride, lane);
-            load_res(res, b0 + 2 * MAXB);
-            process(R1, res1, b0 + MAXB, min(MAXB, my - b0 - MAXB));
+        /* batch j sits in slot j % NR; before computing batch j the wave
+         * issues batch j + NR - 1 into the slot batch j - 1 freed (past the
+         * end: clamped duplicates of its last row, never used) */
+        for (int j0 = 0; j0 * MAXB < my; j0 += NR) {
+#pragma unroll
+            for (int k = 0; k < NR; k++) {
+                const int jn = j0 + k + NR - 1;
+                R[(k + NR - 1) % NR].load(W, rsz, i0 + jn * MAXB * ist, ist, wlast, kstride, lane);
+                load_res(res[(k + NR - 1) % NR], jn * MAXB);
+                process(R[k], res[k], (j0 + k) * MAXB, min(MAXB, my - (j0 + k) * MAXB));
+            }
         }
     }
     if (EPI == EPI_LOGITS) {
@@ -890,6 +908,41 @@ struct Batch {
     static constexpr int v = BUDGET / bytes;
     static constexpr int value = v < 1 ? 1 : (v > CAP ? CAP : v);
 };
+
+/* items per batch (B) and batches held at once (R, phase_mv's ring) of each
+ * matvec phase, shared by the fused and the persistent kernels; LT/NE/NF are
+ * the layer type and its slots per lane at n_embed / n_ff, OT/NO the output
+ * head's */
+#ifndef LG_QKV_B
+#define LG_QKV_B (Batch<LT, NE, 1, 2, 512>::value)
+#endif
+#ifndef LG_QKV_R
+#define LG_QKV_R 2
+#endif
+#ifndef LG_AO_B
+#define LG_AO_B (Batch<LT, NE, 1, 1, 512>::value)
+#endif
+#ifndef LG_AO_R
+#define LG_AO_R 2
+#endif
+#ifndef LG_UG_B
+#define LG_UG_B 1
+#endif
+#ifndef LG_UG_R
+#define LG_UG_R 2
+#endif
+#ifndef LG_DN_B
+#define LG_DN_B (Batch<LT, NF, 1, 1, 512>::value)
+#endif
+#ifndef LG_DN_R
+#define LG_DN_R 2
+#endif
+#ifndef LG_OUT_B
+#define LG_OUT_B 1
+#endif
+#ifndef LG_OUT_R
+#define LG_OUT_R 2
+#endif
 
 /* slots per lane at width n_embed = 4096: one 64-value slot, two Q8_0 slots */
 template <int T>
