@@ -250,9 +250,10 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
 /* ------------------------------------------------------------------ */
 /* Workgroup tile: 16 MI tokens x 128 rows, 8 waves of 16 MI tokens x 16
  * rows (MI MFMA tiles of 16 x 16 per wave: a wave's weight operands,
- * unpacked once per sub-block, feed 2 MI MFMAs).  v_mfma_i32_16x16x32_i8 (layout
- * checked on the part): lane l holds A[token l%16][k 8(l/16)..+7],
- * B[k 8(l/16)..+7][row l%16], D[token 4(l/16)+i][row l%16] in register i.
+ * unpacked once per sub-block pair, feed 2 MI MFMAs).  v_mfma_i32_16x16x64_i8
+ * (checked on the part; twice the rate of the K = 32 form, 4.5 against 2.3
+ * int8 POP/s): lane l holds 16 bytes of A[token l%16] and of B[.][row l%16]
+ * for lane group l/16, and D[token 4(l/16)+i][row l%16] in register i.
  * In a Q4_K block, byte 32c+i of qs holds value 64c+i (low nibble) and
  * 64c+32+i (high nibble), so lane group g takes bytes 32c+8g..+7 of its
  * row: the low nibbles are its 8 values of sub-block 2c, the high ones of
@@ -358,6 +359,12 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
         const int8_t* sa = s_a[buf] + l16 * PF_AST + 8 * g;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
+            /* one K = 64 product per chunk c: bytes 0-7 of a lane are its 8
+             * values of sub-block 2c (low nibbles), bytes 8-15 those of
+             * sub-block 2c+1 (high nibbles), against the matching activation
+             * bytes 64c + 8g and 64c + 32 + 8g (the MFMA pairs byte i of A's
+             * lane group with byte i of B's, whatever k it stands for) */
+            v4i bh, bl;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int j = 2 * c + h;
@@ -366,16 +373,18 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
                 const uint32_t hi = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
                 const uint32_t sc = (scq[j >> 2] >> (8 * (j & 3))) & 0x3Fu;
                 const v2u16 sh = (v2u16)(uint16_t)(sc >> 3), sl = (v2u16)(uint16_t)(sc & 7u);
-                const long bh = (long)((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sh) |
-                                       ((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sh) << 32));
-                const long bl = (long)((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sl) |
-                                       ((uint64_t)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sl) << 32));
+                bh[2 * h] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sh);
+                bh[2 * h + 1] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sh);
+                bl[2 * h] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(lo) * sl);
+                bl[2 * h + 1] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(hi) * sl);
+            }
 #pragma unroll
-                for (int mi = 0; mi < MI; mi++) {
-                    const long af = *(const long*)(sa + 16 * mi * PF_AST + 64 * c + 32 * h);
-                    Sh[mi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bh, Sh[mi], 0, 0, 0);
-                    Sl[mi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bl, Sl[mi], 0, 0, 0);
-                }
+            for (int mi = 0; mi < MI; mi++) {
+                const uint2 a0 = *(const uint2*)(sa + 16 * mi * PF_AST + 64 * c);
+                const uint2 a1 = *(const uint2*)(sa + 16 * mi * PF_AST + 64 * c + 32);
+                const v4i af = {(int)a0.x, (int)a0.y, (int)a1.x, (int)a1.y};
+                Sh[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bh, Sh[mi], 0, 0, 0);
+                Sl[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bl, Sl[mi], 0, 0, 0);
             }
         }
         /* mins term M[token][row] = sum_j m_j (bsums_2j + bsums_2j+1) on the
@@ -443,9 +452,12 @@ int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
      * 128 tokens a workgroup needs 220 and the 512-token up|gate GEMM ran 10%
      * slower) */
     const int nrb8 = (rows + PF_RB - 1) / PF_RB + 7 & ~7;
-    const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
-    if (accumulate) hipLaunchKernelGGL((k_pf_gemm_q4k<1, 4>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
-    else hipLaunchKernelGGL((k_pf_gemm_q4k<0, 4>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+#ifndef LG_PF_MI
+#define LG_PF_MI 4
+#endif
+    const dim3 grid((unsigned)(nrb8 * ((T + 16 * LG_PF_MI - 1) / (16 * LG_PF_MI)))), blk(512);
+    if (accumulate) hipLaunchKernelGGL((k_pf_gemm_q4k<1, LG_PF_MI>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    else hipLaunchKernelGGL((k_pf_gemm_q4k<0, LG_PF_MI>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     return lg_check_launch("prefill gemm");
 }
 
