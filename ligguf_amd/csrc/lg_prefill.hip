@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
  *
  * Per 256-value block the token tile's quants, bsums and block scales are
  * staged in LDS (double-buffered, rows padded to 272 B against bank
- * conflicts) and shared by the 4 waves; each wave reads its rows' bytes
+ * conflicts, quants reordered per lane group) and shared by the 8 waves; each wave reads its rows' bytes
  * straight from the GGUF rows, one block ahead.  Rows and tokens past the
  * ends are clamped for the loads and not stored.  The grid is one
  * dimension: (row block, token tile) from the index, XCD-aware. */
@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
 #define PF_AST 272             /* LDS row stride of the staged quants */
 /* MI token tiles of 16 per workgroup */
 template <int ACC, int MI>
-__global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
                                                      PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
     __shared__ __attribute__((aligned(16))) int8_t s_a[2][(16 * MI) * PF_AST];
@@ -317,11 +317,19 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
         st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
         st.d = *(const uint4*)(x.d + (size_t)b * x.tld + min(t0 + 4 * (tid & (4 * MI - 1)), x.tld - 4));
     };
+    /* LDS order of a token's 256 quants: for each 64-value chunk c and lane
+     * group g, the 8 values 64c + 8g.. then the 8 values 64c + 32 + 8g.. --
+     * the 16 bytes one lane feeds to a K = 64 product, read with one
+     * conflict-free ds_read_b128.  Piece p = 4c + k of the row (bytes
+     * 64c + 16k..+15) holds the first halves of groups 2(k&1), 2(k&1)+1 (k
+     * < 2) or their second halves (k >= 2). */
     auto stage_store = [&](const Stg& st, int buf) {
 #pragma unroll
         for (int i = 0; i < NA; i++) {
-            const int q = tid + 512 * i;
-            *(uint4*)(s_a[buf] + (q >> 4) * PF_AST + (q & 15) * 16) = st.a[i];
+            const int q = tid + 512 * i, p = q & 15, k = p & 3;
+            int8_t* d = s_a[buf] + (q >> 4) * PF_AST + 64 * (p >> 2) + 32 * (k & 1) + 8 * (k >> 1);
+            *(uint2*)d = make_uint2(st.a[i].x, st.a[i].y);
+            *(uint2*)(d + 16) = make_uint2(st.a[i].z, st.a[i].w);
         }
         if (tid < 64 * MI) *(uint2*)(s_bs[buf] + (tid >> 2) * 16 + (tid & 3) * 4) = st.bs;
         if (tid < 4 * MI) *(uint4*)(s_d[buf] + 4 * tid) = st.d;
@@ -356,7 +364,7 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
         v4i Sh[MI], Sl[MI];
 #pragma unroll
         for (int mi = 0; mi < MI; mi++) Sh[mi] = Sl[mi] = (v4i){0, 0, 0, 0};
-        const int8_t* sa = s_a[buf] + l16 * PF_AST + 8 * g;
+        const int8_t* sa = s_a[buf] + l16 * PF_AST + 16 * g;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             /* one K = 64 product per chunk c: bytes 0-7 of a lane are its 8
@@ -380,9 +388,8 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q4k(const uint8_t* __restrict__
             }
 #pragma unroll
             for (int mi = 0; mi < MI; mi++) {
-                const uint2 a0 = *(const uint2*)(sa + 16 * mi * PF_AST + 64 * c);
-                const uint2 a1 = *(const uint2*)(sa + 16 * mi * PF_AST + 64 * c + 32);
-                const v4i af = {(int)a0.x, (int)a0.y, (int)a1.x, (int)a1.y};
+                const uint4 a = *(const uint4*)(sa + 16 * mi * PF_AST + 64 * c);
+                const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
                 Sh[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bh, Sh[mi], 0, 0, 0);
                 Sl[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bl, Sl[mi], 0, 0, 0);
             }
