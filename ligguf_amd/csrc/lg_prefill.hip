@@ -272,11 +272,15 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, 
  * straight from the GGUF rows, one block ahead.  Rows and tokens past the
  * ends are clamped for the loads and not stored.  The grid is one
  * dimension: (row block, token tile) from the index, XCD-aware. */
-#define PF_RB 128              /* rows per workgroup: 8 waves of 16 */
+#ifndef LG_PF_NT
+#define LG_PF_NT 512
+#endif
+#define PF_NT LG_PF_NT         /* threads per workgroup */
+#define PF_RB (PF_NT / 4)      /* rows per workgroup: waves of 16 */
 #define PF_AST 272             /* LDS row stride of the staged quants */
 /* MI token tiles of 16 per workgroup */
 template <int ACC, int MI>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
+__global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_gemm_q4k(const uint8_t* __restrict__ W, uint32_t rsz, int R, int K,
                                                      PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
     __shared__ __attribute__((aligned(16))) int8_t s_a[2][(16 * MI) * PF_AST];
@@ -301,7 +305,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
      * chunk/16, 16-byte piece chunk%16), one 8-byte quarter of a token's
      * bsums (token tid/4, threads < 64 MI) and, threads < 4 MI, four block
      * scales */
-    constexpr int NA = MI / 2;   /* quant chunks per thread: 16 MI tokens x 16 / 512 */
+    constexpr int NA = MI * 256 / PF_NT;   /* quant chunks per thread: 16 MI tokens x 16 / threads */
     struct Stg {
         uint4 a[NA];
         uint2 bs;
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
     auto stage_load = [&](Stg& st, int b) {
 #pragma unroll
         for (int i = 0; i < NA; i++) {
-            const int q = tid + 512 * i, tok = min(t0 + (q >> 4), T - 1);
+            const int q = tid + PF_NT * i, tok = min(t0 + (q >> 4), T - 1);
             st.a[i] = *(const uint4*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
         }
         const int tb = min(t0 + ((tid >> 2) & (16 * MI - 1)), T - 1);
@@ -326,7 +330,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
     auto stage_store = [&](const Stg& st, int buf) {
 #pragma unroll
         for (int i = 0; i < NA; i++) {
-            const int q = tid + 512 * i, p = q & 15, k = p & 3;
+            const int q = tid + PF_NT * i, p = q & 15, k = p & 3;
             int8_t* d = s_a[buf] + (q >> 4) * PF_AST + 64 * (p >> 2) + 32 * (k & 1) + 8 * (k >> 1);
             *(uint2*)d = make_uint2(st.a[i].x, st.a[i].y);
             *(uint2*)(d + 16) = make_uint2(st.a[i].z, st.a[i].w);
@@ -462,7 +466,7 @@ int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
 #ifndef LG_PF_MI
 #define LG_PF_MI 4
 #endif
-    const dim3 grid((unsigned)(nrb8 * ((T + 16 * LG_PF_MI - 1) / (16 * LG_PF_MI)))), blk(512);
+    const dim3 grid((unsigned)(nrb8 * ((T + 16 * LG_PF_MI - 1) / (16 * LG_PF_MI)))), blk(PF_NT);
     if (accumulate) hipLaunchKernelGGL((k_pf_gemm_q4k<1, LG_PF_MI>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     else hipLaunchKernelGGL((k_pf_gemm_q4k<0, LG_PF_MI>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     return lg_check_launch("prefill gemm");
@@ -479,14 +483,230 @@ int lg_prefill_quantize(const float* x, int ldx, const float* norm_w, float eps,
     return lg_check_launch("prefill quantize");
 }
 
+/* ------------------------------------------------------------------ */
+/* causal attention on fp32 MFMA: 16 query tokens x one KV head          */
+/* ------------------------------------------------------------------ */
+/* One workgroup per (16-token query block, KV head g), one wave per query
+ * head of the group.  Per block of 16 key positions the K and V rows come
+ * from the fp16 cache into LDS as fp32 and each wave computes
+ *   S^T[key][q] = sum_d K[key][d] Q[q][d]        (32 v_mfma_f32_16x16x4f32)
+ *   O^T[d][q]  += sum_key V[key][d] P^T[key][q]  (32 more, 8 tiles of 16 dims)
+ * with an online softmax per query column in log2 units, as k_pf_attn does
+ * per lane group.  Lane l holds query column l%16 and keys/dims 4(l/16)..+3
+ * of each tile (the D layout); the MFMA wants P^T with key l/16 of each
+ * 4-key step, so the four registers are transposed across the four 16-lane
+ * groups by two rounds of v_permlane32_swap / v_permlane16_swap.
+ *
+ * A query's own key and value are its fp32 k/v (the cache holds them in
+ * fp16), as in the token-sequential step: in the key block holding a
+ * query's position its score is recomputed from the fp32 k row, and its
+ * value enters as the fp16 row through the MFMA plus p (v32 - v16).  Key
+ * positions past a query's own are masked.  Only fp32 rounding differs
+ * from k_pf_attn (sum orders). */
+template <int HD, int NREP, int SPLIT>
+__global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float* __restrict__ qkv, int qstride, int n_embed,
+                                                            int kv_dim, const uint16_t* __restrict__ kc,
+                                                            const uint16_t* __restrict__ vc, int pos0, int T,
+                                                            float* __restrict__ att)
+{
+    static_assert(HD == 128, "eight 16-dim output tiles per wave");
+    constexpr int NT = 64 * NREP * SPLIT, NS = HD / 4, VST = HD + 16, OST = HD + 4;
+    __shared__ __attribute__((aligned(16))) float s_kt[SPLIT][NS * 16 * 4];   /* K[key][4s + j] at (s*16 + key)*4 + j */
+    __shared__ __attribute__((aligned(16))) float s_vt[SPLIT][16 * VST];      /* V[key][d] */
+    __shared__ __attribute__((aligned(16))) float s_k32[16 * OST];    /* fp32 k / v of the block's 16 tokens */
+    __shared__ __attribute__((aligned(16))) float s_v32[16 * OST];
+    const int qb = blockIdx.x, g = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, r = (tid >> 6) % NREP, half = (tid >> 6) / NREP;
+    const float* __restrict__ s_k = s_kt[half];
+    const float* __restrict__ s_v = s_vt[half];
+    const int col = lane & 15, grp = lane >> 4;
+    const int t0 = qb * 16, tq = t0 + col, tqc = min(tq, T - 1);
+    const int qpos = pos0 + tq;
+    const int last = pos0 + min(t0 + 15, T - 1);   /* last key position this block reads */
+    const float scale2 = 1.44269504088896341f / sqrtf((float)HD);
+
+    /* B operand of S^T: Q[tq][grp + 4s] */
+    float qv[NS];
+    const float* qrow = qkv + (size_t)tqc * qstride + (size_t)(g * NREP + r) * HD;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; s2++) qv[s2] = qrow[grp + 4 * s2];
+    for (int i = tid; i < 16 * HD; i += NT) {
+        const int tt = i / HD, d = i % HD;
+        const float* row = qkv + (size_t)min(t0 + tt, T - 1) * qstride;
+        s_k32[tt * OST + d] = row[n_embed + g * HD + d];
+        s_v32[tt * OST + d] = row[n_embed + kv_dim + g * HD + d];
+    }
+
+    v4f o[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] = (v4f){0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f;   /* l: this lane group's keys only, summed at the end */
+    const int nkb = last / 16 + 1, nit = (nkb + SPLIT - 1) / SPLIT;
+    /* SPLIT key blocks per step, block SPLIT*it + h for the waves of half h;
+     * the next step's K/V rows load into registers while this one computes:
+     * piece i < SPLIT*256 is 8 dims of one key of one block */
+    constexpr int NPC = SPLIT * 16 * (HD / 8), NSTG = (NPC + NT - 1) / NT;
+    uint4 kq[NSTG], vq[NSTG];
+    auto stage_load = [&](int it) {
+#pragma unroll
+        for (int u = 0; u < NSTG; u++) {
+            const int i = min(tid + u * NT, NPC - 1);
+            const int hb = i / (16 * (HD / 8)), kk = (i / (HD / 8)) % 16, d8 = (i % (HD / 8)) * 8;
+            const size_t off = (size_t)min((it * SPLIT + hb) * 16 + kk, last) * kv_dim + (size_t)g * HD + d8;
+            kq[u] = *(const uint4*)(kc + off);
+            vq[u] = *(const uint4*)(vc + off);
+        }
+    };
+    auto half2 = [](uint32_t w, float& a, float& b) {
+        a = lg_h2f((uint16_t)(w & 0xffffu));
+        b = lg_h2f((uint16_t)(w >> 16));
+    };
+    stage_load(0);
+    for (int it = 0; it < nit; it++) {
+        __syncthreads();   /* the previous step's tiles are consumed */
+#pragma unroll
+        for (int u = 0; u < NSTG; u++) {
+            const int i = tid + u * NT;
+            if (i < NPC) {
+                const int hb = i / (16 * (HD / 8)), kk = (i / (HD / 8)) % 16, d8 = (i % (HD / 8)) * 8;
+                float* sk = s_kt[hb];
+                float* sv4 = s_vt[hb];
+                float4 k0, k1, v0, v1;
+                half2(kq[u].x, k0.x, k0.y);
+                half2(kq[u].y, k0.z, k0.w);
+                half2(kq[u].z, k1.x, k1.y);
+                half2(kq[u].w, k1.z, k1.w);
+                half2(vq[u].x, v0.x, v0.y);
+                half2(vq[u].y, v0.z, v0.w);
+                half2(vq[u].z, v1.x, v1.y);
+                half2(vq[u].w, v1.z, v1.w);
+                *(float4*)&sk[((d8 >> 2) * 16 + kk) * 4] = k0;
+                *(float4*)&sk[(((d8 >> 2) + 1) * 16 + kk) * 4] = k1;
+                *(float4*)&sv4[kk * VST + d8] = v0;
+                *(float4*)&sv4[kk * VST + d8 + 4] = v1;
+            }
+        }
+        __syncthreads();
+        stage_load(min(it + 1, nit - 1));
+        const int kb = it * SPLIT + half;
+        if (kb >= nkb) continue;   /* the other half's last block (wave-uniform) */
+
+        v4f sa = (v4f){0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+        for (int s2 = 0; s2 < NS; s2 += 2) {
+            sa = __builtin_amdgcn_mfma_f32_16x16x4f32(s_k[(s2 * 16 + col) * 4 + grp], qv[s2], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x4f32(s_k[((s2 + 1) * 16 + col) * 4 + grp], qv[s2 + 1], sb, 0, 0, 0);
+        }
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) sv[i] = sa[i] + sb[i];
+        /* the block holds some query's own position: exact fp32 scores */
+        const bool diag = kb * 16 + 15 >= pos0 + t0 && kb * 16 <= pos0 + t0 + 15;
+        const int own = qpos - kb * 16;   /* 0..15 when this lane's query owns a key here */
+        if (diag) {
+            float e = 0.0f;
+#pragma unroll
+            for (int s2 = 0; s2 < NS; s2++) e = __builtin_fmaf(qv[s2], s_k32[col * OST + grp + 4 * s2], e);
+            e += lg_partner<4>(e);
+            e += lg_partner<5>(e);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (own == 4 * grp + i) sv[i] = e;
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sv[i] = kb * 16 + 4 * grp + i > qpos ? -INFINITY : sv[i] * scale2;
+            bm = fmaxf(bm, sv[i]);
+        }
+        bm = fmaxf(bm, lg_partner<4>(bm));
+        bm = fmaxf(bm, lg_partner<5>(bm));
+        const float mn = fmaxf(m, bm);   /* finite: key 0 is in every query's range */
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        float pw[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) pw[i] = __builtin_amdgcn_exp2f(sv[i] - mn);
+        l = __builtin_fmaf(l, alpha, (pw[0] + pw[1]) + (pw[2] + pw[3]));
+        m = mn;
+        float pown = 0.0f;   /* p of the own key, broadcast to the column's four lane groups */
+        if (diag) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (own == 4 * grp + i) pown = pw[i];
+            pown += lg_partner<4>(pown);
+            pown += lg_partner<5>(pown);
+        }
+        /* P^T operands: b[mm] at lane (grp, col) = P^T[4 mm + grp][col] */
+        float b[4] = {pw[0], pw[1], pw[2], pw[3]};
+        {
+            auto x02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(b[0]), __float_as_uint(b[2]), false, false);
+            auto x13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(b[1]), __float_as_uint(b[3]), false, false);
+            auto y01 = __builtin_amdgcn_permlane16_swap(x02[0], x13[0], false, false);
+            auto y23 = __builtin_amdgcn_permlane16_swap(x02[1], x13[1], false, false);
+            b[0] = __uint_as_float(y01[0]);
+            b[1] = __uint_as_float(y01[1]);
+            b[2] = __uint_as_float(y23[0]);
+            b[3] = __uint_as_float(y23[1]);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            o[t] *= alpha;
+#pragma unroll
+            for (int mm = 0; mm < 4; mm++)
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(s_v[(4 * mm + grp) * VST + 16 * t + col], b[mm], o[t], 0,
+                                                            0, 0);
+        }
+        if (diag && own >= 0 && own < 16) {
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int d = 16 * t + 4 * grp + i;
+                    o[t][i] = __builtin_fmaf(pown, s_v32[col * OST + d] - s_v[own * VST + d], o[t][i]);
+                }
+        }
+    }
+    if constexpr (SPLIT == 2) {
+        /* the second half's (m, l, o) into the first half's lanes */
+        __shared__ float s_x[NREP][2 + 32][64];
+        if (half == 1) {
+            s_x[r][0][lane] = m;
+            s_x[r][1][lane] = l;
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) s_x[r][2 + 4 * t + i][lane] = o[t][i];
+        }
+        __syncthreads();
+        if (half == 1) return;
+        const float m1 = s_x[r][0][lane], mx = fmaxf(m, m1);
+        const float a0 = __builtin_amdgcn_exp2f(m - mx), a1 = __builtin_amdgcn_exp2f(m1 - mx);
+        l = lg_fma2(l, a0, s_x[r][1][lane], a1);
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[t][i] = lg_fma2(o[t][i], a0, s_x[r][2 + 4 * t + i][lane], a1);
+    }
+    l += lg_partner<4>(l);
+    l += lg_partner<5>(l);
+    if (tq < T) {
+        float* out = att + (size_t)tq * n_embed + (size_t)(g * NREP + r) * HD;
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) out[16 * t + 4 * grp + i] = o[t][i] / l;
+    }
+}
+
 typedef void (*pf_attn_t)(const float*, int, int, int, const uint16_t*, const uint16_t*, int, float*);
 
 static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_t* kc, const uint16_t* vc, int T,
                        int pos0, float* att, hipStream_t s)
 {
     const int nrep = M.n_heads / M.n_kv;
-    const dim3 grid(T, M.n_kv), blk(256);
     if (M.head_dim != 128) { lg_set_error("prefill attention: head_dim %d", M.head_dim); return LG_ERR_TYPE; }
+#ifdef LG_PF_ATTN_VALU
+    const dim3 grid(T, M.n_kv), blk(256);
     switch (nrep) {
     case 1: hipLaunchKernelGGL((k_pf_attn<128, 1>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
     case 2: hipLaunchKernelGGL((k_pf_attn<128, 2>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
@@ -494,6 +714,22 @@ static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_
     case 8: hipLaunchKernelGGL((k_pf_attn<128, 8>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
     default: lg_set_error("prefill attention: %d query heads per KV head", nrep); return LG_ERR_TYPE;
     }
+#else
+    const dim3 grid((T + 15) / 16, M.n_kv);
+    /* two halves of the key blocks per query head up to 4 query heads per
+     * KV head (8 waves); one at 8 (8 waves already) */
+#define PFA(NR)                                                                                             \
+    hipLaunchKernelGGL((k_pf_attn_mfma<128, NR, (NR <= 4 ? 2 : 1)>), grid, dim3(64 * NR * (NR <= 4 ? 2 : 1)), 0, s, \
+                       qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, T, att)
+    switch (nrep) {
+    case 1: PFA(1); break;
+    case 2: PFA(2); break;
+    case 4: PFA(4); break;
+    case 8: PFA(8); break;
+    default: lg_set_error("prefill attention: %d query heads per KV head", nrep); return LG_ERR_TYPE;
+    }
+#undef PFA
+#endif
     return lg_check_launch("prefill attention");
 }
 
