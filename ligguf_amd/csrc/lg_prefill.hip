@@ -112,140 +112,6 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope_kv(float* __restrict__ qkv, 
 }
 
 /* ------------------------------------------------------------------ */
-/* causal attention: query token t, kv head g                           */
-/* ------------------------------------------------------------------ */
-/* 4 waves; LPP lanes hold one key (8 dims each), 16 keys per workgroup step;
- * an online softmax per lane group in log2 units, groups combined by lane
- * permutes and waves in LDS, as the decode step's attention phase. */
-template <int HD, int NREP>
-__global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ qkv, int qstride, int n_embed, int kv_dim,
-                                                 const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
-                                                 int pos0, float* __restrict__ att)
-{
-    constexpr int LPP = HD / 8, PPW = 64 / LPP, WV = 4, PPB = WV * PPW;
-    __shared__ __attribute__((aligned(16))) float s_q[NREP * HD];
-    __shared__ __attribute__((aligned(16))) float s_kv[2 * HD];
-    __shared__ __attribute__((aligned(16))) float s_o[WV * NREP * HD];
-    __shared__ float s_m[WV * NREP], s_l[WV * NREP];
-    const int t = blockIdx.x, g = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int gl = lane & (LPP - 1), grp = lane / LPP;
-    const int pos = pos0 + t;
-    const float* row = qkv + (size_t)t * qstride;
-    for (int i = threadIdx.x; i < NREP * HD; i += 256) s_q[i] = row[(size_t)g * NREP * HD + i];
-    for (int i = threadIdx.x; i < HD; i += 256) {
-        s_kv[i] = row[n_embed + g * HD + i];
-        s_kv[HD + i] = row[n_embed + kv_dim + g * HD + i];
-    }
-    __syncthreads();
-    const float scale2 = 1.44269504088896341f / sqrtf((float)HD);
-    float qr[NREP][8];
-#pragma unroll
-    for (int r = 0; r < NREP; r++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) qr[r][i] = s_q[r * HD + gl * 8 + i];
-    float m[NREP], l[NREP], o[NREP][8];
-#pragma unroll
-    for (int r = 0; r < NREP; r++) {
-        m[r] = -INFINITY;
-        l[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
-    }
-    /* U steps of K/V rows loaded before any is used (positions past pos
-     * load row 0 and are skipped) */
-    constexpr int U = 4;
-    for (int j00 = 0; j00 <= pos; j00 += U * PPB) {
-        uint4 kbu[U], vbu[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int j = j00 + u * PPB + wave * PPW + grp;
-            const size_t off = (size_t)(j < pos ? j : 0) * kv_dim + (size_t)g * HD + gl * 8;
-            kbu[u] = *(const uint4*)(kc + off);
-            vbu[u] = *(const uint4*)(vc + off);
-        }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-        const int j = j00 + u * PPB + wave * PPW + grp;
-        if (j <= pos) {
-            float kf[8], vf[8];
-            if (j < pos) {
-                const uint4 kb = kbu[u], vb = vbu[u];
-                const uint32_t ku[4] = {kb.x, kb.y, kb.z, kb.w}, vu[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    kf[2 * i] = lg_h2f((uint16_t)(ku[i] & 0xffffu));
-                    kf[2 * i + 1] = lg_h2f((uint16_t)(ku[i] >> 16));
-                    vf[2 * i] = lg_h2f((uint16_t)(vu[i] & 0xffffu));
-                    vf[2 * i + 1] = lg_h2f((uint16_t)(vu[i] >> 16));
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
-            }
-#pragma unroll
-            for (int r = 0; r < NREP; r++) {
-                float sc = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; i++) sc += qr[r][i] * kf[i];
-                sc = lg_group_sum<LPP>(sc) * scale2;
-                const float mn = fmaxf(m[r], sc);
-                const float a = __builtin_amdgcn_exp2f(m[r] - mn);
-                const float pw = __builtin_amdgcn_exp2f(sc - mn);
-                l[r] = l[r] * a + pw;
-#pragma unroll
-                for (int i = 0; i < 8; i++) o[r][i] = lg_fma2(o[r][i], a, pw, vf[i]);
-                m[r] = mn;
-            }
-        }
-    }
-    }
-    /* lane groups (16-lane rows) of the wave into group 0 by lane permutes,
-     * then the waves */
-    static_assert(LPP == 16, "key groups are 16-lane rows");
-#pragma unroll
-    for (int step = 0; step < 2; step++) {
-#pragma unroll
-        for (int r = 0; r < NREP; r++) {
-            const float m2 = step ? lg_from_half_above(m[r]) : lg_from_row_above(m[r]);
-            const float l2 = step ? lg_from_half_above(l[r]) : lg_from_row_above(l[r]);
-            const float mn = fmaxf(m[r], m2);
-            const float a = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - mn);
-            const float bb = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
-            l[r] = lg_fma2(l[r], a, l2, bb);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float o2 = step ? lg_from_half_above(o[r][i]) : lg_from_row_above(o[r][i]);
-                o[r][i] = lg_fma2(o[r][i], a, o2, bb);
-            }
-            m[r] = mn;
-        }
-    }
-    if (grp == 0) {
-#pragma unroll
-        for (int r = 0; r < NREP; r++) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) s_o[(wave * NREP + r) * HD + gl * 8 + i] = o[r][i];
-            if (gl == 0) { s_m[wave * NREP + r] = m[r]; s_l[wave * NREP + r] = l[r]; }
-        }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < NREP * HD; i += 256) {
-        const int r = i / HD, d = i % HD;
-        float M = -INFINITY;
-        for (int w = 0; w < WV; w++) M = fmaxf(M, s_m[w * NREP + r]);
-        float O = 0.0f, L = 0.0f;
-        for (int w = 0; w < WV; w++) {
-            const float mw = s_m[w * NREP + r];
-            const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            O += s_o[(w * NREP + r) * HD + d] * wt;
-            L += s_l[w * NREP + r] * wt;
-        }
-        att[(size_t)t * n_embed + (size_t)g * NREP * HD + i] = O / L;
-    }
-}
-
-/* ------------------------------------------------------------------ */
 /* Q4_K x Q8_K GEMM on int8 MFMA                                        */
 /* ------------------------------------------------------------------ */
 /* Workgroup tile: 16 MI tokens x 128 rows, 8 waves of 16 MI tokens x 16
@@ -491,8 +357,8 @@ int lg_prefill_quantize(const float* x, int ldx, const float* norm_w, float eps,
  * from the fp16 cache into LDS as fp32 and each wave computes
  *   S^T[key][q] = sum_d K[key][d] Q[q][d]        (32 v_mfma_f32_16x16x4f32)
  *   O^T[d][q]  += sum_key V[key][d] P^T[key][q]  (32 more, 8 tiles of 16 dims)
- * with an online softmax per query column in log2 units, as k_pf_attn does
- * per lane group.  Lane l holds query column l%16 and keys/dims 4(l/16)..+3
+ * with an online softmax per query column in log2 units (the decode step's
+ * attention does the same per lane group).  Lane l holds query column l%16 and keys/dims 4(l/16)..+3
  * of each tile (the D layout); the MFMA wants P^T with key l/16 of each
  * 4-key step, so the four registers are transposed across the four 16-lane
  * groups by two rounds of v_permlane32_swap / v_permlane16_swap.
@@ -502,7 +368,7 @@ int lg_prefill_quantize(const float* x, int ldx, const float* norm_w, float eps,
  * query's position its score is recomputed from the fp32 k row, and its
  * value enters as the fp16 row through the MFMA plus p (v32 - v16).  Key
  * positions past a query's own are masked.  Only fp32 rounding differs
- * from k_pf_attn (sum orders). */
+ * from the token-sequential step (sum orders). */
 template <int HD, int NREP, int SPLIT>
 __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float* __restrict__ qkv, int qstride, int n_embed,
                                                             int kv_dim, const uint16_t* __restrict__ kc,
@@ -698,23 +564,11 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
     }
 }
 
-typedef void (*pf_attn_t)(const float*, int, int, int, const uint16_t*, const uint16_t*, int, float*);
-
 static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_t* kc, const uint16_t* vc, int T,
                        int pos0, float* att, hipStream_t s)
 {
     const int nrep = M.n_heads / M.n_kv;
     if (M.head_dim != 128) { lg_set_error("prefill attention: head_dim %d", M.head_dim); return LG_ERR_TYPE; }
-#ifdef LG_PF_ATTN_VALU
-    const dim3 grid(T, M.n_kv), blk(256);
-    switch (nrep) {
-    case 1: hipLaunchKernelGGL((k_pf_attn<128, 1>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
-    case 2: hipLaunchKernelGGL((k_pf_attn<128, 2>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
-    case 4: hipLaunchKernelGGL((k_pf_attn<128, 4>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
-    case 8: hipLaunchKernelGGL((k_pf_attn<128, 8>), grid, blk, 0, s, qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, att); break;
-    default: lg_set_error("prefill attention: %d query heads per KV head", nrep); return LG_ERR_TYPE;
-    }
-#else
     const dim3 grid((T + 15) / 16, M.n_kv);
     /* two halves of the key blocks per query head up to 4 query heads per
      * KV head (8 waves); one at 8 (8 waves already) */
@@ -729,7 +583,6 @@ static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_
     default: lg_set_error("prefill attention: %d query heads per KV head", nrep); return LG_ERR_TYPE;
     }
 #undef PFA
-#endif
     return lg_check_launch("prefill attention");
 }
 

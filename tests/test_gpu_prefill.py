@@ -49,6 +49,9 @@ def test_matmul_tokens_rejects_other_types(gpu):
 Q4K_MODELS = [
     ModelConfig("qwen3-w4096-q4k", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
     ModelConfig("llama-w4096-q4k-nrep1", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q8_0, Q4_K),
+    # the other query-head ratios of the prefill attention kernel: 2 (16/8 heads) and 8 (32/4)
+    ModelConfig("qwen3-w2048-q4k-nrep2", 1, 1, 2048, 16, 8, 128, 6144, 1024, 1024, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
+    ModelConfig("llama-w4096-q4k-nrep8", 0, 1, 4096, 32, 4, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q4_K, Q6_K),
 ]
 
 
