@@ -219,13 +219,14 @@ int lg_quantize_q8_K(const float* x, int64_t n, void* y, void* stream);
 int lg_matvec(int type, const void* w, uint32_t rsz, int n, int d, const void* xq, float* out, int accumulate,
               void* stream);
 
-/* The matvec of T tokens at once on int8 MFMA (the batched prefill's GEMM):
- * out[t*d + r] = row r of w . Q8_K(x[t*n ..]) for t < T, r < d, each fp32 row
- * of x quantized as quantize_q8_K does.  Q4_K weights only, n % 256 == 0.
- * The integer sub-block sums are those of lg_matvec (fast/lil_math.cpp:
- * 582-616); only the fp32 accumulation order differs.  Allocates and frees a
- * workspace of about 1.1*T*n bytes and synchronizes `stream` (tests and
- * benches).  No counterpart in the reference, which calls matmul per token. */
+/* The matvec of T tokens at once on int8 MFMA (the batched prefill's GEMMs):
+ * out[t*d + r] = row r of w . Q(x[t*n ..]) for t < T, r < d, each fp32 row
+ * of x quantized as quantize_q8_K (Q4_K weights) or quantize_q8_0 (Q1_G
+ * weights) does; n % 256 == 0.  The integer block sums are those of
+ * lg_matvec (fast/lil_math.cpp:582-616 for Q4_K, :440-464 for Q1_G); only
+ * the fp32 accumulation order differs.  Allocates and frees a workspace of
+ * about 1.3*T*n bytes and synchronizes `stream` (tests and benches).  No
+ * counterpart in the reference, which calls matmul per token. */
 int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, int d, const float* x, int T, float* out,
                      void* stream);
 

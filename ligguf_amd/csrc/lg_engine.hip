@@ -625,18 +625,21 @@ extern "C" int lg_decode_path(const lg_ctx* ctx)
 /* ------------------------------------------------------------------ */
 #define LG_PF_TMAX 512   /* tokens per layer pass */
 
-/* the batched prefill serves models whose layer matrices are all Q4_K (Q|K|V
- * and up|gate stacked), widths multiples of 256, head_dim 128 */
+/* the batched prefill serves models whose layer matrices are all Q4_K or
+ * all Q1_G (Q|K|V and up|gate stacked), widths multiples of 256, head_dim
+ * 128 */
 static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
 {
     ctx->pf_ok = false;
     const int nrep = m->n_heads / m->n_kv_heads;
     bool ok = m->n_embed % 256 == 0 && m->n_ff % 256 == 0 && m->head_dim == 128 &&
               (nrep == 1 || nrep == 2 || nrep == 4 || nrep == 8) && !ctx->layers.empty();
+    const int wt = ok ? ctx->layers[0].qkv.type : -1;
+    ok = ok && (wt == LG_Q4_K || wt == LG_Q1_G);
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
-        ok = D.qkv_fused && D.ug_fused && D.qkv.type == LG_Q4_K && D.att_out.type == LG_Q4_K && D.ug.type == LG_Q4_K &&
-             D.down.type == LG_Q4_K && D.down.cols == m->n_ff;
+        ok = D.qkv_fused && D.ug_fused && D.qkv.type == wt && D.att_out.type == wt && D.ug.type == wt &&
+             D.down.type == wt && D.down.cols == m->n_ff;
     }
     if (!ok) return;
     ctx->pf_layers.resize(m->n_layers);
@@ -649,6 +652,7 @@ static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
     }
     PfModel& M = ctx->pf_model;
     M.layers = ctx->pf_layers.data();
+    M.wtype = wt;
     M.n_layers = m->n_layers; M.n_embed = m->n_embed; M.n_heads = m->n_heads; M.n_kv = m->n_kv_heads;
     M.head_dim = m->head_dim; M.kv_dim = m->kv_dim; M.n_ff = m->n_ff; M.n_ctx = m->n_context;
     M.rope_dim = m->rope_dim; M.eps = m->rms_epsilon;
@@ -663,7 +667,8 @@ static int prefill_buffers(lg_ctx* c)
     if (c->pf.tmax) return LG_OK;
     PfBuffers B = {};
     const int tmax = std::min(LG_PF_TMAX, (c->n_context + 3) / 4 * 4);
-    const size_t ne = c->n_embed, qs = ne + 2 * (size_t)c->kv_dim, nff = c->n_ff, nbm = nff / 256;
+    /* activation blocks of width n_ff: nff/256 Q8_K or nff/32 Q8_0 scales per token */
+    const size_t ne = c->n_embed, qs = ne + 2 * (size_t)c->kv_dim, nff = c->n_ff, nbm = nff / 256, nb0 = nff / 32;
     int rc;
     if ((rc = dalloc(c, (void**)&B.toks, (size_t)tmax * sizeof(int)))) return rc;
     if ((rc = dalloc(c, (void**)&B.x, (size_t)tmax * ne * 4))) return rc;
@@ -671,8 +676,9 @@ static int prefill_buffers(lg_ctx* c)
     if ((rc = dalloc(c, (void**)&B.att, (size_t)tmax * ne * 4))) return rc;
     if ((rc = dalloc(c, (void**)&B.ug, (size_t)tmax * 2 * nff * 4))) return rc;
     if ((rc = dalloc(c, (void**)&B.q.qs, (size_t)tmax * nff))) return rc;
-    if ((rc = dalloc(c, (void**)&B.q.d, nbm * tmax * 4))) return rc;
+    if ((rc = dalloc(c, (void**)&B.q.d, nb0 * tmax * 4))) return rc;
     if ((rc = dalloc(c, (void**)&B.q.bs, (size_t)tmax * nbm * 16 * 2))) return rc;
+    if ((rc = dalloc(c, (void**)&B.q.as, nb0 * tmax * 4))) return rc;
     B.q.tld = tmax;
     B.tmax = tmax;
     c->pf = B;
@@ -1068,23 +1074,32 @@ extern "C" int lg_prefill_path(const lg_ctx* ctx)
 extern "C" int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, int d, const float* x, int T, float* out,
                                 void* stream)
 {
-    if (type != LG_Q4_K) { lg_set_error("matmul_tokens: type %d (Q4_K only)", type); return LG_ERR_TYPE; }
+    if (type != LG_Q4_K && type != LG_Q1_G) {
+        lg_set_error("matmul_tokens: type %d (Q4_K or Q1_G only)", type);
+        return LG_ERR_TYPE;
+    }
     if (!w || !x || !out || n <= 0 || n % 256 || d <= 0 || T <= 0) {
         lg_set_error("matmul_tokens: bad arguments (n %d, d %d, T %d)", n, d, T);
         return LG_ERR_ARG;
     }
-    const int tld = (T + 3) / 4 * 4, nb = n / 256;
+    /* workspace: quants, then scales for n/32 blocks (enough for either
+     * form), the Q8_K bsums and the Q8_0 sums */
+    const int tld = (T + 3) / 4 * 4, nb = n / 256, nb0 = n / 32;
     PfQ8K q = {};
     q.tld = tld;
-    const size_t bytes = (size_t)tld * n + (size_t)nb * tld * 4 + (size_t)tld * nb * 32;
+    const size_t o_d = (size_t)tld * n, o_bs = o_d + (size_t)nb0 * tld * 4, o_as = o_bs + (size_t)tld * nb * 32;
+    const size_t bytes = o_as + (size_t)nb0 * tld * 4;
     uint8_t* ws = nullptr;
     const hipError_t e = hipMalloc((void**)&ws, bytes);
     if (e != hipSuccess) { lg_set_error("matmul_tokens: hipMalloc(%zu): %s", bytes, hipGetErrorString(e)); return LG_ERR_NOMEM; }
     q.qs = (int8_t*)ws;
-    q.d = (float*)(ws + (size_t)tld * n);
-    q.bs = (int16_t*)(ws + (size_t)tld * n + (size_t)nb * tld * 4);
-    int rc = lg_prefill_quantize(x, n, nullptr, 0.0f, n, T, q, (hipStream_t)stream);
-    if (!rc) rc = lg_prefill_gemm_q4k((const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream);
+    q.d = (float*)(ws + o_d);
+    q.bs = (int16_t*)(ws + o_bs);
+    q.as = (int*)(ws + o_as);
+    const bool q1 = type == LG_Q1_G;
+    int rc = lg_prefill_quantize(q1 ? LG_Q8_0 : LG_Q8_K, x, n, nullptr, 0.0f, n, T, q, (hipStream_t)stream);
+    if (!rc) rc = q1 ? lg_prefill_gemm_q1g((const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream)
+                     : lg_prefill_gemm_q4k((const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream);
     const hipError_t e2 = hipStreamSynchronize((hipStream_t)stream);
     hipFree(ws);
     if (!rc && e2 != hipSuccess) { lg_set_error("matmul_tokens: %s", hipGetErrorString(e2)); rc = LG_ERR_HIP; }

@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include "lg_common.h"
+#include "lg_fmt.h"
 #include "lg_prefill.h"
 #include "lg_quant.h"
 #include "lg_rope.h"
@@ -57,8 +58,34 @@ __device__ __forceinline__ void pf_store_q8k(const float v[4], const PfQ8K& q, i
     if (lane == 0) q.d[(size_t)b * q.tld + t] = r.d;
 }
 
-/* block b of token t: rmsnorm(x_t) * w (w != NULL) or x_t, quantized; the
- * sum of squares in the decode kernels' order (fast/lil_math.cpp:922-929) */
+/* one 256-value chunk of one token as eight Q8_0 blocks in the SoA form:
+ * qs as the Q8_K form, d [K/32][tld] the fp16 scale as the reference
+ * stores it (read back as float), asum [K/32][tld] the blocks' sums of q */
+__device__ __forceinline__ void pf_store_q8_0(const float v[4], const PfQ8K& q, int n, int t, int b)
+{
+    const int lane = threadIdx.x & 63;
+    const Q80Lane r = lg_q8_0_lane(v);
+    *(uint32_t*)(q.qs + (size_t)t * n + b * 256 + 4 * lane) = r.packed;
+    /* the block's sum of q over its 8 lanes: integers below 2^24, exact in fp32 */
+    const int bs = (int)lg_group_sum<8>((float)lg_dot4((int)r.packed, 0x01010101, 0));
+    if ((lane & 7) == 0) {
+        const size_t i = (size_t)(8 * b + (lane >> 3)) * q.tld + t;
+        q.d[i] = lg_h2f(lg_f2h(r.d));
+        q.as[i] = bs;
+    }
+}
+
+template <int QT>
+__device__ __forceinline__ void pf_store(const float v[4], const PfQ8K& q, int n, int t, int b)
+{
+    if constexpr (QT == LG_Q8_K) pf_store_q8k(v, q, n, t, b);
+    else pf_store_q8_0(v, q, n, t, b);
+}
+
+/* block b of token t: rmsnorm(x_t) * w (w != NULL) or x_t, quantized (Q8_K
+ * or Q8_0); the sum of squares in the decode kernels' order
+ * (fast/lil_math.cpp:922-929) */
+template <int QT>
 __global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, int ldx, const float* __restrict__ w,
                                                  float eps, int n, PfQ8K q)
 {
@@ -76,11 +103,12 @@ __global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, in
         const float4 g = *(const float4*)(w + base);
         v[0] = tv.x * scale * g.x; v[1] = tv.y * scale * g.y; v[2] = tv.z * scale * g.z; v[3] = tv.w * scale * g.w;
     }
-    pf_store_q8k(v, q, n, t, b);
+    pf_store<QT>(v, q, n, t, b);
 }
 
 /* hb = silu(gate) * up of token t (fast/ligguf_fast_qk.cpp:119-123), block b,
  * quantized; ug row = [up | gate] */
+template <int QT>
 __global__ __launch_bounds__(64) void k_pf_swiglu_quant(const float* __restrict__ ug, int nff, PfQ8K q)
 {
     const int lane = threadIdx.x, b = blockIdx.x, t = blockIdx.y;
@@ -93,7 +121,7 @@ __global__ __launch_bounds__(64) void k_pf_swiglu_quant(const float* __restrict_
     v[1] = (g.y / (1.0f + expf(-g.y))) * u.y;
     v[2] = (g.z / (1.0f + expf(-g.z))) * u.z;
     v[3] = (g.w / (1.0f + expf(-g.w))) * u.w;
-    pf_store_q8k(v, q, nff, t, b);
+    pf_store<QT>(v, q, nff, t, b);
 }
 
 /* QK-norm + RoPE + KV rows of token t at position pos0 + t */
@@ -338,15 +366,164 @@ int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
     return lg_check_launch("prefill gemm");
 }
 
-int lg_prefill_quantize(const float* x, int ldx, const float* norm_w, float eps, int n, int T, const PfQ8K& q,
-                        hipStream_t s)
+int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w, float eps, int n, int T,
+                        const PfQ8K& q, hipStream_t s)
 {
-    if (!x || n <= 0 || n % 256 || T <= 0 || T > q.tld || ldx < n) {
-        lg_set_error("prefill quantize: bad arguments (n %d, T %d)", n, T);
+    if (!x || n <= 0 || n % 256 || T <= 0 || T > q.tld || ldx < n || (qtype != LG_Q8_K && qtype != LG_Q8_0)) {
+        lg_set_error("prefill quantize: bad arguments (type %d, n %d, T %d)", qtype, n, T);
         return LG_ERR_ARG;
     }
-    hipLaunchKernelGGL(k_pf_quant, dim3(n / 256, T), dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    if (qtype == LG_Q8_K) hipLaunchKernelGGL(k_pf_quant<LG_Q8_K>, dim3(n / 256, T), dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    else hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, dim3(n / 256, T), dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
     return lg_check_launch("prefill quantize");
+}
+
+/* ------------------------------------------------------------------ */
+/* Q1_G x Q8_0 GEMM on int8 MFMA                                        */
+/* ------------------------------------------------------------------ */
+/* A Q1_G block (18 B: fp16 d, 128 sign bits, bit i of byte i/8 = value i)
+ * meets four Q8_0 activation blocks of 32.  dot_q8_0_q1_G
+ * (fast/lil_math.cpp:440-464) takes per 32-value block the integer
+ * 2 s1 - asum (s1 = sum of q where the bit is set, asum = sum of q) and
+ * d_w * sum_j d_a,j (2 s1_j - asum_j).  Here s1 is one
+ * v_mfma_i32_16x16x32_i8 per block with the bits as 0/1 bytes (K = 32: each
+ * 32-value block has its own activation scale, so the products cannot run
+ * over two blocks), asum comes with the activation, and
+ * out += d_w * sum_j d_a,j (2 s1_j - asum_j) in fp32 per 128-value group.
+ * Tile and staging as k_pf_gemm_q4k: 128 rows x 64 tokens per workgroup, 8
+ * waves of 16 rows x 4 token tiles; per group the token tile's 128 quants
+ * per token (rows padded to 144 B), the scales and asums in LDS,
+ * double-buffered; lane group g takes values 8g..8g+7 of each block. */
+#define PF1_AST 144
+template <int ACC>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_gemm_q1g(
+    const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
+{
+    constexpr int MI = 4;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][64 * PF1_AST];
+    __shared__ __attribute__((aligned(16))) float s_d[2][4][64];
+    __shared__ __attribute__((aligned(16))) int s_s[2][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int ng = K >> 7;
+    const int nt = (T + 63) / 64;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int rb = (slot / nt) * 8 + xcd;
+    if (rb * 128 >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
+    const int t0 = (slot % nt) * 64;
+    const int r0 = rb * 128 + wave * 16;
+    const uint8_t* wr = W + (size_t)min(r0 + l16, R - 1) * rsz;
+
+    /* staging per group: thread tid takes 16 quants (token tid/8, piece
+     * tid%8); threads < 64 four scales and four asums (block tid/16,
+     * tokens 4(tid%16)..) */
+    struct Stg {
+        uint4 a;
+        float4 d;
+        int4 s;
+    };
+    auto stage_load = [&](Stg& st, int gi) {
+        const int tok = min(t0 + (tid >> 3), T - 1);
+        st.a = *(const uint4*)(x.qs + (size_t)tok * K + (size_t)gi * 128 + (tid & 7) * 16);
+        const size_t di = (size_t)(4 * gi + ((tid >> 4) & 3)) * x.tld + min(t0 + 4 * (tid & 15), x.tld - 4);
+        st.d = *(const float4*)(x.d + di);
+        st.s = *(const int4*)(x.as + di);
+    };
+    auto stage_store = [&](const Stg& st, int buf) {
+        *(uint4*)(s_a[buf] + (tid >> 3) * PF1_AST + (tid & 7) * 16) = st.a;
+        if (tid < 64) {
+            *(float4*)&s_d[buf][tid >> 4][4 * (tid & 15)] = st.d;
+            *(int4*)&s_s[buf][tid >> 4][4 * (tid & 15)] = st.s;
+        }
+    };
+    struct Blk {
+        uint32_t d;
+        uint4 bits;
+    };
+    auto blk_load = [&](Blk& B, int gi) {
+        const uint8_t* p = wr + (size_t)gi * LG_BS_Q1_G;
+        B.d = lg_ld16(p);
+        B.bits = lg_ld<uint4>(p + 2);
+    };
+
+    v4f acc[MI];
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) acc[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int gi, const Blk& cur) {
+        const int buf = gi & 1;
+        const uint32_t bw[4] = {cur.bits.x, cur.bits.y, cur.bits.z, cur.bits.w};
+        const float dw = lg_h2f((uint16_t)cur.d);
+        v4f ga[MI];
+#pragma unroll
+        for (int mi = 0; mi < MI; mi++) ga[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
+        const int8_t* sa = s_a[buf] + l16 * PF1_AST + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            /* bits 32j + 8g.. = byte 4j + g of the 16 sign bytes */
+            const uint32_t b8 = (bw[j] >> (8 * g)) & 0xFFu;
+            const long bb = (long)((uint64_t)(uint32_t)bits4_to_bytes(b8 & 15u) |
+                                   ((uint64_t)(uint32_t)bits4_to_bytes(b8 >> 4) << 32));
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++) {
+                const long af = *(const long*)(sa + 16 * mi * PF1_AST + 32 * j);
+                const v4i s1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bb, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                const float4 da = *(const float4*)&s_d[buf][j][16 * mi + 4 * g];
+                const int4 as = *(const int4*)&s_s[buf][j][16 * mi + 4 * g];
+                const float dav[4] = {da.x, da.y, da.z, da.w};
+                const int asv[4] = {as.x, as.y, as.z, as.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) ga[mi][i] = __builtin_fmaf(dav[i], (float)(2 * s1[i] - asv[i]), ga[mi][i]);
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[mi][i] = __builtin_fmaf(dw, ga[mi][i], acc[mi][i]);
+    };
+
+    Blk cur, nxt;
+    Stg st;
+    stage_load(st, 0);
+    blk_load(cur, 0);
+    stage_store(st, 0);
+    __syncthreads();
+    for (int gi = 0; gi < ng; gi++) {
+        const int gn = min(gi + 1, ng - 1);
+        stage_load(st, gn);
+        blk_load(nxt, gn);
+        compute(gi, cur);
+        stage_store(st, (gi + 1) & 1);
+        cur = nxt;
+        __syncthreads();
+    }
+    const int r = r0 + l16;
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 16 * mi + 4 * g + i;
+            if (t < T && r < R) {
+                float* o = out + (size_t)t * ldo + r;
+                *o = ACC ? *o + acc[mi][i] : acc[mi][i];
+            }
+        }
+    }
+}
+
+int lg_prefill_gemm_q1g(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                        int accumulate, hipStream_t s)
+{
+    if (!W || !out || !x.as || rows <= 0 || cols <= 0 || cols % 256 || T <= 0 || T > x.tld || x.tld % 4 ||
+        rsz != (uint32_t)(cols / 128) * LG_BS_Q1_G || ldo < rows) {
+        lg_set_error("prefill gemm Q1_G: bad arguments (rows %d, cols %d, T %d)", rows, cols, T);
+        return LG_ERR_ARG;
+    }
+    const int nrb8 = (rows + 127) / 128 + 7 & ~7;
+    const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
+    if (accumulate) hipLaunchKernelGGL((k_pf_gemm_q1g<1>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    else hipLaunchKernelGGL((k_pf_gemm_q1g<0>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    return lg_check_launch("prefill gemm Q1_G");
 }
 
 /* ------------------------------------------------------------------ */
@@ -593,6 +770,12 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
         return LG_ERR_STATE;
     }
     const int ne = M.n_embed, kvd = M.kv_dim, qs = ne + 2 * kvd, nff = M.n_ff;
+    const bool q1 = M.wtype == LG_Q1_G;
+    const int qt = q1 ? LG_Q8_0 : LG_Q8_K;
+    auto gemm = [&](const uint8_t* W, uint32_t rsz, int rows, int cols, float* o, int ldo, int acc) {
+        return q1 ? lg_prefill_gemm_q1g(W, rsz, rows, cols, B.q, T, o, ldo, acc, s)
+                  : lg_prefill_gemm_q4k(W, rsz, rows, cols, B.q, T, o, ldo, acc, s);
+    };
     int rc;
     hipLaunchKernelGGL(k_pf_embed, dim3(T), dim3(256), 0, s, M.embd_t, M.embd, M.embd_rsz, B.toks, ne, B.x);
     if ((rc = lg_check_launch("prefill embedding"))) return rc;
@@ -601,21 +784,22 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
         uint16_t* kc = M.kc + (size_t)l * M.n_ctx * kvd;
         uint16_t* vc = M.vc + (size_t)l * M.n_ctx * kvd;
         /* attention branch */
-        if ((rc = lg_prefill_quantize(B.x, ne, L.att_norm, M.eps, ne, T, B.q, s))) return rc;
-        if ((rc = lg_prefill_gemm_q4k(L.qkv, L.qkv_rsz, qs, ne, B.q, T, B.qkv, qs, 0, s))) return rc;
+        if ((rc = lg_prefill_quantize(qt, B.x, ne, L.att_norm, M.eps, ne, T, B.q, s))) return rc;
+        if ((rc = gemm(L.qkv, L.qkv_rsz, qs, ne, B.qkv, qs, 0))) return rc;
         const int waves = M.n_heads + M.n_kv;
         hipLaunchKernelGGL(k_pf_qk_rope_kv, dim3((waves + 3) / 4, T), dim3(256), 0, s, B.qkv, qs, ne, kvd, L.q_norm,
                            L.k_norm, M.n_heads, M.n_kv, M.head_dim, M.rope_dim, pos0, M.rope_freq, M.eps, kc, vc);
         if ((rc = lg_check_launch("prefill qk-norm/rope/kv"))) return rc;
         if ((rc = launch_attn(M, B.qkv, qs, kc, vc, T, pos0, B.att, s))) return rc;
-        if ((rc = lg_prefill_quantize(B.att, ne, nullptr, M.eps, ne, T, B.q, s))) return rc;
-        if ((rc = lg_prefill_gemm_q4k(L.ao, L.ao_rsz, ne, ne, B.q, T, B.x, ne, 1, s))) return rc;
+        if ((rc = lg_prefill_quantize(qt, B.att, ne, nullptr, M.eps, ne, T, B.q, s))) return rc;
+        if ((rc = gemm(L.ao, L.ao_rsz, ne, ne, B.x, ne, 1))) return rc;
         /* FFN branch */
-        if ((rc = lg_prefill_quantize(B.x, ne, L.ffn_norm, M.eps, ne, T, B.q, s))) return rc;
-        if ((rc = lg_prefill_gemm_q4k(L.ug, L.ug_rsz, 2 * nff, ne, B.q, T, B.ug, 2 * nff, 0, s))) return rc;
-        hipLaunchKernelGGL(k_pf_swiglu_quant, dim3(nff / 256, T), dim3(64), 0, s, B.ug, nff, B.q);
+        if ((rc = lg_prefill_quantize(qt, B.x, ne, L.ffn_norm, M.eps, ne, T, B.q, s))) return rc;
+        if ((rc = gemm(L.ug, L.ug_rsz, 2 * nff, ne, B.ug, 2 * nff, 0))) return rc;
+        if (q1) hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_0>, dim3(nff / 256, T), dim3(64), 0, s, B.ug, nff, B.q);
+        else hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_K>, dim3(nff / 256, T), dim3(64), 0, s, B.ug, nff, B.q);
         if ((rc = lg_check_launch("prefill swiglu"))) return rc;
-        if ((rc = lg_prefill_gemm_q4k(L.down, L.down_rsz, ne, nff, B.q, T, B.x, ne, 1, s))) return rc;
+        if ((rc = gemm(L.down, L.down_rsz, ne, nff, B.x, ne, 1))) return rc;
     }
     return LG_OK;
 }

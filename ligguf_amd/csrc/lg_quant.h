@@ -158,13 +158,18 @@ __device__ __forceinline__ void lg_q8k_block(const float v[4], uint8_t* __restri
     if (lane == 0) *(float*)out = q.d;
 }
 
-/* Eight Q8_0 blocks from the wave's 256 values (block = lane/8), or fewer
- * when nvalid < 256.  quantize_q8_0 as compiled (fast/lil_math.cpp:329-351
- * under -Ofast): d = amax * (1/127), id = 127/amax, q = roundf(x*id). */
-__device__ __forceinline__ void lg_q8_0_blocks(const float v[4], uint8_t* __restrict__ out, int nvalid)
+/* one lane's 4 values of the wave's eight Q8_0 blocks (block = lane/8):
+ * quantize_q8_0 as compiled (fast/lil_math.cpp:329-351 under -Ofast):
+ * d = amax * (1/127), id = 127/amax, q = roundf(x*id); every lane of the
+ * wave takes part (group maximum over 8 lanes) */
+struct Q80Lane {
+    uint32_t packed;   /* the lane's 4 int8 values */
+    float d;           /* its block's scale, before the fp16 store */
+};
+
+__device__ __forceinline__ Q80Lane lg_q8_0_lane(const float v[4])
 {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -172,20 +177,30 @@ __device__ __forceinline__ void lg_q8_0_blocks(const float v[4], uint8_t* __rest
         if (amax < a) amax = a;
     }
     amax = lg_group_max_nn<8>(amax);
-    const int blk = lane >> 3;
-    if (32 * blk >= nvalid) return;
-    const float d = amax * (1.0f / 127.0f);
+    Q80Lane r;
+    r.d = amax * (1.0f / 127.0f);
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    uint8_t* b = out + LG_BS_Q8_0 * blk;
-    uint32_t packed = 0;
+    r.packed = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int q = (int)roundf(v[j] * id);
-        packed |= (uint32_t)(q & 255) << (8 * j);
+        r.packed |= (uint32_t)(q & 255) << (8 * j);
     }
-    __builtin_memcpy(b + 2 + 4 * (lane & 7), &packed, 4);
+    return r;
+}
+
+/* Eight Q8_0 blocks from the wave's 256 values (block = lane/8), or fewer
+ * when nvalid < 256 */
+__device__ __forceinline__ void lg_q8_0_blocks(const float v[4], uint8_t* __restrict__ out, int nvalid)
+{
+    const int lane = threadIdx.x & 63;
+    const Q80Lane r = lg_q8_0_lane(v);
+    const int blk = lane >> 3;
+    if (32 * blk >= nvalid) return;
+    uint8_t* b = out + LG_BS_Q8_0 * blk;
+    __builtin_memcpy(b + 2 + 4 * (lane & 7), &r.packed, 4);
     if ((lane & 7) == 0) {
-        const uint16_t dh = lg_f2h(d);
+        const uint16_t dh = lg_f2h(r.d);
         __builtin_memcpy(b, &dh, 2);
     }
 }

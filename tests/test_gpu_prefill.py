@@ -1,12 +1,13 @@
-"""The batched prefill: lg_matmul_tokens (the int8 MFMA GEMM of T tokens)
+"""The batched prefill: lg_matmul_tokens (the int8 MFMA GEMMs of T tokens)
 against the oracle's matvec of every token, and lg_prefill with
 LG_PREFILL_BATCHED against the token-by-token prefill (LG_PREFILL_STEPS,
-itself bit-equal to sequential decode steps) and against the oracle.
+itself bit-equal to sequential decode steps) and against the oracle, for
+Q4_K and Q1_G models.
 
-The GEMM reproduces the integer sub-block sums of the reference's Q4_K x Q8_K
-dot exactly (fast/lil_math.cpp:582-616) and combines them in fp32 per
-256-value block, so each output is held to the matvec bar: within 2e-6 of the
-row's sum of |terms|.  Whole prompts accumulate fp32 order differences over
+The GEMMs reproduce the integer block sums of the reference's Q4_K x Q8_K
+and Q1_G x Q8_0 dots exactly (fast/lil_math.cpp:582-616, :440-464) and
+combine them in fp32 per block, so each output is held to the matvec bar:
+within 2e-6 of the row's sum of |terms|.  Whole prompts accumulate fp32 order differences over
 their tokens; an activation that lands on the other side of an int8 rounding
 boundary moves later logits by up to ~2e-2 (the same effect the decode tests
 document), so the prompt checks bound the logits and the KV cache loosely and
@@ -15,7 +16,7 @@ import numpy as np
 import pytest
 
 from ligguf_amd import encode, ops
-from ligguf_amd.lib import (PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS, Q4_K, Q5_K, Q6_K, Q8_0, LgError,
+from ligguf_amd.lib import (PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0, LgError,
                             row_size)
 from ligguf_amd.model import Engine, HostModel, ModelConfig
 from test_gpu_decode import oracle_state, rel
@@ -39,6 +40,22 @@ def test_matmul_tokens_vs_oracle(gpu, oracle, d, n, T):
         assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
 
 
+@pytest.mark.parametrize("d,n,T", [(200, 512, 37), (130, 256, 1), (384, 12288, 5), (4096, 4096, 64)])
+def test_matmul_tokens_q1g_vs_oracle(gpu, oracle, d, n, T):
+    """The Q1_G x Q8_0 GEMM (one int8 MFMA per 32-value block) against the
+    oracle's matvec of each token's Q8_0 activation."""
+    rng = np.random.default_rng(d + T + 1)
+    w = encode.random_tensor(Q1_G, d + n + 1, Q1_G, d, n)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    rsz = row_size(Q1_G, n)
+    y = host(ops.matmul_tokens(Q1_G, dev(w, gpu), rsz, n, d, dev(x, gpu)))
+    toks = range(T) if T <= 40 else rng.choice(T, 12, replace=False)
+    for t in toks:
+        ref, ab = oracle.matvec_q(Q1_G, w, rsz, n, d, oracle.quantize_q8_0(x[t]), want_abs=True)
+        err = np.abs(y[t] - ref) / np.maximum(ab, 1e-30)
+        assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
+
+
 def test_matmul_tokens_rejects_other_types(gpu):
     x = dev(np.zeros((2, 256), np.float32), gpu)
     w = dev(np.zeros(row_size(Q6_K, 256) * 4, np.uint8), gpu)
@@ -46,17 +63,19 @@ def test_matmul_tokens_rejects_other_types(gpu):
         ops.matmul_tokens(Q6_K, w, row_size(Q6_K, 256), 256, 4, x)
 
 
-Q4K_MODELS = [
+BATCHED_MODELS = [
     ModelConfig("qwen3-w4096-q4k", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
     ModelConfig("llama-w4096-q4k-nrep1", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q8_0, Q4_K),
     # the other query-head ratios of the prefill attention kernel: 2 (16/8 heads) and 8 (32/4)
     ModelConfig("qwen3-w2048-q4k-nrep2", 1, 1, 2048, 16, 8, 128, 6144, 1024, 1024, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
     ModelConfig("llama-w4096-q4k-nrep8", 0, 1, 4096, 32, 4, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q4_K, Q6_K),
+    # Q1_G layers (Q1_G x Q8_0 GEMM), Q8_0 embedding and output
+    ModelConfig("qwen3-w4096-q1g", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q1_G, Q8_0, Q8_0),
 ]
 
 
-@pytest.fixture(scope="module", params=Q4K_MODELS, ids=lambda c: c.name)
-def q4k_model(request, gpu):
+@pytest.fixture(scope="module", params=BATCHED_MODELS, ids=lambda c: c.name)
+def pf_model(request, gpu):
     cfg = request.param
     hm = HostModel.synthetic(cfg)
     eng = Engine(0)
@@ -71,8 +90,8 @@ def run_prefill(eng, path, prompt, pos0=0):
     return lg, eng.argmax()
 
 
-def test_prefill_path_selection(q4k_model):
-    hm, eng = q4k_model
+def test_prefill_path_selection(pf_model):
+    hm, eng = pf_model
     eng.set_prefill_path(PREFILL_AUTO)
     assert eng.prefill_path() == PREFILL_BATCHED
     eng.set_prefill_path(PREFILL_STEPS)
@@ -86,13 +105,13 @@ def near_best(lg, tok, tol=3e-2):
 
 
 @pytest.mark.parametrize("n", [2, 33, 200])
-def test_batched_equals_steps(q4k_model, n):
+def test_batched_equals_steps(pf_model, n):
     """Against the token-by-token prefill, beside the distance between the two
     token-by-token paths (fused kernels and one kernel per op) on the same
     prompt: an int8 flip moves a whole later-layer KV row, for every path
     pair alike.  Layer 0's K/V depend on their own token only, so they agree
     to fp16 rounding."""
-    hm, eng = q4k_model
+    hm, eng = pf_model
     cfg = hm.cfg
     prompt = np.random.default_rng(n).integers(1, cfg.vocab, n)
     lg_s, tok_s = run_prefill(eng, PREFILL_STEPS, prompt)
@@ -122,10 +141,10 @@ def test_batched_equals_steps(q4k_model, n):
     assert np.array_equal(a, eng.decode(int(tok_s), n))
 
 
-def test_batched_prefill_vs_oracle(q4k_model, oracle):
+def test_batched_prefill_vs_oracle(pf_model, oracle):
     """The last token's logits of a 24-token prompt against the oracle's
     sequential inference() over the same prompt."""
-    hm, eng = q4k_model
+    hm, eng = pf_model
     cfg = hm.cfg
     prompt = np.random.default_rng(77).integers(1, cfg.vocab, 24)
     st = oracle_state(oracle, hm)
@@ -139,10 +158,10 @@ def test_batched_prefill_vs_oracle(q4k_model, oracle):
     assert near_best(ref, tok_b)
 
 
-def test_batched_prefill_in_several_passes(q4k_model):
+def test_batched_prefill_in_several_passes(pf_model):
     """A prompt longer than one pass (512 tokens) continues the KV cache across
     passes; at pos0 > 0 the pass reads the rows before it."""
-    hm, eng = q4k_model
+    hm, eng = pf_model
     cfg = hm.cfg
     n = min(600, cfg.n_context - 8)
     prompt = np.random.default_rng(5).integers(1, cfg.vocab, n)
