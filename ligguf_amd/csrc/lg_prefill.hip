@@ -393,10 +393,11 @@ int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w,
  * Tile and staging as k_pf_gemm_q4k: 128 rows x 64 tokens per workgroup, 8
  * waves of 16 rows x 4 token tiles; per group the token tile's 128 quants
  * per token (rows padded to 144 B), the scales and asums in LDS,
- * double-buffered; lane group g takes values 8g..8g+7 of each block. */
+ * double-buffered; lane group g takes values 8g..8g+7 of each block.  Up to
+ * 256 VGPRs (one workgroup per CU): held to 128 the compiler spilled ~110. */
 #define PF1_AST 144
 template <int ACC>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_gemm_q1g(
+__global__ __launch_bounds__(512) void k_pf_gemm_q1g(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
     constexpr int MI = 4;
