@@ -182,8 +182,8 @@ def isolated_kernels(torch, np):
 def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
     """The 1-bit workload: Qwen3-8B shape with Q1_G layers (group 128, sign
     bits, fp16 group scales |N(0,0.02)|) and Q8_0 embedding/output, an
-    8192-token prompt of random ids fed through lg_prefill (token by token:
-    the batched prefill takes Q4_K layers only), then greedy decode at
+    8192-token prompt of random ids fed through lg_prefill (batched: 16 layer
+    passes of 512 tokens on the Q1_G x Q8_0 GEMM), then greedy decode at
     positions 8192.. .  Reports prefill and decode tok/s and the decode
     token roofline (weight + KV bytes per token over the time)."""
     from ligguf_amd.model import QWEN3_8B_Q1G, Engine, HostModel

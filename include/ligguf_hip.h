@@ -176,7 +176,8 @@ int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* logits_host
  * int8 MFMA GEMMs, the tokens' integer sub-block sums and quantizers those
  * of the step; the logits then match n sequential steps to fp32 rounding (an
  * int8 rounding of an activation may differ in rare tokens).  Needs Q4_K
- * layer matrices (Q|K|V and up|gate stackable) and head_dim 128.  STEPS: one
+ * or Q1_G layer matrices, one type throughout (Q|K|V and up|gate
+ * stackable), and head_dim 128.  STEPS: one
  * decode step per token, bit-equal to n lg_decode_step calls.  AUTO (the
  * default): BATCHED when the model allows it and n >= 2, else STEPS.
  * lg_prefill_path reports what a prompt of 2+ tokens takes (-1 without a
