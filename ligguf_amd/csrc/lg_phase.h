@@ -638,20 +638,24 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     float* pml_m = pml + (size_t)(P.att_slots - 1) * P.n_heads * 2;
 
     stamp(tr, 0);
-    uint4 kb[MAXST], vb[MAXST];   /* K/V slices of the unit's steps (static indices only) */
+    /* K/V slices of the unit's steps (static indices only): one batch of
+     * MAXST steps, or (BATCHES) two sets of MAXST/2 steps, the next one
+     * loading while the other computes */
+    constexpr int NB = BATCHES ? 2 : 1, H = MAXST / NB;
+    uint4 kb[NB][H], vb[NB][H];
     float4 hx[NH], hv;            /* this wave's heads h = wave + PK_WAVES*j: q (h < NQ) or k, and v */
     /* unconditional loads (see Rows): positions outside the unit and the
      * row pos itself (not in the cache yet) load the unit's first row */
-    auto load_kv = [&](int u, int sb) {   /* the register batch of steps sb.. */
+    auto load_kv = [&](int set, int u, int sb) {   /* steps sb..sb+H-1 into set `set` */
         const int g = (u % ngc) / nch, c = (u % ngc) % nch;
         const int t0 = c * chunk, t1 = min(t0 + chunk, pos + 1);
 #pragma unroll
-        for (int st = 0; st < MAXST; st++) {
+        for (int st = 0; st < H; st++) {
             int t = t0 + (sb + st) * PPB + wave * PPW + grp;
             t = t < t1 && t != pos ? t : t0;
             const size_t o = loff + (size_t)t * kvd + (size_t)g * HD + gl * 8;
-            kb[st] = *(const uint4*)(P.kc + o);
-            vb[st] = *(const uint4*)(P.vc + o);
+            kb[set][st] = *(const uint4*)(P.kc + o);
+            vb[set][st] = *(const uint4*)(P.vc + o);
         }
     };
     /* q/k norm weights (a dummy slice of the rope table when the model has
@@ -688,7 +692,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
         load_heads(u);
         lg_issue_order();   /* heads first, then K/V */
-        load_kv(u, 0);
+        load_kv(0, u, 0);
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
         *(float4*)(s_kv + HD + l4) = hv;
@@ -741,17 +745,16 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 #pragma unroll
             for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
         }
-        /* register batches of MAXST steps; the next batch's loads follow
-         * the current batch's use (one round trip per batch) */
-        for (int sb = 0;;) {
+        /* the steps of set `set` from step sb on, in step order */
+        auto process = [&](int set, int sb) {
 #pragma unroll
-            for (int st = 0; st < MAXST; st++) {
+            for (int st = 0; st < H; st++) {
                 const int t = t0 + (sb + st) * PPB + wave * PPW + grp;
                 if (sb + st < nsteps && t < t1) {
                     float kf[8], vf[8];
                     if (t != pos) {
-                        h8(kb[st], kf);
-                        h8(vb[st], vf);
+                        h8(kb[set][st], kf);
+                        h8(vb[set][st], vf);
                     } else {
 #pragma unroll
                         for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
@@ -775,9 +778,19 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     }
                 }
             }
-            sb += MAXST;
-            if (!BATCHES || sb >= nsteps) break;   /* one batch: chunks of <= MAXST steps */
-            load_kv(u, sb);
+        };
+        if (!BATCHES) {
+            process(0, 0);   /* one batch: chunks of <= MAXST steps */
+        } else {
+            /* half-batches alternate between the two sets; the set not being
+             * computed loads (past the last step: clamped rows, unused) */
+            for (int sb = 0; sb < nsteps; sb += 2 * H) {
+                load_kv(NB - 1, u, sb + H);
+                process(0, sb);
+                if (sb + H >= nsteps) break;
+                load_kv(0, u, sb + 2 * H);
+                process(NB - 1, sb + H);
+            }
         }
         /* combine the position groups of the wave into group 0 (16-lane
          * rows: row 1 -> 0 and 3 -> 2, then 2 -> 0, by lane permutes), then
@@ -832,7 +845,9 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
             if (s_int[0]) {
                 /* last unit of these heads: merge their nch partials, weights
                  * through LDS, each thread one output value over the chunks
-                 * with 8 loads in flight (the consumer's formula) */
+                 * with 32 loads in flight (one round trip for up to 32
+                 * chunks, the grid's share at 8 KV heads; the consumer's
+                 * formula) */
                 float* s_ml = s_sc;                                   /* [nch][NQ][2] */
                 float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NQ] */
                 for (int i = LG_TID; i < nch * NQ; i += PK_THREADS) {
@@ -858,12 +873,12 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     const int r = i / HD;
                     const float* col = po + (size_t)q0 * HD + i;
                     float acc = 0.0f;
-                    for (int c0 = 0; c0 < nch; c0 += 8) {
-                        float v[8];
+                    for (int c0 = 0; c0 < nch; c0 += 32) {
+                        float v[32];
 #pragma unroll
-                        for (int k = 0; k < 8; k++) v[k] = c0 + k < nch ? cld(col + (size_t)(c0 + k) * P.n_embed) : 0.0f;
+                        for (int k = 0; k < 32; k++) v[k] = cld(col + (size_t)min(c0 + k, nch - 1) * P.n_embed);
 #pragma unroll
-                        for (int k = 0; k < 8; k++)
+                        for (int k = 0; k < 32; k++)
                             if (c0 + k < nch) acc += v[k] * s_w[(c0 + k) * NQ + r];
                     }
                     /* the merged vector as a one-chunk partial (m 0, l 1) */
