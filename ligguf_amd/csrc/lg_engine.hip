@@ -382,7 +382,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         /* per-layer attention partials, each written once per step */
         const size_t L = (size_t)m->n_layers;
         float* ws = nullptr;
-        const size_t slots = (size_t)att_nch + 1;
+        const size_t slots = (size_t)std::max(att_nch, PK_ATT_MERGE) + 1;   /* chunks (at least the short path's), then the merged one */
         if ((rc = dalloc(ctx, (void**)&ws, L * slots * ((size_t)m->n_embed + 2 * m->n_heads) * sizeof(float))))
             return rc;
         P.att_slots = (int)slots;

@@ -58,8 +58,23 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const P
                                                        int l)
 {
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
-    if constexpr (LONG) phase_attn<HD, NREP, NREP, true>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
-    else phase_attn<HD, NREP, 1, false>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
+    if constexpr (LONG) {
+        phase_attn<HD, NREP, NREP, true>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
+    } else {
+        /* the position through a vector load issued first (its index made
+         * opaque, so the compiler keeps it per lane instead of moving it to
+         * a scalar register at once): the short units' loads do not depend
+         * on it and go out behind it; phase_attn waits for it after them.
+         * A scalar load would be waited for (lgkmcnt) with the kernel
+         * arguments, before any of them. */
+        uint64_t* tr = f_tr(Sd, l, 1);
+        stamp(tr, 0);   /* before the position load: a later wait for the stamp's store would wait for it too */
+        int z;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+        const int pos = cld(&Sd->pos + z);
+        lg_issue_order();
+        phase_attn<HD, NREP, 1, false>(P, L, l, pos, P.qkv + (size_t)l * qs, 0, 0, tr, false);
+    }
 }
 
 template <int LT, int HD, int NREP>

@@ -122,15 +122,24 @@ const void* lg_persist_kernel(int layer_type, int out_type, int head_dim, int nr
 int lg_persist_grid(const void* kernel, int* nwg);
 int lg_persist_launch(const void* kernel, const PkParams& P, const PkStep* S, int nwg, hipStream_t s);
 
+/* short contexts: chunks of a fixed pk_att_fch positions (one register
+ * batch at most), one query head per unit, unit u = (kv head u % n_kv,
+ * query head (u / n_kv) % nrep of its group, chunk u / n_heads).  No part of
+ * a unit's rows depends on the step's position, so its loads are issued
+ * before the position arrives (the fused kernels read it from memory);
+ * units past the context skip their work. */
+__host__ __device__ constexpr int pk_att_fch(int head_dim, int nrep)
+{
+    return pk_att_steps(nrep) * (PK_THREADS * 8 / head_dim) < 128 ? pk_att_steps(nrep) * (PK_THREADS * 8 / head_dim)
+                                                                   : 128;
+}
+
 /* attention at position pos takes the long-context units (whole query-head
- * groups, register batches) unless every unit is one batch of one query
- * head with a workgroup of its own */
+ * groups, register batches, pk_attn_split) unless the context fits
+ * PK_ATT_MERGE fixed chunks and every short unit has a workgroup of its own */
 __host__ __device__ inline bool pk_att_long(int pos, int head_dim, int nrep, int n_kv, int nwg)
 {
-    int chunk, nch;
-    pk_attn_split(pos + 1, head_dim, nrep, nwg / n_kv, &chunk, &nch);
-    const bool single = chunk <= pk_att_steps(nrep) * (PK_THREADS * 8 / head_dim);
-    return !(single && pk_att_one_head(n_kv, nrep, nch, nwg));
+    return !(pos + 1 <= PK_ATT_MERGE * pk_att_fch(head_dim, nrep) && pk_att_one_head(n_kv, nrep, PK_ATT_MERGE, nwg));
 }
 
 /* the fused per-phase kernels of one step (lg_fused.hip): 5*n_layers + 1

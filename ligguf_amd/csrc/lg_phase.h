@@ -240,12 +240,18 @@ __device__ __forceinline__ int pk_att_max_nch(const PkParams& P)
 }
 
 /* the attention partials of layer l at position pos as the att_out build
- * reads them: the chunks (pk_attn_split), or the merged slot */
+ * reads them: the fixed chunks (short contexts), the chunks of
+ * pk_attn_split, or the merged slot */
 template <int HD, int NREP>
 __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int pos)
 {
     int chunk, nch;
-    pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
+    if (!pk_att_long(pos, HD, NREP, P.n_kv, gridDim.x)) {
+        chunk = pk_att_fch(HD, NREP);
+        nch = (pos + chunk) / chunk;
+    } else {
+        pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
+    }
     const size_t slot = (size_t)l * P.att_slots + (nch > PK_ATT_MERGE ? P.att_slots - 1 : 0);
     return MergeSrc{P.att_po + slot * P.n_embed, P.att_pml + slot * P.n_heads * 2, nch > PK_ATT_MERGE ? 1 : nch, HD};
 }
@@ -609,10 +615,11 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * merged slot.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
 template <int HD, int NREP, int NQ, bool BATCHES>
-__device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos,
+__device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos_arg,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
-                                           uint64_t* tr)
+                                           uint64_t* tr, bool stamp0 = true)
 {
+    int pos = pos_arg;   /* FIX: first read after the unit's loads (below) */
     constexpr int LPP = HD / 8;            /* lanes per position */
     constexpr int PPW = 64 / LPP;          /* positions per wave step */
     constexpr int PPB = PK_WAVES * PPW;    /* positions per WG step */
@@ -624,10 +631,20 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int gl = lane & (LPP - 1), grp = lane / LPP;
     const int kvd = P.kv_dim;
-    int chunk, nch;
-    pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
-    const int ngc = P.n_kv * nch;           /* (kv head, chunk) pairs */
-    const int nunits = ngc * NSUB;
+    /* FIX (the short-context units): fixed chunks, position-free rows */
+    constexpr bool FIX = !BATCHES;
+    static_assert(!FIX || NQ == 1, "short-context units hold one query head");
+    /* (FIX: nch is computed after the unit's loads are issued, the first use
+     * of pos) */
+    int chunk, nch = 0;
+    if (FIX) chunk = pk_att_fch(HD, NREP);
+    else pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
+    const int ngc = FIX ? 0 : P.n_kv * nch;   /* (kv head, chunk) pairs */
+    const int nunits = FIX ? P.n_heads * PK_ATT_MERGE : ngc * NSUB;
+    /* unit -> kv head, chunk, query-head subset */
+    auto unit_g = [&](int u) { return FIX ? u % P.n_kv : (u % ngc) / nch; };
+    auto unit_c = [&](int u) { return FIX ? u / P.n_heads : (u % ngc) % nch; };
+    auto unit_q = [&](int u) { return FIX ? (u / P.n_kv) % NREP : u / ngc; };
     const size_t loff = (size_t)layer * P.n_ctx * kvd;
     const float scale2 = 1.44269504088896341f / sqrtf((float)HD);   /* log2(e) / sqrt(head_dim) */
     float* po = P.att_po + (size_t)layer * P.att_slots * P.n_embed;
@@ -637,7 +654,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     float* po_m = po + (size_t)(P.att_slots - 1) * P.n_embed;
     float* pml_m = pml + (size_t)(P.att_slots - 1) * P.n_heads * 2;
 
-    stamp(tr, 0);
+    if (stamp0) stamp(tr, 0);
     /* K/V slices of the unit's steps (static indices only): one batch of
      * MAXST steps, or (BATCHES) two sets of MAXST/2 steps, the next one
      * loading while the other computes */
@@ -647,12 +664,15 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     /* unconditional loads (see Rows): positions outside the unit and the
      * row pos itself (not in the cache yet) load the unit's first row */
     auto load_kv = [&](int set, int u, int sb) {   /* steps sb..sb+H-1 into set `set` */
-        const int g = (u % ngc) / nch, c = (u % ngc) % nch;
-        const int t0 = c * chunk, t1 = min(t0 + chunk, pos + 1);
+        const int g = unit_g(u), c = unit_c(u);
+        const int t0 = c * chunk;
 #pragma unroll
         for (int st = 0; st < H; st++) {
             int t = t0 + (sb + st) * PPB + wave * PPW + grp;
-            t = t < t1 && t != pos ? t : t0;
+            /* FIX: every row of the chunk inside the cache (rows past pos
+             * are loaded and not used); else rows of the unit below pos */
+            if (FIX) t = min(t, P.n_ctx - 1);
+            else t = t < min(t0 + chunk, pos + 1) && t != pos ? t : t0;
             const size_t o = loff + (size_t)t * kvd + (size_t)g * HD + gl * 8;
             kb[set][st] = *(const uint4*)(P.kc + o);
             vb[set][st] = *(const uint4*)(P.vc + o);
@@ -665,7 +685,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     float4 ng[NH];
     float2 fr;
     auto load_heads = [&](int u) {
-        const int g = (u % ngc) / nch, q0 = g * NREP + (u / ngc) * NQ;
+        const int g = unit_g(u), q0 = g * NREP + unit_q(u) * NQ;
 #pragma unroll
         for (int j = 0; j < NH; j++) {
             const int h = min(wave + PK_WAVES * j, NQ);
@@ -679,20 +699,34 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     };
     const bool has = (int)blockIdx.x < nunits;
     if (wait_target) pk_wait(P, wait_target);
-    if (!has) stamp(tr, 1);
+    if (!FIX && !has) stamp(tr, 1);   /* FIX: after the loop (no store ahead of the unit's loads) */
 
-    for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
-        /* units ordered (q-head subset, kv head, chunk): the NSUB units that
-         * read the same K/V rows sit ngc apart, on the same XCD (and L2)
-         * when ngc is a multiple of 8 */
-        const int g = (u % ngc) / nch, c = (u % ngc) % nch, qsub = u / ngc;
+    /* one unit: the loads, QK-norm/RoPE (+ the KV row), scores, partials */
+    auto do_unit = [&](int u) {
+        /* long-context units ordered (q-head subset, kv head, chunk): the
+         * NSUB units that read the same K/V rows sit ngc apart, on the same
+         * XCD (and L2) when ngc is a multiple of 8; short ones (kv head
+         * fastest) put a kv head's query heads and chunks on one XCD when
+         * n_kv is a multiple of 8 */
+        const int g = unit_g(u), c = unit_c(u), qsub = unit_q(u);
         const int q0 = g * NREP + qsub * NQ;   /* first query head of the unit */
         const int t0 = c * chunk;
-        const int t1 = min(t0 + chunk, pos + 1);
-        const int nsteps = (t1 - t0 + PPB - 1) / PPB;
         load_heads(u);
         lg_issue_order();   /* heads first, then K/V */
         load_kv(0, u, 0);
+        if (FIX) {
+            /* the position from here on: an empty asm pins its first use
+             * behind the loads above (it may still be in flight) */
+            asm volatile("" : "+v"(pos));
+            pos = __builtin_amdgcn_readfirstlane(pos);
+            nch = (pos + chunk) / chunk;
+        }
+        if (FIX && c >= nch) {   /* a chunk past the context */
+            if (u == (int)blockIdx.x) stamp(tr, 1);
+            return;
+        }
+        const int t1 = min(t0 + chunk, pos + 1);
+        const int nsteps = (t1 - t0 + PPB - 1) / PPB;
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
         *(float4*)(s_kv + HD + l4) = hv;
@@ -892,7 +926,15 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
             }
         }
         bar();
+    };
+    if (FIX) {
+        /* at most one unit per workgroup (pk_att_long): no loop, so no
+         * wait at a loop head for loads of a previous iteration */
+        if (has) do_unit((int)blockIdx.x);
+    } else {
+        for (int u = blockIdx.x; u < nunits; u += gridDim.x) do_unit(u);
     }
+    if (FIX && !has) stamp(tr, 1);
     stamp(tr, 2);
     if (sig) pk_signal(P, sig);
     stamp(tr, 3);
