@@ -215,7 +215,7 @@ def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
     path = {1: "persistent", 2: "multi-kernel", 3: "fused-graph"}.get(eng.path(), "?")
     eng.close()
     mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
-    out = {"workload": "qwen3-8b-shape Q1_G layers, Q8_0 embedding/output, 8192-token prompt then greedy decode",
+    out = {"workload": f"qwen3-8b-shape Q1_G layers, Q8_0 embedding/output, {ctx}-token prompt then greedy decode",
            "prefill_tok_s": round(ctx / pf_s, 1), "decode_tok_s": round(steps / dt, 1),
            "ms_per_token": round(dt / steps * 1e3, 4), "positions": [p_first, pos - 1],
            "bytes_per_token": int(mean_bytes), "hbm_roofline_frac_token": round(mean_bytes / (dt / steps) / HBM_PEAK, 4),
@@ -287,6 +287,9 @@ def main() -> int:
                     help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill: the prompt twice, the second timed (for MFMA counter runs)")
+    ap.add_argument("--q1g-only", action="store_true",
+                    help="run only the Q1_G long-context workload and print its line (profiling)")
+    ap.add_argument("--q1g-ctx", type=int, default=8192, help="prompt length of the Q1_G workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the decode path here is single-GPU (asked for --gpus {args.gpus}).",
@@ -307,6 +310,10 @@ def main() -> int:
         roof = dominant_kernel_roofline(eng, cfg)
         eng.close()
         print(json.dumps({"roofline": roof, "copy": copy_gbs}), flush=True)
+        return 0
+
+    if args.q1g_only:
+        print(json.dumps({"q1g": q1g_context(torch, np, ctx=args.q1g_ctx)}), flush=True)
         return 0
 
     if args.prefill_only:
@@ -372,7 +379,7 @@ def main() -> int:
         log(f"dominant kernel: {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of HBM peak)")
     eng.close()
 
-    q1g = None if args.no_q1g else q1g_context(torch, np)
+    q1g = None if args.no_q1g else q1g_context(torch, np, ctx=args.q1g_ctx)
 
     cpu = None
     if not args.no_cpu:
