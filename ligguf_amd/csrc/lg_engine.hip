@@ -382,7 +382,8 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         /* per-layer attention partials, each written once per step */
         const size_t L = (size_t)m->n_layers;
         float* ws = nullptr;
-        const size_t slots = (size_t)std::max(att_nch, PK_ATT_MERGE) + 1;   /* chunks (at least the short path's), then the merged one */
+        /* chunks (at least the short path's), then the merged groups */
+        const size_t slots = (size_t)std::max(att_nch, PK_ATT_MERGE) + PK_ATT_MERGE;
         if ((rc = dalloc(ctx, (void**)&ws, L * slots * ((size_t)m->n_embed + 2 * m->n_heads) * sizeof(float))))
             return rc;
         P.att_slots = (int)slots;
@@ -391,7 +392,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     }
     /* one zeroed block for the counters and flags */
     const int nwg = ctx->pk_nwg;
-    const size_t cnt_bytes = 256 + (size_t)nwg * (8 + 4 + 4) + 64;
+    const size_t cnt_bytes = 256 + (size_t)nwg * (8 + 4 + 4) + 32 * PK_ATT_MERGE * 4;
     uint8_t* blk = nullptr;
     if ((rc = dalloc(ctx, (void**)&blk, cnt_bytes))) return rc;
     LG_HIP_CHECK(hipMemset(blk, 0, cnt_bytes));
@@ -399,10 +400,10 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.amax_v = (float*)(blk + (size_t)nwg * 8);                    /* nwg x 4 B */
     P.amax_i = (int*)(blk + (size_t)nwg * 12);                     /* nwg x 4 B */
     uint8_t* tail = blk + (size_t)nwg * 16;
-    P.attn_cnt = (uint32_t*)tail;                                  /* up to 32 heads */
-    P.amax_cnt = (uint32_t*)(tail + 128);
-    P.tok_out = (int*)(tail + 192);                                /* {token, error} */
-    P.err = (uint32_t*)(tail + 196);
+    P.amax_cnt = (uint32_t*)tail;
+    P.tok_out = (int*)(tail + 64);                                 /* {token, error} */
+    P.err = (uint32_t*)(tail + 68);
+    P.attn_cnt = (uint32_t*)(tail + 256);                          /* up to 32 heads x PK_ATT_MERGE groups */
     P.spin_cap = 1 << 20;
     /* fused path: device step record, prompt feed, pinned staging */
     if ((rc = dalloc(ctx, (void**)&ctx->step_dev, sizeof(PkStep)))) return rc;

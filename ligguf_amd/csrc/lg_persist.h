@@ -53,8 +53,8 @@ struct PkParams {
     float* logits;
     float* att_po;           /* [n_layers][att_slots][n_embed] unnormalised attention partials */
     float* att_pml;          /* [n_layers][att_slots][n_heads][2] their (max, sum), log2 units */
-    int att_slots;           /* per layer: one per chunk, then one for the vector merged in-kernel */
-    uint32_t* attn_cnt;      /* one per unit head set (n_kv * NREP / NQ <= 32), zero between launches */
+    int att_slots;           /* per layer: one per chunk, then PK_ATT_MERGE for the groups merged in-kernel */
+    uint32_t* attn_cnt;      /* [unit head sets (n_kv * NREP / NQ <= 32)][PK_ATT_MERGE groups], zero between launches */
     uint64_t* progress;      /* one word per workgroup */
     float* amax_v;           /* per-workgroup argmax partials */
     int* amax_i;
@@ -83,7 +83,8 @@ struct PkStep {
  * into at most PK_ATT_MERGE chunks per head, whose partials the att_out build
  * merges; longer ones into max_nch chunks (the grid's workgroups per head
  * group, clamped to [PK_ATT_MERGE, PK_ATT_MAX_NCH]) of one or more batches,
- * merged by the last unit of each head. */
+ * merged in at most PK_ATT_MERGE groups of pk_att_group chunks (by the last
+ * unit of each group), the att_out build merging the groups. */
 __host__ __device__ constexpr int pk_att_steps(int nrep)
 {
     return nrep > 4 ? 4 : 8;
@@ -114,6 +115,16 @@ __host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nre
     }
     *chunk_out = chunk;
     *nch_out = (ctx_len + chunk - 1) / chunk;
+}
+
+/* long contexts: chunks per merge group and the group count (<= PK_ATT_MERGE) */
+__host__ __device__ constexpr int pk_att_group(int nch)
+{
+    return (nch + PK_ATT_MERGE - 1) / PK_ATT_MERGE;
+}
+__host__ __device__ constexpr int pk_att_ngroups(int nch)
+{
+    return (nch + pk_att_group(nch) - 1) / pk_att_group(nch);
 }
 
 /* the kernel instantiated for (layer type, output type, head_dim, query heads

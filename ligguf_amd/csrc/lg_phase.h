@@ -241,7 +241,7 @@ __device__ __forceinline__ int pk_att_max_nch(const PkParams& P)
 
 /* the attention partials of layer l at position pos as the att_out build
  * reads them: the fixed chunks (short contexts), the chunks of
- * pk_attn_split, or the merged slot */
+ * pk_attn_split, or past PK_ATT_MERGE of those their group slots */
 template <int HD, int NREP>
 __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int pos)
 {
@@ -252,8 +252,10 @@ __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int p
     } else {
         pk_attn_split(pos + 1, HD, NREP, pk_att_max_nch(P), &chunk, &nch);
     }
-    const size_t slot = (size_t)l * P.att_slots + (nch > PK_ATT_MERGE ? P.att_slots - 1 : 0);
-    return MergeSrc{P.att_po + slot * P.n_embed, P.att_pml + slot * P.n_heads * 2, nch > PK_ATT_MERGE ? 1 : nch, HD};
+    const bool grp = nch > PK_ATT_MERGE;
+    const size_t slot = (size_t)l * P.att_slots + (grp ? P.att_slots - PK_ATT_MERGE : 0);
+    return MergeSrc{P.att_po + slot * P.n_embed, P.att_pml + slot * P.n_heads * 2,
+                    grp ? pk_att_ngroups(nch) : nch, HD};
 }
 
 /* rmsnorm(x) * w quantized into s_act (fast/lil_math.cpp:922-929 and
@@ -611,8 +613,8 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * 8 dims each); the lane groups of a wave combine by lane permutes, the
  * waves in LDS.  Output: the unit's unnormalised partial (o, and (m, l) per
  * head), merged by the consumer's build (MergeSrc); past PK_ATT_MERGE chunks
- * the last unit of the heads (atomic counter) merges them into the layer's
- * merged slot.  The first unit of g's last chunk also writes the fp16 cache
+ * the last unit of each group of pk_att_group chunks (atomic counter) merges
+ * the group into one of the layer's PK_ATT_MERGE group slots.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
 template <int HD, int NREP, int NQ, bool BATCHES>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos_arg,
@@ -649,10 +651,11 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     const float scale2 = 1.44269504088896341f / sqrtf((float)HD);   /* log2(e) / sqrt(head_dim) */
     float* po = P.att_po + (size_t)layer * P.att_slots * P.n_embed;
     float* pml = P.att_pml + (size_t)layer * P.att_slots * P.n_heads * 2;
-    /* the merged slot: written by nobody else in a launch, so no cache
-     * holds a stale copy of it */
-    float* po_m = po + (size_t)(P.att_slots - 1) * P.n_embed;
-    float* pml_m = pml + (size_t)(P.att_slots - 1) * P.n_heads * 2;
+    /* the group slots (past PK_ATT_MERGE chunks, chunk c merged into group
+     * c / gsz by the group's last unit): written by nobody else in a launch,
+     * so no cache holds a stale copy of them */
+    float* po_m = po + (size_t)(P.att_slots - PK_ATT_MERGE) * P.n_embed;
+    float* pml_m = pml + (size_t)(P.att_slots - PK_ATT_MERGE) * P.n_heads * 2;
 
     if (stamp0) stamp(tr, 0);
     /* K/V slices of the unit's steps (static indices only): one batch of
@@ -869,23 +872,28 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
             }
         }
         if (nch > PK_ATT_MERGE) {
+            /* chunk c belongs to group c / gsz (at most PK_ATT_MERGE groups):
+             * the group's last unit (atomic counter per heads and group)
+             * merges its chunks into the group slot as one partial (o, m, l);
+             * the att_out build merges the groups */
+            const int gsz = pk_att_group(nch), G = c / gsz;
+            const int c_lo = G * gsz, cnt = min(gsz, nch - c_lo);
+            uint32_t* ctr = &P.attn_cnt[(g * NSUB + qsub) * PK_ATT_MERGE + G];
             wait_stores();
             bar();
             if (LG_TID == 0) {
-                const uint32_t old = __hip_atomic_fetch_add(&P.attn_cnt[g * NSUB + qsub], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                s_int[0] = old == (uint32_t)(nch - 1);
+                const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_int[0] = old == (uint32_t)(cnt - 1);
             }
             bar();
             if (s_int[0]) {
-                /* last unit of these heads: merge their nch partials, weights
-                 * through LDS, each thread one output value over the chunks
-                 * with 32 loads in flight (one round trip for up to 32
-                 * chunks, the grid's share at 8 KV heads; the consumer's
-                 * formula) */
-                float* s_ml = s_sc;                                   /* [nch][NQ][2] */
-                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [nch][NQ] */
-                for (int i = LG_TID; i < nch * NQ; i += PK_THREADS) {
-                    const float2 v = cld2(&pml[((size_t)(i / NQ) * P.n_heads + q0 + i % NQ) * 2]);
+                /* weights through LDS, then each thread one output value
+                 * over the group's chunks, 8 loads in flight (the
+                 * consumer's formula, without the division) */
+                float* s_ml = s_sc;                                   /* [cnt][NQ][2] */
+                float* s_w = s_sc + PK_ATT_MAX_NCH * 2 * PK_MAX_NREP; /* [cnt][NQ] */
+                for (int i = LG_TID; i < cnt * NQ; i += PK_THREADS) {
+                    const float2 v = cld2(&pml[((size_t)(c_lo + i / NQ) * P.n_heads + q0 + i % NQ) * 2]);
                     s_ml[2 * i] = v.x;
                     s_ml[2 * i + 1] = v.y;
                 }
@@ -893,36 +901,32 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                 if (LG_TID < NQ) {
                     const int r = LG_TID;
                     float M = -INFINITY;
-                    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_ml[(cc * NQ + r) * 2]);
+                    for (int cc = 0; cc < cnt; cc++) M = fmaxf(M, s_ml[(cc * NQ + r) * 2]);
                     float Ls = 0.0f;
-                    for (int cc = 0; cc < nch; cc++) {
+                    for (int cc = 0; cc < cnt; cc++) {
                         const float wgt = lg_exp2(s_ml[(cc * NQ + r) * 2] - M);
                         s_w[cc * NQ + r] = wgt;
                         Ls += s_ml[(cc * NQ + r) * 2 + 1] * wgt;
                     }
-                    s_red[r] = Ls;
+                    cst(&pml_m[((size_t)G * P.n_heads + q0 + r) * 2], M);
+                    cst(&pml_m[((size_t)G * P.n_heads + q0 + r) * 2 + 1], Ls);
                 }
                 bar();
                 for (int i = LG_TID; i < NQ * HD; i += PK_THREADS) {
                     const int r = i / HD;
-                    const float* col = po + (size_t)q0 * HD + i;
+                    const float* col = po + (size_t)c_lo * P.n_embed + (size_t)q0 * HD + i;
                     float acc = 0.0f;
-                    for (int c0 = 0; c0 < nch; c0 += 32) {
-                        float v[32];
+                    for (int c0 = 0; c0 < cnt; c0 += 8) {
+                        float v[8];
 #pragma unroll
-                        for (int k = 0; k < 32; k++) v[k] = cld(col + (size_t)min(c0 + k, nch - 1) * P.n_embed);
+                        for (int k = 0; k < 8; k++) v[k] = cld(col + (size_t)min(c0 + k, cnt - 1) * P.n_embed);
 #pragma unroll
-                        for (int k = 0; k < 32; k++)
-                            if (c0 + k < nch) acc += v[k] * s_w[(c0 + k) * NQ + r];
+                        for (int k = 0; k < 8; k++)
+                            if (c0 + k < cnt) acc += v[k] * s_w[(c0 + k) * NQ + r];
                     }
-                    /* the merged vector as a one-chunk partial (m 0, l 1) */
-                    cst(&po_m[(size_t)q0 * HD + i], acc / s_red[r]);
+                    cst(&po_m[(size_t)G * P.n_embed + (size_t)q0 * HD + i], acc);
                 }
-                if (LG_TID < NQ) {
-                    cst(&pml_m[(size_t)(q0 + LG_TID) * 2], 0.0f);
-                    cst(&pml_m[(size_t)(q0 + LG_TID) * 2 + 1], 1.0f);
-                }
-                if (LG_TID == 0) cst(&P.attn_cnt[g * NSUB + qsub], 0u);
+                if (LG_TID == 0) cst(ctr, 0u);
             }
         }
         bar();
