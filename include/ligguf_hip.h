@@ -165,6 +165,21 @@ int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters, float* av
  * (sampler_greedy, fast/ligguf_fast_qk.cpp:146-160). */
 int lg_argmax(lg_ctx* ctx, int* tok_out);
 
+/* Top-p / top-k sampling of the current device logits (sampler_topp,
+ * fast/ligguf_fast_qk.cpp:172-214, with g_m.temp, g_m.topp, g_m.topk as
+ * arguments): softmax at temperature temp, entries by probability descending
+ * (ties: lower token first), the cutoff where the cumulative probability
+ * reaches topp (topp <= 0: the first entry's; above 1: 1) or topk entries
+ * (topk <= 0: all), then the entry where it reaches r01 times the cutoff's.
+ * r01 is the caller's uniform draw in [0, 1] -- the reference's
+ * (float)rand() / (float)RAND_MAX.  temp <= 0 gives lg_argmax's token.
+ * The first call allocates a workspace of 5 x vocab entries.  Synchronous. */
+int lg_sample_topp(lg_ctx* ctx, float temp, float topp, int topk, float r01, int* tok_out);
+
+/* lg_sample_topp over n device floats at logits_dev (no context; allocates
+ * and frees its workspace per call, runs on the null stream).  Synchronous. */
+int lg_sample_topp_device(const float* logits_dev, int n, float temp, float topp, int topk, float r01, int* tok_out);
+
 /* feed_text's prompt loop (fast/ligguf_fast_qk.cpp:340-356): n tokens at
  * positions pos0..pos0+n-1, equal to n sequential lg_decode_step calls;
  * logits of the last token to logits_host (NULL allowed). */

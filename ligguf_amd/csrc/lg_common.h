@@ -263,6 +263,15 @@ int lg_launch_embed(int type, const uint8_t* table, uint32_t rsz, const int* tok
                     hipStream_t s);
 int lg_launch_argmax(const float* x, int n, int* out, hipStream_t s);
 
+/* lg_sample.hip: top-p / top-k sampling on the device */
+struct LgSampleWs;
+int lg_sample_ws_alloc(int n, LgSampleWs** out);
+void lg_sample_ws_free(LgSampleWs* w);
+int lg_sample_ws_size(const LgSampleWs* w);
+int* lg_sample_ws_out(LgSampleWs* w);
+int lg_launch_sample_topp(const float* logits, LgSampleWs* w, float temp, float topp, int topk, float r01,
+                          hipStream_t s);
+
 /* lg_matvec.hip */
 int lg_launch_matvec(int type, const void* w, uint32_t rsz, int n, int d, const void* xq, float* out, int accumulate,
                      hipStream_t s);

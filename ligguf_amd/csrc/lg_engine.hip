@@ -127,6 +127,7 @@ struct lg_ctx {
     float* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     int* argmax_dev = nullptr;
+    LgSampleWs* samp = nullptr;  /* top-p sampler workspace, vocab entries */
 
     /* persistent one-launch-per-token path (lg_persist.hip) */
     bool pk_ok = false;          /* the loaded model fits it */
@@ -234,6 +235,7 @@ extern "C" int lg_destroy(lg_ctx* ctx)
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     free_model(ctx);
+    lg_sample_ws_free(ctx->samp);
     if (ctx->pk_status_host) hipHostFree(ctx->pk_status_host);
     if (ctx->step_ring) hipHostFree(ctx->step_ring);
     if (ctx->feed_host) hipHostFree(ctx->feed_host);
@@ -1026,6 +1028,53 @@ extern "C" int lg_argmax(lg_ctx* ctx, int* tok_out)
     const hipError_t e = hipMemcpyAsync(tok_out, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
     if (e != hipSuccess) { lg_set_error("argmax copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
     return lg_sync(ctx);
+}
+
+static int sample_args(float r01, const char* who)
+{
+    if (!(r01 >= 0.0f && r01 <= 1.0f)) {
+        lg_set_error("%s: uniform draw %g outside [0, 1]", who, (double)r01);
+        return LG_ERR_ARG;
+    }
+    return LG_OK;
+}
+
+extern "C" int lg_sample_topp(lg_ctx* ctx, float temp, float topp, int topk, float r01, int* tok_out)
+{
+    if (!ctx || !tok_out) { lg_set_error("lg_sample_topp: null argument"); return LG_ERR_ARG; }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    if (!(temp > 0.0f)) return lg_argmax(ctx, tok_out);   /* the reference's temp <= 0 case */
+    int rc = sample_args(r01, "lg_sample_topp");
+    if (rc) return rc;
+    if (ctx->samp && lg_sample_ws_size(ctx->samp) != ctx->vocab) {
+        LG_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+        lg_sample_ws_free(ctx->samp);
+        ctx->samp = nullptr;
+    }
+    if (!ctx->samp && (rc = lg_sample_ws_alloc(ctx->vocab, &ctx->samp))) return ctx_fail(ctx, rc);
+    if ((rc = lg_launch_sample_topp(ctx->logits, ctx->samp, temp, topp, topk, r01, ctx->stream))) return ctx_fail(ctx, rc);
+    const hipError_t e = hipMemcpyAsync(tok_out, lg_sample_ws_out(ctx->samp), sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) { lg_set_error("sample copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
+    return lg_sync(ctx);
+}
+
+extern "C" int lg_sample_topp_device(const float* logits_dev, int n, float temp, float topp, int topk, float r01,
+                                     int* tok_out)
+{
+    if (!logits_dev || !tok_out || n <= 0) { lg_set_error("lg_sample_topp_device: bad argument"); return LG_ERR_ARG; }
+    int rc = sample_args(r01, "lg_sample_topp_device");
+    if (rc) return rc;
+    LgSampleWs* w = nullptr;
+    if ((rc = lg_sample_ws_alloc(n, &w))) return rc;
+    if (!(temp > 0.0f)) rc = lg_launch_argmax(logits_dev, n, lg_sample_ws_out(w), nullptr);
+    else rc = lg_launch_sample_topp(logits_dev, w, temp, topp, topk, r01, nullptr);
+    if (!rc) {
+        const hipError_t e = hipMemcpy(tok_out, lg_sample_ws_out(w), sizeof(int), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) { lg_set_error("sample copy: %s", hipGetErrorString(e)); rc = LG_ERR_HIP; }
+    }
+    hipDeviceSynchronize();
+    lg_sample_ws_free(w);
+    return rc;
 }
 
 /* the prompt in layer passes of up to LG_PF_TMAX tokens (lg_prefill.hip),

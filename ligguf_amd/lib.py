@@ -62,6 +62,8 @@ SIGNATURES = {
     "lg_sync": (C.c_int, [_vp]),
     "lg_logits_device": (_vp, [_vp]),
     "lg_argmax": (C.c_int, [_vp, C.POINTER(C.c_int)]),
+    "lg_sample_topp": (C.c_int, [_vp, C.c_float, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_int)]),
+    "lg_sample_topp_device": (C.c_int, [_vp, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_int)]),
     "lg_set_decode_path": (C.c_int, [_vp, C.c_int]),
     "lg_decode_path": (C.c_int, [_vp]),
     "lg_trace_next_step": (C.c_int, [_vp, _vp]),
@@ -117,3 +119,11 @@ def row_size(t: int, n: int) -> int:
     if n % qk:
         return -1
     return n // qk * bs
+
+
+def sample_topp_device(logits_ptr: int, n: int, temp: float, topp: float, topk: int, r01: float) -> int:
+    """lg_sample_topp_device over n device floats at logits_ptr (e.g. a torch
+    tensor's data_ptr()): the reference's sampler_topp on the device."""
+    t = C.c_int()
+    check(load().lg_sample_topp_device(C.c_void_p(logits_ptr), n, temp, topp, topk, r01, C.byref(t)))
+    return int(t.value)

@@ -311,6 +311,13 @@ class Engine:
         check(self.lib.lg_argmax(self.ctx, C.byref(t)), self.ctx)
         return int(t.value)
 
+    def sample_topp(self, temp: float, topp: float, topk: int, r01: float) -> int:
+        """lg_sample_topp: the reference's sampler_topp over the device logits,
+        r01 = (float)rand() / (float)RAND_MAX drawn by the caller."""
+        t = C.c_int()
+        check(self.lib.lg_sample_topp(self.ctx, temp, topp, topk, r01, C.byref(t)), self.ctx)
+        return int(t.value)
+
     def set_prefill_path(self, path: int) -> None:
         """lg_set_prefill_path: PREFILL_AUTO, PREFILL_STEPS or PREFILL_BATCHED."""
         check(self.lib.lg_set_prefill_path(self.ctx, path), self.ctx)

@@ -90,6 +90,7 @@ class Oracle:
         L.or_state_kv.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_state_kv_write.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_argmax.argtypes = [_fp, C.c_int]
+        L.or_sampler_topp.argtypes = [_fp, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float]
 
     # --- scalar helpers
     def fp16_to_fp32(self, h: np.ndarray) -> np.ndarray:
@@ -177,6 +178,10 @@ class Oracle:
         x, px = _f32(x)
         return int(self.L.or_argmax(px, x.size))
 
+    def sampler_topp(self, logits, temp: float, topp: float, topk: int, r01: float) -> int:
+        x, px = _f32(logits)
+        return int(self.L.or_sampler_topp(px, x.size, temp, topp, topk, r01))
+
     # --- whole engine
     def new_state(self, model_struct: OrModel):
         self._keep = model_struct
@@ -256,7 +261,14 @@ class Reference:
         L.ref_kv_rows.argtypes = [C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.ref_kv_write_rows.argtypes = [C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.ref_sampler_greedy.restype = C.c_int
+        L.ref_sampler_topp.restype = C.c_int
+        L.ref_sampler_topp.argtypes = [_fp, C.c_int, C.c_float, C.c_float, C.c_int, C.c_uint]
         L.ref_init()
+
+    def sampler_topp(self, logits, temp: float, topp: float, topk: int, seed: int) -> int:
+        """the reference's sampler_topp over these logits after srand(seed)"""
+        x, px = _f32(logits)
+        return int(self.L.ref_sampler_topp(px, x.size, temp, topp, topk, seed))
 
     def fp16_to_fp32(self, h):
         h = np.ascontiguousarray(h, dtype=np.uint16)

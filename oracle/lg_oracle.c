@@ -541,6 +541,59 @@ int or_argmax(const float* x, int n)
     return best;
 }
 
+/* top-p / top-k sampling (sampler_topp, fast/ligguf_fast_qk.cpp:172-214):
+ * softmax at temperature temp with a sequential float sum, a sort by p
+ * descending then token ascending (cmp_sampler_ent_desc, :162-170), the
+ * cutoff where the running sum reaches top (at most topk - 1), and the first
+ * entry whose running sum reaches r01 * cum.  r01 stands for the
+ * reference's (float)rand() / (float)RAND_MAX. */
+typedef struct { float p; int tok; } or_samp;
+
+static int or_samp_cmp(const void* pa, const void* pb)
+{
+    const or_samp* a = (const or_samp*)pa;
+    const or_samp* b = (const or_samp*)pb;
+    if (a->p != b->p) return a->p < b->p ? 1 : -1;
+    return a->tok - b->tok;
+}
+
+int or_sampler_topp(const float* logits, int n, float temp, float topp, int topk, float r01)
+{
+    const int imax = or_argmax(logits, n);
+    if (temp <= 0.0f) return imax;
+    const float inv_temp = 1.0f / temp, maxlog = logits[imax];
+    or_samp* s = (or_samp*)malloc((size_t)n * sizeof(or_samp));
+    if (!s) return -1;
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        s[i].p = expf((logits[i] - maxlog) * inv_temp);
+        s[i].tok = i;
+        sum += s[i].p;
+    }
+    if (sum <= 0.0f) { free(s); return imax; }
+    for (int i = 0; i < n; i++) s[i].p /= sum;
+    qsort(s, (size_t)n, sizeof(or_samp), or_samp_cmp);
+    float top = topp <= 0.0f ? s[0].p : topp;
+    if (top > 1.0f) top = 1.0f;
+    const int k = (topk <= 0 || topk > n) ? n : topk;
+    float cum = 0.0f;
+    int cut = 0;
+    for (; cut < k; cut++) {
+        cum += s[cut].p;
+        if (cum >= top) break;
+    }
+    if (cut >= k) cut = k - 1;
+    const float r = r01 * cum;
+    float pcum = 0.0f;
+    int tok = s[cut].tok;
+    for (int i = 0; i <= cut; i++) {
+        pcum += s[i].p;
+        if (pcum >= r) { tok = s[i].tok; break; }
+    }
+    free(s);
+    return tok;
+}
+
 /* ------------------------------------------------------------------ */
 /* A12: the per-token step (fast/ligguf_fast_qk.cpp:24-144).            */
 /* ------------------------------------------------------------------ */

@@ -112,6 +112,7 @@ void or_state_kv(const or_state* s, int layer, int p0, int np, uint16_t* k, uint
 void or_state_kv_write(or_state* s, int layer, int p0, int np, const uint16_t* k, const uint16_t* v);
 /* greedy argmax, first index wins ties (fast/ligguf_fast_qk.cpp:146-160) */
 int or_argmax(const float* x, int n);
+int or_sampler_topp(const float* logits, int n, float temp, float topp, int topk, float r01);
 
 #ifdef __cplusplus
 }

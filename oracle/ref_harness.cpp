@@ -27,6 +27,7 @@
 
 extern void inference(int tok);
 extern int sampler_greedy();
+extern int sampler_topp();
 
 extern "C" {
 
@@ -283,6 +284,34 @@ void ref_kv_write_rows(int layer, int p0, int np, const uint16_t* k, const uint1
 int ref_sampler_greedy(void)
 {
     return sampler_greedy();
+}
+
+/* sampler_topp (fast/ligguf_fast_qk.cpp:172-214) over n given logits with
+ * srand(seed) before it; the model state's logits, vocabulary size, sampler
+ * settings and work buffer are restored afterwards */
+int ref_sampler_topp(const float* logits, int n, float temp, float topp, int topk, unsigned seed)
+{
+    std::vector<float> keep_logits(n);
+    keep_logits.swap(g_m.logits);
+    g_m.logits.assign(logits, logits + n);
+    const int keep_vocab = g_m.m.vocab_size;
+    const int keep_topk = g_m.topk;
+    const float keep_topp = g_m.topp, keep_temp = g_m.temp;
+    std::vector<sampler_entry> keep_samp(n);
+    keep_samp.swap(g_m.samp);
+    g_m.m.vocab_size = n;
+    g_m.temp = temp;
+    g_m.topp = topp;
+    g_m.topk = topk;
+    srand(seed);
+    const int tok = sampler_topp();
+    g_m.logits.swap(keep_logits);
+    g_m.samp.swap(keep_samp);
+    g_m.m.vocab_size = keep_vocab;
+    g_m.topk = keep_topk;
+    g_m.topp = keep_topp;
+    g_m.temp = keep_temp;
+    return tok;
 }
 
 void ref_model_close(void)

@@ -9,7 +9,7 @@ against the live reference on fresh random inputs.
 import numpy as np
 import pytest
 
-from conftest import golden
+from conftest import golden, sampler_agree
 from ligguf_amd.lib import BLOCK, F16, F32, Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0
 
 WEIGHT_TYPES = [Q8_0, Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
@@ -250,3 +250,51 @@ def test_tiny_one_step_vs_reference(oracle, reference, tmp_path):
     assert np.mean(errs <= 1e-5) >= 0.7
     assert errs.max() <= 5e-2
     assert np.mean(agree) >= 0.95
+
+
+# ---------------- next: top-p / top-k sampling ----------------
+def _libc_draw(seed: int) -> float:
+    """(float)rand() / (float)RAND_MAX after srand(seed), as the reference draws it"""
+    import ctypes
+    libc = ctypes.CDLL(None)
+    libc.srand(ctypes.c_uint(seed))
+    return float(np.float32(libc.rand()) / np.float32(2147483647))
+
+
+def test_sampler_topp_closed_forms(oracle):
+    rng = np.random.default_rng(11)
+    lg = rng.normal(0, 2, 1000).astype(np.float32)
+    lg[[17, 503]] = lg.max() + 1.0            # two equal maxima: the first wins
+    assert oracle.sampler_topp(lg, 0.0, 0.9, 0, 0.5) == 17    # temp <= 0: greedy
+    assert oracle.sampler_topp(lg, 0.8, 0.9, 1, 0.99) == 17   # top-1
+    assert oracle.sampler_topp(lg, 0.8, 0.0, 0, 0.99) == 17   # topp <= 0: the first entry's p
+    assert oracle.sampler_topp(lg, 0.8, 0.9, 2, 1.0) == 503   # the tie's second entry
+    # hand-made distribution: p = 0.4, 0.3, 0.2, 0.1 at tokens 3, 0, 2, 1
+    p = np.array([0.3, 0.1, 0.2, 0.4])
+    lg4 = np.log(p).astype(np.float32)
+    order = [3, 0, 2, 1]
+    cum = np.cumsum(p[order])
+    for i, tok in enumerate(order):
+        lo = cum[i - 1] if i else 0.0
+        r = (lo + cum[i]) / 2                 # the middle of entry i's interval
+        assert oracle.sampler_topp(lg4, 1.0, 1.0, 0, float(r)) == tok
+    # top-p 0.65 cuts after two entries (0.4 + 0.3 >= 0.65): r01 scales their 0.7
+    assert oracle.sampler_topp(lg4, 1.0, 0.65, 0, 0.55) == 3    # 0.385 < 0.4
+    assert oracle.sampler_topp(lg4, 1.0, 0.65, 0, 0.60) == 0    # 0.42 > 0.4
+    assert oracle.sampler_topp(lg4, 1.0, 0.65, 0, 1.0) == 0     # never past the cutoff
+    # top-k 3 with top-p 1: the cutoff is the third entry
+    assert oracle.sampler_topp(lg4, 1.0, 1.0, 3, 1.0) == 2
+
+
+@pytest.mark.parametrize("n,temp,topp,topk", [(1000, 1.0, 0.9, 0), (151936, 0.7, 0.95, 40), (151936, 2.0, 0.9, 0),
+                                              (5000, 1.0, 0.0, 0), (5000, 1.5, 1.5, 5001), (4096, 0.5, 0.5, 3)])
+def test_sampler_topp_vs_reference(oracle, reference, n, temp, topp, topk):
+    rng = np.random.default_rng(n + topk)
+    for seed in range(6):
+        lg = (rng.normal(0, 3, n)).astype(np.float32)
+        lg[rng.integers(0, n, n // 10)] = lg[0]          # ties
+        want = reference.sampler_topp(lg, temp, topp, topk, seed)
+        r01 = _libc_draw(seed)
+        got = oracle.sampler_topp(lg, temp, topp, topk, r01)
+        # the reference's -Ofast build sums and divides in its own order
+        assert sampler_agree(lg, temp, topp, topk, r01, got, want), (seed, got, want)
