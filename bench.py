@@ -224,6 +224,32 @@ def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
     return out
 
 
+def sampler_report(eng, np, tok: int, pos: int, reps: int = 50):
+    """lg_sample_topp (softmax, sort and cutoff on the device, one token back
+    to the host, synchronous) over the decode step's vocabulary logits, per
+    call, against the reference's sampler_topp (qsort of the vocabulary, one
+    host thread) on the same logits."""
+    lg = eng.decode(tok, pos)
+    rng = np.random.default_rng(0)
+    out = {"vocab": int(lg.size)}
+    for name, topk in (("topp0.9_us", 0), ("topp0.9_topk40_us", 40)):
+        eng.sample_topp(0.8, 0.9, topk, 0.5)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            eng.sample_topp(0.8, 0.9, topk, float(rng.random()))
+        out[name] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+    from oracle import binding
+    if binding.reference_available():
+        R = binding.load_reference()
+        t0 = time.perf_counter()
+        for s in range(5):
+            R.sampler_topp(lg, 0.8, 0.9, 0, s)
+        out["reference_host_topp0.9_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        out["reference_cores"] = 1
+    log(f"sampler: {out}")
+    return out
+
+
 def cpu_baseline(hm, seconds: float, max_tokens: int = 4000):
     """The reference FAST engine (oracle/_ref, AVX2, OpenMP) decoding the same
     host model from position 0 for about `seconds`."""
@@ -372,6 +398,7 @@ def main() -> int:
     log(f"decode: {tps:.1f} tok/s, {ms:.3f} ms/token, {mean_bytes / (dt / args.steps) / 1e9:.0f} GB/s per token")
 
     isolated = None if args.no_isolated else isolated_kernels(torch, np)
+    sampler = None if args.no_isolated else sampler_report(eng, np, tok, pos)
 
     roof = None
     if not args.no_kernel and path_name == "fused-graph":
@@ -413,6 +440,7 @@ def main() -> int:
         "roofline": roof,
         "cpu_baseline": cpu,
         "isolated": isolated,
+        "sampler": sampler,
         "q1g_8k": q1g,
     }
     print(json.dumps(out), flush=True)
