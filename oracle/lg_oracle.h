@@ -22,6 +22,11 @@
  * vectors written by the reference engine built from its own sources
  * (tests/golden/), against the live reference build (oracle/_ref) when it is
  * present, and against closed forms / brute force where those exist.
+ * or_sampler_topp (top-p / top-k sampling) has no golden vectors: closed
+ * forms (greedy cases, tie order, a hand-made distribution with draws inside
+ * each interval) and the live reference's sampler_topp pin it; the
+ * reference's -Ofast sums make the two agree to float rounding of the
+ * cumulative probabilities, not bit for bit.
  */
 #pragma once
 #include <stdint.h>
