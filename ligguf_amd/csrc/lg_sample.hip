@@ -14,8 +14,9 @@
  * Here: one pass for the first-index argmax per block, one for p and its
  * block sums, one normalising p by the total, a stable descending radix sort
  * of (p, token) -- equal p keep ascending tokens, the reference's tie rule --
- * and one workgroup scanning the sorted p in tiles of 1024 until the cutoff,
- * then finding r among the scanned sums.  The host passes the uniform draw
+ * and one workgroup scanning the sorted p in tiles of 8192 (8 consecutive
+ * entries per thread) until the cutoff, then finding r among the scanned
+ * sums.  The host passes the uniform draw
  * rand() / RAND_MAX.  Cumulative sums are tree sums, the reference's are
  * sequential: the sampled token is the reference's except where r or top
  * lies within float rounding of a cumulative sum. */
@@ -26,6 +27,7 @@
 #define LG_SMP_PER (LG_SMP_T * 4)   /* logits per block */
 #define LG_SMP_MAXB 1024            /* blocks at most (grid-stride past that) */
 #define LG_SMP_SCAN 1024            /* threads of the scanning workgroup */
+#define LG_SMP_PT 8                 /* consecutive sorted entries per scanning thread and tile */
 
 struct LgSampleWs {
     int n;
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(LG_SMP_T) void k_smp_norm(LgSampleWs ws)
     for (int j = blockIdx.x * LG_SMP_T + threadIdx.x; j < ws.n; j += gridDim.x * LG_SMP_T) ws.p[j] = ws.p[j] / sum;
 }
 
-/* inclusive block scan of v (LG_SMP_SCAN threads); returns the block total
+/* exclusive block scan of v (LG_SMP_SCAN threads); returns the block total
  * in *tot */
 __device__ __forceinline__ float smp_scan(float v, float* tot)
 {
@@ -145,6 +147,8 @@ __device__ __forceinline__ float smp_scan(float v, float* tot)
         const float w = __shfl_up(v, o);
         if (lane >= o) v += w;
     }
+    float ex = __shfl_up(v, 1);
+    if (lane == 0) ex = 0.0f;
     if (lane == 63) sw[wave] = v;
     __syncthreads();
     float pre = 0.0f, all = 0.0f;
@@ -154,7 +158,7 @@ __device__ __forceinline__ float smp_scan(float v, float* tot)
     }
     __syncthreads();
     *tot = all;
-    return pre + v;
+    return pre + ex;
 }
 
 __device__ __forceinline__ int smp_block_min(int c)
@@ -189,15 +193,33 @@ __global__ __launch_bounds__(LG_SMP_SCAN) void k_smp_pick(LgSampleWs ws, float t
     if (top <= 0.0f) top = ws.ps[0];
     if (top > 1.0f) top = 1.0f;
     const int K = (topk <= 0 || topk > ws.n) ? ws.n : topk;
-    /* the cutoff: the first index whose cumulative p reaches top, else K - 1 */
+    /* the cutoff: the first index whose cumulative p reaches top, else K - 1.
+     * Tiles of LG_SMP_SCAN * LG_SMP_PT entries, LG_SMP_PT consecutive ones
+     * per thread: a running sum in the thread on top of the block's
+     * exclusive scan of the thread totals */
+    constexpr int TILE = LG_SMP_SCAN * LG_SMP_PT;
     int cutoff = -1;
     float carry = 0.0f;
-    for (int base = 0; base < K && cutoff < 0; base += LG_SMP_SCAN) {
-        const int i = base + tid;
+    for (int base = 0; base < K && cutoff < 0; base += TILE) {
+        const int i0 = base + tid * LG_SMP_PT;
+        float run[LG_SMP_PT], loc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < LG_SMP_PT; k++) {
+            loc += i0 + k < K ? ws.ps[i0 + k] : 0.0f;
+            run[k] = loc;
+        }
         float tot;
-        const float c = carry + smp_scan(i < K ? ws.ps[i] : 0.0f, &tot);
-        if (i < K) ws.cum[i] = c;
-        const int f = smp_block_min(i < K && c >= top ? i : 0x7fffffff);
+        const float b = carry + smp_scan(loc, &tot);
+        int cand = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < LG_SMP_PT; k++) {
+            const float c = b + run[k];
+            if (i0 + k < K) {
+                ws.cum[i0 + k] = c;
+                if (c >= top && cand == 0x7fffffff) cand = i0 + k;
+            }
+        }
+        const int f = smp_block_min(cand);
         if (f != 0x7fffffff) cutoff = f;
         carry += tot;
     }
@@ -205,11 +227,16 @@ __global__ __launch_bounds__(LG_SMP_SCAN) void k_smp_pick(LgSampleWs ws, float t
     __threadfence_block();
     __syncthreads();
     const float r = r01 * ws.cum[cutoff];
-    /* the first entry up to the cutoff whose cumulative p reaches r */
+    /* the first entry up to the cutoff whose cumulative p reaches r (each
+     * thread reads the sums it wrote, plus the cutoff's) */
     int pick = 0x7fffffff;
-    for (int base = 0; base <= cutoff && pick == 0x7fffffff; base += LG_SMP_SCAN) {
-        const int i = base + tid;
-        pick = smp_block_min(i <= cutoff && ws.cum[i] >= r ? i : 0x7fffffff);
+    for (int base = 0; base <= cutoff && pick == 0x7fffffff; base += TILE) {
+        const int i0 = base + tid * LG_SMP_PT;
+        int cand = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < LG_SMP_PT; k++)
+            if (i0 + k <= cutoff && cand == 0x7fffffff && ws.cum[i0 + k] >= r) cand = i0 + k;
+        pick = smp_block_min(cand);
     }
     if (tid == 0) ws.out[0] = ws.ts[pick == 0x7fffffff ? cutoff : pick];
 }
