@@ -272,6 +272,20 @@ int lg_attn_decode(const float* q, const float* k, const float* v, const uint16_
                    int n_heads, int n_kv_heads, int head_dim, int pos, float* out, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* lg_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid it).  No counterpart in the reference.  The partials go to a scratch
+ * area of lg_attn_scratch_bytes() (8 MiB) that the library keeps in each
+ * device's memory until the process ends; a call whose partials
+ * (lg_attn_workspace_size) exceed it fails with LG_ERR_ARG.  The calling
+ * thread's current device must be the one that owns the pointers and the
+ * stream.  Nothing is allocated: every call on a device shares that device's
+ * scratch area, so calls that overlap on one device (other streams, other
+ * threads) race.  Same kernels and same results as lg_attn_decode. */
+size_t lg_attn_scratch_bytes(void);
+int lg_attn_decode_noalloc(const float* q, const float* k, const float* v, const uint16_t* kc, const uint16_t* vc,
+                           int n_heads, int n_kv_heads, int head_dim, int pos, float* out, void* stream);
+
 /* SwiGLU of fast/ligguf_fast_qk.cpp:119-123, hb[i] = silu(hb2[i]) * hb[i],
  * fused with the activation quantizer of :126 (qtype as lg_rmsnorm_quant;
  * out_q may be NULL when only hb is wanted). */

@@ -17,6 +17,8 @@
  */
 #include <math.h>
 
+#include <mutex>
+
 #include "lg_common.h"
 
 #define LG_ATTN_MAX_CHUNK 1024
@@ -288,4 +290,64 @@ int lg_launch_attn(const float* q, const float* k, const float* v, const uint16_
     }
     if (rc) return rc;
     return lg_check_launch("attention");
+}
+
+/* ------------------------------------------------------------------ */
+/* lg_attn_decode_noalloc: the same kernels on a scratch area that the */
+/* library holds in device memory for the life of the process          */
+/* ------------------------------------------------------------------ */
+/* 8 MiB per device: lg_attn_ws_bytes for 32 heads of 128 at up to
+ * 131072 positions (128 chunks of 1024), or 64 heads of 128 at up to
+ * 65536.  Every partial is written before it is read, so nothing needs
+ * clearing between calls. */
+#define LG_ATTN_SCRATCH_BYTES ((size_t)8 << 20)
+#define LG_ATTN_SCRATCH_DEVICES 64
+
+static __device__ __align__(256) float scratch[LG_ATTN_SCRATCH_BYTES / sizeof(float)];
+
+/* the device address of `scratch` on each device, looked up once per device
+ * (with that device current) at the entry point's first call there; host code
+ * passes only these addresses to kernels */
+static void* g_scratch_dev[LG_ATTN_SCRATCH_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int attn_scratch(void** out)
+{
+    int dev = 0;
+    LG_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= LG_ATTN_SCRATCH_DEVICES) {
+        lg_set_error("attention scratch: device %d beyond the %d supported", dev, LG_ATTN_SCRATCH_DEVICES);
+        return LG_ERR_ARG;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            lg_set_error("attention scratch: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+            return LG_ERR_HIP;
+        }
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return LG_OK;
+}
+
+extern "C" size_t lg_attn_scratch_bytes(void) { return LG_ATTN_SCRATCH_BYTES; }
+
+extern "C" int lg_attn_decode_noalloc(const float* q, const float* k, const float* v, const uint16_t* kc,
+                                      const uint16_t* vc, int n_heads, int n_kv_heads, int head_dim, int pos,
+                                      float* out, void* stream)
+{
+    const size_t need = lg_attn_ws_bytes(n_heads, head_dim, pos);
+    if (need > LG_ATTN_SCRATCH_BYTES) {
+        lg_set_error("attention (no allocation): %zu bytes of partials needed for %d heads of %d at position %d, "
+                     "the scratch area holds %zu", need, n_heads, head_dim, pos, LG_ATTN_SCRATCH_BYTES);
+        return LG_ERR_ARG;
+    }
+    void* ws = nullptr;
+    const int rc = attn_scratch(&ws);
+    if (rc) return rc;
+    return lg_launch_attn(q, k, v, kc, vc, n_heads, n_kv_heads, head_dim, pos, out, ws, LG_ATTN_SCRATCH_BYTES,
+                          (hipStream_t)stream);
 }

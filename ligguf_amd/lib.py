@@ -85,6 +85,8 @@ SIGNATURES = {
     "lg_attn_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "lg_attn_decode": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp,
                                  C.c_size_t, _vp]),
+    "lg_attn_scratch_bytes": (C.c_size_t, []),
+    "lg_attn_decode_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "lg_swiglu_quant": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp]),
 }
 

@@ -54,6 +54,8 @@ def test_row_size_matches_reference_table():
     lambda lib: lib.lg_attn_decode(1, 1, 1, 1, 1, 8, 2, 128, 3, 1, 1, 8, None),         # workspace too small
     lambda lib: lib.lg_attn_decode(1, 1, 1, 1, 1, 8, 2, 96, 3, 1, 1, 1 << 20, None),    # head_dim
     lambda lib: lib.lg_qk_norm_rope_kv(1, 1, 1, None, None, 4, 2, 6, 6, 0, 1, 1e-6, None, None, None),
+    # partials beyond the fixed scratch area (checked before any device call)
+    lambda lib: lib.lg_attn_decode_noalloc(1, 1, 1, 1, 1, 64, 8, 256, 1 << 20, 1, None),
 ])
 def test_bad_arguments_return_errors(call):
     lib = L.load()
