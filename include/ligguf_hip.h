@@ -151,6 +151,19 @@ int lg_decode_path(const lg_ctx* ctx);
 int lg_trace_next_step(lg_ctx* ctx, uint64_t* trace_dev);
 size_t lg_trace_size(const lg_ctx* ctx);
 
+/* Activation trace of the NEXT decode step on any path (no counterpart in
+ * the reference; for parity tests): lg_trace_acts_size(ctx) bytes of device
+ * memory at trace_dev receive every quantized activation the step builds, in
+ * slots of lg_trace_acts_size(ctx) / (4*n_layers + 1) bytes -- per layer the
+ * attention input (rmsnorm), the attention output, the FFN input (rmsnorm)
+ * and the SwiGLU output, then the output head's input -- each in the GGUF
+ * block layout of the activation its weights read (block_q8_K when that is
+ * a K-quant, block_q8_0 for Q8_0/Q1_0/Q1_G; fast/lil_gguf.h:64-67,115-119),
+ * i.e. the quantize_q8_K / quantize_q8_0 outputs of inference()
+ * (fast/ligguf_fast_qk.cpp:39,108,116,126,140). */
+int lg_trace_acts_next_step(lg_ctx* ctx, void* trace_dev);
+size_t lg_trace_acts_size(const lg_ctx* ctx);
+
 /* Times one kernel of the fused step (no counterpart in the reference; for
  * benchmarks and profiles): phase 0 rmsnorm + QKV, 1 attention, 2 att_out,
  * 3 rmsnorm + up|gate + SwiGLU, 4 down, 5 output head + argmax, launched

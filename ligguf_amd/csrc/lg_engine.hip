@@ -136,6 +136,8 @@ struct lg_ctx {
     PkParams pk = {};
     const void* pk_kernel = nullptr; /* the instantiation for this model */
     uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
+    uint8_t* act_trace = nullptr;    /* quantized activations of the next step (any path) */
+    size_t act_stride = 0;           /* bytes per activation slot of that trace */
     uint64_t pk_base = 0;
     int* pk_status_host = nullptr;   /* pinned {token, error} of the last persistent / fused step */
     bool last_was_pk = false;        /* the last step left its greedy token in pk_status_host */
@@ -443,7 +445,8 @@ static bool use_fused(const lg_ctx* c)
 }
 
 /* write {tok, pos, feed_end} into the device step record through a pinned slot */
-static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* trace = nullptr)
+static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* trace = nullptr,
+                          uint8_t* act_trace = nullptr)
 {
     if (c->ring_pending >= LG_STEP_RING) {
         LG_HIP_CHECK(hipStreamSynchronize(c->stream));
@@ -454,6 +457,7 @@ static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* t
     c->ring_pending++;
     memset(s, 0, sizeof(*s));
     s->tok = tok; s->pos = pos; s->feed_end = feed_end; s->trace = trace;
+    s->act_trace = act_trace; s->act_stride = c->act_stride;
     LG_HIP_CHECK(hipMemcpyAsync(c->step_dev, s, sizeof(PkStep), hipMemcpyHostToDevice, c->stream));
     c->dev_feed_end = feed_end;
     return LG_OK;
@@ -500,9 +504,11 @@ static int fused_launch(lg_ctx* c, int pos)
 static int enqueue_fused(lg_ctx* c, int tok, int pos)
 {
     int rc;
-    if (c->pk_trace || !(c->dev_known && c->dev_tok == tok && c->dev_pos == pos && pos >= c->dev_feed_end))
-        if ((rc = fused_set_step(c, tok, pos, 0, c->pk_trace))) return rc;
+    if (c->pk_trace || c->act_trace ||
+        !(c->dev_known && c->dev_tok == tok && c->dev_pos == pos && pos >= c->dev_feed_end))
+        if ((rc = fused_set_step(c, tok, pos, 0, c->pk_trace, c->act_trace))) return rc;
     c->pk_trace = nullptr;
+    c->act_trace = nullptr;
     c->dev_known = false;
     if ((rc = fused_launch(c, pos))) return rc;
     LG_HIP_CHECK(hipMemcpyAsync(c->pk_status_host, c->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
@@ -517,7 +523,10 @@ static int enqueue_pk(lg_ctx* c, int tok, int pos)
     PkStep S = {};
     S.tok = tok; S.pos = pos; S.base = c->pk_base;
     S.trace = c->pk_trace;
+    S.act_trace = c->act_trace;
+    S.act_stride = c->act_stride;
     c->pk_trace = nullptr;   /* one step only */
+    c->act_trace = nullptr;
     int rc = lg_persist_launch(c->pk_kernel, c->pk, &S, c->pk_nwg, c->stream);
     if (rc) return rc;
     c->pk_base += 5ull * c->n_layers + 1;
@@ -573,6 +582,19 @@ extern "C" int lg_trace_next_step(lg_ctx* ctx, uint64_t* trace_dev)
     if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
     ctx->pk_trace = trace_dev;
     return LG_OK;
+}
+
+extern "C" int lg_trace_acts_next_step(lg_ctx* ctx, void* trace_dev)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    ctx->act_trace = (uint8_t*)trace_dev;
+    return LG_OK;
+}
+
+extern "C" size_t lg_trace_acts_size(const lg_ctx* ctx)
+{
+    if (!ctx || !ctx->loaded) return 0;
+    return (size_t)(4 * ctx->n_layers + 1) * ctx->act_stride;
 }
 
 extern "C" size_t lg_trace_size(const lg_ctx* ctx)
@@ -737,6 +759,13 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
     ctx->arch = m->arch; ctx->n_layers = m->n_layers; ctx->n_embed = m->n_embed; ctx->n_heads = m->n_heads;
     ctx->n_kv_heads = m->n_kv_heads; ctx->head_dim = m->head_dim; ctx->kv_dim = m->kv_dim; ctx->n_ff = m->n_ff;
     ctx->vocab = m->vocab_size; ctx->n_context = m->n_context; ctx->rope_dim = m->rope_dim; ctx->eps = m->rms_epsilon;
+    {
+        /* activation trace slot: the widest quantized vector in either form */
+        const int64_t wide = std::max(m->n_embed, m->n_ff);
+        const int64_t qk = std::max<int64_t>(lg_row_size(LG_Q8_K, wide / 256 * 256), 0);
+        const int64_t q0 = std::max<int64_t>(lg_row_size(LG_Q8_0, wide / 32 * 32), 0);
+        ctx->act_stride = (size_t)((std::max(qk, q0) + 255) / 256 * 256);
+    }
 
     if ((rc = upload_weight(ctx, m->token_embd, ctx->embd))) return rc;
     if ((rc = upload_weight(ctx, m->output, ctx->output))) return rc;
@@ -906,11 +935,27 @@ static int mv(lg_ctx* c, const dweight& w, const actbufs& a, float* out, int acc
     return lg_launch_matvec(w.type, w.data, w.rsz, w.cols, w.rows, act_for(a, w.type), out, acc, c->stream);
 }
 
+/* activation trace of the multi-kernel step: the quantized form of an
+ * activation of width n that the weights of family `fam` read (Q8_K when
+ * any of them takes it, else Q8_0), copied to slot k */
+static int trace_act(lg_ctx* c, uint8_t* tr, int k, int fam, int n)
+{
+    if (!tr || !(fam & (ACT_K | ACT_80))) return LG_OK;
+    const bool kq = (fam & ACT_K) != 0;
+    const int64_t bytes = lg_row_size(kq ? LG_Q8_K : LG_Q8_0, n);
+    if (bytes <= 0) return LG_OK;
+    LG_HIP_CHECK(hipMemcpyAsync(tr + (size_t)k * c->act_stride, kq ? c->xqk : c->xq0, (size_t)bytes,
+                                hipMemcpyDeviceToDevice, c->stream));
+    return LG_OK;
+}
+
 static int enqueue_step(lg_ctx* c, int tok, int pos)
 {
     if (use_pk(c)) return enqueue_pk(c, tok, pos);
     if (use_fused(c)) return enqueue_fused(c, tok, pos);
     c->last_was_pk = false;
+    uint8_t* atr = c->act_trace;   /* one step only */
+    c->act_trace = nullptr;
     int rc;
     const int ne = c->n_embed, kvd = c->kv_dim;
     float* q = c->qkv;
@@ -923,6 +968,7 @@ static int enqueue_step(lg_ctx* c, int tok, int pos)
         /* attention branch */
         const int fam_qkv = act_family(L.q.type) | act_family(L.k.type) | act_family(L.v.type);
         if ((rc = prep_norm(c, c->x, L.att_norm, ne, fam_qkv, a))) return rc;
+        if ((rc = trace_act(c, atr, 4 * l, fam_qkv, ne))) return rc;
         if (L.qkv_fused) {
             if ((rc = mv(c, L.qkv, a, c->qkv, 0))) return rc;
         } else {
@@ -941,10 +987,12 @@ static int enqueue_step(lg_ctx* c, int tok, int pos)
                                  c->attn_ws_bytes, c->stream)))
             return rc;
         if ((rc = prep_plain(c, c->att, ne, act_family(L.att_out.type), a))) return rc;
+        if ((rc = trace_act(c, atr, 4 * l + 1, act_family(L.att_out.type), ne))) return rc;
         if ((rc = mv(c, L.att_out, a, c->x, 1))) return rc;
         /* FFN branch */
         const int fam_ug = act_family(L.up.type) | act_family(L.gate.type);
         if ((rc = prep_norm(c, c->x, L.ffn_norm, ne, fam_ug, a))) return rc;
+        if ((rc = trace_act(c, atr, 4 * l + 2, fam_ug, ne))) return rc;
         float* hb = c->hb;
         float* hb2 = c->hb + c->n_ff;
         if (L.ug_fused) {
@@ -962,10 +1010,12 @@ static int enqueue_step(lg_ctx* c, int tok, int pos)
             if ((rc = lg_launch_swiglu_quant(hb, hb2, c->n_ff, LG_F32, nullptr, c->stream))) return rc;
         }
         a.k = c->xqk; a.q0 = c->xq0; a.f = hb;
+        if ((rc = trace_act(c, atr, 4 * l + 3, fam_d, c->n_ff))) return rc;
         if ((rc = mv(c, L.down, a, c->x, 1))) return rc;
     }
     actbufs a;
     if ((rc = prep_norm(c, c->x, c->out_norm, ne, act_family(c->output.type), a))) return rc;
+    if ((rc = trace_act(c, atr, 4 * c->n_layers, act_family(c->output.type), ne))) return rc;
     if ((rc = mv(c, c->output, a, c->logits, 0))) return rc;
     return LG_OK;
 }

@@ -35,6 +35,13 @@ __device__ __forceinline__ uint64_t* f_tr(const PkStep* Sd, int l, int k)
     return t ? t + ((size_t)(5 * l + k) * gridDim.x + blockIdx.x) * 4 : nullptr;
 }
 
+/* activation trace slot k of the step (PkStep.act_trace) */
+__device__ __forceinline__ uint8_t* f_atr(const PkStep* Sd, int k)
+{
+    uint8_t* a = Sd->act_trace;
+    return a ? a + (size_t)k * Sd->act_stride : nullptr;
+}
+
 /* EMB: layer 0, whose input is the embedding row of the step's token */
 template <int LT, bool EMB>
 __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
@@ -47,7 +54,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const Pk
     const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
     phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, 2, LG_QKV_R>(
         P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, P.qkv + (size_t)l * qs, xin, 0, 0,
-        f_tr(Sd, l, 0));
+        f_tr(Sd, l, 0), f_atr(Sd, 4 * l));
 }
 
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
@@ -84,7 +91,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkL
     const int ne = P.n_embed;
     phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
         P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, P.xs + (size_t)l * ne, P.xm + (size_t)l * ne, nullptr, 0, 0,
-        f_tr(Sd, l, 2), att_partials<HD, NREP>(P, l, Sd->pos));
+        f_tr(Sd, l, 2), f_atr(Sd, 4 * l + 1), att_partials<HD, NREP>(P, l, Sd->pos));
 }
 
 template <int LT>
@@ -94,7 +101,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkL
     const int ne = P.n_embed, nff = P.n_ff;
     phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, 2, LG_UG_R>(
         P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, P.xm + (size_t)l * ne, nullptr, P.hb + (size_t)l * nff, nullptr, 0,
-        0, f_tr(Sd, l, 3));
+        0, f_tr(Sd, l, 3), f_atr(Sd, 4 * l + 2));
 }
 
 template <int LT>
@@ -104,7 +111,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const P
     const int ne = P.n_embed, nff = P.n_ff;
     phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, 6, LG_DN_R>(
         P, 0, L.down, L.down_rsz, ne, 0, nullptr, P.hb + (size_t)l * nff, P.xm + (size_t)l * ne,
-        P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4));
+        P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(Sd, 4 * l + 3));
 }
 
 template <int OT>
@@ -114,12 +121,13 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
     const int pos = Sd->pos;
         phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
-        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0));
+        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0), f_atr(Sd, 4 * P.n_layers));
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
     if (s_int[0] && threadIdx.x == 0) {
         Sd->tok = cld(P.tok_out);
         Sd->pos = pos + 1;
         Sd->trace = nullptr;    /* a trace covers one step */
+        Sd->act_trace = nullptr;
     }
 }
 

@@ -74,6 +74,11 @@ struct PkStep {
     uint64_t base;           /* progress value at launch; the launch adds 5*n_layers + 1 */
     uint64_t* trace;         /* NULL, or [5*n_layers+1][gridDim][4] timestamps (100 MHz clock):
                                 phase entry, wait done, activation built, phase published */
+    uint8_t* act_trace;      /* NULL, or [4*n_layers+1][act_stride] bytes: every quantized
+                                activation of the step as workgroup 0 built it (per layer: attention
+                                input, attention output, FFN input, SwiGLU output; then the output
+                                head's input), in its GGUF block layout */
+    uint64_t act_stride;
 };
 
 /* attention work split.  A workgroup step covers ppb = PK_THREADS * 8 /

@@ -89,6 +89,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
     const uint64_t B = S.base;
     constexpr int NE = NsE<LT>::value, NF = 3 * NE;
 #define TR(p) (S.trace ? S.trace + ((size_t)(p) * gridDim.x + blockIdx.x) * 4 : nullptr)
+#define ATR(k) (S.act_trace ? S.act_trace + (size_t)(k) * S.act_stride : nullptr)
     for (int l = 0; l < P.n_layers; l++) {
         const PkLayer L = pk_layer(P, l);
         const uint64_t p0 = B + 5ull * l;
@@ -99,25 +100,28 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
         float* hb = P.hb + (size_t)l * nff;
         if (l == 0)
             phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, BLD_EMB, 2, LG_QKV_R>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l));
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l), ATR(4 * l));
         else
             phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, BLD_RMS, 2, LG_QKV_R>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l));
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l), ATR(4 * l));
         phase_attn_any<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
         phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
             P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2),
-            att_partials<HD, NREP>(P, l, S.pos));
+            ATR(4 * l + 1), att_partials<HD, NREP>(P, l, S.pos));
         phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, 2, LG_UG_R>(
-            P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, xmid, nullptr, hb, nullptr, p0 + 3, p0 + 4, TR(5 * l + 3));
+            P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, xmid, nullptr, hb, nullptr, p0 + 3, p0 + 4, TR(5 * l + 3),
+            ATR(4 * l + 2));
         phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, 6, LG_DN_R>(
-            P, 0, L.down, L.down_rsz, ne, 0, nullptr, hb, xmid, xout, nullptr, p0 + 4, p0 + 5, TR(5 * l + 4));
+            P, 0, L.down, L.down_rsz, ne, 0, nullptr, hb, xmid, xout, nullptr, p0 + 4, p0 + 5, TR(5 * l + 4),
+            ATR(4 * l + 3));
     }
     const uint64_t pf = B + 5ull * P.n_layers;
     constexpr int NO = NsE<OT>::value;
     phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * ne, nullptr, P.logits, nullptr,
-        pf, pf + 1, TR(5 * P.n_layers));
+        pf, pf + 1, TR(5 * P.n_layers), ATR(4 * P.n_layers));
 #undef TR
+#undef ATR
 }
 
 /* ------------------------------------------------------------------ */

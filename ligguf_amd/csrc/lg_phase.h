@@ -373,7 +373,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                                          int items, int kstride, const float* __restrict__ normw,
                                          const float* __restrict__ src, const float* __restrict__ res_src,
                                          float* __restrict__ out, float* __restrict__ emb_out,
-                                         uint64_t wait_target, uint64_t sig, uint64_t* tr,
+                                         uint64_t wait_target, uint64_t sig, uint64_t* tr, uint8_t* atr,
                                          const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0})
 {
     using F = Fmt<FMT>;
@@ -438,6 +438,12 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         build_plain<QT, CPW>(as);
     }
     stamp(tr, 2);
+    if (atr && blockIdx.x == 0) {
+        /* activation trace (tests): the quantized blocks as built */
+        constexpr int n = CPW * 256 * PK_WAVES;
+        constexpr int words = (QT == LG_Q8_K ? n / 256 * LG_BS_Q8_K : n / 32 * LG_BS_Q8_0) / 4;
+        for (int i = LG_TID; i < words; i += PK_THREADS) ((uint32_t*)atr)[i] = ((const uint32_t*)s_act)[i];
+    }
 
     typename F::Act act[NS];
 #pragma unroll

@@ -300,6 +300,18 @@ class Engine:
         check(self.lib.lg_decode_step(self.ctx, tok, pos, None), self.ctx)
         return None
 
+    def decode_traced(self, tok: int, pos: int):
+        """lg_decode_step with lg_trace_acts_next_step: (logits, [4L+1][stride]
+        uint8 quantized activations of the step).  Device memory from torch."""
+        import torch
+        n = int(self.lib.lg_trace_acts_size(self.ctx))
+        buf = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()          # the fill runs on torch's stream, the step on the context's
+        check(self.lib.lg_trace_acts_next_step(self.ctx, C.c_void_p(buf.data_ptr())), self.ctx)
+        logits = self.decode(tok, pos)
+        tr = buf.cpu().numpy().reshape(4 * self.cfg.n_layers + 1, -1)
+        return logits, tr
+
     def decode_async(self, tok: int, pos: int) -> None:
         check(self.lib.lg_decode_step_async(self.ctx, tok, pos), self.ctx)
 

@@ -87,6 +87,7 @@ class Oracle:
         L.or_state_pos.argtypes = [_vp]
         L.or_state_set_pos.argtypes = [_vp, C.c_int]
         L.or_inference.argtypes = [_vp, C.c_int, _fp]
+        L.or_state_trace.argtypes = [_vp, _fp]
         L.or_state_kv.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_state_kv_write.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_argmax.argtypes = [_fp, C.c_int]
@@ -195,6 +196,15 @@ class Oracle:
         rc = self.L.or_inference(st, tok, out.ctypes.data_as(_fp))
         assert rc == 0
         return out
+
+    def inference_traced(self, st, tok: int, cfg):
+        """inference() plus the float vector before each of its 4 n_layers + 1
+        activation quantizations: (logits, trace [4 L + 1][max(n_embed, n_ff)])."""
+        wide = max(cfg.n_embed, cfg.n_ff)
+        tr = np.zeros((4 * cfg.n_layers + 1, wide), np.float32)
+        self.L.or_state_trace(st, tr.ctypes.data_as(_fp))
+        out = self.inference(st, tok, cfg.vocab)
+        return out, tr
 
     def state_kv_write(self, st, layer, p0, np_, k, v):
         k = np.ascontiguousarray(k, dtype=np.uint16)

@@ -602,6 +602,7 @@ struct or_state {
     int pos;
     float *x, *xb, *xb2, *hb, *hb2, *q, *k, *v, *logits, *tmp;
     uint16_t *kc, *vc;
+    float* trace;   /* NULL, or [4*n_layers+1][max(n_embed, n_ff)] for the next step only */
 };
 
 or_state* or_state_new(const or_model* m)
@@ -632,6 +633,17 @@ void or_state_free(or_state* s)
     free(s);
 }
 
+void or_state_trace(or_state* s, float* trace) { s->trace = trace; }
+
+/* the float vector inference() quantizes at point k of the step (before
+ * quantize_q8_K / quantize_q8_0, fast/ligguf_fast_qk.cpp:39,108,116,126,140) */
+static void trace_vec(or_state* s, float* tr, int k, const float* v, int n)
+{
+    if (!tr) return;
+    const int wide = s->m.n_ff > s->m.n_embed ? s->m.n_ff : s->m.n_embed;
+    memcpy(tr + (size_t)k * wide, v, (size_t)n * 4);
+}
+
 int or_state_pos(const or_state* s) { return s->pos; }
 void or_state_set_pos(or_state* s, int pos) { s->pos = pos; }
 
@@ -647,12 +659,15 @@ int or_inference(or_state* s, int tok, float* logits)
     const int hd = m->head_dim, kvd = m->kv_dim, ne = m->n_embed;
     if (pos < 0 || pos >= m->n_context || tok < 0 || tok >= m->token_embd.rows) return -1;
     s->pos++;
+    float* tr = s->trace;   /* one step only */
+    s->trace = NULL;
 
     or_dequantize_row(m->token_embd.type, (const uint8_t*)m->token_embd.data + (size_t)tok * m->token_embd.rsz, s->x, ne);
 
     for (int l = 0; l < m->n_layers; l++) {
         const or_layer* L = &m->layers[l];
         or_rmsnorm(s->xb, s->x, L->att_norm, ne, m->rms_epsilon);
+        trace_vec(s, tr, 4 * l, s->xb, ne);
         mv(&L->att_q, s->xb, s->q);
         mv(&L->att_k, s->xb, s->k);
         mv(&L->att_v, s->xb, s->v);
@@ -669,18 +684,22 @@ int or_inference(or_state* s, int tok, float* logits)
 
         or_attention(s->q, s->k, s->v, s->kc + loff, s->vc + loff, m->n_heads, m->n_kv_heads, hd, pos, s->xb);
 
+        trace_vec(s, tr, 4 * l + 1, s->xb, ne);
         mv(&L->att_out, s->xb, s->xb2);
         for (int j = 0; j < ne; j++) s->x[j] += s->xb2[j];
 
         or_rmsnorm(s->xb, s->x, L->ffn_norm, ne, m->rms_epsilon);
+        trace_vec(s, tr, 4 * l + 2, s->xb, ne);
         mv(&L->ffn_up, s->xb, s->hb);
         mv(&L->ffn_gate, s->xb, s->hb2);
         or_swiglu(s->hb, s->hb2, m->n_ff);
+        trace_vec(s, tr, 4 * l + 3, s->hb, m->n_ff);
         mv(&L->ffn_down, s->hb, s->xb);
         for (int j = 0; j < ne; j++) s->x[j] += s->xb[j];
     }
 
     or_rmsnorm(s->x, s->x, m->output_norm, ne, m->rms_epsilon);
+    trace_vec(s, tr, 4 * m->n_layers, s->x, ne);
     mv(&m->output, s->x, s->logits);
     if (logits) memcpy(logits, s->logits, (size_t)m->vocab_size * 4);
     return 0;

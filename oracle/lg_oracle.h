@@ -112,6 +112,11 @@ int or_state_pos(const or_state* s);
 void or_state_set_pos(or_state* s, int pos);
 /* inference(tok) at the state's position; copies logits (vocab floats) */
 int or_inference(or_state* s, int tok, float* logits);
+/* the next or_inference records the float vector before each activation
+ * quantization into trace: [4*n_layers+1][max(n_embed, n_ff)] floats -- per
+ * layer the rmsnorm'd attention input, the attention output, the rmsnorm'd
+ * FFN input and the SwiGLU output, then the rmsnorm'd output-head input */
+void or_state_trace(or_state* s, float* trace);
 /* fp16 KV rows of one layer for positions [p0, p0+np) */
 void or_state_kv(const or_state* s, int layer, int p0, int np, uint16_t* k, uint16_t* v);
 void or_state_kv_write(or_state* s, int layer, int p0, int np, const uint16_t* k, const uint16_t* v);

@@ -6,7 +6,8 @@ outputs are small .npz fixtures next to this script; tests compare the oracle
 (and through it the GPU path) against them on machines without the
 reference.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py                  # everything
+    python tests/golden/make_golden.py --teacher-only   # tiny_teacher.npz alone
 """
 from __future__ import annotations
 
@@ -22,7 +23,7 @@ sys.path.insert(0, ROOT)
 from ligguf_amd import encode  # noqa: E402
 from ligguf_amd.lib import BLOCK, F16, F32, Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0  # noqa: E402
 from ligguf_amd.model import TINY, HostModel  # noqa: E402
-from oracle.binding import RefLayer, RefModel, RefWeight, load_reference  # noqa: E402
+from oracle.binding import OrLayer, OrModel, OrWeight, RefLayer, RefModel, RefWeight, load_oracle, load_reference  # noqa: E402
 
 WEIGHT_TYPES = [Q8_0, Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
 # block field offsets of the fp16 scales (fast/lil_gguf.h:64-113)
@@ -166,5 +167,46 @@ def main():
     print("golden vectors written to", HERE)
 
 
+def tiny_teacher():
+    """tiny_teacher.npz: for each of the 128 generated steps of the tiny greedy
+    run (tiny_decode.npz), the reference's 32 largest logits (ids, values)
+    and top-2 gap, and -- the reference and the oracle each fed the same
+    tokens from its own KV state -- the oracle's largest absolute logit
+    difference from the reference and its argmax: the spread that separates
+    two correct engines once an int8 rounding flip has entered their caches."""
+    R = load_reference()
+    O = load_oracle()
+    g = np.load(os.path.join(HERE, "tiny_decode.npz"))
+    hm = HostModel.synthetic(TINY)
+    hm.rope_freq = g["rope_freq"]
+    path = os.path.join("/tmp", "ligguf_tiny_teacher.gguf")
+    hm.write_gguf(path)
+    R.model_open(path, 0)
+    st = O.new_state(hm.fill_desc(OrModel, OrLayer, OrWeight))
+    toks = np.concatenate([g["prompt"], g["greedy"]])
+    ids, vals, gap, diff, otok = [], [], [], [], []
+    for pos in range(len(toks) - 1):
+        a = R.inference(int(toks[pos]), TINY.vocab)
+        b = O.inference(st, int(toks[pos]), TINY.vocab)
+        if pos >= len(g["prompt"]) - 1:
+            top = np.argsort(-a, kind="stable")[:32]
+            assert int(top[0]) == int(g["greedy"][pos - len(g["prompt"]) + 1])
+            ids.append(top.astype(np.int32))
+            vals.append(a[top])
+            gap.append(a[top[0]] - a[top[1]])
+            diff.append(float(np.max(np.abs(a - b))))
+            otok.append(int(np.argmax(b)))
+    O.free_state(st)
+    os.unlink(path)
+    np.savez_compressed(os.path.join(HERE, "tiny_teacher.npz"), top_ids=np.array(ids), top_vals=np.array(vals),
+                        gap=np.array(gap, np.float32), oracle_maxdiff=np.array(diff, np.float32),
+                        oracle_tok=np.array(otok, np.int32))
+    print("tiny_teacher.npz written to", HERE)
+
+
 if __name__ == "__main__":
-    main()
+    if "--teacher-only" in sys.argv:
+        tiny_teacher()
+    else:
+        main()
+        tiny_teacher()

@@ -1,0 +1,142 @@
+"""Flip-explained parity: the quantized activations of a GPU step against the
+oracle's, element by element.
+
+inference() quantizes 4 n_layers + 1 activations per token
+(fast/ligguf_fast_qk.cpp:39,108,116,126,140) with quantize_q8_K or
+quantize_q8_0 (fast/lil_math.cpp:329-394).  Two correct implementations that
+round their fp32 sums in different orders produce int8 values that agree
+except where an activation lies within that rounding noise of a rounding
+boundary (x * 127/amax = k + 1/2).  Such a "flip" moves one int8 by one step
+and, on these random-weight models, the logits by ~1e-3..1e-2.
+
+``step_flips`` walks the quantized activations of one step in execution order
+and compares the GPU's int8 values (lg_trace_acts_next_step) with the int8
+values the as-compiled quantizer gives for the oracle's float vector at the
+same point (or_state_trace).  The first activation that differs must differ
+only by flips: every differing value one step away, and the oracle's
+pre-rounding value within FLIP_TOL of k + 1/2.  Everything after it in the
+step depends on the flipped value, so the walk stops there.  A step with no
+differing int8 at all must match the oracle's logits to fp32 noise.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from ligguf_amd.lib import BLOCK, F16, F32, Q1_0, Q1_G, Q8_0, Q8_K
+
+# distance of the oracle's scaled value v = x * 127/amax from k + 1/2 below
+# which a one-step difference counts as a rounding flip.  Matvec outputs are
+# exact only to ~2e-6 of the row's sum of |terms| (the fp32 combination of
+# exact integer block sums), so a value formed by cancelling terms, then
+# normalised and scaled to v, differs between the GPU and the oracle by up to
+# ~1e-2 of a quantization step (largest seen: 0.0117 on the tiny model).
+# 0.05 keeps a 4x margin; a differing value that is no flip lands this close to
+# a boundary with probability 0.1, and MAX_FLIPS bounds how many may differ.
+FLIP_TOL = 0.05
+# differing int8 values allowed in the first differing activation of a step:
+# when a block's largest value itself moves by the noise above, every value of
+# the block shifts with it, so several flips can share one block (9 of 768
+# seen on the tiny model); a fraction of the width bounds them
+MAX_FLIP_FRAC = 0.02
+# logits rel-L2 of a step whose int8 activations all agree with the oracle's
+EXACT_STEP = 1e-5
+
+K_FAMILY = {10, 11, 12, 13, 14}   # Q2_K..Q6_K read Q8_K activations
+
+
+def slot_formats(cfg):
+    """(quantized form, width) of each of the 4 n_layers + 1 activations of a
+    step, as lg_trace_acts_next_step records them (None: float activation)."""
+    def form(t):
+        if t in K_FAMILY:
+            return Q8_K
+        if t in (Q8_0, Q1_0, Q1_G):
+            return Q8_0
+        return None
+    out = []
+    for _ in range(cfg.n_layers):
+        f = form(cfg.layer_type)
+        out += [(f, cfg.n_embed), (f, cfg.n_embed), (f, cfg.n_embed), (f, cfg.n_ff)]
+    out.append((form(cfg.out_type), cfg.n_embed))
+    return out
+
+
+def parse_q(buf: np.ndarray, qtype: int, n: int):
+    """int8 quants and float scales of n values in block_q8_K / block_q8_0."""
+    qk, bs = BLOCK[qtype]
+    nb = n // qk
+    blk = np.asarray(buf[:nb * bs], np.uint8).reshape(nb, bs)
+    if qtype == Q8_K:
+        d = blk[:, 0:4].copy().view(np.float32).ravel()
+        qs = blk[:, 4:260].copy().view(np.int8).ravel()
+    else:
+        d = blk[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+        qs = blk[:, 2:34].copy().view(np.int8).ravel()
+    return qs, d
+
+
+def quantize_ref(x: np.ndarray, qtype: int):
+    """quantize_q8_K / quantize_q8_0 as the reference compiles them, in
+    float32 arithmetic (the oracle's or_quantize_*): (int8 quants, the scaled
+    values v they round)."""
+    x = np.asarray(x, np.float32)
+    if qtype == Q8_0:
+        b = x.reshape(-1, 32)
+        amax = np.abs(b).max(axis=1)
+        idv = np.where(amax != 0, np.float32(127.0) / np.where(amax != 0, amax, np.float32(1)), np.float32(0))
+        v = (b * idv[:, None].astype(np.float32)).astype(np.float32)
+        t = np.trunc(v)
+        q = t + np.sign(v) * (np.abs(v - t) >= np.float32(0.5))     # roundf: half away from zero
+        return q.astype(np.int8).ravel(), v.ravel()
+    b = x.reshape(-1, 256)
+    ia = np.argmax(np.abs(b), axis=1)                                # first index of the largest magnitude
+    mx = b[np.arange(b.shape[0]), ia]
+    isc = np.where(mx != 0, np.float32(-127.0) / np.where(mx != 0, mx, np.float32(1)), np.float32(0))
+    v = (b * isc[:, None].astype(np.float32)).astype(np.float32)
+    r = np.where(v < 0, v - np.float32(0.5), v + np.float32(0.5)).astype(np.float32)   # nearest_int as compiled
+    q = np.minimum(np.trunc(r), 127)
+    return q.astype(np.int8).ravel(), v.ravel()
+
+
+def boundary_dist(v: np.ndarray) -> np.ndarray:
+    a = np.abs(v.astype(np.float64))
+    return np.abs(a - np.floor(a) - 0.5)
+
+
+def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
+    """(first differing activation or -1, list of unexplained differences).
+
+    gpu_trace: [4L+1][stride] bytes from lg_trace_acts_next_step;
+    oracle_trace: [4L+1][max(n_embed, n_ff)] floats from or_state_trace."""
+    for k, (qt, n) in enumerate(slot_formats(cfg)):
+        if qt is None:
+            continue
+        qg, _ = parse_q(gpu_trace[k], qt, n)
+        qo, v = quantize_ref(oracle_trace[k][:n], qt)
+        diff = np.nonzero(qg != qo)[0]
+        if diff.size == 0:
+            continue
+        bad = []
+        if diff.size > max(8, int(MAX_FLIP_FRAC * n)):
+            bad.append((k, -1, int(diff.size), n, 0.0, 1.0))
+        for i in diff:
+            step = abs(int(qg[i]) - int(qo[i]))
+            dist = float(boundary_dist(v[i:i + 1])[0])
+            if step != 1 or dist > FLIP_TOL:
+                bad.append((k, int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
+        return k, bad
+    return -1, []
+
+
+def flip_summary(rows):
+    """rows: (first_slot, n_bad, rel) per step -> printable counts."""
+    exact = sum(1 for f, b, r in rows if f < 0)
+    flips = sum(1 for f, b, r in rows if f >= 0 and b == 0)
+    bad = sum(1 for f, b, r in rows if b)
+    worst_exact = max([r for f, b, r in rows if f < 0] or [0.0])
+    return f"{len(rows)} steps: {exact} without int8 differences (max rel-L2 {worst_exact:.1e}), " \
+           f"{flips} with rounding flips only, {bad} unexplained"
+
+
+__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "EXACT_STEP", "slot_formats", "parse_q", "quantize_ref", "step_flips", "flip_summary",
+           "F16", "F32"]

@@ -1,19 +1,27 @@
-"""GPU decode step (lg_decode_step) against the oracle and the reference's
-golden run.
+"""GPU decode step (lg_decode_step) against the oracle and the reference.
 
 The models here quantize every activation to int8 (Q8_0 / Q8_K) before each
 matvec, as the reference does.  Two correct fp32 implementations that sum in
 different orders therefore agree to ~1e-7 until some activation lands within
-that noise of a rounding boundary of roundf(x*127/amax); from then on they
-differ by one int8 step in one element, which these random-weight models
-amplify to ~1e-3..1e-2 in the logits.  The reference itself is not immune:
-its rmsnorm and SwiGLU use the approximate rsqrtss/rcpps instructions, whose
-bits differ between CPU vendors.  The tests therefore check
-  * one-step parity: GPU and oracle run the same token from the SAME KV
-    state (the oracle's, written into the GPU cache); most steps agree to
-    fp32 noise and the rest by no more than one such flip;
-  * free-running greedy agreement with the reference's golden sequence up
-    to the first divergence, compared with the oracle's own agreement.
+that noise of a rounding boundary of the quantizer; there they differ by one
+int8 step in one element (a "flip"), which these random-weight models amplify
+to ~1e-3..1e-2 in the logits.  The reference itself is not immune: its
+rmsnorm and SwiGLU use the approximate rsqrtss/rcpps instructions, whose bits
+differ between CPU vendors, and the oracle (double sums) leaves the
+reference's own greedy sequence at token 38 of 128 for exactly this reason.
+The tests therefore check
+  * one-step parity with every difference explained: GPU and oracle run the
+    same token from the SAME KV state (the oracle's, written into the GPU
+    cache); each step's quantized activations are compared with the oracle's
+    (tests/parity.py): a step without any differing int8 must match the
+    oracle's logits to EXACT_STEP, and the first differing activation of a
+    step may differ only by rounding flips;
+  * teacher-forced greedy on the tiny config: fed the reference's greedy
+    sequence from its own KV state, the GPU picks the reference's token at
+    every step whose reference top-2 gap exceeds the measured flip noise, and
+    its logits stay within that noise of the reference's;
+  * free-running greedy: the GPU's sequence equals the reference's up to a
+    first divergence, which must fall on such a near-tie.
 """
 import numpy as np
 import pytest
@@ -21,6 +29,13 @@ import pytest
 from conftest import golden
 from ligguf_amd.lib import Q4_K, Q5_K, Q6_K, Q8_0, Q3_K, Q2_K, Q1_G
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
+from parity import EXACT_STEP, flip_summary, step_flips
+
+# largest logit difference allowed between two correct engines fed the same
+# tokens once a flip has entered their KV caches: the oracle (double sums)
+# against the reference on the tiny teacher-forced run peaks at 0.0177
+# (tests/golden/tiny_teacher.npz oracle_maxdiff); 0.03 keeps a margin
+FLIP_NOISE = 0.03
 
 pytestmark = pytest.mark.gpu
 
@@ -32,6 +47,38 @@ def rel(a, b):
 def oracle_state(oracle, hm):
     from oracle.binding import OrLayer, OrModel, OrWeight
     return oracle.new_state(hm.fill_desc(OrModel, OrLayer, OrWeight))
+
+
+def one_step_flips(eng, oracle, hm, toks):
+    """Each token on the GPU and in the oracle from the oracle's KV state,
+    with both steps' quantized activations: rows (first differing
+    activation or -1, unexplained differences, logits rel-L2, argmax agree)."""
+    cfg = hm.cfg
+    st = oracle_state(oracle, hm)
+    rows = []
+    for pos, t in enumerate(toks):
+        if pos:
+            for l in range(cfg.n_layers):
+                k, v = oracle.state_kv(st, l, 0, pos, cfg.kv_dim)
+                eng.kv_write(l, 1, 0, pos, k, v)
+        g, gtr = eng.decode_traced(int(t), pos)
+        o, otr = oracle.inference_traced(st, int(t), cfg)
+        first, bad = step_flips(gtr, otr, cfg)
+        rows.append((first, bad, rel(g, o), int(np.argmax(g)) == int(np.argmax(o))))
+    oracle.free_state(st)
+    return rows
+
+
+def assert_flips_explained(rows, name, max_flip_rel=5e-2):
+    """No unexplained int8 difference; steps without one exact to fp32 noise;
+    steps with a flip within the reach of one flip."""
+    print(f"\n{name}: " + flip_summary([(f, len(b), r) for f, b, r, _ in rows]))
+    for i, (first, bad, r, _) in enumerate(rows):
+        assert not bad, f"step {i}: int8 differences that are not rounding flips: {bad[:5]}"
+        if first < 0:
+            assert r <= EXACT_STEP, f"step {i}: no int8 difference yet logits rel-L2 {r:.2e}"
+        else:
+            assert r <= max_flip_rel, f"step {i}: flip at activation {first}, logits rel-L2 {r:.2e}"
 
 
 def one_step_errors(eng, oracle, hm, toks):
@@ -73,7 +120,10 @@ def test_tiny_first_step_matches_reference(tiny):
 def test_tiny_one_step_vs_live_reference(tiny, reference, tmp_path):
     """GPU and the reference engine (built from its own sources, running on
     this host's CPU) each run a token of the reference's greedy trajectory
-    from the reference's KV state."""
+    from the reference's KV state.  The reference's internal activations are
+    not observable, so flips are explained against the oracle
+    (test_tiny_one_step_flips_explained); here most steps must agree to fp32
+    noise and none by more than one flip."""
     hm, eng, g = tiny
     path = str(tmp_path / "tiny.gguf")
     hm.write_gguf(path)
@@ -91,28 +141,55 @@ def test_tiny_one_step_vs_live_reference(tiny, reference, tmp_path):
         agree.append(int(np.argmax(a)) == int(np.argmax(b)))
     errs = np.array(errs)
     print(f"\nGPU vs live reference one-step: median {np.median(errs):.2e} p90 {np.quantile(errs, 0.9):.2e}"
-          f" max {errs.max():.2e} argmax agree {np.mean(agree):.3f}")
+          f" max {errs.max():.2e}; steps within 1e-5: {np.mean(errs <= 1e-5):.3f} argmax agree {np.mean(agree):.3f}")
     assert np.median(errs) <= 1e-5
-    assert np.mean(errs <= 1e-3) >= 0.7
-    assert errs.max() <= 5e-2
+    assert np.mean(errs <= 1e-5) >= 0.8
+    assert errs.max() <= 3e-2
     assert np.mean(agree) >= 0.95
 
 
-def test_tiny_one_step_parity(tiny, oracle):
+def test_tiny_one_step_flips_explained(tiny, oracle):
     hm, eng, g = tiny
-    toks = np.concatenate([g["prompt"], g["greedy"][:64]])
-    errs, agree = one_step_errors(eng, oracle, hm, toks)
-    print(f"\none-step rel-L2: median {np.median(errs):.2e}  p90 {np.quantile(errs, 0.9):.2e}  max {errs.max():.2e}"
-          f"  steps<=1e-5: {np.mean(errs <= 1e-5):.2f}  argmax agree {agree.mean():.3f}")
-    assert np.median(errs) <= 1e-5
-    assert np.mean(errs <= 1e-3) >= 0.75
-    assert errs.max() <= 5e-2
-    assert agree.mean() >= 0.95
+    toks = np.concatenate([g["prompt"], g["greedy"][:80]])
+    rows = one_step_flips(eng, oracle, hm, toks)
+    assert_flips_explained(rows, "tiny, GPU vs oracle one-step")
+    assert np.mean([a for *_, a in rows]) >= 0.95
 
 
-def test_tiny_greedy_against_reference(tiny, oracle):
-    """Free-running greedy decode of the 16-token prompt + 128 tokens."""
+def test_tiny_teacher_forced_greedy(tiny):
+    """The reference's 128-token greedy sequence fed to the GPU (own KV
+    state): the GPU's greedy token equals the reference's at every step whose
+    top-2 gap exceeds FLIP_NOISE, and its logits stay within FLIP_NOISE of the
+    reference's 32 largest (tests/golden/tiny_teacher.npz)."""
     hm, eng, g = tiny
+    tt = golden("tiny_teacher.npz")
+    toks = np.concatenate([g["prompt"], g["greedy"]])
+    n0 = len(g["prompt"]) - 1
+    miss, worst = [], 0.0
+    for pos in range(len(toks) - 1):
+        lg = eng.decode(int(toks[pos]), pos)
+        if pos < n0:
+            continue
+        j = pos - n0
+        d = float(np.max(np.abs(lg[tt["top_ids"][j]] - tt["top_vals"][j])))
+        worst = max(worst, d)
+        assert d <= FLIP_NOISE, f"step {j}: logits {d:.3e} from the reference's"
+        if int(np.argmax(lg)) != int(g["greedy"][j]):
+            miss.append((j, float(tt["gap"][j])))
+    print(f"\nteacher-forced: GPU greedy equals the reference's on {128 - len(miss)} of 128 steps; "
+          f"largest logit difference {worst:.2e}; near-tie steps that differ {miss} "
+          f"(the oracle differs on {int(np.sum(tt['oracle_tok'] != tt['top_ids'][:, 0]))})")
+    for j, gap in miss:
+        assert gap < FLIP_NOISE, f"step {j}: the GPU left the reference's token at a top-2 gap of {gap:.3e}"
+
+
+def test_tiny_greedy_free_running(tiny):
+    """Free-running greedy decode of the 16-token prompt + 128 tokens: equal
+    to the reference's sequence up to the first divergence, and that
+    divergence falls on a step whose reference top-2 gap is below
+    FLIP_NOISE (until then both engines saw the same tokens)."""
+    hm, eng, g = tiny
+    tt = golden("tiny_teacher.npz")
     toks = []
     logits = None
     for pos, t in enumerate(g["prompt"]):
@@ -127,10 +204,13 @@ def test_tiny_greedy_against_reference(tiny, oracle):
         pos += 1
     ref = g["greedy"].tolist()
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, ref)) if a != b), len(ref))
-    print(f"\nGPU greedy agrees with the reference for the first {first_diff} of 128 tokens")
-    # the first generated token comes from the prompt, before any divergence can compound
+    same = sum(a == b for a, b in zip(toks, ref))
+    print(f"\nGPU greedy equals the reference's first {first_diff} of 128 tokens ({same} equal overall); "
+          f"the oracle's free run leaves it at token 38")
     assert toks[0] == ref[0]
-    assert first_diff >= 8
+    if first_diff < len(ref):
+        assert float(tt["gap"][first_diff]) < FLIP_NOISE, \
+            f"diverged at {first_diff} where the reference's top-2 gap is {float(tt['gap'][first_diff]):.3e}"
 
 
 def test_tiny_decode_deterministic_and_async(tiny):
@@ -185,9 +265,7 @@ def test_small_models_one_step(gpu, oracle, cfg):
     eng = Engine(0)
     eng.load(hm)
     toks = np.random.default_rng(3).integers(1, cfg.vocab, 24)
-    errs, agree = one_step_errors(eng, oracle, hm, toks)
-    print(f"\n{cfg.name}: median {np.median(errs):.2e} max {errs.max():.2e} agree {agree.mean():.2f}")
-    assert np.median(errs) <= 1e-5
-    assert np.mean(errs <= 1e-3) >= 0.75
-    assert agree.mean() >= 0.9
+    rows = one_step_flips(eng, oracle, hm, toks)
+    assert_flips_explained(rows, cfg.name)
+    assert np.mean([a for *_, a in rows]) >= 0.9
     eng.close()
