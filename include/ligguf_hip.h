@@ -224,6 +224,20 @@ int lg_kv_read(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, uint16_
 int lg_kv_write(lg_ctx* ctx, int layer0, int nlayers, int pos0, int npos, const uint16_t* k_host,
                 const uint16_t* v_host);
 
+/* The reference's state file (save_model_state / load_model_state,
+ * fast/ligguf_fast_qk.cpp:216-302): the 24-byte packed model_file header
+ * {int pos; int n_context; uint64 kv_size; uint64 logits_size}
+ * (fast/common.h:26-31), per layer the first pos x kv_dim fp16 K values,
+ * then the same for V, then vocab fp32 logits.  lg_state_save writes the
+ * device cache rows [0, pos) and the logits of the last step (the reference
+ * refuses pos 0); lg_state_load checks the header as the reference does
+ * (kv_size = n_layers x pos x kv_dim, logits_size = vocab) and pos against
+ * this context, fills the device cache and logits, and returns pos, at which
+ * the next step continues (and the logits, when logits_host is not NULL).
+ * Files are interchangeable with the reference's own. */
+int lg_state_save(lg_ctx* ctx, const char* path, int pos);
+int lg_state_load(lg_ctx* ctx, const char* path, int* pos_out, float* logits_host);
+
 /* ===================================================================== */
 /* Per-op entry points (device pointers, asynchronous on `stream`)        */
 /* ===================================================================== */

@@ -264,12 +264,70 @@ static int check_weight(const lg_weight& w, int rows, int cols, const char* name
     return LG_OK;
 }
 
+/* Host-to-device copies of the model through two pinned staging buffers: the
+ * CPU copies the next chunk from the caller's (pageable, often mmap-ed) tensor
+ * into one buffer while the DMA engine moves the other, so the upload runs
+ * at the pinned transfer rate instead of a pageable copy's. */
+struct lg_uploader {
+    static constexpr size_t CHUNK = (size_t)32 << 20;
+    uint8_t* pin[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool used[2] = {false, false};
+    int cur = 0;
+    hipStream_t s = nullptr;
+    size_t bytes = 0;
+
+    int init(hipStream_t stream)
+    {
+        s = stream;
+        for (int i = 0; i < 2; i++) {
+            LG_HIP_CHECK(hipHostMalloc((void**)&pin[i], CHUNK, 0));
+            LG_HIP_CHECK(hipEventCreateWithFlags(&done[i], hipEventDisableTiming));
+        }
+        return LG_OK;
+    }
+    int copy(void* dst, const void* src, size_t n)
+    {
+        const uint8_t* h = (const uint8_t*)src;
+        uint8_t* d = (uint8_t*)dst;
+        while (n) {
+            const size_t c = n < CHUNK ? n : CHUNK;
+            if (used[cur]) LG_HIP_CHECK(hipEventSynchronize(done[cur]));   /* its last DMA has finished */
+            memcpy(pin[cur], h, c);
+            LG_HIP_CHECK(hipMemcpyAsync(d, pin[cur], c, hipMemcpyHostToDevice, s));
+            LG_HIP_CHECK(hipEventRecord(done[cur], s));
+            used[cur] = true;
+            cur ^= 1;
+            h += c; d += c; n -= c;
+            bytes += c;
+        }
+        return LG_OK;
+    }
+    int finish() { LG_HIP_CHECK(hipStreamSynchronize(s)); return LG_OK; }
+    ~lg_uploader()
+    {
+        if (s) hipStreamSynchronize(s);
+        for (int i = 0; i < 2; i++) {
+            if (pin[i]) hipHostFree(pin[i]);
+            if (done[i]) hipEventDestroy(done[i]);
+        }
+    }
+};
+static thread_local lg_uploader* g_up = nullptr;   /* set for the duration of one lg_load_model */
+
+static int h2d(void* dst, const void* src, size_t n)
+{
+    if (g_up) return g_up->copy(dst, src, n);
+    LG_HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+    return LG_OK;
+}
+
 static int upload_weight(lg_ctx* ctx, const lg_weight& w, dweight& d, uint8_t* dst = nullptr)
 {
     const size_t bytes = (size_t)w.rows * w.rsz;
     int rc = dst ? (d.data = dst, LG_OK) : dalloc(ctx, (void**)&d.data, bytes);
     if (rc) return rc;
-    LG_HIP_CHECK(hipMemcpy(d.data, w.data, bytes, hipMemcpyHostToDevice));
+    if ((rc = h2d(d.data, w.data, bytes))) return rc;
     d.type = w.type; d.rsz = w.rsz; d.rows = w.rows; d.cols = w.cols;
     return LG_OK;
 }
@@ -286,7 +344,7 @@ static int upload_stacked(lg_ctx* ctx, const lg_weight* const* ws, int n, dweigh
     size_t off = 0;
     for (int i = 0; i < n; i++) {
         const size_t b = (size_t)ws[i]->rows * ws[i]->rsz;
-        LG_HIP_CHECK(hipMemcpy(out.data + off, ws[i]->data, b, hipMemcpyHostToDevice));
+        if ((rc = h2d(out.data + off, ws[i]->data, b))) return rc;
         views[i].data = out.data + off;
         views[i].type = ws[i]->type; views[i].rsz = ws[i]->rsz; views[i].rows = ws[i]->rows; views[i].cols = ws[i]->cols;
         off += b;
@@ -300,8 +358,7 @@ static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const
     if (!h) { lg_set_error("load_model: %s missing", name); return LG_ERR_ARG; }
     int rc = dst ? (*d = dst, LG_OK) : dalloc(ctx, (void**)d, n * sizeof(float));
     if (rc) return rc;
-    LG_HIP_CHECK(hipMemcpy(*d, h, n * sizeof(float), hipMemcpyHostToDevice));
-    return LG_OK;
+    return h2d(*d, h, n * sizeof(float));
 }
 
 /* ------------------------------------------------------------------ */
@@ -889,7 +946,17 @@ extern "C" int lg_load_model(lg_ctx* ctx, const lg_model_desc* desc)
 {
     if (!ctx) { lg_set_error("lg_load_model: null context"); return LG_ERR_ARG; }
     hipSetDevice(ctx->device);
-    const int rc = load_model_impl(ctx, desc);
+    int rc;
+    {
+        lg_uploader up;
+        rc = up.init(ctx->stream);
+        if (!rc) {
+            g_up = &up;
+            rc = load_model_impl(ctx, desc);
+            g_up = nullptr;
+            if (!rc) rc = up.finish();
+        }
+    }
     if (rc) free_model(ctx);
     return ctx_fail(ctx, rc);
 }
@@ -1285,6 +1352,111 @@ extern "C" int lg_kv_write(lg_ctx* ctx, int layer0, int nlayers, int pos0, int n
                            const uint16_t* v_host)
 {
     return kv_io(ctx, layer0, nlayers, pos0, npos, (uint16_t*)k_host, (uint16_t*)v_host, true);
+}
+
+/* ------------------------------------------------------------------ */
+/* state files (save_model_state / load_model_state,                   */
+/* fast/ligguf_fast_qk.cpp:216-302)                                     */
+/* ------------------------------------------------------------------ */
+/* model_file (fast/common.h:26-31): packed, little-endian */
+#pragma pack(push, 1)
+struct lg_model_file {
+    int32_t pos;
+    int32_t n_context;
+    uint64_t kv_size;       /* n_layers * pos * kv_dim fp16 values per cache */
+    uint64_t logits_size;   /* vocab floats */
+};
+#pragma pack(pop)
+static_assert(sizeof(lg_model_file) == 24, "model_file is 24 packed bytes");
+
+/* pinned staging for one layer's K or V block or the logits */
+struct lg_pinned {
+    void* p = nullptr;
+    ~lg_pinned() { if (p) hipHostFree(p); }
+};
+
+extern "C" int lg_state_save(lg_ctx* ctx, const char* path, int pos)
+{
+    if (!ctx || !path) { lg_set_error("lg_state_save: null argument"); return ctx_fail(ctx, LG_ERR_ARG); }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    /* the reference refuses an empty state (fast/ligguf_fast_qk.cpp:266-269) */
+    if (pos <= 0 || pos > ctx->n_context) {
+        lg_set_error("lg_state_save: position %d outside 1..%d", pos, ctx->n_context);
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    hipSetDevice(ctx->device);
+    LG_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    const size_t blk = (size_t)pos * ctx->kv_dim * 2, lbytes = (size_t)ctx->vocab * 4;
+    lg_pinned buf;
+    LG_HIP_CHECK(hipHostMalloc(&buf.p, std::max(blk, lbytes), 0));
+    FILE* f = fopen(path, "wb");
+    if (!f) { lg_set_error("lg_state_save: cannot create %s", path); return ctx_fail(ctx, LG_ERR_ARG); }
+    lg_model_file hdr = {};
+    hdr.pos = pos;
+    hdr.n_context = ctx->n_context;
+    hdr.kv_size = (uint64_t)ctx->n_layers * pos * ctx->kv_dim;
+    hdr.logits_size = (uint64_t)ctx->vocab;
+    bool ok = fwrite(&hdr, sizeof(hdr), 1, f) == 1;
+    for (int q = 0; q < 2 && ok; q++) {
+        const uint16_t* cache = q ? ctx->vc : ctx->kc;
+        for (int l = 0; l < ctx->n_layers && ok; l++) {
+            const hipError_t e = hipMemcpy(buf.p, cache + (size_t)l * ctx->n_context * ctx->kv_dim, blk,
+                                           hipMemcpyDeviceToHost);
+            ok = e == hipSuccess && fwrite(buf.p, blk, 1, f) == 1;
+        }
+    }
+    if (ok) ok = hipMemcpy(buf.p, ctx->logits, lbytes, hipMemcpyDeviceToHost) == hipSuccess &&
+                 fwrite(buf.p, lbytes, 1, f) == 1;
+    if (fclose(f) != 0) ok = false;
+    if (!ok) { lg_set_error("lg_state_save: writing %s failed", path); return ctx_fail(ctx, LG_ERR_STATE); }
+    return LG_OK;
+}
+
+extern "C" int lg_state_load(lg_ctx* ctx, const char* path, int* pos_out, float* logits_host)
+{
+    if (!ctx || !path) { lg_set_error("lg_state_load: null argument"); return ctx_fail(ctx, LG_ERR_ARG); }
+    if (!ctx->loaded) { lg_set_error("no model loaded"); return ctx_fail(ctx, LG_ERR_STATE); }
+    hipSetDevice(ctx->device);
+    FILE* f = fopen(path, "rb");
+    if (!f) { lg_set_error("lg_state_load: cannot read %s", path); return ctx_fail(ctx, LG_ERR_ARG); }
+    lg_model_file hdr = {};
+    /* the checks of load_model_state (fast/ligguf_fast_qk.cpp:229-235,250) */
+    bool ok = fread(&hdr, sizeof(hdr), 1, f) == 1 && hdr.kv_size && hdr.logits_size && hdr.pos > 0 &&
+              hdr.pos <= ctx->n_context && hdr.kv_size == (uint64_t)ctx->n_layers * hdr.pos * ctx->kv_dim &&
+              hdr.logits_size == (uint64_t)ctx->vocab;
+    if (!ok) {
+        fclose(f);
+        lg_set_error("lg_state_load: %s is not a state file of this model (pos %d, kv %llu, logits %llu)", path,
+                     hdr.pos, (unsigned long long)hdr.kv_size, (unsigned long long)hdr.logits_size);
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    const int pos = hdr.pos;
+    const size_t blk = (size_t)pos * ctx->kv_dim * 2, lbytes = (size_t)ctx->vocab * 4;
+    lg_pinned buf;
+    const hipError_t ea = hipHostMalloc(&buf.p, std::max(blk, lbytes), 0);
+    if (ea != hipSuccess) {
+        fclose(f);
+        lg_set_error("lg_state_load: pinned staging: %s", hipGetErrorString(ea));
+        return ctx_fail(ctx, LG_ERR_NOMEM);
+    }
+    LG_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    for (int q = 0; q < 2 && ok; q++) {
+        uint16_t* cache = q ? ctx->vc : ctx->kc;
+        for (int l = 0; l < ctx->n_layers && ok; l++)
+            ok = fread(buf.p, blk, 1, f) == 1 &&
+                 hipMemcpy(cache + (size_t)l * ctx->n_context * ctx->kv_dim, buf.p, blk, hipMemcpyHostToDevice) ==
+                     hipSuccess;
+    }
+    if (ok) ok = fread(buf.p, lbytes, 1, f) == 1 &&
+                 hipMemcpy(ctx->logits, buf.p, lbytes, hipMemcpyHostToDevice) == hipSuccess;
+    fclose(f);
+    if (!ok) { lg_set_error("lg_state_load: reading %s failed", path); return ctx_fail(ctx, LG_ERR_STATE); }
+    if (logits_host) memcpy(logits_host, buf.p, lbytes);
+    /* the device step record and the last greedy token no longer describe the state */
+    ctx->dev_known = false;
+    ctx->last_was_pk = false;
+    if (pos_out) *pos_out = pos;
+    return LG_OK;
 }
 
 /* ------------------------------------------------------------------ */

@@ -76,6 +76,8 @@ SIGNATURES = {
     "lg_prefill_path": (C.c_int, [_vp]),
     "lg_kv_read": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "lg_kv_write": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "lg_state_save": (C.c_int, [_vp, C.c_char_p, C.c_int]),
+    "lg_state_load": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int), _vp]),
     "lg_dequantize_row": (C.c_int, [C.c_int, _vp, _vp, C.c_int64, _vp]),
     "lg_quantize_q8_0": (C.c_int, [_vp, C.c_int64, _vp, _vp]),
     "lg_quantize_q8_K": (C.c_int, [_vp, C.c_int64, _vp, _vp]),

@@ -312,6 +312,18 @@ class Engine:
         tr = buf.cpu().numpy().reshape(4 * self.cfg.n_layers + 1, -1)
         return logits, tr
 
+    def state_save(self, path: str, pos: int) -> None:
+        """lg_state_save: the reference's state file of cache rows [0, pos)
+        and the last step's logits."""
+        check(self.lib.lg_state_save(self.ctx, path.encode(), pos), self.ctx)
+
+    def state_load(self, path: str):
+        """lg_state_load: (pos, logits) of a reference state file."""
+        pos = C.c_int()
+        out = np.empty(self.vocab, np.float32)
+        check(self.lib.lg_state_load(self.ctx, path.encode(), C.byref(pos), out.ctypes.data), self.ctx)
+        return int(pos.value), out
+
     def decode_async(self, tok: int, pos: int) -> None:
         check(self.lib.lg_decode_step_async(self.ctx, tok, pos), self.ctx)
 

@@ -270,6 +270,9 @@ class Reference:
         L.ref_set_pos.argtypes = [C.c_int]
         L.ref_kv_rows.argtypes = [C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.ref_kv_write_rows.argtypes = [C.c_int, C.c_int, C.c_int, _vp, _vp]
+        L.ref_state_save.argtypes = [C.c_char_p]
+        L.ref_state_load.argtypes = [C.c_char_p]
+        L.ref_logits.argtypes = [_fp]
         L.ref_sampler_greedy.restype = C.c_int
         L.ref_sampler_topp.restype = C.c_int
         L.ref_sampler_topp.argtypes = [_fp, C.c_int, C.c_float, C.c_float, C.c_int, C.c_uint]
@@ -395,6 +398,17 @@ class Reference:
 
     def get_pos(self) -> int:
         return int(self.L.ref_get_pos())
+
+    def state_save(self, path: str) -> None:
+        assert self.L.ref_state_save(path.encode()) == 0, path
+
+    def state_load(self, path: str) -> None:
+        assert self.L.ref_state_load(path.encode()) == 0, path
+
+    def logits(self, vocab: int) -> np.ndarray:
+        out = np.empty(vocab, np.float32)
+        self.L.ref_logits(out.ctypes.data_as(_fp))
+        return out
 
     def kv_rows(self, layer, p0, np_, kv_dim):
         k = np.empty(np_ * kv_dim, np.uint16)

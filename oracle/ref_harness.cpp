@@ -10,6 +10,7 @@
  *   matmul / matmul2 / matmul3                    fast/lil_math.cpp:748-899
  *   rope / rmsnorm / rmsnorm_inplace / softmax    fast/lil_math.cpp:901-976
  *   inference()                                   fast/ligguf_fast_qk.cpp:24-144
+ *   save_model_state / load_model_state           fast/ligguf_fast_qk.cpp:216-302
  *   model_state::allocate                         fast/common.cpp:11-40
  *   gguf_model::open_mmap/read_gguf/read_tokenizer fast/lil_gguf.cpp:227-395
  * The attention entry (ref_attention) replays the inline attention block of
@@ -26,6 +27,8 @@
 #include "lil_math.h"
 
 extern void inference(int tok);
+extern bool load_model_state(const char* fn);
+extern bool save_model_state(const char* fn);
 extern int sampler_greedy();
 extern int sampler_topp();
 
@@ -313,6 +316,13 @@ int ref_sampler_topp(const float* logits, int n, float temp, float topp, int top
     g_m.temp = keep_temp;
     return tok;
 }
+
+/* save_model_state / load_model_state (fast/ligguf_fast_qk.cpp:216-302) on g_m */
+int ref_state_save(const char* fn) { return save_model_state(fn) ? 0 : -1; }
+int ref_state_load(const char* fn) { return load_model_state(fn) ? 0 : -1; }
+
+/* the current logits (vocab floats) */
+void ref_logits(float* out) { memcpy(out, g_m.logits.data(), g_m.logits.size() * sizeof(float)); }
 
 void ref_model_close(void)
 {
