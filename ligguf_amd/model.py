@@ -190,7 +190,11 @@ class HostModel:
         return m
 
     # ---- export
-    def write_gguf(self, path: str) -> None:
+    def write_gguf(self, path: str, byte_tokens: bool = False) -> None:
+        """A GGUF v3 file the reference loader reads (fast/lil_gguf.cpp:328-499).
+        The tokenizer vocabulary is placeholder strings; with byte_tokens the
+        first 256 are the byte tokens <0x00>..<0xFF>, so the reference's
+        fallback tokenizer (fast/tokenize.cpp:68-104) can encode any text."""
         c = self.cfg
         if c.arch == ARCH_LLAMA:
             p = "llama."
@@ -210,7 +214,8 @@ class HostModel:
                   (p + "attention.layer_norm_rms_epsilon", GFLOAT32, c.rms_eps),
                   (p + "rope.freq_base", GFLOAT32, c.rope_theta), (p + "attention.key_length", GUINT32, c.head_dim),
                   (p + "attention.value_length", GUINT32, c.head_dim), (p + "feed_forward_length", GUINT32, c.n_ff)]
-        kv.append(("tokenizer.ggml.tokens", GARRAY, (GSTRING, [f"<t{i}>" for i in range(c.vocab)])))
+        names = [f"<0x{i:02X}>" if byte_tokens and i < 256 else f"<t{i}>" for i in range(c.vocab)]
+        kv.append(("tokenizer.ggml.tokens", GARRAY, (GSTRING, names)))
         tensors = []
         for name, (t, rows, cols, data) in self.weights.items():
             tensors.append((name, t, [cols, rows], data))

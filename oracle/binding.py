@@ -27,6 +27,8 @@ def build_reference() -> bool:
     if not os.path.isdir(REF_SRC):
         return False
     subprocess.run(["make", "-s", "-C", ORACLE_DIR, "ref", "-j8"], check=True)
+    # the reference's own driver, as is and with the LG_HIP patch (needs libligguf_hip.so built)
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR, "driver"], check=True)
     return True
 
 
