@@ -30,6 +30,12 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+# the CPU baseline's OpenMP threads stay on their cores (set before any
+# OpenMP runtime starts in this process)
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+USABLE_CPUS = len(os.sched_getaffinity(0))      # before any OpenMP runtime pins this thread
+
 HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 
 
@@ -122,15 +128,19 @@ def _time_launches(torch, fn, reps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / reps
 
 
+ROTATE_BYTES = 512 << 20    # distinct buffers cycled per isolated kernel: twice the 256 MB Infinity Cache
+
+
 def isolated_kernels(torch, np):
     """The isolated-kernel workloads: batch-1 quantized matvec (k_matvec)
     for Q4_K 4096x4096, Q4_K 14336x4096 and Q6_K 128256x4096 (weights N(0,
-    0.02) through the reference quantizers, activation N(0,1) as Q8_K), each
-    cycled over enough distinct copies to exceed the 256 MB Infinity Cache;
-    and GQA decode attention (lg_attn_decode: 32 query / 8 KV heads of 128,
-    fp16 cache, the reference's KV format) at 512, 4096 and 32768 positions.
-    Rates are algorithmic bytes (weights + activation + output; K and V rows
-    read) per launch over the launch time."""
+    0.02) through the reference quantizers, activation N(0,1) as Q8_K); and
+    GQA decode attention (lg_attn_decode: 32 query / 8 KV heads of 128, fp16
+    cache, the reference's KV format) at 512, 4096 and 32768 positions.  Each
+    launch takes the next of enough distinct weight copies / KV caches to
+    cover at least 512 MiB, so no launch finds its bytes in the 256 MB
+    Infinity Cache.  Rates are algorithmic bytes (weights + activation +
+    output; K and V rows read) per launch over the launch time."""
     from ligguf_amd import ops
     from ligguf_amd.encode import random_tensor
     from ligguf_amd.lib import Q4_K, Q6_K, row_size
@@ -139,7 +149,7 @@ def isolated_kernels(torch, np):
     for t, name, rows, cols in ((Q4_K, "Q4_K", 4096, 4096), (Q4_K, "Q4_K", 14336, 4096), (Q6_K, "Q6_K", 128256, 4096)):
         rsz = row_size(t, cols)
         mbytes = rows * rsz
-        copies = max(1, -(-300_000_000 // mbytes))
+        copies = max(2, -(-ROTATE_BYTES // mbytes))
         w0 = torch.from_numpy(random_tensor(t, 7, 0, rows, cols)).to(dev)
         ws = [w0] + [w0.clone() for _ in range(copies - 1)]
         x = torch.from_numpy(np.random.default_rng(3).standard_normal(cols).astype(np.float32)).to(dev)
@@ -161,25 +171,33 @@ def isolated_kernels(torch, np):
     rng = np.random.default_rng(5)
     for ctx in (512, 4096, 32768):
         kvd = nkv * hd
-        kc = torch.from_numpy(rng.standard_normal(ctx * kvd).astype(np.float16).view(np.uint16)).to(dev)
-        vc = torch.from_numpy(rng.standard_normal(ctx * kvd).astype(np.float16).view(np.uint16)).to(dev)
+        cache_bytes = 2 * ctx * kvd * 2
+        ncache = max(2, -(-ROTATE_BYTES // cache_bytes))
+        base = torch.from_numpy(rng.standard_normal(2 * ctx * kvd).astype(np.float16).view(np.uint16)).to(dev)
+        caches = [base] + [base.clone() for _ in range(ncache - 1)]
         q = torch.from_numpy(rng.standard_normal(nh * hd).astype(np.float32)).to(dev)
         kk = torch.from_numpy(rng.standard_normal(kvd).astype(np.float32)).to(dev)
         vv = torch.from_numpy(rng.standard_normal(kvd).astype(np.float32)).to(dev)
         pos = ctx - 1
         wsz = max(16, ops.load().lg_attn_workspace_size(nh, hd, pos))
         ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
-        us = _time_launches(torch, lambda: ops.attention(q, kk, vv, kc, vc, nh, nkv, hd, pos, ws), 50)
+        k = [0]
+
+        def att():
+            c = caches[k[0] % ncache]
+            ops.attention(q, kk, vv, c[:ctx * kvd], c[ctx * kvd:], nh, nkv, hd, pos, ws)
+            k[0] += 1
+        us = _time_launches(torch, att, max(50, 4 * ncache))
         alg = pos * kvd * 2 * 2 + (nh * hd + 2 * kvd) * 4 + nh * hd * 4
         out["attention"].append({"ctx": ctx, "us": round(us, 2), "GB/s": round(alg / us / 1e3, 1),
-                                 "frac": round(alg / (us * 1e-6) / HBM_PEAK, 4)})
-        del kc, vc
+                                 "frac": round(alg / (us * 1e-6) / HBM_PEAK, 4), "caches": ncache})
+        del caches, base
     torch.cuda.empty_cache()
     log(f"isolated: {out}")
     return out
 
 
-def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
+def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8, cpu_seconds: float = 0.0):
     """The 1-bit workload: Qwen3-8B shape with Q1_G layers (group 128, sign
     bits, fp16 group scales |N(0,0.02)|) and Q8_0 embedding/output, an
     8192-token prompt of random ids fed through lg_prefill (batched: 16 layer
@@ -198,6 +216,11 @@ def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
     t0 = time.perf_counter()
     logits = eng.prefill(prompt, 0)
     pf_s = time.perf_counter() - t0
+    state = None
+    if cpu_seconds > 0:
+        import tempfile
+        state = os.path.join(tempfile.mkdtemp(prefix="lg_q1g_"), "ctx.state")
+        eng.state_save(state, ctx)
     tok, pos = int(np.argmax(logits)), ctx
     for _ in range(warmup):
         eng.decode_async(tok, pos)
@@ -220,6 +243,10 @@ def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8):
            "ms_per_token": round(dt / steps * 1e3, 4), "positions": [p_first, pos - 1],
            "bytes_per_token": int(mean_bytes), "hbm_roofline_frac_token": round(mean_bytes / (dt / steps) / HBM_PEAK, 4),
            "decode_path": path}
+    if state:
+        with _stdout_to_stderr():
+            out["cpu_baseline"] = cpu_baseline_q1g(hm, state, cpu_seconds)
+        os.unlink(state)
     log(f"q1g: {out}")
     return out
 
@@ -250,21 +277,62 @@ def sampler_report(eng, np, tok: int, pos: int, reps: int = 50):
     return out
 
 
-def cpu_baseline(hm, seconds: float, max_tokens: int = 4000):
-    """The reference FAST engine (oracle/_ref, AVX2, OpenMP) decoding the same
-    host model from position 0 for about `seconds`."""
+def cpu_info():
+    """The host CPU as lscpu reports it and the OpenMP threads the reference
+    runs with."""
+    import ctypes as C
+    import subprocess
+    info = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict(line.split(":", 1) for line in txt.splitlines() if ":" in line)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        info["model"] = kv.get("Model name")
+        sockets = int(kv.get("Socket(s)", "1"))
+        info["physical_cores"] = sockets * int(kv.get("Core(s) per socket", "0"))
+        info["logical_cpus"] = int(kv.get("CPU(s)", "0"))
+    except Exception as e:          # lscpu missing: report what is known
+        info["lscpu_error"] = str(e)
+    try:
+        gomp = C.CDLL("libgomp.so.1")
+        info["omp_threads"] = int(gomp.omp_get_max_threads())
+    except OSError:
+        info["omp_threads"] = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    info["OMP_PROC_BIND"] = os.environ.get("OMP_PROC_BIND")
+    info["usable_cpus"] = USABLE_CPUS
+    return info
+
+
+class _stdout_to_stderr:
+    """The reference prints progress to stdout (its DBG lines); the bench's
+    stdout carries only the JSON line, so C-level stdout goes to stderr
+    meanwhile."""
+
+    def __enter__(self):
+        sys.stdout.flush()
+        self.saved = os.dup(1)
+        os.dup2(2, 1)
+        return self
+
+    def __exit__(self, *exc):
+        import ctypes as C
+        C.CDLL(None).fflush(None)
+        os.dup2(self.saved, 1)
+        os.close(self.saved)
+        return False
+
+
+def _ref_bind(R, hm):
+    """Bind a host model's tensors into the reference engine's g_m."""
     import ctypes as C
     import numpy as np
+    from ligguf_amd.lib import row_size
     from oracle import binding
-    if not binding.reference_available():
-        return None
-    R = binding.load_reference()
     c = hm.cfg
     layers = (binding.RefLayer * c.n_layers)()
 
     def w(name):
         t, rows, cols, data = hm.weights[name]
-        from ligguf_amd.lib import row_size
         return binding.RefWeight(np.asarray(data).ctypes.data, t, row_size(t, cols))
 
     def f(name):
@@ -282,20 +350,72 @@ def cpu_baseline(hm, seconds: float, max_tokens: int = 4000):
                          c.vocab, c.n_context, c.rope_dim, c.rms_eps, c.rope_theta, w("token_embd.weight"),
                          w("output.weight"), f("output_norm.weight"), C.cast(layers, C.c_void_p))
     R.model_bind(m)
+
+
+def cpu_baseline(hm, seconds: float, prompt_tokens: int = 64, max_tokens: int = 4000):
+    """The reference FAST engine (oracle/_ref, AVX2, OpenMP) on the same host
+    model: its prefill (feed_text: one inference() per prompt token,
+    fast/ligguf_fast_qk.cpp:340-356) over `prompt_tokens` random ids, then
+    greedy decode from there for about `seconds`."""
+    import numpy as np
+    from oracle import binding
+    if not binding.reference_available():
+        return None
+    R = binding.load_reference()
+    c = hm.cfg
+    _ref_bind(R, hm)
     rng = np.random.default_rng(1)
     R.inference(int(rng.integers(1, c.vocab)), c.vocab)      # untimed: faults pages in, warms caches
-    max_tokens = min(max_tokens, c.n_context - 2)          # positions 1..n stay inside the context
+    R.set_pos(0)
+    prompt = rng.integers(1, c.vocab, prompt_tokens)
+    t0 = time.perf_counter()
+    for t in prompt:
+        logits = R.inference(int(t), c.vocab)
+    pf_s = time.perf_counter() - t0
+    max_tokens = min(max_tokens, c.n_context - prompt_tokens - 2)
     n, t0 = 0, time.perf_counter()
-    tok = 1
+    tok = int(np.argmax(logits))
     while n < max_tokens and (time.perf_counter() - t0 < seconds or n < 2):
         logits = R.inference(tok, c.vocab)
         tok = int(np.argmax(logits))
         n += 1
     dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    ci = cpu_info()
+    threads = ci.get("omp_threads")
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"{n} greedy decode tokens at positions 1..{n} of the same model (reference FAST engine, "
-                      f"AVX2 build, {threads} OpenMP threads)"}
+            "prefill_tok_s": round(prompt_tokens / pf_s, 3), "cpu": ci,
+            "sample": f"prefill of {prompt_tokens} random ids (token by token, as feed_text), then {n} greedy "
+                      f"decode tokens at positions {prompt_tokens}..{prompt_tokens + n - 1} of the same model "
+                      f"(reference FAST engine, AVX2 build, {threads} OpenMP threads)"}
+
+
+def cpu_baseline_q1g(hm, state_path: str, seconds: float, max_tokens: int = 64):
+    """The reference on the Q1_G model, decoding from the 8192-token state
+    the GPU saved in the reference's own state-file format (load_model_state,
+    fast/ligguf_fast_qk.cpp:216-263): an 8192-token prefill on the CPU would
+    take hours, so the baseline starts from the file, as the -L option does."""
+    import numpy as np
+    from oracle import binding
+    if not binding.reference_available():
+        return None
+    R = binding.load_reference()
+    c = hm.cfg
+    _ref_bind(R, hm)
+    R.state_load(state_path)
+    pos0 = R.get_pos()
+    tok = int(np.argmax(R.logits(c.vocab)))
+    logits = R.inference(tok, c.vocab)                     # untimed: faults the weights in
+    tok = int(np.argmax(logits))
+    n, t0 = 0, time.perf_counter()
+    while n < max_tokens and (time.perf_counter() - t0 < seconds or n < 2):
+        logits = R.inference(tok, c.vocab)
+        tok = int(np.argmax(logits))
+        n += 1
+    dt = time.perf_counter() - t0
+    threads = cpu_info().get("omp_threads")
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} greedy decode tokens at positions {pos0 + 1}..{pos0 + n} from the GPU's state file "
+                      f"(reference FAST engine, AVX2 build, {threads} OpenMP threads)"}
 
 
 def main() -> int:
@@ -406,12 +526,16 @@ def main() -> int:
         log(f"dominant kernel: {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of HBM peak)")
     eng.close()
 
-    q1g = None if args.no_q1g else q1g_context(torch, np, ctx=args.q1g_ctx)
+    copy = plain_copy(torch)
+    log(f"plain copy: {copy}")
+    q1g = None if args.no_q1g else q1g_context(torch, np, ctx=args.q1g_ctx,
+                                               cpu_seconds=0.0 if args.no_cpu else args.cpu_seconds)
 
     cpu = None
     if not args.no_cpu:
         t0 = time.perf_counter()
-        cpu = cpu_baseline(hm, args.cpu_seconds)
+        with _stdout_to_stderr():
+            cpu = cpu_baseline(hm, args.cpu_seconds)
         log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f}s)")
 
     out = {
@@ -435,6 +559,9 @@ def main() -> int:
             "bytes_per_token": int(mean_bytes), "decode_path": path_name,
         },
         "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) / HBM_PEAK, 4),
+        "hbm_practical": {"copy_GB/s": copy["GB/s"], "bytes_each_way": copy["bytes_each_way"],
+                          "frac_of_peak": round(copy["GB/s"] * 1e9 / HBM_PEAK, 4),
+                          "token_frac_of_practical": round(mean_bytes / (dt / args.steps) / (copy["GB/s"] * 1e9), 4)},
         "prefill_tok_s": round(args.prefill / prefill_s, 1),
         "prefill": prefill,
         "roofline": roof,

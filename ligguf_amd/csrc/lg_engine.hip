@@ -481,6 +481,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.err = (uint32_t*)(tail + 68);
     P.attn_cnt = (uint32_t*)(tail + 256);                          /* up to 32 heads x PK_ATT_MERGE groups */
     P.spin_cap = 1 << 20;
+    P.act_stride = ctx->act_stride;
     /* fused path: device step record, prompt feed, pinned staging */
     if ((rc = dalloc(ctx, (void**)&ctx->step_dev, sizeof(PkStep)))) return rc;
     LG_HIP_CHECK(hipMemset(ctx->step_dev, 0, sizeof(PkStep)));
@@ -517,8 +518,7 @@ static bool use_fused(const lg_ctx* c)
 }
 
 /* write {tok, pos, feed_end} into the device step record through a pinned slot */
-static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* trace = nullptr,
-                          uint8_t* act_trace = nullptr)
+static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* trace = nullptr)
 {
     if (c->ring_pending >= LG_STEP_RING) {
         LG_HIP_CHECK(hipStreamSynchronize(c->stream));
@@ -529,7 +529,6 @@ static int fused_set_step(lg_ctx* c, int tok, int pos, int feed_end, uint64_t* t
     c->ring_pending++;
     memset(s, 0, sizeof(*s));
     s->tok = tok; s->pos = pos; s->feed_end = feed_end; s->trace = trace;
-    s->act_trace = act_trace; s->act_stride = c->act_stride;
     LG_HIP_CHECK(hipMemcpyAsync(c->step_dev, s, sizeof(PkStep), hipMemcpyHostToDevice, c->stream));
     c->dev_feed_end = feed_end;
     return LG_OK;
@@ -542,10 +541,14 @@ static bool att_long(const lg_ctx* c, int pos)
 }
 
 /* one fused step at position pos on the stream: its graph (captured on first
- * use; one per attention kernel) or the same launches issued directly */
-static int fused_launch(lg_ctx* c, int pos)
+ * use; one per attention kernel) or the same launches issued directly (a
+ * step with an activation trace is always launched directly) */
+static int fused_launch(lg_ctx* c, int pos, uint8_t* act_trace = nullptr)
 {
     const bool lc = att_long(c, pos);
+    if (act_trace)
+        return lg_fused_enqueue(c->fused_fn, c->pk, c->pk_layers.data(), c->step_dev, c->n_layers, c->pk_nwg, lc,
+                                c->stream, act_trace);
     hipGraphExec_t& graph = c->graph[lc ? 1 : 0];
     if (c->use_graph && !graph) {
         hipGraph_t g = nullptr;
@@ -576,13 +579,13 @@ static int fused_launch(lg_ctx* c, int pos)
 static int enqueue_fused(lg_ctx* c, int tok, int pos)
 {
     int rc;
-    if (c->pk_trace || c->act_trace ||
-        !(c->dev_known && c->dev_tok == tok && c->dev_pos == pos && pos >= c->dev_feed_end))
-        if ((rc = fused_set_step(c, tok, pos, 0, c->pk_trace, c->act_trace))) return rc;
+    if (c->pk_trace || !(c->dev_known && c->dev_tok == tok && c->dev_pos == pos && pos >= c->dev_feed_end))
+        if ((rc = fused_set_step(c, tok, pos, 0, c->pk_trace))) return rc;
+    uint8_t* atr = c->act_trace;
     c->pk_trace = nullptr;
     c->act_trace = nullptr;
     c->dev_known = false;
-    if ((rc = fused_launch(c, pos))) return rc;
+    if ((rc = fused_launch(c, pos, atr))) return rc;
     LG_HIP_CHECK(hipMemcpyAsync(c->pk_status_host, c->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
     c->last_was_pk = true;
     c->last_pos = pos;
@@ -596,7 +599,6 @@ static int enqueue_pk(lg_ctx* c, int tok, int pos)
     S.tok = tok; S.pos = pos; S.base = c->pk_base;
     S.trace = c->pk_trace;
     S.act_trace = c->act_trace;
-    S.act_stride = c->act_stride;
     c->pk_trace = nullptr;   /* one step only */
     c->act_trace = nullptr;
     int rc = lg_persist_launch(c->pk_kernel, c->pk, &S, c->pk_nwg, c->stream);

@@ -35,17 +35,17 @@ __device__ __forceinline__ uint64_t* f_tr(const PkStep* Sd, int l, int k)
     return t ? t + ((size_t)(5 * l + k) * gridDim.x + blockIdx.x) * 4 : nullptr;
 }
 
-/* activation trace slot k of the step (PkStep.act_trace) */
-__device__ __forceinline__ uint8_t* f_atr(const PkStep* Sd, int k)
+/* activation trace slot k (a kernel argument: NULL in the captured graph,
+ * so a traced step is launched directly) */
+__device__ __forceinline__ uint8_t* f_atr(uint8_t* atr, const PkParams& P, int k)
 {
-    uint8_t* a = Sd->act_trace;
-    return a ? a + (size_t)k * Sd->act_stride : nullptr;
+    return atr ? atr + (size_t)k * P.act_stride : nullptr;
 }
 
 /* EMB: layer 0, whose input is the embedding row of the step's token */
 template <int LT, bool EMB>
 __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
-                                                      int l)
+                                                      int l, uint8_t* atr)
 {
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const Pk
     const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
     phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, 2, LG_QKV_R>(
         P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, P.qkv + (size_t)l * qs, xin, 0, 0,
-        f_tr(Sd, l, 0), f_atr(Sd, 4 * l));
+        f_tr(Sd, l, 0), f_atr(atr, P, 4 * l));
 }
 
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
@@ -85,72 +85,74 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const P
 }
 
 template <int LT, int HD, int NREP>
-__global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
+__global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
+                                                     uint8_t* atr)
 {
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed;
     phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
         P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, P.xs + (size_t)l * ne, P.xm + (size_t)l * ne, nullptr, 0, 0,
-        f_tr(Sd, l, 2), f_atr(Sd, 4 * l + 1), att_partials<HD, NREP>(P, l, Sd->pos));
+        f_tr(Sd, l, 2), f_atr(atr, P, 4 * l + 1), att_partials<HD, NREP>(P, l, Sd->pos));
 }
 
 template <int LT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
+__global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
+                                                     uint8_t* atr)
 {
     constexpr int NE = NsE<LT>::value;
     const int ne = P.n_embed, nff = P.n_ff;
     phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, 2, LG_UG_R>(
         P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, P.xm + (size_t)l * ne, nullptr, P.hb + (size_t)l * nff, nullptr, 0,
-        0, f_tr(Sd, l, 3), f_atr(Sd, 4 * l + 2));
+        0, f_tr(Sd, l, 3), f_atr(atr, P, 4 * l + 2));
 }
 
 template <int LT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
+__global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
+                                                       uint8_t* atr)
 {
     constexpr int NF = 3 * NsE<LT>::value;
     const int ne = P.n_embed, nff = P.n_ff;
     phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, 6, LG_DN_R>(
         P, 0, L.down, L.down_rsz, ne, 0, nullptr, P.hb + (size_t)l * nff, P.xm + (size_t)l * ne,
-        P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(Sd, 4 * l + 3));
+        P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(atr, P, 4 * l + 3));
 }
 
 template <int OT>
-__global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* __restrict__ Sd)
+__global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* __restrict__ Sd, uint8_t* atr)
 {
     constexpr int NO = NsE<OT>::value;
     const int pos = Sd->pos;
         phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
-        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0), f_atr(Sd, 4 * P.n_layers));
+        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0), f_atr(atr, P, 4 * P.n_layers));
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
     if (s_int[0] && threadIdx.x == 0) {
         Sd->tok = cld(P.tok_out);
         Sd->pos = pos + 1;
         Sd->trace = nullptr;    /* a trace covers one step */
-        Sd->act_trace = nullptr;
     }
 }
 
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t);
+typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t, uint8_t*);
 
 template <int LT, int OT, int HD, int NREP>
 static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n_layers, int nwg, bool long_ctx,
-                          hipStream_t st)
+                          hipStream_t st, uint8_t* atr)
 {
     const dim3 g(nwg), b(PK_THREADS);
     for (int l = 0; l < n_layers; l++) {
-        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l);
-        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l);
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l, atr);
+        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l, atr);
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
-        hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l);
-        hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l);
-        hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l);
+        hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, atr);
+        hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l, atr);
+        hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l, atr);
     }
-    hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S);
+    hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S, atr);
 }
 
 typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, bool, hipStream_t);
@@ -163,17 +165,17 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
     const dim3 g(nwg), b(PK_THREADS);
     switch (phase) {
     case 0:
-        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l);
-        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l);
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l, nullptr);
+        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l, nullptr);
         break;
     case 1:
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         break;
-    case 2: hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l); break;
-    case 3: hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l); break;
-    case 4: hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l); break;
-    default: hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S); break;
+    case 2: hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    case 3: hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    case 4: hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    default: hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S, nullptr); break;
     }
 }
 
@@ -201,9 +203,9 @@ const void* lg_fused_variant(int lt, int ot, int hd, int nrep)
 }
 
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
-                     bool long_ctx, hipStream_t s)
+                     bool long_ctx, hipStream_t s, uint8_t* act_trace)
 {
-    ((const FusedVariant*)variant)->fn(P, layers, S_dev, n_layers, nwg, long_ctx, s);
+    ((const FusedVariant*)variant)->fn(P, layers, S_dev, n_layers, nwg, long_ctx, s, act_trace);
     return lg_check_launch("fused decode step");
 }
 

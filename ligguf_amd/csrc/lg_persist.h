@@ -63,6 +63,7 @@ struct PkParams {
     uint32_t* err;           /* nonzero: a sync wait expired (or an unsupported phase) */
     const int* feed;         /* [n_ctx] prompt tokens for positions < PkStep.feed_end (fused path) */
     int spin_cap;
+    uint64_t act_stride;     /* bytes per slot of an activation trace */
 };
 
 /* what changes from token to token (PkParams, fixed per model, and PkStep
@@ -74,11 +75,11 @@ struct PkStep {
     uint64_t base;           /* progress value at launch; the launch adds 5*n_layers + 1 */
     uint64_t* trace;         /* NULL, or [5*n_layers+1][gridDim][4] timestamps (100 MHz clock):
                                 phase entry, wait done, activation built, phase published */
-    uint8_t* act_trace;      /* NULL, or [4*n_layers+1][act_stride] bytes: every quantized
-                                activation of the step as workgroup 0 built it (per layer: attention
-                                input, attention output, FFN input, SwiGLU output; then the output
-                                head's input), in its GGUF block layout */
-    uint64_t act_stride;
+    uint8_t* act_trace;      /* persistent kernel: NULL, or [4*n_layers+1][PkParams.act_stride] bytes:
+                                every quantized activation of the step as workgroup 0 built it (per
+                                layer: attention input, attention output, FFN input, SwiGLU output;
+                                then the output head's input), in its GGUF block layout (the fused
+                                kernels take the same pointer as a kernel argument) */
 };
 
 /* attention work split.  A workgroup step covers ppb = PK_THREADS * 8 /
@@ -165,7 +166,7 @@ __host__ __device__ inline bool pk_att_long(int pos, int head_dim, int nrep, int
  * the step's position selects the attention kernel. */
 const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep);
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
-                     bool long_ctx, hipStream_t s);
+                     bool long_ctx, hipStream_t s, uint8_t* act_trace = nullptr);
 /* one kernel of the fused step: phase 0 rmsnorm+QKV, 1 attention, 2 att_out,
  * 3 up|gate, 4 down (of `layer`), 5 output head */
 int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int phase, int layer,

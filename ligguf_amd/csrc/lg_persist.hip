@@ -89,7 +89,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
     const uint64_t B = S.base;
     constexpr int NE = NsE<LT>::value, NF = 3 * NE;
 #define TR(p) (S.trace ? S.trace + ((size_t)(p) * gridDim.x + blockIdx.x) * 4 : nullptr)
-#define ATR(k) (S.act_trace ? S.act_trace + (size_t)(k) * S.act_stride : nullptr)
+#define ATR(k) (S.act_trace ? S.act_trace + (size_t)(k) * P.act_stride : nullptr)
     for (int l = 0; l < P.n_layers; l++) {
         const PkLayer L = pk_layer(P, l);
         const uint64_t p0 = B + 5ull * l;
