@@ -189,8 +189,10 @@ int lg_argmax(lg_ctx* ctx, int* tok_out);
  * The first call allocates a workspace of 5 x vocab entries.  Synchronous. */
 int lg_sample_topp(lg_ctx* ctx, float temp, float topp, int topk, float r01, int* tok_out);
 
-/* lg_sample_topp over n device floats at logits_dev (no context; allocates
- * and frees its workspace per call, runs on the null stream).  Synchronous. */
+/* lg_sample_topp over n device floats at logits_dev (no context): a helper
+ * for tests and benchmarks -- it allocates and frees its workspace (about
+ * 5 n entries) on every call and runs on the null stream, waiting for it.
+ * Decode loops use lg_sample_topp, whose workspace lives in the context. */
 int lg_sample_topp_device(const float* logits_dev, int n, float temp, float topp, int topk, float r01, int* tok_out);
 
 /* feed_text's prompt loop (fast/ligguf_fast_qk.cpp:340-356): n tokens at

@@ -1207,7 +1207,7 @@ extern "C" int lg_sample_topp_device(const float* logits_dev, int n, float temp,
         const hipError_t e = hipMemcpy(tok_out, lg_sample_ws_out(w), sizeof(int), hipMemcpyDeviceToHost);
         if (e != hipSuccess) { lg_set_error("sample copy: %s", hipGetErrorString(e)); rc = LG_ERR_HIP; }
     }
-    hipDeviceSynchronize();
+    hipStreamSynchronize(nullptr);
     lg_sample_ws_free(w);
     return rc;
 }

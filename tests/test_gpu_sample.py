@@ -1,32 +1,67 @@
 """On-device top-p / top-k sampling (lg_sample_topp, lg_sample_topp_device)
-against the oracle's sampler_topp (fast/ligguf_fast_qk.cpp:172-214).
+against sampler_topp (fast/ligguf_fast_qk.cpp:172-214) evaluated in float64.
 
-The device sums probabilities as trees, the oracle (like the reference
-source) sequentially: tokens must be identical unless the draw or top-p lies
-within float rounding of a cumulative probability (conftest.sampler_agree),
-and identical in most trials of every case.
+The device computes p = expf((l - max) / temp) in float32 and sums as trees;
+its normalising sum and cumulative sums are within ~1e-6 of exact.  The
+float64 restatement (sampler64) takes the same float32 exponentials and sums
+them exactly enough, so the device must return its token unless the draw or
+top-p lies within DEVICE_TOL of a cumulative probability (then a token within
+DEVICE_TOL plus one entry of it), and must return exactly its token in at
+least 6 of 8 trials of every case.  (The oracle's or_sampler_topp sums
+sequentially in float, as the reference does, and is compared with the
+reference in tests/test_oracle.py under the looser float-sum bound.)
 """
 import numpy as np
 import pytest
 import torch
 
-from conftest import sampler_agree
 from ligguf_amd.lib import LgError, sample_topp_device
 from ligguf_amd.model import TINY, Engine, HostModel
 
 pytestmark = pytest.mark.gpu
 
-# (n, temp, topp, topk, identical trials of 8 at least): top-p over all of a
-# 151936-entry vocabulary normalises by a sum of 151936 terms, which the
-# oracle's sequential float sum gets wrong by ~5e-4 relative -- several
-# entries' widths at the cutoff -- so only the tolerance holds there
-CASES = [(151936, 0.8, 0.9, 0, 0), (151936, 0.7, 0.95, 40, 6), (151936, 2.0, 0.9, 0, 0), (151936, 1.0, 0.0, 0, 6),
-         (151936, 1.0, 1.5, 0, 0), (151936, 0.5, 0.5, 3, 6), (1000, 1.0, 0.9, 0, 6), (1, 1.0, 0.9, 0, 8),
-         (2049, 1.3, 0.99, 2056, 6)]
+# cumulative-probability distance within which two correct samplers may
+# disagree: the device's float32 tree sums of up to 151936 terms are within
+# ~1e-6 of exact; 1e-5 keeps a margin
+DEVICE_TOL = 1e-5
+
+CASES = [(151936, 0.8, 0.9, 0), (151936, 0.7, 0.95, 40), (151936, 2.0, 0.9, 0), (151936, 1.0, 0.0, 0),
+         (151936, 1.0, 1.5, 0), (151936, 0.5, 0.5, 3), (1000, 1.0, 0.9, 0), (1, 1.0, 0.9, 0),
+         (2049, 1.3, 0.99, 2056)]
 
 
-@pytest.mark.parametrize("n,temp,topp,topk,min_exact", CASES)
-def test_sample_topp_device_vs_oracle(gpu, oracle, n, temp, topp, topk, min_exact):
+def sampler64(lg, temp, topp, topk, r01):
+    """sampler_topp with the float32 exponentials of the device and float64
+    sums: (token, cumulative sums in sorted order, cutoff, r, order)."""
+    lg = np.asarray(lg, np.float32)
+    imax = int(np.argmax(lg))
+    inv = np.float32(1.0) / np.float32(temp)
+    e = np.exp(((lg - lg[imax]).astype(np.float32) * inv).astype(np.float32)).astype(np.float64)
+    p = e / e.sum()
+    order = np.lexsort((np.arange(p.size), -p))        # p descending, token ascending
+    cum = np.cumsum(p[order])
+    top = min(p[order[0]] if topp <= 0 else topp, 1.0)
+    k = p.size if topk <= 0 or topk > p.size else topk
+    cut = min(int(np.searchsorted(cum, top)), k - 1)
+    r = r01 * cum[cut]
+    pick = min(int(np.searchsorted(cum[:cut + 1], r)), cut)
+    return int(order[pick]), cum, cut, r, order, top
+
+
+def device_agrees(lg, temp, topp, topk, r01, got):
+    want, cum, cut, r, order, top = sampler64(lg, temp, topp, topk, r01)
+    if got == want:
+        return True, True
+    near = abs(cum[cut] - top) <= DEVICE_TOL or np.min(np.abs(cum[:cut + 1] - r)) <= DEVICE_TOL
+    rank = np.empty(order.size, np.int64)
+    rank[order] = np.arange(order.size)
+    p = np.diff(np.concatenate([[0.0], cum]))
+    far = abs(cum[rank[got]] - cum[rank[want]]) - max(p[rank[got]], p[rank[want]])
+    return bool(near) and far <= DEVICE_TOL, False
+
+
+@pytest.mark.parametrize("n,temp,topp,topk", CASES)
+def test_sample_topp_device_vs_float64(gpu, n, temp, topp, topk):
     print(f"sample n={n} temp={temp} topp={topp} topk={topk}", flush=True)
     rng = np.random.default_rng(n * 7 + topk)
     exact = 0
@@ -37,10 +72,11 @@ def test_sample_topp_device_vs_oracle(gpu, oracle, n, temp, topp, topk, min_exac
         r01 = 1.0 if trial == 0 else 0.0 if trial == 1 else float(np.float32(rng.random()))
         t = torch.from_numpy(lg).to("cuda:0")
         got = sample_topp_device(t.data_ptr(), n, temp, topp, topk, r01)
-        want = oracle.sampler_topp(lg, temp, topp, topk, r01)
-        assert sampler_agree(lg, temp, topp, topk, r01, got, want), (trial, got, want)
-        exact += got == want
-    assert exact >= min_exact, exact
+        ok, same = device_agrees(lg, temp, topp, topk, r01, got)
+        assert ok, (trial, got, sampler64(lg, temp, topp, topk, r01)[0])
+        exact += same
+    print(f"  identical in {exact} of 8 trials")
+    assert exact >= 6, exact
 
 
 def test_sample_topp_ties_take_lower_token(gpu):
@@ -64,9 +100,9 @@ def test_sample_topp_rejects_bad_draw(gpu):
         sample_topp_device(t.data_ptr(), 16, 1.0, 0.9, 0, 1.5)
 
 
-def test_engine_sample_topp_after_decode(gpu, oracle):
+def test_engine_sample_topp_after_decode(gpu):
     """lg_sample_topp over the logits a decode step left on the device, the
-    same draw through the oracle on their host copy; the second context size
+    same draw through sampler64 on their host copy; the second context size
     check reuses the workspace."""
     hm = HostModel.synthetic(TINY)
     eng = Engine(0)
@@ -79,8 +115,10 @@ def test_engine_sample_topp_after_decode(gpu, oracle):
             for temp, topp, topk in ((0.8, 0.9, 0), (1.0, 0.5, 5), (0.0, 0.9, 0)):
                 r01 = float(np.float32(rng.random()))
                 got = eng.sample_topp(temp, topp, topk, r01)
-                want = oracle.sampler_topp(lg, temp, topp, topk, r01)
-                assert sampler_agree(lg, temp, topp, topk, r01, got, want), (pos, temp, got, want)
+                if temp > 0:
+                    assert device_agrees(lg, temp, topp, topk, r01, got)[0], (pos, temp, got)
+                else:
+                    assert got == int(np.argmax(lg))
             tok = got
     finally:
         eng.close()
