@@ -186,12 +186,15 @@ int lg_argmax(lg_ctx* ctx, int* tok_out);
  * (topk <= 0: all), then the entry where it reaches r01 times the cutoff's.
  * r01 is the caller's uniform draw in [0, 1] -- the reference's
  * (float)rand() / (float)RAND_MAX.  temp <= 0 gives lg_argmax's token.
- * The first call allocates a workspace of 5 x vocab entries.  Synchronous. */
+ * The first call allocates a workspace of about 9 bytes per vocabulary entry
+ * and one pinned host word; vocabularies above 2^21 entries are refused
+ * (LG_ERR_ARG).  LG_ERR_STATE if a workgroup's bounded publish wait expired.
+ * Synchronous. */
 int lg_sample_topp(lg_ctx* ctx, float temp, float topp, int topk, float r01, int* tok_out);
 
 /* lg_sample_topp over n device floats at logits_dev (no context): a helper
  * for tests and benchmarks -- it allocates and frees its workspace (about
- * 5 n entries) on every call and runs on the null stream, waiting for it.
+ * 9 n bytes) on every call and runs on the null stream, waiting for it.
  * Decode loops use lg_sample_topp, whose workspace lives in the context. */
 int lg_sample_topp_device(const float* logits_dev, int n, float temp, float topp, int topk, float r01, int* tok_out);
 

@@ -269,6 +269,7 @@ int lg_sample_ws_alloc(int n, LgSampleWs** out);
 void lg_sample_ws_free(LgSampleWs* w);
 int lg_sample_ws_size(const LgSampleWs* w);
 int* lg_sample_ws_out(LgSampleWs* w);
+int* lg_sample_ws_out_host(LgSampleWs* w);   /* pinned host word the top-p launches also write */
 int lg_launch_sample_topp(const float* logits, LgSampleWs* w, float temp, float topp, int topk, float r01,
                           hipStream_t s);
 

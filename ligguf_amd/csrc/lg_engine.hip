@@ -1188,9 +1188,13 @@ extern "C" int lg_sample_topp(lg_ctx* ctx, float temp, float topp, int topk, flo
     }
     if (!ctx->samp && (rc = lg_sample_ws_alloc(ctx->vocab, &ctx->samp))) return ctx_fail(ctx, rc);
     if ((rc = lg_launch_sample_topp(ctx->logits, ctx->samp, temp, topp, topk, r01, ctx->stream))) return ctx_fail(ctx, rc);
-    const hipError_t e = hipMemcpyAsync(tok_out, lg_sample_ws_out(ctx->samp), sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
-    if (e != hipSuccess) { lg_set_error("sample copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
-    return lg_sync(ctx);
+    if ((rc = lg_sync(ctx))) return rc;
+    *tok_out = *(volatile int*)lg_sample_ws_out_host(ctx->samp);
+    if (*tok_out < 0) {
+        lg_set_error("sampler: a workgroup did not publish its entries in time");
+        return ctx_fail(ctx, LG_ERR_STATE);
+    }
+    return LG_OK;
 }
 
 extern "C" int lg_sample_topp_device(const float* logits_dev, int n, float temp, float topp, int topk, float r01,
@@ -1201,11 +1205,19 @@ extern "C" int lg_sample_topp_device(const float* logits_dev, int n, float temp,
     if (rc) return rc;
     LgSampleWs* w = nullptr;
     if ((rc = lg_sample_ws_alloc(n, &w))) return rc;
-    if (!(temp > 0.0f)) rc = lg_launch_argmax(logits_dev, n, lg_sample_ws_out(w), nullptr);
-    else rc = lg_launch_sample_topp(logits_dev, w, temp, topp, topk, r01, nullptr);
-    if (!rc) {
-        const hipError_t e = hipMemcpy(tok_out, lg_sample_ws_out(w), sizeof(int), hipMemcpyDeviceToHost);
-        if (e != hipSuccess) { lg_set_error("sample copy: %s", hipGetErrorString(e)); rc = LG_ERR_HIP; }
+    if (!(temp > 0.0f)) {
+        rc = lg_launch_argmax(logits_dev, n, lg_sample_ws_out(w), nullptr);
+        if (!rc) {
+            const hipError_t e = hipMemcpy(tok_out, lg_sample_ws_out(w), sizeof(int), hipMemcpyDeviceToHost);
+            if (e != hipSuccess) { lg_set_error("sample copy: %s", hipGetErrorString(e)); rc = LG_ERR_HIP; }
+        }
+    } else if (!(rc = lg_launch_sample_topp(logits_dev, w, temp, topp, topk, r01, nullptr))) {
+        const hipError_t e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) { lg_set_error("sampler: %s", hipGetErrorString(e)); rc = LG_ERR_HIP; }
+        else if ((*tok_out = *(volatile int*)lg_sample_ws_out_host(w)) < 0) {
+            lg_set_error("sampler: a workgroup did not publish its entries in time");
+            rc = LG_ERR_STATE;
+        }
     }
     hipStreamSynchronize(nullptr);
     lg_sample_ws_free(w);

@@ -94,6 +94,32 @@ def test_sample_topp_ties_take_lower_token(gpu):
     assert sample_topp_device(t.data_ptr(), n, 0.0, 0.9, 0, 0.3) == 7
 
 
+def test_sample_topp_large_buckets(gpu):
+    """Leading-digit buckets holding more entries than the select pass keeps
+    in LDS (12288): the selections read every block's slice from global
+    memory.  40000 equal logits (one bucket, every pick a tie broken by
+    token, ranks past 0 taking the token selection), and a near-flat
+    151936-entry vocabulary against sampler64."""
+    n = 40000
+    t = torch.zeros(n, dtype=torch.float32, device="cuda:0")
+    for i in (0, 1, 12287, 12288, 20000, 39999):
+        assert sample_topp_device(t.data_ptr(), n, 1.0, 1.0, 0, (i + 0.5) / n) == i
+    # top-k 30000: the draw scaled to the first 30000, mid-way through entry 15000
+    assert sample_topp_device(t.data_ptr(), n, 1.0, 1.0, 30000, 15000.5 / 30000) == 15000
+    rng = np.random.default_rng(11)
+    exact = 0
+    for trial in range(8):
+        lg = rng.normal(0, 0.02, 151936).astype(np.float32)
+        r01 = float(np.float32(rng.random()))
+        x = torch.from_numpy(lg).to("cuda:0")
+        got = sample_topp_device(x.data_ptr(), lg.size, 1.0, 0.9, 0, r01)
+        ok, same = device_agrees(lg, 1.0, 0.9, 0, r01, got)
+        assert ok, (trial, got, sampler64(lg, 1.0, 0.9, 0, r01)[0])
+        exact += same
+    print(f"  near-flat: identical in {exact} of 8 trials")
+    assert exact >= 6
+
+
 def test_sample_topp_rejects_bad_draw(gpu):
     t = torch.zeros(16, dtype=torch.float32, device="cuda:0")
     with pytest.raises(LgError):
