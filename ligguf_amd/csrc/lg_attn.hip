@@ -4,16 +4,30 @@
  *
  * Split over the sequence ("flash-decoding"): workgroup (chunk c, KV head
  * kh) takes positions [c*CH, min((c+1)*CH, pos+1)) and all NREP query heads
- * that share kh, so every K/V row is read from HBM once.  A K/V row of one
- * head is HD fp16 = 2*HD bytes; LPP lanes split it (DPL dims each, one
- * 128-bit load when DPL = 8), so a wave covers 64/LPP positions per step.
- *   pass 1: scores s[h][t] = q_h . k_t * scale into LDS (t == pos reads the
- *           fp32 k of this step, as fast/ligguf_fast_qk.cpp:77-79 does);
+ * that share kh, so every K/V row is read from HBM once.  The partials
+ * (m in log2 units, l, o) of each chunk go to the workspace; k_attn_merge
+ * rescales them by 2^(m_c - M) and divides by the total, which equals the
+ * reference's single-pass softmax.  t == pos takes the fp32 k and v of this
+ * step (fast/ligguf_fast_qk.cpp:77-79, 98-99): the cache row is not written
+ * yet.
+ *
+ * k_attn_tile (head_dim 64, 128, 256): one pass, 4 waves.  Each wave streams
+ * its own rows of every tile of TP positions (TP/4 per wave) into LDS with
+ * direct-to-LDS loads (global_load_lds_dwordx4), NBUF tiles deep, counting
+ * its waits by hand; the rows never pass through registers, and since no
+ * wave reads another's rows the loop has no workgroup barrier.  Per tile a
+ * wave takes the scores by LPP = HD/8 lanes per position (8 dims each, the
+ * 16-lane tree of the three-pass kernel), the online softmax in log2 units
+ * one (head, position) per lane (v_exp_f32; one rescale of the running sums
+ * per head and tile), then p.V by the position lanes.  The waves merge at
+ * the end.
+ *
+ * k_attn_split (head_dim 48, and position 0): three passes per chunk.
+ * A K/V row of one head is HD fp16 = 2*HD bytes; LPP lanes split it (DPL
+ * dims each), so a wave covers 64/LPP positions per step.
+ *   pass 1: scores s[h][t] = q_h . k_t * scale into LDS;
  *   pass 2: chunk max m and p = exp(s - m), l = sum p;
- *   pass 3: o[h] = sum_t p[h][t] v_t (fp32 v at t == pos, :98-99).
- * The partials (m, l, o) go to the workspace; k_attn_merge rescales them by
- * exp(m_c - M) and divides by the total, which equals the reference's
- * single-pass softmax.
+ *   pass 3: o[h] = sum_t p[h][t] v_t.
  */
 #include <math.h>
 
@@ -35,13 +49,60 @@ static int attn_chunk(int ctx)
     return c;
 }
 
+/* k_attn_tile: 4 waves; per tile each lane holds two 16-byte pieces of K
+ * (and of V), fewer when the softmax would need more than one lane per
+ * (query head, position): TPW positions per wave, TP = 4 TPW per tile.
+ * Chunks of a whole number of tiles, 64 of them (fewer for short contexts:
+ * at least 64 positions each), more past 4096 positions per chunk */
+#define LG_ATTN_TW 4
+#define LG_ATTN_TCH 64
+#define LG_ATTN_TMAX 4096
+__host__ __device__ constexpr int attn_tpw(int hd, int nrep)
+{
+    return (2 * 64 * 8 / hd) < (64 / nrep) ? (2 * 64 * 8 / hd) : (64 / nrep);
+}
+__host__ __device__ constexpr int attn_tp(int hd, int nrep) { return LG_ATTN_TW * attn_tpw(hd, nrep); }
+
+static bool attn_tiled(int head_dim, int pos)
+{
+    return pos > 0 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+static void attn_tile_split(int ctx, int hd, int nrep, int* chunk, int* nch)
+{
+    const int tp = attn_tp(hd, nrep);
+    int n = (ctx + 63) / 64;
+    if (n > LG_ATTN_TCH) n = LG_ATTN_TCH;
+    const int nmin = (ctx + LG_ATTN_TMAX - 1) / LG_ATTN_TMAX;
+    if (n < nmin) n = nmin;
+    int c = (ctx + n - 1) / n;
+    c = (c + tp - 1) / tp * tp;
+    *chunk = c;
+    *nch = (ctx + c - 1) / c;
+}
+
+/* chunks of a context: never fewer for a longer context, so a workspace
+ * sized for the last position serves every earlier one */
+static int attn_nch_bound(int head_dim, int pos)
+{
+    const int ctx = pos + 1;
+    if (attn_tiled(head_dim, pos)) {
+        const int nmin = (ctx + LG_ATTN_TMAX - 1) / LG_ATTN_TMAX;
+        return nmin > LG_ATTN_TCH ? nmin : LG_ATTN_TCH;
+    }
+    const int over = (ctx + LG_ATTN_MAX_CHUNK - 1) / LG_ATTN_MAX_CHUNK;
+    return over > 128 ? over : 128;
+}
+
 size_t lg_attn_ws_bytes(int n_heads, int head_dim, int pos)
 {
     if (n_heads <= 0 || head_dim <= 0 || pos < 0) return 0;
-    const int ctx = pos + 1;
-    const int ch = attn_chunk(ctx);
-    const int nch = (ctx + ch - 1) / ch;
-    return (size_t)n_heads * nch * (head_dim + 2) * sizeof(float);
+    /* the three-pass kernel of head_dim 48 and position 0 as well, at any
+     * earlier position */
+    int nb = attn_nch_bound(head_dim, pos);
+    const int nb3 = attn_nch_bound(48, pos);
+    if (nb3 > nb) nb = nb3;
+    return (size_t)n_heads * nb * (head_dim + 2) * sizeof(float);
 }
 
 template <int DPL>
@@ -68,8 +129,8 @@ __device__ __forceinline__ void load_f32_row(const float* __restrict__ p, float 
     for (int i = 0; i < DPL; i++) out[i] = p[i];
 }
 
-/* workspace layout per (kv head kh, chunk c): NREP m, NREP l, NREP*HD o;
- * i.e. per query head h = kh*NREP + r: index ((kh*nch + c)*NREP + r) */
+/* workspace layout per (kv head kh, chunk c): NREP m (log2 units), NREP l,
+ * NREP*HD o; i.e. per query head h = kh*NREP + r: index ((kh*nch + c)*NREP + r) */
 template <int HD, int NREP, int LPP>
 __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q, const float* __restrict__ kcur,
                                                     const float* __restrict__ vcur, const uint16_t* __restrict__ kc,
@@ -211,30 +272,329 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
     }
     if (threadIdx.x < NREP) {
         const int r = threadIdx.x;
-        out[r] = m[r];
+        out[r] = m[r] * 1.44269504088896341f;   /* log2 units, as k_attn_tile's */
         out[NREP + r] = s_m[r] + s_m[NREP + r] + s_m[2 * NREP + r] + s_m[3 * NREP + r];
     }
 }
 
-/* one workgroup per query head: merge the chunk partials */
+/* 16 bytes from global memory to LDS at m0 + 16 * lane (m0 wave-uniform);
+ * completion counts in vmcnt like any vector load, and nothing but an
+ * explicit s_waitcnt waits for it.  m0 is named as clobbered although the
+ * compiler reserves it (it warns): none of these kernels uses m0 otherwise
+ * (checked in their ISA). */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void attn_dma16(const void* g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void attn_wait_vm()
+{
+    static_assert(N >= 0 && N <= 63, "vmcnt field");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* barrier: this wave's LDS operations done, then every wave */
+__device__ __forceinline__ void attn_bar()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+/* the 8 halves of a 16-byte piece, each converted inside the fma that uses
+ * it (v_fma_mix_f32: the conversion is exact, the fma the same) */
+struct AttnH8 {
+    _Float16 h[8];
+    __device__ __forceinline__ void set(uint4 u) { __builtin_memcpy(h, &u, 16); }
+    __device__ __forceinline__ float f(int i) const { return (float)h[i]; }
+};
+
+/* workspace layout as k_attn_split's; LG_ATTN_TW waves, chunk a multiple of TP */
+template <int HD, int NREP>
+__global__ __launch_bounds__(LG_ATTN_TW * 64) void k_attn_tile(const float* __restrict__ q, const float* __restrict__ kcur,
+                                                   const float* __restrict__ vcur, const uint16_t* __restrict__ kc,
+                                                   const uint16_t* __restrict__ vc, int kv_dim, int pos, int chunk,
+                                                   int nch, float scale2, float* __restrict__ ws)
+{
+    constexpr int NW = LG_ATTN_TW;
+    constexpr int TPW = attn_tpw(HD, NREP);  /* positions per wave and tile */
+    constexpr int TP = NW * TPW;             /* positions per tile */
+    constexpr int CPR = HD * 2 / 16;         /* 16-byte pieces per fp16 row */
+    constexpr int PW = TPW * CPR;            /* pieces per wave, tile and matrix */
+    constexpr int NBUF = 4;
+    constexpr int IPW = PW / 64;             /* DMA instructions per wave, tile and matrix */
+    constexpr int IPT = 2 * IPW;
+    constexpr int LPP = HD / 8;              /* lanes per position in the scores and p.V */
+    constexpr int PPW = 64 / LPP;            /* positions per wave step */
+    constexpr int SPT = TPW / PPW;           /* steps per wave and tile */
+    constexpr int HP = (NREP * HD + 2 * HD) * 4 / 16;   /* pieces of q, k, v of this step */
+    constexpr int HI = (HP + NW * 64 - 1) / (NW * 64);   /* their instructions per wave */
+    static_assert(PW % 64 == 0 && IPW >= 1, "tile in whole wave instructions");
+    static_assert(TPW % PPW == 0 && NREP * TPW <= 64, "wave geometry");
+    static_assert(HI + (NBUF - 2) * IPT <= 63, "vmcnt range");
+    /* each wave's own rows of every buffered tile: no wave reads another's */
+    __shared__ __attribute__((aligned(16))) uint4 s_kv[2][NBUF][NW][PW];   /* K, V */
+    __shared__ __attribute__((aligned(16))) float s_head[HI * NW * 64 * 4];   /* q (NREP x HD), k, v */
+    __shared__ float s_s[NW][NREP * TPW];   /* per wave: scores, then exponentials */
+    __shared__ float s_a[NW][NREP];         /* per wave: rescale of the running sums */
+    __shared__ float s_ml[NW][2 * NREP];
+    static_assert(NW * NREP * HD * 4 <= (int)sizeof(s_kv), "the waves' outputs fit the tile buffers");
+
+    const int c = blockIdx.x, kh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gl = lane & (LPP - 1), grp = lane / LPP;
+    const int t0 = c * chunk;
+    const int t1 = min(t0 + chunk, pos + 1);
+    const int ntiles = (t1 - t0 + TP - 1) / TP;
+    const uint32_t lds_k = (uint32_t)(uintptr_t)&s_kv[0][0][wave][0], lds_v = (uint32_t)(uintptr_t)&s_kv[1][0][wave][0];
+
+    /* q of the group's heads, k and v of this step, shared by the waves
+     * (pieces past the end load the last one again) */
+#pragma unroll
+    for (int k = 0; k < HI; k++) {
+        const int pc = min((k * NW + wave) * 64 + lane, HP - 1);
+        const int f = pc * 4;                  /* float index in s_head */
+        const float* src = f < NREP * HD ? q + (size_t)kh * NREP * HD + f
+                         : f < NREP * HD + HD ? kcur + (size_t)kh * HD + (f - NREP * HD)
+                                              : vcur + (size_t)kh * HD + (f - NREP * HD - HD);
+        attn_dma16(src, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)s_head + (k * NW + wave) * 1024));
+    }
+    /* this wave's rows of tile j (positions t0 + j*TP + wave*TPW ..) into
+     * buffer j % NBUF.  Rows past the chunk, past the context and row pos
+     * (not in the cache yet) load the chunk's last cache row instead and are
+     * not used. */
+    const int tend = min(t1, pos);        /* the tiles' positions: [t0, tend) from the cache */
+    const int tlast = tend - 1;           /* the last row read from the cache */
+    auto issue = [&](int j) {
+        const int b = j % NBUF;
+#pragma unroll
+        for (int k = 0; k < IPW; k++) {
+            const int pc = k * 64 + lane;
+            const int row = pc / CPR, col = pc % CPR;
+            const int t = min(t0 + j * TP + wave * TPW + row, tlast);
+            const size_t o = (size_t)t * kv_dim + (size_t)kh * HD + col * 8;
+            const uint32_t off = (uint32_t)((b * NW * PW + k * 64) * 16);
+            attn_dma16(kc + o, __builtin_amdgcn_readfirstlane(lds_k + off));
+            attn_dma16(vc + o, __builtin_amdgcn_readfirstlane(lds_v + off));
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; j++) issue(j);
+
+    float qr[NREP][8];
+    float o[NREP][8];
+    float m_run = -INFINITY, l_run = 0.0f;   /* lanes i < NREP*TPW: head i / TPW (log2 units) */
+#pragma unroll
+    for (int r = 0; r < NREP; r++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[r][i] = 0.0f;
+    const int sr = lane / TPW, sp = lane % TPW;   /* this lane's (head, position) in the softmax */
+    const bool slane = lane < NREP * TPW;
+
+    for (int i = 0; i < ntiles; i++) {
+        attn_wait_vm<(NBUF - 2) * IPT>();   /* this wave's tile i (and its head pieces) */
+        if (i == 0) {
+            attn_bar();                      /* every wave's head pieces */
+#pragma unroll
+            for (int r = 0; r < NREP; r++)
+#pragma unroll
+                for (int d = 0; d < 8; d++) qr[r][d] = s_head[r * HD + gl * 8 + d];
+        }
+        /* the buffer of tile i - 1 (read by this wave only) takes tile
+         * i + NBUF - 1 once this wave's reads of it are done */
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + NBUF - 1);
+        const int b = i % NBUF;
+        const int tb = t0 + i * TP + wave * TPW;   /* first position of this wave's share */
+        /* scores (log2 units); position pos is taken after the tiles */
+#pragma unroll
+        for (int st = 0; st < SPT; st++) {
+            const int pl = st * PPW + grp;          /* position in the wave's share */
+            const int t = tb + pl;
+            AttnH8 kh8;
+            kh8.set(s_kv[0][b][wave][pl * CPR + gl]);
+#pragma unroll
+            for (int r = 0; r < NREP; r++) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; d++) sc = __builtin_fmaf(kh8.f(d), qr[r][d], sc);
+                sc = lg_group_sum<LPP>(sc);
+                if (gl == 0) s_s[wave][r * TPW + pl] = t < tend ? sc * scale2 : -INFINITY;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        /* softmax: lane (head sr, position sp); tile max and sum over the
+         * TPW lanes of the head */
+        if (slane) {
+            const float sv = s_s[wave][sr * TPW + sp];
+            const float mn = fmaxf(m_run, lg_group_max<TPW>(sv));
+            const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mn);
+            const float p = sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv - mn);
+            l_run = l_run * a + lg_group_sum<TPW>(p);
+            m_run = mn;
+            s_s[wave][sr * TPW + sp] = p;
+            if (sp == 0) s_a[wave][sr] = a;
+        }
+        __builtin_amdgcn_wave_barrier();
+        /* p.V; the running sums rescale only when a head's maximum moved
+         * (a is 1 otherwise: the branch is uniform over the wave) */
+#pragma unroll
+        for (int r = 0; r < NREP; r++) {
+            const float ar = s_a[wave][r];
+            if (ar != 1.0f) {
+#pragma unroll
+                for (int d = 0; d < 8; d++) o[r][d] *= ar;
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < SPT; st++) {
+            const int pl = st * PPW + grp;
+            AttnH8 vh8;
+            vh8.set(s_kv[1][b][wave][pl * CPR + gl]);
+#pragma unroll
+            for (int r = 0; r < NREP; r++) {
+                const float p = s_s[wave][r * TPW + pl];
+#pragma unroll
+                for (int d = 0; d < 8; d++) o[r][d] = __builtin_fmaf(vh8.f(d), p, o[r][d]);
+            }
+        }
+    }
+    attn_wait_vm<0>();   /* the trailing tiles (not used) land before the buffers are reused */
+    /* position pos (the chunk holding it, wave 0): this step's fp32 k and v,
+     * one more online-softmax step on the wave's state; every position
+     * group computes it, the groups' p.V terms are summed below, so only
+     * group 0 adds its o term */
+    if (wave == 0 && pos < t1) {
+#pragma unroll
+        for (int r = 0; r < NREP; r++) {
+            float sc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 8; d++) sc = __builtin_fmaf(s_head[NREP * HD + gl * 8 + d], qr[r][d], sc);
+            const float sv = lg_group_sum<LPP>(sc) * scale2;
+            const float mr = __shfl(m_run, r * TPW, 64), lr = __shfl(l_run, r * TPW, 64);
+            const float mn = fmaxf(mr, sv);
+            const float a = mr == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr - mn);
+            const float p = __builtin_amdgcn_exp2f(sv - mn);
+#pragma unroll
+            for (int d = 0; d < 8; d++)
+                o[r][d] = __builtin_fmaf(grp == 0 ? p : 0.0f, s_head[NREP * HD + HD + gl * 8 + d], o[r][d] * a);
+            if (slane && sr == r) {
+                m_run = mn;
+                l_run = lr * a + p;
+            }
+        }
+    }
+    /* the wave's position groups share its running max: plain sums over
+     * the lanes holding the same dims (lane ^ LPP, ^ 2 LPP, ..) */
+#pragma unroll
+    for (int r = 0; r < NREP; r++)
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            float v = o[r][d];
+            if constexpr (LPP <= 8) v += __shfl_xor(v, 8, 64);
+            if constexpr (LPP <= 16) v += lg_partner<4>(v);
+            if constexpr (LPP <= 32) v += lg_partner<5>(v);
+            o[r][d] = v;
+        }
+    attn_bar();
+    float* s_o = (float*)&s_kv[0][0][0][0];   /* [NW waves][NREP][HD] */
+    if (grp == 0) {
+#pragma unroll
+        for (int r = 0; r < NREP; r++)
+#pragma unroll
+            for (int d = 0; d < 8; d++) s_o[(wave * NREP + r) * HD + gl * 8 + d] = o[r][d];
+    }
+    if (slane && sp == 0) {
+        s_ml[wave][sr] = m_run;
+        s_ml[wave][NREP + sr] = l_run;
+    }
+    attn_bar();
+    float* out = ws + ((size_t)kh * nch + c) * NREP * (HD + 2);
+    for (int k = tid; k < NREP * HD; k += NW * 64) {
+        const int r = k / HD, d = k % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, s_ml[w][r]);
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float mw = s_ml[w][r];
+            const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            O += s_o[(w * NREP + r) * HD + d] * wt;
+            L += s_ml[w][NREP + r] * wt;
+        }
+        out[2 * NREP + r * HD + d] = O;
+        if (d == 0) {
+            out[r] = M;
+            out[NREP + r] = L;
+        }
+    }
+}
+
+/* one workgroup of 256 per query head: merge the chunk partials.  The
+ * chunk weights 2^(m_c - M) and the total L once (threads over chunks,
+ * weights of the first LG_ATTN_MERGE_W chunks kept in LDS), then each thread
+ * sums one dim over a share of the chunks (PARTS threads per dim, their
+ * loads issued together) and the shares add in LDS. */
+#define LG_ATTN_MERGE_W 1024
 template <int HD, int NREP>
 __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws, int nch, float* __restrict__ out)
 {
-    const int h = blockIdx.x;
+    constexpr int PARTS = HD >= 256 ? 1 : 256 / HD;
+    constexpr int U = 8;
+    __shared__ float s_w[LG_ATTN_MERGE_W];
+    __shared__ float s_red[8];
+    __shared__ float s_acc[PARTS][HD];
+    const int h = blockIdx.x, tid = threadIdx.x;
     const int kh = h / NREP, r = h % NREP;
+    const size_t stride = (size_t)NREP * (HD + 2);
+    const float* base = ws + (size_t)kh * nch * stride;
     float M = -INFINITY;
-#pragma unroll 8
-    for (int c = 0; c < nch; c++) M = fmaxf(M, ws[((size_t)kh * nch + c) * NREP * (HD + 2) + r]);
-    for (int dd = threadIdx.x; dd < HD; dd += blockDim.x) {
-        float L = 0.0f, acc = 0.0f;
-#pragma unroll 8
-        for (int c = 0; c < nch; c++) {
-            const float* p = ws + ((size_t)kh * nch + c) * NREP * (HD + 2);
-            const float w = expf(p[r] - M);
-            L += p[NREP + r] * w;
-            acc += p[2 * NREP + r * HD + dd] * w;
+    for (int c = tid; c < nch; c += 256) M = fmaxf(M, base[c * stride + r]);
+    M = lg_group_max<64>(M);
+    if ((tid & 63) == 0) s_red[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float L = 0.0f;
+    for (int c = tid; c < nch; c += 256) {
+        const float w = __builtin_amdgcn_exp2f(base[c * stride + r] - M);
+        if (c < LG_ATTN_MERGE_W) s_w[c] = w;
+        L += base[c * stride + NREP + r] * w;
+    }
+    L = lg_group_sum<64>(L);
+    __syncthreads();
+    if ((tid & 63) == 0) s_red[4 + (tid >> 6)] = L;
+    __syncthreads();
+    L = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
+    for (int d0 = 0; d0 < HD; d0 += 256 / PARTS) {
+        const int d = d0 + tid % (256 / PARTS), part = tid / (256 / PARTS);
+        float acc = 0.0f;
+        if (d < HD) {
+            const float* col = base + 2 * NREP + r * HD + d;
+            for (int c0 = part; c0 < nch; c0 += PARTS * U) {
+                float v[U], w[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int c = min(c0 + u * PARTS, nch - 1);
+                    v[u] = col[c * stride];
+                    w[u] = c < LG_ATTN_MERGE_W ? s_w[c] : __builtin_amdgcn_exp2f(base[c * stride + r] - M);
+                }
+#pragma unroll
+                for (int u = 0; u < U; u++)
+                    if (c0 + u * PARTS < nch) acc += v[u] * w[u];
+            }
+            s_acc[part][d] = acc;
         }
-        out[(size_t)h * HD + dd] = acc / L;
+        __syncthreads();
+        if (part == 0 && d < HD) {
+            float t = s_acc[0][d];
+#pragma unroll
+            for (int k = 1; k < PARTS; k++) t += s_acc[k][d];
+            out[(size_t)h * HD + d] = t / L;
+        }
+        __syncthreads();
     }
 }
 
@@ -243,13 +603,22 @@ static void launch_attn(const float* q, const float* k, const float* v, const ui
                         int n_kv_heads, int pos, float* out, float* ws, hipStream_t s)
 {
     const int ctx = pos + 1;
-    const int ch = attn_chunk(ctx);
-    const int nch = (ctx + ch - 1) / ch;
     const float scale = 1.0f / sqrtf((float)HD);
+    int ch, nch;
+    if constexpr (HD == 64 || HD == 128 || HD == 256) {
+        if (attn_tiled(HD, pos)) {
+            attn_tile_split(ctx, HD, NREP, &ch, &nch);
+            hipLaunchKernelGGL((k_attn_tile<HD, NREP>), dim3(nch, n_kv_heads), dim3(LG_ATTN_TW * 64), 0, s, q, k, v, kc, vc,
+                               n_kv_heads * HD, pos, ch, nch, scale * 1.44269504088896341f, ws);
+            hipLaunchKernelGGL((k_attn_merge<HD, NREP>), dim3(n_kv_heads * NREP), dim3(256), 0, s, ws, nch, out);
+            return;
+        }
+    }
+    ch = attn_chunk(ctx);
+    nch = (ctx + ch - 1) / ch;
     hipLaunchKernelGGL((k_attn_split<HD, NREP, LPP>), dim3(nch, n_kv_heads), dim3(256), 0, s, q, k, v, kc, vc,
                        n_kv_heads * HD, pos, ch, nch, scale, ws);
-    hipLaunchKernelGGL((k_attn_merge<HD, NREP>), dim3(n_kv_heads * NREP), dim3(HD < 256 ? (HD + 63) / 64 * 64 : 256), 0, s,
-                       ws, nch, out);
+    hipLaunchKernelGGL((k_attn_merge<HD, NREP>), dim3(n_kv_heads * NREP), dim3(256), 0, s, ws, nch, out);
 }
 
 template <int HD, int LPP>
@@ -296,10 +665,9 @@ int lg_launch_attn(const float* q, const float* k, const float* v, const uint16_
 /* lg_attn_decode_noalloc: the same kernels on a scratch area that the */
 /* library holds in device memory for the life of the process          */
 /* ------------------------------------------------------------------ */
-/* 8 MiB per device: lg_attn_ws_bytes for 32 heads of 128 at up to
- * 131072 positions (128 chunks of 1024), or 64 heads of 128 at up to
- * 65536.  Every partial is written before it is read, so nothing needs
- * clearing between calls. */
+/* 8 MiB per device: lg_attn_ws_bytes for 32 heads of 128 at up to ~2M
+ * positions (504 chunks), 64 heads of 256 at up to ~500k.  Every partial is
+ * written before it is read, so nothing needs clearing between calls. */
 #define LG_ATTN_SCRATCH_BYTES ((size_t)8 << 20)
 #define LG_ATTN_SCRATCH_DEVICES 64
 

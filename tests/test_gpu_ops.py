@@ -194,7 +194,8 @@ def _attn_case(gpu, oracle, nh, nkv, hd, pos, seed):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos", [(32, 8, 128, 511), (32, 8, 128, 4095), (32, 8, 128, 32767),
-                                           (6, 6, 48, 200), (8, 4, 64, 1000), (16, 2, 128, 77), (32, 8, 128, 0)])
+                                           (6, 6, 48, 200), (8, 4, 64, 1000), (16, 2, 128, 77), (32, 8, 128, 0),
+                                           (32, 8, 128, 1), (16, 4, 256, 700), (8, 8, 64, 33), (32, 8, 128, 300000)])
 def test_attention(gpu, oracle, nh, nkv, hd, pos):
     out, ref = _attn_case(gpu, oracle, nh, nkv, hd, pos, pos + hd)
     assert np.max(np.abs(out - ref)) <= 2e-6 * max(1.0, float(np.max(np.abs(ref)))), float(np.max(np.abs(out - ref)))
