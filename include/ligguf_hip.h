@@ -323,6 +323,115 @@ int lg_attn_decode_noalloc(const float* q, const float* k, const float* v, const
  * out_q may be NULL when only hb is wanted). */
 int lg_swiglu_quant(float* hb, const float* hb2, int n, int qtype, void* out_q, void* stream);
 
+/* ===================================================================== */
+/* BERT sentence embedding and the vector memory (fast/vdb.cpp)           */
+/* ===================================================================== */
+/* The chat driver's retrieval memory embeds every logged user turn and each
+ * new user line with a BERT encoder (bert_embed, fast/vdb.cpp:123-245) and
+ * searches the stored fp16 vectors by cosine similarity (vdb_query,
+ * fast/vdb.cpp:337-377).  Text handling -- WordPiece tokenization
+ * (bert_tokenize, :75-121), the chat-log parser (vdb_create, :269-335) and
+ * the prompt text (vdb_to_prompt, :408-424) -- stays on the host; the
+ * encoder and the search run here.
+ *
+ * Weight types: F32 and F16 matrices are used as stored and multiply fp32
+ * activations (dot_f32 / dot_f16_f32, fast/lil_math.cpp:761-762); Q8_0, Q1_0
+ * and Q1_G matrices multiply Q8_0-quantized activations as matmul() does for
+ * them (:751-755) -- they are repacked at upload into int8 values plus one
+ * fp32 scale per 32.  K-quant matrices are refused with LG_ERR_TYPE: the
+ * reference's bert_embed passes no Q8_K activation for them
+ * (fast/vdb.cpp:180,220,224,228). */
+typedef struct lg_bert lg_bert;
+
+/* One encoder block: bert_block (fast/lil_gguf.h:146-160).  Biases and
+ * LayerNorm vectors are F32 host arrays of the matrix's output width. */
+typedef struct {
+    lg_weight attn_q, attn_k, attn_v, attn_out;      /* n_embed x n_embed */
+    const float *attn_q_bias, *attn_k_bias, *attn_v_bias, *attn_out_bias;
+    const float *attn_norm_w, *attn_norm_b;          /* attn_output_norm */
+    lg_weight ffn_up;                                /* n_ff x n_embed */
+    lg_weight ffn_down;                              /* n_embed x n_ff */
+    const float *ffn_up_bias, *ffn_down_bias;
+    const float *ffn_norm_w, *ffn_norm_b;            /* layer_output_norm */
+} lg_bert_layer_desc;
+
+/* The encoder: the BERT fields of gguf_model (fast/lil_gguf.h:200-205, read
+ * by read_bert, fast/lil_gguf.cpp:501-556) and the tokenizer ids bert_embed
+ * wraps a sequence with (tok_cls, tok_sep, fast/lil_gguf.cpp:384-386). */
+typedef struct {
+    int32_t n_layers, n_embed, n_heads, n_ff, n_context, vocab_size;
+    int32_t tok_cls, tok_sep;
+    float eps;                                  /* bert.attention.layer_norm_epsilon */
+    lg_weight tok_embd;                         /* vocab_size x n_embed */
+    lg_weight pos_embd;                         /* n_context x n_embed */
+    lg_weight tok_types;                        /* >= 1 x n_embed; row 0 is used */
+    const float *emb_norm_w, *emb_norm_b;       /* token_embd_norm */
+    const lg_bert_layer_desc* layers;           /* n_layers entries */
+} lg_bert_desc;
+
+/* Open device `device` and create an encoder handle (no model yet).  The
+ * reference keeps one static bert_runtime (fast/vdb.cpp:16-35). */
+int lg_bert_create(int device, lg_bert** out);
+int lg_bert_destroy(lg_bert* b);
+const char* lg_bert_last_error(const lg_bert* b);
+
+/* Copy the encoder into HBM (ensure_bert's model, fast/vdb.cpp:62-73) and
+ * allocate activations for up to max_tokens tokens per pass (0: the larger
+ * of n_context and 4096).  Requires n_embed % n_heads == 0, head_dim <= 128,
+ * n_embed and n_ff multiples of 32. */
+int lg_bert_load(lg_bert* b, const lg_bert_desc* desc, int max_tokens);
+
+/* bert_embed (fast/vdb.cpp:123-245) after tokenization: toks are
+ * bert_tokenize's ids; they are cut to n_context-2, wrapped in
+ * tok_cls ... tok_sep, run through the encoder, mean-pooled over the
+ * sequence and L2-normalised into out_host[n_embed].  Synchronous. */
+int lg_bert_embed(lg_bert* b, const int* toks, int ntok, float* out_host);
+
+/* Several sequences in one pass (each attends only to itself): sequence s is
+ * toks[offsets[s] .. offsets[s+1]), out_host receives nseq x n_embed.  Same
+ * result per sequence as lg_bert_embed; no counterpart in the reference,
+ * which embeds the log's turns one at a time (fast/vdb.cpp:256,316). */
+int lg_bert_embed_batch(lg_bert* b, const int* toks, const int* offsets, int nseq, float* out_host);
+
+/* Test hook, no counterpart in the reference: the next pass (the first pass
+ * of the next lg_bert_embed / _batch / lg_bert_query call) copies each Q8_0
+ * activation it quantizes for a Q8_0/Q1 matrix into trace_dev, device memory
+ * of lg_bert_trace_size() bytes: slot (layer l, point s) -- s = 0 the block
+ * input, 1 the attention output, 2 the normalised attention-block output,
+ * 3 the GELU output -- starts at (4 l + s) * lg_bert_trace_size() /
+ * (4 n_layers) and holds int8 quants [T][width] followed, at max_tokens *
+ * max(n_embed, n_ff) bytes, by the fp16-rounded block scales as floats
+ * [width/32][T] (T: the pass's tokens, max_tokens as lg_bert_load rounded it
+ * up to a multiple of 64).  Lets a test tell rounding flips of the int8
+ * quantizer from arithmetic errors. */
+size_t lg_bert_trace_size(const lg_bert* b);
+int lg_bert_trace_next(lg_bert* b, void* trace_dev);
+
+/* The vector memory: fp16 vectors [n][dim] in HBM (vdb_entry::vec,
+ * fast/vdb.h:10-14, filled by f32_to_f16_row at fast/vdb.cpp:258).
+ * lg_bert_vdb_set replaces the contents, lg_bert_vdb_append adds rows at the
+ * end (vdb_create / vdb_log_turn, fast/vdb.cpp:269-335,426-436); dim must be
+ * the encoder's n_embed. */
+int lg_bert_vdb_set(lg_bert* b, const uint16_t* vecs_host, int n, int dim);
+int lg_bert_vdb_append(lg_bert* b, const uint16_t* vecs_host, int n, int dim);
+int lg_bert_vdb_size(const lg_bert* b);
+
+/* vdb_query's search (fast/vdb.cpp:352-368) for the embedding emb_host[dim]:
+ * sim_i = fp16 row i . emb; rows with sim < threshold are skipped (the
+ * reference's VDB_LIKENESS_THRESHOLD is 0.75, fast/vdb.h:8); the k best
+ * (k <= 8; VDB_MAX_RETRIEVAL is 3) go to idx_out/sim_out in descending
+ * similarity, the lower row first among equal ones, as the reference's
+ * strict-greater insertion orders them.  NaN similarities are skipped.
+ * Returns the number found (0..k) or a negative LG_ERR_*. */
+int lg_bert_vdb_query(lg_bert* b, const float* emb_host, int dim, float threshold, int k, int* idx_out,
+                      float* sim_out);
+
+/* vdb_query (fast/vdb.cpp:337-377) from tokens: lg_bert_embed followed by
+ * the search, the embedding staying in HBM; emb_out_host (optional)
+ * receives it.  Returns the number found or a negative LG_ERR_*. */
+int lg_bert_query(lg_bert* b, const int* toks, int ntok, float threshold, int k, int* idx_out, float* sim_out,
+                  float* emb_out_host);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,20 @@ class LgModelDesc(C.Structure):
                 ("output_norm", _vp), ("layers", _vp)]
 
 
+class LgBertLayerDesc(C.Structure):
+    _fields_ = [("attn_q", LgWeight), ("attn_k", LgWeight), ("attn_v", LgWeight), ("attn_out", LgWeight),
+                ("attn_q_bias", _vp), ("attn_k_bias", _vp), ("attn_v_bias", _vp), ("attn_out_bias", _vp),
+                ("attn_norm_w", _vp), ("attn_norm_b", _vp), ("ffn_up", LgWeight), ("ffn_down", LgWeight),
+                ("ffn_up_bias", _vp), ("ffn_down_bias", _vp), ("ffn_norm_w", _vp), ("ffn_norm_b", _vp)]
+
+
+class LgBertDesc(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("n_embed", C.c_int32), ("n_heads", C.c_int32), ("n_ff", C.c_int32),
+                ("n_context", C.c_int32), ("vocab_size", C.c_int32), ("tok_cls", C.c_int32), ("tok_sep", C.c_int32),
+                ("eps", C.c_float), ("tok_embd", LgWeight), ("pos_embd", LgWeight), ("tok_types", LgWeight),
+                ("emb_norm_w", _vp), ("emb_norm_b", _vp), ("layers", _vp)]
+
+
 # Every exported symbol of include/ligguf_hip.h with its ctypes signature.
 SIGNATURES = {
     "lg_row_size": (C.c_int64, [C.c_int, C.c_int64]),
@@ -92,6 +106,19 @@ SIGNATURES = {
     "lg_attn_scratch_bytes": (C.c_size_t, []),
     "lg_attn_decode_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "lg_swiglu_quant": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "lg_bert_create": (C.c_int, [C.c_int, C.POINTER(_vp)]),
+    "lg_bert_destroy": (C.c_int, [_vp]),
+    "lg_bert_last_error": (C.c_char_p, [_vp]),
+    "lg_bert_load": (C.c_int, [_vp, C.POINTER(LgBertDesc), C.c_int]),
+    "lg_bert_embed": (C.c_int, [_vp, _vp, C.c_int, _vp]),
+    "lg_bert_embed_batch": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp]),
+    "lg_bert_trace_size": (C.c_size_t, [_vp]),
+    "lg_bert_trace_next": (C.c_int, [_vp, _vp]),
+    "lg_bert_vdb_set": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
+    "lg_bert_vdb_append": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
+    "lg_bert_vdb_size": (C.c_int, [_vp]),
+    "lg_bert_vdb_query": (C.c_int, [_vp, _vp, C.c_int, C.c_float, C.c_int, _vp, _vp]),
+    "lg_bert_query": (C.c_int, [_vp, _vp, C.c_int, C.c_float, C.c_int, _vp, _vp, _vp]),
 }
 
 _lib = None

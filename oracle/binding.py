@@ -59,6 +59,20 @@ class OrModel(C.Structure):
                 ("output_norm", _vp), ("layers", _vp)]
 
 
+class OrBertLayer(C.Structure):
+    _fields_ = [("attn_q", OrWeight), ("attn_k", OrWeight), ("attn_v", OrWeight), ("attn_out", OrWeight),
+                ("attn_q_bias", _vp), ("attn_k_bias", _vp), ("attn_v_bias", _vp), ("attn_out_bias", _vp),
+                ("attn_norm_w", _vp), ("attn_norm_b", _vp), ("ffn_up", OrWeight), ("ffn_down", OrWeight),
+                ("ffn_up_bias", _vp), ("ffn_down_bias", _vp), ("ffn_norm_w", _vp), ("ffn_norm_b", _vp)]
+
+
+class OrBert(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("n_embed", C.c_int32), ("n_heads", C.c_int32), ("n_ff", C.c_int32),
+                ("n_context", C.c_int32), ("vocab_size", C.c_int32), ("tok_cls", C.c_int32), ("tok_sep", C.c_int32),
+                ("eps", C.c_float), ("tok_embd", OrWeight), ("pos_embd", OrWeight), ("tok_types", OrWeight),
+                ("emb_norm_w", _vp), ("emb_norm_b", _vp), ("layers", _vp)]
+
+
 class Oracle:
     """The plain-C restatement."""
 
@@ -94,6 +108,10 @@ class Oracle:
         L.or_state_kv_write.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_argmax.argtypes = [_fp, C.c_int]
         L.or_sampler_topp.argtypes = [_fp, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float]
+        L.or_layernorm.argtypes = [_fp, _fp, _fp, _fp, C.c_int, C.c_float]
+        L.or_bert_embed.argtypes = [C.POINTER(OrBert), _vp, C.c_int, _fp]
+        L.or_bert_embed_traced.argtypes = [C.POINTER(OrBert), _vp, C.c_int, _fp, _fp]
+        L.or_vdb_search.argtypes = [_vp, C.c_int, C.c_int, _fp, C.c_float, C.c_int, _vp, _fp]
 
     # --- scalar helpers
     def fp16_to_fp32(self, h: np.ndarray) -> np.ndarray:
@@ -185,6 +203,45 @@ class Oracle:
         x, px = _f32(logits)
         return int(self.L.or_sampler_topp(px, x.size, temp, topp, topk, r01))
 
+    # --- BERT / vector memory
+    def layernorm(self, x, w, b, eps):
+        x, px = _f32(x)
+        w, pw = _f32(w)
+        b, pb = _f32(b)
+        out = np.empty(x.size, np.float32)
+        self.L.or_layernorm(out.ctypes.data_as(_fp), px, pw, pb, x.size, eps)
+        return out
+
+    def bert_embed(self, hb, toks) -> np.ndarray:
+        """or_bert_embed of a HostBert (ligguf_amd.bert) for bert_tokenize's ids"""
+        d = hb.fill_desc(OrBert, OrBertLayer, OrWeight)
+        a = np.ascontiguousarray(toks, dtype=np.int32)
+        out = np.empty(hb.cfg.n_embed, np.float32)
+        assert self.L.or_bert_embed(C.byref(d), a.ctypes.data, a.size, out.ctypes.data_as(_fp)) == 0
+        return out
+
+    def bert_embed_traced(self, hb, toks):
+        """(embedding, trace [n_layers][4][T][max(n_embed, n_ff)]): the float
+        vectors at the four quantization points of each block"""
+        c = hb.cfg
+        d = hb.fill_desc(OrBert, OrBertLayer, OrWeight)
+        a = np.ascontiguousarray(toks, dtype=np.int32)
+        T = min(a.size, c.n_context - 2) + 2
+        tr = np.zeros((c.n_layers, 4, T, max(c.n_embed, c.n_ff)), np.float32)
+        out = np.empty(c.n_embed, np.float32)
+        assert self.L.or_bert_embed_traced(C.byref(d), a.ctypes.data, a.size, out.ctypes.data_as(_fp),
+                                           tr.ctypes.data_as(_fp)) == 0
+        return out, tr
+
+    def vdb_search(self, vecs, emb, thr: float, k: int):
+        v = np.ascontiguousarray(vecs, dtype=np.uint16)
+        e, pe = _f32(emb)
+        idx = np.empty(k, np.int32)
+        sim = np.empty(k, np.float32)
+        n = self.L.or_vdb_search(v.ctypes.data, v.shape[0] if v.ndim == 2 else v.size // e.size, e.size, pe, thr, k,
+                                 idx.ctypes.data, sim.ctypes.data_as(_fp))
+        return idx[:n].copy(), sim[:n].copy()
+
     # --- whole engine
     def new_state(self, model_struct: OrModel):
         self._keep = model_struct
@@ -255,6 +312,13 @@ class Reference:
         L.ref_dequantize_row.argtypes = [C.c_int, _vp, _fp, C.c_int64]
         L.ref_quantize_q8_0.argtypes = [_fp, C.c_int, _vp]
         L.ref_quantize_q8_K.argtypes = [_fp, C.c_int, _vp]
+        L.ref_bert_open.argtypes = [C.c_char_p]
+        L.ref_bert_n_embed.argtypes = []
+        L.ref_bert_tokenize.argtypes = [C.c_char_p, _vp, C.c_int]
+        L.ref_bert_embed.argtypes = [C.c_char_p, _fp, C.c_int]
+        L.ref_vdb_create.argtypes = [C.c_char_p]
+        L.ref_vdb_entry.argtypes = [C.c_int, _vp, _vp, C.c_int]
+        L.ref_vdb_query.argtypes = [C.c_char_p, _vp, C.c_int]
         L.ref_matmul.argtypes = [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _fp, _fp]
         L.ref_matmul_q.argtypes = [C.c_int, _vp, C.c_uint32, C.c_int, C.c_int, _vp, _fp]
         L.ref_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
@@ -411,6 +475,39 @@ class Reference:
         out = np.empty(vocab, np.float32)
         self.L.ref_logits(out.ctypes.data_as(_fp))
         return out
+
+    # --- BERT / vector memory (fast/vdb.cpp, through oracle/ref_bert.cpp)
+    def bert_open(self, path: str) -> int:
+        """vdb_set_model + ensure_bert; returns n_embed"""
+        assert self.L.ref_bert_open(path.encode()) == 0, path
+        return int(self.L.ref_bert_n_embed())
+
+    def bert_tokenize(self, text: bytes) -> list:
+        cap = 4 * len(text) + 16
+        out = np.empty(cap, np.int32)
+        n = self.L.ref_bert_tokenize(text, out.ctypes.data, cap)
+        return [int(x) for x in out[:n]]
+
+    def bert_embed(self, text: bytes) -> np.ndarray:
+        ne = int(self.L.ref_bert_n_embed())
+        out = np.empty(ne, np.float32)
+        assert self.L.ref_bert_embed(text, out.ctypes.data_as(_fp), ne) == ne
+        return out
+
+    def vdb_create(self, log: bytes) -> int:
+        return int(self.L.ref_vdb_create(log))
+
+    def vdb_entry(self, i: int):
+        ne = int(self.L.ref_bert_n_embed())
+        ts = C.c_uint32()
+        vec = np.empty(ne, np.uint16)
+        assert self.L.ref_vdb_entry(i, C.byref(ts), vec.ctypes.data, ne) == ne
+        return int(ts.value), vec
+
+    def vdb_query(self, text: bytes) -> list:
+        idx = np.empty(16, np.int32)
+        n = self.L.ref_vdb_query(text, idx.ctypes.data, 16)
+        return [int(x) for x in idx[:n]]
 
     def kv_rows(self, layer, p0, np_, kv_dim):
         k = np.empty(np_ * kv_dim, np.uint16)

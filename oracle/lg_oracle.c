@@ -720,3 +720,175 @@ void or_state_kv(const or_state* s, int layer, int p0, int np, uint16_t* k, uint
     if (k) memcpy(k, s->kc + off, cnt * 2);
     if (v) memcpy(v, s->vc + off, cnt * 2);
 }
+
+/* ------------------------------------------------------------------ */
+/* (f)4: BERT sentence embedding (fast/vdb.cpp:123-245).               */
+/* Token / position / type rows are dequantized and summed in fp32 as  */
+/* the reference does (:162-165); matrix products go through           */
+/* or_matvec (Q8_0 activations for Q8_0/Q1 weights, fp32 for F32/F16,  */
+/* fast/lil_math.cpp:748-776); biases, residuals, attention, GELU,     */
+/* pooling and the L2 norm are evaluated in double and rounded once.   */
+/* ------------------------------------------------------------------ */
+void or_layernorm(float* out, const float* x, const float* w, const float* b, int n, float eps)
+{
+    /* the reference's own double accumulation (fast/lil_math.cpp:948-962) */
+    double mean = 0.0, var = 0.0;
+    for (int i = 0; i < n; i++) mean += x[i];
+    mean /= n;
+    for (int i = 0; i < n; i++) {
+        const double d = x[i] - mean;
+        var += d * d;
+    }
+    var /= n;
+    const float scale = 1.0f / sqrtf((float)(var + (double)eps));
+    for (int i = 0; i < n; i++) out[i] = (float)(((double)x[i] - mean) * (double)scale * (double)w[i] + (double)b[i]);
+}
+
+static float or_gelu1(float v)
+{
+    /* gelu (fast/lil_math.cpp:978-984) with its float constants */
+    const double c0 = (double)0.7978845608f, c1 = (double)0.044715f, d = v;
+    return (float)(0.5 * d * (1.0 + tanh(c0 * (d + c1 * d * d * d))));
+}
+
+int or_bert_embed(const or_bert* m, const int* toks_in, int ntok_in, float* out)
+{
+    return or_bert_embed_traced(m, toks_in, ntok_in, out, NULL);
+}
+
+int or_bert_embed_traced(const or_bert* m, const int* toks_in, int ntok_in, float* out, float* trace)
+{
+    const int ne = m->n_embed, nff = m->n_ff, nh = m->n_heads, hd = ne / nh;
+    int raw = ntok_in;
+    if (raw > m->n_context - 2) raw = m->n_context - 2;      /* toks.resize(n_context - 2), :135 */
+    const int T = raw + 2;
+    int* toks = (int*)malloc((size_t)T * sizeof(int));
+    toks[0] = m->tok_cls;                                     /* :136-137 */
+    for (int i = 0; i < raw; i++) toks[1 + i] = toks_in[i];
+    toks[T - 1] = m->tok_sep;
+    for (int i = 0; i < T; i++)
+        if (toks[i] < 0 || toks[i] >= m->vocab_size) { free(toks); return -1; }
+
+    float* x = (float*)malloc((size_t)T * ne * 4);
+    float* q = (float*)malloc((size_t)T * ne * 4);
+    float* k = (float*)malloc((size_t)T * ne * 4);
+    float* v = (float*)malloc((size_t)T * ne * 4);
+    float* ctx = (float*)malloc((size_t)T * ne * 4);
+    float* r0 = (float*)malloc((size_t)ne * 4);
+    float* r1 = (float*)malloc((size_t)ne * 4);
+    float* r2 = (float*)malloc((size_t)ne * 4);
+    float* hf = (float*)malloc((size_t)nff * 4);
+    double* att = (double*)malloc((size_t)T * sizeof(double));
+    double* acc = (double*)malloc((size_t)hd * sizeof(double));
+
+    /* embeddings + layernorm (:155-168) */
+    or_dequantize_row(m->tok_types.type, m->tok_types.data, r2, ne);
+    for (int t = 0; t < T; t++) {
+        or_dequantize_row(m->tok_embd.type, (const uint8_t*)m->tok_embd.data + (size_t)toks[t] * m->tok_embd.rsz, r0, ne);
+        or_dequantize_row(m->pos_embd.type, (const uint8_t*)m->pos_embd.data + (size_t)t * m->pos_embd.rsz, r1, ne);
+        for (int i = 0; i < ne; i++) r0[i] = r0[i] + r1[i] + r2[i];
+        or_layernorm(x + (size_t)t * ne, r0, m->emb_norm_w, m->emb_norm_b, ne, m->eps);
+    }
+    const double scale = (double)(1.0f / sqrtf((float)hd));
+    const int wmax = ne > nff ? ne : nff;
+#define OR_TRACE(l, s, t, src, n) \
+    if (trace) memcpy(trace + (((size_t)(l) * 4 + (s)) * T + (t)) * wmax, (src), (size_t)(n) * 4)
+    for (int l = 0; l < m->n_layers; l++) {
+        const or_bert_layer* L = &m->layers[l];
+        /* q, k, v (:173-187) */
+        for (int t = 0; t < T; t++) {
+            const float* xt = x + (size_t)t * ne;
+            OR_TRACE(l, 0, t, xt, ne);
+            or_matvec(L->attn_q.type, L->attn_q.data, L->attn_q.rsz, ne, ne, xt, q + (size_t)t * ne);
+            or_matvec(L->attn_k.type, L->attn_k.data, L->attn_k.rsz, ne, ne, xt, k + (size_t)t * ne);
+            or_matvec(L->attn_v.type, L->attn_v.data, L->attn_v.rsz, ne, ne, xt, v + (size_t)t * ne);
+            for (int i = 0; i < ne; i++) {
+                q[(size_t)t * ne + i] = (float)((double)q[(size_t)t * ne + i] + L->attn_q_bias[i]);
+                k[(size_t)t * ne + i] = (float)((double)k[(size_t)t * ne + i] + L->attn_k_bias[i]);
+                v[(size_t)t * ne + i] = (float)((double)v[(size_t)t * ne + i] + L->attn_v_bias[i]);
+            }
+        }
+        /* bidirectional attention per head (:189-212) */
+        for (int t = 0; t < T; t++)
+            for (int h = 0; h < nh; h++) {
+                const float* qh = q + (size_t)t * ne + h * hd;
+                double mx = -INFINITY, sum = 0.0;
+                for (int u = 0; u < T; u++) {
+                    const float* kh = k + (size_t)u * ne + h * hd;
+                    double s = 0.0;
+                    for (int d = 0; d < hd; d++) s += (double)qh[d] * kh[d];
+                    att[u] = s * scale;
+                    if (att[u] > mx) mx = att[u];
+                }
+                for (int u = 0; u < T; u++) { att[u] = exp(att[u] - mx); sum += att[u]; }
+                for (int d = 0; d < hd; d++) acc[d] = 0.0;
+                for (int u = 0; u < T; u++) {
+                    const float* vh = v + (size_t)u * ne + h * hd;
+                    const double p = att[u] / sum;
+                    for (int d = 0; d < hd; d++) acc[d] += p * vh[d];
+                }
+                for (int d = 0; d < hd; d++) ctx[(size_t)t * ne + h * hd + d] = (float)acc[d];
+            }
+        /* att_out + bias + residual, layernorm; up + bias, gelu; down + bias
+         * + residual, layernorm (:214-232) */
+        for (int t = 0; t < T; t++) {
+            float* xt = x + (size_t)t * ne;
+            OR_TRACE(l, 1, t, ctx + (size_t)t * ne, ne);
+            or_matvec(L->attn_out.type, L->attn_out.data, L->attn_out.rsz, ne, ne, ctx + (size_t)t * ne, r1);
+            for (int i = 0; i < ne; i++) r1[i] = (float)((double)r1[i] + L->attn_out_bias[i] + xt[i]);
+            or_layernorm(r0, r1, L->attn_norm_w, L->attn_norm_b, ne, m->eps);
+            OR_TRACE(l, 2, t, r0, ne);
+            or_matvec(L->ffn_up.type, L->ffn_up.data, L->ffn_up.rsz, ne, nff, r0, hf);
+            for (int i = 0; i < nff; i++) hf[i] = or_gelu1((float)((double)hf[i] + L->ffn_up_bias[i]));
+            OR_TRACE(l, 3, t, hf, nff);
+            or_matvec(L->ffn_down.type, L->ffn_down.data, L->ffn_down.rsz, nff, ne, hf, r1);
+            for (int i = 0; i < ne; i++) r1[i] = (float)((double)r1[i] + L->ffn_down_bias[i] + r0[i]);
+            or_layernorm(xt, r1, L->ffn_norm_w, L->ffn_norm_b, ne, m->eps);
+        }
+    }
+#undef OR_TRACE
+    /* mean over the tokens, l2norm (:237-244, fast/lil_math.cpp:939-946) */
+    double ss = 0.0;
+    for (int i = 0; i < ne; i++) {
+        double s = 0.0;
+        for (int t = 0; t < T; t++) s += x[(size_t)t * ne + i];
+        r0[i] = (float)(s / T);
+        ss += (double)r0[i] * r0[i];
+    }
+    for (int i = 0; i < ne; i++) out[i] = ss > 0.0 ? (float)(r0[i] / sqrt(ss)) : r0[i];
+
+    free(toks); free(x); free(q); free(k); free(v); free(ctx); free(r0); free(r1); free(r2); free(hf); free(att); free(acc);
+    return 0;
+}
+
+/* vdb_query's loop (fast/vdb.cpp:352-368): similarity of each fp16 row
+ * (vec_dot_f16_f32, in double, rounded once), rows below thr skipped, and
+ * the reference's strict-greater insertion into the k best */
+int or_vdb_search(const uint16_t* vecs, int n, int dim, const float* emb, float thr, int k, int* idx, float* sim)
+{
+    float best[64];
+    int bi[64];
+    if (k <= 0 || k > 64) return -1;
+    for (int i = 0; i < k; i++) { best[i] = -1e30f; bi[i] = -1; }
+    for (int r = 0; r < n; r++) {
+        double s = 0.0;
+        for (int d = 0; d < dim; d++) s += (double)or_fp16_to_fp32(vecs[(size_t)r * dim + d]) * emb[d];
+        const float sf = (float)s;
+        if (!(sf >= thr)) continue;
+        for (int j = 0; j < k; j++) {
+            if (sf <= best[j]) continue;
+            for (int u = k - 1; u > j; u--) { best[u] = best[u - 1]; bi[u] = bi[u - 1]; }
+            best[j] = sf;
+            bi[j] = r;
+            break;
+        }
+    }
+    int cnt = 0;
+    for (int j = 0; j < k; j++) {
+        if (bi[j] < 0) continue;
+        idx[cnt] = bi[j];
+        sim[cnt] = best[j];
+        cnt++;
+    }
+    return cnt;
+}

@@ -124,6 +124,41 @@ void or_state_kv_write(or_state* s, int layer, int p0, int np, const uint16_t* k
 int or_argmax(const float* x, int n);
 int or_sampler_topp(const float* logits, int n, float temp, float topp, int topk, float r01);
 
+/* ---- (f)4: BERT embedding and vector-memory search (fast/vdb.cpp) ----
+ * Descriptors laid out as lg_bert_layer_desc / lg_bert_desc
+ * (include/ligguf_hip.h), bert_block / gguf_model's BERT fields
+ * (fast/lil_gguf.h:146-160,200-205). */
+typedef struct {
+    or_weight attn_q, attn_k, attn_v, attn_out;
+    const float *attn_q_bias, *attn_k_bias, *attn_v_bias, *attn_out_bias;
+    const float *attn_norm_w, *attn_norm_b;
+    or_weight ffn_up, ffn_down;
+    const float *ffn_up_bias, *ffn_down_bias;
+    const float *ffn_norm_w, *ffn_norm_b;
+} or_bert_layer;
+
+typedef struct {
+    int32_t n_layers, n_embed, n_heads, n_ff, n_context, vocab_size, tok_cls, tok_sep;
+    float eps;
+    or_weight tok_embd, pos_embd, tok_types;
+    const float *emb_norm_w, *emb_norm_b;
+    const or_bert_layer* layers;
+} or_bert;
+
+/* layernorm (fast/lil_math.cpp:948-962) */
+void or_layernorm(float* out, const float* x, const float* w, const float* b, int n, float eps);
+/* bert_embed (fast/vdb.cpp:123-245) of bert_tokenize's ids: out[n_embed] */
+int or_bert_embed(const or_bert* m, const int* toks, int ntok, float* out);
+/* the same, recording the float vector at each of the 4 points per block
+ * where matmul() would quantize it for a Q8_0/Q1 matrix -- the block input,
+ * the attention output, the normalised attention-block output and the GELU
+ * output -- into trace [n_layers][4][T][max(n_embed, n_ff)] (T = the
+ * wrapped sequence length) */
+int or_bert_embed_traced(const or_bert* m, const int* toks, int ntok, float* out, float* trace);
+/* vdb_query's search (fast/vdb.cpp:352-368) over fp16 rows [n][dim]: the k
+ * best at or above thr in the reference's insertion order; returns the count */
+int or_vdb_search(const uint16_t* vecs, int n, int dim, const float* emb, float thr, int k, int* idx, float* sim);
+
 #ifdef __cplusplus
 }
 #endif

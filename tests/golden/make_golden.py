@@ -8,6 +8,7 @@ reference.
 
     python tests/golden/make_golden.py                  # everything
     python tests/golden/make_golden.py --teacher-only   # tiny_teacher.npz alone
+    python tests/golden/make_golden.py --bert-only      # bert.npz alone
 """
 from __future__ import annotations
 
@@ -204,9 +205,55 @@ def tiny_teacher():
     print("tiny_teacher.npz written to", HERE)
 
 
+BERT_TEXTS = [b"Hello world, the cat sat on the mat!", b"What is the WEATHER like in Paris on Monday?",
+              b"", b"xyzzy quux", b"caf\xc3\xa9 \xe2\x82\xac42 coffee", b"(a)[b]{c}", b"python code " * 40]
+BERT_LOG = (b"@@1700000000\n<<<<<<<\nthe cat sat on the mat\n>>>>>>>\nnice cat\n"
+            b"@@1700000100\n<<<<<<<\nwhat is the weather in paris\n>>>>>>>\nsunny and warm\n"
+            b"@@1700000200\n<<<<<<<\nI like pizza for dinner\nand coffee\n>>>>>>>\nme too\n"
+            b"@@1700000300\n<<<<<<<\nthe cat sat on the mat\n>>>>>>>\nagain?\n"
+            b"@@1700000400\n<<<<<<<\npython code search\n>>>>>>>\nok")
+BERT_QUERIES = [b"the cat sat on the mat", b"weather in paris", b"pizza dinner coffee", b"river mountain tree"]
+BERT_TYPES = [(F32, F16), (F16, F16), (Q8_0, Q8_0), (Q1_G, F32)]
+
+
+def bert_golden():
+    """bert.npz: the reference's bert_tokenize ids and bert_embed vectors
+    (fast/vdb.cpp:75-245) for BERT_TEXTS on the tiny synthetic encoder in four
+    weight types, and for its vector memory (vdb_create over BERT_LOG, then
+    vdb_query) the entries' timestamps and fp16 vectors and the indices found
+    for each of BERT_QUERIES."""
+    from ligguf_amd.bert import BERT_TINY, HostBert
+    R = load_reference()
+    out = {}
+    for lt, et in BERT_TYPES:
+        hb = HostBert.synthetic(BERT_TINY.with_(layer_type=lt, embd_type=et))
+        path = os.path.join("/tmp", f"ligguf_bert_{lt}.gguf")
+        hb.write_gguf(path)
+        R.bert_open(path)
+        key = f"t{lt}_{et}"
+        out[key + "_wsum"] = np.array([int(np.sum(hb.weights[nm][3], dtype=np.uint64) % (1 << 61))
+                                       for nm in sorted(hb.weights)], np.uint64)
+        for i, t in enumerate(BERT_TEXTS):
+            out[f"{key}_tok{i}"] = np.array(R.bert_tokenize(t), np.int32)
+            out[f"{key}_emb{i}"] = R.bert_embed(t)
+        n = R.vdb_create(BERT_LOG)
+        ents = [R.vdb_entry(i) for i in range(n)]
+        out[key + "_vdb_ts"] = np.array([e[0] for e in ents], np.uint32)
+        out[key + "_vdb_vec"] = np.stack([e[1] for e in ents])
+        for i, q in enumerate(BERT_QUERIES):
+            out[f"{key}_q{i}_emb"] = R.bert_embed(q)
+            out[f"{key}_q{i}_idx"] = np.array(R.vdb_query(q), np.int32)
+        os.unlink(path)
+    np.savez_compressed(os.path.join(HERE, "bert.npz"), **out)
+    print("bert.npz written to", HERE)
+
+
 if __name__ == "__main__":
     if "--teacher-only" in sys.argv:
         tiny_teacher()
+    elif "--bert-only" in sys.argv:
+        bert_golden()
     else:
         main()
         tiny_teacher()
+        bert_golden()
