@@ -220,133 +220,158 @@ struct BGemm {
     int ldo;
 };
 
-/* One wave per 32-token x 32-row tile (2 x 2 MFMA tiles of 16 x 16).
- * MFMA operand A holds tokens (M), B weight rows (N); the output D[m][n]
- * of a 16 x 16 tile sits in lane (g = l/16, m = l%16) as tokens 4g..4g+3,
- * row m.  fp32 form: per 32-value chunk, lane group g takes values
- * 8g..8g+7 of its token and its row, and MFMA step j (of 8) multiplies
- * value 8g+j -- the four lane groups give the K = 4 of each step, so the
- * eight steps cover the chunk.  int8 form: one v_mfma_i32_16x16x32_i8 per
- * 32-value block (lane group g: bytes 8g..8g+7), the block's integer sum
- * scaled by both block scales. */
-template <int WT, int EP>
+/* One wave per (16 TM)-token x (16 TN)-row tile (TM x TN MFMA tiles of
+ * 16 x 16; the launcher picks the largest tile that still gives the grid
+ * enough waves).  MFMA operand A holds tokens (M), B weight rows (N); the
+ * output D[m][n] of a 16 x 16 tile sits in lane (g = l/16, m = l%16) as
+ * tokens 4g..4g+3, row m.  fp32 form: per 32-value chunk, lane group g
+ * takes values 8g..8g+7 of its token and its row, and MFMA step j (of 8)
+ * multiplies value 8g+j -- the four lane groups give the K = 4 of each
+ * step, so the eight steps cover the chunk.  int8 form: one
+ * v_mfma_i32_16x16x32_i8 per 32-value block (lane group g: bytes
+ * 8g..8g+7), the block's integer sum scaled by both block scales. */
+template <int WT, int EP, int TM, int TN>
 __global__ __launch_bounds__(64) void k_bert_gemm(BGemm a)
 {
     const int lane = threadIdx.x, g = lane >> 4, m = lane & 15;
-    const int ntt = (a.T + 31) >> 5;
-    const int t0 = (blockIdx.x % ntt) * 32, r0 = (blockIdx.x / ntt) * 32;
-    int tr[2], wr[2];
+    const int ntt = (a.T + 16 * TM - 1) / (16 * TM);
+    const int t0 = (blockIdx.x % ntt) * 16 * TM, r0 = (blockIdx.x / ntt) * 16 * TN;
+    int tr[TM], wr[TN];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        tr[i] = min(t0 + 16 * i + m, a.T - 1);
-        wr[i] = min(r0 + 16 * i + m, a.R - 1);
-    }
-    v4f acc[2][2];
+    for (int i = 0; i < TM; i++) tr[i] = min(t0 + 16 * i + m, a.T - 1);
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int j = 0; j < TN; j++) wr[j] = min(r0 + 16 * j + m, a.R - 1);
+    v4f acc[TM][TN];
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
+    /* NPF chunks of 32 values in flight: chunk c sits in register slot
+     * c % NPF, loaded NPF - 1 chunks before it is multiplied */
+    constexpr int NPF = 4;
     if constexpr (WT == BF_I8) {
-        const int8_t* ap[2];
-        const int8_t* bp[2];
+        const int8_t* ap[TM];
+        const int8_t* bp[TN];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            ap[i] = a.q + (size_t)tr[i] * a.K + 8 * g;
-            bp[i] = (const int8_t*)a.w + (size_t)wr[i] * a.K + 8 * g;
-        }
+        for (int i = 0; i < TM; i++) ap[i] = a.q + (size_t)tr[i] * a.K + 8 * g;
+#pragma unroll
+        for (int j = 0; j < TN; j++) bp[j] = (const int8_t*)a.w + (size_t)wr[j] * a.K + 8 * g;
         const int nb = a.K >> 5;
-        for (int b = 0; b < nb; b++) {
-            long av[2], bv[2];
-            float4 xd[2];
-            float wdv[2];
+        long av[NPF][TM], bv[NPF][TN];
+        float4 xd[NPF][TM];
+        float wdv[NPF][TN];
+        auto load = [&](int u, int b) {
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                av[i] = *(const long*)(ap[i] + 32 * b);
-                bv[i] = *(const long*)(bp[i] + 32 * b);
-                xd[i] = *(const float4*)(a.qd + (size_t)b * a.ldd + t0 + 16 * i + 4 * g);
-                wdv[i] = a.wd[(size_t)b * a.R + wr[i]];
+            for (int i = 0; i < TM; i++) {
+                av[u][i] = *(const long*)(ap[i] + 32 * b);
+                xd[u][i] = *(const float4*)(a.qd + (size_t)b * a.ldd + t0 + 16 * i + 4 * g);
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const float xs[4] = {xd[i].x, xd[i].y, xd[i].z, xd[i].w};
+            for (int j = 0; j < TN; j++) {
+                bv[u][j] = *(const long*)(bp[j] + 32 * b);
+                wdv[u][j] = a.wd[(size_t)b * a.R + wr[j]];
+            }
+        };
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        for (int u = 0; u < NPF - 1; u++)
+            if (u < nb) load(u, u);
+        for (int b0 = 0; b0 < nb; b0 += NPF) {
 #pragma unroll
-                    for (int v = 0; v < 4; v++) acc[i][j][v] = __builtin_fmaf(xs[v] * wdv[j], (float)s[v], acc[i][j][v]);
+            for (int u = 0; u < NPF; u++) {
+                const int b = b0 + u;
+                if (b + NPF - 1 < nb) load((u + NPF - 1) % NPF, b + NPF - 1);
+                if (b < nb) {
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        const float xs[4] = {xd[u][i].x, xd[u][i].y, xd[u][i].z, xd[u][i].w};
+#pragma unroll
+                        for (int j = 0; j < TN; j++) {
+                            const v4i sm = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][i], bv[u][j], (v4i){0, 0, 0, 0},
+                                                                                 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                acc[i][j][v] = __builtin_fmaf(xs[v] * wdv[u][j], (float)sm[v], acc[i][j][v]);
+                        }
+                    }
                 }
             }
         }
     } else {
         constexpr int ESZ = WT == LG_F32 ? 4 : 2;
-        const float* ap[2];
-        const uint8_t* bp[2];
+        const float* ap[TM];
+        const uint8_t* bp[TN];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            ap[i] = a.x + (size_t)tr[i] * a.ldx + 8 * g;
-            bp[i] = a.w + ((size_t)wr[i] * a.K + 8 * g) * ESZ;
-        }
-        float4 A[2][2], An[2][2];
-        uint4 B[2][ESZ / 2], Bn[2][ESZ / 2];
-        auto load = [&](float4 (&Ar)[2][2], uint4 (&Br)[2][ESZ / 2], int k0) {
+        for (int i = 0; i < TM; i++) ap[i] = a.x + (size_t)tr[i] * a.ldx + 8 * g;
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                Ar[i][0] = *(const float4*)(ap[i] + k0);
-                Ar[i][1] = *(const float4*)(ap[i] + k0 + 4);
+        for (int j = 0; j < TN; j++) bp[j] = a.w + ((size_t)wr[j] * a.K + 8 * g) * ESZ;
+        float4 A[NPF][TM][2];
+        uint4 B[NPF][TN][ESZ / 2];
+        auto load = [&](int u, int k0) {
 #pragma unroll
-                for (int h = 0; h < ESZ / 2; h++) Br[i][h] = *(const uint4*)(bp[i] + (size_t)k0 * ESZ + 16 * h);
+            for (int i = 0; i < TM; i++) {
+                A[u][i][0] = *(const float4*)(ap[i] + k0);
+                A[u][i][1] = *(const float4*)(ap[i] + k0 + 4);
             }
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int h = 0; h < ESZ / 2; h++) B[u][j][h] = *(const uint4*)(bp[j] + (size_t)k0 * ESZ + 16 * h);
         };
-        load(A, B, 0);
-        for (int k0 = 0; k0 < a.K; k0 += 32) {
-            if (k0 + 32 < a.K) load(An, Bn, k0 + 32);
-            float af[2][8], bf[2][8];
+        const int nc = a.K >> 5;
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                af[i][0] = A[i][0].x; af[i][1] = A[i][0].y; af[i][2] = A[i][0].z; af[i][3] = A[i][0].w;
-                af[i][4] = A[i][1].x; af[i][5] = A[i][1].y; af[i][6] = A[i][1].z; af[i][7] = A[i][1].w;
-                if constexpr (WT == LG_F32) {
+        for (int u = 0; u < NPF - 1; u++)
+            if (u < nc) load(u, 32 * u);
+        for (int c0 = 0; c0 < nc; c0 += NPF) {
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        bf[i][4 * h + 0] = __uint_as_float(B[i][h].x);
-                        bf[i][4 * h + 1] = __uint_as_float(B[i][h].y);
-                        bf[i][4 * h + 2] = __uint_as_float(B[i][h].z);
-                        bf[i][4 * h + 3] = __uint_as_float(B[i][h].w);
+            for (int u = 0; u < NPF; u++) {
+                const int c = c0 + u;
+                if (c + NPF - 1 < nc) load((u + NPF - 1) % NPF, 32 * (c + NPF - 1));
+                if (c < nc) {
+                    float af[TM][8], bf[TN][8];
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        af[i][0] = A[u][i][0].x; af[i][1] = A[u][i][0].y; af[i][2] = A[u][i][0].z; af[i][3] = A[u][i][0].w;
+                        af[i][4] = A[u][i][1].x; af[i][5] = A[u][i][1].y; af[i][6] = A[u][i][1].z; af[i][7] = A[u][i][1].w;
                     }
-                } else {
-                    const uint32_t u[4] = {B[i][0].x, B[i][0].y, B[i][0].z, B[i][0].w};
 #pragma unroll
-                    for (int h = 0; h < 4; h++) {
-                        bf[i][2 * h] = lg_h2f((uint16_t)(u[h] & 0xffffu));
-                        bf[i][2 * h + 1] = lg_h2f((uint16_t)(u[h] >> 16));
+                    for (int j = 0; j < TN; j++) {
+                        if constexpr (WT == LG_F32) {
+#pragma unroll
+                            for (int h = 0; h < 2; h++) {
+                                bf[j][4 * h + 0] = __uint_as_float(B[u][j][h].x);
+                                bf[j][4 * h + 1] = __uint_as_float(B[u][j][h].y);
+                                bf[j][4 * h + 2] = __uint_as_float(B[u][j][h].z);
+                                bf[j][4 * h + 3] = __uint_as_float(B[u][j][h].w);
+                            }
+                        } else {
+                            const uint32_t uu[4] = {B[u][j][0].x, B[u][j][0].y, B[u][j][0].z, B[u][j][0].w};
+#pragma unroll
+                            for (int h = 0; h < 4; h++) {
+                                bf[j][2 * h] = lg_h2f((uint16_t)(uu[h] & 0xffffu));
+                                bf[j][2 * h + 1] = lg_h2f((uint16_t)(uu[h] >> 16));
+                            }
+                        }
                     }
+#pragma unroll
+                    for (int st = 0; st < 8; st++)
+#pragma unroll
+                        for (int i = 0; i < TM; i++)
+#pragma unroll
+                            for (int j = 0; j < TN; j++)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][st], bf[j][st], acc[i][j], 0, 0, 0);
                 }
-            }
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                A[i][0] = An[i][0];
-                A[i][1] = An[i][1];
-#pragma unroll
-                for (int h = 0; h < ESZ / 2; h++) B[i][h] = Bn[i][h];
             }
         }
     }
 
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < TN; j++) {
         const int r = r0 + 16 * j + m;
         if (r >= a.R) continue;
         const float bias = a.bias[r];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int t = t0 + 16 * i + 4 * g + v;
@@ -455,37 +480,168 @@ __global__ __launch_bounds__(256) void k_bert_attn(const float* __restrict__ qkv
     }
 }
 
+/* The same on fp32 MFMA for sequences of up to PMAX positions: one block
+ * per (16 query tokens of one sequence, head), 4 waves.  K, then V, come
+ * into LDS in chunks of KC positions, each chunk with all its loads in
+ * flight at once (the sequence is short: a handful of round trips in all).
+ * Scores: wave w takes the 16-key tiles 16w, 16w+64, ... of a chunk; a
+ * tile is S[q][key] = sum_d Q[q][d] K[key][d], HD/4 v_mfma_f32_16x16x4f32
+ * (A = Q: lane (g, m) holds Q[m][d0+g]; B = K^T: K[key0+m][d0+g]; D:
+ * queries 4g..4g+3, key m), scaled and kept in LDS.  The reference's
+ * softmax runs on the rows as in k_bert_attn.  Then O[q][d] = sum_key
+ * P[q][key] V[key][d]: per 4 keys one MFMA per 16 dims (A = P:
+ * P[m][key0+g]; B = V: V[key0+g][16 dt + m]), wave w over the w-th quarter
+ * of each chunk; the four waves' partial O are summed in LDS.  LDS rows are
+ * padded to an odd number of floats so the 16 rows a lane group reads fall
+ * in distinct banks. */
+template <int HD>
+struct BAttnChunk {
+    static constexpr int KC = HD <= 64 ? 256 : 128;   /* positions per K/V chunk */
+};
+
+template <int HD, int PMAX>
+__global__ __launch_bounds__(256) void k_bert_attn_mfma(const float* __restrict__ qkv, int ne,
+                                                        const BAttnBlk* __restrict__ blks, float scale,
+                                                        float* __restrict__ ctx)
+{
+    constexpr int LD = HD + 1, PS = PMAX + 1, NDT = HD / 16, KC = BAttnChunk<HD>::KC, H4 = HD / 4;
+    __shared__ float s_q[16 * LD];
+    __shared__ float s_kv[KC * LD];
+    __shared__ float s_p[16 * PS];
+    const BAttnBlk bk = blks[blockIdx.x];
+    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, m = lane & 15;
+    const size_t ld = 3 * (size_t)ne;
+
+    /* rows [c0, c0 + KC) of the head's K (off = ne) or V (off = 2 ne) into s_kv */
+    auto load_chunk = [&](int c0, int off) {
+        for (int idx = tid; idx < KC * H4; idx += 256) {
+            const int r = idx / H4, c4 = idx % H4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c0 + r < bk.n) v = *(const float4*)(qkv + (size_t)(bk.s0 + c0 + r) * ld + off + h * HD + 4 * c4);
+            float* d = s_kv + r * LD + 4 * c4;
+            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        }
+    };
+
+    for (int idx = tid; idx < 16 * HD; idx += 256) {
+        const int r = idx / HD, d = idx % HD;
+        s_q[r * LD + d] = qkv[(size_t)(bk.q0 + min(r, bk.nq - 1)) * ld + h * HD + d];
+    }
+    for (int c0 = 0; c0 < bk.n; c0 += KC) {
+        __syncthreads();
+        load_chunk(c0, ne);
+        __syncthreads();
+        const int kn = min(KC, bk.n - c0);
+        for (int k16 = 16 * w; k16 < kn; k16 += 64) {
+            v4f acc = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d0 = 0; d0 < HD; d0 += 4)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s_q[m * LD + d0 + g], s_kv[(k16 + m) * LD + d0 + g], acc, 0, 0,
+                                                           0);
+            const int key = c0 + k16 + m;
+            if (key < bk.n) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) s_p[(4 * g + v) * PS + key] = acc[v] * scale;
+            }
+        }
+    }
+    __syncthreads();
+    {
+        /* softmax (fast/lil_math.cpp:964-976), 16 lanes per row */
+        const int qi = tid >> 4, kk = tid & 15;
+        float* prow = s_p + qi * PS;
+        float mx = -INFINITY;
+        for (int c = kk; c < bk.n; c += 16) mx = fmaxf(mx, prow[c]);
+#pragma unroll
+        for (int o = 8; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        float sum = 0.0f;
+        for (int c = kk; c < bk.n; c += 16) {
+            const float e = expf(prow[c] - mx);
+            prow[c] = e;
+            sum += e;
+        }
+#pragma unroll
+        for (int o = 8; o; o >>= 1) sum += __shfl_xor(sum, o);
+        for (int c = kk; c < bk.n; c += 16) prow[c] = prow[c] / sum;
+    }
+    v4f o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) o[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < bk.n; c0 += KC) {
+        __syncthreads();
+        load_chunk(c0, 2 * ne);
+        __syncthreads();
+        const int kq = min(KC / 4, max(0, bk.n - c0 - w * (KC / 4)));   /* keys of this wave's quarter */
+        for (int k4 = 0; k4 < kq; k4 += 4) {
+            const int kl = w * (KC / 4) + k4;                            /* chunk-local key of the step */
+            const float pa = c0 + kl + g < bk.n ? s_p[m * PS + c0 + kl + g] : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, s_kv[(kl + g) * LD + 16 * dt + m], o[dt], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    float* s_o = s_kv;                                   /* [4 waves][16 queries][HD] */
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) s_o[(w * 16 + 4 * g + v) * HD + 16 * dt + m] = o[dt][v];
+    __syncthreads();
+    for (int idx = tid; idx < 16 * HD; idx += 256) {
+        const int q = idx / HD, d = idx % HD;
+        if (q < bk.nq)
+            ctx[(size_t)(bk.q0 + q) * ne + h * HD + d] =
+                ((s_o[q * HD + d] + s_o[(16 + q) * HD + d]) + s_o[(32 + q) * HD + d]) + s_o[(48 + q) * HD + d];
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* mean over the sequence + l2norm (fast/vdb.cpp:237-244,              */
 /* fast/lil_math.cpp:939-946)                                           */
 /* ------------------------------------------------------------------ */
-__global__ __launch_bounds__(256) void k_bert_pool(const float* __restrict__ x, int ne, const int2* __restrict__ seqs,
-                                                   float* __restrict__ emb)
+/* sums over the sequence: block (sequence, 64 columns), 1024 threads =
+ * 64 columns x 16 position groups; group j adds positions j, j+16, ... and
+ * the 16 partial sums are added in order, then divided by the length
+ * (out[i] /= ntok) into mean[seq][n] */
+__global__ __launch_bounds__(1024) void k_bert_pool_mean(const float* __restrict__ x, int ne,
+                                                         const int2* __restrict__ seqs, float* __restrict__ mean)
 {
-    __shared__ float s_m[BERT_NE_MAX];
-    __shared__ float red[4];
+    __shared__ float s_part[16][64];
     const int2 sq = seqs[blockIdx.x];
-    const float* base = x + (size_t)sq.x * ne;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < ne; i += 256) {
-        /* the reference's order: token by token in fp32 */
-        float s = 0.0f;
-        int t = 0;
-        for (; t + 8 <= sq.y; t += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = base[(size_t)(t + u) * ne + i];
-#pragma unroll
-            for (int u = 0; u < 8; u++) s += v[u];
+    const int dg = threadIdx.x & 63, tg = threadIdx.x >> 6;
+    const int i = blockIdx.y * 64 + dg;
+    float s = 0.0f;
+    if (i < ne) {
+        const float* base = x + (size_t)sq.x * ne + i;
+        int t = tg;
+        for (; t + 48 < sq.y; t += 64) {
+            const float v0 = base[(size_t)t * ne], v1 = base[(size_t)(t + 16) * ne];
+            const float v2 = base[(size_t)(t + 32) * ne], v3 = base[(size_t)(t + 48) * ne];
+            s += v0; s += v1; s += v2; s += v3;
         }
-        for (; t < sq.y; t++) s += base[(size_t)t * ne + i];
-        s = s / (float)sq.y;
-        s_m[i] = s;
-        ss = __builtin_fmaf(s, s, ss);
+        for (; t < sq.y; t += 16) s += base[(size_t)t * ne];
     }
+    s_part[tg][dg] = s;
+    __syncthreads();
+    if (tg == 0 && i < ne) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) tot += s_part[j][dg];
+        mean[(size_t)blockIdx.x * ne + i] = tot / (float)sq.y;
+    }
+}
+
+/* l2norm (fast/lil_math.cpp:939-946) of each sequence's mean, in place */
+__global__ __launch_bounds__(256) void k_bert_l2norm(float* __restrict__ emb, int ne)
+{
+    __shared__ float red[4];
+    float* e = emb + (size_t)blockIdx.x * ne;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < ne; i += 256) ss = __builtin_fmaf(e[i], e[i], ss);
     ss = lg_block_sum(ss, red);
-    const float inv = ss > 0.0f ? 1.0f / sqrtf(ss) : 1.0f;
-    for (int i = threadIdx.x; i < ne; i += 256) emb[(size_t)blockIdx.x * ne + i] = ss > 0.0f ? s_m[i] * inv : s_m[i];
+    if (ss <= 0.0f) return;
+    const float inv = 1.0f / sqrtf(ss);
+    for (int i = threadIdx.x; i < ne; i += 256) e[i] = e[i] * inv;
 }
 
 /* ------------------------------------------------------------------ */
@@ -606,9 +762,12 @@ __global__ __launch_bounds__(256) void k_vdb_search(const uint16_t* __restrict__
         float acc = 0.0f;
         if (row < n) {
             const uint16_t* rp = vecs + (size_t)row * dim;
+            /* each row is read once: nontemporal loads keep it out of the caches */
+#pragma unroll 8
             for (int c = 8 * sl; c < dim; c += 64) {
-                const uint4 hv = *(const uint4*)(rp + c);
-                const uint32_t u[4] = {hv.x, hv.y, hv.z, hv.w};
+                typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+                const v4u hv = __builtin_nontemporal_load((const v4u*)(rp + c));
+                const uint32_t u[4] = {hv[0], hv[1], hv[2], hv[3]};
 #pragma unroll
                 for (int h = 0; h < 4; h++) {
                     acc = __builtin_fmaf(lg_h2f((uint16_t)(u[h] & 0xffffu)), s_e[c + 2 * h], acc);
@@ -737,6 +896,7 @@ static void bert_free_model(lg_bert* b)
 extern "C" int lg_bert_create(int device, lg_bert** out)
 {
     if (!out) { lg_set_error("lg_bert_create: null output"); return LG_ERR_ARG; }
+    lg_rand_guard keep_rand;
     *out = nullptr;
     int n = 0;
     LG_HIP_CHECK(hipGetDeviceCount(&n));
@@ -969,6 +1129,23 @@ extern "C" int lg_bert_load(lg_bert* b, const lg_bert_desc* desc, int max_tokens
 }
 
 /* ---- one pass ---- */
+template <int WT, int EP, int TM, int TN>
+static void gemm_launch(const BGemm& a, hipStream_t s)
+{
+    const dim3 grid((unsigned)(((a.T + 16 * TM - 1) / (16 * TM)) * ((a.R + 16 * TN - 1) / (16 * TN))));
+    hipLaunchKernelGGL((k_bert_gemm<WT, EP, TM, TN>), grid, dim3(64), 0, s, a);
+}
+
+template <int WT, int EP>
+static void gemm_tiles(const BGemm& a, hipStream_t s)
+{
+    /* the largest wave tile whose grid still has ~3 waves per SIMD */
+    auto waves = [&](int tm, int tn) { return (long)((a.T + 16 * tm - 1) / (16 * tm)) * ((a.R + 16 * tn - 1) / (16 * tn)); };
+    if (waves(2, 2) >= 3072) gemm_launch<WT, EP, 2, 2>(a, s);
+    else if (waves(1, 2) >= 3072) gemm_launch<WT, EP, 1, 2>(a, s);
+    else gemm_launch<WT, EP, 1, 1>(a, s);
+}
+
 template <int EP>
 static int gemm_ep(const BMat& W, const float* x, int ldx, const lg_bert* b, int T, const float* bias, const float* res,
                    int ldr, float* out, int ldo)
@@ -977,11 +1154,10 @@ static int gemm_ep(const BMat& W, const float* x, int ldx, const lg_bert* b, int
     a.w = W.w; a.wd = W.d; a.R = W.rows; a.K = W.cols;
     a.x = x; a.ldx = ldx; a.q = b->aq; a.qd = b->ad; a.ldd = b->ldd;
     a.T = T; a.bias = bias; a.res = res; a.ldr = ldr; a.out = out; a.ldo = ldo;
-    const dim3 grid((unsigned)(((T + 31) / 32) * ((W.rows + 31) / 32)));
     switch (W.type) {
-    case LG_F32: hipLaunchKernelGGL((k_bert_gemm<LG_F32, EP>), grid, dim3(64), 0, b->stream, a); break;
-    case LG_F16: hipLaunchKernelGGL((k_bert_gemm<LG_F16, EP>), grid, dim3(64), 0, b->stream, a); break;
-    default: hipLaunchKernelGGL((k_bert_gemm<BF_I8, EP>), grid, dim3(64), 0, b->stream, a); break;
+    case LG_F32: gemm_tiles<LG_F32, EP>(a, b->stream); break;
+    case LG_F16: gemm_tiles<LG_F16, EP>(a, b->stream); break;
+    default: gemm_tiles<BF_I8, EP>(a, b->stream); break;
     }
     return lg_check_launch("bert gemm");
 }
@@ -1070,8 +1246,15 @@ static int bert_layers(lg_bert* b, int T, int nblk, int qb, int pst, int nseq)
         }
         /* attention (fast/vdb.cpp:189-212) */
         const dim3 ag((unsigned)nblk, (unsigned)b->nh);
-#define ATT_CASE(HD) \
-    case HD: hipLaunchKernelGGL(k_bert_attn<HD>, ag, dim3(256), 0, b->stream, b->qkv, ne, blks, qb, pst, scale, b->ctx); break
+#define ATT_CASE(HD)                                                                                                  \
+    case HD:                                                                                                          \
+        if (pst <= 512)                                                                                               \
+            hipLaunchKernelGGL((k_bert_attn_mfma<HD, 512>), ag, dim3(256), 0, b->stream, b->qkv, ne, blks, scale, b->ctx); \
+        else if (pst <= 1024)                                                                                         \
+            hipLaunchKernelGGL((k_bert_attn_mfma<HD, 1024>), ag, dim3(256), 0, b->stream, b->qkv, ne, blks, scale, b->ctx); \
+        else                                                                                                          \
+            hipLaunchKernelGGL(k_bert_attn<HD>, ag, dim3(256), 0, b->stream, b->qkv, ne, blks, qb, pst, scale, b->ctx); \
+        break
         switch (b->hd) {
             ATT_CASE(16); ATT_CASE(32); ATT_CASE(48); ATT_CASE(64); ATT_CASE(80); ATT_CASE(96); ATT_CASE(112); ATT_CASE(128);
         default: lg_set_error("bert: head_dim %d", b->hd); return LG_ERR_ARG;
@@ -1092,8 +1275,11 @@ static int bert_layers(lg_bert* b, int T, int nblk, int qb, int pst, int nseq)
         if ((rc = launch_ln(b, b->y, L.ln2_w, L.ln2_b, b->x, qn, T))) return rc;
         if (qn && (rc = trace_copy(b, l + 1, 0, ne, T))) return rc;
     }
-    hipLaunchKernelGGL(k_bert_pool, dim3(nseq), dim3(256), 0, b->stream, b->x, ne, seqs, b->emb_dev);
-    return lg_check_launch("bert pool");
+    hipLaunchKernelGGL(k_bert_pool_mean, dim3(nseq, (ne + 63) / 64), dim3(1024), 0, b->stream, b->x, ne, seqs,
+                       b->emb_dev);
+    if ((rc = lg_check_launch("bert pool"))) return rc;
+    hipLaunchKernelGGL(k_bert_l2norm, dim3(nseq), dim3(256), 0, b->stream, b->emb_dev, ne);
+    return lg_check_launch("bert l2norm");
 }
 
 /* the attention query block for the longest sequence of a pass */

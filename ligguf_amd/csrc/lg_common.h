@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../../include/ligguf_hip.h"
@@ -245,6 +246,20 @@ __device__ __forceinline__ float lg_block_sum(float v, float* red)
     for (int i = 0; i < nw; i++) s += red[i];
     return s;
 }
+
+/* The HIP runtime's device initialisation draws numbers from the C library's
+ * rand(), which shifts a caller's seeded sequence -- the reference samples
+ * top-p with rand() after srand(seed) (fast/ligguf_fast_qk.cpp:204,487-489),
+ * so its output would change with the library linked in.  Calls that may
+ * initialise the runtime run with a private generator state swapped in
+ * (initstate/setstate leave the caller's state untouched meanwhile); another
+ * thread calling rand() during lg_create would draw from the private state. */
+struct lg_rand_guard {
+    char buf[256];
+    char* caller;
+    lg_rand_guard() { caller = initstate(1u, buf, sizeof(buf)); }
+    ~lg_rand_guard() { setstate(caller); }
+};
 
 /* host helper: turn a failed kernel launch into LG_ERR_HIP */
 int lg_check_launch(const char* what);

@@ -209,20 +209,6 @@ static void free_model(lg_ctx* ctx)
     }
 }
 
-/* The HIP runtime's device initialisation draws numbers from the C library's
- * rand(), which shifts a caller's seeded sequence -- the reference samples
- * top-p with rand() after srand(seed) (fast/ligguf_fast_qk.cpp:204,487-489),
- * so its output would change with the library linked in.  Calls that may
- * initialise the runtime run with a private generator state swapped in
- * (initstate/setstate leave the caller's state untouched meanwhile); another
- * thread calling rand() during lg_create would draw from the private state. */
-struct lg_rand_guard {
-    char buf[256];
-    char* caller;
-    lg_rand_guard() { caller = initstate(1u, buf, sizeof(buf)); }
-    ~lg_rand_guard() { setstate(caller); }
-};
-
 extern "C" int lg_create(int device, lg_ctx** out)
 {
     if (!out) { lg_set_error("lg_create: null output"); return LG_ERR_ARG; }

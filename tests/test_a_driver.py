@@ -99,3 +99,45 @@ def test_driver_state_files_cross(drv_model):
         outs[name] = generated(run(binary, "-m", path, "-L", state, "-p", "xyz", "-G", "-n", "12"), "xyz")
     print("\n" + "\n".join(f"  {k}: {v[:100]}" for k, v in outs.items()))
     assert len(set(outs.values())) == 1, outs
+
+
+CHAT_LOG = ("@@1700000000\n<<<<<<<\nthe cat sat on the mat\n>>>>>>>\nnice cat\n"
+            "@@1700000100\n<<<<<<<\nwhat is the weather in paris\n>>>>>>>\nsunny and warm\n"
+            "@@1700000200\n<<<<<<<\nI like pizza for dinner\nand coffee\n>>>>>>>\nme too\n"
+            "@@1700000300\n<<<<<<<\nthe cat sat on the mat\n>>>>>>>\nagain?\n")
+
+
+def test_driver_chat_memory_equals_cpu_build(tmp_path):
+    """Chat mode with the BERT vector memory (-C -B -l): vdb_create embeds the
+    log's user turns, the typed line is embedded and searched (vdb_query),
+    the records found are fed to the model (vdb_to_prompt).  The LG_HIP build
+    runs bert_embed and the search on the GPU (oracle/vdb_lg_hip.patch); the
+    records it retrieves and the prompt text it builds from them must be the
+    CPU build's, and the similarities it reports equal to the 4 decimals
+    printed (within one unit of the last)."""
+    if not (os.path.exists(BIN_CPU) and os.path.exists(BIN_HIP)):
+        pytest.skip("reference driver builds (make -C oracle driver) not present")
+    from ligguf_amd.bert import BERT_TINY, HostBert
+    from ligguf_amd.model import TINY, HostModel
+    llm, bert = str(tmp_path / "llm.gguf"), str(tmp_path / "bert.gguf")
+    HostModel.synthetic(TINY.with_(n_context=2048)).write_gguf(llm, byte_tokens=True)
+    HostBert.synthetic(BERT_TINY).write_gguf(bert)
+    res = {}
+    for name, binary in (("cpu", BIN_CPU), ("hip", BIN_HIP)):
+        log = tmp_path / f"chat_{name}.txt"
+        log.write_text(CHAT_LOG)
+        r = subprocess.run([binary, "-m", llm, "-C", "-B", bert, "-l", str(log), "-p", "abc", "-G", "-n", "4",
+                            "-A", "AI", "-U", "User"], input="the cat sat on the mat\n", capture_output=True,
+                           text=True, timeout=120)
+        assert r.returncode == 0, f"{name}: rc {r.returncode}\n{r.stdout[-2000:]}\n{r.stderr[-2000:]}"
+        hits = re.findall(r"VDB hit (\d+) idx=(\d+) sim=([0-9.]+) ts=(\d+)", r.stdout)
+        prompt = re.search(r"VDB prompt = '(.*?\*\*\* End of records)'", r.stdout, re.S)
+        created = re.findall(r"VDB created: (\d+) records", r.stdout)
+        res[name] = (hits, prompt.group(1) if prompt else None, created)
+        print(f"\n{name}: created {created}, hits {hits}")
+    (hc, pc, cc), (hh, ph, ch) = res["cpu"], res["hip"]
+    assert cc == ch == ["4"]
+    assert len(hc) == len(hh) == 2
+    assert [(a[0], a[1], a[3]) for a in hc] == [(a[0], a[1], a[3]) for a in hh]
+    assert all(abs(float(a[2]) - float(b[2])) <= 1.5e-4 for a, b in zip(hc, hh))
+    assert pc is not None and pc == ph

@@ -197,6 +197,19 @@ def test_bert_minilm_shape(dev, oracle):
         check_embed(dev, oracle, hb, rng.integers(5, hb.cfg.vocab, n), "MiniLM shape")
 
 
+def test_bert_long_sequences(dev, oracle):
+    """the attention variants by sequence length: up to 512 and up to 1024
+    positions on MFMA with the score rows in LDS, longer ones on the
+    vector-ALU kernel with fewer queries per block; a batch mixing them"""
+    hb = load(dev, HostBert.synthetic(BERT_TINY.with_(n_context=2048, seed=21)))
+    rng = np.random.default_rng(12)
+    seqs = [rng.integers(5, hb.cfg.vocab, n) for n in (300, 700, 1500, 2046)]
+    single = [check_embed(dev, oracle, hb, s, "long") for s in seqs]
+    batch = dev.embed_batch(seqs)
+    for i in range(len(seqs)):
+        assert rel(batch[i], single[i]) < EXACT
+
+
 def test_bert_live_reference(dev, reference):
     """text in, vector out: the reference's bert_tokenize + bert_embed on its
     own GGUF load against the GPU fed the same ids"""
