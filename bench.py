@@ -197,6 +197,97 @@ def isolated_kernels(torch, np):
     return out
 
 
+FP32_MFMA_PEAK = 157.3e12   # MI355X dense fp32 matrix, flop/s
+
+
+def bert_report(torch, np, cpu_seconds: float = 0.0):
+    """BERT sentence embedding and vector-memory search (lg_bert_*, the
+    bert_embed / vdb_query path of fast/vdb.cpp:123-245,337-377) on the
+    all-MiniLM-L6-v2 shape (6 blocks, 384 wide, 12 heads of 32, FFN 1536, 512
+    positions, 30522 pieces), synthetic F16 matrices:
+      - one 510-piece text (512 positions with CLS/SEP), embeddings/s of
+        synchronous lg_bert_embed calls (host tables, upload of the ids and
+        download of the vector included);
+      - 64 texts of 126 pieces in lg_bert_embed_batch calls (a chat log's
+        turns, as vdb_create embeds them);
+      - a 2^20-row fp16 memory of 384-wide vectors: lg_bert_vdb_query (top 3
+        at threshold 0, so every row is a candidate) per synchronous call.
+    TFLOP/s count the layer matrices and attention products (BertConfig.flops)
+    against the 157.3 TFLOP/s dense fp32 MFMA peak the F16 x fp32 products run
+    on; the search counts the rows' bytes against 8 TB/s.  cpu_baseline: the
+    reference's bert_embed (oracle/_ref, OpenMP over matrix rows) on a
+    510-word text of the same encoder, a bounded number of calls."""
+    from ligguf_amd.bert import MINILM_L6, Bert, HostBert
+    cfg = MINILM_L6
+    hb = HostBert.synthetic(cfg)
+    b = Bert(0)
+    b.load(hb)
+    rng = np.random.default_rng(0)
+    out = {"workload": "minilm-l6-shape F16 (6x384, 12 heads of 32, FFN 1536, vocab 30522)"}
+    toks = rng.integers(5, cfg.vocab, 510)
+    for _ in range(3):
+        b.embed(toks)
+    reps = 30
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b.embed(toks)
+    dt = (time.perf_counter() - t0) / reps
+    fl = cfg.flops(512)
+    out["single_512"] = {"ms": round(dt * 1e3, 3), "emb_per_s": round(1 / dt, 1), "TFLOP/s": round(fl / dt / 1e12, 2),
+                         "frac_fp32_mfma": round(fl / dt / FP32_MFMA_PEAK, 4)}
+    seqs = [rng.integers(5, cfg.vocab, 126) for _ in range(64)]
+    b.embed_batch(seqs)
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b.embed_batch(seqs)
+    dt = (time.perf_counter() - t0) / reps
+    fl = 64 * cfg.flops(128)
+    out["batch_64x128"] = {"ms": round(dt * 1e3, 3), "emb_per_s": round(64 / dt, 1), "tok_per_s": round(64 * 128 / dt),
+                           "TFLOP/s": round(fl / dt / 1e12, 2), "frac_fp32_mfma": round(fl / dt / FP32_MFMA_PEAK, 4)}
+    n, dim = 1 << 20, cfg.n_embed
+    vecs = (rng.standard_normal((n, dim), dtype=np.float32) / np.float32(dim ** 0.5)).astype(np.float16)
+    b.vdb_set(vecs.view(np.uint16))
+    del vecs
+    emb = rng.standard_normal(dim).astype(np.float32)
+    emb /= np.linalg.norm(emb)
+    for _ in range(3):
+        b.vdb_query(emb, 0.0, 3)
+    reps = 30
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b.vdb_query(emb, 0.0, 3)
+    dt = (time.perf_counter() - t0) / reps
+    out["vdb_search"] = {"rows": n, "dim": dim, "us": round(dt * 1e6, 1), "GB/s": round(n * dim * 2 / dt / 1e9, 1),
+                         "frac": round(n * dim * 2 / dt / HBM_PEAK, 4)}
+    b.close()
+    if cpu_seconds > 0:
+        from oracle import load_reference, reference_available
+        if reference_available():
+            import tempfile
+            R = load_reference()
+            words = [w for w in hb.tokens if w.isalpha() and w.islower() and len(w) > 1]
+            text = " ".join(rng.choice(words, 510)).encode()
+            assert len(hb.tokenize(text)) == 510
+            with tempfile.TemporaryDirectory() as d:
+                fn = os.path.join(d, "bert.gguf")
+                hb.write_gguf(fn)
+                with _stdout_to_stderr():
+                    R.bert_open(fn)
+                    R.bert_embed(text)
+                    calls, t0 = 0, time.perf_counter()
+                    while time.perf_counter() - t0 < cpu_seconds and calls < 200:
+                        R.bert_embed(text)
+                        calls += 1
+                    dt = (time.perf_counter() - t0) / calls
+            info = cpu_info()
+            out["cpu_baseline"] = {"value": round(1 / dt, 2), "unit": "embeddings/s (512 positions)",
+                                   "ms": round(dt * 1e3, 2), "cores": info.get("omp_threads"), "kind": "reference",
+                                   "sample": f"{calls} bert_embed calls of a 510-word text"}
+    log(f"bert: {out}")
+    return out
+
+
 def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8, cpu_seconds: float = 0.0):
     """The 1-bit workload: Qwen3-8B shape with Q1_G layers (group 128, sign
     bits, fp16 group scales |N(0,0.02)|) and Q8_0 embedding/output, an
@@ -436,6 +527,9 @@ def main() -> int:
     ap.add_argument("--q1g-only", action="store_true",
                     help="run only the Q1_G long-context workload and print its line (profiling)")
     ap.add_argument("--q1g-ctx", type=int, default=8192, help="prompt length of the Q1_G workload")
+    ap.add_argument("--no-bert", action="store_true", help="skip the BERT embedding / vector-memory lines")
+    ap.add_argument("--bert-only", action="store_true",
+                    help="run only the BERT embedding / vector-memory workloads and print their line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the decode path here is single-GPU (asked for --gpus {args.gpus}).",
@@ -460,6 +554,10 @@ def main() -> int:
 
     if args.q1g_only:
         print(json.dumps({"q1g": q1g_context(torch, np, ctx=args.q1g_ctx)}), flush=True)
+        return 0
+
+    if args.bert_only:
+        print(json.dumps({"bert": bert_report(torch, np, 0.0 if args.no_cpu else args.cpu_seconds)}), flush=True)
         return 0
 
     if args.prefill_only:
@@ -530,6 +628,7 @@ def main() -> int:
     log(f"plain copy: {copy}")
     q1g = None if args.no_q1g else q1g_context(torch, np, ctx=args.q1g_ctx,
                                                cpu_seconds=0.0 if args.no_cpu else args.cpu_seconds)
+    bert = None if args.no_bert else bert_report(torch, np, 0.0 if args.no_cpu else min(args.cpu_seconds, 10.0))
 
     cpu = None
     if not args.no_cpu:
@@ -569,6 +668,7 @@ def main() -> int:
         "isolated": isolated,
         "sampler": sampler,
         "q1g_8k": q1g,
+        "bert": bert,
     }
     print(json.dumps(out), flush=True)
     return 0

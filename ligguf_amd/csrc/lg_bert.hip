@@ -494,9 +494,10 @@ __global__ __launch_bounds__(256) void k_bert_attn(const float* __restrict__ qkv
  * of each chunk; the four waves' partial O are summed in LDS.  LDS rows are
  * padded to an odd number of floats so the 16 rows a lane group reads fall
  * in distinct banks. */
-template <int HD>
+template <int HD, int PMAX>
 struct BAttnChunk {
-    static constexpr int KC = HD <= 64 ? 256 : 128;   /* positions per K/V chunk */
+    static constexpr int KC0 = HD <= 64 ? 256 : 128;
+    static constexpr int KC = KC0 < PMAX ? KC0 : PMAX;   /* positions per K/V chunk */
 };
 
 template <int HD, int PMAX>
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(256) void k_bert_attn_mfma(const float* __restrict_
                                                         const BAttnBlk* __restrict__ blks, float scale,
                                                         float* __restrict__ ctx)
 {
-    constexpr int LD = HD + 1, PS = PMAX + 1, NDT = HD / 16, KC = BAttnChunk<HD>::KC, H4 = HD / 4;
+    constexpr int LD = HD + 1, PS = PMAX + 1, NDT = HD / 16, KC = BAttnChunk<HD, PMAX>::KC, H4 = HD / 4;
     __shared__ float s_q[16 * LD];
     __shared__ float s_kv[KC * LD];
     __shared__ float s_p[16 * PS];
@@ -1248,7 +1249,11 @@ static int bert_layers(lg_bert* b, int T, int nblk, int qb, int pst, int nseq)
         const dim3 ag((unsigned)nblk, (unsigned)b->nh);
 #define ATT_CASE(HD)                                                                                                  \
     case HD:                                                                                                          \
-        if (pst <= 512)                                                                                               \
+        if (pst <= 128)                                                                                               \
+            hipLaunchKernelGGL((k_bert_attn_mfma<HD, 128>), ag, dim3(256), 0, b->stream, b->qkv, ne, blks, scale, b->ctx); \
+        else if (pst <= 256)                                                                                          \
+            hipLaunchKernelGGL((k_bert_attn_mfma<HD, 256>), ag, dim3(256), 0, b->stream, b->qkv, ne, blks, scale, b->ctx); \
+        else if (pst <= 512)                                                                                          \
             hipLaunchKernelGGL((k_bert_attn_mfma<HD, 512>), ag, dim3(256), 0, b->stream, b->qkv, ne, blks, scale, b->ctx); \
         else if (pst <= 1024)                                                                                         \
             hipLaunchKernelGGL((k_bert_attn_mfma<HD, 1024>), ag, dim3(256), 0, b->stream, b->qkv, ne, blks, scale, b->ctx); \
