@@ -389,7 +389,12 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     if (m->head_dim > 0 && m->head_dim <= 128 && nrep >= 1 && nrep <= PK_MAX_NREP && m->n_kv_heads > 0)
         pk_attn_split(m->n_context, m->head_dim, nrep, ncu / m->n_kv_heads, &att_chunk, &att_nch);
     att_nch = std::max(att_nch, PK_ATT_MERGE);
-    bool ok = m->n_embed == 4096 && m->n_ff == 3 * m->n_embed && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
+    /* widths: any the activation builds hold (LDS staging of n_embed and of
+     * the quantized n_ff vector), in whole 256-value Q8_K blocks for K-quant
+     * and Q1_G layers; which widths have kernels is up to the variants */
+    const bool q8act = lt == LG_Q8_0 || lt == LG_Q1_0;
+    bool ok = m->n_embed <= PK_MAX_EMBED && m->n_ff <= PK_MAX_FF && m->n_embed % (q8act ? 32 : 256) == 0 &&
+              m->n_ff % (q8act ? 32 : 256) == 0 && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
               m->n_kv_heads <= 32 && m->n_heads <= 32 && ctx->output.cols == m->n_embed && ctx->arena.ok;
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
@@ -397,10 +402,19 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
              pk_shape_ok(D.att_out, lt, m->n_embed, m->n_embed) && pk_shape_ok(D.ug, lt, 2 * m->n_ff, m->n_embed) &&
              pk_shape_ok(D.down, lt, m->n_embed, m->n_ff);
     }
-    const void* kern = ok ? lg_persist_kernel(lt, ctx->output.type, m->head_dim, nrep) : nullptr;
-    if (!kern) return LG_OK;   /* the multi-kernel path serves this model */
+    /* the fused kernels come in width classes; the persistent kernel is
+     * instantiated for n_embed 4096 / n_ff 12288 only */
+    const void* fused = ok ? lg_fused_variant(lt, ctx->output.type, m->head_dim, nrep, m->n_embed, m->n_ff) : nullptr;
+    const void* kern = ok && m->n_embed == 4096 && m->n_ff == 3 * m->n_embed
+                           ? lg_persist_kernel(lt, ctx->output.type, m->head_dim, nrep)
+                           : nullptr;
+    if (!kern && !fused) return LG_OK;   /* the multi-kernel path serves this model */
     int rc;
-    if ((rc = lg_persist_grid(kern, &ctx->pk_nwg))) return rc;
+    if (kern) {
+        if ((rc = lg_persist_grid(kern, &ctx->pk_nwg))) return rc;
+    } else {
+        ctx->pk_nwg = ncu;   /* one workgroup per CU, as the persistent grid */
+    }
     std::vector<PkLayer> hl(m->n_layers);
     for (int l = 0; l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
@@ -478,7 +492,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     LG_HIP_CHECK(hipHostMalloc((void**)&ctx->feed_host, (size_t)m->n_context * sizeof(int), 0));
     if (!ctx->step_ring) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->step_ring, LG_STEP_RING * sizeof(PkStep), 0));
     ctx->ring_next = ctx->ring_pending = 0;
-    ctx->fused_fn = lg_fused_variant(lt, ctx->output.type, m->head_dim, nrep);
+    ctx->fused_fn = fused;
     if (!ctx->pk_status_host) LG_HIP_CHECK(hipHostMalloc((void**)&ctx->pk_status_host, 2 * sizeof(int), 0));
     ctx->pk_base = 0;
     ctx->pk_kernel = kern;
@@ -497,7 +511,7 @@ static void pk_reset(lg_ctx* c)
 
 /* AUTO takes the multi-kernel path until the persistent kernel measures
  * faster on the headline workload; PERSISTENT selects it explicitly */
-static bool use_pk(const lg_ctx* c) { return c->pk_ok && c->path == LG_PATH_PERSISTENT; }
+static bool use_pk(const lg_ctx* c) { return c->pk_ok && c->pk_kernel && c->path == LG_PATH_PERSISTENT; }
 static bool use_fused(const lg_ctx* c)
 {
     return c->pk_ok && c->fused_fn && (c->path == LG_PATH_FUSED || c->path == LG_PATH_AUTO);
@@ -629,7 +643,7 @@ extern "C" int lg_set_decode_path(lg_ctx* ctx, int path)
         lg_set_error("lg_set_decode_path: the loaded model is not supported by the fused kernels");
         return ctx_fail(ctx, LG_ERR_STATE);
     }
-    if (path == LG_PATH_PERSISTENT && !ctx->pk_ok) {
+    if (path == LG_PATH_PERSISTENT && !(ctx->pk_ok && ctx->pk_kernel)) {
         lg_set_error("lg_set_decode_path: the loaded model is not supported by the persistent kernel");
         return ctx_fail(ctx, LG_ERR_STATE);
     }

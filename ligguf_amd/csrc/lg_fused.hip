@@ -42,19 +42,29 @@ __device__ __forceinline__ uint8_t* f_atr(uint8_t* atr, const PkParams& P, int k
     return atr ? atr + (size_t)k * P.act_stride : nullptr;
 }
 
+/* Widths.  S carries the slots per lane of a row of n_embed values (NE for
+ * the layer type, NO for the output type) and of n_ff values (NF), and the
+ * 256-value activation chunks per wave of an n_embed (CE) and an n_ff (CF)
+ * wide build; the widths themselves are runtime values (phase_mv masks the
+ * slots and chunks past them). */
+template <int NE_, int NO_, int CE_, int NF_, int CF_>
+struct FShape {
+    static constexpr int NE = NE_, NO = NO_, CE = CE_, NF = NF_, CF = CF_;
+};
+
 /* EMB: layer 0, whose input is the embedding row of the step's token */
-template <int LT, bool EMB>
+template <int LT, class S, bool EMB>
 __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                       int l, uint8_t* atr)
 {
-    constexpr int NE = NsE<LT>::value;
+    constexpr int NE = S::NE;
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
     float* xin = P.xs + (size_t)l * ne;
     const int pos = Sd->pos;
     const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
-    phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, 2, LG_QKV_R>(
+    phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, S::CE, LG_QKV_R>(
         P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, P.qkv + (size_t)l * qs, xin, 0, 0,
-        f_tr(Sd, l, 0), f_atr(atr, P, 4 * l));
+        f_tr(Sd, l, 0), f_atr(atr, P, 4 * l), ne);
 }
 
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
@@ -84,47 +94,47 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const P
     }
 }
 
-template <int LT, int HD, int NREP>
+template <int LT, class S, int HD, int NREP>
 __global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
                                                      uint8_t* atr)
 {
-    constexpr int NE = NsE<LT>::value;
+    constexpr int NE = S::NE;
     const int ne = P.n_embed;
-    phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
+    phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, S::CE, LG_AO_R>(
         P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, P.xs + (size_t)l * ne, P.xm + (size_t)l * ne, nullptr, 0, 0,
-        f_tr(Sd, l, 2), f_atr(atr, P, 4 * l + 1), att_partials<HD, NREP>(P, l, Sd->pos));
+        f_tr(Sd, l, 2), f_atr(atr, P, 4 * l + 1), ne, att_partials<HD, NREP>(P, l, Sd->pos));
 }
 
-template <int LT>
+template <int LT, class S>
 __global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
                                                      uint8_t* atr)
 {
-    constexpr int NE = NsE<LT>::value;
+    constexpr int NE = S::NE;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, 2, LG_UG_R>(
+    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, S::CE, LG_UG_R>(
         P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, P.xm + (size_t)l * ne, nullptr, P.hb + (size_t)l * nff, nullptr, 0,
-        0, f_tr(Sd, l, 3), f_atr(atr, P, 4 * l + 2));
+        0, f_tr(Sd, l, 3), f_atr(atr, P, 4 * l + 2), ne);
 }
 
-template <int LT>
+template <int LT, class S>
 __global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
                                                        uint8_t* atr)
 {
-    constexpr int NF = 3 * NsE<LT>::value;
+    constexpr int NF = S::NF;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, 6, LG_DN_R>(
+    phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, S::CF, LG_DN_R>(
         P, 0, L.down, L.down_rsz, ne, 0, nullptr, P.hb + (size_t)l * nff, P.xm + (size_t)l * ne,
-        P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(atr, P, 4 * l + 3));
+        P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(atr, P, 4 * l + 3), nff);
 }
 
-template <int OT>
+template <int OT, class S>
 __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* __restrict__ Sd, uint8_t* atr)
 {
-    constexpr int NO = NsE<OT>::value;
+    constexpr int NO = S::NO;
     const int pos = Sd->pos;
-        phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
+    phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, S::CE, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
-        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0), f_atr(atr, P, 4 * P.n_layers));
+        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0), f_atr(atr, P, 4 * P.n_layers), P.n_embed);
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
     if (s_int[0] && threadIdx.x == 0) {
         Sd->tok = cld(P.tok_out);
@@ -138,67 +148,101 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 /* ------------------------------------------------------------------ */
 typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t, uint8_t*);
 
-template <int LT, int OT, int HD, int NREP>
+template <int LT, int OT, int HD, int NREP, class SH>
 static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n_layers, int nwg, bool long_ctx,
                           hipStream_t st, uint8_t* atr)
 {
     const dim3 g(nwg), b(PK_THREADS);
     for (int l = 0; l < n_layers; l++) {
-        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l, atr);
-        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l, atr);
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, atr);
+        else hipLaunchKernelGGL((k_f_qkv<LT, SH, false>), g, b, 0, st, P, Lh[l], S, l, atr);
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
-        hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, atr);
-        hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l, atr);
-        hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l, atr);
+        hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, atr);
+        hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
+        hipLaunchKernelGGL((k_f_down<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
     }
-    hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S, atr);
+    hipLaunchKernelGGL((k_f_out<OT, SH>), g, b, 0, st, P, S, atr);
 }
 
 typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, bool, hipStream_t);
 
 /* one kernel of the step: phase 0..4 of layer l, 5 = output head */
-template <int LT, int OT, int HD, int NREP>
+template <int LT, int OT, int HD, int NREP, class SH>
 static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int phase, int l, int nwg, bool long_ctx,
                         hipStream_t st)
 {
     const dim3 g(nwg), b(PK_THREADS);
     switch (phase) {
     case 0:
-        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, true>), g, b, 0, st, P, Lh[l], S, l, nullptr);
-        else hipLaunchKernelGGL((k_f_qkv<LT, false>), g, b, 0, st, P, Lh[l], S, l, nullptr);
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, nullptr);
+        else hipLaunchKernelGGL((k_f_qkv<LT, SH, false>), g, b, 0, st, P, Lh[l], S, l, nullptr);
         break;
     case 1:
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         break;
-    case 2: hipLaunchKernelGGL((k_f_ao<LT, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
-    case 3: hipLaunchKernelGGL((k_f_ug<LT>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
-    case 4: hipLaunchKernelGGL((k_f_down<LT>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
-    default: hipLaunchKernelGGL((k_f_out<OT>), g, b, 0, st, P, S, nullptr); break;
+    case 2: hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    case 3: hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    case 4: hipLaunchKernelGGL((k_f_down<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    default: hipLaunchKernelGGL((k_f_out<OT, SH>), g, b, 0, st, P, S, nullptr); break;
     }
 }
 
+/* slots per lane of a row of n values of type t, and 256-value chunks per
+ * wave of an n-wide activation build */
+static constexpr int f_vps(int t) { return (t == LG_Q8_0 || t == LG_Q1_0) ? 32 : 64; }
+static constexpr int f_ns(int t, int n) { return (n / f_vps(t) + 63) / 64; }
+static constexpr int f_cpw(int n) { return (n + 256 * PK_WAVES - 1) / (256 * PK_WAVES); }
+
 struct FusedVariant {
     int lt, ot, hd, nrep;
+    int ne, no, ce, nf, cf;       /* the FShape */
     fused_enqueue_t fn;
     fused_phase_t phase;
 };
 
-#define FV(LT, OT, HD, NR) {LT, OT, HD, NR, fused_enqueue<LT, OT, HD, NR>, fused_phase<LT, OT, HD, NR>}
+/* one variant per (layer type, output type, head_dim, query heads per KV
+ * head) and width class: n_embed 4096 / n_ff 12288 (the Qwen3-8B shape),
+ * n_embed 4096 / n_ff 14336 (Llama-3-8B, Mistral-7B), n_embed 2560 / n_ff
+ * 9728 (Qwen3-4B), n_embed 2048 / n_ff 5632 (TinyLlama-1.1B, head_dim 64),
+ * and any width up to 2048 / 2048 (tiny models) */
+#define FVS(LT, OT, HD, NR, E, F)                                                                              \
+    {LT, OT, HD, NR, f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F),                                \
+     fused_enqueue<LT, OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,         \
+     fused_phase<LT, OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>}
+#define FV(LT, OT, HD, NR) FVS(LT, OT, HD, NR, 4096, 12288)
 static const FusedVariant f_variants[] = {
     FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
     FV(LG_Q5_K, LG_Q6_K, 128, 4), FV(LG_Q6_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q8_0, 128, 4),
     FV(LG_Q1_G, LG_Q8_0, 128, 4), FV(LG_Q1_G, LG_Q6_K, 128, 4),
     FV(LG_Q4_K, LG_Q6_K, 128, 8), FV(LG_Q4_K, LG_Q6_K, 128, 1), FV(LG_Q5_K, LG_Q4_K, 128, 1),
     FV(LG_Q8_0, LG_Q8_0, 128, 1),
+    FVS(LG_Q4_K, LG_Q6_K, 128, 4, 4096, 14336), FVS(LG_Q8_0, LG_Q8_0, 128, 4, 4096, 14336),
+    FVS(LG_Q4_K, LG_Q6_K, 128, 4, 2560, 9728),
+    FVS(LG_Q4_K, LG_Q6_K, 64, 8, 2048, 5632), FVS(LG_Q8_0, LG_Q8_0, 64, 8, 2048, 5632),
+    FVS(LG_Q8_0, LG_Q8_0, 48, 1, 2048, 2048), FVS(LG_Q8_0, LG_Q8_0, 64, 1, 2048, 2048),
+    FVS(LG_Q4_K, LG_Q6_K, 64, 1, 2048, 2048),
 };
 #undef FV
+#undef FVS
 
-const void* lg_fused_variant(int lt, int ot, int hd, int nrep)
+const void* lg_fused_variant(int lt, int ot, int hd, int nrep, int ne, int nff)
 {
-    for (const FusedVariant& v : f_variants)
-        if (v.lt == lt && v.ot == ot && v.hd == hd && v.nrep == nrep) return (const void*)&v;
+    /* a variant serves the model when its slots and chunks hold the model's
+     * widths (masked past them) and it wastes no more than its class does */
+    for (const FusedVariant& v : f_variants) {
+        if (v.lt != lt || v.ot != ot || v.hd != hd || v.nrep != nrep) continue;
+        if (f_ns(lt, ne) == v.ne && f_ns(ot, ne) == v.no && f_cpw(ne) == v.ce && f_ns(lt, nff) == v.nf &&
+            f_cpw(nff) == v.cf)
+            return (const void*)&v;
+    }
+    for (const FusedVariant& v : f_variants) {
+        if (v.lt != lt || v.ot != ot || v.hd != hd || v.nrep != nrep) continue;
+        if (f_ns(lt, ne) <= v.ne && f_ns(ot, ne) <= v.no && f_cpw(ne) <= v.ce && f_ns(lt, nff) <= v.nf &&
+            f_cpw(nff) <= v.cf && v.ce <= 1 && v.cf <= 1)
+            return (const void*)&v;
+    }
     return nullptr;
 }
 

@@ -82,8 +82,16 @@ struct PkStep {
                                 kernels take the same pointer as a kernel argument) */
 };
 
+/* the head width the attention lanes are laid out for: a position takes
+ * pk_hdp / 8 lanes of 8 values (a power of two; head_dim 48 runs as 64 with
+ * its last 16 values zero) */
+__host__ __device__ constexpr int pk_hdp(int head_dim)
+{
+    return head_dim <= 64 ? 64 : 128;
+}
+
 /* attention work split.  A workgroup step covers ppb = PK_THREADS * 8 /
- * head_dim positions (one 16-byte slice of a cache row per lane) and a unit
+ * pk_hdp(head_dim) positions (one 16-byte slice of a cache row per lane) and a unit
  * (kv head, chunk) holds pk_att_steps(nrep) steps of K and V in registers at
  * a time -- one register batch.  Contexts up to PK_ATT_MERGE batches are cut
  * into at most PK_ATT_MERGE chunks per head, whose partials the att_out build
@@ -111,7 +119,7 @@ __host__ __device__ inline bool pk_att_one_head(int n_kv, int nrep, int nch, int
 __host__ __device__ inline void pk_attn_split(int ctx_len, int head_dim, int nrep, int max_nch, int* chunk_out,
                                               int* nch_out)
 {
-    const int ppb = PK_THREADS * 8 / head_dim;
+    const int ppb = PK_THREADS * 8 / pk_hdp(head_dim);
     int chunk = (ctx_len + PK_ATT_MERGE - 1) / PK_ATT_MERGE;
     chunk = (chunk + ppb - 1) / ppb * ppb;
     if (chunk > pk_att_steps(nrep) * ppb) {
@@ -147,8 +155,9 @@ int lg_persist_launch(const void* kernel, const PkParams& P, const PkStep* S, in
  * units past the context skip their work. */
 __host__ __device__ constexpr int pk_att_fch(int head_dim, int nrep)
 {
-    return pk_att_steps(nrep) * (PK_THREADS * 8 / head_dim) < 128 ? pk_att_steps(nrep) * (PK_THREADS * 8 / head_dim)
-                                                                   : 128;
+    return pk_att_steps(nrep) * (PK_THREADS * 8 / pk_hdp(head_dim)) < 128
+               ? pk_att_steps(nrep) * (PK_THREADS * 8 / pk_hdp(head_dim))
+               : 128;
 }
 
 /* attention at position pos takes the long-context units (whole query-head
@@ -164,7 +173,7 @@ __host__ __device__ inline bool pk_att_long(int pos, int head_dim, int nrep, int
  * greedy token to P->tok_out and advances S_dev to {token, pos + 1}.  NULL
  * when the variant is not instantiated.  long_ctx = pk_att_long(pos, ...) of
  * the step's position selects the attention kernel. */
-const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep);
+const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep, int n_embed, int n_ff);
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
                      bool long_ctx, hipStream_t s, uint8_t* act_trace = nullptr);
 /* one kernel of the fused step: phase 0 rmsnorm+QKV, 1 attention, 2 att_out,

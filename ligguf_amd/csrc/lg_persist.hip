@@ -74,7 +74,7 @@ __device__ __forceinline__ PkLayer pk_layer(const PkParams& P, int l)
 }
 
 /* One instantiation per (layer type, output type, head_dim, query heads per
- * KV head): every phase body is inlined, so no call saves registers, and the
+ * KV head), for n_embed 4096 and n_ff 12288 (the engine checks the widths): every phase body is inlined, so no call saves registers, and the
  * phases use the matvec batch sizes of the fused kernels (no spills: the
  * opaque thread index above keeps per-phase address arithmetic inside the
  * layer loop).  Activation buffers (each written once per launch): xs[l] =
@@ -100,26 +100,26 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
         float* hb = P.hb + (size_t)l * nff;
         if (l == 0)
             phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, BLD_EMB, 2, LG_QKV_R>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l), ATR(4 * l));
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l), ATR(4 * l), ne);
         else
             phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, BLD_RMS, 2, LG_QKV_R>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l), ATR(4 * l));
+                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l), ATR(4 * l), ne);
         phase_attn_any<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
         phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
             P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2),
-            ATR(4 * l + 1), att_partials<HD, NREP>(P, l, S.pos));
+            ATR(4 * l + 1), ne, att_partials<HD, NREP>(P, l, S.pos));
         phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, 2, LG_UG_R>(
             P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, xmid, nullptr, hb, nullptr, p0 + 3, p0 + 4, TR(5 * l + 3),
-            ATR(4 * l + 2));
+            ATR(4 * l + 2), ne);
         phase_mv<LT, NF, LG_DN_B, 1, EPI_RESID, BLD_PLAIN, 6, LG_DN_R>(
             P, 0, L.down, L.down_rsz, ne, 0, nullptr, hb, xmid, xout, nullptr, p0 + 4, p0 + 5, TR(5 * l + 4),
-            ATR(4 * l + 3));
+            ATR(4 * l + 3), nff);
     }
     const uint64_t pf = B + 5ull * P.n_layers;
     constexpr int NO = NsE<OT>::value;
     phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * ne, nullptr, P.logits, nullptr,
-        pf, pf + 1, TR(5 * P.n_layers), ATR(4 * P.n_layers));
+        pf, pf + 1, TR(5 * P.n_layers), ATR(4 * P.n_layers), ne);
 #undef TR
 #undef ATR
 }

@@ -156,14 +156,23 @@ __device__ __forceinline__ int chunk_base(int c)
     return ((LG_TID >> 6) + PK_WAVES * c) * 256 + 4 * (LG_TID & 63);
 }
 
+/* an activation of width n below the CPW * 256 * PK_WAVES a build covers:
+ * loads past n read its last four values (unconditional loads), and those
+ * values count as zero */
+__device__ __forceinline__ int chunk_ld(int c, int n)
+{
+    const int b = chunk_base(c);
+    return b < n ? b : n - 4;
+}
+
 /* rmsnorm weights of this wave's chunks: constants, loaded before the wait */
 template <int CPW>
 struct NormW {
     float4 g[CPW];
-    __device__ __forceinline__ void load(const float* __restrict__ w)
+    __device__ __forceinline__ void load(const float* __restrict__ w, int n)
     {
 #pragma unroll
-        for (int c = 0; c < CPW; c++) g[c] = *(const float4*)(w + chunk_base(c));
+        for (int c = 0; c < CPW; c++) g[c] = *(const float4*)(w + chunk_ld(c, n));
     }
 };
 
@@ -173,10 +182,10 @@ struct NormW {
 template <int CPW>
 struct ActSrc {
     float4 v[CPW];
-    __device__ __forceinline__ void load(const float* __restrict__ src)
+    __device__ __forceinline__ void load(const float* __restrict__ src, int n)
     {
 #pragma unroll
-        for (int c = 0; c < CPW; c++) v[c] = *(const float4*)(src + chunk_base(c));
+        for (int c = 0; c < CPW; c++) v[c] = *(const float4*)(src + chunk_ld(c, n));
     }
 };
 
@@ -202,7 +211,7 @@ struct MergeAct {
             const int cc = min(c, ms.nch - 1);   /* unconditional loads (see Rows) */
 #pragma unroll
             for (int k = 0; k < CPW; k++) {
-                const int b = chunk_base(k);
+                const int b = chunk_ld(k, ne);
                 o[c][k] = *(const float4*)(ms.po + (size_t)cc * ne + b);
                 ml[c][k] = *(const float2*)(ms.pml + ((size_t)cc * nh + b / ms.head_dim) * 2);
             }
@@ -267,9 +276,8 @@ __device__ __forceinline__ MergeSrc att_partials(const PkParams& P, int l, int p
  * stores that row as the residual stream `emb_out`. */
 template <int QT, int CPW>
 __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const NormW<CPW>& nw, const ActSrc<CPW>& xsrc,
-                                          bool from_embed, float* __restrict__ emb_out)
+                                          bool from_embed, float* __restrict__ emb_out, int n)
 {
-    constexpr int n = CPW * 256 * PK_WAVES;
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     float4 xv[CPW];
     if (from_embed) {
@@ -281,8 +289,8 @@ __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const Norm
 #pragma unroll
         for (int c = 0; c < CPW; c++) {
             const int b = chunk_base(c);
-            xv[c] = *(const float4*)(s_x + b);
-            if (blockIdx.x == 0) {
+            xv[c] = *(const float4*)(s_x + chunk_ld(c, n));
+            if (blockIdx.x == 0 && b < n) {
                 cst(&emb_out[b], xv[c].x); cst(&emb_out[b + 1], xv[c].y);
                 cst(&emb_out[b + 2], xv[c].z); cst(&emb_out[b + 3], xv[c].w);
             }
@@ -291,6 +299,9 @@ __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const Norm
 #pragma unroll
         for (int c = 0; c < CPW; c++) xv[c] = xsrc.v[c];
     }
+#pragma unroll
+    for (int c = 0; c < CPW; c++)
+        if (chunk_base(c) >= n) xv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     float p = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPW; c++) p += lg_sq4(xv[c]);
@@ -303,22 +314,27 @@ __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const Norm
     const float scale = 1.0f / sqrtf(ss / (float)n + P.eps);
 #pragma unroll
     for (int c = 0; c < CPW; c++) {
+        const int ch = wave + PK_WAVES * c;
+        if (256 * ch >= n) break;   /* wave-uniform */
         const float4 t = xv[c], g = nw.g[c];
         const float v[4] = {t.x * scale * g.x, t.y * scale * g.y, t.z * scale * g.z, t.w * scale * g.w};
-        lg_emit(v, QT, s_act, wave + PK_WAVES * c, 256);
+        lg_emit(v, QT, s_act, ch, min(256, n - 256 * ch));
     }
     bar();
 }
 
 /* the source chunks quantized into s_act */
 template <int QT, int CPW>
-__device__ __forceinline__ void build_plain(const ActSrc<CPW>& a)
+__device__ __forceinline__ void build_plain(const ActSrc<CPW>& a, int n)
 {
     const int wave = LG_TID >> 6;
 #pragma unroll
     for (int c = 0; c < CPW; c++) {
-        const float v[4] = {a.v[c].x, a.v[c].y, a.v[c].z, a.v[c].w};
-        lg_emit(v, QT, s_act, wave + PK_WAVES * c, 256);
+        const int ch = wave + PK_WAVES * c;
+        if (256 * ch >= n) break;   /* wave-uniform */
+        const bool ok = chunk_base(c) < n;
+        const float v[4] = {ok ? a.v[c].x : 0.f, ok ? a.v[c].y : 0.f, ok ? a.v[c].z : 0.f, ok ? a.v[c].w : 0.f};
+        lg_emit(v, QT, s_act, ch, min(256, n - 256 * ch));
     }
     bar();
 }
@@ -341,9 +357,10 @@ template <int FMT, int NS, int MAXB, int K>
 struct Rows {
     typename Fmt<FMT>::W w[MAXB][K][NS];
 
-    /* items i0, i0+ist, ... (MAXB of them), those past `wlast` replaced by wlast */
+    /* items i0, i0+ist, ... (MAXB of them), those past `wlast` replaced by
+     * wlast; slots past the row's nslots read its last slot (not used) */
     __device__ __forceinline__ void load(const uint8_t* __restrict__ W, uint32_t rsz, int i0, int ist, int wlast,
-                                         int kstride, int lane)
+                                         int kstride, int lane, int nslots)
     {
 #pragma unroll
         for (int b = 0; b < MAXB; b++) {
@@ -352,7 +369,7 @@ struct Rows {
             for (int k = 0; k < K; k++) {
                 const uint8_t* row = W + (size_t)(i + k * kstride) * rsz;
 #pragma unroll
-                for (int s = 0; s < NS; s++) Fmt<FMT>::load_w(w[b][k][s], row, lane + 64 * s);
+                for (int s = 0; s < NS; s++) Fmt<FMT>::load_w(w[b][k][s], row, min(lane + 64 * s, nslots - 1));
             }
         }
     }
@@ -373,11 +390,14 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                                          int items, int kstride, const float* __restrict__ normw,
                                          const float* __restrict__ src, const float* __restrict__ res_src,
                                          float* __restrict__ out, float* __restrict__ emb_out,
-                                         uint64_t wait_target, uint64_t sig, uint64_t* tr, uint8_t* atr,
+                                         uint64_t wait_target, uint64_t sig, uint64_t* tr, uint8_t* atr, int n_act,
                                          const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0})
 {
     using F = Fmt<FMT>;
     constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q1_0 || FMT == LG_Q1_G) ? LG_Q8_0 : LG_Q8_K;
+    /* a row of n_act values is nslots slots; lane j takes slots j, j+64, ..
+     * (NS of them, those past nslots unused) */
+    const int nslots = n_act / F::VALS;
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int nwv = gridDim.x * PK_WAVES;
     const int gw = blockIdx.x * PK_WAVES + wave;
@@ -402,7 +422,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
     auto load_src = [&]() {
         if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
-        else if (!from_embed) as.load(src);
+        else if (!from_embed) as.load(src, n_act);
     };
     auto load_res = [&](float* r, int b0) {
         if (EPI == EPI_RESID) {
@@ -413,7 +433,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     auto prefetch = [&]() {
 #pragma unroll
         for (int k = 0; k < (NR > 1 ? NR - 1 : 1); k++) {
-            R[k].load(W, rsz, i0 + k * MAXB * ist, ist, wlast, kstride, lane);
+            R[k].load(W, rsz, i0 + k * MAXB * ist, ist, wlast, kstride, lane, nslots);
             load_res(res[k], k * MAXB);
         }
     };
@@ -421,33 +441,32 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         /* no dependency wait (fused kernels): the activation and the norm
          * weights go first, the rows after them */
         load_src();
-        if (rms) nw.load(normw);
+        if (rms) nw.load(normw, n_act);
         lg_issue_order();   /* activation first */
         prefetch();
     } else {
-        if (rms) nw.load(normw);
+        if (rms) nw.load(normw, n_act);
         if (wave != 0) prefetch();
         pk_wait(P, wait_target);
         load_src();
         if (wave == 0) prefetch();
     }
     stamp(tr, 1);
-    if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out);
+    if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out, n_act);
     else {
         if (BLD == BLD_MERGE) mg.merge(ms.nch, as);
-        build_plain<QT, CPW>(as);
+        build_plain<QT, CPW>(as, n_act);
     }
     stamp(tr, 2);
     if (atr && blockIdx.x == 0) {
         /* activation trace (tests): the quantized blocks as built */
-        constexpr int n = CPW * 256 * PK_WAVES;
-        constexpr int words = (QT == LG_Q8_K ? n / 256 * LG_BS_Q8_K : n / 32 * LG_BS_Q8_0) / 4;
+        const int words = ((QT == LG_Q8_K ? n_act / 256 * LG_BS_Q8_K : n_act / 32 * LG_BS_Q8_0) + 3) / 4;
         for (int i = LG_TID; i < words; i += PK_THREADS) ((uint32_t*)atr)[i] = ((const uint32_t*)s_act)[i];
     }
 
     typename F::Act act[NS];
 #pragma unroll
-    for (int s = 0; s < NS; s++) F::load_act(act[s], s_act, lane + 64 * s);
+    for (int s = 0; s < NS; s++) F::load_act(act[s], s_act, min(lane + 64 * s, nslots - 1));
 
     float best = -INFINITY;
     int besti = 0x7fffffff;
@@ -460,7 +479,8 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                 for (int k = 0; k < K; k++) {
                     float a = 0.0f;
 #pragma unroll
-                    for (int s = 0; s < NS; s++) a += F::dot(R.w[b][k][s], act[s], lane + 64 * s);
+                    for (int s = 0; s < NS; s++)
+                        if (64 * (s + 1) <= nslots || lane + 64 * s < nslots) a += F::dot(R.w[b][k][s], act[s], lane + 64 * s);
                     acc[k] = lg_wave_sum(a);
                 }
                 const int i = i0 + (b0 + b) * ist;
@@ -483,7 +503,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     if (NR == 1) {
         for (int b0 = 0; b0 < my; b0 += MAXB) {
             if (b0 > 0) {
-                R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane);
+                R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane, nslots);
                 load_res(res[0], b0);
             }
             process(R[0], res[0], b0, min(MAXB, my - b0));
@@ -496,7 +516,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
 #pragma unroll
             for (int k = 0; k < NR; k++) {
                 const int jn = j0 + k + NR - 1;
-                R[(k + NR - 1) % NR].load(W, rsz, i0 + jn * MAXB * ist, ist, wlast, kstride, lane);
+                R[(k + NR - 1) % NR].load(W, rsz, i0 + jn * MAXB * ist, ist, wlast, kstride, lane, nslots);
                 load_res(res[(k + NR - 1) % NR], jn * MAXB);
                 process(R[k], res[k], (j0 + k) * MAXB, min(MAXB, my - (j0 + k) * MAXB));
             }
@@ -628,13 +648,16 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                                            uint64_t* tr, bool stamp0 = true)
 {
     int pos = pos_arg;   /* FIX: first read after the unit's loads (below) */
-    constexpr int LPP = HD / 8;            /* lanes per position */
+    constexpr int HDP = pk_hdp(HD);        /* lane layout width: HD padded to a power of two */
+    constexpr int LPP = HDP / 8;           /* lanes per position */
+    constexpr int GLV = HD / 8;            /* lanes of a position holding values (the rest zero) */
     constexpr int PPW = 64 / LPP;          /* positions per wave step */
     constexpr int PPB = PK_WAVES * PPW;    /* positions per WG step */
     constexpr int MAXST = pk_att_steps(NREP);
     constexpr int NSUB = NREP / NQ;       /* units per (kv head, chunk) */
     constexpr int NH = (NQ + PK_WAVES) / PK_WAVES;     /* heads normed per wave: NQ q + 1 k */
-    static_assert(PPB == PK_THREADS * 8 / HD, "step geometry of pk_attn_split");
+    static_assert(PPB == PK_THREADS * 8 / HDP, "step geometry of pk_attn_split");
+    static_assert(HD % 16 == 0 && HD <= 128, "head_dim: 48, 64, 128 (a multiple of 16 up to 128)");
     static_assert(NREP % NQ == 0, "query heads per unit divide the group");
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int gl = lane & (LPP - 1), grp = lane / LPP;
@@ -682,7 +705,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
              * are loaded and not used); else rows of the unit below pos */
             if (FIX) t = min(t, P.n_ctx - 1);
             else t = t < min(t0 + chunk, pos + 1) && t != pos ? t : t0;
-            const size_t o = loff + (size_t)t * kvd + (size_t)g * HD + gl * 8;
+            const size_t o = loff + (size_t)t * kvd + (size_t)g * HD + min(gl, GLV - 1) * 8;
             kb[set][st] = *(const uint4*)(P.kc + o);
             vb[set][st] = *(const uint4*)(P.vc + o);
         }
@@ -690,7 +713,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     /* q/k norm weights (a dummy slice of the rope table when the model has
      * none) and the rope frequencies of the lane's two pairs */
     const bool has_norm = L.q_norm != nullptr;
-    const int l4 = 4 * (lane & (HD / 4 - 1));
+    const int l4 = 4 * (lane % (HD / 4));
     float4 ng[NH];
     float2 fr;
     auto load_heads = [&](int u) {
@@ -738,7 +761,9 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int nsteps = (t1 - t0 + PPB - 1) / PPB;
         /* v of g into LDS, by every wave (the same values): an unconditional
          * use keeps its load ahead of the K/V loads */
-        *(float4*)(s_kv + HD + l4) = hv;
+        *(float4*)(s_kv + HDP + l4) = hv;
+        if (HD < HDP && 4 * lane >= HD && 4 * lane < HDP)
+            *(float4*)(s_kv + HDP + 4 * lane) = make_float4(0.f, 0.f, 0.f, 0.f);
         /* q heads q0.., then k of g: normed/roped into LDS (waves past
          * the last head compute a copy and store nothing: the operands' loads
          * are used unconditionally and stay where they are issued) */
@@ -749,8 +774,10 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
             float e[4] = {hx[j].x, hx[j].y, hx[j].z, hx[j].w};
             norm_rope_head<HD>(e, has_norm, ng[j], P.eps, P.rope_dim, pos, fr);
             if (h <= NQ) {
+                if (HD < HDP && 4 * lane >= HD && 4 * lane < HDP)
+                    *(float4*)((is_q ? s_q + h * HDP : s_kv) + 4 * lane) = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (4 * lane < HD) {
-                    float* dst = is_q ? s_q + h * HD : s_kv;
+                    float* dst = is_q ? s_q + h * HDP : s_kv;
                     *(float4*)(dst + 4 * lane) = make_float4(e[0], e[1], e[2], e[3]);
                     if (!is_q) {
                         if (c == nch - 1 && qsub == 0) {
@@ -776,7 +803,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 #pragma unroll
         for (int r = 0; r < QREG; r++)
 #pragma unroll
-            for (int i = 0; i < 8; i++) qr[r][i] = s_q[r * HD + gl * 8 + i];
+            for (int i = 0; i < 8; i++) qr[r][i] = s_q[r * HDP + gl * 8 + i];
 
         /* one pass: scores, online softmax, p.V (t == pos uses the fp32 k/v
          * of this step, fast/ligguf_fast_qk.cpp:77-79,98-99) */
@@ -800,13 +827,13 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                         h8(vb[set][st], vf);
                     } else {
 #pragma unroll
-                        for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HD + gl * 8 + i]; }
+                        for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HDP + gl * 8 + i]; }
                     }
 #pragma unroll
                     for (int r = 0; r < NQ; r++) {
                         float qv[8];
 #pragma unroll
-                        for (int i = 0; i < 8; i++) qv[i] = NQ <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HD + gl * 8 + i];
+                        for (int i = 0; i < 8; i++) qv[i] = NQ <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HDP + gl * 8 + i];
                         float sc = 0.0f;
 #pragma unroll
                         for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];
@@ -835,10 +862,20 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                 process(NB - 1, sb + H);
             }
         }
-        /* combine the position groups of the wave into group 0 (16-lane
-         * rows: row 1 -> 0 and 3 -> 2, then 2 -> 0, by lane permutes), then
-         * the waves (LDS) */
-        static_assert(LPP == 16, "position groups are 16-lane rows");
+        /* combine the position groups of the wave into group 0 (8-lane
+         * groups first pairwise by xor 8; then 16-lane rows: row 1 -> 0 and
+         * 3 -> 2, then 2 -> 0, by lane permutes), then the waves (LDS) */
+        static_assert(LPP == 16 || LPP == 8, "position groups of 8 or 16 lanes");
+        if constexpr (LPP == 8) {
+#pragma unroll
+            for (int r = 0; r < NQ; r++) {
+                float o2[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) o2[i] = __shfl_xor(o[r][i], 8);
+                const float m2 = __shfl_xor(m[r], 8), l2 = __shfl_xor(l[r], 8);
+                osm_merge(m[r], l[r], o[r], m2, l2, o2, 8);
+            }
+        }
 #pragma unroll
         for (int step = 0; step < 2; step++) {
 #pragma unroll
@@ -854,8 +891,10 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         if (grp == 0) {
 #pragma unroll
             for (int r = 0; r < NQ; r++) {
+                if (gl < GLV) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) s_o[(wave * NQ + r) * HD + gl * 8 + i] = o[r][i];
+                    for (int i = 0; i < 8; i++) s_o[(wave * NQ + r) * HD + gl * 8 + i] = o[r][i];
+                }
                 if (gl == 0) { s_m[wave * NQ + r] = m[r]; s_sc[wave * NQ + r] = l[r]; }
             }
         }
