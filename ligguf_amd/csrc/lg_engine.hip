@@ -155,6 +155,8 @@ struct lg_ctx {
     } arena = {};
     /* batched prefill */
     bool pf_ok = false;
+    int pf_fam = 0;                  /* activation forms of the model's matrices: bit 0 Q8_K, bit 1 Q8_0 */
+    uint8_t* pf_trace = nullptr;     /* quantized activations of every token of the next batched prefill */
     int prefill_path = LG_PREFILL_AUTO;
     std::vector<PfLayer> pf_layers;
     PfModel pf_model = {};
@@ -200,6 +202,8 @@ static void free_model(lg_ctx* ctx)
     ctx->dev_known = false;
     ctx->dev_feed_end = 0;
     ctx->pf_ok = false;
+    ctx->pf_fam = 0;
+    ctx->pf_trace = nullptr;
     ctx->arena = {};
     ctx->pf_layers.clear();
     ctx->pf = PfBuffers{};
@@ -665,6 +669,13 @@ extern "C" int lg_trace_acts_next_step(lg_ctx* ctx, void* trace_dev)
     return LG_OK;
 }
 
+extern "C" int lg_trace_acts_next_prefill(lg_ctx* ctx, void* trace_dev)
+{
+    if (!ctx) { lg_set_error("null context"); return LG_ERR_ARG; }
+    ctx->pf_trace = (uint8_t*)trace_dev;
+    return LG_OK;
+}
+
 extern "C" size_t lg_trace_acts_size(const lg_ctx* ctx)
 {
     if (!ctx || !ctx->loaded) return 0;
@@ -724,61 +735,87 @@ extern "C" int lg_decode_path(const lg_ctx* ctx)
 /* ------------------------------------------------------------------ */
 #define LG_PF_TMAX 512   /* tokens per layer pass */
 
-/* the batched prefill serves models whose layer matrices are all Q4_K or
- * all Q1_G (Q|K|V and up|gate stacked), widths multiples of 256, head_dim
- * 128 */
+/* the batched prefill serves models whose layer matrices all have a batched
+ * GEMM (the K-quants, Q8_0, Q1_0, Q1_G; any mix, Q|K|V and up|gate stacked
+ * or not) and whose attention shape the prefill attention kernel takes */
+static PfMat pf_mat(const dweight& w) { return PfMat{w.data, w.rsz, w.type, w.rows}; }
+
 static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
 {
     ctx->pf_ok = false;
-    const int nrep = m->n_heads / m->n_kv_heads;
-    bool ok = m->n_embed % 256 == 0 && m->n_ff % 256 == 0 && m->head_dim == 128 &&
-              (nrep == 1 || nrep == 2 || nrep == 4 || nrep == 8) && !ctx->layers.empty();
-    const int wt = ok ? ctx->layers[0].qkv.type : -1;
-    ok = ok && (wt == LG_Q4_K || wt == LG_Q1_G);
+    ctx->pf_fam = 0;
+    bool ok = lg_prefill_attn_supported(m->head_dim, m->n_heads / m->n_kv_heads) && !ctx->layers.empty();
+    int fam = 0;
+    auto take = [&](const dweight& w) {
+        const int at = lg_prefill_act_type(w.type);
+        /* the Q1_G GEMM steps 256 values */
+        if (at < 0 || (w.type == LG_Q1_G && w.cols % 256)) ok = false;
+        fam |= at == LG_Q8_K ? 1 : 2;
+    };
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
-        ok = D.qkv_fused && D.ug_fused && D.qkv.type == wt && D.att_out.type == wt && D.ug.type == wt &&
-             D.down.type == wt && D.down.cols == m->n_ff;
+        if (D.qkv_fused) take(D.qkv);
+        else { take(D.q); take(D.k); take(D.v); }
+        take(D.att_out);
+        if (D.ug_fused) take(D.ug);
+        else { take(D.up); take(D.gate); }
+        take(D.down);
+        ok = ok && D.down.cols == m->n_ff;
     }
     if (!ok) return;
     ctx->pf_layers.resize(m->n_layers);
     for (int l = 0; l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
         PfLayer& L = ctx->pf_layers[l];
-        L.qkv = D.qkv.data; L.ao = D.att_out.data; L.ug = D.ug.data; L.down = D.down.data;
-        L.qkv_rsz = D.qkv.rsz; L.ao_rsz = D.att_out.rsz; L.ug_rsz = D.ug.rsz; L.down_rsz = D.down.rsz;
+        L = PfLayer{};
+        L.qkv_fused = D.qkv_fused;
+        L.ug_fused = D.ug_fused;
+        if (D.qkv_fused) L.qkv = pf_mat(D.qkv);
+        else { L.q = pf_mat(D.q); L.k = pf_mat(D.k); L.v = pf_mat(D.v); }
+        L.ao = pf_mat(D.att_out);
+        if (D.ug_fused) L.ug = pf_mat(D.ug);
+        else { L.up = pf_mat(D.up); L.gate = pf_mat(D.gate); }
+        L.down = pf_mat(D.down);
         L.att_norm = D.att_norm; L.ffn_norm = D.ffn_norm; L.q_norm = D.q_norm; L.k_norm = D.k_norm;
     }
     PfModel& M = ctx->pf_model;
     M.layers = ctx->pf_layers.data();
-    M.wtype = wt;
     M.n_layers = m->n_layers; M.n_embed = m->n_embed; M.n_heads = m->n_heads; M.n_kv = m->n_kv_heads;
     M.head_dim = m->head_dim; M.kv_dim = m->kv_dim; M.n_ff = m->n_ff; M.n_ctx = m->n_context;
     M.rope_dim = m->rope_dim; M.eps = m->rms_epsilon;
     M.embd = ctx->embd.data; M.embd_rsz = ctx->embd.rsz; M.embd_t = ctx->embd.type;
     M.rope_freq = ctx->rope_freq; M.kc = ctx->kc; M.vc = ctx->vc;
+    ctx->pf_fam = fam;
     ctx->pf_ok = true;
 }
 
-/* buffers for LG_PF_TMAX tokens, allocated at the first batched prefill */
+/* buffers for LG_PF_TMAX tokens, allocated at the first batched prefill:
+ * the activation forms the model's matrices take, width up to
+ * max(n_embed, n_ff) */
 static int prefill_buffers(lg_ctx* c)
 {
     if (c->pf.tmax) return LG_OK;
     PfBuffers B = {};
     const int tmax = std::min(LG_PF_TMAX, (c->n_context + 3) / 4 * 4);
-    /* activation blocks of width n_ff: nff/256 Q8_K or nff/32 Q8_0 scales per token */
-    const size_t ne = c->n_embed, qs = ne + 2 * (size_t)c->kv_dim, nff = c->n_ff, nbm = nff / 256, nb0 = nff / 32;
+    const size_t ne = c->n_embed, qs = ne + 2 * (size_t)c->kv_dim, nff = c->n_ff, wide = std::max(ne, nff);
     int rc;
     if ((rc = dalloc(c, (void**)&B.toks, (size_t)tmax * sizeof(int)))) return rc;
     if ((rc = dalloc(c, (void**)&B.x, (size_t)tmax * ne * 4))) return rc;
     if ((rc = dalloc(c, (void**)&B.qkv, (size_t)tmax * qs * 4))) return rc;
     if ((rc = dalloc(c, (void**)&B.att, (size_t)tmax * ne * 4))) return rc;
     if ((rc = dalloc(c, (void**)&B.ug, (size_t)tmax * 2 * nff * 4))) return rc;
-    if ((rc = dalloc(c, (void**)&B.q.qs, (size_t)tmax * nff))) return rc;
-    if ((rc = dalloc(c, (void**)&B.q.d, nb0 * tmax * 4))) return rc;
-    if ((rc = dalloc(c, (void**)&B.q.bs, (size_t)tmax * nbm * 16 * 2))) return rc;
-    if ((rc = dalloc(c, (void**)&B.q.as, nb0 * tmax * 4))) return rc;
-    B.q.tld = tmax;
+    if (c->pf_fam & 1) {   /* Q8_K: quants, a scale and 16 bsums per 256 values */
+        if ((rc = dalloc(c, (void**)&B.qk.qs, (size_t)tmax * wide))) return rc;
+        if ((rc = dalloc(c, (void**)&B.qk.d, wide / 256 * tmax * 4))) return rc;
+        if ((rc = dalloc(c, (void**)&B.qk.bs, (size_t)tmax * (wide / 256) * 16 * 2))) return rc;
+        B.qk.tld = tmax;
+    }
+    if (c->pf_fam & 2) {   /* Q8_0: quants, a scale and a sum per 32 values */
+        if ((rc = dalloc(c, (void**)&B.q0.qs, (size_t)tmax * wide))) return rc;
+        if ((rc = dalloc(c, (void**)&B.q0.d, wide / 32 * tmax * 4))) return rc;
+        if ((rc = dalloc(c, (void**)&B.q0.as, wide / 32 * tmax * 4))) return rc;
+        B.q0.tld = tmax;
+    }
     B.tmax = tmax;
     c->pf = B;
     return LG_OK;
@@ -1231,17 +1268,27 @@ static int prefill_batched(lg_ctx* c, const int* toks, int n, int pos0)
     int rc;
     if ((rc = prefill_buffers(c))) return rc;
     LG_HIP_CHECK(hipStreamSynchronize(c->stream));   /* the token staging below reuses one buffer */
+    /* a trace request covers every token of this prompt */
+    uint8_t* tr = c->pf_trace;
+    c->pf_trace = nullptr;
+    const size_t tok_bytes = (size_t)(4 * c->n_layers + 1) * c->act_stride;
+    c->pf.trace_stride = c->act_stride;
     int T = 0;
     for (int off = 0; off < n; off += T) {
         T = std::min(c->pf.tmax, n - off);
+        c->pf.trace = tr ? tr + (size_t)off * tok_bytes : nullptr;
         LG_HIP_CHECK(hipMemcpyAsync(c->pf.toks, toks + off, (size_t)T * sizeof(int), hipMemcpyHostToDevice, c->stream));
-        if ((rc = lg_prefill_layers(c->pf_model, c->pf, T, pos0 + off, c->stream))) return rc;
+        rc = lg_prefill_layers(c->pf_model, c->pf, T, pos0 + off, c->stream);
+        c->pf.trace = nullptr;
+        if (rc) return rc;
         if (off + T < n) LG_HIP_CHECK(hipStreamSynchronize(c->stream));
     }
     LG_HIP_CHECK(hipMemcpyAsync(c->x, c->pf.x + (size_t)(T - 1) * c->n_embed, (size_t)c->n_embed * 4,
                                 hipMemcpyDeviceToDevice, c->stream));
     actbufs a;
-    if ((rc = prep_norm(c, c->x, c->out_norm, c->n_embed, act_family(c->output.type), a))) return rc;
+    const int fam_o = act_family(c->output.type);
+    if ((rc = prep_norm(c, c->x, c->out_norm, c->n_embed, fam_o, a))) return rc;
+    if ((rc = trace_act(c, tr ? tr + (size_t)(n - 1) * tok_bytes : nullptr, 4 * c->n_layers, fam_o, c->n_embed))) return rc;
     if ((rc = mv(c, c->output, a, c->logits, 0))) return rc;
     c->last_was_pk = false;
     c->dev_known = false;
@@ -1255,7 +1302,8 @@ extern "C" int lg_set_prefill_path(lg_ctx* ctx, int path)
         return ctx_fail(ctx, LG_ERR_ARG);
     }
     if (path == LG_PREFILL_BATCHED && ctx->loaded && !ctx->pf_ok) {
-        lg_set_error("set_prefill_path: the batched prefill needs Q4_K layer matrices and head_dim 128");
+        lg_set_error("set_prefill_path: the batched prefill needs quantized layer matrices (K-quants, Q8_0, Q1_0, "
+                     "Q1_G) and head_dim 48, 64 or 128");
         return ctx_fail(ctx, LG_ERR_TYPE);
     }
     ctx->prefill_path = path;
@@ -1271,11 +1319,12 @@ extern "C" int lg_prefill_path(const lg_ctx* ctx)
 extern "C" int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, int d, const float* x, int T, float* out,
                                 void* stream)
 {
-    if (type != LG_Q4_K && type != LG_Q1_G) {
-        lg_set_error("matmul_tokens: type %d (Q4_K or Q1_G only)", type);
+    const int at = lg_prefill_act_type(type);
+    if (at < 0) {
+        lg_set_error("matmul_tokens: type %d has no batched GEMM (K-quants, Q8_0, Q1_0, Q1_G)", type);
         return LG_ERR_TYPE;
     }
-    if (!w || !x || !out || n <= 0 || n % 256 || d <= 0 || T <= 0) {
+    if (!w || !x || !out || n <= 0 || n % (at == LG_Q8_K ? 256 : 32) || d <= 0 || T <= 0) {
         lg_set_error("matmul_tokens: bad arguments (n %d, d %d, T %d)", n, d, T);
         return LG_ERR_ARG;
     }
@@ -1293,12 +1342,10 @@ extern "C" int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, in
     q.d = (float*)(ws + o_d);
     q.bs = (int16_t*)(ws + o_bs);
     q.as = (int*)(ws + o_as);
-    const bool q1 = type == LG_Q1_G;
-    int rc = lg_prefill_quantize(q1 ? LG_Q8_0 : LG_Q8_K, x, n, nullptr, 0.0f, n, T, q, (hipStream_t)stream);
-    if (!rc) rc = q1 ? lg_prefill_gemm_q1g((const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream)
-                     : lg_prefill_gemm_q4k((const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream);
+    int rc = lg_prefill_quantize(at, x, n, nullptr, 0.0f, n, T, q, (hipStream_t)stream);
+    if (!rc) rc = lg_prefill_gemm(type, (const uint8_t*)w, rsz, d, n, q, T, out, d, 0, (hipStream_t)stream);
     const hipError_t e2 = hipStreamSynchronize((hipStream_t)stream);
-    hipFree(ws);
+    (void)hipFree(ws);
     if (!rc && e2 != hipSuccess) { lg_set_error("matmul_tokens: %s", hipGetErrorString(e2)); rc = LG_ERR_HIP; }
     return rc;
 }
@@ -1315,6 +1362,7 @@ extern "C" int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* 
     hipSetDevice(ctx->device);
     const bool batched = ctx->pf_ok && (ctx->prefill_path == LG_PREFILL_BATCHED ||
                                         (ctx->prefill_path == LG_PREFILL_AUTO && n >= 2));
+    if (!batched) ctx->pf_trace = nullptr;   /* the prefill trace covers the batched path only */
     if (batched) {
         int rc = prefill_batched(ctx, toks, n, pos0);
         if (rc) return ctx_fail(ctx, rc);

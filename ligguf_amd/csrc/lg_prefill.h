@@ -5,10 +5,11 @@
 #include <stdint.h>
 
 /* Quantized activations of T tokens, structure of arrays (the GEMMs stage a
- * token tile with 16-byte loads).  Q8_K (Q4_K weights): qs [T][K] int8, d
- * [K/256][tld] block scales (tokens contiguous), bs [T][K/256][16] the
- * blocks' bsums.  Q8_0 (Q1_G weights): qs [T][K], d [K/32][tld] the fp16
- * block scales as floats, as [K/32][tld] the blocks' sums of q. */
+ * token tile with 16-byte loads).  Q8_K form (K-quant weights): qs [T][K]
+ * int8, d [K/256][tld] block scales (tokens contiguous), bs [T][K/256][16]
+ * the blocks' bsums.  Q8_0 form (Q8_0, Q1_0, Q1_G weights): qs [T][K], d
+ * [K/32][tld] the fp16 block scales as floats, as [K/32][tld] the blocks'
+ * sums of q. */
 struct PfQ8K {
     int8_t* qs;
     float* d;
@@ -17,17 +18,25 @@ struct PfQ8K {
     int tld;
 };
 
-/* one layer as the batched prefill reads it: fused Q|K|V and up|gate
- * matrices, all of the model's weight type (PfModel.wtype) */
+/* one weight matrix as the prefill reads it: GGUF rows of `type` */
+struct PfMat {
+    const uint8_t* w;
+    uint32_t rsz;
+    int type;
+    int rows;
+};
+
+/* one layer: Q|K|V as one stacked matrix (qkv_fused) or three, up|gate as
+ * one (ug_fused) or two; each matrix of any type the batched GEMMs take */
 struct PfLayer {
-    const uint8_t *qkv, *ao, *ug, *down;
-    uint32_t qkv_rsz, ao_rsz, ug_rsz, down_rsz;
+    PfMat q, k, v, qkv;
+    PfMat ao, up, gate, ug, down;
+    bool qkv_fused, ug_fused;
     const float *att_norm, *ffn_norm, *q_norm, *k_norm;   /* q/k norms NULL for llama */
 };
 
 struct PfModel {
     const PfLayer* layers;   /* host array */
-    int wtype;               /* LG_Q4_K (Q8_K activations) or LG_Q1_G (Q8_0) */
     int n_layers, n_embed, n_heads, n_kv, head_dim, kv_dim, n_ff, n_ctx, rope_dim;
     float eps;
     const uint8_t* embd;
@@ -46,22 +55,33 @@ struct PfBuffers {
     float* qkv;      /* [tmax][n_embed + 2 kv_dim] */
     float* att;      /* [tmax][n_embed] */
     float* ug;       /* [tmax][2 n_ff] */
-    PfQ8K q;         /* activations of width up to n_ff */
+    PfQ8K qk;        /* Q8_K form, width up to n_ff (qs NULL when no matrix takes it) */
+    PfQ8K q0;        /* Q8_0 form (likewise) */
+    /* activation trace of one pass (NULL: none): token t's activation k in
+     * block_q8_K / block_q8_0 rows at trace + (t (4 L + 1) + k) stride */
+    uint8_t* trace;
+    size_t trace_stride;
 };
+
+/* activation form a weight type takes: LG_Q8_K, LG_Q8_0, or -1 when the
+ * batched GEMMs do not take the type */
+int lg_prefill_act_type(int wtype);
+
+/* the prefill attention's head widths and query heads per KV head */
+int lg_prefill_attn_supported(int head_dim, int nrep);
 
 /* The layers of T prompt tokens at positions pos0.. (T <= B.tmax, tokens in
  * B.toks): KV rows pos0..pos0+T-1 written, B.x = the residual stream after
  * the last layer. */
 int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream_t s);
 
-/* one Q4_K x Q8_K GEMM, out[t][r] (+)= sum_k W[r][k] x[t][k] over T tokens
- * of quantized activations (tests and benches) */
-int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out,
-                        int ldo, int accumulate, hipStream_t s);
-/* one Q1_G x Q8_0 GEMM, as lg_prefill_gemm_q4k */
-int lg_prefill_gemm_q1g(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out,
-                        int ldo, int accumulate, hipStream_t s);
-/* rmsnorm (norm_w != NULL) and the activation quantizer of qtype (LG_Q8_K or
- * LG_Q8_0) for T tokens of width n */
+/* One GEMM out[t][r] (+)= sum_k W[r][k] x[t][k] over T tokens of activations
+ * quantized in the form lg_prefill_act_type(wtype) gives (tests, benches and
+ * the layer passes). */
+int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out,
+                    int ldo, int accumulate, hipStream_t s);
+/* rmsnorm (norm_w != NULL) and the activation quantizer of qtype (LG_Q8_K,
+ * n a multiple of 256, or LG_Q8_0, n a multiple of 32) for T tokens of
+ * width n */
 int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w, float eps, int n, int T,
                         const PfQ8K& q, hipStream_t s);

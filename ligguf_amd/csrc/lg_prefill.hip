@@ -65,9 +65,10 @@ __device__ __forceinline__ void pf_store_q8_0(const float v[4], const PfQ8K& q, 
 {
     const int lane = threadIdx.x & 63;
     const Q80Lane r = lg_q8_0_lane(v);
-    *(uint32_t*)(q.qs + (size_t)t * n + b * 256 + 4 * lane) = r.packed;
     /* the block's sum of q over its 8 lanes: integers below 2^24, exact in fp32 */
     const int bs = (int)lg_group_sum<8>((float)lg_dot4((int)r.packed, 0x01010101, 0));
+    if (b * 256 + 4 * lane >= n) return;   /* blocks past a width that is no multiple of 256 (8 lanes each) */
+    *(uint32_t*)(q.qs + (size_t)t * n + b * 256 + 4 * lane) = r.packed;
     if ((lane & 7) == 0) {
         const size_t i = (size_t)(8 * b + (lane >> 3)) * q.tld + t;
         q.d[i] = lg_h2f(lg_f2h(r.d));
@@ -97,9 +98,10 @@ __global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, in
         scale = 1.0f / sqrtf(ss / (float)n + eps);
     }
     const int base = b * 256 + 4 * lane;
-    const float4 tv = *(const float4*)(xr + base);
+    const bool in = base < n;   /* Q8_0 widths that are no multiple of 256: zeros past the end, not stored */
+    const float4 tv = in ? *(const float4*)(xr + base) : make_float4(0.f, 0.f, 0.f, 0.f);
     float v[4] = {tv.x, tv.y, tv.z, tv.w};
-    if (w) {
+    if (w && in) {
         const float4 g = *(const float4*)(w + base);
         v[0] = tv.x * scale * g.x; v[1] = tv.y * scale * g.y; v[2] = tv.z * scale * g.z; v[3] = tv.w * scale * g.w;
     }
@@ -114,8 +116,9 @@ __global__ __launch_bounds__(64) void k_pf_swiglu_quant(const float* __restrict_
     const int lane = threadIdx.x, b = blockIdx.x, t = blockIdx.y;
     const float* ur = ug + (size_t)t * 2 * nff;
     const int base = b * 256 + 4 * lane;
-    const float4 u = *(const float4*)(ur + base);
-    const float4 g = *(const float4*)(ur + nff + base);
+    const bool in = base < nff;
+    const float4 u = in ? *(const float4*)(ur + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 g = in ? *(const float4*)(ur + nff + base) : make_float4(0.f, 0.f, 0.f, 0.f);
     float v[4];
     v[0] = (g.x / (1.0f + expf(-g.x))) * u.x;
     v[1] = (g.y / (1.0f + expf(-g.y))) * u.y;
@@ -345,8 +348,8 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(4))) void
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
-                        int accumulate, hipStream_t s)
+static int gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                    int accumulate, hipStream_t s)
 {
     if (!W || !out || rows <= 0 || cols <= 0 || cols % 256 || T <= 0 || T > x.tld || x.tld % 4 ||
         rsz != (uint32_t)(cols / 256) * LG_BS_Q4_K || ldo < rows) {
@@ -369,12 +372,14 @@ int lg_prefill_gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
 int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w, float eps, int n, int T,
                         const PfQ8K& q, hipStream_t s)
 {
-    if (!x || n <= 0 || n % 256 || T <= 0 || T > q.tld || ldx < n || (qtype != LG_Q8_K && qtype != LG_Q8_0)) {
+    if (!x || !q.qs || n <= 0 || n % (qtype == LG_Q8_K ? 256 : 32) || T <= 0 || T > q.tld || ldx < n ||
+        (qtype != LG_Q8_K && qtype != LG_Q8_0)) {
         lg_set_error("prefill quantize: bad arguments (type %d, n %d, T %d)", qtype, n, T);
         return LG_ERR_ARG;
     }
-    if (qtype == LG_Q8_K) hipLaunchKernelGGL(k_pf_quant<LG_Q8_K>, dim3(n / 256, T), dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
-    else hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, dim3(n / 256, T), dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    const dim3 grid((n + 255) / 256, T);
+    if (qtype == LG_Q8_K) hipLaunchKernelGGL(k_pf_quant<LG_Q8_K>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    else hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
     return lg_check_launch("prefill quantize");
 }
 
@@ -512,8 +517,8 @@ __global__ __launch_bounds__(512) void k_pf_gemm_q1g(
     }
 }
 
-int lg_prefill_gemm_q1g(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
-                        int accumulate, hipStream_t s)
+static int gemm_q1g(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                    int accumulate, hipStream_t s)
 {
     if (!W || !out || !x.as || rows <= 0 || cols <= 0 || cols % 256 || T <= 0 || T > x.tld || x.tld % 4 ||
         rsz != (uint32_t)(cols / 128) * LG_BS_Q1_G || ldo < rows) {
@@ -525,6 +530,526 @@ int lg_prefill_gemm_q1g(const uint8_t* W, uint32_t rsz, int rows, int cols, cons
     if (accumulate) hipLaunchKernelGGL((k_pf_gemm_q1g<1>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     else hipLaunchKernelGGL((k_pf_gemm_q1g<0>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
     return lg_check_launch("prefill gemm Q1_G");
+}
+
+/* ------------------------------------------------------------------ */
+/* Q2_K, Q3_K, Q5_K, Q6_K x Q8_K GEMMs on int8 MFMA                      */
+/* ------------------------------------------------------------------ */
+/* Tile, grid and token staging as k_pf_gemm_q4k: 128 rows x 64 tokens per
+ * workgroup, the Q8_K token tile of each 256-value block in LDS in the same
+ * lane-group order (per 64-value chunk c, lane group g: the 8 values
+ * 64c+8g.. then the 8 values 64c+32+8g..).  Each sub-block's integer sum
+ * isum_j is one v_mfma_i32_16x16x32_i8 (8 bytes a lane): the first 8
+ * staged bytes of every lane group are values 64c..64c+31, the second 8
+ * values 64c+32..64c+63.  A 32-value sub-block (Q5_K) is one such product;
+ * a 16-value one (Q2_K, Q3_K, Q6_K) is half of it, so two products run
+ * with the weight bytes of lane groups 2,3 or 0,1 zeroed.  The sub-block
+ * scale of the lane's row then multiplies isum_j in int32:
+ * S = sum_j sc_j isum_j is the reference's integer (its aux32 / isum sums),
+ * exact; the mins term M (Q2_K, Q5_K) is an fp32 MFMA product of the bsums
+ * and the 4-bit / 6-bit mins, exact (integers below 2^24); per block
+ *   Q2_K, Q5_K: out += d_a (d_w S - dmin_w M)
+ *   Q3_K, Q6_K: out += (d_w d_a) S
+ * fp32 rounding order aside, the reference's dot of each type. */
+template <int WT>
+struct PfKq;
+
+/* Q2_K (84 B: scales[16], qs[64], d, dmin): value 128n + 32j + l is bits
+ * 2j of qs[32n + l]; 16-value sub-block i: scale = low nibble of
+ * scales[i], min = high nibble.  fast/lil_math.cpp:539-580 */
+template <>
+struct PfKq<LG_Q2_K> {
+    static constexpr int SUB = 16, MINS = 1;
+    struct Blk {
+        uint2 q[2];
+        uint4 sc;
+        uint32_t dd;
+    };
+    static __device__ __forceinline__ void load(Blk& B, const uint8_t* p, int g)
+    {
+        B.q[0] = lg_ld<uint2>(p + 16 + 8 * g);
+        B.q[1] = lg_ld<uint2>(p + 48 + 8 * g);
+        B.sc = lg_ld<uint4>(p);
+        B.dd = lg_ld<uint32_t>(p + 80);
+    }
+    /* the lane's 8 values of half h of chunk c (values 64c + 32h + 8g..) */
+    static __device__ __forceinline__ uint2 vals(const Blk& B, int c, int h)
+    {
+        const int j = 2 * (c & 1) + h;
+        const uint2 q = c >> 1 ? B.q[1] : B.q[0];
+        return make_uint2((q.x >> (2 * j)) & 0x03030303u, (q.y >> (2 * j)) & 0x03030303u);
+    }
+    static __device__ __forceinline__ int scale(const Blk& B, int i) { return byte16(B.sc, i) & 15; }
+    static __device__ __forceinline__ float minv(const Blk& B, int i) { return (float)(byte16(B.sc, i) >> 4); }
+    static __device__ __forceinline__ float d(const Blk& B) { return lg_h2f((uint16_t)(B.dd & 0xffffu)); }
+    static __device__ __forceinline__ float dmin(const Blk& B) { return lg_h2f((uint16_t)(B.dd >> 16)); }
+};
+
+/* Q3_K (110 B: hmask[32], qs[64], scales[12], d): value 128n + 32j + l is
+ * bits 2j of qs[32n + l], minus 4 where bit 4n + j of hmask[l] is clear;
+ * 16 six-bit scales minus 32.  fast/lil_math.cpp:466-537 */
+template <>
+struct PfKq<LG_Q3_K> {
+    static constexpr int SUB = 16, MINS = 0;
+    struct Blk {
+        uint2 q[2], hm;
+        uint32_t s0, s1, s2, d;
+    };
+    static __device__ __forceinline__ void load(Blk& B, const uint8_t* p, int g)
+    {
+        B.hm = lg_ld<uint2>(p + 8 * g);
+        B.q[0] = lg_ld<uint2>(p + 32 + 8 * g);
+        B.q[1] = lg_ld<uint2>(p + 64 + 8 * g);
+        B.s0 = lg_ld<uint32_t>(p + 96);
+        B.s1 = lg_ld<uint32_t>(p + 100);
+        B.s2 = lg_ld<uint32_t>(p + 104);
+        B.d = lg_ld16(p + 108);
+    }
+    static __device__ __forceinline__ uint2 vals(const Blk& B, int c, int h)
+    {
+        const int n = c >> 1, j = 2 * (c & 1) + h;
+        const uint2 q = n ? B.q[1] : B.q[0];
+        auto one = [&](uint32_t qw, uint32_t hw) {
+            const uint32_t u = ((qw >> (2 * j)) & 0x03030303u) | (((hw >> (4 * n + j)) & 0x01010101u) << 2);
+            return ((u | 0x80808080u) - 0x04040404u) ^ 0x80808080u;   /* bytewise u - 4 (u < 8) */
+        };
+        return make_uint2(one(q.x, B.hm.x), one(q.y, B.hm.y));
+    }
+    /* scale i: low nibble of byte i (i < 8) or high nibble of byte i - 8 of
+     * the first 8 bytes, two high bits from byte 8 + (i & 3) at 2 (i / 4) */
+    static __device__ __forceinline__ int scale(const Blk& B, int i)
+    {
+        const uint32_t lw = (i & 7) < 4 ? B.s0 : B.s1;
+        const int lo = i < 8 ? byte_of(lw, i & 3) & 15 : byte_of(lw, i & 3) >> 4;
+        const int hi = (byte_of(B.s2, i & 3) >> (2 * (i >> 2))) & 3;
+        return (lo | (hi << 4)) - 32;
+    }
+    static __device__ __forceinline__ float minv(const Blk&, int) { return 0.0f; }
+    static __device__ __forceinline__ float d(const Blk& B) { return lg_h2f((uint16_t)B.d); }
+    static __device__ __forceinline__ float dmin(const Blk&) { return 0.0f; }
+};
+
+/* Q5_K (176 B: d, dmin, scales[12], qh[32], qs[128]): value 64c + 32h + i
+ * is nibble h of qs[32c + i] plus 16 x bit 2c + h of qh[i]; 32-value
+ * sub-blocks with the Q4_K scale/min packing.  fast/lil_math.cpp:618-686 */
+template <>
+struct PfKq<LG_Q5_K> {
+    static constexpr int SUB = 32, MINS = 1;
+    struct Blk {
+        uint4 hdr;
+        uint2 qh, q[4];
+    };
+    static __device__ __forceinline__ void load(Blk& B, const uint8_t* p, int g)
+    {
+        B.hdr = lg_ld<uint4>(p);
+        B.qh = lg_ld<uint2>(p + 16 + 8 * g);
+#pragma unroll
+        for (int c = 0; c < 4; c++) B.q[c] = lg_ld<uint2>(p + 48 + 32 * c + 8 * g);
+    }
+    static __device__ __forceinline__ uint2 vals(const Blk& B, int c, int h)
+    {
+        auto one = [&](uint32_t qw, uint32_t hw) {
+            return ((qw >> (4 * h)) & 0x0F0F0F0Fu) | (((hw >> (2 * c + h)) & 0x01010101u) << 4);
+        };
+        const uint2 q = c == 0 ? B.q[0] : c == 1 ? B.q[1] : c == 2 ? B.q[2] : B.q[3];
+        return make_uint2(one(q.x, B.qh.x), one(q.y, B.qh.y));
+    }
+    /* get_scale_min_k4 (fast/lil_math.cpp:129-138) */
+    static __device__ __forceinline__ int scale(const Blk& B, int j)
+    {
+        const uint32_t w = j < 4 ? B.hdr.y & 0x3F3F3F3Fu : (B.hdr.w & 0x0F0F0F0Fu) | ((B.hdr.y >> 2) & 0x30303030u);
+        return byte_of(w, j & 3);
+    }
+    static __device__ __forceinline__ float minv(const Blk& B, int j)
+    {
+        const uint32_t w = j < 4 ? B.hdr.z & 0x3F3F3F3Fu
+                                 : ((B.hdr.w >> 4) & 0x0F0F0F0Fu) | ((B.hdr.z >> 2) & 0x30303030u);
+        return (float)byte_of(w, j & 3);
+    }
+    static __device__ __forceinline__ float d(const Blk& B) { return lg_h2f((uint16_t)(B.hdr.x & 0xffffu)); }
+    static __device__ __forceinline__ float dmin(const Blk& B) { return lg_h2f((uint16_t)(B.hdr.x >> 16)); }
+};
+
+/* Q6_K (210 B: ql[128], qh[64], scales[16] int8, d): value
+ * 128n + 64c' + 32h + l is nibble c' of ql[64n + 32h + l] with bits
+ * 2(2c' + h) of qh[32n + l] above it, minus 32.  fast/lil_math.cpp:688-739 */
+template <>
+struct PfKq<LG_Q6_K> {
+    static constexpr int SUB = 16, MINS = 0;
+    struct Blk {
+        uint2 ql[2][2], qh[2];
+        uint4 sc;
+        uint32_t d;
+    };
+    static __device__ __forceinline__ void load(Blk& B, const uint8_t* p, int g)
+    {
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            B.ql[n][0] = lg_ld<uint2>(p + 64 * n + 8 * g);
+            B.ql[n][1] = lg_ld<uint2>(p + 64 * n + 32 + 8 * g);
+            B.qh[n] = lg_ld<uint2>(p + 128 + 32 * n + 8 * g);
+        }
+        B.sc = lg_ld<uint4>(p + 192);
+        B.d = lg_ld16(p + 208);
+    }
+    static __device__ __forceinline__ uint2 vals(const Blk& B, int c, int h)
+    {
+        const int n = c >> 1, cp = c & 1, sh = 2 * (2 * cp + h);
+        const uint2 l = n ? B.ql[1][h] : B.ql[0][h], hq = n ? B.qh[1] : B.qh[0];
+        auto one = [&](uint32_t lw, uint32_t hw) {
+            const uint32_t u = ((lw >> (4 * cp)) & 0x0F0F0F0Fu) | (((hw >> sh) & 0x03030303u) << 4);
+            return ((u | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   /* bytewise u - 32 (u < 64) */
+        };
+        return make_uint2(one(l.x, hq.x), one(l.y, hq.y));
+    }
+    static __device__ __forceinline__ int scale(const Blk& B, int i) { return (int)(int8_t)byte16(B.sc, i); }
+    static __device__ __forceinline__ float minv(const Blk&, int) { return 0.0f; }
+    static __device__ __forceinline__ float d(const Blk& B) { return lg_h2f((uint16_t)B.d); }
+    static __device__ __forceinline__ float dmin(const Blk&) { return 0.0f; }
+};
+
+__device__ __forceinline__ long pf_u2l(uint2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
+
+template <int WT, int ACC>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_kq(
+    const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
+{
+    using F = PfKq<WT>;
+    constexpr int MI = 4, BSZ = WT == LG_Q2_K ? LG_BS_Q2_K : WT == LG_Q3_K ? LG_BS_Q3_K : WT == LG_Q5_K ? LG_BS_Q5_K : LG_BS_Q6_K;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][64 * PF_AST];
+    __shared__ __attribute__((aligned(16))) int16_t s_bs[2][64 * 16];
+    __shared__ __attribute__((aligned(16))) float s_d[2][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int nb = K >> 8;
+    const int nt = (T + 63) / 64;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int rb = (slot / nt) * 8 + xcd;
+    if (rb * 128 >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
+    const int t0 = (slot % nt) * 64;
+    const int r0 = rb * 128 + wave * 16;
+    const uint8_t* wr = W + (size_t)min(r0 + l16, R - 1) * rsz;
+
+    /* staging per block as k_pf_gemm_q4k with 64 tokens: thread tid takes
+     * quant chunks tid and tid + 512 (token chunk/16, 16-byte piece
+     * chunk%16), a quarter of token tid/4's bsums (tid < 256) and four block
+     * scales (tid < 16) */
+    struct Stg {
+        uint4 a[2];
+        uint2 bs;
+        uint4 d;
+    };
+    auto stage_load = [&](Stg& st, int b) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int q = tid + 512 * i, tok = min(t0 + (q >> 4), T - 1);
+            st.a[i] = *(const uint4*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
+        }
+        const int tb = min(t0 + ((tid >> 2) & 63), T - 1);
+        st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
+        st.d = *(const uint4*)(x.d + (size_t)b * x.tld + min(t0 + 4 * (tid & 15), x.tld - 4));
+    };
+    auto stage_store = [&](const Stg& st, int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int q = tid + 512 * i, p = q & 15, k = p & 3;
+            int8_t* dst = s_a[buf] + (q >> 4) * PF_AST + 64 * (p >> 2) + 32 * (k & 1) + 8 * (k >> 1);
+            *(uint2*)dst = make_uint2(st.a[i].x, st.a[i].y);
+            *(uint2*)(dst + 16) = make_uint2(st.a[i].z, st.a[i].w);
+        }
+        if (tid < 256) *(uint2*)(s_bs[buf] + (tid >> 2) * 16 + (tid & 3) * 4) = st.bs;
+        if (tid < 16) *(uint4*)(s_d[buf] + 4 * tid) = st.d;
+    };
+
+    v4f acc[MI];
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) acc[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int b, const typename F::Blk& cur) {
+        const int buf = b & 1;
+        v4i S[MI];
+#pragma unroll
+        for (int mi = 0; mi < MI; mi++) S[mi] = (v4i){0, 0, 0, 0};
+        const int8_t* sa = s_a[buf] + l16 * PF_AST + 16 * g;
+        /* one chunk at a time for the 16-value types: the 16 products of a
+         * chunk give the MFMA enough independent work, and more chunks in
+         * flight spill */
+        constexpr int UC = F::SUB == 16 ? 1 : 4;
+#pragma unroll UC
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const long bw = pf_u2l(F::vals(cur, c, h));
+                if constexpr (F::SUB == 32) {
+                    const int sc = F::scale(cur, 2 * c + h);
+#pragma unroll
+                    for (int mi = 0; mi < MI; mi++) {
+                        const long a = *(const long*)(sa + 16 * mi * PF_AST + 64 * c + 8 * h);
+                        const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bw, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                        S[mi] += sc * is;
+                    }
+                } else {
+                    /* sub-blocks 4c + 2h (lane groups 0, 1) and 4c + 2h + 1 (groups 2, 3) */
+                    const long b0 = g < 2 ? bw : 0L, b1 = g < 2 ? 0L : bw;
+                    const int sc0 = F::scale(cur, 4 * c + 2 * h), sc1 = F::scale(cur, 4 * c + 2 * h + 1);
+#pragma unroll
+                    for (int mi = 0; mi < MI; mi++) {
+                        const long a = *(const long*)(sa + 16 * mi * PF_AST + 64 * c + 8 * h);
+                        const v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                        const v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                        S[mi] += sc0 * i0 + sc1 * i1;
+                    }
+                }
+            }
+        }
+        const float dw = F::d(cur), dmw = F::dmin(cur);
+#pragma unroll
+        for (int mi = 0; mi < MI; mi++) {
+            const float4 dx = *(const float4*)(s_d[buf] + 16 * mi + 4 * g);
+            const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+            if constexpr (F::MINS) {
+                /* M[token][row] = sum_i min_i bsum_i (k = g: the lane's mins) */
+                const int16_t* bsr = s_bs[buf] + (16 * mi + l16) * 16;
+                v4f M = (v4f){0.f, 0.f, 0.f, 0.f};
+                if constexpr (F::SUB == 16) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        M = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bsr[4 * q + g], F::minv(cur, 4 * q + g), M, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 2; q++) {
+                        const int j = 4 * q + g, v = *(const int*)(bsr + 2 * j);
+                        const float bp = (float)((int)(int16_t)(v & 0xffff) + (int)(int16_t)(v >> 16));
+                        M = __builtin_amdgcn_mfma_f32_16x16x4f32(bp, F::minv(cur, j), M, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[mi][i] = __builtin_fmaf(dxs[i], lg_fma2(dw, (float)S[mi][i], -dmw, M[i]), acc[mi][i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mi][i] = __builtin_fmaf(dw * dxs[i], (float)S[mi][i], acc[mi][i]);
+            }
+        }
+    };
+
+    typename F::Blk cur, nxt;
+    Stg st;
+    stage_load(st, 0);
+    F::load(cur, wr, g);
+    stage_store(st, 0);
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        const int bn = min(b + 1, nb - 1);
+        stage_load(st, bn);
+        F::load(nxt, wr + (size_t)bn * BSZ, g);
+        compute(b, cur);
+        stage_store(st, (b + 1) & 1);
+        cur = nxt;
+        __syncthreads();
+    }
+    const int r = r0 + l16;
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 16 * mi + 4 * g + i;
+            if (t < T && r < R) {
+                float* o = out + (size_t)t * ldo + r;
+                *o = ACC ? *o + acc[mi][i] : acc[mi][i];
+            }
+        }
+    }
+}
+
+template <int WT>
+static int gemm_kq(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                   int accumulate, hipStream_t s)
+{
+    const int nrb8 = (rows + 127) / 128 + 7 & ~7;
+    const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
+    if (accumulate) hipLaunchKernelGGL((k_pf_gemm_kq<WT, 1>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    else hipLaunchKernelGGL((k_pf_gemm_kq<WT, 0>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    return lg_check_launch("prefill gemm (K-quant)");
+}
+
+/* ------------------------------------------------------------------ */
+/* Q8_0 and Q1_0 x Q8_0 GEMMs on int8 MFMA                              */
+/* ------------------------------------------------------------------ */
+/* dot_q8_0_q8_0 and dot_q8_0_q1_0 (fast/lil_math.cpp:411-438): per 32-value
+ * block the integer sum s of w*q (Q1_0: w = +1 where the bit is set, else
+ * -1), then acc += d_w d_a s.  s is one v_mfma_i32_16x16x32_i8 (lane group
+ * g feeds values 8g..8g+7 of the block: 8 Q8_0 bytes, or bit byte g of a
+ * Q1_0 block as +-1 bytes), exact; the fp32 combination runs per block.
+ * Tile and staging as k_pf_gemm_q1g: 128 rows x 64 tokens, the token
+ * tile's quants in groups of 4 blocks (128 values) in LDS with their
+ * scales, double-buffered.  The width need only be a multiple of 32: a
+ * last group of fewer than 4 blocks stages clamped bytes it never uses. */
+template <int WT, int ACC>
+__global__ __launch_bounds__(512) void k_pf_gemm_b32(
+    const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
+{
+    constexpr int MI = 4, BSZ = WT == LG_Q8_0 ? LG_BS_Q8_0 : LG_BS_Q1_0;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][64 * PF1_AST];
+    __shared__ __attribute__((aligned(16))) float s_d[2][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int nbk = K >> 5, ng = (nbk + 3) >> 2;
+    const int nt = (T + 63) / 64;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int rb = (slot / nt) * 8 + xcd;
+    if (rb * 128 >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
+    const int t0 = (slot % nt) * 64;
+    const int r0 = rb * 128 + wave * 16;
+    const uint8_t* wr = W + (size_t)min(r0 + l16, R - 1) * rsz;
+
+    struct Stg {
+        uint4 a;
+        float4 d;
+    };
+    auto stage_load = [&](Stg& st, int gi) {
+        const int tok = min(t0 + (tid >> 3), T - 1);
+        st.a = *(const uint4*)(x.qs + (size_t)tok * K + min(gi * 128 + (tid & 7) * 16, K - 16));
+        const size_t di = (size_t)min(4 * gi + ((tid >> 4) & 3), nbk - 1) * x.tld + min(t0 + 4 * (tid & 15), x.tld - 4);
+        st.d = *(const float4*)(x.d + di);
+    };
+    auto stage_store = [&](const Stg& st, int buf) {
+        *(uint4*)(s_a[buf] + (tid >> 3) * PF1_AST + (tid & 7) * 16) = st.a;
+        if (tid < 64) *(float4*)&s_d[buf][tid >> 4][4 * (tid & 15)] = st.d;
+    };
+    struct Blk {
+        uint32_t d[4];
+        uint2 q[4];
+    };
+    auto blk_load = [&](Blk& B, int gi) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint8_t* p = wr + (size_t)min(4 * gi + j, nbk - 1) * BSZ;
+            B.d[j] = lg_ld16(p);
+            if constexpr (WT == LG_Q8_0) {
+                B.q[j] = lg_ld<uint2>(p + 2 + 8 * g);
+            } else {
+                const uint32_t b8 = p[2 + g];
+                /* bit i -> byte i: +1 where set, -1 (0xFF) where clear */
+                B.q[j] = make_uint2(0xFFFFFFFFu ^ ((uint32_t)bits4_to_bytes(b8 & 15u) * 0xFEu),
+                                    0xFFFFFFFFu ^ ((uint32_t)bits4_to_bytes(b8 >> 4) * 0xFEu));
+            }
+        }
+    };
+
+    v4f acc[MI];
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) acc[mi] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int gi, const Blk& cur) {
+        const int buf = gi & 1;
+        const int8_t* sa = s_a[buf] + l16 * PF1_AST + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (4 * gi + j >= nbk) break;   /* the last group's missing blocks (uniform) */
+            const long bw = pf_u2l(cur.q[j]);
+            const float dw = lg_h2f((uint16_t)cur.d[j]);
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++) {
+                const long a = *(const long*)(sa + 16 * mi * PF1_AST + 32 * j);
+                const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bw, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                const float4 da = *(const float4*)&s_d[buf][j][16 * mi + 4 * g];
+                const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mi][i] = __builtin_fmaf(dw * dav[i], (float)is[i], acc[mi][i]);
+            }
+        }
+    };
+
+    Blk cur, nxt;
+    Stg st;
+    stage_load(st, 0);
+    blk_load(cur, 0);
+    stage_store(st, 0);
+    __syncthreads();
+    for (int gi = 0; gi < ng; gi++) {
+        const int gn = min(gi + 1, ng - 1);
+        stage_load(st, gn);
+        blk_load(nxt, gn);
+        compute(gi, cur);
+        stage_store(st, (gi + 1) & 1);
+        cur = nxt;
+        __syncthreads();
+    }
+    const int r = r0 + l16;
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 16 * mi + 4 * g + i;
+            if (t < T && r < R) {
+                float* o = out + (size_t)t * ldo + r;
+                *o = ACC ? *o + acc[mi][i] : acc[mi][i];
+            }
+        }
+    }
+}
+
+template <int WT>
+static int gemm_b32(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                    int accumulate, hipStream_t s)
+{
+    const int nrb8 = (rows + 127) / 128 + 7 & ~7;
+    const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
+    if (accumulate) hipLaunchKernelGGL((k_pf_gemm_b32<WT, 1>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    else hipLaunchKernelGGL((k_pf_gemm_b32<WT, 0>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
+    return lg_check_launch("prefill gemm (32-value blocks)");
+}
+
+int lg_prefill_act_type(int wtype)
+{
+    switch (wtype) {
+    case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: return LG_Q8_K;
+    case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: return LG_Q8_0;
+    default: return -1;
+    }
+}
+
+static int64_t pf_row_bytes(int wtype, int cols)
+{
+    switch (wtype) {
+    case LG_Q2_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q2_K;
+    case LG_Q3_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q3_K;
+    case LG_Q4_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q4_K;
+    case LG_Q5_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q5_K;
+    case LG_Q6_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q6_K;
+    case LG_Q8_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q8_0;
+    case LG_Q1_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q1_0;
+    case LG_Q1_G: return cols % 256 ? -1 : (int64_t)cols / 128 * LG_BS_Q1_G;   /* the Q1_G GEMM steps 256 values */
+    default: return -1;
+    }
+}
+
+int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out,
+                    int ldo, int accumulate, hipStream_t s)
+{
+    const int at = lg_prefill_act_type(wtype);
+    if (at < 0) {
+        lg_set_error("prefill gemm: weight type %d is not batched", wtype);
+        return LG_ERR_TYPE;
+    }
+    const int64_t rb = pf_row_bytes(wtype, cols);
+    if (!W || !out || !x.qs || !x.d || (at == LG_Q8_K && !x.bs) || (wtype == LG_Q1_G && !x.as) || rows <= 0 ||
+        cols < 32 || rb < 0 || rsz != (uint32_t)rb || T <= 0 || T > x.tld || x.tld % 4 || ldo < rows) {
+        lg_set_error("prefill gemm: bad arguments (type %d, rows %d, cols %d, row bytes %u, T %d)", wtype, rows, cols,
+                     rsz, T);
+        return LG_ERR_ARG;
+    }
+    switch (wtype) {
+    case LG_Q4_K: return gemm_q4k(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q1_G: return gemm_q1g(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q2_K: return gemm_kq<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q3_K: return gemm_kq<LG_Q3_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q5_K: return gemm_kq<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q6_K: return gemm_kq<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q8_0: return gemm_b32<LG_Q8_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    default: return gemm_b32<LG_Q1_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    }
 }
 
 /* ------------------------------------------------------------------ */
@@ -553,8 +1078,8 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
                                                             const uint16_t* __restrict__ vc, int pos0, int T,
                                                             float* __restrict__ att)
 {
-    static_assert(HD == 128, "eight 16-dim output tiles per wave");
-    constexpr int NT = 64 * NREP * SPLIT, NS = HD / 4, VST = HD + 16, OST = HD + 4;
+    static_assert(HD % 16 == 0 && HD <= 256, "16-dim output tiles");
+    constexpr int NT = 64 * NREP * SPLIT, NS = HD / 4, NTL = HD / 16, VST = HD + 16, OST = HD + 4;
     __shared__ __attribute__((aligned(16))) float s_kt[SPLIT][NS * 16 * 4];   /* K[key][4s + j] at (s*16 + key)*4 + j */
     __shared__ __attribute__((aligned(16))) float s_vt[SPLIT][16 * VST];      /* V[key][d] */
     __shared__ __attribute__((aligned(16))) float s_k32[16 * OST];    /* fp32 k / v of the block's 16 tokens */
@@ -581,9 +1106,9 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
         s_v32[tt * OST + d] = row[n_embed + kv_dim + g * HD + d];
     }
 
-    v4f o[8];
+    v4f o[NTL];
 #pragma unroll
-    for (int t = 0; t < 8; t++) o[t] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NTL; t++) o[t] = (v4f){0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;   /* l: this lane group's keys only, summed at the end */
     const int nkb = last / 16 + 1, nit = (nkb + SPLIT - 1) / SPLIT;
     /* SPLIT key blocks per step, block SPLIT*it + h for the waves of half h;
@@ -693,7 +1218,7 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
             b[3] = __uint_as_float(y23[1]);
         }
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
+        for (int t = 0; t < NTL; t++) {
             o[t] *= alpha;
 #pragma unroll
             for (int mm = 0; mm < 4; mm++)
@@ -702,7 +1227,7 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
         }
         if (diag && own >= 0 && own < 16) {
 #pragma unroll
-            for (int t = 0; t < 8; t++)
+            for (int t = 0; t < NTL; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int d = 16 * t + 4 * grp + i;
@@ -712,12 +1237,12 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
     }
     if constexpr (SPLIT == 2) {
         /* the second half's (m, l, o) into the first half's lanes */
-        __shared__ float s_x[NREP][2 + 32][64];
+        __shared__ float s_x[NREP][2 + 4 * NTL][64];
         if (half == 1) {
             s_x[r][0][lane] = m;
             s_x[r][1][lane] = l;
 #pragma unroll
-            for (int t = 0; t < 8; t++)
+            for (int t = 0; t < NTL; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) s_x[r][2 + 4 * t + i][lane] = o[t][i];
         }
@@ -727,7 +1252,7 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
         const float a0 = __builtin_amdgcn_exp2f(m - mx), a1 = __builtin_amdgcn_exp2f(m1 - mx);
         l = lg_fma2(l, a0, s_x[r][1][lane], a1);
 #pragma unroll
-        for (int t = 0; t < 8; t++)
+        for (int t = 0; t < NTL; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) o[t][i] = lg_fma2(o[t][i], a0, s_x[r][2 + 4 * t + i][lane], a1);
     }
@@ -736,32 +1261,73 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
     if (tq < T) {
         float* out = att + (size_t)tq * n_embed + (size_t)(g * NREP + r) * HD;
 #pragma unroll
-        for (int t = 0; t < 8; t++)
+        for (int t = 0; t < NTL; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) out[16 * t + 4 * grp + i] = o[t][i] / l;
     }
+}
+
+int lg_prefill_attn_supported(int head_dim, int nrep)
+{
+    return (head_dim == 48 || head_dim == 64 || head_dim == 128) && (nrep == 1 || nrep == 2 || nrep == 4 || nrep == 8);
 }
 
 static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_t* kc, const uint16_t* vc, int T,
                        int pos0, float* att, hipStream_t s)
 {
     const int nrep = M.n_heads / M.n_kv;
-    if (M.head_dim != 128) { lg_set_error("prefill attention: head_dim %d", M.head_dim); return LG_ERR_TYPE; }
+    if (!lg_prefill_attn_supported(M.head_dim, nrep)) {
+        lg_set_error("prefill attention: head_dim %d with %d query heads per KV head", M.head_dim, nrep);
+        return LG_ERR_TYPE;
+    }
     const dim3 grid((T + 15) / 16, M.n_kv);
     /* two halves of the key blocks per query head up to 4 query heads per
      * KV head (8 waves); one at 8 (8 waves already) */
-#define PFA(NR)                                                                                             \
-    hipLaunchKernelGGL((k_pf_attn_mfma<128, NR, (NR <= 4 ? 2 : 1)>), grid, dim3(64 * NR * (NR <= 4 ? 2 : 1)), 0, s, \
+#define PFA(HD, NR)                                                                                          \
+    hipLaunchKernelGGL((k_pf_attn_mfma<HD, NR, (NR <= 4 ? 2 : 1)>), grid, dim3(64 * NR * (NR <= 4 ? 2 : 1)), 0, s, \
                        qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, T, att)
-    switch (nrep) {
-    case 1: PFA(1); break;
-    case 2: PFA(2); break;
-    case 4: PFA(4); break;
-    case 8: PFA(8); break;
-    default: lg_set_error("prefill attention: %d query heads per KV head", nrep); return LG_ERR_TYPE;
+#define PFA_HD(HD)                    \
+    switch (nrep) {                   \
+    case 1: PFA(HD, 1); break;        \
+    case 2: PFA(HD, 2); break;        \
+    case 4: PFA(HD, 4); break;        \
+    default: PFA(HD, 8); break;       \
     }
+    switch (M.head_dim) {
+    case 48: PFA_HD(48); break;
+    case 64: PFA_HD(64); break;
+    default: PFA_HD(128); break;
+    }
+#undef PFA_HD
 #undef PFA
     return lg_check_launch("prefill attention");
+}
+
+/* one pass's quantized activation of every token into the trace, as the
+ * reference's blocks (block_q8_K: d, qs[256], bsums[16]; block_q8_0: fp16 d,
+ * qs[32]): block b of token t */
+template <int QT>
+__global__ __launch_bounds__(64) void k_pf_trace(PfQ8K q, int n, uint8_t* __restrict__ tr, size_t tok_stride)
+{
+    const int b = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    constexpr int QK = QT == LG_Q8_K ? 256 : 32, BS = QT == LG_Q8_K ? LG_BS_Q8_K : LG_BS_Q8_0;
+    uint8_t* o = tr + (size_t)t * tok_stride + (size_t)b * BS;
+    const int8_t* qs = q.qs + (size_t)t * n + (size_t)b * QK;
+    const int off = QT == LG_Q8_K ? 4 : 2;
+    for (int i = lane; i < QK; i += 64) o[off + i] = (uint8_t)qs[i];
+    if (QT == LG_Q8_K) {
+        if (lane < 16) {
+            const int16_t v = q.bs[((size_t)t * (n >> 8) + b) * 16 + lane];
+            __builtin_memcpy(o + 260 + 2 * lane, &v, 2);
+        }
+        if (lane == 0) {
+            const float d = q.d[(size_t)b * q.tld + t];
+            __builtin_memcpy(o, &d, 4);
+        }
+    } else if (lane == 0) {
+        const uint16_t dh = lg_f2h(q.d[(size_t)b * q.tld + t]);
+        __builtin_memcpy(o, &dh, 2);
+    }
 }
 
 int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream_t s)
@@ -771,11 +1337,26 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
         return LG_ERR_STATE;
     }
     const int ne = M.n_embed, kvd = M.kv_dim, qs = ne + 2 * kvd, nff = M.n_ff;
-    const bool q1 = M.wtype == LG_Q1_G;
-    const int qt = q1 ? LG_Q8_0 : LG_Q8_K;
-    auto gemm = [&](const uint8_t* W, uint32_t rsz, int rows, int cols, float* o, int ldo, int acc) {
-        return q1 ? lg_prefill_gemm_q1g(W, rsz, rows, cols, B.q, T, o, ldo, acc, s)
-                  : lg_prefill_gemm_q4k(W, rsz, rows, cols, B.q, T, o, ldo, acc, s);
+    const size_t tstride = (size_t)(4 * M.n_layers + 1) * B.trace_stride;
+    /* activation forms the matrices take: bit 0 Q8_K, bit 1 Q8_0 */
+    auto fam = [](const PfMat& W) { return lg_prefill_act_type(W.type) == LG_Q8_K ? 1 : 2; };
+    auto trace = [&](int f, int n, int k) -> int {
+        if (!B.trace) return LG_OK;
+        uint8_t* tr = B.trace + (size_t)k * B.trace_stride;
+        if (f & 1) hipLaunchKernelGGL(k_pf_trace<LG_Q8_K>, dim3(n / 256, T), dim3(64), 0, s, B.qk, n, tr, tstride);
+        else hipLaunchKernelGGL(k_pf_trace<LG_Q8_0>, dim3(n / 32, T), dim3(64), 0, s, B.q0, n, tr, tstride);
+        return lg_check_launch("prefill trace");
+    };
+    /* rmsnorm (w) and quantization of T rows of x in each form f asks for;
+     * the trace records the Q8_K form when both are made, as a step does */
+    auto quant = [&](int f, const float* x, const float* w, int n, int k) -> int {
+        int rc;
+        if ((f & 1) && (rc = lg_prefill_quantize(LG_Q8_K, x, n, w, M.eps, n, T, B.qk, s))) return rc;
+        if ((f & 2) && (rc = lg_prefill_quantize(LG_Q8_0, x, n, w, M.eps, n, T, B.q0, s))) return rc;
+        return trace(f, n, k);
+    };
+    auto gemm = [&](const PfMat& W, int cols, float* o, int ldo, int acc) {
+        return lg_prefill_gemm(W.type, W.w, W.rsz, W.rows, cols, fam(W) == 1 ? B.qk : B.q0, T, o, ldo, acc, s);
     };
     int rc;
     hipLaunchKernelGGL(k_pf_embed, dim3(T), dim3(256), 0, s, M.embd_t, M.embd, M.embd_rsz, B.toks, ne, B.x);
@@ -785,22 +1366,38 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
         uint16_t* kc = M.kc + (size_t)l * M.n_ctx * kvd;
         uint16_t* vc = M.vc + (size_t)l * M.n_ctx * kvd;
         /* attention branch */
-        if ((rc = lg_prefill_quantize(qt, B.x, ne, L.att_norm, M.eps, ne, T, B.q, s))) return rc;
-        if ((rc = gemm(L.qkv, L.qkv_rsz, qs, ne, B.qkv, qs, 0))) return rc;
+        const int f_qkv = L.qkv_fused ? fam(L.qkv) : fam(L.q) | fam(L.k) | fam(L.v);
+        if ((rc = quant(f_qkv, B.x, L.att_norm, ne, 4 * l))) return rc;
+        if (L.qkv_fused) {
+            if ((rc = gemm(L.qkv, ne, B.qkv, qs, 0))) return rc;
+        } else {
+            if ((rc = gemm(L.q, ne, B.qkv, qs, 0))) return rc;
+            if ((rc = gemm(L.k, ne, B.qkv + ne, qs, 0))) return rc;
+            if ((rc = gemm(L.v, ne, B.qkv + ne + kvd, qs, 0))) return rc;
+        }
         const int waves = M.n_heads + M.n_kv;
         hipLaunchKernelGGL(k_pf_qk_rope_kv, dim3((waves + 3) / 4, T), dim3(256), 0, s, B.qkv, qs, ne, kvd, L.q_norm,
                            L.k_norm, M.n_heads, M.n_kv, M.head_dim, M.rope_dim, pos0, M.rope_freq, M.eps, kc, vc);
         if ((rc = lg_check_launch("prefill qk-norm/rope/kv"))) return rc;
         if ((rc = launch_attn(M, B.qkv, qs, kc, vc, T, pos0, B.att, s))) return rc;
-        if ((rc = lg_prefill_quantize(qt, B.att, ne, nullptr, M.eps, ne, T, B.q, s))) return rc;
-        if ((rc = gemm(L.ao, L.ao_rsz, ne, ne, B.x, ne, 1))) return rc;
+        if ((rc = quant(fam(L.ao), B.att, nullptr, ne, 4 * l + 1))) return rc;
+        if ((rc = gemm(L.ao, ne, B.x, ne, 1))) return rc;
         /* FFN branch */
-        if ((rc = lg_prefill_quantize(qt, B.x, ne, L.ffn_norm, M.eps, ne, T, B.q, s))) return rc;
-        if ((rc = gemm(L.ug, L.ug_rsz, 2 * nff, ne, B.ug, 2 * nff, 0))) return rc;
-        if (q1) hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_0>, dim3(nff / 256, T), dim3(64), 0, s, B.ug, nff, B.q);
-        else hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_K>, dim3(nff / 256, T), dim3(64), 0, s, B.ug, nff, B.q);
+        const int f_ug = L.ug_fused ? fam(L.ug) : fam(L.up) | fam(L.gate);
+        if ((rc = quant(f_ug, B.x, L.ffn_norm, ne, 4 * l + 2))) return rc;
+        if (L.ug_fused) {
+            if ((rc = gemm(L.ug, ne, B.ug, 2 * nff, 0))) return rc;
+        } else {
+            if ((rc = gemm(L.up, ne, B.ug, 2 * nff, 0))) return rc;
+            if ((rc = gemm(L.gate, ne, B.ug + nff, 2 * nff, 0))) return rc;
+        }
+        const int f_d = fam(L.down);
+        const dim3 sg((nff + 255) / 256, T);
+        if (f_d == 1) hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_K>, sg, dim3(64), 0, s, B.ug, nff, B.qk);
+        else hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_0>, sg, dim3(64), 0, s, B.ug, nff, B.q0);
         if ((rc = lg_check_launch("prefill swiglu"))) return rc;
-        if ((rc = gemm(L.down, L.down_rsz, ne, nff, B.x, ne, 1))) return rc;
+        if ((rc = trace(f_d, nff, 4 * l + 3))) return rc;
+        if ((rc = gemm(L.down, nff, B.x, ne, 1))) return rc;
     }
     return LG_OK;
 }

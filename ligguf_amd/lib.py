@@ -83,6 +83,7 @@ SIGNATURES = {
     "lg_trace_next_step": (C.c_int, [_vp, _vp]),
     "lg_trace_size": (C.c_size_t, [_vp]),
     "lg_trace_acts_next_step": (C.c_int, [_vp, _vp]),
+    "lg_trace_acts_next_prefill": (C.c_int, [_vp, _vp]),
     "lg_trace_acts_size": (C.c_size_t, [_vp]),
     "lg_time_fused_phase": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "lg_prefill": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),

@@ -44,6 +44,13 @@ class ModelConfig:
     sigma: float = 0.02
     q1_direct: bool = False   # 1-bit layers drawn as Bernoulli signs + |N(0,sigma)| scales
     seed: int = 1234
+    # per-tensor types that replace layer_type in every layer, e.g.
+    # (("attn_v", Q6_K), ("ffn_down", Q6_K)) for a Q4_K_M-style mix
+    overrides: tuple = ()
+
+    def tensor_type(self, tensor: str) -> int:
+        """The type of layer tensor `tensor` ("attn_q" .. "ffn_down")."""
+        return dict(self.overrides).get(tensor, self.layer_type)
 
     @property
     def kv_dim(self) -> int:
@@ -137,7 +144,7 @@ class HostModel:
                   "ffn_up": (ff, ne), "ffn_gate": (ff, ne), "ffn_down": (ne, ff)}
         for l in range(cfg.n_layers):
             for t in LAYER_TENSORS:
-                draw(f"blk.{l}.{t}.weight", cfg.layer_type, *shapes[t])
+                draw(f"blk.{l}.{t}.weight", cfg.tensor_type(t), *shapes[t])
             m.norms[f"blk.{l}.attn_norm.weight"] = np.ones(ne, np.float32)
             m.norms[f"blk.{l}.ffn_norm.weight"] = np.ones(ne, np.float32)
             if cfg.arch == ARCH_QWEN3:
@@ -315,6 +322,20 @@ class Engine:
         check(self.lib.lg_trace_acts_next_step(self.ctx, C.c_void_p(buf.data_ptr())), self.ctx)
         logits = self.decode(tok, pos)
         tr = buf.cpu().numpy().reshape(4 * self.cfg.n_layers + 1, -1)
+        return logits, tr
+
+    def prefill_traced(self, toks, pos0: int = 0):
+        """lg_prefill with lg_trace_acts_next_prefill: (logits, [n][4L+1][stride]
+        uint8 quantized activations of every token; the output head's slot
+        for the last token only).  The prompt must run batched."""
+        import torch
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        n1 = int(self.lib.lg_trace_acts_size(self.ctx))
+        buf = torch.zeros(len(toks) * n1, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        check(self.lib.lg_trace_acts_next_prefill(self.ctx, C.c_void_p(buf.data_ptr())), self.ctx)
+        logits = self.prefill(toks, pos0)
+        tr = buf.cpu().numpy().reshape(len(toks), 4 * self.cfg.n_layers + 1, -1)
         return logits, tr
 
     def state_save(self, path: str, pos: int) -> None:

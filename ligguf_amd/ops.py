@@ -51,7 +51,8 @@ def matvec(t: int, w: torch.Tensor, rsz: int, n: int, d: int, xq: torch.Tensor, 
 
 
 def matmul_tokens(t: int, w: torch.Tensor, rsz: int, n: int, d: int, x: torch.Tensor) -> torch.Tensor:
-    """lg_matmul_tokens: x [T, n] fp32 -> [T, d], each row quantized to Q8_K."""
+    """lg_matmul_tokens: x [T, n] fp32 -> [T, d], each row quantized to the
+    activation form of weight type t (Q8_K for the K-quants, else Q8_0)."""
     T = x.shape[0]
     out = torch.empty((T, d), dtype=torch.float32, device=w.device)
     check(load().lg_matmul_tokens(t, _p(w), rsz, n, d, _p(x), T, _p(out), _stream()))

@@ -38,6 +38,13 @@ FLIP_TOL = 0.05
 # the block shifts with it, so several flips can share one block (9 of 768
 # seen on the tiny model); a fraction of the width bounds them
 MAX_FLIP_FRAC = 0.02
+# values this close to a boundary are ties at fp32 resolution (|v| <= 127.5,
+# so fp32 rounding alone moves v by ~1e-5): any reordering rounds them either
+# way, and they do not count against MAX_FLIP_FRAC.  Quantized tables make
+# many: a Q6_K embedding row is integers times per-16 scales, so values of
+# the block holding the maximum scale to exact halves (127 q / 32 for q = 16)
+# -- 60-80 of 1024 per token on the synthetic Q6_K models.
+TIE_TOL = 1e-4
 # logits rel-L2 of a step whose int8 activations all agree with the oracle's
 EXACT_STEP = 1e-5
 
@@ -47,16 +54,18 @@ K_FAMILY = {10, 11, 12, 13, 14}   # Q2_K..Q6_K read Q8_K activations
 def slot_formats(cfg):
     """(quantized form, width) of each of the 4 n_layers + 1 activations of a
     step, as lg_trace_acts_next_step records them (None: float activation)."""
-    def form(t):
-        if t in K_FAMILY:
+    def form(*types):
+        # the Q8_K form when any consumer is a K-quant, as the step records it
+        if any(t in K_FAMILY for t in types):
             return Q8_K
-        if t in (Q8_0, Q1_0, Q1_G):
+        if any(t in (Q8_0, Q1_0, Q1_G) for t in types):
             return Q8_0
         return None
+    tt = cfg.tensor_type
     out = []
     for _ in range(cfg.n_layers):
-        f = form(cfg.layer_type)
-        out += [(f, cfg.n_embed), (f, cfg.n_embed), (f, cfg.n_embed), (f, cfg.n_ff)]
+        out += [(form(tt("attn_q"), tt("attn_k"), tt("attn_v")), cfg.n_embed), (form(tt("attn_output")), cfg.n_embed),
+                (form(tt("ffn_up"), tt("ffn_gate")), cfg.n_embed), (form(tt("ffn_down")), cfg.n_ff)]
     out.append((form(cfg.out_type), cfg.n_embed))
     return out
 
@@ -117,7 +126,8 @@ def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
         if diff.size == 0:
             continue
         bad = []
-        if diff.size > max(8, int(MAX_FLIP_FRAC * n)):
+        nties = int(np.sum(boundary_dist(v[diff]) < TIE_TOL))
+        if diff.size - nties > max(8, int(MAX_FLIP_FRAC * n)):
             bad.append((k, -1, int(diff.size), n, 0.0, 1.0))
         for i in diff:
             step = abs(int(qg[i]) - int(qo[i]))
@@ -126,6 +136,50 @@ def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
                 bad.append((k, int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
         return k, bad
     return -1, []
+
+
+def prefill_flips(gpu_trace: np.ndarray, oracle_traces, cfg):
+    """The quantized activations of a batched prefill of n tokens against the
+    oracle's token-by-token run of the same prompt.
+
+    gpu_trace: [n][4L+1][stride] (lg_trace_acts_next_prefill); oracle_traces:
+    n arrays [4L+1][wide] (or_state_trace per step).  A pass computes
+    activation k of every token before activation k+1 of any, and token t's
+    activation k depends on activations < k of tokens <= t only (its own
+    stream and, through the KV rows, the earlier tokens').  So (token t,
+    activation k) is compared while no token <= t differed at an activation
+    < k; every difference found there must be a rounding flip as in
+    step_flips.  Returns (compared, differing, unexplained list, last token
+    clean through every activation)."""
+    fm = slot_formats(cfg)
+    n, nk = len(oracle_traces), len(fm)
+    first = np.full(n, nk + 1)          # first differing activation of each token
+    compared, differing, bad = 0, 0, []
+    for k in range(nk):
+        qt, w = fm[k]
+        if qt is None:
+            continue
+        toks = [n - 1] if k == nk - 1 else range(n)      # the output head's input: the last token only
+        for t in toks:
+            if first[:t + 1].min() < k:
+                continue
+            qg, _ = parse_q(gpu_trace[t][k], qt, w)
+            qo, v = quantize_ref(oracle_traces[t][k][:w], qt)
+            compared += 1
+            diff = np.nonzero(qg != qo)[0]
+            if diff.size == 0:
+                continue
+            differing += 1
+            first[t] = k
+            nties = int(np.sum(boundary_dist(v[diff]) < TIE_TOL))
+            if diff.size - nties > max(8, int(MAX_FLIP_FRAC * w)):
+                bad.append((t, k, -1, int(diff.size), w, 0.0, 1.0))
+            for i in diff:
+                step = abs(int(qg[i]) - int(qo[i]))
+                dist = float(boundary_dist(v[i:i + 1])[0])
+                if step != 1 or dist > FLIP_TOL:
+                    bad.append((t, k, int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
+    return compared, differing, bad, bool(first.min() > nk)
 
 
 def flip_summary(rows):
@@ -138,5 +192,6 @@ def flip_summary(rows):
            f"{flips} with rounding flips only, {bad} unexplained"
 
 
-__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "EXACT_STEP", "slot_formats", "parse_q", "quantize_ref", "step_flips", "flip_summary",
+__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "TIE_TOL", "EXACT_STEP", "slot_formats", "parse_q", "quantize_ref", "step_flips",
+           "prefill_flips", "flip_summary",
            "F16", "F32"]

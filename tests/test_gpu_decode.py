@@ -225,13 +225,22 @@ def test_tiny_decode_deterministic_and_async(tiny):
 
 
 def test_prefill_equals_sequential(tiny):
+    """Token by token the prefill is the step loop bit for bit; AUTO takes the
+    batched prefill on this config (test_gpu_prefill.py holds it to the
+    oracle activation by activation)."""
+    from ligguf_amd.lib import PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS
     hm, eng, g = tiny
     seq = [eng.decode(int(t), p) for p, t in enumerate(g["prompt"])][-1]
     k1, v1 = eng.kv_read(0, TINY.n_layers, 0, 16)
+    eng.set_prefill_path(PREFILL_STEPS)
     pre = eng.prefill(g["prompt"], 0)
     k2, v2 = eng.kv_read(0, TINY.n_layers, 0, 16)
+    eng.set_prefill_path(PREFILL_AUTO)
     assert np.array_equal(pre, seq)
     assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    assert eng.prefill_path() == PREFILL_BATCHED
+    bat = eng.prefill(g["prompt"], 0)
+    assert int(np.argmax(bat)) == int(np.argmax(seq))
 
 
 def test_kv_roundtrip_and_errors(tiny):

@@ -2,23 +2,25 @@
 against the oracle's matvec of every token, and lg_prefill with
 LG_PREFILL_BATCHED against the token-by-token prefill (LG_PREFILL_STEPS,
 itself bit-equal to sequential decode steps) and against the oracle, for
-Q4_K and Q1_G models.
+models of every quantized layer type the GEMMs take (Q2_K..Q6_K, Q8_0,
+Q1_0, Q1_G), a Q4_K_M-style mix and head_dim 48 / 64 / 128.
 
-The GEMMs reproduce the integer block sums of the reference's Q4_K x Q8_K
-and Q1_G x Q8_0 dots exactly (fast/lil_math.cpp:582-616, :440-464) and
-combine them in fp32 per block, so each output is held to the matvec bar:
-within 2e-6 of the row's sum of |terms|.  Whole prompts accumulate fp32 order differences over
-their tokens; an activation that lands on the other side of an int8 rounding
-boundary moves later logits by up to ~2e-2 (the same effect the decode tests
-document), so the prompt checks bound the logits and the KV cache loosely and
-require the greedy next token to agree."""
+The GEMMs reproduce the integer (sub-)block sums of the reference's dots
+exactly (fast/lil_math.cpp:411-739) and combine them in fp32 per block, so
+each output is held to the matvec bar: within 2e-6 of the row's sum of
+|terms|.  A whole prompt is held to the flip-explained bar
+(tests/parity.py, prefill_flips): every quantized activation of every token
+the pass builds before any difference can reach it equals the oracle's
+token-by-token value or differs by a rounding flip, and a prompt without
+any difference matches the oracle's logits to fp32 noise."""
 import numpy as np
 import pytest
 
 from ligguf_amd import encode, ops
-from ligguf_amd.lib import (PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS, Q1_G, Q4_K, Q5_K, Q6_K, Q8_0, LgError,
-                            row_size)
-from ligguf_amd.model import Engine, HostModel, ModelConfig
+from ligguf_amd.lib import (F16, PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS,
+                            Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, TYPE_NAMES, LgError, row_size)
+from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
+from parity import EXACT_STEP, prefill_flips
 from test_gpu_decode import oracle_state, rel
 from test_gpu_ops import MATVEC_TOL, dev, host
 
@@ -56,11 +58,38 @@ def test_matmul_tokens_q1g_vs_oracle(gpu, oracle, d, n, T):
         assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
 
 
+GEMM_CASES = [(t, d, n, T) for t in (Q2_K, Q3_K, Q5_K, Q6_K)
+              for d, n, T in [(200, 512, 37), (130, 256, 1), (4096, 4096, 64)]] + \
+             [(t, d, n, T) for t in (Q8_0, Q1_0)
+              for d, n, T in [(200, 288, 37), (130, 32, 1), (100, 1376, 70), (4096, 4096, 64)]]
+
+
+@pytest.mark.parametrize("wt,d,n,T", GEMM_CASES,
+                         ids=[f"{TYPE_NAMES[t]}-{d}x{n}-T{T}" for t, d, n, T in GEMM_CASES])
+def test_matmul_tokens_types_vs_oracle(gpu, oracle, wt, d, n, T):
+    """The K-quant GEMM (one int8 MFMA per 16- or 32-value sub-block, the
+    sub-block scales in int32) and the Q8_0 / Q1_0 GEMM (one per 32-value
+    block, widths any multiple of 32) against the oracle's matvec of each
+    token's quantized activation."""
+    rng = np.random.default_rng(d + n + T + wt)
+    w = encode.random_tensor(wt, d + n + wt, wt, d, n)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    rsz = row_size(wt, n)
+    y = host(ops.matmul_tokens(wt, dev(w, gpu), rsz, n, d, dev(x, gpu)))
+    kq = wt in (Q2_K, Q3_K, Q5_K, Q6_K)
+    toks = range(T) if T <= 40 else rng.choice(T, 12, replace=False)
+    for t in toks:
+        xq = oracle.quantize_q8_K(x[t]) if kq else oracle.quantize_q8_0(x[t])
+        ref, ab = oracle.matvec_q(wt, w, rsz, n, d, xq, want_abs=True)
+        err = np.abs(y[t] - ref) / np.maximum(ab, 1e-30)
+        assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
+
+
 def test_matmul_tokens_rejects_other_types(gpu):
     x = dev(np.zeros((2, 256), np.float32), gpu)
-    w = dev(np.zeros(row_size(Q6_K, 256) * 4, np.uint8), gpu)
+    w = dev(np.zeros(row_size(F16, 256) * 4, np.uint8), gpu)
     with pytest.raises(LgError):
-        ops.matmul_tokens(Q6_K, w, row_size(Q6_K, 256), 256, 4, x)
+        ops.matmul_tokens(F16, w, row_size(F16, 256), 256, 4, x)
 
 
 BATCHED_MODELS = [
@@ -71,6 +100,21 @@ BATCHED_MODELS = [
     ModelConfig("llama-w4096-q4k-nrep8", 0, 1, 4096, 32, 4, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q4_K, Q6_K),
     # Q1_G layers (Q1_G x Q8_0 GEMM), Q8_0 embedding and output
     ModelConfig("qwen3-w4096-q1g", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q1_G, Q8_0, Q8_0),
+    # the tiny parity config: Q8_0 throughout, width 288 (no multiple of 256), head_dim 48
+    TINY.with_(name="tiny-q8_0-hd48", n_context=1024),
+    # Q4_K_M-style: Q6_K attn_v and ffn_down among Q4_K matrices (Q|K|V not stacked), head_dim 64
+    ModelConfig("llama-w2048-q4k_m-hd64", 0, 2, 2048, 32, 8, 64, 5632, 1024, 1024, 1e4, 1e-5, Q4_K, Q4_K, Q6_K,
+                overrides=(("attn_v", Q6_K), ("ffn_down", Q6_K))),
+    # one K-quant type throughout each (a Q4_K embedding: a Q6_K one puts 60-80 of every 1024 first
+    # activations on exact rounding ties, which end the flip walk at its first activation)
+    ModelConfig("qwen3-w1024-q6k", 1, 2, 1024, 16, 8, 64, 2816, 1024, 1024, 1e6, 1e-6, Q6_K, Q4_K, Q6_K),
+    ModelConfig("llama-w1024-q5k", 0, 2, 1024, 8, 8, 128, 2816, 1024, 1024, 1e4, 1e-5, Q5_K, Q5_K, Q6_K),
+    ModelConfig("llama-w1024-q3k", 0, 2, 1024, 16, 4, 64, 2816, 1024, 1024, 1e4, 1e-5, Q3_K, Q4_K, Q6_K),
+    ModelConfig("llama-w1024-q2k", 0, 2, 1024, 16, 4, 64, 2816, 1024, 1024, 1e4, 1e-5, Q2_K, Q4_K, Q6_K),
+    # Q1_0 layers, and a mix of the two activation forms (Q8_0 ffn_down under Q4_K up|gate)
+    ModelConfig("llama-w1024-q1_0", 0, 2, 1024, 16, 16, 64, 2816, 1024, 1024, 1e4, 1e-5, Q1_0, Q8_0, Q8_0),
+    ModelConfig("qwen3-w1024-q4k-q8down", 1, 2, 1024, 8, 2, 128, 2816, 1024, 1024, 1e6, 1e-6, Q4_K, Q4_K, Q8_0,
+                overrides=(("ffn_down", Q8_0), ("attn_output", Q8_0))),
 ]
 
 
@@ -180,8 +224,34 @@ def test_batched_prefill_in_several_passes(pf_model):
     assert near_best(lg_s, tok_b)
 
 
+def test_batched_prefill_flips_explained(pf_model, oracle):
+    """Every quantized activation of a 24-token batched prefill against the
+    oracle's token-by-token run (prefill_flips): no difference that is not a
+    rounding flip, and the last token's logits to fp32 noise when no
+    difference reached it, within a flip's reach otherwise."""
+    hm, eng = pf_model
+    cfg = hm.cfg
+    prompt = np.random.default_rng(77).integers(1, cfg.vocab, 24)
+    st = oracle_state(oracle, hm)
+    otr = []
+    for t in prompt:
+        ref, tr = oracle.inference_traced(st, int(t), cfg)
+        otr.append(tr)
+    oracle.free_state(st)
+    eng.set_prefill_path(PREFILL_BATCHED)
+    lg_b, gtr = eng.prefill_traced(prompt)
+    compared, differing, bad, clean = prefill_flips(gtr, otr, cfg)
+    e = rel(lg_b, ref)
+    print(f"\n{cfg.name}: {compared} token activations compared, {differing} with rounding flips, "
+          f"{len(bad)} unexplained; last token {'clean' if clean else 'after a flip'}; logits vs oracle {e:.2e}")
+    assert not bad, bad[:5]
+    assert compared >= 4 * cfg.n_layers + 1                 # at least the first token all the way
+    assert e <= (EXACT_STEP if clean else 5e-2)
+    assert near_best(ref, int(np.argmax(lg_b)))
+
+
 def test_batched_prefill_unavailable_for_other_types(gpu):
-    cfg = ModelConfig("llama-w4096-q5k", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q5_K, Q8_0, Q4_K)
+    cfg = ModelConfig("llama-w1024-f16", 0, 1, 1024, 8, 8, 128, 2816, 1024, 1024, 1e4, 1e-5, F16, Q8_0, Q4_K)
     hm = HostModel.synthetic(cfg)
     eng = Engine(0)
     eng.load(hm)
@@ -189,7 +259,6 @@ def test_batched_prefill_unavailable_for_other_types(gpu):
         assert eng.prefill_path() == PREFILL_STEPS
         with pytest.raises(LgError):
             eng.set_prefill_path(PREFILL_BATCHED)
-        eng.set_path(PATH_FUSED)
         lg = eng.prefill(np.arange(1, 9), 0)       # AUTO falls back to steps
         assert np.all(np.isfinite(lg))
     finally:

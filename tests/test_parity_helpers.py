@@ -8,7 +8,7 @@ import numpy as np
 from conftest import golden
 from ligguf_amd.lib import Q8_0, Q8_K
 from ligguf_amd.model import TINY
-from parity import boundary_dist, parse_q, quantize_ref, slot_formats, step_flips
+from parity import boundary_dist, parse_q, prefill_flips, quantize_ref, slot_formats, step_flips
 
 
 def _vectors():
@@ -53,3 +53,92 @@ def test_step_flips_reports_planted_differences(oracle):
     gt[2][blk * 34 + 2 + j] = np.uint8((int(gt[2][blk * 34 + 2 + j].view(np.int8)) + 1) & 255)
     first, bad = step_flips(gt, ot, cfg)
     assert first == 2 and len(bad) == 1 and bad[0][1] == i
+
+
+def _prefill_traces(oracle, cfg, n, seed):
+    rng = np.random.default_rng(seed)
+    wide = max(cfg.n_embed, cfg.n_ff)
+    nk = 4 * cfg.n_layers + 1
+    ots = [(rng.standard_normal((nk, wide)) * 0.5).astype(np.float32) for _ in range(n)]
+    gt = np.zeros((n, nk, 1024), np.uint8)
+    for t in range(n):
+        for k, (qt, w) in enumerate(slot_formats(cfg)):
+            b = oracle.quantize_q8_0(ots[t][k][:w])
+            gt[t, k, :b.size] = b
+    return gt, ots
+
+
+def _bump(gt, t, k, i):
+    blk, j = divmod(i, 32)
+    gt[t, k, blk * 34 + 2 + j] = np.uint8((int(gt[t, k, blk * 34 + 2 + j].view(np.int8)) + 1) & 255)
+
+
+def test_prefill_flips_walk(oracle):
+    """The causal walk of prefill_flips: a difference at (token t, activation
+    k) stops the comparisons of tokens >= t past k, not those of earlier
+    tokens; an off-boundary one is reported, a near-boundary one is a flip."""
+    cfg = TINY.with_(n_layers=2)
+    n, nk = 4, 9
+    gt, ots = _prefill_traces(oracle, cfg, n, 8)
+    full = n * (nk - 1) + 1
+    assert prefill_flips(gt, ots, cfg) == (full, 0, [], True)
+    # an off-boundary one-step change at token 2, activation 1
+    _, v = quantize_ref(ots[2][1][:cfg.n_embed], Q8_0)
+    far = int(np.argmax(boundary_dist(v)))
+    g2 = gt.copy()
+    _bump(g2, 2, 1, far)
+    compared, differing, bad, clean = prefill_flips(g2, ots, cfg)
+    assert differing == 1 and len(bad) == 1 and bad[0][:3] == (2, 1, far) and not clean
+    # tokens 2, 3 stop after activation 1; tokens 0, 1 run to the end
+    assert compared == full - 2 * (nk - 3) - 1
+    # a value planted on a rounding boundary differing by one step is a flip
+    g3 = gt.copy()
+    x = ots[0][3][:cfg.n_embed].copy()
+    amax = np.abs(x[:32]).max()
+    x[5] = np.float32((10.5 / 127.0) * amax)             # v = 10.5 exactly: roundf gives 11
+    ots3 = [o.copy() for o in ots]
+    ots3[0][3][:cfg.n_embed] = x
+    b = oracle.quantize_q8_0(x)
+    g3[0, 3, :b.size] = b
+    g3[0, 3, 2 + 5] = np.uint8(10)                       # the other side of the boundary
+    compared, differing, bad, clean = prefill_flips(g3, ots3, cfg)
+    assert differing == 1 and bad == [] and not clean
+    assert compared == full - n * (nk - 5) - 1
+
+
+def test_ties_do_not_count_against_the_cap(oracle):
+    """Values on exact halves (as a Q6_K embedding makes them) may all round
+    either way; flips at larger boundary distances stay capped."""
+    cfg = TINY.with_(n_layers=1)
+    n = cfg.n_embed
+    rng = np.random.default_rng(4)
+    x = np.clip(rng.standard_normal(n) * 0.3, -0.9, 0.9).astype(np.float32)
+    x[0::32] = 1.0                                           # each block's maximum
+    ties = [b * 32 + j for b in range(n // 32) for j in (3, 7, 11)]
+    x[ties] = np.float32(63.5 / 127.0)                        # v = 63.5: a tie, roundf gives 64
+    ot = np.zeros((4 * cfg.n_layers + 1, max(n, cfg.n_ff)), np.float32)
+    ot[0][:n] = x
+    gt = np.zeros((4 * cfg.n_layers + 1, 1024), np.uint8)
+    for k, (qt, w) in enumerate(slot_formats(cfg)):
+        b = oracle.quantize_q8_0(ot[k][:w])
+        gt[k][:b.size] = b
+    _, v = quantize_ref(x, Q8_0)
+    assert np.all(boundary_dist(v[ties]) < 1e-4) and len(ties) > 20
+    g = gt.copy()
+    for i in ties:
+        blk, j = divmod(i, 32)
+        g[0][blk * 34 + 2 + j] = np.uint8(63)
+    assert step_flips(g, ot, cfg) == (0, [])
+    # the same number of one-step changes at distance ~0.01 exceed the cap
+    x2 = x.copy()
+    x2[ties] = np.float32(63.49 / 127.0)
+    ot2 = ot.copy()
+    ot2[0][:n] = x2
+    g2 = gt.copy()
+    b = oracle.quantize_q8_0(x2)
+    g2[0][:b.size] = b
+    for i in ties:
+        blk, j = divmod(i, 32)
+        g2[0][blk * 34 + 2 + j] = np.uint8(64)
+    first, bad = step_flips(g2, ot2, cfg)
+    assert first == 0 and bad and bad[0][1] == -1
