@@ -524,6 +524,9 @@ def main() -> int:
                     help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill: the prompt twice, the second timed (for MFMA counter runs)")
+    ap.add_argument("--layer-type", default="Q4_K",
+                    help="with --prefill-only: the layer matrices' type (Q2_K..Q6_K, Q8_0, Q1_0, Q1_G; "
+                         "Q4_K_M: Q4_K with Q6_K attn_v and ffn_down)")
     ap.add_argument("--q1g-only", action="store_true",
                     help="run only the Q1_G long-context workload and print its line (profiling)")
     ap.add_argument("--q1g-ctx", type=int, default=8192, help="prompt length of the Q1_G workload")
@@ -561,6 +564,12 @@ def main() -> int:
         return 0
 
     if args.prefill_only:
+        from ligguf_amd.lib import TYPE_NAMES, Q4_K, Q6_K
+        if args.layer_type == "Q4_K_M":
+            cfg = cfg.with_(name=cfg.name + "_m", overrides=(("attn_v", Q6_K), ("ffn_down", Q6_K)))
+        elif args.layer_type != "Q4_K":
+            lt = {v: k for k, v in TYPE_NAMES.items()}[args.layer_type]
+            cfg = cfg.with_(name=cfg.name.replace("q4_k", args.layer_type.lower()), layer_type=lt)
         hm = HostModel.synthetic(cfg)
         eng = Engine(0)
         eng.load(hm)
@@ -571,6 +580,7 @@ def main() -> int:
         eng.prefill(prompt, 0)
         seconds = time.perf_counter() - t0
         rep = prefill_report(cfg, args.prefill, seconds, eng.prefill_path())
+        rep["model"] = cfg.name
         eng.close()
         print(json.dumps({"prefill": rep}), flush=True)
         return 0

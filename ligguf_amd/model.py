@@ -69,9 +69,11 @@ class ModelConfig:
         """Bytes read per decode token: every layer weight, the output head,
         the norms and one embedding row."""
         ne, kv, ff = self.n_embed, self.kv_dim, self.n_ff
-        lt = self.layer_type
-        per_layer = (ne * row_size(lt, ne) + 2 * kv * row_size(lt, ne) + ne * row_size(lt, ne) +
-                     2 * ff * row_size(lt, ne) + ne * row_size(lt, ff) + 2 * ne * 4)
+        tt = self.tensor_type
+        per_layer = (ne * row_size(tt("attn_q"), ne) + kv * row_size(tt("attn_k"), ne) +
+                     kv * row_size(tt("attn_v"), ne) + ne * row_size(tt("attn_output"), ne) +
+                     ff * row_size(tt("ffn_up"), ne) + ff * row_size(tt("ffn_gate"), ne) +
+                     ne * row_size(tt("ffn_down"), ff) + 2 * ne * 4)
         if self.arch == ARCH_QWEN3:
             per_layer += 2 * self.head_dim * 4
         return (self.n_layers * per_layer + self.vocab * row_size(self.out_type, ne) + ne * 4 +
