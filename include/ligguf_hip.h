@@ -219,11 +219,11 @@ int lg_prefill(lg_ctx* ctx, const int* toks, int n, int pos0, float* logits_host
  * each weight matrix read once per pass and multiplied by all of them with
  * int8 MFMA GEMMs, the tokens' integer sub-block sums and quantizers those
  * of the step; the logits then match n sequential steps to fp32 rounding (an
- * int8 rounding of an activation may differ in rare tokens).  Needs
- * quantized layer matrices -- Q2_K..Q6_K, Q8_0, Q1_0 or Q1_G, in any mix
- * (a Q4_K_M-style model with Q6_K matrices among its Q4_K ones included) --
- * and head_dim 48, 64 or 128 with 1, 2, 4 or 8 query heads per KV head;
- * F32/F16 layer matrices prefill token by token.  STEPS: one
+ * int8 rounding of an activation may differ in rare tokens).  Takes every
+ * layer type -- Q2_K..Q6_K, Q8_0, Q1_0, Q1_G on int8 MFMA, F32/F16 on fp32
+ * MFMA, in any mix (a Q4_K_M-style model with Q6_K matrices among its Q4_K
+ * ones included) -- and needs head_dim 48, 64 or 128 with 1, 2, 4 or 8 query
+ * heads per KV head.  STEPS: one
  * decode step per token, bit-equal to n lg_decode_step calls.  AUTO (the
  * default): BATCHED when the model allows it and n >= 2, else STEPS.
  * lg_prefill_path reports what a prompt of 2+ tokens takes (-1 without a
@@ -284,8 +284,9 @@ int lg_matvec(int type, const void* w, uint32_t rsz, int n, int d, const void* x
  * out[t*d + r] = row r of w . Q(x[t*n ..]) for t < T, r < d, each fp32 row
  * of x quantized as quantize_q8_K (K-quant weights, n % 256 == 0) or
  * quantize_q8_0 (Q8_0, Q1_0, Q1_G weights; n % 32 == 0, n % 256 for Q1_G)
- * does.  The integer block sums are those of lg_matvec (the dot products of
- * fast/lil_math.cpp:411-739); only the fp32 accumulation order differs.  Allocates and frees a workspace of
+ * does, or taken as fp32 (F32/F16 weights, n % 32 == 0, on fp32 MFMA).  The
+ * integer block sums are those of lg_matvec (the dot products of
+ * fast/lil_math.cpp:397-739); only the fp32 accumulation order differs.  Allocates and frees a workspace of
  * about 1.3*T*n bytes and synchronizes `stream` (tests and benches).  No
  * counterpart in the reference, which calls matmul per token. */
 int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, int d, const float* x, int T, float* out,

@@ -38,6 +38,7 @@
 #include <vector>
 
 #include "lg_common.h"
+#include "lg_prefill.h"
 #include "lg_quant.h"
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(256) void k_bert_quant(const float* __restrict__ x,
 /* ------------------------------------------------------------------ */
 /* token-batched GEMM: out[t][r] = W[r] . act[t] (+ epilogue)           */
 /* ------------------------------------------------------------------ */
-enum { EP_BIAS = 0, EP_BIAS_RES = 1, EP_BIAS_GELU = 2 };
+enum { EP_BIAS = 0, EP_BIAS_RES = 1, EP_BIAS_GELU = 2, EP_STORE = 3, EP_ADD = 4 };   /* STORE/ADD: no bias; ADD: out += */
 
 struct BGemm {
     const uint8_t* w;          /* F32/F16: [R][K]; BF_I8: int8 [R][K] */
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(64) void k_bert_gemm(BGemm a)
     for (int j = 0; j < TN; j++) {
         const int r = r0 + 16 * j + m;
         if (r >= a.R) continue;
-        const float bias = a.bias[r];
+        const float bias = EP <= EP_BIAS_GELU ? a.bias[r] : 0.0f;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -377,7 +378,10 @@ __global__ __launch_bounds__(64) void k_bert_gemm(BGemm a)
                 const int t = t0 + 16 * i + 4 * g + v;
                 if (t >= a.T) continue;
                 float o = acc[i][j][v];
-                if constexpr (EP == EP_BIAS) {
+                if constexpr (EP == EP_STORE) {
+                } else if constexpr (EP == EP_ADD) {
+                    o = a.out[(size_t)t * a.ldo + r] + o;
+                } else if constexpr (EP == EP_BIAS) {
                     o = o + bias;
                 } else if constexpr (EP == EP_BIAS_RES) {
                     o = o + (bias + a.res[(size_t)t * a.ldr + r]);
@@ -1161,6 +1165,28 @@ static int gemm_ep(const BMat& W, const float* x, int ldx, const lg_bert* b, int
     default: gemm_tiles<BF_I8, EP>(a, b->stream); break;
     }
     return lg_check_launch("bert gemm");
+}
+
+/* The same GEMM for the batched prefill's F32/F16 layer matrices
+ * (lg_prefill.h): out[t][r] (+)= W[r] . x[t], fp32 activations. */
+int lg_fgemm_tokens(int wtype, const uint8_t* W, int rows, int cols, const float* x, int ldx, int T, float* out, int ldo,
+                    int accumulate, hipStream_t s)
+{
+    if ((wtype != LG_F32 && wtype != LG_F16) || !W || !x || !out || rows <= 0 || cols <= 0 || cols % 32 || T <= 0 ||
+        ldx < cols || ldx % 4 || ldo < rows) {
+        lg_set_error("fp gemm: bad arguments (type %d, rows %d, cols %d, T %d)", wtype, rows, cols, T);
+        return LG_ERR_ARG;
+    }
+    BGemm a = {};
+    a.w = W; a.R = rows; a.K = cols; a.x = x; a.ldx = ldx; a.T = T; a.out = out; a.ldo = ldo;
+    if (wtype == LG_F32) {
+        if (accumulate) gemm_tiles<LG_F32, EP_ADD>(a, s);
+        else gemm_tiles<LG_F32, EP_STORE>(a, s);
+    } else {
+        if (accumulate) gemm_tiles<LG_F16, EP_ADD>(a, s);
+        else gemm_tiles<LG_F16, EP_STORE>(a, s);
+    }
+    return lg_check_launch("fp gemm");
 }
 
 static int launch_quant(const lg_bert* b, const float* x, int n, int T)

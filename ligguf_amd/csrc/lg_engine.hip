@@ -736,8 +736,9 @@ extern "C" int lg_decode_path(const lg_ctx* ctx)
 #define LG_PF_TMAX 512   /* tokens per layer pass */
 
 /* the batched prefill serves models whose layer matrices all have a batched
- * GEMM (the K-quants, Q8_0, Q1_0, Q1_G; any mix, Q|K|V and up|gate stacked
- * or not) and whose attention shape the prefill attention kernel takes */
+ * GEMM (the K-quants, Q8_0, Q1_0, Q1_G on int8 MFMA, F32/F16 on fp32 MFMA;
+ * any mix, Q|K|V and up|gate stacked or not) and whose attention shape the
+ * prefill attention kernel takes */
 static PfMat pf_mat(const dweight& w) { return PfMat{w.data, w.rsz, w.type, w.rows}; }
 
 static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
@@ -750,7 +751,7 @@ static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
         const int at = lg_prefill_act_type(w.type);
         /* the Q1_G GEMM steps 256 values */
         if (at < 0 || (w.type == LG_Q1_G && w.cols % 256)) ok = false;
-        fam |= at == LG_Q8_K ? 1 : 2;
+        fam |= at == LG_Q8_K ? 1 : at == LG_Q8_0 ? 2 : 4;
     };
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
@@ -809,6 +810,10 @@ static int prefill_buffers(lg_ctx* c)
         if ((rc = dalloc(c, (void**)&B.qk.d, wide / 256 * tmax * 4))) return rc;
         if ((rc = dalloc(c, (void**)&B.qk.bs, (size_t)tmax * (wide / 256) * 16 * 2))) return rc;
         B.qk.tld = tmax;
+    }
+    if (c->pf_fam & 4) {   /* F32/F16 weights: the fp32 activations */
+        if ((rc = dalloc(c, (void**)&B.qf.f, (size_t)tmax * wide * 4))) return rc;
+        B.qf.tld = tmax;
     }
     if (c->pf_fam & 2) {   /* Q8_0: quants, a scale and a sum per 32 values */
         if ((rc = dalloc(c, (void**)&B.q0.qs, (size_t)tmax * wide))) return rc;
@@ -1302,8 +1307,8 @@ extern "C" int lg_set_prefill_path(lg_ctx* ctx, int path)
         return ctx_fail(ctx, LG_ERR_ARG);
     }
     if (path == LG_PREFILL_BATCHED && ctx->loaded && !ctx->pf_ok) {
-        lg_set_error("set_prefill_path: the batched prefill needs quantized layer matrices (K-quants, Q8_0, Q1_0, "
-                     "Q1_G) and head_dim 48, 64 or 128");
+        lg_set_error("set_prefill_path: the batched prefill needs head_dim 48, 64 or 128 with 1, 2, 4 or 8 query "
+                     "heads per KV head");
         return ctx_fail(ctx, LG_ERR_TYPE);
     }
     ctx->prefill_path = path;
@@ -1321,12 +1326,22 @@ extern "C" int lg_matmul_tokens(int type, const void* w, uint32_t rsz, int n, in
 {
     const int at = lg_prefill_act_type(type);
     if (at < 0) {
-        lg_set_error("matmul_tokens: type %d has no batched GEMM (K-quants, Q8_0, Q1_0, Q1_G)", type);
+        lg_set_error("matmul_tokens: type %d has no batched GEMM", type);
         return LG_ERR_TYPE;
     }
     if (!w || !x || !out || n <= 0 || n % (at == LG_Q8_K ? 256 : 32) || d <= 0 || T <= 0) {
         lg_set_error("matmul_tokens: bad arguments (n %d, d %d, T %d)", n, d, T);
         return LG_ERR_ARG;
+    }
+    if (at == LG_F32) {   /* fp32 activations as given */
+        if (rsz != (uint32_t)n * (type == LG_F32 ? 4u : 2u)) {
+            lg_set_error("matmul_tokens: row bytes %u for %d values", rsz, n);
+            return LG_ERR_ARG;
+        }
+        int rc = lg_fgemm_tokens(type, (const uint8_t*)w, d, n, x, n, T, out, d, 0, (hipStream_t)stream);
+        const hipError_t e2 = hipStreamSynchronize((hipStream_t)stream);
+        if (!rc && e2 != hipSuccess) { lg_set_error("matmul_tokens: %s", hipGetErrorString(e2)); rc = LG_ERR_HIP; }
+        return rc;
     }
     /* workspace: quants, then scales for n/32 blocks (enough for either
      * form), the Q8_K bsums and the Q8_0 sums */

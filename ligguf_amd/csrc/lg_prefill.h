@@ -16,6 +16,7 @@ struct PfQ8K {
     int16_t* bs;
     int* as;
     int tld;
+    float* f;        /* F32 form (F32/F16 weights): the fp32 activations [T][K], nothing quantized */
 };
 
 /* one weight matrix as the prefill reads it: GGUF rows of `type` */
@@ -57,14 +58,15 @@ struct PfBuffers {
     float* ug;       /* [tmax][2 n_ff] */
     PfQ8K qk;        /* Q8_K form, width up to n_ff (qs NULL when no matrix takes it) */
     PfQ8K q0;        /* Q8_0 form (likewise) */
+    PfQ8K qf;        /* F32 form (likewise; only f and tld) */
     /* activation trace of one pass (NULL: none): token t's activation k in
      * block_q8_K / block_q8_0 rows at trace + (t (4 L + 1) + k) stride */
     uint8_t* trace;
     size_t trace_stride;
 };
 
-/* activation form a weight type takes: LG_Q8_K, LG_Q8_0, or -1 when the
- * batched GEMMs do not take the type */
+/* activation form a weight type takes: LG_Q8_K, LG_Q8_0, LG_F32 (F32/F16
+ * weights), or -1 when the batched GEMMs do not take the type */
 int lg_prefill_act_type(int wtype);
 
 /* the prefill attention's head widths and query heads per KV head */
@@ -81,7 +83,12 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
 int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out,
                     int ldo, int accumulate, hipStream_t s);
 /* rmsnorm (norm_w != NULL) and the activation quantizer of qtype (LG_Q8_K,
- * n a multiple of 256, or LG_Q8_0, n a multiple of 32) for T tokens of
- * width n */
+ * n a multiple of 256, or LG_Q8_0, n a multiple of 32; LG_F32: the fp32
+ * values into q.f) for T tokens of width n */
 int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w, float eps, int n, int T,
                         const PfQ8K& q, hipStream_t s);
+
+/* F32/F16 weights x fp32 activations on fp32 MFMA (lg_bert.hip's token
+ * GEMM): out[t][r] (+)= W[r] . x[t] */
+int lg_fgemm_tokens(int wtype, const uint8_t* W, int rows, int cols, const float* x, int ldx, int T, float* out, int ldo,
+                    int accumulate, hipStream_t s);

@@ -80,7 +80,12 @@ template <int QT>
 __device__ __forceinline__ void pf_store(const float v[4], const PfQ8K& q, int n, int t, int b)
 {
     if constexpr (QT == LG_Q8_K) pf_store_q8k(v, q, n, t, b);
-    else pf_store_q8_0(v, q, n, t, b);
+    else if constexpr (QT == LG_Q8_0) pf_store_q8_0(v, q, n, t, b);
+    else {
+        /* the fp32 values (F32/F16 weights take them unquantized) */
+        const int i = b * 256 + 4 * (threadIdx.x & 63);
+        if (i < n) *(float4*)(q.f + (size_t)t * n + i) = make_float4(v[0], v[1], v[2], v[3]);
+    }
 }
 
 /* block b of token t: rmsnorm(x_t) * w (w != NULL) or x_t, quantized (Q8_K
@@ -372,14 +377,15 @@ static int gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const Pf
 int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w, float eps, int n, int T,
                         const PfQ8K& q, hipStream_t s)
 {
-    if (!x || !q.qs || n <= 0 || n % (qtype == LG_Q8_K ? 256 : 32) || T <= 0 || T > q.tld || ldx < n ||
-        (qtype != LG_Q8_K && qtype != LG_Q8_0)) {
+    if (!x || !(qtype == LG_F32 ? (void*)q.f : (void*)q.qs) || n <= 0 || n % (qtype == LG_Q8_K ? 256 : 32) ||
+        T <= 0 || T > q.tld || ldx < n || (qtype != LG_Q8_K && qtype != LG_Q8_0 && qtype != LG_F32)) {
         lg_set_error("prefill quantize: bad arguments (type %d, n %d, T %d)", qtype, n, T);
         return LG_ERR_ARG;
     }
     const dim3 grid((n + 255) / 256, T);
     if (qtype == LG_Q8_K) hipLaunchKernelGGL(k_pf_quant<LG_Q8_K>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
-    else hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    else if (qtype == LG_Q8_0) hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    else hipLaunchKernelGGL(k_pf_quant<LG_F32>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
     return lg_check_launch("prefill quantize");
 }
 
@@ -1006,6 +1012,7 @@ int lg_prefill_act_type(int wtype)
     switch (wtype) {
     case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: return LG_Q8_K;
     case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: return LG_Q8_0;
+    case LG_F32: case LG_F16: return LG_F32;
     default: return -1;
     }
 }
@@ -1021,6 +1028,8 @@ static int64_t pf_row_bytes(int wtype, int cols)
     case LG_Q8_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q8_0;
     case LG_Q1_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q1_0;
     case LG_Q1_G: return cols % 256 ? -1 : (int64_t)cols / 128 * LG_BS_Q1_G;   /* the Q1_G GEMM steps 256 values */
+    case LG_F32: return cols % 32 ? -1 : (int64_t)cols * 4;
+    case LG_F16: return cols % 32 ? -1 : (int64_t)cols * 2;
     default: return -1;
     }
 }
@@ -1034,6 +1043,13 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
         return LG_ERR_TYPE;
     }
     const int64_t rb = pf_row_bytes(wtype, cols);
+    if (at == LG_F32) {
+        if (rb < 0 || rsz != (uint32_t)rb || !x.f || T > x.tld) {
+            lg_set_error("prefill gemm: bad arguments (type %d, cols %d, row bytes %u, T %d)", wtype, cols, rsz, T);
+            return LG_ERR_ARG;
+        }
+        return lg_fgemm_tokens(wtype, W, rows, cols, x.f, cols, T, out, ldo, accumulate, s);
+    }
     if (!W || !out || !x.qs || !x.d || (at == LG_Q8_K && !x.bs) || (wtype == LG_Q1_G && !x.as) || rows <= 0 ||
         cols < 32 || rb < 0 || rsz != (uint32_t)rb || T <= 0 || T > x.tld || x.tld % 4 || ldo < rows) {
         lg_set_error("prefill gemm: bad arguments (type %d, rows %d, cols %d, row bytes %u, T %d)", wtype, rows, cols,
@@ -1338,10 +1354,13 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
     }
     const int ne = M.n_embed, kvd = M.kv_dim, qs = ne + 2 * kvd, nff = M.n_ff;
     const size_t tstride = (size_t)(4 * M.n_layers + 1) * B.trace_stride;
-    /* activation forms the matrices take: bit 0 Q8_K, bit 1 Q8_0 */
-    auto fam = [](const PfMat& W) { return lg_prefill_act_type(W.type) == LG_Q8_K ? 1 : 2; };
+    /* activation forms the matrices take: bit 0 Q8_K, bit 1 Q8_0, bit 2 F32 */
+    auto fam = [](const PfMat& W) {
+        const int at = lg_prefill_act_type(W.type);
+        return at == LG_Q8_K ? 1 : at == LG_Q8_0 ? 2 : 4;
+    };
     auto trace = [&](int f, int n, int k) -> int {
-        if (!B.trace) return LG_OK;
+        if (!B.trace || !(f & 3)) return LG_OK;   /* fp32 activations are not quantized: nothing to record */
         uint8_t* tr = B.trace + (size_t)k * B.trace_stride;
         if (f & 1) hipLaunchKernelGGL(k_pf_trace<LG_Q8_K>, dim3(n / 256, T), dim3(64), 0, s, B.qk, n, tr, tstride);
         else hipLaunchKernelGGL(k_pf_trace<LG_Q8_0>, dim3(n / 32, T), dim3(64), 0, s, B.q0, n, tr, tstride);
@@ -1353,10 +1372,12 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
         int rc;
         if ((f & 1) && (rc = lg_prefill_quantize(LG_Q8_K, x, n, w, M.eps, n, T, B.qk, s))) return rc;
         if ((f & 2) && (rc = lg_prefill_quantize(LG_Q8_0, x, n, w, M.eps, n, T, B.q0, s))) return rc;
+        if ((f & 4) && (rc = lg_prefill_quantize(LG_F32, x, n, w, M.eps, n, T, B.qf, s))) return rc;
         return trace(f, n, k);
     };
     auto gemm = [&](const PfMat& W, int cols, float* o, int ldo, int acc) {
-        return lg_prefill_gemm(W.type, W.w, W.rsz, W.rows, cols, fam(W) == 1 ? B.qk : B.q0, T, o, ldo, acc, s);
+        const int f = fam(W);
+        return lg_prefill_gemm(W.type, W.w, W.rsz, W.rows, cols, f == 1 ? B.qk : f == 2 ? B.q0 : B.qf, T, o, ldo, acc, s);
     };
     int rc;
     hipLaunchKernelGGL(k_pf_embed, dim3(T), dim3(256), 0, s, M.embd_t, M.embd, M.embd_rsz, B.toks, ne, B.x);
@@ -1394,7 +1415,8 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
         const int f_d = fam(L.down);
         const dim3 sg((nff + 255) / 256, T);
         if (f_d == 1) hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_K>, sg, dim3(64), 0, s, B.ug, nff, B.qk);
-        else hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_0>, sg, dim3(64), 0, s, B.ug, nff, B.q0);
+        else if (f_d == 2) hipLaunchKernelGGL(k_pf_swiglu_quant<LG_Q8_0>, sg, dim3(64), 0, s, B.ug, nff, B.q0);
+        else hipLaunchKernelGGL(k_pf_swiglu_quant<LG_F32>, sg, dim3(64), 0, s, B.ug, nff, B.qf);
         if ((rc = lg_check_launch("prefill swiglu"))) return rc;
         if ((rc = trace(f_d, nff, 4 * l + 3))) return rc;
         if ((rc = gemm(L.down, nff, B.x, ne, 1))) return rc;

@@ -3,7 +3,7 @@ against the oracle's matvec of every token, and lg_prefill with
 LG_PREFILL_BATCHED against the token-by-token prefill (LG_PREFILL_STEPS,
 itself bit-equal to sequential decode steps) and against the oracle, for
 models of every quantized layer type the GEMMs take (Q2_K..Q6_K, Q8_0,
-Q1_0, Q1_G), a Q4_K_M-style mix and head_dim 48 / 64 / 128.
+Q1_0, Q1_G, F16, F32), a Q4_K_M-style mix and head_dim 48 / 64 / 128.
 
 The GEMMs reproduce the integer (sub-)block sums of the reference's dots
 exactly (fast/lil_math.cpp:411-739) and combine them in fp32 per block, so
@@ -17,10 +17,10 @@ import numpy as np
 import pytest
 
 from ligguf_amd import encode, ops
-from ligguf_amd.lib import (F16, PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS,
+from ligguf_amd.lib import (F16, F32, PATH_AUTO, PATH_FUSED, PATH_MULTI, PREFILL_AUTO, PREFILL_BATCHED, PREFILL_STEPS,
                             Q1_0, Q1_G, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, TYPE_NAMES, LgError, row_size)
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
-from parity import EXACT_STEP, prefill_flips
+from parity import EXACT_STEP, prefill_flips, slot_formats
 from test_gpu_decode import oracle_state, rel
 from test_gpu_ops import MATVEC_TOL, dev, host
 
@@ -58,9 +58,12 @@ def test_matmul_tokens_q1g_vs_oracle(gpu, oracle, d, n, T):
         assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
 
 
+# fp32 sums of n products in two orders differ by ~sqrt(n) 2^-24 of the sum of |terms| (3.8e-6 at 4096)
+FLOAT_GEMM_TOL = 2e-5
+
 GEMM_CASES = [(t, d, n, T) for t in (Q2_K, Q3_K, Q5_K, Q6_K)
               for d, n, T in [(200, 512, 37), (130, 256, 1), (4096, 4096, 64)]] + \
-             [(t, d, n, T) for t in (Q8_0, Q1_0)
+             [(t, d, n, T) for t in (Q8_0, Q1_0, F16, F32)
               for d, n, T in [(200, 288, 37), (130, 32, 1), (100, 1376, 70), (4096, 4096, 64)]]
 
 
@@ -68,9 +71,9 @@ GEMM_CASES = [(t, d, n, T) for t in (Q2_K, Q3_K, Q5_K, Q6_K)
                          ids=[f"{TYPE_NAMES[t]}-{d}x{n}-T{T}" for t, d, n, T in GEMM_CASES])
 def test_matmul_tokens_types_vs_oracle(gpu, oracle, wt, d, n, T):
     """The K-quant GEMM (one int8 MFMA per 16- or 32-value sub-block, the
-    sub-block scales in int32) and the Q8_0 / Q1_0 GEMM (one per 32-value
-    block, widths any multiple of 32) against the oracle's matvec of each
-    token's quantized activation."""
+    sub-block scales in int32), the Q8_0 / Q1_0 GEMM (one per 32-value
+    block, widths any multiple of 32) and the F16 / F32 GEMM (fp32 MFMA on
+    the unquantized activation) against the oracle's matvec of each token."""
     rng = np.random.default_rng(d + n + T + wt)
     w = encode.random_tensor(wt, d + n + wt, wt, d, n)
     x = rng.standard_normal((T, n)).astype(np.float32)
@@ -79,17 +82,26 @@ def test_matmul_tokens_types_vs_oracle(gpu, oracle, wt, d, n, T):
     kq = wt in (Q2_K, Q3_K, Q5_K, Q6_K)
     toks = range(T) if T <= 40 else rng.choice(T, 12, replace=False)
     for t in toks:
-        xq = oracle.quantize_q8_K(x[t]) if kq else oracle.quantize_q8_0(x[t])
-        ref, ab = oracle.matvec_q(wt, w, rsz, n, d, xq, want_abs=True)
+        if wt in (F16, F32):
+            ref = oracle.matvec(wt, w, rsz, n, d, x[t])
+            wf = np.frombuffer(np.asarray(w, np.uint8).tobytes()[:d * rsz], np.float16 if wt == F16 else np.float32)
+            ab = np.abs(wf.reshape(d, n).astype(np.float64)) @ np.abs(x[t].astype(np.float64))
+            tol = FLOAT_GEMM_TOL
+        else:
+            xq = oracle.quantize_q8_K(x[t]) if kq else oracle.quantize_q8_0(x[t])
+            ref, ab = oracle.matvec_q(wt, w, rsz, n, d, xq, want_abs=True)
+            tol = MATVEC_TOL
         err = np.abs(y[t] - ref) / np.maximum(ab, 1e-30)
-        assert np.all(err <= MATVEC_TOL), (t, float(err.max()))
+        assert np.all(err <= tol), (t, float(err.max()))
 
 
 def test_matmul_tokens_rejects_other_types(gpu):
     x = dev(np.zeros((2, 256), np.float32), gpu)
-    w = dev(np.zeros(row_size(F16, 256) * 4, np.uint8), gpu)
-    with pytest.raises(LgError):
-        ops.matmul_tokens(F16, w, row_size(F16, 256), 256, 4, x)
+    w = dev(np.zeros(row_size(Q8_0, 256) * 4, np.uint8), gpu)
+    with pytest.raises(LgError):                 # Q8_K is an activation form, not a weight type
+        ops.matmul_tokens(15, w, row_size(Q8_0, 256), 256, 4, x)
+    with pytest.raises(LgError):                 # a K-quant row is a whole number of 256-value blocks
+        ops.matmul_tokens(Q4_K, w, row_size(Q4_K, 256), 288, 4, dev(np.zeros((2, 288), np.float32), gpu))
 
 
 BATCHED_MODELS = [
@@ -115,6 +127,10 @@ BATCHED_MODELS = [
     ModelConfig("llama-w1024-q1_0", 0, 2, 1024, 16, 16, 64, 2816, 1024, 1024, 1e4, 1e-5, Q1_0, Q8_0, Q8_0),
     ModelConfig("qwen3-w1024-q4k-q8down", 1, 2, 1024, 8, 2, 128, 2816, 1024, 1024, 1e6, 1e-6, Q4_K, Q4_K, Q8_0,
                 overrides=(("ffn_down", Q8_0), ("attn_output", Q8_0))),
+    # unquantized layers (fp32 MFMA on the fp32 activations), one with a K-quant among them
+    ModelConfig("llama-w1024-f16", 0, 2, 1024, 16, 4, 64, 2816, 1024, 1024, 1e4, 1e-5, F16, Q8_0, Q8_0),
+    ModelConfig("llama-w512-f32-q4kdown", 0, 2, 512, 8, 8, 64, 1536, 1024, 1024, 1e4, 1e-5, F32, Q8_0, Q8_0,
+                overrides=(("ffn_down", Q4_K),)),
 ]
 
 
@@ -245,13 +261,15 @@ def test_batched_prefill_flips_explained(pf_model, oracle):
     print(f"\n{cfg.name}: {compared} token activations compared, {differing} with rounding flips, "
           f"{len(bad)} unexplained; last token {'clean' if clean else 'after a flip'}; logits vs oracle {e:.2e}")
     assert not bad, bad[:5]
-    assert compared >= 4 * cfg.n_layers + 1                 # at least the first token all the way
+    quantized = sum(1 for qt, _ in slot_formats(cfg) if qt is not None)
+    assert compared >= quantized                            # at least the first token all the way
     assert e <= (EXACT_STEP if clean else 5e-2)
     assert near_best(ref, int(np.argmax(lg_b)))
 
 
-def test_batched_prefill_unavailable_for_other_types(gpu):
-    cfg = ModelConfig("llama-w1024-f16", 0, 1, 1024, 8, 8, 128, 2816, 1024, 1024, 1e4, 1e-5, F16, Q8_0, Q4_K)
+def test_batched_prefill_unavailable_for_other_shapes(gpu):
+    """head_dim 256 has no prefill attention kernel: the prompt runs token by token."""
+    cfg = ModelConfig("llama-w1024-hd256", 0, 1, 1024, 4, 4, 256, 2816, 1024, 1024, 1e4, 1e-5, Q4_K, Q8_0, Q4_K)
     hm = HostModel.synthetic(cfg)
     eng = Engine(0)
     eng.load(hm)
