@@ -730,6 +730,12 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         fr = *(const float2*)(P.rope_freq + l4 / 2);
     };
     const bool has = (int)blockIdx.x < nunits;
+    /* with a dependency wait (the persistent kernel), the short-context
+     * unit's K/V rows -- cache rows of earlier steps, position-free -- load
+     * before it, by waves 1.. (wave 0 polls: its loads would hold the poll
+     * back), and the heads after it */
+    const bool pre = FIX && wait_target != 0;
+    if (pre && has && wave != 0) load_kv(0, blockIdx.x, 0);
     if (wait_target) pk_wait(P, wait_target);
     if (!FIX && !has) stamp(tr, 1);   /* FIX: after the loop (no store ahead of the unit's loads) */
 
@@ -745,7 +751,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int t0 = c * chunk;
         load_heads(u);
         lg_issue_order();   /* heads first, then K/V */
-        load_kv(0, u, 0);
+        if (!pre || wave == 0) load_kv(0, u, 0);
         if (FIX) {
             /* the position from here on: an empty asm pins its first use
              * behind the loads above (it may still be in flight) */
