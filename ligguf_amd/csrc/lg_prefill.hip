@@ -1069,52 +1069,74 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
 }
 
 /* ------------------------------------------------------------------ */
-/* causal attention on fp32 MFMA: 16 query tokens x one KV head          */
+/* causal attention on fp16 MFMA: 16 query tokens x one KV head          */
 /* ------------------------------------------------------------------ */
 /* One workgroup per (16-token query block, KV head g), one wave per query
- * head of the group.  Per block of 16 key positions the K and V rows come
- * from the fp16 cache into LDS as fp32 and each wave computes
- *   S^T[key][q] = sum_d K[key][d] Q[q][d]        (32 v_mfma_f32_16x16x4f32)
- *   O^T[d][q]  += sum_key V[key][d] P^T[key][q]  (32 more, 8 tiles of 16 dims)
- * with an online softmax per query column in log2 units (the decode step's
- * attention does the same per lane group).  Lane l holds query column l%16 and keys/dims 4(l/16)..+3
- * of each tile (the D layout); the MFMA wants P^T with key l/16 of each
- * 4-key step, so the four registers are transposed across the four 16-lane
- * groups by two rounds of v_permlane32_swap / v_permlane16_swap.
- *
- * A query's own key and value are its fp32 k/v (the cache holds them in
- * fp16), as in the token-sequential step: in the key block holding a
- * query's position its score is recomputed from the fp32 k row, and its
+ * head of the group (and, up to 4 query heads per KV head, per half of the
+ * key blocks: the halves merge at the end).  Per block of 16 key positions
+ * the K and V rows come from the fp16 cache into LDS, and each wave
+ * computes the scores and the output with an online softmax per query
+ * column in log2 units (the decode step's attention does the same per lane
+ * group).  A query's own key and value are its fp32 k/v (the cache holds
+ * them in fp16), as in the token-sequential step: in the key block holding
+ * a query's position its score is recomputed from the fp32 k row, and its
  * value enters as the fp16 row through the MFMA plus p (v32 - v16).  Key
- * positions past a query's own are masked.  Only fp32 rounding differs
- * from the token-sequential step (sum orders). */
+ * positions past a query's own are masked.
+ *
+ * The products run on fp16 MFMA (v_mfma_f32_16x16x16_f16, fp32
+ * accumulation): the cache rows are fp16 already, and each fp32
+ * operand goes in as two fp16 parts, x = hi + lo (hi = fp16(x), lo =
+ * fp16(x - hi)), so q.k = hi.k + lo.k and p.v = hi.v + lo.v keep ~22 bits of
+ * every fp32 operand (each fp16 x fp16 product is exact in fp32).  p <= 1 is
+ * scaled by 2^15 before the split, so p down to 2^-29 stays a normal fp16,
+ * and the sums are unscaled at the end.  K is staged in LDS as it is
+ * stored ([key][dim], rows padded 16 B against bank conflicts), V transposed
+ * ([dim][key]): an MFMA lane takes 4 consecutive keys of one dim.
+ *   S^T[key][q] = sum_d K[key][d] Q[q][d]   A = K, B = Q^T (16 dims a step)
+ *   O^T[d][q]  += sum_key V^T[d][key] P^T[key][q]   A = V^T, B = P^T
+ * P^T is the D layout of S^T (lane (g, q) holds keys 4g..4g+3), so it feeds
+ * the second product without a transpose.  Only fp32 rounding differs from
+ * the token-sequential step (sum orders, ~2^-22 per operand). */
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
 template <int HD, int NREP, int SPLIT>
-__global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float* __restrict__ qkv, int qstride, int n_embed,
-                                                            int kv_dim, const uint16_t* __restrict__ kc,
-                                                            const uint16_t* __restrict__ vc, int pos0, int T,
-                                                            float* __restrict__ att)
+__global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_h(const float* __restrict__ qkv, int qstride, int n_embed,
+                                                         int kv_dim, const uint16_t* __restrict__ kc,
+                                                         const uint16_t* __restrict__ vc, int pos0, int T,
+                                                         float* __restrict__ att)
 {
     static_assert(HD % 16 == 0 && HD <= 256, "16-dim output tiles");
-    constexpr int NT = 64 * NREP * SPLIT, NS = HD / 4, NTL = HD / 16, VST = HD + 16, OST = HD + 4;
-    __shared__ __attribute__((aligned(16))) float s_kt[SPLIT][NS * 16 * 4];   /* K[key][4s + j] at (s*16 + key)*4 + j */
-    __shared__ __attribute__((aligned(16))) float s_vt[SPLIT][16 * VST];      /* V[key][d] */
+    constexpr int NT = 64 * NREP * SPLIT, NTL = HD / 16, KST = HD + 8, VTS = 20, OST = HD + 4;
+    constexpr float PS = 32768.0f;
+    __shared__ __attribute__((aligned(16))) _Float16 s_kh[SPLIT][16 * KST];   /* K[key][d] */
+    __shared__ __attribute__((aligned(16))) _Float16 s_vt[SPLIT][HD * VTS];   /* V^T[d][key] */
     __shared__ __attribute__((aligned(16))) float s_k32[16 * OST];    /* fp32 k / v of the block's 16 tokens */
     __shared__ __attribute__((aligned(16))) float s_v32[16 * OST];
     const int qb = blockIdx.x, g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, r = (tid >> 6) % NREP, half = (tid >> 6) / NREP;
-    const float* __restrict__ s_k = s_kt[half];
-    const float* __restrict__ s_v = s_vt[half];
+    const _Float16* __restrict__ s_k = s_kh[half];
+    const _Float16* __restrict__ s_v = s_vt[half];
     const int col = lane & 15, grp = lane >> 4;
     const int t0 = qb * 16, tq = t0 + col, tqc = min(tq, T - 1);
     const int qpos = pos0 + tq;
     const int last = pos0 + min(t0 + 15, T - 1);   /* last key position this block reads */
     const float scale2 = 1.44269504088896341f / sqrtf((float)HD);
 
-    /* B operand of S^T: Q[tq][grp + 4s] */
-    float qv[NS];
+    /* B operand of S^T: Q[tq][16j + 4 grp + i], fp32 and as hi + lo */
+    float qf[NTL][4];
+    v4h qh[NTL], ql[NTL];
     const float* qrow = qkv + (size_t)tqc * qstride + (size_t)(g * NREP + r) * HD;
 #pragma unroll
-    for (int s2 = 0; s2 < NS; s2++) qv[s2] = qrow[grp + 4 * s2];
+    for (int j = 0; j < NTL; j++) {
+        const float4 v = *(const float4*)(qrow + 16 * j + 4 * grp);
+        qf[j][0] = v.x; qf[j][1] = v.y; qf[j][2] = v.z; qf[j][3] = v.w;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const _Float16 h = (_Float16)qf[j][i];
+            qh[j][i] = h;
+            ql[j][i] = (_Float16)(qf[j][i] - (float)h);
+        }
+    }
     for (int i = tid; i < 16 * HD; i += NT) {
         const int tt = i / HD, d = i % HD;
         const float* row = qkv + (size_t)min(t0 + tt, T - 1) * qstride;
@@ -1127,71 +1149,67 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
     for (int t = 0; t < NTL; t++) o[t] = (v4f){0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;   /* l: this lane group's keys only, summed at the end */
     const int nkb = last / 16 + 1, nit = (nkb + SPLIT - 1) / SPLIT;
-    /* SPLIT key blocks per step, block SPLIT*it + h for the waves of half h;
-     * the next step's K/V rows load into registers while this one computes:
-     * piece i < SPLIT*256 is 8 dims of one key of one block */
     constexpr int NPC = SPLIT * 16 * (HD / 8), NSTG = (NPC + NT - 1) / NT;
-    uint4 kq[NSTG], vq[NSTG];
+    /* the K/V pieces of the next step (piece i: 8 dims of one key of one
+     * half's block), loaded while this step computes */
+    struct Pieces {
+        uint4 k[NSTG], v[NSTG];
+    };
     auto stage_load = [&](int it) {
+        Pieces P;
 #pragma unroll
         for (int u = 0; u < NSTG; u++) {
             const int i = min(tid + u * NT, NPC - 1);
             const int hb = i / (16 * (HD / 8)), kk = (i / (HD / 8)) % 16, d8 = (i % (HD / 8)) * 8;
             const size_t off = (size_t)min((it * SPLIT + hb) * 16 + kk, last) * kv_dim + (size_t)g * HD + d8;
-            kq[u] = *(const uint4*)(kc + off);
-            vq[u] = *(const uint4*)(vc + off);
+            P.k[u] = *(const uint4*)(kc + off);
+            P.v[u] = *(const uint4*)(vc + off);
         }
+        return P;
     };
-    auto half2 = [](uint32_t w, float& a, float& b) {
-        a = lg_h2f((uint16_t)(w & 0xffffu));
-        b = lg_h2f((uint16_t)(w >> 16));
-    };
-    stage_load(0);
+    Pieces pc = stage_load(0);
     for (int it = 0; it < nit; it++) {
         __syncthreads();   /* the previous step's tiles are consumed */
 #pragma unroll
         for (int u = 0; u < NSTG; u++) {
             const int i = tid + u * NT;
-            if (i < NPC) {
+            if (NSTG * NT == NPC || i < NPC) {   /* (every thread has a piece when the pieces divide evenly) */
                 const int hb = i / (16 * (HD / 8)), kk = (i / (HD / 8)) % 16, d8 = (i % (HD / 8)) * 8;
-                float* sk = s_kt[hb];
-                float* sv4 = s_vt[hb];
-                float4 k0, k1, v0, v1;
-                half2(kq[u].x, k0.x, k0.y);
-                half2(kq[u].y, k0.z, k0.w);
-                half2(kq[u].z, k1.x, k1.y);
-                half2(kq[u].w, k1.z, k1.w);
-                half2(vq[u].x, v0.x, v0.y);
-                half2(vq[u].y, v0.z, v0.w);
-                half2(vq[u].z, v1.x, v1.y);
-                half2(vq[u].w, v1.z, v1.w);
-                *(float4*)&sk[((d8 >> 2) * 16 + kk) * 4] = k0;
-                *(float4*)&sk[(((d8 >> 2) + 1) * 16 + kk) * 4] = k1;
-                *(float4*)&sv4[kk * VST + d8] = v0;
-                *(float4*)&sv4[kk * VST + d8 + 4] = v1;
+                *(uint4*)&s_kh[hb][kk * KST + d8] = pc.k[u];
+                const uint4 vv = pc.v[u];
+                uint16_t* vt = (uint16_t*)s_vt[hb] + d8 * VTS + kk;
+                vt[0] = (uint16_t)(vv.x & 0xffffu);
+                vt[VTS] = (uint16_t)(vv.x >> 16);
+                vt[2 * VTS] = (uint16_t)(vv.y & 0xffffu);
+                vt[3 * VTS] = (uint16_t)(vv.y >> 16);
+                vt[4 * VTS] = (uint16_t)(vv.z & 0xffffu);
+                vt[5 * VTS] = (uint16_t)(vv.z >> 16);
+                vt[6 * VTS] = (uint16_t)(vv.w & 0xffffu);
+                vt[7 * VTS] = (uint16_t)(vv.w >> 16);
             }
         }
         __syncthreads();
-        stage_load(min(it + 1, nit - 1));
+        pc = stage_load(min(it + 1, nit - 1));
         const int kb = it * SPLIT + half;
         if (kb >= nkb) continue;   /* the other half's last block (wave-uniform) */
 
-        v4f sa = (v4f){0.f, 0.f, 0.f, 0.f}, sb = sa;
+        v4f sa = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s2 = 0; s2 < NS; s2 += 2) {
-            sa = __builtin_amdgcn_mfma_f32_16x16x4f32(s_k[(s2 * 16 + col) * 4 + grp], qv[s2], sa, 0, 0, 0);
-            sb = __builtin_amdgcn_mfma_f32_16x16x4f32(s_k[((s2 + 1) * 16 + col) * 4 + grp], qv[s2 + 1], sb, 0, 0, 0);
+        for (int j = 0; j < NTL; j++) {
+            const v4h a = *(const v4h*)(s_k + col * KST + 16 * j + 4 * grp);
+            sa = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qh[j], sa, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ql[j], sa, 0, 0, 0);
         }
-        float sv[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) sv[i] = sa[i] + sb[i];
+        float sv[4] = {sa[0], sa[1], sa[2], sa[3]};
         /* the block holds some query's own position: exact fp32 scores */
         const bool diag = kb * 16 + 15 >= pos0 + t0 && kb * 16 <= pos0 + t0 + 15;
         const int own = qpos - kb * 16;   /* 0..15 when this lane's query owns a key here */
         if (diag) {
             float e = 0.0f;
 #pragma unroll
-            for (int s2 = 0; s2 < NS; s2++) e = __builtin_fmaf(qv[s2], s_k32[col * OST + grp + 4 * s2], e);
+            for (int j = 0; j < NTL; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) e = __builtin_fmaf(qf[j][i], s_k32[col * OST + 16 * j + 4 * grp + i], e);
             e += lg_partner<4>(e);
             e += lg_partner<5>(e);
 #pragma unroll
@@ -1221,33 +1239,30 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
             pown += lg_partner<4>(pown);
             pown += lg_partner<5>(pown);
         }
-        /* P^T operands: b[mm] at lane (grp, col) = P^T[4 mm + grp][col] */
-        float b[4] = {pw[0], pw[1], pw[2], pw[3]};
-        {
-            auto x02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(b[0]), __float_as_uint(b[2]), false, false);
-            auto x13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(b[1]), __float_as_uint(b[3]), false, false);
-            auto y01 = __builtin_amdgcn_permlane16_swap(x02[0], x13[0], false, false);
-            auto y23 = __builtin_amdgcn_permlane16_swap(x02[1], x13[1], false, false);
-            b[0] = __uint_as_float(y01[0]);
-            b[1] = __uint_as_float(y01[1]);
-            b[2] = __uint_as_float(y23[0]);
-            b[3] = __uint_as_float(y23[1]);
+        /* P^T operand: the lane's keys 4 grp..+3, scaled, as hi + lo */
+        v4h ph, pl;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float ps = pw[i] * PS;
+            const _Float16 h = (_Float16)ps;
+            ph[i] = h;
+            pl[i] = (_Float16)(ps - (float)h);
         }
 #pragma unroll
         for (int t = 0; t < NTL; t++) {
             o[t] *= alpha;
-#pragma unroll
-            for (int mm = 0; mm < 4; mm++)
-                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(s_v[(4 * mm + grp) * VST + 16 * t + col], b[mm], o[t], 0,
-                                                            0, 0);
+            const v4h a = *(const v4h*)(s_v + (16 * t + col) * VTS + 4 * grp);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ph, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pl, o[t], 0, 0, 0);
         }
         if (diag && own >= 0 && own < 16) {
+            const float pso = pown * PS;
 #pragma unroll
             for (int t = 0; t < NTL; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int d = 16 * t + 4 * grp + i;
-                    o[t][i] = __builtin_fmaf(pown, s_v32[col * OST + d] - s_v[own * VST + d], o[t][i]);
+                    o[t][i] = __builtin_fmaf(pso, s_v32[col * OST + d] - (float)s_v[d * VTS + own], o[t][i]);
                 }
         }
     }
@@ -1275,11 +1290,12 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_mfma(const float*
     l += lg_partner<4>(l);
     l += lg_partner<5>(l);
     if (tq < T) {
+        const float inv = 1.0f / (l * PS);
         float* out = att + (size_t)tq * n_embed + (size_t)(g * NREP + r) * HD;
 #pragma unroll
         for (int t = 0; t < NTL; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) out[16 * t + 4 * grp + i] = o[t][i] / l;
+            for (int i = 0; i < 4; i++) out[16 * t + 4 * grp + i] = o[t][i] * inv;
     }
 }
 
@@ -1300,7 +1316,7 @@ static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_
     /* two halves of the key blocks per query head up to 4 query heads per
      * KV head (8 waves); one at 8 (8 waves already) */
 #define PFA(HD, NR)                                                                                          \
-    hipLaunchKernelGGL((k_pf_attn_mfma<HD, NR, (NR <= 4 ? 2 : 1)>), grid, dim3(64 * NR * (NR <= 4 ? 2 : 1)), 0, s, \
+    hipLaunchKernelGGL((k_pf_attn_h<HD, NR, (NR <= 4 ? 2 : 1)>), grid, dim3(64 * NR * (NR <= 4 ? 2 : 1)), 0, s, \
                        qkv, qs, M.n_embed, M.kv_dim, kc, vc, pos0, T, att)
 #define PFA_HD(HD)                    \
     switch (nrep) {                   \
