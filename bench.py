@@ -509,6 +509,24 @@ def cpu_baseline_q1g(hm, state_path: str, seconds: float, max_tokens: int = 64):
                       f"(reference FAST engine, AVX2 build, {threads} OpenMP threads)"}
 
 
+def layer_type_config(cfg, name: str):
+    """The headline shape with its layer matrices of another type (or mix)."""
+    from ligguf_amd.lib import TYPE_NAMES, Q6_K
+    if name == "Q4_K":
+        return cfg
+    if name == "Q4_K_M":
+        return cfg.with_(name=cfg.name + "_m", overrides=(("attn_v", Q6_K), ("ffn_down", Q6_K)))
+    if name == "Q4_K_Mx":
+        # llama.cpp's Q4_K_M choice of layers for the larger attn_v / ffn_down type: the first and last
+        # eighth of the layers and every third one between them
+        n = cfg.n_layers
+        more = [l for l in range(n) if l < n // 8 or l >= 7 * n // 8 or (l - n // 8) % 3 == 2]
+        return cfg.with_(name=cfg.name + "_mx", overrides=tuple((f"{t}.{l}", Q6_K) for l in more
+                                                                 for t in ("attn_v", "ffn_down")))
+    lt = {v: k for k, v in TYPE_NAMES.items()}[name]
+    return cfg.with_(name=cfg.name.replace("q4_k", name.lower()), layer_type=lt)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -525,8 +543,11 @@ def main() -> int:
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill: the prompt twice, the second timed (for MFMA counter runs)")
     ap.add_argument("--layer-type", default="Q4_K",
-                    help="with --prefill-only: the layer matrices' type (Q2_K..Q6_K, Q8_0, Q1_0, Q1_G; "
-                         "Q4_K_M: Q4_K with Q6_K attn_v and ffn_down)")
+                    help="with --prefill-only / --decode-only: the layer matrices' type (Q2_K..Q6_K, Q8_0, Q1_0, "
+                         "Q1_G; Q4_K_M: Q4_K with Q6_K attn_v and ffn_down; Q4_K_Mx: Q6_K attn_v and ffn_down in "
+                         "the layers where llama.cpp's Q4_K_M mix puts them, Q4_K elsewhere)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the prefill and greedy decode of the --layer-type model, one JSON record")
     ap.add_argument("--q1g-only", action="store_true",
                     help="run only the Q1_G long-context workload and print its line (profiling)")
     ap.add_argument("--q1g-ctx", type=int, default=8192, help="prompt length of the Q1_G workload")
@@ -563,13 +584,38 @@ def main() -> int:
         print(json.dumps({"bert": bert_report(torch, np, 0.0 if args.no_cpu else args.cpu_seconds)}), flush=True)
         return 0
 
+    if args.prefill_only or args.decode_only:
+        cfg = layer_type_config(cfg, args.layer_type)
+    if args.decode_only:
+        hm = HostModel.synthetic(cfg)
+        eng = Engine(0)
+        eng.load(hm)
+        prompt = np.random.default_rng(0).integers(1, cfg.vocab, args.prefill).astype(np.int32)
+        logits = eng.prefill(prompt, 0)
+        tok, pos = int(np.argmax(logits)), args.prefill
+        for _ in range(args.warmup):
+            eng.decode_async(tok, pos)
+            tok = eng.argmax()
+            pos += 1
+        torch.cuda.synchronize()
+        p_first, t0 = pos, time.perf_counter()
+        for _ in range(args.steps):
+            eng.decode_async(tok, pos)
+            tok = eng.argmax()
+            pos += 1
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
+        rep = {"model": cfg.name, "tok_s": round(args.steps / dt, 2), "ms_per_token": round(dt / args.steps * 1e3, 4),
+               "bytes_per_token": int(mean_bytes), "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) /
+                                                                                   HBM_PEAK, 4),
+               "decode_path": {1: "persistent", 2: "multi-kernel", 3: "fused-graph"}.get(eng.path(), "?"),
+               "positions": [p_first, pos - 1]}
+        eng.close()
+        print(json.dumps({"decode": rep}), flush=True)
+        return 0
+
     if args.prefill_only:
-        from ligguf_amd.lib import TYPE_NAMES, Q4_K, Q6_K
-        if args.layer_type == "Q4_K_M":
-            cfg = cfg.with_(name=cfg.name + "_m", overrides=(("attn_v", Q6_K), ("ffn_down", Q6_K)))
-        elif args.layer_type != "Q4_K":
-            lt = {v: k for k, v in TYPE_NAMES.items()}[args.layer_type]
-            cfg = cfg.with_(name=cfg.name.replace("q4_k", args.layer_type.lower()), layer_type=lt)
         hm = HostModel.synthetic(cfg)
         eng = Engine(0)
         eng.load(hm)

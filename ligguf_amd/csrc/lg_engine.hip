@@ -98,6 +98,7 @@ struct dlayer {
     float *att_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
     dweight q, k, v;        /* views into qkv when fused */
     bool qkv_fused = false;
+    bool qk_fused = false;  /* Q|K stacked in qkv, V of another type on its own */
     dweight qkv;
     dweight att_out;
     dweight up, gate;
@@ -399,17 +400,28 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     const bool q8act = lt == LG_Q8_0 || lt == LG_Q1_0;
     bool ok = m->n_embed <= PK_MAX_EMBED && m->n_ff <= PK_MAX_FF && m->n_embed % (q8act ? 32 : 256) == 0 &&
               m->n_ff % (q8act ? 32 : 256) == 0 && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
-              m->n_kv_heads <= 32 && m->n_heads <= 32 && ctx->output.cols == m->n_embed && ctx->arena.ok;
+              m->n_kv_heads <= 32 && m->n_heads <= 32 && ctx->output.cols == m->n_embed;
+    /* uniform: every layer matrix of type lt (the persistent kernel's and
+     * the fused step's case); otherwise the fused step also takes layers
+     * whose V (Q|K stacked) and down matrices are of a side type */
+    bool uniform = ok && ctx->arena.ok;
     for (int l = 0; ok && l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
-        ok = D.qkv_fused && D.ug_fused && pk_shape_ok(D.qkv, lt, m->n_embed + 2 * m->kv_dim, m->n_embed) &&
-             pk_shape_ok(D.att_out, lt, m->n_embed, m->n_embed) && pk_shape_ok(D.ug, lt, 2 * m->n_ff, m->n_embed) &&
-             pk_shape_ok(D.down, lt, m->n_embed, m->n_ff);
+        const int ne = m->n_embed, kvd = m->kv_dim;
+        const bool qkv_u = D.qkv_fused && pk_shape_ok(D.qkv, lt, ne + 2 * kvd, ne);
+        const bool qkv_m = D.qk_fused && pk_shape_ok(D.qkv, lt, ne + kvd, ne) && lg_fused_side_type(lt, D.v.type) &&
+                           pk_shape_ok(D.v, D.v.type, kvd, ne);
+        const bool down_u = pk_shape_ok(D.down, lt, ne, m->n_ff);
+        const bool down_m = lg_fused_side_type(lt, D.down.type) && pk_shape_ok(D.down, D.down.type, ne, m->n_ff);
+        ok = D.ug_fused && pk_shape_ok(D.att_out, lt, ne, ne) && pk_shape_ok(D.ug, lt, 2 * m->n_ff, ne) &&
+             (qkv_u || qkv_m) && (down_u || down_m);
+        uniform = uniform && qkv_u && down_u;
     }
+    uniform = uniform && ok;
     /* the fused kernels come in width classes; the persistent kernel is
      * instantiated for n_embed 4096 / n_ff 12288 only */
     const void* fused = ok ? lg_fused_variant(lt, ctx->output.type, m->head_dim, nrep, m->n_embed, m->n_ff) : nullptr;
-    const void* kern = ok && m->n_embed == 4096 && m->n_ff == 3 * m->n_embed
+    const void* kern = uniform && m->n_embed == 4096 && m->n_ff == 3 * m->n_embed
                            ? lg_persist_kernel(lt, ctx->output.type, m->head_dim, nrep)
                            : nullptr;
     if (!kern && !fused) return LG_OK;   /* the multi-kernel path serves this model */
@@ -427,6 +439,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.ao = D.att_out.data; P.ao_rsz = D.att_out.rsz; P.ao_t = D.att_out.type;
         P.ug = D.ug.data; P.ug_rsz = D.ug.rsz; P.ug_t = D.ug.type;
         P.down = D.down.data; P.down_rsz = D.down.rsz; P.down_t = D.down.type;
+        P.v = D.qk_fused ? D.v.data : nullptr; P.v_rsz = D.v.rsz; P.v_t = D.v.type;
         P.att_norm = D.att_norm; P.ffn_norm = D.ffn_norm; P.q_norm = D.q_norm; P.k_norm = D.k_norm;
     }
     PkLayer* dl = nullptr;
@@ -957,6 +970,14 @@ static int load_model_impl(lg_ctx* ctx, const lg_model_desc* m)
             if ((rc = upload_stacked(ctx, ws, 3, D.qkv, views, slot(AR.qkv, AR.qkv_b, l)))) return rc;
             D.q = views[0]; D.k = views[1]; D.v = views[2];
             D.qkv_fused = true;
+        } else if (L.att_q.type == L.att_k.type && L.att_q.rsz == L.att_k.rsz) {
+            /* a Q4_K_M-style V of its own type: Q|K still one matrix */
+            const lg_weight* ws[2] = {&L.att_q, &L.att_k};
+            dweight views[2];
+            if ((rc = upload_stacked(ctx, ws, 2, D.qkv, views, nullptr))) return rc;
+            D.q = views[0]; D.k = views[1];
+            if ((rc = upload_weight(ctx, L.att_v, D.v))) return rc;
+            D.qk_fused = true;
         } else {
             if ((rc = upload_weight(ctx, L.att_q, D.q))) return rc;
             if ((rc = upload_weight(ctx, L.att_k, D.k))) return rc;

@@ -67,6 +67,28 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv(const PkParams P, const Pk
         f_tr(Sd, l, 0), f_atr(atr, P, 4 * l), ne);
 }
 
+/* Q|K and V of different types (L.v): one rmsnorm build, the Q|K rows,
+ * then the V rows on the activation the first sweep left in LDS, mapped to
+ * start on the waves the Q|K rows left with fewer items */
+template <int LT, int VT, class S, bool EMB>
+__global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
+                                                       int l, uint8_t* atr)
+{
+    constexpr int NE = S::NE;
+    const int ne = P.n_embed, kvd = P.kv_dim, qs = ne + 2 * kvd;
+    float* xin = P.xs + (size_t)l * ne;
+    float* out = P.qkv + (size_t)l * qs;
+    const int pos = Sd->pos;
+    const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
+    phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, S::CE, LG_QKV_R>(
+        P, tok, L.qkv, L.qkv_rsz, ne + kvd, 0, L.att_norm, xin, nullptr, out, xin, 0, 0, f_tr(Sd, l, 0),
+        f_atr(atr, P, 4 * l), ne);
+    const int nwv = gridDim.x * PK_WAVES, left = (ne + kvd) % nwv;
+    phase_mv<VT, NE, (Batch<VT, NE, 1, 2, 512>::value), 1, EPI_STORE, BLD_KEEP, S::CE, LG_QKV_R>(
+        P, tok, L.v, L.v_rsz, kvd, 0, nullptr, nullptr, nullptr, out + ne + kvd, nullptr, 0, 0, nullptr, nullptr, ne,
+        MergeSrc{nullptr, nullptr, 0, 0}, left ? nwv - left : 0);
+}
+
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
  * position); otherwise one-head single-batch units.  Two kernels, so the
  * short-context one carries no long-context code or registers. */
@@ -148,19 +170,65 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 /* ------------------------------------------------------------------ */
 typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t, uint8_t*);
 
+/* the V and down types a layer of type LT may carry besides LT itself */
+template <int LT>
+static constexpr bool f_mixable() { return LT == LG_Q4_K || LT == LG_Q5_K; }
+
+bool lg_fused_side_type(int lt, int t)
+{
+    return t == lt || ((lt == LG_Q4_K || lt == LG_Q5_K) && (t == LG_Q5_K || t == LG_Q6_K));
+}
+
+/* phase 0 of layer l: Q|K|V stacked, or Q|K and a V of its own type */
+template <int LT, class SH>
+static void f_launch_qkv(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
+                         uint8_t* atr)
+{
+    if constexpr (f_mixable<LT>()) {
+        if (L.v) {
+#define QKV2(VT)                                                                                                \
+    do {                                                                                                        \
+        if (l == 0) hipLaunchKernelGGL((k_f_qkv2<LT, VT, SH, true>), g, b, 0, st, P, L, S, l, atr);            \
+        else hipLaunchKernelGGL((k_f_qkv2<LT, VT, SH, false>), g, b, 0, st, P, L, S, l, atr);                   \
+    } while (0)
+            if (L.v_t == LG_Q6_K) QKV2(LG_Q6_K);
+            else if (L.v_t == LG_Q5_K) QKV2(LG_Q5_K);
+            else QKV2(LT);
+#undef QKV2
+            return;
+        }
+    }
+    if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, SH, true>), g, b, 0, st, P, L, S, l, atr);
+    else hipLaunchKernelGGL((k_f_qkv<LT, SH, false>), g, b, 0, st, P, L, S, l, atr);
+}
+
+/* phase 4 of layer l: down rows of the layer's down type */
+template <int LT, class SH>
+static void f_launch_down(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
+                          uint8_t* atr)
+{
+    if constexpr (f_mixable<LT>()) {
+        if (L.down_t != LT) {
+            if (L.down_t == LG_Q6_K) hipLaunchKernelGGL((k_f_down<LG_Q6_K, SH>), g, b, 0, st, P, L, S, l, atr);
+            else hipLaunchKernelGGL((k_f_down<LG_Q5_K, SH>), g, b, 0, st, P, L, S, l, atr);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_f_down<LT, SH>), g, b, 0, st, P, L, S, l, atr);
+}
+
 template <int LT, int OT, int HD, int NREP, class SH>
 static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n_layers, int nwg, bool long_ctx,
                           hipStream_t st, uint8_t* atr)
 {
     const dim3 g(nwg), b(PK_THREADS);
     for (int l = 0; l < n_layers; l++) {
-        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, atr);
-        else hipLaunchKernelGGL((k_f_qkv<LT, SH, false>), g, b, 0, st, P, Lh[l], S, l, atr);
+        f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, atr);
         hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
-        hipLaunchKernelGGL((k_f_down<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
+        f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
     }
     hipLaunchKernelGGL((k_f_out<OT, SH>), g, b, 0, st, P, S, atr);
 }
@@ -174,17 +242,14 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
 {
     const dim3 g(nwg), b(PK_THREADS);
     switch (phase) {
-    case 0:
-        if (l == 0) hipLaunchKernelGGL((k_f_qkv<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, nullptr);
-        else hipLaunchKernelGGL((k_f_qkv<LT, SH, false>), g, b, 0, st, P, Lh[l], S, l, nullptr);
-        break;
+    case 0: f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
     case 1:
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         break;
     case 2: hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
     case 3: hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
-    case 4: hipLaunchKernelGGL((k_f_down<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    case 4: f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
     default: hipLaunchKernelGGL((k_f_out<OT, SH>), g, b, 0, st, P, S, nullptr); break;
     }
 }

@@ -12,7 +12,9 @@
 #define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
 #define PK_ATT_MAX_NCH 160  /* attention chunks per head at most */
 
-/* one layer as the kernel reads it: fused Q|K|V and up|gate matrices */
+/* one layer as the kernels read it: fused Q|K|V and up|gate matrices; in
+ * the fused step's mixed layers (v != NULL) qkv is Q|K and V a matrix of
+ * its own type v_t, and down_t may differ from the layer type */
 struct PkLayer {
     const uint8_t* qkv;
     const uint8_t* ao;
@@ -24,6 +26,9 @@ struct PkLayer {
     const float* ffn_norm;
     const float* q_norm;     /* NULL for llama */
     const float* k_norm;
+    const uint8_t* v;        /* NULL: V is part of qkv */
+    uint32_t v_rsz;
+    int v_t;
 };
 
 struct PkParams {
@@ -174,6 +179,10 @@ __host__ __device__ inline bool pk_att_long(int pos, int head_dim, int nrep, int
  * when the variant is not instantiated.  long_ctx = pk_att_long(pos, ...) of
  * the step's position selects the attention kernel. */
 const void* lg_fused_variant(int layer_type, int out_type, int head_dim, int nrep, int n_embed, int n_ff);
+/* whether the fused step takes a V or down matrix of type t among layers of
+ * layer_type (Q4_K_M / Q4_K_S / Q5_K_M-style mixes: Q5_K or Q6_K among Q4_K
+ * or Q5_K layers) */
+bool lg_fused_side_type(int layer_type, int t);
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
                      bool long_ctx, hipStream_t s, uint8_t* act_trace = nullptr);
 /* one kernel of the fused step: phase 0 rmsnorm+QKV, 1 attention, 2 att_out,

@@ -148,8 +148,9 @@ __device__ __forceinline__ void stamp(uint64_t* tr, int k)
  * (the launch starts with invalidated caches). */
 /* BLD_RMS: rmsnorm of the source vector; BLD_EMB: rmsnorm of the embedding
  * row; BLD_PLAIN: the source vector as it is; BLD_MERGE: the attention
- * partials merged (MergeSrc) */
-enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3 };
+ * partials merged (MergeSrc); BLD_KEEP: the activation the previous sweep of
+ * the same kernel left in LDS (a second matrix on the same input) */
+enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3, BLD_KEEP = 4 };
 
 __device__ __forceinline__ int chunk_base(int c)
 {
@@ -384,14 +385,16 @@ struct Rows {
  * store, publish.  CPW = 256-value activation chunks per wave; NR = batches
  * of MAXB items held at once: 1 = load a batch, then compute it; NR >= 2 = a
  * ring in which NR - 1 batches load while one computes (the first NR - 1
- * batches load before the build). */
+ * batches load before the build).  rot shifts the item-to-wave mapping by
+ * that many waves (a second sweep starts on the waves the first left with
+ * fewer items). */
 template <int FMT, int NS, int MAXB, int K, int EPI, int BLD, int CPW, int NR>
 __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8_t* __restrict__ W, uint32_t rsz,
                                          int items, int kstride, const float* __restrict__ normw,
                                          const float* __restrict__ src, const float* __restrict__ res_src,
                                          float* __restrict__ out, float* __restrict__ emb_out,
                                          uint64_t wait_target, uint64_t sig, uint64_t* tr, uint8_t* atr, int n_act,
-                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0})
+                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0}, int rot = 0)
 {
     using F = Fmt<FMT>;
     constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q1_0 || FMT == LG_Q1_G) ? LG_Q8_0 : LG_Q8_K;
@@ -400,7 +403,8 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     const int nslots = n_act / F::VALS;
     const int lane = LG_TID & 63, wave = LG_TID >> 6;
     const int nwv = gridDim.x * PK_WAVES;
-    const int gw = blockIdx.x * PK_WAVES + wave;
+    int gw = blockIdx.x * PK_WAVES + wave + rot;   /* 0 <= rot < nwv */
+    gw -= gw >= nwv ? nwv : 0;
 #if LG_MV_SPREAD
     const int ist = nwv, i0 = gw;
     const int my = gw < items ? (items - gw + nwv - 1) / nwv : 0;
@@ -422,7 +426,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
     auto load_src = [&]() {
         if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
-        else if (!from_embed) as.load(src, n_act);
+        else if (!from_embed && BLD != BLD_KEEP) as.load(src, n_act);
     };
     auto load_res = [&](float* r, int b0) {
         if (EPI == EPI_RESID) {
@@ -453,7 +457,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     }
     stamp(tr, 1);
     if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out, n_act);
-    else {
+    else if (BLD != BLD_KEEP) {
         if (BLD == BLD_MERGE) mg.merge(ms.nch, as);
         build_plain<QT, CPW>(as, n_act);
     }

@@ -44,13 +44,19 @@ class ModelConfig:
     sigma: float = 0.02
     q1_direct: bool = False   # 1-bit layers drawn as Bernoulli signs + |N(0,sigma)| scales
     seed: int = 1234
-    # per-tensor types that replace layer_type in every layer, e.g.
-    # (("attn_v", Q6_K), ("ffn_down", Q6_K)) for a Q4_K_M-style mix
+    # per-tensor types that replace layer_type, in every layer ("attn_v") or
+    # in one ("attn_v.3", taking precedence), e.g. (("attn_v", Q6_K),
+    # ("ffn_down", Q6_K)) for a Q4_K_M-style mix
     overrides: tuple = ()
 
-    def tensor_type(self, tensor: str) -> int:
-        """The type of layer tensor `tensor` ("attn_q" .. "ffn_down")."""
-        return dict(self.overrides).get(tensor, self.layer_type)
+    def tensor_type(self, tensor: str, layer: int = None) -> int:
+        """The type of layer tensor `tensor` ("attn_q" .. "ffn_down") in
+        layer `layer` (None: the type every layer has without a per-layer
+        override)."""
+        o = dict(self.overrides)
+        if layer is not None and f"{tensor}.{layer}" in o:
+            return o[f"{tensor}.{layer}"]
+        return o.get(tensor, self.layer_type)
 
     @property
     def kv_dim(self) -> int:
@@ -69,15 +75,17 @@ class ModelConfig:
         """Bytes read per decode token: every layer weight, the output head,
         the norms and one embedding row."""
         ne, kv, ff = self.n_embed, self.kv_dim, self.n_ff
-        tt = self.tensor_type
-        per_layer = (ne * row_size(tt("attn_q"), ne) + kv * row_size(tt("attn_k"), ne) +
-                     kv * row_size(tt("attn_v"), ne) + ne * row_size(tt("attn_output"), ne) +
-                     ff * row_size(tt("ffn_up"), ne) + ff * row_size(tt("ffn_gate"), ne) +
-                     ne * row_size(tt("ffn_down"), ff) + 2 * ne * 4)
-        if self.arch == ARCH_QWEN3:
-            per_layer += 2 * self.head_dim * 4
-        return (self.n_layers * per_layer + self.vocab * row_size(self.out_type, ne) + ne * 4 +
-                row_size(self.embd_type, ne))
+        total = 0
+        for l in range(self.n_layers):
+            def tt(t):
+                return self.tensor_type(t, l)
+            total += (ne * row_size(tt("attn_q"), ne) + kv * row_size(tt("attn_k"), ne) +
+                      kv * row_size(tt("attn_v"), ne) + ne * row_size(tt("attn_output"), ne) +
+                      ff * row_size(tt("ffn_up"), ne) + ff * row_size(tt("ffn_gate"), ne) +
+                      ne * row_size(tt("ffn_down"), ff) + 2 * ne * 4)
+            if self.arch == ARCH_QWEN3:
+                total += 2 * self.head_dim * 4
+        return total + self.vocab * row_size(self.out_type, ne) + ne * 4 + row_size(self.embd_type, ne)
 
     def kv_bytes(self, pos: int) -> int:
         """fp16 K and V bytes the attention reads at position pos (all layers)."""
@@ -146,7 +154,7 @@ class HostModel:
                   "ffn_up": (ff, ne), "ffn_gate": (ff, ne), "ffn_down": (ne, ff)}
         for l in range(cfg.n_layers):
             for t in LAYER_TENSORS:
-                draw(f"blk.{l}.{t}.weight", cfg.tensor_type(t), *shapes[t])
+                draw(f"blk.{l}.{t}.weight", cfg.tensor_type(t, l), *shapes[t])
             m.norms[f"blk.{l}.attn_norm.weight"] = np.ones(ne, np.float32)
             m.norms[f"blk.{l}.ffn_norm.weight"] = np.ones(ne, np.float32)
             if cfg.arch == ARCH_QWEN3:

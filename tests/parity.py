@@ -61,9 +61,10 @@ def slot_formats(cfg):
         if any(t in (Q8_0, Q1_0, Q1_G) for t in types):
             return Q8_0
         return None
-    tt = cfg.tensor_type
     out = []
-    for _ in range(cfg.n_layers):
+    for l in range(cfg.n_layers):
+        def tt(t):
+            return cfg.tensor_type(t, l)
         out += [(form(tt("attn_q"), tt("attn_k"), tt("attn_v")), cfg.n_embed), (form(tt("attn_output")), cfg.n_embed),
                 (form(tt("ffn_up"), tt("ffn_gate")), cfg.n_embed), (form(tt("ffn_down")), cfg.n_ff)]
     out.append((form(cfg.out_type), cfg.n_embed))

@@ -8,11 +8,13 @@ on the fused and the multi-kernel path, the two paths must agree as on the
 long-context units with their 8-lane position groups) against the oracle's
 exact attention over the same fp16 cache.  The tiny parity config T runs
 its own tests (tests/test_gpu_decode.py) on the path AUTO picks, which is
-this one."""
+this one.  A model mixing V and down types per layer (Q4_K_M-style) runs the
+same tests on the fused path's mixed-layer kernels."""
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q4_K, Q6_K, Q8_0, LgError
+from ligguf_amd.lib import (PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q4_K, Q5_K, Q6_K, Q8_0,
+                            LgError)
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
 from parity import step_flips
 from test_gpu_decode import assert_flips_explained, one_step_flips, oracle_state, rel
@@ -29,6 +31,10 @@ SHAPES = [
     ModelConfig("small-w576-ff1376-hd64-q8", 0, 2, 576, 9, 9, 64, 1376, 1024, 2048, 1e4, 1e-5, Q8_0, Q8_0, Q8_0),
     # the tiny config's shape (head_dim 48) with a context long enough for the long-context units
     TINY.with_(name="tiny-ctx2048", n_context=2048),
+    # Q4_K_M / Q4_K_S-style layers: Q6_K attn_v and ffn_down in layer 0, none in layer 1, Q5_K in layer 2
+    # (Q|K one matrix, V on its own; the persistent kernel takes uniform layers only)
+    ModelConfig("qwen3-w4096-q4k-mixed", 1, 3, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q4_K, Q4_K, Q6_K,
+                overrides=(("attn_v.0", Q6_K), ("ffn_down.0", Q6_K), ("attn_v.2", Q5_K), ("ffn_down.2", Q5_K))),
 ]
 
 
