@@ -88,29 +88,44 @@ __device__ __forceinline__ void pf_store(const float v[4], const PfQ8K& q, int n
     }
 }
 
-/* block b of token t: rmsnorm(x_t) * w (w != NULL) or x_t, quantized (Q8_K
- * or Q8_0); the sum of squares in the decode kernels' order
- * (fast/lil_math.cpp:922-929) */
+/* token t (one workgroup of 4 waves): rmsnorm(x_t) * w (w != NULL) or
+ * x_t, quantized (Q8_K or Q8_0) block by block, wave w taking blocks w,
+ * w + 4, ...  The sum of squares in the decode kernels' order
+ * (lg_sumsq_chunked, fast/lil_math.cpp:922-929): eight 2048-strided chunk
+ * sets, each one wave sum, added in set order -- here sets v and v + 4 by
+ * wave v, the eight sums through LDS -- computed once per token. */
 template <int QT>
-__global__ __launch_bounds__(64) void k_pf_quant(const float* __restrict__ x, int ldx, const float* __restrict__ w,
-                                                 float eps, int n, PfQ8K q)
+__global__ __launch_bounds__(256) void k_pf_quant(const float* __restrict__ x, int ldx, const float* __restrict__ w,
+                                                  float eps, int n, PfQ8K q)
 {
-    const int lane = threadIdx.x, b = blockIdx.x, t = blockIdx.y;
+    __shared__ float s_ss[8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = blockIdx.x;
     const float* xr = x + (size_t)t * ldx;
     float scale = 1.0f;
     if (w) {
-        const float ss = lg_sumsq_chunked(xr, n, lane);
+        for (int v = wave; v < 8; v += 4) {
+            float p = 0.0f;
+            for (int i = 256 * v + 4 * lane; i < n; i += 2048) p += lg_sq4(*(const float4*)(xr + i));
+            const float sv = lg_wave_sum(p);
+            if (lane == 0) s_ss[v] = sv;
+        }
+        __syncthreads();
+        float ss = 0.0f;
+        for (int v = 0; v < 8; v++) ss += s_ss[v];
         scale = 1.0f / sqrtf(ss / (float)n + eps);
     }
-    const int base = b * 256 + 4 * lane;
-    const bool in = base < n;   /* Q8_0 widths that are no multiple of 256: zeros past the end, not stored */
-    const float4 tv = in ? *(const float4*)(xr + base) : make_float4(0.f, 0.f, 0.f, 0.f);
-    float v[4] = {tv.x, tv.y, tv.z, tv.w};
-    if (w && in) {
-        const float4 g = *(const float4*)(w + base);
-        v[0] = tv.x * scale * g.x; v[1] = tv.y * scale * g.y; v[2] = tv.z * scale * g.z; v[3] = tv.w * scale * g.w;
+    const int nb = (n + 255) / 256;
+    for (int b = wave; b < nb; b += 4) {
+        const int base = b * 256 + 4 * lane;
+        const bool in = base < n;   /* Q8_0 widths that are no multiple of 256: zeros past the end, not stored */
+        const float4 tv = in ? *(const float4*)(xr + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float v[4] = {tv.x, tv.y, tv.z, tv.w};
+        if (w && in) {
+            const float4 g = *(const float4*)(w + base);
+            v[0] = tv.x * scale * g.x; v[1] = tv.y * scale * g.y; v[2] = tv.z * scale * g.z; v[3] = tv.w * scale * g.w;
+        }
+        pf_store<QT>(v, q, n, t, b);
     }
-    pf_store<QT>(v, q, n, t, b);
 }
 
 /* hb = silu(gate) * up of token t (fast/ligguf_fast_qk.cpp:119-123), block b,
@@ -382,10 +397,10 @@ int lg_prefill_quantize(int qtype, const float* x, int ldx, const float* norm_w,
         lg_set_error("prefill quantize: bad arguments (type %d, n %d, T %d)", qtype, n, T);
         return LG_ERR_ARG;
     }
-    const dim3 grid((n + 255) / 256, T);
-    if (qtype == LG_Q8_K) hipLaunchKernelGGL(k_pf_quant<LG_Q8_K>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
-    else if (qtype == LG_Q8_0) hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
-    else hipLaunchKernelGGL(k_pf_quant<LG_F32>, grid, dim3(64), 0, s, x, ldx, norm_w, eps, n, q);
+    const dim3 grid(T), blk(256);
+    if (qtype == LG_Q8_K) hipLaunchKernelGGL(k_pf_quant<LG_Q8_K>, grid, blk, 0, s, x, ldx, norm_w, eps, n, q);
+    else if (qtype == LG_Q8_0) hipLaunchKernelGGL(k_pf_quant<LG_Q8_0>, grid, blk, 0, s, x, ldx, norm_w, eps, n, q);
+    else hipLaunchKernelGGL(k_pf_quant<LG_F32>, grid, blk, 0, s, x, ldx, norm_w, eps, n, q);
     return lg_check_launch("prefill quantize");
 }
 
