@@ -134,6 +134,7 @@ struct lg_ctx {
     bool pk_ok = false;          /* the loaded model fits it */
     int path = LG_PATH_AUTO;
     int pk_nwg = 0;
+    size_t pk_cnt_bytes = 0;     /* the zeroed block of counters and flags */
     PkParams pk = {};
     const void* pk_kernel = nullptr; /* the instantiation for this model */
     uint64_t* pk_trace = nullptr;    /* phase timestamps of the next persistent step */
@@ -483,16 +484,19 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.att_po = ws;
         P.att_pml = ws + L * slots * m->n_embed;
     }
-    /* one zeroed block for the counters and flags */
+    /* one zeroed block for the counters and flags; argmax partials for up
+     * to LG_OUT_MAX_WGS output-head workgroups per CU */
     const int nwg = ctx->pk_nwg;
-    const size_t cnt_bytes = 256 + (size_t)nwg * (8 + 4 + 4) + 32 * PK_ATT_MERGE * 4;
+    const size_t namax = (size_t)nwg * LG_OUT_MAX_WGS;
+    const size_t cnt_bytes = (size_t)nwg * 8 + namax * 8 + 256 + 32 * PK_ATT_MERGE * 4;
     uint8_t* blk = nullptr;
     if ((rc = dalloc(ctx, (void**)&blk, cnt_bytes))) return rc;
     LG_HIP_CHECK(hipMemset(blk, 0, cnt_bytes));
+    ctx->pk_cnt_bytes = cnt_bytes;
     P.progress = (uint64_t*)blk;                                   /* nwg x 8 B */
-    P.amax_v = (float*)(blk + (size_t)nwg * 8);                    /* nwg x 4 B */
-    P.amax_i = (int*)(blk + (size_t)nwg * 12);                     /* nwg x 4 B */
-    uint8_t* tail = blk + (size_t)nwg * 16;
+    P.amax_v = (float*)(blk + (size_t)nwg * 8);                    /* namax x 4 B */
+    P.amax_i = (int*)(blk + (size_t)nwg * 8 + namax * 4);          /* namax x 4 B */
+    uint8_t* tail = blk + (size_t)nwg * 8 + namax * 8;
     P.amax_cnt = (uint32_t*)tail;
     P.tok_out = (int*)(tail + 64);                                 /* {token, error} */
     P.err = (uint32_t*)(tail + 68);
@@ -520,8 +524,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
 /* the persistent kernel's counters after an expired wait: back to zero */
 static void pk_reset(lg_ctx* c)
 {
-    const size_t bytes = 256 + (size_t)c->pk_nwg * 16 + 64;
-    hipMemsetAsync(c->pk.progress, 0, bytes, c->stream);
+    hipMemsetAsync(c->pk.progress, 0, c->pk_cnt_bytes, c->stream);
     hipStreamSynchronize(c->stream);
     c->pk_base = 0;
 }

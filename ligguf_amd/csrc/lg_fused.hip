@@ -28,6 +28,13 @@
  */
 #include "lg_phase.h"
 
+/* output-head workgroups per CU: the head's rows need no more than one
+ * build per workgroup, and more workgroups hold more rows in flight */
+#ifndef LG_OUT_WGS
+#define LG_OUT_WGS 1
+#endif
+static_assert(LG_OUT_WGS >= 1 && LG_OUT_WGS <= LG_OUT_MAX_WGS, "argmax partials");
+
 /* trace slot of phase k of layer l for this workgroup (PkStep.trace) */
 __device__ __forceinline__ uint64_t* f_tr(const PkStep* Sd, int l, int k)
 {
@@ -154,9 +161,14 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 {
     constexpr int NO = S::NO;
     const int pos = Sd->pos;
+    /* the step trace holds one slot per workgroup of the layer grid: the
+     * first gridDim.x / LG_OUT_WGS workgroups stamp theirs */
+    const int nwg = gridDim.x / LG_OUT_WGS;
+    uint64_t* tr = Sd->trace && (int)blockIdx.x < nwg
+                       ? Sd->trace + ((size_t)5 * P.n_layers * nwg + blockIdx.x) * 4 : nullptr;
     phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, S::CE, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
-        nullptr, 0, 0, f_tr(Sd, P.n_layers, 0), f_atr(atr, P, 4 * P.n_layers), P.n_embed);
+        nullptr, 0, 0, tr, f_atr(atr, P, 4 * P.n_layers), P.n_embed);
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
     if (s_int[0] && threadIdx.x == 0) {
         Sd->tok = cld(P.tok_out);
@@ -230,7 +242,7 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
         hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
         f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
     }
-    hipLaunchKernelGGL((k_f_out<OT, SH>), g, b, 0, st, P, S, atr);
+    hipLaunchKernelGGL((k_f_out<OT, SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, atr);
 }
 
 typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, bool, hipStream_t);
@@ -250,7 +262,7 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
     case 2: hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
     case 3: hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
     case 4: f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
-    default: hipLaunchKernelGGL((k_f_out<OT, SH>), g, b, 0, st, P, S, nullptr); break;
+    default: hipLaunchKernelGGL((k_f_out<OT, SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, nullptr); break;
     }
 }
 

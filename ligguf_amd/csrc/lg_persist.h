@@ -11,6 +11,7 @@
 #define PK_MAX_NREP 8       /* query heads per KV head */
 #define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
 #define PK_ATT_MAX_NCH 160  /* attention chunks per head at most */
+#define LG_OUT_MAX_WGS 4     /* output-head workgroups per CU at most (argmax partials) */
 
 /* one layer as the kernels read it: fused Q|K|V and up|gate matrices; in
  * the fused step's mixed layers (v != NULL) qkv is Q|K and V a matrix of
