@@ -392,9 +392,13 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     LG_HIP_CHECK(hipGetDevice(&dev));
     LG_HIP_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
     int att_chunk = 0, att_nch = 0;
+    const int att_max = m->n_kv_heads > 0 ? ncu * LG_ATT_WGS / m->n_kv_heads : 0;
     if (m->head_dim > 0 && m->head_dim <= 128 && nrep >= 1 && nrep <= PK_MAX_NREP && m->n_kv_heads > 0)
-        pk_attn_split(m->n_context, m->head_dim, nrep, ncu / m->n_kv_heads, &att_chunk, &att_nch);
-    att_nch = std::max(att_nch, PK_ATT_MERGE);
+        pk_attn_split(m->n_context, m->head_dim, nrep, att_max, &att_chunk, &att_nch);
+    /* slots for the most chunks any position takes: the chunk size is
+     * rounded up to whole steps, so a shorter context can take more chunks
+     * than n_context does (up to the clamped att_max, never more) */
+    att_nch = std::max(std::min(std::max(att_max, PK_ATT_MERGE), PK_ATT_MAX_NCH), PK_ATT_MERGE);
     /* widths: any the activation builds hold (LDS staging of n_embed and of
      * the quantized n_ff vector), in whole 256-value Q8_K blocks for K-quant
      * and Q1_G layers; which widths have kernels is up to the variants */
@@ -481,6 +485,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         if ((rc = dalloc(ctx, (void**)&ws, L * slots * ((size_t)m->n_embed + 2 * m->n_heads) * sizeof(float))))
             return rc;
         P.att_slots = (int)slots;
+        P.att_grid = ncu * LG_ATT_WGS;
         P.att_po = ws;
         P.att_pml = ws + L * slots * m->n_embed;
     }

@@ -35,12 +35,14 @@
 #endif
 static_assert(LG_OUT_WGS >= 1 && LG_OUT_WGS <= LG_OUT_MAX_WGS, "argmax partials");
 
-/* trace slot of phase k of layer l for this workgroup (PkStep.trace) */
-__device__ __forceinline__ uint64_t* f_tr(const PkStep* Sd, int l, int k)
+/* trace slot of phase k of layer l for this workgroup (PkStep.trace, one
+ * slot per workgroup of an nwg-workgroup layer grid) */
+__device__ __forceinline__ uint64_t* f_tr_n(const PkStep* Sd, int l, int k, int nwg)
 {
     uint64_t* t = Sd->trace;
-    return t ? t + ((size_t)(5 * l + k) * gridDim.x + blockIdx.x) * 4 : nullptr;
+    return t ? t + ((size_t)(5 * l + k) * nwg + blockIdx.x) * 4 : nullptr;
 }
+__device__ __forceinline__ uint64_t* f_tr(const PkStep* Sd, int l, int k) { return f_tr_n(Sd, l, k, gridDim.x); }
 
 /* activation trace slot k (a kernel argument: NULL in the captured graph,
  * so a traced step is launched directly) */
@@ -100,12 +102,16 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const P
  * position); otherwise one-head single-batch units.  Two kernels, so the
  * short-context one carries no long-context code or registers. */
 template <int HD, int NREP, bool LONG>
-__global__ __launch_bounds__(PK_THREADS) void k_f_attn(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
-                                                       int l)
+__global__ __launch_bounds__(PK_THREADS) __attribute__((amdgpu_waves_per_eu(LONG ? 2 * LG_ATT_WGS : 2)))
+void k_f_attn(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l)
 {
     const int ne = P.n_embed, qs = ne + 2 * P.kv_dim;
     if constexpr (LONG) {
-        phase_attn<HD, NREP, NREP, true>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, f_tr(Sd, l, 1));
+        /* a grid of P.att_grid workgroups, LG_ATT_WGS per CU; the step trace
+         * holds the first gridDim.x / LG_ATT_WGS */
+        uint64_t* tr = (int)blockIdx.x < (int)gridDim.x / LG_ATT_WGS
+                           ? f_tr_n(Sd, l, 1, gridDim.x / LG_ATT_WGS) : nullptr;
+        phase_attn<HD, NREP, NREP, true, LG_ATT_WGS>(P, L, l, Sd->pos, P.qkv + (size_t)l * qs, 0, 0, tr);
     } else {
         /* the position through a vector load issued first (its index made
          * opaque, so the compiler keeps it per lane instead of moving it to
@@ -236,7 +242,7 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
     const dim3 g(nwg), b(PK_THREADS);
     for (int l = 0; l < n_layers; l++) {
         f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
-        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
+        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), dim3(P.att_grid), b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, atr);
         hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
@@ -256,7 +262,7 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
     switch (phase) {
     case 0: f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
     case 1:
-        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), g, b, 0, st, P, Lh[l], S, l);
+        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), dim3(P.att_grid), b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         break;
     case 2: hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;

@@ -12,6 +12,14 @@
 #define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
 #define PK_ATT_MAX_NCH 160  /* attention chunks per head at most */
 #define LG_OUT_MAX_WGS 4     /* output-head workgroups per CU at most (argmax partials) */
+/* long-context attention workgroups per CU: with 2 the fused step's kernel
+ * runs two side by side at 128 VGPRs (half the chunk length, q from LDS)
+ * and the persistent kernel takes the same units in turn, so both compute
+ * the same chunks; measured slower than one (Q1_G 8192-context decode 442
+ * against 478 tok/s), so one */
+#ifndef LG_ATT_WGS
+#define LG_ATT_WGS 1
+#endif
 
 /* one layer as the kernels read it: fused Q|K|V and up|gate matrices; in
  * the fused step's mixed layers (v != NULL) qkv is Q|K and V a matrix of
@@ -60,6 +68,7 @@ struct PkParams {
     float* att_po;           /* [n_layers][att_slots][n_embed] unnormalised attention partials */
     float* att_pml;          /* [n_layers][att_slots][n_heads][2] their (max, sum), log2 units */
     int att_slots;           /* per layer: one per chunk, then PK_ATT_MERGE for the groups merged in-kernel */
+    int att_grid;            /* long-context split: units sized for this many workgroups (LG_ATT_WGS per CU) */
     uint32_t* attn_cnt;      /* [unit head sets (n_kv * NREP / NQ <= 32)][PK_ATT_MERGE groups], zero between launches */
     uint64_t* progress;      /* one word per workgroup */
     float* amax_v;           /* per-workgroup argmax partials */

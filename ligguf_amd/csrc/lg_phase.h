@@ -243,10 +243,15 @@ struct MergeAct {
     }
 };
 
-/* long-context chunks per head: the grid's workgroups per head group */
+#ifndef LG_ATT_H2
+#define LG_ATT_H2 2
+#endif
+
+/* long-context chunks per head: the attention grid's workgroups per head
+ * group (the same for the fused and the persistent step) */
 __device__ __forceinline__ int pk_att_max_nch(const PkParams& P)
 {
-    return (int)gridDim.x / P.n_kv;
+    return P.att_grid / P.n_kv;
 }
 
 /* the attention partials of layer l at position pos as the att_out build
@@ -646,7 +651,7 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * the last unit of each group of pk_att_group chunks (atomic counter) merges
  * the group into one of the layer's PK_ATT_MERGE group slots.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
-template <int HD, int NREP, int NQ, bool BATCHES>
+template <int HD, int NREP, int NQ, bool BATCHES, int WPC = 1>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos_arg,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
                                            uint64_t* tr, bool stamp0 = true)
@@ -694,7 +699,12 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     /* K/V slices of the unit's steps (static indices only): one batch of
      * MAXST steps, or (BATCHES) two sets of MAXST/2 steps, the next one
      * loading while the other computes */
-    constexpr int NB = BATCHES ? 2 : 1, H = MAXST / NB;
+    /* WPC = 2: two workgroups per CU (128 VGPRs): 1 / LG_ATT_H2 of the
+     * steps per set, q read from LDS */
+    static_assert(WPC == 1 || (WPC == 2 && BATCHES), "two workgroups per CU: long-context units");
+    constexpr int NB = BATCHES ? 2 : 1, H0 = WPC == 1 ? MAXST / NB : MAXST / NB / LG_ATT_H2;
+    constexpr int H = H0 < 1 ? 1 : H0;   /* steps per register set */
+    static_assert(H >= 1, "a register set holds at least one step");
     uint4 kb[NB][H], vb[NB][H];
     float4 hx[NH], hv;            /* this wave's heads h = wave + PK_WAVES*j: q (h < NQ) or k, and v */
     /* unconditional loads (see Rows): positions outside the unit and the
@@ -808,12 +818,13 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         if (u == (int)blockIdx.x) stamp(tr, 1);
         /* q in registers; with 8 query heads per KV head it is re-read from
          * LDS each step (registers go to K/V and the accumulators) */
-        constexpr int QREG = NQ <= 4 ? NQ : 1;
+        constexpr bool QIN = NQ <= 4 && WPC == 1;   /* q in registers */
+        constexpr int QREG = QIN ? NQ : 1;
         float qr[QREG][8];
 #pragma unroll
         for (int r = 0; r < QREG; r++)
 #pragma unroll
-            for (int i = 0; i < 8; i++) qr[r][i] = s_q[r * HDP + gl * 8 + i];
+            for (int i = 0; i < 8; i++) qr[r][i] = QIN ? s_q[r * HDP + gl * 8 + i] : 0.0f;
 
         /* one pass: scores, online softmax, p.V (t == pos uses the fp32 k/v
          * of this step, fast/ligguf_fast_qk.cpp:77-79,98-99) */
@@ -843,7 +854,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
                     for (int r = 0; r < NQ; r++) {
                         float qv[8];
 #pragma unroll
-                        for (int i = 0; i < 8; i++) qv[i] = NQ <= 4 ? qr[r < QREG ? r : 0][i] : s_q[r * HDP + gl * 8 + i];
+                        for (int i = 0; i < 8; i++) qv[i] = QIN ? qr[r < QREG ? r : 0][i] : s_q[r * HDP + gl * 8 + i];
                         float sc = 0.0f;
 #pragma unroll
                         for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];

@@ -106,8 +106,9 @@ def att_split(ctx_len, head_dim=128, nrep=4, max_nch=32):
     """(chunk, chunks) of the whole-step long-context attention: the host
     formula pk_attn_split (ligguf_amd/csrc/lg_persist.h) restated, 512
     threads x 8 halves per head_dim-wide row per workgroup step, at most 8
-    chunks merged by the att_out build, else max_nch chunks (the grid's
-    workgroups per KV head, 256 / 8 here) merged in at most 8 groups."""
+    chunks merged by the att_out build, else max_nch chunks (the attention
+    grid's workgroups per KV head, 256 / 8 here) merged in at most 8
+    groups."""
     ppb = 512 * 8 // head_dim
     steps = 4 if nrep > 4 else 8
     chunk = -(-ctx_len // 8)
@@ -134,7 +135,7 @@ def oracle_step_from_cache(oracle, hm, k_layers, v_layers, pos, tok):
 # 300: 3 fixed chunks merged by the att_out build; 2899: 31 chunks in 8 groups
 # of 4, the last group holding 3 (a partial group); 3001: 32 chunks, 8 full
 # groups (on 256 workgroups)
-@pytest.mark.parametrize("want_pos", [300, 2899, 3001], ids=["merged-by-att-out", "partial-group", "full-groups"])
+@pytest.mark.parametrize("want_pos", [300, 2899, 3071], ids=["merged-by-att-out", "partial-group", "full-groups"])
 @pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
 def test_long_context_attention(pk_model, oracle, path, want_pos):
     """Decode at a long position over a random fp16 cache: the whole-step
@@ -182,10 +183,11 @@ def long_model(gpu):
 @pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
 def test_long_context_attention_batches(long_model, oracle, path):
     """At 10000 positions the context is cut into one chunk per workgroup of
-    the head group's share of the grid (32 on 256 CUs), each chunk longer
-    than one register batch (320 positions: two batches), whole query-head
-    groups per unit, merged by the last unit of each head: against the
-    multi-kernel split from the same random fp16 cache."""
+    the head group's share of the attention grid (32 on 256 workgroups),
+    each chunk longer than one register batch (320 positions: ten steps of
+    32 in register sets of four), whole query-head groups per unit, merged
+    by the last unit of each group: against the multi-kernel split from the
+    same random fp16 cache."""
     hm, eng = long_model
     cfg = hm.cfg
     pos = 10000
@@ -212,6 +214,47 @@ def test_long_context_attention_batches(long_model, oracle, path):
     other = PATH_PERSISTENT if path == PATH_FUSED else PATH_FUSED
     eng.set_path(other)
     assert np.array_equal(eng.decode(7, pos).view(np.uint32), res[path].view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def ctx4100_model(gpu):
+    cfg = ModelConfig("qwen3-w4096-ctx4100", 1, 1, 4096, 32, 8, 128, 12288, 2048, 4100, 1e6, 1e-6, Q4_K, Q4_K, Q6_K)
+    hm = HostModel.synthetic(cfg)
+    eng = Engine(0)
+    eng.load(hm)
+    yield hm, eng
+    eng.close()
+
+
+def test_long_context_more_chunks_than_at_n_context(ctx4100_model, oracle):
+    """Chunk sizes are rounded up to whole steps, so a context shorter than
+    n_context can take more chunks: 4096 positions take 32 chunks of 128,
+    4100 take 26 of 160.  The partial slots are sized for the most chunks any
+    position takes (sized for n_context's 26, chunks 26..31 landed on the
+    group slots); the step at position 4095 against the oracle's exact
+    attention and the multi-kernel split, fused equal to persistent."""
+    hm, eng = ctx4100_model
+    cfg = hm.cfg
+    pos = 4095
+    assert att_split(pos + 1)[1] == 32 and att_split(cfg.n_context)[1] == 26
+    rng = np.random.default_rng(6)
+    k = rng.standard_normal(pos * cfg.kv_dim).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(pos * cfg.kv_dim).astype(np.float16).view(np.uint16)
+    eng.kv_write(0, 1, 0, pos, k, v)
+    eng.set_path(PATH_MULTI)
+    multi = eng.decode(7, pos)
+    eng.set_path(PATH_FUSED)
+    g, gtr = eng.decode_traced(7, pos)
+    o, otr = oracle_step_from_cache(oracle, hm, [k], [v], pos, 7)
+    first, bad = step_flips(gtr, otr, cfg)
+    e, em = rel(g, o), rel(g, multi)
+    print(f"\n{cfg.name}: pos {pos} vs oracle {e:.2e} (first int8 difference at activation {first}), "
+          f"vs multi {em:.2e}")
+    assert not bad, bad[:5]
+    assert e <= (1e-5 if first < 0 else 3e-2)
+    assert em <= 3e-2
+    eng.set_path(PATH_PERSISTENT)
+    assert np.array_equal(eng.decode(7, pos).view(np.uint32), g.view(np.uint32))
 
 
 @pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
