@@ -17,6 +17,13 @@ only by flips: every differing value one step away, and the oracle's
 pre-rounding value within FLIP_TOL of k + 1/2.  Everything after it in the
 step depends on the flipped value, so the walk stops there.  A step with no
 differing int8 at all must match the oracle's logits to fp32 noise.
+
+Q8_0 blocks also carry an fp16 scale, fp16(amax / 127), which the next matvec
+multiplies in: when amax / 127 lies on an fp16 rounding tie, an amax one fp32
+ulp apart rounds the scale one fp16 ulp (~1e-3) the other way with every int8
+equal.  A differing Q8_0 scale is therefore a difference of its activation
+too, a flip when the oracle's amax / 127 is within SCALE_TIE_TOL fp16 ulps of
+a tie.
 """
 from __future__ import annotations
 
@@ -45,6 +52,10 @@ MAX_FLIP_FRAC = 0.02
 # the block holding the maximum scale to exact halves (127 q / 32 for q = 16)
 # -- 60-80 of 1024 per token on the synthetic Q6_K models.
 TIE_TOL = 1e-4
+# distance (in fp16 ulps) of a Q8_0 block's amax / 127 from an fp16 rounding
+# tie below which a scale one fp16 ulp off counts as a flip: amax moves by
+# ~1e-7..1e-5 relative between two correct paths (1e-4..1e-2 of an fp16 ulp)
+SCALE_TIE_TOL = 0.1
 # logits rel-L2 of a step whose int8 activations all agree with the oracle's
 EXACT_STEP = 1e-5
 
@@ -113,6 +124,28 @@ def boundary_dist(v: np.ndarray) -> np.ndarray:
     return np.abs(a - np.floor(a) - 0.5)
 
 
+def scale_diffs(buf: np.ndarray, x: np.ndarray, qtype: int, n: int):
+    """Q8_0 blocks whose fp16 scale in `buf` differs from fp16(amax / 127) of
+    the oracle's values x (quantize_q8_0, fast/lil_math.cpp:363-394): the
+    blocks and, per block, the distance of amax / 127 from an fp16 rounding
+    tie in fp16 ulps -- or 1.0 when the two scales are not neighbours.
+    Empty for other forms."""
+    if qtype != Q8_0:
+        return np.zeros(0, np.int64), np.zeros(0)
+    _, dg = parse_q(buf, qtype, n)
+    amax = np.abs(np.asarray(x[:n], np.float32).reshape(-1, 32)).max(axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    d16 = d.astype(np.float16).astype(np.float32)
+    diff = np.nonzero(dg != d16)[0]
+    dd = d[diff].astype(np.float64)
+    e = np.maximum(np.floor(np.log2(np.where(dd > 0, dd, 1.0))), -14.0)   # fp16 subnormals: ulp 2^-24
+    ulp = 2.0 ** (e - 10)
+    f = dd / ulp
+    dist = np.abs(f - np.floor(f) - 0.5)
+    neighbours = np.abs(dg[diff].astype(np.float64) - d16[diff]) <= ulp * 1.0000001
+    return diff, np.where(neighbours, dist, 1.0)
+
+
 def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
     """(first differing activation or -1, list of unexplained differences).
 
@@ -124,7 +157,8 @@ def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
         qg, _ = parse_q(gpu_trace[k], qt, n)
         qo, v = quantize_ref(oracle_trace[k][:n], qt)
         diff = np.nonzero(qg != qo)[0]
-        if diff.size == 0:
+        sdiff, sdist = scale_diffs(gpu_trace[k], oracle_trace[k], qt, n)
+        if diff.size == 0 and sdiff.size == 0:
             continue
         bad = []
         nties = int(np.sum(boundary_dist(v[diff]) < TIE_TOL))
@@ -135,6 +169,9 @@ def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
             dist = float(boundary_dist(v[i:i + 1])[0])
             if step != 1 or dist > FLIP_TOL:
                 bad.append((k, int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
+        for b, dist in zip(sdiff, sdist):
+            if dist > SCALE_TIE_TOL:
+                bad.append((k, -2, int(b), 0, 0.0, float(dist)))     # a scale off an fp16 tie
         return k, bad
     return -1, []
 
@@ -168,7 +205,8 @@ def prefill_flips(gpu_trace: np.ndarray, oracle_traces, cfg):
             qo, v = quantize_ref(oracle_traces[t][k][:w], qt)
             compared += 1
             diff = np.nonzero(qg != qo)[0]
-            if diff.size == 0:
+            sdiff, sdist = scale_diffs(gpu_trace[t][k], oracle_traces[t][k], qt, w)
+            if diff.size == 0 and sdiff.size == 0:
                 continue
             differing += 1
             first[t] = k
@@ -180,6 +218,9 @@ def prefill_flips(gpu_trace: np.ndarray, oracle_traces, cfg):
                 dist = float(boundary_dist(v[i:i + 1])[0])
                 if step != 1 or dist > FLIP_TOL:
                     bad.append((t, k, int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
+            for b, dist in zip(sdiff, sdist):
+                if dist > SCALE_TIE_TOL:
+                    bad.append((t, k, -2, int(b), 0, 0.0, float(dist)))
     return compared, differing, bad, bool(first.min() > nk)
 
 
@@ -193,6 +234,6 @@ def flip_summary(rows):
            f"{flips} with rounding flips only, {bad} unexplained"
 
 
-__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "TIE_TOL", "EXACT_STEP", "slot_formats", "parse_q", "quantize_ref", "step_flips",
-           "prefill_flips", "flip_summary",
+__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "TIE_TOL", "SCALE_TIE_TOL", "EXACT_STEP", "slot_formats", "parse_q",
+           "quantize_ref", "scale_diffs", "step_flips", "prefill_flips", "flip_summary",
            "F16", "F32"]

@@ -142,3 +142,37 @@ def test_ties_do_not_count_against_the_cap(oracle):
         g2[0][blk * 34 + 2 + j] = np.uint8(64)
     first, bad = step_flips(g2, ot2, cfg)
     assert first == 0 and bad and bad[0][1] == -1
+
+
+def test_scale_flips(oracle):
+    """A Q8_0 block scale one fp16 ulp off is a flip when amax / 127 lies on an
+    fp16 rounding tie, and unexplained off a tie or more than one ulp off."""
+    cfg = TINY.with_(n_layers=1)
+    n = cfg.n_embed
+    rng = np.random.default_rng(5)
+    ulp = 2.0 ** -16                       # fp16 spacing in [2^-6, 2^-5)
+    x = (rng.standard_normal(n) * 0.2).astype(np.float32)
+    x = np.clip(x, -1.0, 1.0)
+
+    def run(m, planted):
+        xs = x.copy()
+        xs[64] = np.float32(127 * m * ulp)            # block 2's maximum: amax / 127 = m fp16 ulps exactly
+        assert np.float32(xs[64]) / np.float32(127) == np.float32(m * ulp)
+        ot = np.zeros((4 * cfg.n_layers + 1, max(n, cfg.n_ff)), np.float32)
+        ot[0][:n] = xs
+        gt = np.zeros((4 * cfg.n_layers + 1, 1024), np.uint8)
+        for k, (qt, w) in enumerate(slot_formats(cfg)):
+            b = oracle.quantize_q8_0(ot[k][:w])
+            gt[k][:b.size] = b
+        assert step_flips(gt, ot, cfg) == (-1, [])
+        gt[0][2 * 34:2 * 34 + 2] = np.frombuffer(np.float16(planted * ulp).tobytes(), np.uint8)
+        return step_flips(gt, ot, cfg)
+
+    # 1171.5 ulps: a tie, fp16 rounds to the even 1172; 1171 is the other side
+    assert run(1171.5, 1171) == (0, [])
+    # 1171.25 ulps rounds to 1171 with no tie near: 1172 is no flip
+    first, bad = run(1171.25, 1172)
+    assert first == 0 and bad and bad[0][1] == -2 and bad[0][2] == 2
+    # two ulps off a tie is no flip either
+    first, bad = run(1171.5, 1170)
+    assert first == 0 and bad and bad[0][5] == 1.0
