@@ -374,6 +374,41 @@ static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const
 #define LG_STEP_RING 64   /* pinned step records in flight before a forced sync */
 /* the persistent kernel reads every layer matrix at width n_embed = 4096
  * (n_ff = 12288 for down), one type for all layer matrices */
+/* The output head regrouped for the whole-step kernels' aligned loads
+ * (Fmt<LG_Q8_0_R>, Fmt<LG_Q6_K_R>): each run of 8 blocks of a row becomes
+ * its quants, then its scales (Q6_K: ql, qh, scales, d).  Only for widths of
+ * whole groups on 16-byte row boundaries; empty otherwise. */
+static std::vector<uint8_t> repack_rows(const lg_weight& w)
+{
+    std::vector<uint8_t> out;
+    if (!w.data || w.cols <= 0) return out;
+    const bool q8 = w.type == LG_Q8_0 && w.cols % 256 == 0;
+    const bool q6 = w.type == LG_Q6_K && w.cols % 2048 == 0;
+    if (!q8 && !q6) return out;
+    const size_t bs = q8 ? LG_BS_Q8_0 : LG_BS_Q6_K, ng = (size_t)w.cols / (q8 ? 256 : 2048);
+    if (w.rsz != ng * 8 * bs) return out;
+    out.resize((size_t)w.rows * w.rsz);
+    const uint8_t* src = (const uint8_t*)w.data;
+    for (size_t r = 0; r < (size_t)w.rows; r++)
+        for (size_t g = 0; g < ng; g++) {
+            const uint8_t* in = src + r * w.rsz + g * 8 * bs;
+            uint8_t* o = out.data() + r * w.rsz + g * 8 * bs;
+            for (int j = 0; j < 8; j++) {
+                const uint8_t* b = in + j * bs;
+                if (q8) {
+                    memcpy(o + 256 + 2 * j, b, 2);          /* d */
+                    memcpy(o + 32 * j, b + 2, 32);          /* qs */
+                } else {
+                    memcpy(o + 128 * j, b, 128);            /* ql */
+                    memcpy(o + 1024 + 64 * j, b + 128, 64); /* qh */
+                    memcpy(o + 1536 + 16 * j, b + 192, 16); /* scales */
+                    memcpy(o + 1664 + 2 * j, b + 208, 2);   /* d */
+                }
+            }
+        }
+    return out;
+}
+
 static bool pk_shape_ok(const dweight& w, int type, int rows, int cols)
 {
     return w.type == type && w.rows == rows && w.cols == cols;
@@ -462,6 +497,16 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.n_ctx = m->n_context; P.rope_dim = m->rope_dim; P.eps = m->rms_epsilon;
     P.embd = ctx->embd.data; P.embd_rsz = ctx->embd.rsz; P.embd_t = ctx->embd.type;
     P.out_w = ctx->output.data; P.out_rsz = ctx->output.rsz; P.out_t = ctx->output.type;
+    P.out_wr = nullptr;
+    if (fused) {
+        const std::vector<uint8_t> rp = repack_rows(m->output);
+        if (!rp.empty()) {
+            uint8_t* d = nullptr;
+            if ((rc = dalloc(ctx, (void**)&d, rp.size()))) return rc;
+            if ((rc = h2d(d, rp.data(), rp.size()))) return rc;
+            P.out_wr = d;
+        }
+    }
     P.out_norm = ctx->out_norm; P.rope_freq = ctx->rope_freq;
     P.kc = ctx->kc; P.vc = ctx->vc;
     P.logits = ctx->logits;

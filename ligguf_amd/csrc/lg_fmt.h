@@ -99,6 +99,10 @@ struct Fmt;
 /* Q4_K (144 B: d, dmin, scales[12], qs[128]); slot (block b, pair c) =
  * sub-blocks 2c (low nibbles of qs[32c..32c+31]) and 2c+1 (high nibbles).
  * dot_q8_K_q4_K: fast/lil_math.cpp:582-616, fast/arch_avx2.h:272-323. */
+/* regrouped output-head forms (see Fmt<LG_Q8_0_R>) */
+#define LG_Q8_0_R 108
+#define LG_Q6_K_R 114
+
 template <>
 struct Fmt<LG_Q4_K> {
     static constexpr int VALS = 64;
@@ -240,6 +244,20 @@ struct Fmt<LG_Q6_K> {
     }
 };
 
+template <>
+struct Fmt<LG_Q6_K_R> : Fmt<LG_Q6_K> {
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s)
+    {
+        const int blk = s >> 2, n = (s & 3) >> 1, sh = s & 1, j = blk & 7;
+        const uint8_t* g = row + (size_t)(blk >> 3) * (8 * LG_BS_Q6_K);
+        w.a = *(const uint4*)(g + 128 * j + 64 * n + 16 * sh);
+        w.b = *(const uint4*)(g + 128 * j + 64 * n + 32 + 16 * sh);
+        w.h = *(const uint4*)(g + 1024 + 64 * j + 32 * n + 16 * sh);
+        w.sc = *(const uint2*)(g + 1536 + 16 * j + 8 * n);
+        w.d = *(const uint16_t*)(g + 1664 + 2 * j);
+    }
+};
+
 /* Q2_K (84 B: scales[16], qs[64], d, dmin); slot (block, half n, h) =
  * values 128n + 32j + 16h + l, q = (qs[32n+16h+l] >> 2j) & 3.
  * fast/lil_math.cpp:539-580, fast/arch_avx2.h:160-212 */
@@ -346,6 +364,24 @@ struct Fmt<LG_Q8_0> {
 #pragma unroll
         for (int i = 0; i < 8; i++) S = lg_dot4((int)q[i], A.a[i], S);
         return lg_h2f((uint16_t)w.d) * A.d * (float)S;
+    }
+};
+
+/* Q8_0 and Q6_K rows regrouped for aligned loads (an output head copy that
+ * only the whole-step kernels read; lg_repack_rows).  Each run of 8 blocks
+ * of a row becomes one group: Q8_0 (272 B) the 8 x 32 quants, then the 8
+ * fp16 scales; Q6_K (1680 B) the 8 x 128 ql bytes, the 8 x 64 qh, the 8 x
+ * 16 scales, the 8 fp16 d.  Groups, and so every 16-byte piece, are 16-byte
+ * aligned when the row is; the values and the dot are the GGUF format's. */
+template <>
+struct Fmt<LG_Q8_0_R> : Fmt<LG_Q8_0> {
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s)
+    {
+        const uint8_t* g = row + (size_t)(s >> 3) * (8 * LG_BS_Q8_0);
+        const int j = s & 7;
+        w.d = *(const uint16_t*)(g + 256 + 2 * j);
+        w.q0 = *(const uint4*)(g + 32 * j);
+        w.q1 = *(const uint4*)(g + 32 * j + 16);
     }
 };
 

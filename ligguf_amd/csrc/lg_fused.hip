@@ -162,10 +162,12 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const P
         P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(atr, P, 4 * l + 3), nff);
 }
 
+/* OT may be a regrouped form (LG_Q8_0_R, LG_Q6_K_R): the head's copy in P.out_wr */
 template <int OT, class S>
 __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* __restrict__ Sd, uint8_t* atr)
 {
     constexpr int NO = S::NO;
+    const uint8_t* W = (OT == LG_Q8_0_R || OT == LG_Q6_K_R) ? P.out_wr : P.out_w;
     const int pos = Sd->pos;
     /* the step trace holds one slot per workgroup of the layer grid: the
      * first gridDim.x / LG_OUT_WGS workgroups stamp theirs */
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
     uint64_t* tr = Sd->trace && (int)blockIdx.x < nwg
                        ? Sd->trace + ((size_t)5 * P.n_layers * nwg + blockIdx.x) * 4 : nullptr;
     phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, S::CE, LG_OUT_R>(
-        P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
+        P, 0, W, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * P.n_embed, nullptr, P.logits,
         nullptr, 0, 0, tr, f_atr(atr, P, 4 * P.n_layers), P.n_embed);
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
     if (s_int[0] && threadIdx.x == 0) {
@@ -187,6 +189,17 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
 typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t, uint8_t*);
+
+/* the regrouped form of an output type (P.out_wr), or the type itself */
+static constexpr int f_rep(int t) { return t == LG_Q8_0 ? LG_Q8_0_R : t == LG_Q6_K ? LG_Q6_K_R : t; }
+
+template <int OT, class SH>
+static void f_launch_out(const PkParams& P, PkStep* S, int nwg, dim3 b, hipStream_t st, uint8_t* atr)
+{
+    if (f_rep(OT) != OT && P.out_wr)
+        hipLaunchKernelGGL((k_f_out<f_rep(OT), SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, atr);
+    else hipLaunchKernelGGL((k_f_out<OT, SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, atr);
+}
 
 /* the V and down types a layer of type LT may carry besides LT itself */
 template <int LT>
@@ -248,7 +261,7 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
         hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
         f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
     }
-    hipLaunchKernelGGL((k_f_out<OT, SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, atr);
+    f_launch_out<OT, SH>(P, S, nwg, b, st, atr);
 }
 
 typedef void (*fused_phase_t)(const PkParams&, const PkLayer*, PkStep*, int, int, int, bool, hipStream_t);
@@ -268,7 +281,7 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
     case 2: hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
     case 3: hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
     case 4: f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
-    default: hipLaunchKernelGGL((k_f_out<OT, SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, nullptr); break;
+    default: f_launch_out<OT, SH>(P, S, nwg, b, st, nullptr); break;
     }
 }
 

@@ -54,6 +54,7 @@ struct PkParams {
     uint32_t embd_rsz;
     int embd_t;
     const uint8_t* out_w;
+    const uint8_t* out_wr;    /* the output head regrouped for aligned loads (lg_repack_rows), or NULL */
     uint32_t out_rsz;
     int out_t;
     const float* out_norm;
