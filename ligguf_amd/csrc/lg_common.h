@@ -11,6 +11,11 @@
 /* GGUF block byte sizes and field offsets (fast/lil_gguf.h:64-119) */
 #define LG_QK8_0 32
 #define LG_QK_K 256
+/* internal forms of Q8_0 / Q6_K rows regrouped for aligned loads (copies the
+ * whole-step kernels read; Fmt<LG_Q8_0_R> in lg_fmt.h) */
+#define LG_Q8_0_R 108
+#define LG_Q6_K_R 114
+#define LG_Q1_G_R 141
 #define LG_BS_Q8_0 34
 #define LG_BS_Q1_0 6
 #define LG_BS_Q1_G 18

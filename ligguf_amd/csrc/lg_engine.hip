@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <string>
+#include <initializer_list>
 #include <vector>
 
 #include "lg_common.h"
@@ -374,9 +375,9 @@ static int upload_floats(lg_ctx* ctx, const float* h, size_t n, float** d, const
 #define LG_STEP_RING 64   /* pinned step records in flight before a forced sync */
 /* the persistent kernel reads every layer matrix at width n_embed = 4096
  * (n_ff = 12288 for down), one type for all layer matrices */
-/* The output head regrouped for the whole-step kernels' aligned loads
- * (Fmt<LG_Q8_0_R>, Fmt<LG_Q6_K_R>): each run of 8 blocks of a row becomes
- * its quants, then its scales (Q6_K: ql, qh, scales, d).  Only for widths of
+/* Rows regrouped for the fused kernels' aligned loads (Fmt<LG_Q8_0_R>,
+ * Fmt<LG_Q6_K_R>, Fmt<LG_Q1_G_R>): each run of 8 blocks of a row becomes its
+ * quants, then its scales (Q6_K: ql, qh, scales, d).  Only for widths of
  * whole groups on 16-byte row boundaries; empty otherwise. */
 static std::vector<uint8_t> repack_rows(const lg_weight& w)
 {
@@ -384,8 +385,10 @@ static std::vector<uint8_t> repack_rows(const lg_weight& w)
     if (!w.data || w.cols <= 0) return out;
     const bool q8 = w.type == LG_Q8_0 && w.cols % 256 == 0;
     const bool q6 = w.type == LG_Q6_K && w.cols % 2048 == 0;
-    if (!q8 && !q6) return out;
-    const size_t bs = q8 ? LG_BS_Q8_0 : LG_BS_Q6_K, ng = (size_t)w.cols / (q8 ? 256 : 2048);
+    const bool q1 = w.type == LG_Q1_G && w.cols % 1024 == 0;
+    if (!q8 && !q6 && !q1) return out;
+    const size_t bs = q8 ? LG_BS_Q8_0 : q6 ? LG_BS_Q6_K : LG_BS_Q1_G;
+    const size_t ng = (size_t)w.cols / (q8 ? 256 : q6 ? 2048 : 1024);
     if (w.rsz != ng * 8 * bs) return out;
     out.resize((size_t)w.rows * w.rsz);
     const uint8_t* src = (const uint8_t*)w.data;
@@ -398,6 +401,9 @@ static std::vector<uint8_t> repack_rows(const lg_weight& w)
                 if (q8) {
                     memcpy(o + 256 + 2 * j, b, 2);          /* d */
                     memcpy(o + 32 * j, b + 2, 32);          /* qs */
+                } else if (q1) {
+                    memcpy(o + 128 + 2 * j, b, 2);          /* d */
+                    memcpy(o + 16 * j, b + 2, 16);          /* sign bits */
                 } else {
                     memcpy(o + 128 * j, b, 128);            /* ql */
                     memcpy(o + 1024 + 64 * j, b + 128, 64); /* qh */
@@ -472,6 +478,28 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         ctx->pk_nwg = ncu;   /* one workgroup per CU, as the persistent grid */
     }
     std::vector<PkLayer> hl(m->n_layers);
+    /* uniform Q8_0 / Q6_K / Q1_G layers: the fused kernels read regrouped
+     * copies of every layer matrix (aligned loads); the persistent kernel
+     * keeps the GGUF rows of the arenas -- same values, same results */
+    const int gw = lt == LG_Q8_0 ? 256 : lt == LG_Q6_K ? 2048 : lt == LG_Q1_G ? 1024 : 0;
+#ifndef LG_REP_LAYERS
+#define LG_REP_LAYERS 1
+#endif
+    const bool rep_layers = LG_REP_LAYERS && fused && uniform && gw && m->n_embed % gw == 0 && m->n_ff % gw == 0;
+    auto upload_rep = [&](std::initializer_list<const lg_weight*> ws, const uint8_t*& ptr) -> int {
+        std::vector<uint8_t> all;
+        for (const lg_weight* w : ws) {
+            const std::vector<uint8_t> rp = repack_rows(*w);
+            if (rp.empty()) { lg_set_error("load_model: regrouping a layer matrix failed"); return LG_ERR_ARG; }
+            all.insert(all.end(), rp.begin(), rp.end());
+        }
+        uint8_t* d = nullptr;
+        int rc2;
+        if ((rc2 = dalloc(ctx, (void**)&d, all.size()))) return rc2;
+        if ((rc2 = h2d(d, all.data(), all.size()))) return rc2;
+        ptr = d;
+        return LG_OK;
+    };
     for (int l = 0; l < m->n_layers; l++) {
         const dlayer& D = ctx->layers[l];
         PkLayer& P = hl[l];
@@ -480,6 +508,34 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.ug = D.ug.data; P.ug_rsz = D.ug.rsz; P.ug_t = D.ug.type;
         P.down = D.down.data; P.down_rsz = D.down.rsz; P.down_t = D.down.type;
         P.v = D.qk_fused ? D.v.data : nullptr; P.v_rsz = D.v.rsz; P.v_t = D.v.type;
+        if (!kern) {
+            /* a mixed layer's Q6_K V and down matrices: the fused kernels read
+             * regrouped copies (aligned loads, Fmt<LG_Q6_K_R>) */
+            const lg_layer_desc& ML = m->layers[l];
+            auto regroup = [&](const lg_weight& w, const uint8_t*& ptr, int& t) -> int {
+                if (w.type != LG_Q6_K || w.type == lt) return LG_OK;
+                const std::vector<uint8_t> rp = repack_rows(w);
+                if (rp.empty()) return LG_OK;
+                uint8_t* d = nullptr;
+                int rc2;
+                if ((rc2 = dalloc(ctx, (void**)&d, rp.size()))) return rc2;
+                if ((rc2 = h2d(d, rp.data(), rp.size()))) return rc2;
+                ptr = d;
+                t = LG_Q6_K_R;
+                return LG_OK;
+            };
+            if (P.v && (rc = regroup(ML.att_v, P.v, P.v_t))) return rc;
+            if ((rc = regroup(ML.ffn_down, P.down, P.down_t))) return rc;
+        }
+        if (rep_layers) {
+            const lg_layer_desc& ML = m->layers[l];
+            const int rt = lt == LG_Q8_0 ? LG_Q8_0_R : lt == LG_Q6_K ? LG_Q6_K_R : LG_Q1_G_R;
+            if ((rc = upload_rep({&ML.att_q, &ML.att_k, &ML.att_v}, P.qkv))) return rc;
+            if ((rc = upload_rep({&ML.att_out}, P.ao))) return rc;
+            if ((rc = upload_rep({&ML.ffn_up, &ML.ffn_gate}, P.ug))) return rc;
+            if ((rc = upload_rep({&ML.ffn_down}, P.down))) return rc;
+            P.qkv_t = P.ao_t = P.ug_t = P.down_t = rt;
+        }
         P.att_norm = D.att_norm; P.ffn_norm = D.ffn_norm; P.q_norm = D.q_norm; P.k_norm = D.k_norm;
     }
     PkLayer* dl = nullptr;
@@ -498,6 +554,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.embd = ctx->embd.data; P.embd_rsz = ctx->embd.rsz; P.embd_t = ctx->embd.type;
     P.out_w = ctx->output.data; P.out_rsz = ctx->output.rsz; P.out_t = ctx->output.type;
     P.out_wr = nullptr;
+    P.layers_rep = rep_layers ? 1 : 0;
     if (fused) {
         const std::vector<uint8_t> rp = repack_rows(m->output);
         if (!rp.empty()) {

@@ -99,10 +99,6 @@ struct Fmt;
 /* Q4_K (144 B: d, dmin, scales[12], qs[128]); slot (block b, pair c) =
  * sub-blocks 2c (low nibbles of qs[32c..32c+31]) and 2c+1 (high nibbles).
  * dot_q8_K_q4_K: fast/lil_math.cpp:582-616, fast/arch_avx2.h:272-323. */
-/* regrouped output-head forms (see Fmt<LG_Q8_0_R>) */
-#define LG_Q8_0_R 108
-#define LG_Q6_K_R 114
-
 template <>
 struct Fmt<LG_Q4_K> {
     static constexpr int VALS = 64;
@@ -444,6 +440,19 @@ struct Fmt<LG_Q1_G> {
         }
         const float sumi = lg_fma2(A.b[0].d, (float)(2 * s0 - A.b[0].asum), A.b[1].d, (float)(2 * s1 - A.b[1].asum));
         return lg_h2f((uint16_t)w.d) * sumi;
+    }
+};
+
+/* Q1_G rows regrouped like Fmt<LG_Q8_0_R>: each run of 8 blocks (144 B)
+ * holds the 8 x 16 bytes of sign bits, then the 8 fp16 scales */
+template <>
+struct Fmt<LG_Q1_G_R> : Fmt<LG_Q1_G> {
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s)
+    {
+        const int blk = s >> 1, j = blk & 7;
+        const uint8_t* g = row + (size_t)(blk >> 3) * (8 * LG_BS_Q1_G);
+        w.d = *(const uint16_t*)(g + 128 + 2 * j);
+        w.bits = *(const uint2*)(g + 16 * j + 8 * (s & 1));
     }
 };
 

@@ -191,7 +191,10 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
 typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, int, bool, hipStream_t, uint8_t*);
 
 /* the regrouped form of an output type (P.out_wr), or the type itself */
-static constexpr int f_rep(int t) { return t == LG_Q8_0 ? LG_Q8_0_R : t == LG_Q6_K ? LG_Q6_K_R : t; }
+static constexpr int f_rep(int t)
+{
+    return t == LG_Q8_0 ? LG_Q8_0_R : t == LG_Q6_K ? LG_Q6_K_R : t == LG_Q1_G ? LG_Q1_G_R : t;
+}
 
 template <int OT, class SH>
 static void f_launch_out(const PkParams& P, PkStep* S, int nwg, dim3 b, hipStream_t st, uint8_t* atr)
@@ -222,7 +225,8 @@ static void f_launch_qkv(const PkParams& P, const PkLayer& L, PkStep* S, int l, 
         if (l == 0) hipLaunchKernelGGL((k_f_qkv2<LT, VT, SH, true>), g, b, 0, st, P, L, S, l, atr);            \
         else hipLaunchKernelGGL((k_f_qkv2<LT, VT, SH, false>), g, b, 0, st, P, L, S, l, atr);                   \
     } while (0)
-            if (L.v_t == LG_Q6_K) QKV2(LG_Q6_K);
+            if (L.v_t == LG_Q6_K_R) QKV2(LG_Q6_K_R);
+            else if (L.v_t == LG_Q6_K) QKV2(LG_Q6_K);
             else if (L.v_t == LG_Q5_K) QKV2(LG_Q5_K);
             else QKV2(LT);
 #undef QKV2
@@ -240,7 +244,8 @@ static void f_launch_down(const PkParams& P, const PkLayer& L, PkStep* S, int l,
 {
     if constexpr (f_mixable<LT>()) {
         if (L.down_t != LT) {
-            if (L.down_t == LG_Q6_K) hipLaunchKernelGGL((k_f_down<LG_Q6_K, SH>), g, b, 0, st, P, L, S, l, atr);
+            if (L.down_t == LG_Q6_K_R) hipLaunchKernelGGL((k_f_down<LG_Q6_K_R, SH>), g, b, 0, st, P, L, S, l, atr);
+            else if (L.down_t == LG_Q6_K) hipLaunchKernelGGL((k_f_down<LG_Q6_K, SH>), g, b, 0, st, P, L, S, l, atr);
             else hipLaunchKernelGGL((k_f_down<LG_Q5_K, SH>), g, b, 0, st, P, L, S, l, atr);
             return;
         }
@@ -296,6 +301,8 @@ struct FusedVariant {
     int ne, no, ce, nf, cf;       /* the FShape */
     fused_enqueue_t fn;
     fused_phase_t phase;
+    fused_enqueue_t fn_r;         /* the same on regrouped layer matrices (PkParams.layers_rep) */
+    fused_phase_t phase_r;
 };
 
 /* one variant per (layer type, output type, head_dim, query heads per KV
@@ -306,7 +313,9 @@ struct FusedVariant {
 #define FVS(LT, OT, HD, NR, E, F)                                                                              \
     {LT, OT, HD, NR, f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F),                                \
      fused_enqueue<LT, OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,         \
-     fused_phase<LT, OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>}
+     fused_phase<LT, OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,           \
+     fused_enqueue<f_rep(LT), OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,  \
+     fused_phase<f_rep(LT), OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>}
 #define FV(LT, OT, HD, NR) FVS(LT, OT, HD, NR, 4096, 12288)
 static const FusedVariant f_variants[] = {
     FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
@@ -345,13 +354,15 @@ const void* lg_fused_variant(int lt, int ot, int hd, int nrep, int ne, int nff)
 int lg_fused_enqueue(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int n_layers, int nwg,
                      bool long_ctx, hipStream_t s, uint8_t* act_trace)
 {
-    ((const FusedVariant*)variant)->fn(P, layers, S_dev, n_layers, nwg, long_ctx, s, act_trace);
+    const FusedVariant* v = (const FusedVariant*)variant;
+    (P.layers_rep ? v->fn_r : v->fn)(P, layers, S_dev, n_layers, nwg, long_ctx, s, act_trace);
     return lg_check_launch("fused decode step");
 }
 
 int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers, PkStep* S_dev, int phase, int layer,
                    int nwg, bool long_ctx, hipStream_t s)
 {
-    ((const FusedVariant*)variant)->phase(P, layers, S_dev, phase, layer, nwg, long_ctx, s);
+    const FusedVariant* v = (const FusedVariant*)variant;
+    (P.layers_rep ? v->phase_r : v->phase)(P, layers, S_dev, phase, layer, nwg, long_ctx, s);
     return lg_check_launch("fused decode phase");
 }

@@ -54,7 +54,8 @@ struct PkParams {
     uint32_t embd_rsz;
     int embd_t;
     const uint8_t* out_w;
-    const uint8_t* out_wr;    /* the output head regrouped for aligned loads (lg_repack_rows), or NULL */
+    const uint8_t* out_wr;    /* the output head regrouped for aligned loads (repack_rows), or NULL */
+    int layers_rep;           /* the fused step's PkLayer matrices are regrouped copies (Q8_0, Q6_K, Q1_G layers) */
     uint32_t out_rsz;
     int out_t;
     const float* out_norm;

@@ -32,6 +32,10 @@ PK_MODELS = [
     ModelConfig("llama-w4096-q5k", 0, 1, 4096, 32, 32, 128, 12288, 1024, 1024, 1e4, 1e-5, Q5_K, Q8_0, Q4_K),
     # 8 query heads per KV head
     ModelConfig("qwen3-w4096-nrep8", 1, 1, 4096, 32, 4, 128, 12288, 1024, 2048, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
+    # Q6_K and Q8_0 layers: the fused step reads regrouped copies of the layer matrices (aligned loads),
+    # the persistent kernel the GGUF rows
+    ModelConfig("qwen3-w4096-q6k", 1, 1, 4096, 32, 8, 128, 12288, 1024, 2048, 1e6, 1e-6, Q6_K, Q4_K, Q6_K),
+    ModelConfig("qwen3-w4096-q8_0", 1, 1, 4096, 32, 8, 128, 12288, 1024, 2048, 1e6, 1e-6, Q8_0, Q8_0, Q8_0),
 ]
 WHOLE = [PATH_FUSED, PATH_PERSISTENT]
 
