@@ -1,7 +1,7 @@
 """The reference's own driver program (fast/ligguf_fast_qk.cpp: main, CLI,
 tokenizer, samplers, state files) built twice by `make -C oracle driver` from
 the reference's sources: as it is (CPU), and with oracle/driver_lg_hip.patch
--- the LG_HIP insertions a maintainer would add: the upload
+-- the LG_HIP insertions a maintainer would add to the driver: the upload
 after allocate(), inference() delegated to lg_decode_step, the state file to
 lg_state_save / lg_state_load -- linked to libligguf_hip.so.  Both run the
 same GGUF and prompt as separate programs; their outputs must agree.
