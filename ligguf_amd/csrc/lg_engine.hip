@@ -172,6 +172,7 @@ struct lg_ctx {
     bool dev_known = false;          /* step_dev holds {dev_tok, dev_pos} (read back after a sync) */
     int dev_tok = 0, dev_pos = 0, dev_feed_end = 0, last_pos = 0;
     bool use_graph = true;
+    bool regroup = true;             /* fused kernels read regrouped copies of misaligned formats */
     hipGraphExec_t graph[2] = {nullptr, nullptr};   /* the step with short / long-context attention */
 };
 
@@ -229,6 +230,8 @@ extern "C" int lg_create(int device, lg_ctx** out)
     ctx->device = device;
     const char* ng = getenv("LG_NO_GRAPH");
     ctx->use_graph = !(ng && ng[0] == '1');
+    const char* nr = getenv("LG_NO_REGROUP");
+    ctx->regroup = !(nr && nr[0] == '1');
     const hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         lg_set_error("hipStreamCreate failed: %s", hipGetErrorString(e));
@@ -485,7 +488,8 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
 #ifndef LG_REP_LAYERS
 #define LG_REP_LAYERS 1
 #endif
-    const bool rep_layers = LG_REP_LAYERS && fused && uniform && gw && m->n_embed % gw == 0 && m->n_ff % gw == 0;
+    const bool rep_layers = LG_REP_LAYERS && ctx->regroup && fused && uniform && gw && m->n_embed % gw == 0 &&
+                            m->n_ff % gw == 0;
     auto upload_rep = [&](std::initializer_list<const lg_weight*> ws, const uint8_t*& ptr) -> int {
         std::vector<uint8_t> all;
         for (const lg_weight* w : ws) {
@@ -508,7 +512,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.ug = D.ug.data; P.ug_rsz = D.ug.rsz; P.ug_t = D.ug.type;
         P.down = D.down.data; P.down_rsz = D.down.rsz; P.down_t = D.down.type;
         P.v = D.qk_fused ? D.v.data : nullptr; P.v_rsz = D.v.rsz; P.v_t = D.v.type;
-        if (!kern) {
+        if (!kern && ctx->regroup) {
             /* a mixed layer's Q6_K V and down matrices: the fused kernels read
              * regrouped copies (aligned loads, Fmt<LG_Q6_K_R>) */
             const lg_layer_desc& ML = m->layers[l];
@@ -555,7 +559,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.out_w = ctx->output.data; P.out_rsz = ctx->output.rsz; P.out_t = ctx->output.type;
     P.out_wr = nullptr;
     P.layers_rep = rep_layers ? 1 : 0;
-    if (fused) {
+    if (fused && ctx->regroup) {
         const std::vector<uint8_t> rp = repack_rows(m->output);
         if (!rp.empty()) {
             uint8_t* d = nullptr;

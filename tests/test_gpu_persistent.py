@@ -390,3 +390,22 @@ def test_fused_greedy_vs_live_reference(gpu, reference, tmp_path):
     # can only leave the reference's sequence at the first near-tie miss
     assert first == (miss[0][0] if miss else len(gen_ref)), (first, miss)
     eng.close()
+
+
+def test_regrouped_copies_equal_gguf_rows(pk_model, monkeypatch):
+    """The fused step reads Q8_0 / Q6_K / Q1_G matrices from regrouped copies;
+    with LG_NO_REGROUP=1 (read at lg_create) it reads the GGUF rows: the
+    same logits bit for bit."""
+    hm, eng = pk_model
+    toks = np.random.default_rng(13).integers(1, hm.cfg.vocab, 4)
+    eng.set_path(PATH_FUSED)
+    a = [eng.decode(int(t), i) for i, t in enumerate(toks)]
+    monkeypatch.setenv("LG_NO_REGROUP", "1")
+    other = Engine(0)
+    try:
+        other.load(hm)
+        other.set_path(PATH_FUSED)
+        b = [other.decode(int(t), i) for i, t in enumerate(toks)]
+    finally:
+        other.close()
+    assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
