@@ -35,6 +35,9 @@ SHAPES = [
     # (Q|K one matrix, V on its own; the persistent kernel takes uniform layers only)
     ModelConfig("qwen3-w4096-q4k-mixed", 1, 3, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q4_K, Q4_K, Q6_K,
                 overrides=(("attn_v.0", Q6_K), ("ffn_down.0", Q6_K), ("attn_v.2", Q5_K), ("ffn_down.2", Q5_K))),
+    # Q5_K_M-style: Q5_K layers, Q6_K attn_v and ffn_down in layer 1
+    ModelConfig("qwen3-w4096-q5k-mixed", 1, 2, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K,
+                overrides=(("attn_v.1", Q6_K), ("ffn_down.1", Q6_K))),
 ]
 
 
