@@ -13,8 +13,8 @@ same tests on the fused path's mixed-layer kernels."""
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import (PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q4_K, Q5_K, Q6_K, Q8_0,
-                            LgError)
+from ligguf_amd.lib import (PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q2_K, Q3_K, Q4_K, Q5_K,
+                            Q6_K, Q8_0, LgError)
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
 from parity import step_flips
 from test_gpu_decode import assert_flips_explained, one_step_flips, oracle_state, rel
@@ -35,6 +35,9 @@ SHAPES = [
     # (Q|K one matrix, V on its own; the persistent kernel takes uniform layers only)
     ModelConfig("qwen3-w4096-q4k-mixed", 1, 3, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q4_K, Q4_K, Q6_K,
                 overrides=(("attn_v.0", Q6_K), ("ffn_down.0", Q6_K), ("attn_v.2", Q5_K), ("ffn_down.2", Q5_K))),
+    # Q3_K and Q2_K layers (Q6_K output head)
+    ModelConfig("qwen3-w4096-q3k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q3_K, Q4_K, Q6_K),
+    ModelConfig("qwen3-w4096-q2k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q2_K, Q4_K, Q6_K),
     # Q5_K_M-style: Q5_K layers, Q6_K attn_v and ffn_down in layer 1
     ModelConfig("qwen3-w4096-q5k-mixed", 1, 2, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K,
                 overrides=(("attn_v.1", Q6_K), ("ffn_down.1", Q6_K))),
