@@ -456,6 +456,25 @@ struct Fmt<LG_Q1_G_R> : Fmt<LG_Q1_G> {
     }
 };
 
+/* Q3_K rows regrouped like Fmt<LG_Q6_K_R>, 8 blocks (880 B) a group: the
+ * 8 x 32 hmask bytes, the 8 x 64 qs, the 8 x 12 scale bytes, the 8 d.  (A
+ * regrouped Q2_K measured slower: its fused kernels spill more.) */
+template <>
+struct Fmt<LG_Q3_K_R> : Fmt<LG_Q3_K> {
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s)
+    {
+        const int blk = s >> 2, n = (s & 3) >> 1, h = s & 1, j = blk & 7;
+        const uint8_t* g = row + (size_t)(blk >> 3) * (8 * LG_BS_Q3_K);
+        w.hm = *(const uint4*)(g + 32 * j + 16 * h);
+        w.q = *(const uint4*)(g + 256 + 64 * j + 32 * n + 16 * h);
+        const uint32_t* sc = (const uint32_t*)(g + 768 + 12 * j);
+        w.s0 = sc[0];
+        w.s1 = sc[1];
+        w.s2 = sc[2];
+        w.d = *(const uint16_t*)(g + 864 + 2 * j);
+    }
+};
+
 /* F16 / F32 rows against the float activation (dot_f16_f32 / dot_f32,
  * fast/arch_avx2.h:83-109) */
 template <>

@@ -145,3 +145,22 @@ def test_attention_past_the_short_split(shape_model, oracle, want_pos):
     assert not bad, bad[:5]
     assert e <= (1e-5 if first < 0 else 5e-2)
     assert em <= 5e-2
+
+
+def test_regrouped_copies_equal_gguf_rows(shape_model, monkeypatch):
+    """Where the fused step reads regrouped copies (Q8_0, Q6_K, Q1_G, Q3_K
+    matrices in whole 8-block groups), LG_NO_REGROUP=1 reads the GGUF rows:
+    the same logits bit for bit."""
+    hm, eng = shape_model
+    toks = np.random.default_rng(17).integers(1, hm.cfg.vocab, 3)
+    eng.set_path(PATH_FUSED)
+    a = [eng.decode(int(t), i) for i, t in enumerate(toks)]
+    monkeypatch.setenv("LG_NO_REGROUP", "1")
+    other = Engine(0)
+    try:
+        other.load(hm)
+        other.set_path(PATH_FUSED)
+        b = [other.decode(int(t), i) for i, t in enumerate(toks)]
+    finally:
+        other.close()
+    assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
