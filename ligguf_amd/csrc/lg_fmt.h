@@ -275,13 +275,18 @@ struct Fmt<LG_Q2_K> {
     {
         const int n = (s & 3) >> 1, h = s & 1;
         const uint32_t qv[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        /* scale bytes 8n + 2j + h: word 2n + j/2, byte (2j + h) & 3, picked
+         * with masks and shifts (an index or a select between the uint4's
+         * words made the compiler copy it to scratch and load it back) */
+        const uint32_t mn = 0u - (uint32_t)n;
+        const uint32_t s_lo = w.sc.x ^ ((w.sc.x ^ w.sc.z) & mn), s_hi = w.sc.y ^ ((w.sc.y ^ w.sc.w) & mn);
         int S = 0, M = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int dj = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) dj = lg_dot4((int)((qv[i] >> (2 * j)) & 0x03030303u), A.a[4 * j + i], dj);
-            const int sb = byte16(w.sc, 8 * n + 2 * j + h);
+            const int sb = (int)(((j >> 1 ? s_hi : s_lo) >> (8 * ((2 * j + h) & 3))) & 0xFFu);
             S += (sb & 15) * dj;
             M += (sb >> 4) * A.bs[j];
         }
