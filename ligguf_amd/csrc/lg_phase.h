@@ -1063,7 +1063,9 @@ struct Batch {
 #define LG_DN_B (Batch<LT, NF, 1, 1, 512>::value)
 #endif
 #ifndef LG_DN_R
-#define LG_DN_R 2
+/* a second batch in flight only while the rows of one fit the register budget
+ * (Q5_K / Q6_K down rows of 14336 values spilled with two) */
+#define LG_DN_R (Batch<LT, NF, 1, 1, 512>::bytes > 192 ? 1 : 2)
 #endif
 #ifndef LG_OUT_B
 #define LG_OUT_B 1
