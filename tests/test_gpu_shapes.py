@@ -38,6 +38,8 @@ SHAPES = [
     # Q3_K and Q2_K layers (Q6_K output head)
     ModelConfig("qwen3-w4096-q3k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q3_K, Q4_K, Q6_K),
     ModelConfig("qwen3-w4096-q2k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q2_K, Q4_K, Q6_K),
+    # Q8_0 layers with a Q6_K output head
+    ModelConfig("qwen3-w4096-q8_0-q6khead", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q8_0, Q4_K, Q6_K),
     # Q5_K_M-style: Q5_K layers, Q6_K attn_v and ffn_down in layer 1
     ModelConfig("qwen3-w4096-q5k-mixed", 1, 2, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K,
                 overrides=(("attn_v.1", Q6_K), ("ffn_down.1", Q6_K))),
