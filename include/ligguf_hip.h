@@ -131,8 +131,8 @@ const float* lg_logits_device(lg_ctx* ctx);
  * may also carry Q5_K / Q6_K attn_v and ffn_down matrices in any layer, as
  * Q4_K_M / Q4_K_S / Q5_K_M files do) with a matching output type and
  * head_dim 128, 64 or 48 in one of the width classes the library is built
- * with: n_embed 4096 with n_ff 12288 (Q2_K..Q6_K, Q1_G, Q8_0 layers; 1, 4 or
- * 8 query heads per KV head) or 14336 (Q4_K, Q8_0; 4),
+ * with: n_embed 4096 with n_ff 12288 (Q2_K..Q6_K, Q1_G, Q1_0, Q8_0 layers; 1,
+ * 4 or 8 query heads per KV head) or 14336 (Q4_K, Q8_0; 4),
  * 2560 / 9728 (Q4_K; 4), 2048 / 5632 (Q4_K, Q8_0; head_dim 64, 8), and any
  * widths up to 2048 / 2048 (Q8_0 with head_dim 48 or 64, Q4_K with 64; one
  * query head per KV head) -- widths are runtime values within a class.

@@ -321,7 +321,7 @@ static const FusedVariant f_variants[] = {
     FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
     FV(LG_Q5_K, LG_Q6_K, 128, 4), FV(LG_Q6_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q8_0, 128, 4),
     FV(LG_Q1_G, LG_Q8_0, 128, 4), FV(LG_Q1_G, LG_Q6_K, 128, 4), FV(LG_Q3_K, LG_Q6_K, 128, 4),
-    FV(LG_Q2_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q6_K, 128, 4),
+    FV(LG_Q2_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q6_K, 128, 4), FV(LG_Q1_0, LG_Q8_0, 128, 4),
     FV(LG_Q4_K, LG_Q6_K, 128, 8), FV(LG_Q4_K, LG_Q6_K, 128, 1), FV(LG_Q5_K, LG_Q4_K, 128, 1),
     FV(LG_Q8_0, LG_Q8_0, 128, 1),
     FVS(LG_Q4_K, LG_Q6_K, 128, 4, 4096, 14336), FVS(LG_Q8_0, LG_Q8_0, 128, 4, 4096, 14336),

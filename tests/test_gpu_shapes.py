@@ -13,8 +13,8 @@ same tests on the fused path's mixed-layer kernels."""
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import (PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q2_K, Q3_K, Q4_K, Q5_K,
-                            Q6_K, Q8_0, LgError)
+from ligguf_amd.lib import (PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q1_0, Q2_K, Q3_K, Q4_K,
+                            Q5_K, Q6_K, Q8_0, LgError)
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
 from parity import step_flips
 from test_gpu_decode import assert_flips_explained, one_step_flips, oracle_state, rel
@@ -38,6 +38,8 @@ SHAPES = [
     # Q3_K and Q2_K layers (Q6_K output head)
     ModelConfig("qwen3-w4096-q3k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q3_K, Q4_K, Q6_K),
     ModelConfig("qwen3-w4096-q2k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q2_K, Q4_K, Q6_K),
+    # Q1_0 layers (32-value sign blocks) with a Q8_0 output head
+    ModelConfig("qwen3-w4096-q1_0", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q1_0, Q8_0, Q8_0),
     # Q8_0 layers with a Q6_K output head
     ModelConfig("qwen3-w4096-q8_0-q6khead", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q8_0, Q4_K, Q6_K),
     # Q5_K_M-style: Q5_K layers, Q6_K attn_v and ffn_down in layer 1
