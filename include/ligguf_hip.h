@@ -136,7 +136,7 @@ const float* lg_logits_device(lg_ctx* ctx);
  * 2560 / 9728 (Q4_K; 4), 2048 / 5632 (Q4_K, Q8_0; head_dim 64, 8), and any
  * widths up to 2048 / 2048 (Q8_0 with head_dim 48 or 64, Q4_K with 64; one
  * query head per KV head) -- widths are runtime values within a class.
- * FUSED reads Q8_0 / Q6_K / Q3_K / Q1_G matrices (the output head, uniform
+ * FUSED reads Q8_0 / Q6_K / Q3_K / Q1_0 / Q1_G matrices (the output head, uniform
  * layers of those types, a mixed layer's Q6_K attn_v / ffn_down) from copies
  * regrouped for aligned loads, which costs their size again in device
  * memory; LG_NO_REGROUP=1 in the environment before lg_create reads the GGUF

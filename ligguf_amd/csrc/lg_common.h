@@ -17,6 +17,7 @@
 #define LG_Q6_K_R 114
 #define LG_Q1_G_R 141
 #define LG_Q3_K_R 111
+#define LG_Q1_0_R 140
 #define LG_BS_Q8_0 34
 #define LG_BS_Q1_0 6
 #define LG_BS_Q1_G 18

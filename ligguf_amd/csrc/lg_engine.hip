@@ -390,9 +390,10 @@ static std::vector<uint8_t> repack_rows(const lg_weight& w)
     const bool q6 = w.type == LG_Q6_K && w.cols % 2048 == 0;
     const bool q1 = w.type == LG_Q1_G && w.cols % 1024 == 0;
     const bool q3 = w.type == LG_Q3_K && w.cols % 2048 == 0;
-    if (!q8 && !q6 && !q1 && !q3) return out;
-    const size_t bs = q8 ? LG_BS_Q8_0 : q6 ? LG_BS_Q6_K : q1 ? LG_BS_Q1_G : LG_BS_Q3_K;
-    const size_t ng = (size_t)w.cols / (q8 ? 256 : q1 ? 1024 : 2048);
+    const bool q0 = w.type == LG_Q1_0 && w.cols % 256 == 0;
+    if (!q8 && !q6 && !q1 && !q3 && !q0) return out;
+    const size_t bs = q8 ? LG_BS_Q8_0 : q6 ? LG_BS_Q6_K : q1 ? LG_BS_Q1_G : q0 ? LG_BS_Q1_0 : LG_BS_Q3_K;
+    const size_t ng = (size_t)w.cols / ((q8 || q0) ? 256 : q1 ? 1024 : 2048);
     if (w.rsz != ng * 8 * bs) return out;
     out.resize((size_t)w.rows * w.rsz);
     const uint8_t* src = (const uint8_t*)w.data;
@@ -405,6 +406,9 @@ static std::vector<uint8_t> repack_rows(const lg_weight& w)
                 if (q8) {
                     memcpy(o + 256 + 2 * j, b, 2);          /* d */
                     memcpy(o + 32 * j, b + 2, 32);          /* qs */
+                } else if (q0) {
+                    memcpy(o + 32 + 2 * j, b, 2);           /* d */
+                    memcpy(o + 4 * j, b + 2, 4);            /* sign bits */
                 } else if (q1) {
                     memcpy(o + 128 + 2 * j, b, 2);          /* d */
                     memcpy(o + 16 * j, b + 2, 16);          /* sign bits */
@@ -490,7 +494,8 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     /* uniform Q8_0 / Q6_K / Q1_G layers: the fused kernels read regrouped
      * copies of every layer matrix (aligned loads); the persistent kernel
      * keeps the GGUF rows of the arenas -- same values, same results */
-    const int gw = lt == LG_Q8_0 ? 256 : (lt == LG_Q6_K || lt == LG_Q3_K) ? 2048 : lt == LG_Q1_G ? 1024 : 0;
+    const int gw = (lt == LG_Q8_0 || lt == LG_Q1_0) ? 256 : (lt == LG_Q6_K || lt == LG_Q3_K) ? 2048
+                 : lt == LG_Q1_G ? 1024 : 0;
 #ifndef LG_REP_LAYERS
 #define LG_REP_LAYERS 1
 #endif
@@ -539,7 +544,8 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         }
         if (rep_layers) {
             const lg_layer_desc& ML = m->layers[l];
-            const int rt = lt == LG_Q8_0 ? LG_Q8_0_R : lt == LG_Q6_K ? LG_Q6_K_R : lt == LG_Q3_K ? LG_Q3_K_R : LG_Q1_G_R;
+            const int rt = lt == LG_Q8_0 ? LG_Q8_0_R : lt == LG_Q6_K ? LG_Q6_K_R : lt == LG_Q3_K ? LG_Q3_K_R
+                         : lt == LG_Q1_0 ? LG_Q1_0_R : LG_Q1_G_R;
             if ((rc = upload_rep({&ML.att_q, &ML.att_k, &ML.att_v}, P.qkv))) return rc;
             if ((rc = upload_rep({&ML.att_out}, P.ao))) return rc;
             if ((rc = upload_rep({&ML.ffn_up, &ML.ffn_gate}, P.ug))) return rc;

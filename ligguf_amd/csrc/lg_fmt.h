@@ -412,6 +412,19 @@ struct Fmt<LG_Q1_0> {
     }
 };
 
+/* Q1_0 rows regrouped: each run of 8 blocks (48 B) holds the 8 x 4 bytes of
+ * sign bits, then the 8 fp16 scales */
+template <>
+struct Fmt<LG_Q1_0_R> : Fmt<LG_Q1_0> {
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s)
+    {
+        const uint8_t* g = row + (size_t)(s >> 3) * (8 * LG_BS_Q1_0);
+        const int j = s & 7;
+        w.d = *(const uint16_t*)(g + 32 + 2 * j);
+        w.bits = *(const uint32_t*)(g + 4 * j);
+    }
+};
+
 /* Q1_G (18 B: d, 128 sign bits); slot = half a block (64 values) against
  * two Q8_0 activation blocks: d * (da0*S0 + da1*S1).
  * dot_q8_0_q1_G: fast/lil_math.cpp:440-464, fast/arch_avx2.h:141-158 */

@@ -193,7 +193,8 @@ typedef void (*fused_enqueue_t)(const PkParams&, const PkLayer*, PkStep*, int, i
 /* the regrouped form of an output type (P.out_wr), or the type itself */
 static constexpr int f_rep(int t)
 {
-    return t == LG_Q8_0 ? LG_Q8_0_R : t == LG_Q6_K ? LG_Q6_K_R : t == LG_Q1_G ? LG_Q1_G_R : t == LG_Q3_K ? LG_Q3_K_R : t;
+    return t == LG_Q8_0 ? LG_Q8_0_R : t == LG_Q6_K ? LG_Q6_K_R : t == LG_Q1_G ? LG_Q1_G_R : t == LG_Q3_K ? LG_Q3_K_R
+         : t == LG_Q1_0 ? LG_Q1_0_R : t;
 }
 
 template <int OT, class SH>

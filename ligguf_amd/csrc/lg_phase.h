@@ -402,8 +402,8 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                                          const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0}, int rot = 0)
 {
     using F = Fmt<FMT>;
-    constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q8_0_R || FMT == LG_Q1_0 || FMT == LG_Q1_G || FMT == LG_Q1_G_R)
-                           ? LG_Q8_0 : LG_Q8_K;
+    constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q8_0_R || FMT == LG_Q1_0 || FMT == LG_Q1_0_R || FMT == LG_Q1_G ||
+                        FMT == LG_Q1_G_R) ? LG_Q8_0 : LG_Q8_K;
     /* a row of n_act values is nslots slots; lane j takes slots j, j+64, ..
      * (NS of them, those past nslots unused) */
     const int nslots = n_act / F::VALS;
