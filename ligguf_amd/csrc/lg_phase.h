@@ -407,7 +407,9 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     /* a row of n_act values is nslots slots; lane j takes slots j, j+64, ..
      * (NS of them, those past nslots unused) */
     const int nslots = n_act / F::VALS;
-    const int lane = LG_TID & 63, wave = LG_TID >> 6;
+    /* the wave index as a wave-uniform value: item indices and row addresses
+     * are then scalar (a row base in SGPRs, the lane's slot offset in a VGPR) */
+    const int lane = LG_TID & 63, wave = __builtin_amdgcn_readfirstlane(LG_TID >> 6);
     const int nwv = gridDim.x * PK_WAVES;
     int gw = blockIdx.x * PK_WAVES + wave + rot;   /* 0 <= rot < nwv */
     gw -= gw >= nwv ? nwv : 0;
@@ -424,7 +426,9 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     stamp(tr, 0);
     static_assert(NR >= 1 && NR <= 4, "ring depth");
     Rows<FMT, NS, MAXB, K> R[NR];
-    float res[NR][MAXB];
+    /* EPI_RESID: lane j holds the residual of the wave's item j (of the
+     * current 64-item chunk; items past the wave's last load its last) */
+    float resl = 0.0f;
     NormW<CPW> nw;
     ActSrc<CPW> as;
     MergeAct<CPW> mg;
@@ -434,18 +438,14 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
         else if (!from_embed && BLD != BLD_KEEP) as.load(src, n_act);
     };
-    auto load_res = [&](float* r, int b0) {
-        if (EPI == EPI_RESID) {
-#pragma unroll
-            for (int b = 0; b < MAXB; b++) r[b] = res_src[min(i0 + (b0 + b) * ist, wlast)];
-        }
+    auto load_res = [&](int c0) {
+        if (EPI == EPI_RESID) resl = res_src[min(i0 + (c0 + lane) * ist, wlast)];
     };
     auto prefetch = [&]() {
 #pragma unroll
-        for (int k = 0; k < (NR > 1 ? NR - 1 : 1); k++) {
+        for (int k = 0; k < (NR > 1 ? NR - 1 : 1); k++)
             R[k].load(W, rsz, i0 + k * MAXB * ist, ist, wlast, kstride, lane, nslots);
-            load_res(res[k], k * MAXB);
-        }
+        load_res(0);
     };
     if (!wait_target) {
         /* no dependency wait (fused kernels): the activation and the norm
@@ -478,9 +478,32 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
 #pragma unroll
     for (int s = 0; s < NS; s++) F::load_act(act[s], s_act, min(lane + 64 * s, nslots - 1));
 
-    float best = -INFINITY;
+    /* Item results gather in lanes -- lane j holds the wave's item c0 + j
+     * (ov; og the gate row's for EPI_SWIGLU) -- and every 64 items, and
+     * after the last, all lanes finish their items at once: one epilogue and
+     * one store instruction per 64 items instead of a lane-0 epilogue per
+     * item (the same arithmetic per item). */
+    float ov = 0.0f, og = 0.0f;
+    float best = -INFINITY;   /* EPI_LOGITS: this lane's best item so far, first index on ties */
     int besti = 0x7fffffff;
-    auto process = [&](const Rows<FMT, NS, MAXB, K>& R, const float* rs, int b0, int nb) {
+    int c0 = 0;
+    auto flush = [&](int n) {
+        if (lane < n) {
+            const int i = i0 + (c0 + lane) * ist;
+            float v = ov;
+            if (EPI == EPI_RESID) v = resl + ov;
+            else if (EPI == EPI_SWIGLU) v = (og / (1.0f + expf(-og))) * ov;
+            if (EPI == EPI_LOGITS) {
+                out[i] = v;
+                if (v > best) { best = v; besti = i; }
+            } else {
+                cst(&out[i], v);
+            }
+        }
+        c0 += 64;
+        if (c0 < my) load_res(c0);
+    };
+    auto process = [&](const Rows<FMT, NS, MAXB, K>& R, int b0, int nb) {
 #pragma unroll
         for (int b = 0; b < MAXB; b++) {
             if (b < nb) {
@@ -493,30 +516,17 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                         if (64 * (s + 1) <= nslots || lane + 64 * s < nslots) a += F::dot(R.w[b][k][s], act[s], lane + 64 * s);
                     acc[k] = lg_wave_sum(a);
                 }
-                const int i = i0 + (b0 + b) * ist;
-                if (EPI == EPI_LOGITS) {
-                    if (acc[0] > best) { best = acc[0]; besti = i; }
-                }
-                if (lane == 0) {
-                    float v = acc[0];
-                    if (EPI == EPI_RESID) v = rs[b] + acc[0];
-                    else if (EPI == EPI_SWIGLU) {
-                        const float u = acc[0], g = acc[1];
-                        v = (g / (1.0f + expf(-g))) * u;
-                    }
-                    if (EPI == EPI_LOGITS) out[i] = v;
-                    else cst(&out[i], v);
-                }
+                const int li = b0 + b - c0;   /* wave-uniform */
+                ov = lane == li ? acc[0] : ov;
+                if (EPI == EPI_SWIGLU) og = lane == li ? acc[1] : og;
+                if (li == 63) flush(64);
             }
         }
     };
     if (NR == 1) {
         for (int b0 = 0; b0 < my; b0 += MAXB) {
-            if (b0 > 0) {
-                R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane, nslots);
-                load_res(res[0], b0);
-            }
-            process(R[0], res[0], b0, min(MAXB, my - b0));
+            if (b0 > 0) R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane, nslots);
+            process(R[0], b0, min(MAXB, my - b0));
         }
     } else {
         /* batch j sits in slot j % NR; before computing batch j the wave
@@ -527,10 +537,23 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
             for (int k = 0; k < NR; k++) {
                 const int jn = j0 + k + NR - 1;
                 R[(k + NR - 1) % NR].load(W, rsz, i0 + jn * MAXB * ist, ist, wlast, kstride, lane, nslots);
-                load_res(res[(k + NR - 1) % NR], jn * MAXB);
-                process(R[k], res[k], (j0 + k) * MAXB, min(MAXB, my - (j0 + k) * MAXB));
+                process(R[k], (j0 + k) * MAXB, min(MAXB, my - (j0 + k) * MAXB));
             }
         }
+    }
+    if (my > c0) flush(my - c0);
+    if (EPI == EPI_LOGITS) {
+        /* the wave's best: the largest value, the lowest row index among
+         * equal ones (each lane's best is its first among equal values; its
+         * rows ascend) */
+        float mx = best;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        int mi = best == mx ? besti : 0x7fffffff;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mi = min(mi, __shfl_xor(mi, o, 64));
+        best = mx;
+        besti = mi;
     }
     if (EPI == EPI_LOGITS) {
         /* first index wins ties: rows are visited in increasing order per
