@@ -7,8 +7,11 @@ Workload (one "step" = one greedy decode token, batch 1):
   with synthetic N(0, 0.02) weights encoded to Q4_K (attention, FFN,
   embedding) and Q6_K (output head), norms 1.0.  A 512-token random-id
   prompt is prefilled first, then W warm-up and K timed greedy tokens run
-  through lg_decode_step + lg_argmax (the reference's inference() +
-  sampler_greedy loop, fast/ligguf_fast_qk.cpp:368-382).
+  through lg_decode_greedy: the reference's inference() + sampler_greedy
+  loop (fast/ligguf_fast_qk.cpp:368-382) with each step's greedy token fed
+  to the next on the device, the steps queued back to back.  The same K
+  steps with the token read back to the host every step (lg_decode_step_async
+  + lg_argmax) are reported beside it.
 
 Prints one JSON line.  `value` is decode tokens/s with weights and KV
 resident in HBM.  `roofline` is for the dominant kernel of the step, the
@@ -313,19 +316,16 @@ def q1g_context(torch, np, ctx: int = 8192, steps: int = 128, warmup: int = 8, c
         state = os.path.join(tempfile.mkdtemp(prefix="lg_q1g_"), "ctx.state")
         eng.state_save(state, ctx)
     tok, pos = int(np.argmax(logits)), ctx
-    for _ in range(warmup):
-        eng.decode_async(tok, pos)
-        tok = eng.argmax()
-        pos += 1
+    if warmup:
+        tok = int(eng.decode_greedy(tok, pos, warmup)[-1])
+        pos += warmup
     torch.cuda.synchronize()
     p_first = pos
     t0 = time.perf_counter()
-    for _ in range(steps):
-        eng.decode_async(tok, pos)
-        tok = eng.argmax()
-        pos += 1
+    eng.decode_greedy(tok, pos, steps)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    pos += steps
     path = {1: "persistent", 2: "multi-kernel", 3: "fused-graph"}.get(eng.path(), "?")
     eng.close()
     mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
@@ -564,7 +564,7 @@ def main() -> int:
     import torch
     from ligguf_amd.model import QWEN3_8B_Q4K, Engine, HostModel
 
-    cfg = QWEN3_8B_Q4K.with_(n_context=max(1024, args.prefill + args.warmup + args.steps + 1))
+    cfg = QWEN3_8B_Q4K.with_(n_context=max(1024, args.prefill + args.warmup + 2 * args.steps + 1))
     if args.kernel_only:
         hm = HostModel.synthetic(cfg)
         eng = Engine(0)
@@ -593,18 +593,15 @@ def main() -> int:
         prompt = np.random.default_rng(0).integers(1, cfg.vocab, args.prefill).astype(np.int32)
         logits = eng.prefill(prompt, 0)
         tok, pos = int(np.argmax(logits)), args.prefill
-        for _ in range(args.warmup):
-            eng.decode_async(tok, pos)
-            tok = eng.argmax()
-            pos += 1
+        if args.warmup:
+            tok = int(eng.decode_greedy(tok, pos, args.warmup)[-1])
+            pos += args.warmup
         torch.cuda.synchronize()
         p_first, t0 = pos, time.perf_counter()
-        for _ in range(args.steps):
-            eng.decode_async(tok, pos)
-            tok = eng.argmax()
-            pos += 1
+        eng.decode_greedy(tok, pos, args.steps)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
+        pos += args.steps
         mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
         rep = {"model": cfg.name, "tok_s": round(args.steps / dt, 2), "ms_per_token": round(dt / args.steps * 1e3, 4),
                "bytes_per_token": int(mean_bytes), "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) /
@@ -653,23 +650,30 @@ def main() -> int:
 
     pos = args.prefill
     tok = int(np.argmax(logits))
-    for _ in range(args.warmup):
-        eng.decode_async(tok, pos)
-        tok = eng.argmax()
-        pos += 1
+    if args.warmup:
+        tok = int(eng.decode_greedy(tok, pos, args.warmup)[-1])   # greedy steps queued back to back
+        pos += args.warmup
     torch.cuda.synchronize()
     p_first = pos
+    t0 = time.perf_counter()
+    toks = eng.decode_greedy(tok, pos, args.steps)   # returns after the last step's token is on the host
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok = int(toks[-1])
+    pos += args.steps
+    ms = dt / args.steps * 1e3
+    tps = args.steps / dt
+    mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
+    log(f"decode: {tps:.1f} tok/s, {ms:.3f} ms/token, {mean_bytes / (dt / args.steps) / 1e9:.0f} GB/s per token")
+    # the same steps with the greedy token read back to the host each step (lg_decode_step_async + lg_argmax)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         eng.decode_async(tok, pos)
         tok = eng.argmax()
         pos += 1
     torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    ms = dt / args.steps * 1e3
-    tps = args.steps / dt
-    mean_bytes = cfg.weight_bytes() + np.mean([cfg.kv_bytes(p) for p in range(p_first, pos)])
-    log(f"decode: {tps:.1f} tok/s, {ms:.3f} ms/token, {mean_bytes / (dt / args.steps) / 1e9:.0f} GB/s per token")
+    host_loop_tps = args.steps / (time.perf_counter() - t0)
+    log(f"decode with a host round trip per token: {host_loop_tps:.1f} tok/s")
 
     isolated = None if args.no_isolated else isolated_kernels(torch, np)
     sampler = None if args.no_isolated else sampler_report(eng, np, tok, pos)
@@ -712,7 +716,9 @@ def main() -> int:
             "ffn": cfg.n_ff, "vocab": cfg.vocab, "weights": "Q4_K layers+embedding, Q6_K output",
             "prefill_tokens": args.prefill, "positions": [p_first, pos - 1],
             "bytes_per_token": int(mean_bytes), "decode_path": path_name,
+            "decode_loop": "lg_decode_greedy: greedy steps queued back to back, argmax fed forward on the device",
         },
+        "decode_host_loop_tok_s": round(host_loop_tps, 1),
         "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) / HBM_PEAK, 4),
         "hbm_practical": {"copy_GB/s": copy["GB/s"], "bytes_each_way": copy["bytes_each_way"],
                           "frac_of_peak": round(copy["GB/s"] * 1e9 / HBM_PEAK, 4),

@@ -196,6 +196,18 @@ int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters, float* av
  * (sampler_greedy, fast/ligguf_fast_qk.cpp:146-160). */
 int lg_argmax(lg_ctx* ctx, int* tok_out);
 
+/* n greedy decode steps queued back to back: the step at position pos takes
+ * token tok, each later one the greedy token of the step before it, which
+ * stays on the device (no host round trip per token on the fused and
+ * persistent paths); toks_out[i] is the greedy token of step pos + i.  The
+ * same tokens, logits and KV rows as n rounds of lg_decode_step + lg_argmax
+ * -- the reference's generation loop feeding sampler_greedy's token back to
+ * inference() (fast/ligguf_fast_qk.cpp:368-382) -- except that it does not
+ * stop at an end-of-sequence token: the caller truncates toks_out there.
+ * Needs pos + n <= n_context; the device logits are the last step's.  No
+ * counterpart in the reference (its loop runs on the host). */
+int lg_decode_greedy(lg_ctx* ctx, int tok, int pos, int n, int* toks_out);
+
 /* Top-p / top-k sampling of the current device logits (sampler_topp,
  * fast/ligguf_fast_qk.cpp:172-214, with g_m.temp, g_m.topp, g_m.topk as
  * arguments): softmax at temperature temp, entries by probability descending

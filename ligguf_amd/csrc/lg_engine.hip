@@ -629,6 +629,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     /* fused path: device step record, prompt feed, pinned staging */
     if ((rc = dalloc(ctx, (void**)&ctx->step_dev, sizeof(PkStep)))) return rc;
     LG_HIP_CHECK(hipMemset(ctx->step_dev, 0, sizeof(PkStep)));
+    if ((rc = dalloc(ctx, (void**)&P.tok_hist, (size_t)m->n_context * sizeof(int)))) return rc;
     if ((rc = dalloc(ctx, (void**)&ctx->feed_dev, (size_t)m->n_context * sizeof(int)))) return rc;
     LG_HIP_CHECK(hipMemset(ctx->feed_dev, 0, (size_t)m->n_context * sizeof(int)));
     P.feed = ctx->feed_dev;
@@ -1352,6 +1353,45 @@ extern "C" int lg_argmax(lg_ctx* ctx, int* tok_out)
     const hipError_t e = hipMemcpyAsync(tok_out, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
     if (e != hipSuccess) { lg_set_error("argmax copy: %s", hipGetErrorString(e)); return ctx_fail(ctx, LG_ERR_HIP); }
     return lg_sync(ctx);
+}
+
+extern "C" int lg_decode_greedy(lg_ctx* ctx, int tok, int pos, int n, int* toks_out)
+{
+    int rc = step_checks(ctx, tok, pos);
+    if (rc) return ctx_fail(ctx, rc);
+    if (n <= 0 || !toks_out || n > ctx->n_context - pos) {
+        lg_set_error("lg_decode_greedy: %d steps from position %d (context %d), or no output", n, pos, ctx->n_context);
+        return ctx_fail(ctx, LG_ERR_ARG);
+    }
+    hipSetDevice(ctx->device);
+    if (use_fused(ctx) || use_pk(ctx)) {
+        /* whole-step paths: every step leaves its greedy token on the device
+         * (the fused output kernel advances the step record; the persistent
+         * kernel takes tok < 0 as the previous step's token) and in tok_hist */
+        if (use_fused(ctx)) {
+            if ((rc = fused_set_step(ctx, tok, pos, 0))) return ctx_fail(ctx, rc);
+            for (int i = 0; i < n; i++)
+                if ((rc = fused_launch(ctx, pos + i))) return ctx_fail(ctx, rc);
+            ctx->last_pos = pos + n - 1;
+        } else {
+            for (int i = 0; i < n; i++)
+                if ((rc = enqueue_pk(ctx, i ? -1 : tok, pos + i))) return ctx_fail(ctx, rc);
+        }
+        ctx->dev_known = false;
+        LG_HIP_CHECK(hipMemcpyAsync(ctx->pk_status_host, ctx->pk.tok_out, 2 * sizeof(int), hipMemcpyDeviceToHost,
+                                    ctx->stream));
+        LG_HIP_CHECK(hipMemcpyAsync(toks_out, ctx->pk.tok_hist + pos, (size_t)n * sizeof(int), hipMemcpyDeviceToHost,
+                                    ctx->stream));
+        ctx->last_was_pk = true;
+        return lg_sync(ctx);
+    }
+    /* the multi-kernel path: a step and its argmax at a time */
+    for (int i = 0; i < n; i++) {
+        if ((rc = lg_decode_step_async(ctx, tok, pos + i))) return rc;
+        if ((rc = lg_argmax(ctx, &tok))) return rc;
+        toks_out[i] = tok;
+    }
+    return LG_OK;
 }
 
 static int sample_args(float r01, const char* who)

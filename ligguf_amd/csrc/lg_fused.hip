@@ -179,7 +179,9 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* 
         nullptr, 0, 0, tr, f_atr(atr, P, 4 * P.n_layers), P.n_embed);
     /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
     if (s_int[0] && threadIdx.x == 0) {
-        Sd->tok = cld(P.tok_out);
+        const int t = cld(P.tok_out);
+        P.tok_hist[pos] = t;
+        Sd->tok = t;
         Sd->pos = pos + 1;
         Sd->trace = nullptr;    /* a trace covers one step */
     }

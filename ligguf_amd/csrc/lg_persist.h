@@ -77,6 +77,7 @@ struct PkParams {
     int* amax_i;
     uint32_t* amax_cnt;      /* zero between launches */
     int* tok_out;            /* greedy token of this step */
+    int* tok_hist;           /* [n_ctx]: the greedy token of the step at each position */
     uint32_t* err;           /* nonzero: a sync wait expired (or an unsupported phase) */
     const int* feed;         /* [n_ctx] prompt tokens for positions < PkStep.feed_end (fused path) */
     int spin_cap;
@@ -86,7 +87,7 @@ struct PkParams {
 /* what changes from token to token (PkParams, fixed per model, and PkStep
  * are kernel arguments; the fused kernels read PkStep from device memory) */
 struct PkStep {
-    int tok, pos;
+    int tok, pos;            /* persistent kernel: tok < 0 takes the previous step's greedy token (tok_out) */
     int feed_end;            /* fused path: positions below this take their token from PkParams.feed */
     int pad_;
     uint64_t base;           /* progress value at launch; the launch adds 5*n_layers + 1 */

@@ -90,6 +90,9 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
     constexpr int NE = NsE<LT>::value, NF = 3 * NE;
 #define TR(p) (S.trace ? S.trace + ((size_t)(p) * gridDim.x + blockIdx.x) * 4 : nullptr)
 #define ATR(k) (S.act_trace ? S.act_trace + (size_t)(k) * P.act_stride : nullptr)
+    /* a step queued behind another without a host round trip takes the
+     * greedy token the step before it left in tok_out */
+    const int tok = S.tok >= 0 ? S.tok : __builtin_amdgcn_readfirstlane(cld(P.tok_out));
     for (int l = 0; l < P.n_layers; l++) {
         const PkLayer L = pk_layer(P, l);
         const uint64_t p0 = B + 5ull * l;
@@ -100,10 +103,10 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
         float* hb = P.hb + (size_t)l * nff;
         if (l == 0)
             phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, BLD_EMB, 2, LG_QKV_R>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l), ATR(4 * l), ne);
+                P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, 0, p0 + 1, TR(5 * l), ATR(4 * l), ne);
         else
             phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, BLD_RMS, 2, LG_QKV_R>(
-                P, S.tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l), ATR(4 * l), ne);
+                P, tok, L.qkv, L.qkv_rsz, qs, 0, L.att_norm, xin, nullptr, qkv, xin, p0, p0 + 1, TR(5 * l), ATR(4 * l), ne);
         phase_attn_any<HD, NREP>(P, L, l, S.pos, qkv, p0 + 1, p0 + 2, TR(5 * l + 1));
         phase_mv<LT, NE, LG_AO_B, 1, EPI_RESID, BLD_MERGE, 2, LG_AO_R>(
             P, 0, L.ao, L.ao_rsz, ne, 0, nullptr, nullptr, xin, xmid, nullptr, p0 + 2, p0 + 3, TR(5 * l + 2),
@@ -120,6 +123,8 @@ __global__ __launch_bounds__(PK_THREADS) void k_decode_persistent(const PkParams
     phase_mv<OT, NO, LG_OUT_B, 1, EPI_LOGITS, BLD_RMS, 2, LG_OUT_R>(
         P, 0, P.out_w, P.out_rsz, P.vocab, 0, P.out_norm, P.xs + (size_t)P.n_layers * ne, nullptr, P.logits, nullptr,
         pf, pf + 1, TR(5 * P.n_layers), ATR(4 * P.n_layers), ne);
+    /* s_int[0]: this workgroup reduced the argmax and wrote tok_out */
+    if (s_int[0] && LG_TID == 0) cst(&P.tok_hist[S.pos], cld(P.tok_out));
 #undef TR
 #undef ATR
 }

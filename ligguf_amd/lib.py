@@ -76,6 +76,7 @@ SIGNATURES = {
     "lg_sync": (C.c_int, [_vp]),
     "lg_logits_device": (_vp, [_vp]),
     "lg_argmax": (C.c_int, [_vp, C.POINTER(C.c_int)]),
+    "lg_decode_greedy": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "lg_sample_topp": (C.c_int, [_vp, C.c_float, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_int)]),
     "lg_sample_topp_device": (C.c_int, [_vp, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_int)]),
     "lg_set_decode_path": (C.c_int, [_vp, C.c_int]),

@@ -371,6 +371,13 @@ class Engine:
         check(self.lib.lg_argmax(self.ctx, C.byref(t)), self.ctx)
         return int(t.value)
 
+    def decode_greedy(self, tok: int, pos: int, n: int) -> np.ndarray:
+        """lg_decode_greedy: n greedy steps from (tok, pos) queued back to
+        back; the greedy token of each step."""
+        out = np.zeros(n, dtype=np.int32)
+        check(self.lib.lg_decode_greedy(self.ctx, tok, pos, n, out.ctypes.data_as(C.POINTER(C.c_int))), self.ctx)
+        return out
+
     def sample_topp(self, temp: float, topp: float, topk: int, r01: float) -> int:
         """lg_sample_topp: the reference's sampler_topp over the device logits,
         r01 = (float)rand() / (float)RAND_MAX drawn by the caller."""

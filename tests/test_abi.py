@@ -72,3 +72,5 @@ def test_null_context_errors():
     assert lib.lg_destroy(None) == 0
     t = C.c_int()
     assert lib.lg_argmax(None, C.byref(t)) == -1
+    toks = (C.c_int * 4)()
+    assert lib.lg_decode_greedy(None, 1, 0, 4, toks) == -1

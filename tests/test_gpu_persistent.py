@@ -91,6 +91,33 @@ def test_fused_equals_persistent_bitwise(pk_model):
     assert af == ap
 
 
+@pytest.mark.parametrize("path", WHOLE + [PATH_MULTI], ids=["fused", "persistent", "multi"])
+def test_decode_greedy_equals_step_loop(pk_model, path):
+    """lg_decode_greedy (steps queued back to back, each step's greedy token
+    fed to the next on the device) against the same steps one at a time with
+    the token read back to the host: the same tokens, and the same KV state
+    (the next step from either gives bit-identical logits)."""
+    hm, eng = pk_model
+    eng.set_path(path)
+    tok0, pos0, n = 17, 3, 9
+    loop, tok = [], tok0
+    for i in range(n):
+        eng.decode(tok, pos0 + i)
+        tok = eng.argmax()
+        loop.append(tok)
+    after_loop = eng.decode(tok, pos0 + n)
+    q = eng.decode_greedy(tok0, pos0, n)
+    assert q.tolist() == loop
+    after_q = eng.decode(int(q[-1]), pos0 + n)
+    assert np.array_equal(after_loop.view(np.uint32), after_q.view(np.uint32))
+    # a queued run right after another (the device step record and the
+    # persistent kernel's token word carry over), then past the context's end
+    q2 = eng.decode_greedy(int(q[-1]), pos0 + n, 4)
+    assert len(q2) == 4
+    with pytest.raises(LgError):
+        eng.decode_greedy(1, hm.cfg.n_context - 2, 3)
+
+
 @pytest.mark.parametrize("path", WHOLE, ids=["fused", "persistent"])
 def test_matches_multikernel(pk_model, path):
     hm, eng = pk_model
