@@ -104,6 +104,7 @@ class Oracle:
         L.or_state_set_pos.argtypes = [_vp, C.c_int]
         L.or_inference.argtypes = [_vp, C.c_int, _fp]
         L.or_state_trace.argtypes = [_vp, _fp]
+        L.or_state_force.argtypes = [_vp, _vp, C.c_size_t, _vp]
         L.or_state_kv.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_state_kv_write.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
         L.or_argmax.argtypes = [_fp, C.c_int]
@@ -264,6 +265,17 @@ class Oracle:
         self.L.or_state_trace(st, tr.ctypes.data_as(_fp))
         out = self.inference(st, tok, cfg.vocab)
         return out, tr
+
+    def inference_forced(self, st, tok: int, cfg, acts: np.ndarray, forms):
+        """inference_traced() with the quantized activations of `acts`
+        ([4 L + 1][stride] bytes, block_q8_K / block_q8_0) in place of the
+        step's own at every point whose form in `forms` is Q8_K or Q8_0
+        (None / 0: the step quantizes its own): (logits, trace)."""
+        acts = np.ascontiguousarray(acts, dtype=np.uint8)
+        fm = np.array([f or 0 for f in forms], np.int32)
+        assert acts.ndim == 2 and acts.shape[0] == len(fm) == 4 * cfg.n_layers + 1
+        self.L.or_state_force(st, acts.ctypes.data, acts.shape[1], fm.ctypes.data)
+        return self.inference_traced(st, tok, cfg)
 
     def state_kv_write(self, st, layer, p0, np_, k, v):
         k = np.ascontiguousarray(k, dtype=np.uint16)

@@ -603,6 +603,11 @@ struct or_state {
     float *x, *xb, *xb2, *hb, *hb2, *q, *k, *v, *logits, *tmp;
     uint16_t *kc, *vc;
     float* trace;   /* NULL, or [4*n_layers+1][max(n_embed, n_ff)] for the next step only */
+    /* next step only: quantized activations to use in place of the step's own
+     * at each quantization point k whose form force_forms[k] is set */
+    const uint8_t* force;
+    size_t force_stride;
+    const int* force_forms;
 };
 
 or_state* or_state_new(const or_model* m)
@@ -652,6 +657,42 @@ static void mv(const or_weight* w, const float* x, float* out)
     or_matvec(w->type, w->data, w->rsz, w->cols, w->rows, x, out);
 }
 
+void or_state_force(or_state* s, const void* acts, size_t stride, const int* forms)
+{
+    s->force = (const uint8_t*)acts;
+    s->force_stride = stride;
+    s->force_forms = forms;
+}
+
+/* mv() at quantization point k.  When the step forces that point in the
+ * weight's activation form (Q8_K for the K-quants, Q8_0 for the Q8_0 family:
+ * fast/ligguf_fast_qk.cpp:39-41) the matvec reads the given blocks instead of
+ * quantizing x.  A Q8_K block's bsums are the 16-value sums of its quants
+ * (quantize_q8_K, fast/lil_math.cpp:329-361), so they are recomputed from
+ * the given quants rather than taken from the caller. */
+static void mv_at(const or_state* s, const uint8_t* force, int k, const or_weight* w, const float* x, float* out)
+{
+    const int f = force ? s->force_forms[k] : 0;
+    const uint8_t* a = force ? force + (size_t)k * s->force_stride : NULL;
+    if (f == OR_Q8_K && is_k(w->type)) {
+        const int nb = w->cols / 256;
+        b_q8_k* q = (b_q8_k*)malloc((size_t)nb * sizeof(b_q8_k));
+        memcpy(q, a, (size_t)nb * sizeof(b_q8_k));
+        for (int b = 0; b < nb; b++)
+            for (int g = 0; g < 16; g++) {
+                int sum = 0;
+                for (int i = 0; i < 16; i++) sum += q[b].qs[16 * g + i];
+                q[b].bsums[g] = (int16_t)sum;
+            }
+        or_matvec_q(w->type, w->data, w->rsz, w->cols, w->rows, q, out, NULL);
+        free(q);
+    } else if (f == OR_Q8_0 && is_q8_0_family(w->type)) {
+        or_matvec_q(w->type, w->data, w->rsz, w->cols, w->rows, a, out, NULL);
+    } else {
+        mv(w, x, out);
+    }
+}
+
 int or_inference(or_state* s, int tok, float* logits)
 {
     const or_model* m = &s->m;
@@ -660,7 +701,9 @@ int or_inference(or_state* s, int tok, float* logits)
     if (pos < 0 || pos >= m->n_context || tok < 0 || tok >= m->token_embd.rows) return -1;
     s->pos++;
     float* tr = s->trace;   /* one step only */
+    const uint8_t* fc = s->force;
     s->trace = NULL;
+    s->force = NULL;
 
     or_dequantize_row(m->token_embd.type, (const uint8_t*)m->token_embd.data + (size_t)tok * m->token_embd.rsz, s->x, ne);
 
@@ -668,9 +711,9 @@ int or_inference(or_state* s, int tok, float* logits)
         const or_layer* L = &m->layers[l];
         or_rmsnorm(s->xb, s->x, L->att_norm, ne, m->rms_epsilon);
         trace_vec(s, tr, 4 * l, s->xb, ne);
-        mv(&L->att_q, s->xb, s->q);
-        mv(&L->att_k, s->xb, s->k);
-        mv(&L->att_v, s->xb, s->v);
+        mv_at(s, fc, 4 * l, &L->att_q, s->xb, s->q);
+        mv_at(s, fc, 4 * l, &L->att_k, s->xb, s->k);
+        mv_at(s, fc, 4 * l, &L->att_v, s->xb, s->v);
         if (m->arch == 1) {
             for (int h = 0; h < m->n_heads; h++) or_rmsnorm(s->q + h * hd, s->q + h * hd, L->att_q_norm, hd, m->rms_epsilon);
             for (int h = 0; h < m->n_kv_heads; h++) or_rmsnorm(s->k + h * hd, s->k + h * hd, L->att_k_norm, hd, m->rms_epsilon);
@@ -685,22 +728,22 @@ int or_inference(or_state* s, int tok, float* logits)
         or_attention(s->q, s->k, s->v, s->kc + loff, s->vc + loff, m->n_heads, m->n_kv_heads, hd, pos, s->xb);
 
         trace_vec(s, tr, 4 * l + 1, s->xb, ne);
-        mv(&L->att_out, s->xb, s->xb2);
+        mv_at(s, fc, 4 * l + 1, &L->att_out, s->xb, s->xb2);
         for (int j = 0; j < ne; j++) s->x[j] += s->xb2[j];
 
         or_rmsnorm(s->xb, s->x, L->ffn_norm, ne, m->rms_epsilon);
         trace_vec(s, tr, 4 * l + 2, s->xb, ne);
-        mv(&L->ffn_up, s->xb, s->hb);
-        mv(&L->ffn_gate, s->xb, s->hb2);
+        mv_at(s, fc, 4 * l + 2, &L->ffn_up, s->xb, s->hb);
+        mv_at(s, fc, 4 * l + 2, &L->ffn_gate, s->xb, s->hb2);
         or_swiglu(s->hb, s->hb2, m->n_ff);
         trace_vec(s, tr, 4 * l + 3, s->hb, m->n_ff);
-        mv(&L->ffn_down, s->hb, s->xb);
+        mv_at(s, fc, 4 * l + 3, &L->ffn_down, s->hb, s->xb);
         for (int j = 0; j < ne; j++) s->x[j] += s->xb[j];
     }
 
     or_rmsnorm(s->x, s->x, m->output_norm, ne, m->rms_epsilon);
     trace_vec(s, tr, 4 * m->n_layers, s->x, ne);
-    mv(&m->output, s->x, s->logits);
+    mv_at(s, fc, 4 * m->n_layers, &m->output, s->x, s->logits);
     if (logits) memcpy(logits, s->logits, (size_t)m->vocab_size * 4);
     return 0;
 }

@@ -117,6 +117,14 @@ int or_inference(or_state* s, int tok, float* logits);
  * layer the rmsnorm'd attention input, the attention output, the rmsnorm'd
  * FFN input and the SwiGLU output, then the rmsnorm'd output-head input */
 void or_state_trace(or_state* s, float* trace);
+/* the next or_inference takes quantized activations from acts instead of
+ * quantizing its own: at point k (numbered as in the trace) where forms[k]
+ * is OR_Q8_K or OR_Q8_0, the matvecs whose weights read that form read the
+ * blocks at acts + k*stride (block_q8_K / block_q8_0 layout; Q8_K bsums are
+ * recomputed from the quants).  Each point of a step then starts from the
+ * same quantized inputs as the step that recorded acts.  acts and forms must
+ * outlive that call. */
+void or_state_force(or_state* s, const void* acts, size_t stride, const int* forms);
 /* fp16 KV rows of one layer for positions [p0, p0+np) */
 void or_state_kv(const or_state* s, int layer, int p0, int np, uint16_t* k, uint16_t* v);
 void or_state_kv_write(or_state* s, int layer, int p0, int np, const uint16_t* k, const uint16_t* v);

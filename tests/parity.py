@@ -18,6 +18,14 @@ pre-rounding value within FLIP_TOL of k + 1/2.  Everything after it in the
 step depends on the flipped value, so the walk stops there.  A step with no
 differing int8 at all must match the oracle's logits to fp32 noise.
 
+``forced_flips`` compares every activation of a step instead: the oracle
+step takes the GPU's quantized activations as the inputs of its matvecs
+(or_state_force), so activation k is formed from the same quantized
+activations < k on both sides, a flip does not propagate, and each of the
+4 n_layers + 1 activations is held to the flip rule on its own.  The logits
+of such a step are then a function of the same quantized head input on both
+sides and must agree to fp32 noise.
+
 Q8_0 blocks also carry an fp16 scale, fp16(amax / 127), which the next matvec
 multiplies in: when amax / 127 lies on an fp16 rounding tie, an amax one fp32
 ulp apart rounds the scale one fp16 ulp (~1e-3) the other way with every int8
@@ -58,6 +66,15 @@ TIE_TOL = 1e-4
 SCALE_TIE_TOL = 0.1
 # logits rel-L2 of a step whose int8 activations all agree with the oracle's
 EXACT_STEP = 1e-5
+# with the GPU's quantized activations forced into the oracle step every
+# activation is formed from identical quantized inputs: a differing int8 is
+# then within fp32 noise of a boundary (at most 3.1e-5 from it over every
+# step measured: the 36-layer Qwen3-8B-shape Q4_K and Q1_G models at 13
+# positions and the small models of the GPU suite), so a one-step
+# difference farther than 1e-3 is no flip; the logits, one matvec of the same
+# head input, agree to ~8e-8 (at most 8.4e-8 measured)
+FORCED_FLIP_TOL = 1e-3
+FORCED_STEP = 1e-6
 
 K_FAMILY = {10, 11, 12, 13, 14}   # Q2_K..Q6_K read Q8_K activations
 
@@ -146,6 +163,37 @@ def scale_diffs(buf: np.ndarray, x: np.ndarray, qtype: int, n: int):
     return diff, np.where(neighbours, dist, 1.0)
 
 
+def slot_check(gbuf: np.ndarray, x: np.ndarray, qt: int, n: int, tag=(), flip_tol=FLIP_TOL):
+    """One quantized activation: the GPU's blocks `gbuf` against the
+    as-compiled quantizer applied to the oracle's float vector x at the same
+    point.  Returns (differs, unexplained): every differing int8 must be one
+    step away with the oracle's pre-rounding value within FLIP_TOL of k + 1/2,
+    at most max(8, MAX_FLIP_FRAC n) of them off exact ties, and every
+    differing Q8_0 scale must sit within SCALE_TIE_TOL of an fp16 tie.
+    Returns (differs, unexplained, largest boundary distance of a differing
+    int8); entries of `unexplained` start with `tag`."""
+    qg, _ = parse_q(gbuf, qt, n)
+    qo, v = quantize_ref(x[:n], qt)
+    diff = np.nonzero(qg != qo)[0]
+    sdiff, sdist = scale_diffs(gbuf, x, qt, n)
+    if diff.size == 0 and sdiff.size == 0:
+        return False, [], 0.0
+    bad = []
+    dists = boundary_dist(v[diff])
+    nties = int(np.sum(dists < TIE_TOL))
+    if diff.size - nties > max(8, int(MAX_FLIP_FRAC * n)):
+        bad.append(tag + (-1, int(diff.size), n, 0.0, 1.0))
+    for i in diff:
+        step = abs(int(qg[i]) - int(qo[i]))
+        dist = float(boundary_dist(v[i:i + 1])[0])
+        if step != 1 or dist > flip_tol:
+            bad.append(tag + (int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
+    for b, dist in zip(sdiff, sdist):
+        if dist > SCALE_TIE_TOL:
+            bad.append(tag + (-2, int(b), 0, 0.0, float(dist)))     # a scale off an fp16 tie
+    return True, bad, float(dists.max()) if diff.size else 0.0
+
+
 def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
     """(first differing activation or -1, list of unexplained differences).
 
@@ -154,26 +202,29 @@ def step_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg):
     for k, (qt, n) in enumerate(slot_formats(cfg)):
         if qt is None:
             continue
-        qg, _ = parse_q(gpu_trace[k], qt, n)
-        qo, v = quantize_ref(oracle_trace[k][:n], qt)
-        diff = np.nonzero(qg != qo)[0]
-        sdiff, sdist = scale_diffs(gpu_trace[k], oracle_trace[k], qt, n)
-        if diff.size == 0 and sdiff.size == 0:
-            continue
-        bad = []
-        nties = int(np.sum(boundary_dist(v[diff]) < TIE_TOL))
-        if diff.size - nties > max(8, int(MAX_FLIP_FRAC * n)):
-            bad.append((k, -1, int(diff.size), n, 0.0, 1.0))
-        for i in diff:
-            step = abs(int(qg[i]) - int(qo[i]))
-            dist = float(boundary_dist(v[i:i + 1])[0])
-            if step != 1 or dist > FLIP_TOL:
-                bad.append((k, int(i), int(qg[i]), int(qo[i]), float(v[i]), dist))
-        for b, dist in zip(sdiff, sdist):
-            if dist > SCALE_TIE_TOL:
-                bad.append((k, -2, int(b), 0, 0.0, float(dist)))     # a scale off an fp16 tie
-        return k, bad
+        differs, bad, _ = slot_check(gpu_trace[k], oracle_trace[k], qt, n, (k,))
+        if differs:
+            return k, bad
     return -1, []
+
+
+def forced_flips(gpu_trace: np.ndarray, oracle_trace: np.ndarray, cfg, flip_tol=FORCED_FLIP_TOL):
+    """Every quantized activation of a step against an oracle step that took
+    the GPU's quantized activations as its inputs (or_state_force): there each
+    activation k is computed from the same quantized activations < k on both
+    sides, so no flip propagates and every one of the 4 L + 1 points is
+    compared, with differing values held to flip_tol.  Returns (compared, differing, unexplained, largest boundary
+    distance of a differing int8)."""
+    compared, differing, bad, worst = 0, 0, [], 0.0
+    for k, (qt, n) in enumerate(slot_formats(cfg)):
+        if qt is None:
+            continue
+        differs, b, d = slot_check(gpu_trace[k], oracle_trace[k], qt, n, (k,), flip_tol)
+        compared += 1
+        differing += int(differs)
+        bad += b
+        worst = max(worst, d)
+    return compared, differing, bad, worst
 
 
 def prefill_flips(gpu_trace: np.ndarray, oracle_traces, cfg):
@@ -234,6 +285,6 @@ def flip_summary(rows):
            f"{flips} with rounding flips only, {bad} unexplained"
 
 
-__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "TIE_TOL", "SCALE_TIE_TOL", "EXACT_STEP", "slot_formats", "parse_q",
-           "quantize_ref", "scale_diffs", "step_flips", "prefill_flips", "flip_summary",
+__all__ = ["FLIP_TOL", "MAX_FLIP_FRAC", "TIE_TOL", "SCALE_TIE_TOL", "EXACT_STEP", "FORCED_FLIP_TOL", "FORCED_STEP", "slot_formats", "parse_q",
+           "quantize_ref", "scale_diffs", "slot_check", "step_flips", "forced_flips", "prefill_flips", "flip_summary",
            "F16", "F32"]

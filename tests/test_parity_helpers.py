@@ -4,11 +4,12 @@ the oracle's int8 values bit for bit (the oracle itself is pinned to the
 reference's golden vectors in test_oracle.py), and a planted off-boundary
 difference must be reported."""
 import numpy as np
+import pytest
 
 from conftest import golden
 from ligguf_amd.lib import Q8_0, Q8_K
 from ligguf_amd.model import TINY
-from parity import boundary_dist, parse_q, prefill_flips, quantize_ref, slot_formats, step_flips
+from parity import boundary_dist, forced_flips, parse_q, prefill_flips, quantize_ref, slot_formats, step_flips
 
 
 def _vectors():
@@ -176,3 +177,124 @@ def test_scale_flips(oracle):
     # two ulps off a tie is no flip either
     first, bad = run(1171.5, 1170)
     assert first == 0 and bad and bad[0][5] == 1.0
+
+
+# ---------------- forced activations (or_state_force) ----------------
+def _k_model():
+    """Small K-quant model with a Q8_0 consumer beside Q4_K ones in the
+    attention input (that activation is recorded in the Q8_K form; the
+    Q8_0 matvec quantizes its own)."""
+    from ligguf_amd.lib import ARCH_QWEN3, Q4_K, Q6_K
+    from ligguf_amd.model import ModelConfig
+    return ModelConfig("k-mix", ARCH_QWEN3, 3, 256, 4, 2, 64, 512, 700, 32, 1e6, 1e-6, Q4_K, Q4_K, Q6_K,
+                       overrides=(("attn_v", Q8_0), ("ffn_down", Q6_K)))
+
+
+def _quantized(oracle, cfg, tr):
+    """[4L+1][stride] blocks: each traced float vector through the oracle's
+    own quantizer in its recorded form."""
+    fm = slot_formats(cfg)
+    stride = max(n // 256 * 292 for _, n in fm)
+    acts = np.zeros((len(fm), stride), np.uint8)
+    for k, (qt, n) in enumerate(fm):
+        if qt is not None:
+            b = (oracle.quantize_q8_K if qt == Q8_K else oracle.quantize_q8_0)(tr[k][:n])
+            acts[k, :b.size] = b
+    return acts
+
+
+def _forced_state(oracle, cfg, npos):
+    """An oracle state after npos unforced steps (with the host model whose
+    arrays it points into), the next token, its logits and trace."""
+    from oracle.binding import OrLayer, OrModel, OrWeight
+    from ligguf_amd.model import HostModel
+    hm = HostModel.synthetic(cfg)
+    st = oracle.new_state(hm.fill_desc(OrModel, OrLayer, OrWeight))
+    toks = np.random.default_rng(5).integers(1, cfg.vocab, npos + 1)
+    for t in toks[:npos]:
+        oracle.inference(st, int(t), cfg.vocab)
+    lg, tr = oracle.inference_traced(st, int(toks[npos]), cfg)
+    return (hm, st), int(toks[npos]), lg, tr
+
+
+def _forced(oracle, st, cfg, pos, tok, acts):
+    oracle.L.or_state_set_pos(st, pos)
+    return oracle.inference_forced(st, tok, cfg, acts, [f for f, _ in slot_formats(cfg)])
+
+
+def _bump_q(acts, k, qt, i):
+    """one int8 of activation k one step up (or down at 127)"""
+    qk, bs = (256, 292) if qt == Q8_K else (32, 34)
+    blk, j = divmod(i, qk)
+    off = blk * bs + (4 if qt == Q8_K else 2) + j
+    q = int(acts[k, off].view(np.int8))
+    acts[k, off] = np.uint8((q + (1 if q < 127 else -1)) & 255)
+
+
+def _consistent(oracle, st, cfg, pos, tok, acts, k):
+    """acts with every activation after k re-quantized from a forced step
+    over acts (repeated until stable): what a GPU step whose activation k
+    went wrong would record after it."""
+    for _ in range(len(slot_formats(cfg))):
+        _, tr = _forced(oracle, st, cfg, pos, tok, acts)
+        nxt = _quantized(oracle, cfg, tr)
+        new = acts.copy()
+        new[k + 1:] = nxt[k + 1:]
+        if np.array_equal(new, acts):
+            return acts
+        acts = new
+    raise AssertionError("forced re-quantization did not settle")
+
+
+@pytest.mark.parametrize("which", ["tiny", "kmix"])
+def test_forced_step_reproduces_own_activations(oracle, which):
+    """Forcing a step's own quantized activations back into it changes
+    nothing: logits and every traced vector bit for bit, every activation
+    compared and equal.  A wrong slot offset, form or block layout in the
+    forced path would break this."""
+    cfg = TINY.with_(n_context=16) if which == "tiny" else _k_model()
+    (hm, st), tok, lg, tr = _forced_state(oracle, cfg, 5)
+    acts = _quantized(oracle, cfg, tr)
+    lg2, tr2 = _forced(oracle, st, cfg, 5, tok, acts)
+    assert np.array_equal(lg.view(np.uint32), lg2.view(np.uint32))
+    assert np.array_equal(tr.view(np.uint32), tr2.view(np.uint32))
+    nq = sum(1 for f, _ in slot_formats(cfg) if f is not None)
+    assert nq == 4 * cfg.n_layers + 1
+    assert forced_flips(acts, tr2, cfg) == (nq, 0, [], 0.0)
+    # the Q8_K bsums are recomputed from the quants, not read
+    if which == "kmix":
+        a2 = acts.copy()
+        a2[0, 260:292] = 0x55
+        lg3, _ = _forced(oracle, st, cfg, 5, tok, a2)
+        assert np.array_equal(lg.view(np.uint32), lg3.view(np.uint32))
+    oracle.free_state(st)
+
+
+@pytest.mark.parametrize("which", ["tiny", "kmix"])
+def test_forced_flips_localise_planted_differences(oracle, which):
+    """A one-step int8 change far from a rounding boundary at one activation
+    -- the attention output of layer 0, the SwiGLU output of the last layer,
+    the output head's input -- is reported at that activation and nowhere
+    else once the activations after it follow from it; the changed value is
+    read (the next activation, or the logits, move)."""
+    cfg = TINY.with_(n_context=16) if which == "tiny" else _k_model()
+    (hm, st), tok, lg, tr = _forced_state(oracle, cfg, 5)
+    base = _quantized(oracle, cfg, tr)
+    fm = slot_formats(cfg)
+    nq = len(fm)
+    for k in (1, 4 * cfg.n_layers - 1, 4 * cfg.n_layers):
+        qt, n = fm[k]
+        _, v = quantize_ref(tr[k][:n], qt)
+        far = int(np.argmax(boundary_dist(v)))
+        acts = base.copy()
+        _bump_q(acts, k, qt, far)
+        acts = _consistent(oracle, st, cfg, 5, tok, acts, k)
+        lg2, tr2 = _forced(oracle, st, cfg, 5, tok, acts)
+        if k < nq - 1:
+            assert not np.array_equal(tr[k + 1], tr2[k + 1])     # the next activation reads it
+        else:
+            assert not np.array_equal(lg, lg2)                   # the logits read the head's input
+        compared, differing, bad, _ = forced_flips(acts, tr2, cfg)
+        assert compared == nq and differing == 1
+        assert len(bad) == 1 and bad[0][:2] == (k, far), bad
+    oracle.free_state(st)
