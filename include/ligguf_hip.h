@@ -342,11 +342,15 @@ int lg_attn_decode(const float* q, const float* k, const float* v, const uint16_
  * forbid it).  No counterpart in the reference.  The partials go to a scratch
  * area of lg_attn_scratch_bytes() (8 MiB) that the library keeps in each
  * device's memory until the process ends; a call whose partials
- * (lg_attn_workspace_size) exceed it fails with LG_ERR_ARG.  The calling
- * thread's current device must be the one that owns the pointers and the
- * stream.  Nothing is allocated: every call on a device shares that device's
- * scratch area, so calls that overlap on one device (other streams, other
- * threads) race.  Same kernels and same results as lg_attn_decode. */
+ * (lg_attn_workspace_size) exceed it fails with LG_ERR_ARG -- at 32 heads of
+ * 128 that is any position past 2064383.  The calling thread's current
+ * device must be the one that owns the pointers and the stream.  The scratch
+ * area's address on a device is looked up by lg_create on that device, else
+ * by the first call there; a first call on a device under graph capture
+ * fails with LG_ERR_STATE.  Nothing is allocated: every call on a device
+ * shares that device's scratch area, so calls that overlap on one device
+ * (other streams, other threads) race.  Same kernels and same results as
+ * lg_attn_decode. */
 size_t lg_attn_scratch_bytes(void);
 int lg_attn_decode_noalloc(const float* q, const float* k, const float* v, const uint16_t* kc, const uint16_t* vc,
                            int n_heads, int n_kv_heads, int head_dim, int pos, float* out, void* stream);

@@ -90,18 +90,20 @@ static int attn_nch_bound(int head_dim, int pos)
         const int nmin = (ctx + LG_ATTN_TMAX - 1) / LG_ATTN_TMAX;
         return nmin > LG_ATTN_TCH ? nmin : LG_ATTN_TCH;
     }
+    /* attn_chunk: chunks of 64 keys up to 8192 keys (at most 128 chunks),
+     * at most 128 chunks up to 131072 keys, chunks of LG_ATTN_MAX_CHUNK past */
+    const int small = (ctx + 63) / 64 < 128 ? (ctx + 63) / 64 : 128;
     const int over = (ctx + LG_ATTN_MAX_CHUNK - 1) / LG_ATTN_MAX_CHUNK;
-    return over > 128 ? over : 128;
+    return over > small ? over : small;
 }
 
 size_t lg_attn_ws_bytes(int n_heads, int head_dim, int pos)
 {
     if (n_heads <= 0 || head_dim <= 0 || pos < 0) return 0;
-    /* the three-pass kernel of head_dim 48 and position 0 as well, at any
-     * earlier position */
-    int nb = attn_nch_bound(head_dim, pos);
-    const int nb3 = attn_nch_bound(48, pos);
-    if (nb3 > nb) nb = nb3;
+    /* a workspace sized for pos serves every earlier position (for the
+     * tiled head sizes that includes position 0, one chunk of the
+     * three-pass kernel) */
+    const int nb = attn_nch_bound(head_dim, pos);
     return (size_t)n_heads * nb * (head_dim + 2) * sizeof(float);
 }
 
@@ -665,28 +667,38 @@ int lg_launch_attn(const float* q, const float* k, const float* v, const uint16_
 /* lg_attn_decode_noalloc: the same kernels on a scratch area that the */
 /* library holds in device memory for the life of the process          */
 /* ------------------------------------------------------------------ */
-/* 8 MiB per device: lg_attn_ws_bytes for 32 heads of 128 at up to ~2M
- * positions (504 chunks), 64 heads of 256 at up to ~500k.  Every partial is
- * written before it is read, so nothing needs clearing between calls. */
+/* 8 MiB per device: lg_attn_ws_bytes for 32 heads of 128 up to position
+ * 2064383 (504 chunks of 4096 keys), 64 heads of 256 up to 520191 (127
+ * chunks).  Every partial is written before it is read, so nothing needs
+ * clearing between calls. */
 #define LG_ATTN_SCRATCH_BYTES ((size_t)8 << 20)
 #define LG_ATTN_SCRATCH_DEVICES 64
 
 static __device__ __align__(256) float scratch[LG_ATTN_SCRATCH_BYTES / sizeof(float)];
 
 /* the device address of `scratch` on each device, looked up once per device
- * (with that device current) at the entry point's first call there; host code
- * passes only these addresses to kernels */
+ * with that device current: by lg_create for its device, else by the entry
+ * point's first call there; host code passes only these addresses to
+ * kernels */
 static void* g_scratch_dev[LG_ATTN_SCRATCH_DEVICES];
 static std::mutex g_scratch_mu;
 
-static int attn_scratch(void** out)
+static int scratch_device(int* dev)
 {
-    int dev = 0;
-    LG_HIP_CHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= LG_ATTN_SCRATCH_DEVICES) {
-        lg_set_error("attention scratch: device %d beyond the %d supported", dev, LG_ATTN_SCRATCH_DEVICES);
+    LG_HIP_CHECK(hipGetDevice(dev));
+    if (*dev < 0 || *dev >= LG_ATTN_SCRATCH_DEVICES) {
+        lg_set_error("attention scratch: device %d beyond the %d supported", *dev, LG_ATTN_SCRATCH_DEVICES);
         return LG_ERR_ARG;
     }
+    return LG_OK;
+}
+
+/* looks up the current device's scratch address (once per device) */
+int lg_attn_scratch_setup(void)
+{
+    int dev = 0;
+    const int rc = scratch_device(&dev);
+    if (rc) return rc;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_dev[dev]) {
         void* p = nullptr;
@@ -697,6 +709,30 @@ static int attn_scratch(void** out)
         }
         g_scratch_dev[dev] = p;
     }
+    return LG_OK;
+}
+
+/* the current device's scratch address; the lookup is not made while the
+ * stream is being captured into a graph */
+static int attn_scratch(hipStream_t stream, void** out)
+{
+    int dev = 0;
+    int rc = scratch_device(&dev);
+    if (rc) return rc;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        *out = g_scratch_dev[dev];
+    }
+    if (*out) return LG_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    LG_HIP_CHECK(hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone) {
+        lg_set_error("attention (no allocation): the scratch area of device %d is not set up; create a context on "
+                     "it (lg_create) or make one call outside graph capture first", dev);
+        return LG_ERR_STATE;
+    }
+    if ((rc = lg_attn_scratch_setup())) return rc;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
     *out = g_scratch_dev[dev];
     return LG_OK;
 }
@@ -714,7 +750,7 @@ extern "C" int lg_attn_decode_noalloc(const float* q, const float* k, const floa
         return LG_ERR_ARG;
     }
     void* ws = nullptr;
-    const int rc = attn_scratch(&ws);
+    const int rc = attn_scratch((hipStream_t)stream, &ws);
     if (rc) return rc;
     return lg_launch_attn(q, k, v, kc, vc, n_heads, n_kv_heads, head_dim, pos, out, ws, LG_ATTN_SCRATCH_BYTES,
                           (hipStream_t)stream);

@@ -301,6 +301,8 @@ int lg_launch_matvec(int type, const void* w, uint32_t rsz, int n, int d, const 
 
 /* lg_attn.hip */
 size_t lg_attn_ws_bytes(int n_heads, int head_dim, int pos);
+/* looks up the no-allocation attention's scratch address on the current device */
+int lg_attn_scratch_setup(void);
 int lg_launch_attn(const float* q, const float* k, const float* v, const uint16_t* kc, const uint16_t* vc,
                    int n_heads, int n_kv_heads, int head_dim, int pos, float* out, void* ws, size_t ws_bytes,
                    hipStream_t s);

@@ -20,6 +20,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
 
 #include <string>
 #include <initializer_list>
@@ -226,6 +227,8 @@ extern "C" int lg_create(int device, lg_ctx** out)
     LG_HIP_CHECK(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) { lg_set_error("lg_create: device %d of %d", device, n); return LG_ERR_ARG; }
     LG_HIP_CHECK(hipSetDevice(device));
+    int rc = lg_attn_scratch_setup();   /* before any caller's graph capture on this device */
+    if (rc) return rc;
     lg_ctx* ctx = new lg_ctx();
     ctx->device = device;
     const char* ng = getenv("LG_NO_GRAPH");
@@ -1712,6 +1715,18 @@ extern "C" int lg_state_load(lg_ctx* ctx, const char* path, int* pos_out, float*
     }
     const int pos = hdr.pos;
     const size_t blk = (size_t)pos * ctx->kv_dim * 2, lbytes = (size_t)ctx->vocab * 4;
+    /* load_model_state reads into a copy and keeps the old state when a
+     * read fails (fast/ligguf_fast_qk.cpp:224-259); here the file must hold
+     * every block before the first one reaches the cache, so a short file
+     * leaves the cache untouched */
+    const uint64_t need = sizeof(hdr) + 2 * hdr.kv_size * 2 + hdr.logits_size * 4;
+    struct stat fst;
+    if (fstat(fileno(f), &fst) || (uint64_t)fst.st_size < need) {
+        fclose(f);
+        lg_set_error("lg_state_load: %s is truncated (%lld bytes, %llu needed)", path, (long long)fst.st_size,
+                     (unsigned long long)need);
+        return ctx_fail(ctx, LG_ERR_STATE);
+    }
     lg_pinned buf;
     const hipError_t ea = hipHostMalloc(&buf.p, std::max(blk, lbytes), 0);
     if (ea != hipSuccess) {

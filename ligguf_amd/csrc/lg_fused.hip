@@ -162,12 +162,19 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_down(const PkParams P, const P
         P.xs + (size_t)(l + 1) * ne, nullptr, 0, 0, f_tr(Sd, l, 4), f_atr(atr, P, 4 * l + 3), nff);
 }
 
-/* OT may be a regrouped form (LG_Q8_0_R, LG_Q6_K_R): the head's copy in P.out_wr */
+/* the regrouped forms (lg_repack_rows): a head of one of them is read from
+ * its copy in P.out_wr */
+static constexpr bool f_is_rep(int t)
+{
+    return t == LG_Q8_0_R || t == LG_Q6_K_R || t == LG_Q1_G_R || t == LG_Q3_K_R || t == LG_Q1_0_R;
+}
+
+/* OT may be a regrouped form: the head's copy in P.out_wr */
 template <int OT, class S>
 __global__ __launch_bounds__(PK_THREADS) void k_f_out(const PkParams P, PkStep* __restrict__ Sd, uint8_t* atr)
 {
     constexpr int NO = S::NO;
-    const uint8_t* W = (OT == LG_Q8_0_R || OT == LG_Q6_K_R) ? P.out_wr : P.out_w;
+    const uint8_t* W = f_is_rep(OT) ? P.out_wr : P.out_w;
     const int pos = Sd->pos;
     /* the step trace holds one slot per workgroup of the layer grid: the
      * first gridDim.x / LG_OUT_WGS workgroups stamp theirs */
@@ -202,6 +209,7 @@ static constexpr int f_rep(int t)
 template <int OT, class SH>
 static void f_launch_out(const PkParams& P, PkStep* S, int nwg, dim3 b, hipStream_t st, uint8_t* atr)
 {
+    static_assert(f_rep(OT) == OT || f_is_rep(f_rep(OT)), "k_f_out reads every form f_rep makes from P.out_wr");
     if (f_rep(OT) != OT && P.out_wr)
         hipLaunchKernelGGL((k_f_out<f_rep(OT), SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, atr);
     else hipLaunchKernelGGL((k_f_out<OT, SH>), dim3(nwg * LG_OUT_WGS), b, 0, st, P, S, atr);

@@ -114,6 +114,20 @@ def test_state_rejects_bad_files(tiny_state):
         f.write(raw[:100])                                        # truncated
     with pytest.raises(LgError):
         eng.state_load(bad)
+    # a file cut inside the V blocks: rejected before any block reaches the
+    # cache, as load_model_state keeps the old state on a failed read
+    k0, v0 = eng.kv_read(0, TINY.n_layers, 0, 1)
+    other = str(d / "other.state")
+    eng.decode(2, 0)                                              # another row 0 ...
+    eng.state_save(other, 1)
+    eng.kv_write(0, TINY.n_layers, 0, 1, k0, v0)                  # ... and back
+    raw2 = open(other, "rb").read()
+    with open(bad, "wb") as f:
+        f.write(raw2[:len(raw2) - TINY.vocab * 4 - 8])
+    with pytest.raises(LgError, match="truncated"):
+        eng.state_load(bad)
+    k1, v1 = eng.kv_read(0, TINY.n_layers, 0, 1)
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
     hdr = bytearray(raw)
     hdr[8:16] = (12345).to_bytes(8, "little")                     # kv_size of another model
     with open(bad, "wb") as f:
