@@ -20,7 +20,9 @@ on its own through lg_time_fused_phase over all 36 layers in turn (2 GB of
 distinct weights, far above the 256 MB Infinity Cache) and timed with HIP
 events on the stream it runs on; `cpu_baseline` is the reference FAST engine
 (built from its own sources, AVX2) decoding the same model on this host's
-cores.
+cores at the GPU's positions, from the state the GPU saved after its
+prefill.  `hbm_practical` holds two measured bounds: a read-only pass over
+2 GiB (lg_hbm_read_probe) and a device copy.
 """
 from __future__ import annotations
 
@@ -96,6 +98,22 @@ def plain_copy(torch, nbytes: int = 256 << 20, reps: int = 20):
     del src, dst
     torch.cuda.empty_cache()
     return {"bytes_each_way": nbytes, "avg_us": round(avg_s * 1e6, 2), "GB/s": round(2 * nbytes / avg_s / 1e9, 1)}
+
+
+def plain_read(torch, nbytes: int = 2 << 30, iters: int = 10):
+    """lg_hbm_read_probe over a buffer of nbytes (8x the 256 MiB last-level
+    cache): the practical read-only HBM rate, the bound a decode step that
+    only reads weights and cache rows can reach."""
+    import ctypes as C
+    from ligguf_amd import lib as L
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    us = C.c_float()
+    L.check(L.load().lg_hbm_read_probe(C.c_void_p(buf.data_ptr()), nbytes, iters, C.byref(us),
+                                       C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    del buf
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "avg_us": round(us.value, 2), "GB/s": round(nbytes / (us.value * 1e-6) / 1e9, 1)}
 
 
 MFMA_INT8_PEAK = 5.0e15    # MI355X dense int8, ops/s
@@ -443,11 +461,15 @@ def _ref_bind(R, hm):
     R.model_bind(m)
 
 
-def cpu_baseline(hm, seconds: float, prompt_tokens: int = 64, max_tokens: int = 4000):
+def cpu_baseline(hm, state_path: str, last_pos: int, prompt_tokens: int = 64):
     """The reference FAST engine (oracle/_ref, AVX2, OpenMP) on the same host
-    model: its prefill (feed_text: one inference() per prompt token,
-    fast/ligguf_fast_qk.cpp:340-356) over `prompt_tokens` random ids, then
-    greedy decode from there for about `seconds`."""
+    model, decoding the GPU's positions: it loads the state the GPU saved
+    after its 512-token prefill (the reference's own state-file format,
+    load_model_state, fast/ligguf_fast_qk.cpp:216-263) and decodes greedily
+    from there through `last_pos`, the GPU's last timed position.  Its
+    prefill rate (feed_text: one inference() per prompt token,
+    fast/ligguf_fast_qk.cpp:340-356) is timed on `prompt_tokens` random ids
+    beforehand."""
     import numpy as np
     from oracle import binding
     if not binding.reference_available():
@@ -461,12 +483,13 @@ def cpu_baseline(hm, seconds: float, prompt_tokens: int = 64, max_tokens: int = 
     prompt = rng.integers(1, c.vocab, prompt_tokens)
     t0 = time.perf_counter()
     for t in prompt:
-        logits = R.inference(int(t), c.vocab)
+        R.inference(int(t), c.vocab)
     pf_s = time.perf_counter() - t0
-    max_tokens = min(max_tokens, c.n_context - prompt_tokens - 2)
+    R.state_load(state_path)
+    pos0 = R.get_pos()
+    tok = int(np.argmax(R.logits(c.vocab)))
     n, t0 = 0, time.perf_counter()
-    tok = int(np.argmax(logits))
-    while n < max_tokens and (time.perf_counter() - t0 < seconds or n < 2):
+    while pos0 + n <= last_pos:
         logits = R.inference(tok, c.vocab)
         tok = int(np.argmax(logits))
         n += 1
@@ -475,9 +498,10 @@ def cpu_baseline(hm, seconds: float, prompt_tokens: int = 64, max_tokens: int = 
     threads = ci.get("omp_threads")
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
             "prefill_tok_s": round(prompt_tokens / pf_s, 3), "cpu": ci,
-            "sample": f"prefill of {prompt_tokens} random ids (token by token, as feed_text), then {n} greedy "
-                      f"decode tokens at positions {prompt_tokens}..{prompt_tokens + n - 1} of the same model "
-                      f"(reference FAST engine, AVX2 build, {threads} OpenMP threads)"}
+            "sample": f"{n} greedy decode tokens at positions {pos0}..{pos0 + n - 1} from the state the GPU saved "
+                      f"after its {pos0}-token prefill, the GPU's timed positions among them (reference FAST engine, "
+                      f"AVX2 build, {threads} OpenMP threads); prefill rate from {prompt_tokens} random ids fed "
+                      f"token by token, as feed_text"}
 
 
 def cpu_baseline_q1g(hm, state_path: str, seconds: float, max_tokens: int = 64):
@@ -647,6 +671,11 @@ def main() -> int:
     prefill_s = time.perf_counter() - t0
     log(f"prefill {args.prefill} tokens: {args.prefill / prefill_s:.1f} tok/s")
     prefill = prefill_report(cfg, args.prefill, prefill_s, eng.prefill_path())
+    state = None
+    if not args.no_cpu:
+        import tempfile
+        state = os.path.join(tempfile.mkdtemp(prefix="lg_q4k_"), "prefill.state")
+        eng.state_save(state, args.prefill)        # the CPU baseline decodes from here
 
     pos = args.prefill
     tok = int(np.argmax(logits))
@@ -686,6 +715,8 @@ def main() -> int:
 
     copy = plain_copy(torch)
     log(f"plain copy: {copy}")
+    read = plain_read(torch)
+    log(f"plain read: {read}")
     q1g = None if args.no_q1g else q1g_context(torch, np, ctx=args.q1g_ctx,
                                                cpu_seconds=0.0 if args.no_cpu else args.cpu_seconds)
     bert = None if args.no_bert else bert_report(torch, np, 0.0 if args.no_cpu else min(args.cpu_seconds, 10.0))
@@ -694,7 +725,7 @@ def main() -> int:
     if not args.no_cpu:
         t0 = time.perf_counter()
         with _stdout_to_stderr():
-            cpu = cpu_baseline(hm, args.cpu_seconds)
+            cpu = cpu_baseline(hm, state, p_first + args.steps - 1)
         log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f}s)")
 
     out = {
@@ -720,7 +751,10 @@ def main() -> int:
         },
         "decode_host_loop_tok_s": round(host_loop_tps, 1),
         "hbm_roofline_frac_token": round(mean_bytes / (dt / args.steps) / HBM_PEAK, 4),
-        "hbm_practical": {"copy_GB/s": copy["GB/s"], "bytes_each_way": copy["bytes_each_way"],
+        "hbm_practical": {"read_GB/s": read["GB/s"], "read_bytes": read["bytes"],
+                          "read_frac_of_peak": round(read["GB/s"] * 1e9 / HBM_PEAK, 4),
+                          "token_frac_of_read": round(mean_bytes / (dt / args.steps) / (read["GB/s"] * 1e9), 4),
+                          "copy_GB/s": copy["GB/s"], "bytes_each_way": copy["bytes_each_way"],
                           "frac_of_peak": round(copy["GB/s"] * 1e9 / HBM_PEAK, 4),
                           "token_frac_of_practical": round(mean_bytes / (dt / args.steps) / (copy["GB/s"] * 1e9), 4)},
         "prefill_tok_s": round(args.prefill / prefill_s, 1),

@@ -192,6 +192,13 @@ int lg_trace_acts_next_prefill(lg_ctx* ctx, void* trace_dev);
  * everything they touch.  LG_ERR_STATE unless the fused path is in use. */
 int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters, float* avg_us);
 
+/* HBM read probe (no counterpart in the reference; the practical read
+ * bound for benchmarks): reads the `bytes` bytes at buf (device memory,
+ * 16-byte aligned, a multiple of 16) once per pass, `iters` timed passes
+ * after an untimed one on `stream` (NULL: the null stream); *avg_us
+ * receives the mean time per pass.  Writes nothing. */
+int lg_hbm_read_probe(const void* buf, size_t bytes, int iters, float* avg_us, void* stream);
+
 /* Greedy argmax of the current device logits, first index wins ties
  * (sampler_greedy, fast/ligguf_fast_qk.cpp:146-160). */
 int lg_argmax(lg_ctx* ctx, int* tok_out);

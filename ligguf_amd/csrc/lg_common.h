@@ -270,6 +270,7 @@ struct lg_rand_guard {
 
 /* host helper: turn a failed kernel launch into LG_ERR_HIP */
 int lg_check_launch(const char* what);
+int lg_launch_read_probe(const void* buf, size_t bytes, hipStream_t s);
 
 /* internal launchers (lg_kernels.hip) */
 int lg_launch_quantize_q8_0(const float* x, int64_t n, void* y, hipStream_t s);

@@ -831,6 +831,29 @@ extern "C" size_t lg_trace_size(const lg_ctx* ctx)
     return (size_t)(5 * ctx->n_layers + 1) * ctx->pk_nwg * 4 * sizeof(uint64_t);
 }
 
+extern "C" int lg_hbm_read_probe(const void* buf, size_t bytes, int iters, float* avg_us, void* stream)
+{
+    if (iters <= 0 || !avg_us) { lg_set_error("lg_hbm_read_probe: bad arguments"); return LG_ERR_ARG; }
+    hipStream_t s = (hipStream_t)stream;
+    int rc = lg_launch_read_probe(buf, bytes, s);   /* untimed first pass */
+    if (rc) return rc;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    LG_HIP_CHECK(hipEventCreate(&e0));
+    LG_HIP_CHECK(hipEventCreate(&e1));
+    hipEventRecord(e0, s);
+    for (int i = 0; i < iters && !rc; i++) rc = lg_launch_read_probe(buf, bytes, s);
+    hipEventRecord(e1, s);
+    const hipError_t e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (!rc && e == hipSuccess) hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc) return rc;
+    if (e != hipSuccess) { lg_set_error("lg_hbm_read_probe: %s", hipGetErrorString(e)); return LG_ERR_HIP; }
+    *avg_us = ms * 1e3f / (float)iters;
+    return LG_OK;
+}
+
 extern "C" int lg_time_fused_phase(lg_ctx* ctx, int phase, int layer0, int iters, float* avg_us)
 {
     if (!ctx || !avg_us || iters <= 0 || phase < 0 || phase > 5 || layer0 < 0) {

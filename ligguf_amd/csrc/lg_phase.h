@@ -348,6 +348,34 @@ __device__ __forceinline__ void build_plain(const ActSrc<CPW>& a, int n)
 /* ------------------------------------------------------------------ */
 /* matvec phases                                                        */
 /* ------------------------------------------------------------------ */
+/* The grid's greedy row from the per-workgroup partials (P.amax_v/amax_i
+ * [0, n)): the largest value, the lowest row among equal ones -- an
+ * order-free rule, so the NT threads of the calling workgroup reduce the
+ * partials in parallel (strided loads, then lanes, then waves).  Every
+ * thread calls it; thread 0 gets the row (0x7fffffff when no value is a
+ * number). */
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i)
+{
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+template <int NT>
+__device__ __forceinline__ int argmax_partials(const PkParams& P, int n)
+{
+    __shared__ float s_av[NT / 64];
+    __shared__ int s_ai[NT / 64];
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int w = (int)threadIdx.x; w < n; w += NT) argmax_take(bv, bi, cld(&P.amax_v[w]), cld(&P.amax_i[w]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_take(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    if ((threadIdx.x & 63) == 0) { s_av[threadIdx.x >> 6] = bv; s_ai[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < NT / 64; w++) argmax_take(bv, bi, s_av[w], s_ai[w]);
+    return bi;
+}
+
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 /* Items of one phase are split evenly over all waves of the grid in
@@ -582,16 +610,12 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
             s_int[0] = old == gridDim.x - 1;
         }
         bar();
-        if (s_int[0] && LG_TID == 0) {
-            float bv = -INFINITY;
-            int bi = 0x7fffffff;
-            for (int w = 0; w < (int)gridDim.x; w++) {
-                const float v = cld(&P.amax_v[w]);
-                const int i = cld(&P.amax_i[w]);
-                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+        if (s_int[0]) {   /* workgroup-uniform */
+            const int bi = argmax_partials<PK_THREADS>(P, gridDim.x);
+            if (LG_TID == 0) {
+                cst(P.tok_out, bi == 0x7fffffff ? 0 : bi);
+                cst(P.amax_cnt, 0u);
             }
-            cst(P.tok_out, bi == 0x7fffffff ? 0 : bi);
-            cst(P.amax_cnt, 0u);
         }
     }
 }

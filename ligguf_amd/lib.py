@@ -87,6 +87,7 @@ SIGNATURES = {
     "lg_trace_acts_next_prefill": (C.c_int, [_vp, _vp]),
     "lg_trace_acts_size": (C.c_size_t, [_vp]),
     "lg_time_fused_phase": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "lg_hbm_read_probe": (C.c_int, [_vp, C.c_size_t, C.c_int, C.POINTER(C.c_float), _vp]),
     "lg_prefill": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),
     "lg_set_prefill_path": (C.c_int, [_vp, C.c_int]),
     "lg_prefill_path": (C.c_int, [_vp]),

@@ -74,3 +74,6 @@ def test_null_context_errors():
     assert lib.lg_argmax(None, C.byref(t)) == -1
     toks = (C.c_int * 4)()
     assert lib.lg_decode_greedy(None, 1, 0, 4, toks) == -1
+    us = C.c_float()
+    assert lib.lg_hbm_read_probe(None, 1 << 20, 1, C.byref(us), None) == -1      # no buffer
+    assert lib.lg_hbm_read_probe(C.c_void_p(16), 1 << 20, 0, C.byref(us), None) == -1   # no passes

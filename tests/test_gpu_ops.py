@@ -207,3 +207,18 @@ def test_attention_golden(gpu):
     out = host(ops.attention(dev(g["att_q"], gpu), dev(g["att_k"], gpu), dev(g["att_v"], gpu),
                              dev(g["att_kc"], gpu), dev(g["att_vc"], gpu), 8, 2, 128, pos))
     assert np.max(np.abs(out - g["att_out"])) < 1e-5 * np.max(np.abs(g["att_out"]))
+
+
+def test_hbm_read_probe(gpu):
+    """lg_hbm_read_probe reads its buffer: a 1 GiB pass takes at least the
+    time 8 TB/s allows (a rate above the peak would mean loads were dropped)."""
+    import ctypes as C
+    from ligguf_amd import lib as L
+    n = 1 << 30
+    buf = torch.ones(n // 4, dtype=torch.float32, device=gpu)
+    us = C.c_float()
+    L.check(L.load().lg_hbm_read_probe(C.c_void_p(buf.data_ptr()), n, 3, C.byref(us),
+                                       C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    gbs = n / (us.value * 1e-6) / 1e9
+    print(f"\nread probe: {gbs:.0f} GB/s over 1 GiB")
+    assert 1000.0 < gbs < 8100.0
