@@ -174,6 +174,7 @@ struct lg_ctx {
     int dev_tok = 0, dev_pos = 0, dev_feed_end = 0, last_pos = 0;
     bool use_graph = true;
     bool regroup = true;             /* fused kernels read regrouped copies of misaligned formats */
+    bool qkva = true;                /* fused step: QKV and short-context attention in one kernel */
     hipGraphExec_t graph[2] = {nullptr, nullptr};   /* the step with short / long-context attention */
 };
 
@@ -235,6 +236,8 @@ extern "C" int lg_create(int device, lg_ctx** out)
     ctx->use_graph = !(ng && ng[0] == '1');
     const char* nr = getenv("LG_NO_REGROUP");
     ctx->regroup = !(nr && nr[0] == '1');
+    const char* nq = getenv("LG_NO_QKVA");
+    ctx->qkva = !(nq && nq[0] == '1');
     const hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         lg_set_error("hipStreamCreate failed: %s", hipGetErrorString(e));
@@ -614,7 +617,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
      * to LG_OUT_MAX_WGS output-head workgroups per CU */
     const int nwg = ctx->pk_nwg;
     const size_t namax = (size_t)nwg * LG_OUT_MAX_WGS;
-    const size_t cnt_bytes = (size_t)nwg * 8 + namax * 8 + 256 + 32 * PK_ATT_MERGE * 4;
+    const size_t cnt_bytes = (size_t)nwg * 8 + namax * 8 + 256 + 32 * PK_ATT_MERGE * 4 + LG_MAX_GROUP_WORDS * 8;
     uint8_t* blk = nullptr;
     if ((rc = dalloc(ctx, (void**)&blk, cnt_bytes))) return rc;
     LG_HIP_CHECK(hipMemset(blk, 0, cnt_bytes));
@@ -627,6 +630,8 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.tok_out = (int*)(tail + 64);                                 /* {token, error} */
     P.err = (uint32_t*)(tail + 68);
     P.attn_cnt = (uint32_t*)(tail + 256);                          /* up to 32 heads x PK_ATT_MERGE groups */
+    P.grp_cnt = (uint64_t*)(tail + 256 + 32 * PK_ATT_MERGE * 4);   /* LG_MAX_GROUP_WORDS x 8 B */
+    P.qkva = ctx->qkva;
     P.spin_cap = 1 << 20;
     P.act_stride = ctx->act_stride;
     /* fused path: device step record, prompt feed, pinned staging */

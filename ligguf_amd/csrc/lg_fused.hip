@@ -98,6 +98,54 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const P
         MergeSrc{nullptr, nullptr, 0, 0}, left ? nwv - left : 0);
 }
 
+/* Q|K|V rows and the short-context attention units of one KV group in one
+ * kernel.  Workgroup b works for KV group g = b % n_kv: first the group's
+ * rows -- q of its NREP heads, k and v of head g -- split over the group's
+ * nwg / n_kv workgroups (the V rows from L.v when VT is not 0, on the
+ * activation the Q|K sweep left in LDS), then, once every workgroup of the
+ * group has stored its rows (group_arrive / group_wait), attention unit b,
+ * which belongs to group g by the units' order (kv head fastest).  The
+ * group's K/V cache rows load before the wait.  With the workgroups of a
+ * group on one XCD (workgroup b on XCD b % 8, n_kv = 8) the barrier stays in
+ * that XCD's L2.  The same rows, units and arithmetic as k_f_qkv(2) +
+ * k_f_attn, so the same bits. */
+template <int LT, int VT, class S, int HD, int NREP, bool EMB>
+__global__ __launch_bounds__(PK_THREADS) void k_f_qkva(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
+                                                       int l, uint8_t* atr)
+{
+    constexpr int NE = S::NE;
+    const int ne = P.n_embed, kvd = P.kv_dim, qs = ne + 2 * kvd;
+    const int nkv = P.n_kv, g = (int)blockIdx.x % nkv, gsz = (int)gridDim.x / nkv, r = (int)blockIdx.x / nkv;
+    float* xin = P.xs + (size_t)l * ne;
+    float* out = P.qkv + (size_t)l * qs;
+    uint64_t* words = P.grp_cnt + (size_t)g * gsz;   /* the group's words, this workgroup's at r */
+    const uint64_t round = group_round(words + r);
+    const int pos = Sd->pos;
+    const int tok = pos < Sd->feed_end ? P.feed[pos] : Sd->tok;
+    const WaveSet ws{r * PK_WAVES, gsz * PK_WAVES};
+    const MergeSrc none{nullptr, nullptr, 0, 0};
+    if constexpr (VT == 0) {
+        const RowMap rm{NREP * HD, g * NREP * HD, HD, ne + g * HD, ne + kvd + g * HD};
+        phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, S::CE, LG_QKV_R>(
+            P, tok, L.qkv, L.qkv_rsz, (NREP + 2) * HD, 0, L.att_norm, xin, nullptr, out, xin, 0, 0, f_tr(Sd, l, 0),
+            f_atr(atr, P, 4 * l), ne, none, 0, rm, ws);
+    } else {
+        const RowMap rm{NREP * HD, g * NREP * HD, HD, ne + g * HD, 0};
+        phase_mv<LT, NE, LG_QKV_B, 1, EPI_STORE, EMB ? BLD_EMB : BLD_RMS, S::CE, LG_QKV_R>(
+            P, tok, L.qkv, L.qkv_rsz, (NREP + 1) * HD, 0, L.att_norm, xin, nullptr, out, xin, 0, 0, f_tr(Sd, l, 0),
+            f_atr(atr, P, 4 * l), ne, none, 0, rm, ws);
+        const int left = ((NREP + 1) * HD) % ws.nwv;
+        const RowMap rv{HD, g * HD, 0, 0, 0};
+        phase_mv<VT, NE, (Batch<VT, NE, 1, 2, 512>::value), 1, EPI_STORE, BLD_KEEP, S::CE, LG_QKV_R>(
+            P, tok, L.v, L.v_rsz, HD, 0, nullptr, nullptr, nullptr, out + ne + kvd, nullptr, 0, 0, nullptr, nullptr, ne,
+            none, left ? ws.nwv - left : 0, rv, ws);
+    }
+    group_arrive(words + r, round);
+    uint64_t* tr = f_tr(Sd, l, 1);
+    stamp(tr, 0);
+    phase_attn<HD, NREP, 1, false>(P, L, l, pos, out, round, 0, tr, false, words, gsz);
+}
+
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
  * position); otherwise one-head single-batch units.  Two kernels, so the
  * short-context one carries no long-context code or registers. */
@@ -248,6 +296,37 @@ static void f_launch_qkv(const PkParams& P, const PkLayer& L, PkStep* S, int l, 
     else hipLaunchKernelGGL((k_f_qkv<LT, SH, false>), g, b, 0, st, P, L, S, l, atr);
 }
 
+/* the fused QKV + attention kernel serves the step: short-context units,
+ * the grid split evenly over the KV groups */
+static bool f_qkva_ok(const PkParams& P, int nwg, bool long_ctx)
+{
+    return P.qkva && !long_ctx && nwg % P.n_kv == 0 && nwg <= LG_MAX_GROUP_WORDS;
+}
+
+/* phases 0 and 1 of layer l in one kernel (k_f_qkva) */
+template <int LT, class SH, int HD, int NREP>
+static void f_launch_qkva(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
+                          uint8_t* atr)
+{
+    if constexpr (f_mixable<LT>()) {
+        if (L.v) {
+#define QKVA2(VT)                                                                                                  \
+    do {                                                                                                           \
+        if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, true>), g, b, 0, st, P, L, S, l, atr);     \
+        else hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, false>), g, b, 0, st, P, L, S, l, atr);          \
+    } while (0)
+            if (L.v_t == LG_Q6_K_R) QKVA2(LG_Q6_K_R);
+            else if (L.v_t == LG_Q6_K) QKVA2(LG_Q6_K);
+            else if (L.v_t == LG_Q5_K) QKVA2(LG_Q5_K);
+            else QKVA2(LT);
+#undef QKVA2
+            return;
+        }
+    }
+    if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, true>), g, b, 0, st, P, L, S, l, atr);
+    else hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, false>), g, b, 0, st, P, L, S, l, atr);
+}
+
 /* phase 4 of layer l: down rows of the layer's down type */
 template <int LT, class SH>
 static void f_launch_down(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
@@ -269,10 +348,15 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
                           hipStream_t st, uint8_t* atr)
 {
     const dim3 g(nwg), b(PK_THREADS);
+    const bool qkva = f_qkva_ok(P, nwg, long_ctx);
     for (int l = 0; l < n_layers; l++) {
-        f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
-        if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), dim3(P.att_grid), b, 0, st, P, Lh[l], S, l);
-        else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
+        if (qkva) {
+            f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, atr);
+        } else {
+            f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
+            if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), dim3(P.att_grid), b, 0, st, P, Lh[l], S, l);
+            else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
+        }
         hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, atr);
         hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, atr);
         f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
@@ -289,7 +373,10 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
 {
     const dim3 g(nwg), b(PK_THREADS);
     switch (phase) {
-    case 0: f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
+    case 0:   /* with the fused QKV + attention kernel in use, that kernel */
+        if (f_qkva_ok(P, nwg, long_ctx)) f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, nullptr);
+        else f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr);
+        break;
     case 1:
         if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), dim3(P.att_grid), b, 0, st, P, Lh[l], S, l);
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);

@@ -10,6 +10,7 @@
 #define PK_MAX_FF 16384     /* n_ff limit (quantized activation in LDS) */
 #define PK_MAX_NREP 8       /* query heads per KV head */
 #define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
+#define LG_MAX_GROUP_WORDS 1024 /* workgroups of the fused QKV + attention kernel, at most (one barrier word each) */
 #define PK_ATT_MAX_NCH 160  /* attention chunks per head at most */
 #define LG_OUT_MAX_WGS 4     /* output-head workgroups per CU at most (argmax partials) */
 /* long-context attention workgroups per CU: with 2 the fused step's kernel
@@ -72,6 +73,8 @@ struct PkParams {
     int att_slots;           /* per layer: one per chunk, then PK_ATT_MERGE for the groups merged in-kernel */
     int att_grid;            /* long-context split: units sized for this many workgroups (LG_ATT_WGS per CU) */
     uint32_t* attn_cnt;      /* [unit head sets (n_kv * NREP / NQ <= 32)][PK_ATT_MERGE groups], zero between launches */
+    uint64_t* grp_cnt;       /* [LG_MAX_GROUP_WORDS] KV-group barrier words of the fused QKV + attention kernel (launch counts) */
+    int qkva;                /* fused path: QKV and short-context attention in one kernel (LG_NO_QKVA=1: two) */
     uint64_t* progress;      /* one word per workgroup */
     float* amax_v;           /* per-workgroup argmax partials */
     int* amax_i;

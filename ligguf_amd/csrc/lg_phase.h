@@ -122,6 +122,49 @@ __device__ __forceinline__ void pk_wait(const PkParams& P, uint64_t target)
     bar();
 }
 
+/* KV-group barrier of the fused QKV + attention kernel.  Each workgroup of
+ * a group owns one word of the group's gsz consecutive words and counts its
+ * launches in it: it reads its word at kernel start (group_round), stores
+ * the incremented value once its rows are stored (group_arrive: stores
+ * acknowledged first, as pk_signal), and waits until every word of the
+ * group holds at least that value (group_wait: one load per lane, wave 0;
+ * bounded by spin_cap, past which P.err is set, as pk_wait).  Every
+ * workgroup arrives once per launch, so the words advance in step. */
+__device__ __forceinline__ uint64_t group_round(const uint64_t* mine)
+{
+    return cld(mine) + 1;
+}
+
+__device__ __forceinline__ void group_arrive(uint64_t* mine, uint64_t round)
+{
+    wait_stores();
+    bar();
+    if (LG_TID == 0) cst(mine, round);
+}
+
+__device__ __forceinline__ void group_wait(const PkParams& P, const uint64_t* words, int gsz, uint64_t round)
+{
+    if (LG_TID < 64) {
+        bool ok = false;
+        int it = 0;
+        do {
+            uint64_t mn = ~0ull;
+            for (int i = LG_TID; i < gsz; i += 64) {
+                const uint64_t v = cld(&words[i]);
+                mn = v < mn ? v : mn;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const uint64_t t = __shfl_xor(mn, o, 64);
+                mn = t < mn ? t : mn;
+            }
+            ok = mn >= round;
+        } while (!ok && ++it < P.spin_cap);
+        if (!ok && LG_TID == 0) cst(P.err, 1u);
+    }
+    bar();
+}
+
 /* 2^x (v_exp_f32): attention scores are kept in log2 units */
 __device__ __forceinline__ float lg_exp2(float x)
 {
@@ -387,6 +430,26 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
  * still in flight with vmcnt, and where a load sits under a branch it must
  * assume the shorter path and wait for every later load as well -- the
  * activation build would then wait for all the wave's weights. */
+/* The items of a matvec phase as matrix rows (and output indices): the
+ * identity, or (a phase restricted to one KV group's rows) up to three row
+ * ranges back to back -- n0 rows from b0, n1 from b1, the rest from b2. */
+struct RowMap {
+    int n0, b0, n1, b1, b2;   /* n0 < 0: the identity */
+    __device__ __forceinline__ int row(int i) const
+    {
+        if (n0 < 0) return i;
+        return i < n0 ? b0 + i : (i < n0 + n1 ? b1 + (i - n0) : b2 + (i - n0 - n1));
+    }
+};
+#define LG_ROWS_ALL (RowMap{-1, 0, 0, 0, 0})
+
+/* The waves that share a phase's items: the whole grid (nwv = 0), or nwv
+ * waves of which this workgroup's wave 0 is number gw0 */
+struct WaveSet {
+    int gw0, nwv;
+};
+#define LG_WAVES_ALL (WaveSet{0, 0})
+
 template <int FMT, int NS, int MAXB, int K>
 struct Rows {
     typename Fmt<FMT>::W w[MAXB][K][NS];
@@ -394,11 +457,11 @@ struct Rows {
     /* items i0, i0+ist, ... (MAXB of them), those past `wlast` replaced by
      * wlast; slots past the row's nslots read its last slot (not used) */
     __device__ __forceinline__ void load(const uint8_t* __restrict__ W, uint32_t rsz, int i0, int ist, int wlast,
-                                         int kstride, int lane, int nslots)
+                                         int kstride, int lane, int nslots, const RowMap& rm)
     {
 #pragma unroll
         for (int b = 0; b < MAXB; b++) {
-            const int i = min(i0 + b * ist, wlast);
+            const int i = rm.row(min(i0 + b * ist, wlast));
 #pragma unroll
             for (int k = 0; k < K; k++) {
                 const uint8_t* row = W + (size_t)(i + k * kstride) * rsz;
@@ -427,7 +490,8 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                                          const float* __restrict__ src, const float* __restrict__ res_src,
                                          float* __restrict__ out, float* __restrict__ emb_out,
                                          uint64_t wait_target, uint64_t sig, uint64_t* tr, uint8_t* atr, int n_act,
-                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0}, int rot = 0)
+                                         const MergeSrc& ms = MergeSrc{nullptr, nullptr, 0, 0}, int rot = 0,
+                                         const RowMap& rm = LG_ROWS_ALL, const WaveSet& wset = LG_WAVES_ALL)
 {
     using F = Fmt<FMT>;
     constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q8_0_R || FMT == LG_Q1_0 || FMT == LG_Q1_0_R || FMT == LG_Q1_G ||
@@ -438,8 +502,8 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     /* the wave index as a wave-uniform value: item indices and row addresses
      * are then scalar (a row base in SGPRs, the lane's slot offset in a VGPR) */
     const int lane = LG_TID & 63, wave = __builtin_amdgcn_readfirstlane(LG_TID >> 6);
-    const int nwv = gridDim.x * PK_WAVES;
-    int gw = blockIdx.x * PK_WAVES + wave + rot;   /* 0 <= rot < nwv */
+    const int nwv = wset.nwv ? wset.nwv : gridDim.x * PK_WAVES;
+    int gw = (wset.nwv ? wset.gw0 : blockIdx.x * PK_WAVES) + wave + rot;   /* 0 <= rot < nwv */
     gw -= gw >= nwv ? nwv : 0;
 #if LG_MV_SPREAD
     const int ist = nwv, i0 = gw;
@@ -467,12 +531,12 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         else if (!from_embed && BLD != BLD_KEEP) as.load(src, n_act);
     };
     auto load_res = [&](int c0) {
-        if (EPI == EPI_RESID) resl = res_src[min(i0 + (c0 + lane) * ist, wlast)];
+        if (EPI == EPI_RESID) resl = res_src[rm.row(min(i0 + (c0 + lane) * ist, wlast))];
     };
     auto prefetch = [&]() {
 #pragma unroll
         for (int k = 0; k < (NR > 1 ? NR - 1 : 1); k++)
-            R[k].load(W, rsz, i0 + k * MAXB * ist, ist, wlast, kstride, lane, nslots);
+            R[k].load(W, rsz, i0 + k * MAXB * ist, ist, wlast, kstride, lane, nslots, rm);
         load_res(0);
     };
     if (!wait_target) {
@@ -517,7 +581,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     int c0 = 0;
     auto flush = [&](int n) {
         if (lane < n) {
-            const int i = i0 + (c0 + lane) * ist;
+            const int i = rm.row(i0 + (c0 + lane) * ist);
             float v = ov;
             if (EPI == EPI_RESID) v = resl + ov;
             else if (EPI == EPI_SWIGLU) v = (og / (1.0f + expf(-og))) * ov;
@@ -553,7 +617,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     };
     if (NR == 1) {
         for (int b0 = 0; b0 < my; b0 += MAXB) {
-            if (b0 > 0) R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane, nslots);
+            if (b0 > 0) R[0].load(W, rsz, i0 + b0 * ist, ist, wlast, kstride, lane, nslots, rm);
             process(R[0], b0, min(MAXB, my - b0));
         }
     } else {
@@ -564,7 +628,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
 #pragma unroll
             for (int k = 0; k < NR; k++) {
                 const int jn = j0 + k + NR - 1;
-                R[(k + NR - 1) % NR].load(W, rsz, i0 + jn * MAXB * ist, ist, wlast, kstride, lane, nslots);
+                R[(k + NR - 1) % NR].load(W, rsz, i0 + jn * MAXB * ist, ist, wlast, kstride, lane, nslots, rm);
                 process(R[k], (j0 + k) * MAXB, min(MAXB, my - (j0 + k) * MAXB));
             }
         }
@@ -702,7 +766,8 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
 template <int HD, int NREP, int NQ, bool BATCHES, int WPC = 1>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos_arg,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
-                                           uint64_t* tr, bool stamp0 = true)
+                                           uint64_t* tr, bool stamp0 = true, const uint64_t* gwords = nullptr,
+                                           int gsz = 0)
 {
     int pos = pos_arg;   /* FIX: first read after the unit's loads (below) */
     constexpr int HDP = pk_hdp(HD);        /* lane layout width: HD padded to a power of two */
@@ -798,7 +863,10 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
      * back), and the heads after it */
     const bool pre = FIX && wait_target != 0;
     if (pre && has && wave != 0) load_kv(0, blockIdx.x, 0);
-    if (wait_target) pk_wait(P, wait_target);
+    if (wait_target) {
+        if (gwords) group_wait(P, gwords, gsz, wait_target);
+        else pk_wait(P, wait_target);
+    }
     if (!FIX && !has) stamp(tr, 1);   /* FIX: after the loop (no store ahead of the unit's loads) */
 
     /* one unit: the loads, QK-norm/RoPE (+ the KV row), scores, partials */

@@ -436,3 +436,40 @@ def test_regrouped_copies_equal_gguf_rows(pk_model, monkeypatch):
     finally:
         other.close()
     assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
+
+
+QKVA_MIX = ModelConfig("qwen3-w4096-q4k-m", 1, 2, 4096, 32, 8, 128, 12288, 1024, 2048, 1e6, 1e-6, Q4_K, Q4_K, Q6_K,
+                       overrides=(("attn_v", Q6_K), ("ffn_down", Q6_K)))
+
+
+@pytest.mark.parametrize("mix", [False, True], ids=["stacked-qkv", "q4k-m-mix"])
+def test_fused_qkva_equals_two_kernels(pk_model, mix, monkeypatch):
+    """The fused step's QKV + short-context attention kernel (k_f_qkva: one
+    KV group's rows, a group barrier, the group's attention units) against
+    the two kernels it replaces (LG_NO_QKVA=1, read at lg_create): the same
+    logits and greedy tokens bit for bit over a prompt and queued greedy
+    steps.  The mix runs the separate-V form (Q|K rows, then V rows of
+    their own type)."""
+    if mix:
+        if pk_model[0].cfg.name != PK_MODELS[0].name:
+            pytest.skip("the mix runs once")
+        hm = HostModel.synthetic(QKVA_MIX)
+    else:
+        hm = pk_model[0]
+    prompt = np.random.default_rng(21).integers(1, hm.cfg.vocab, 5).astype(np.int32)
+    runs = []
+    for env in ("0", "1"):
+        monkeypatch.setenv("LG_NO_QKVA", env)
+        eng = Engine(0)
+        try:
+            eng.load(hm)
+            eng.set_path(PATH_FUSED)
+            lg = [eng.decode(int(t), i) for i, t in enumerate(prompt)]
+            toks = eng.decode_greedy(int(np.argmax(lg[-1])), len(prompt), 6)
+            lg.append(eng.decode(int(toks[-1]), len(prompt) + 6))
+            runs.append((lg, toks))
+        finally:
+            eng.close()
+    (a, ta), (b, tb) = runs
+    assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
+    assert np.array_equal(ta, tb)
