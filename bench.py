@@ -136,11 +136,31 @@ def prefill_report(cfg, tokens: int, seconds: float, path: int):
             "mfma_frac": round(ops / seconds / MFMA_INT8_PEAK, 4)}
 
 
+_SLEEP_CYCLES_PER_MS = None
+
+
 def _time_launches(torch, fn, reps: int) -> float:
-    """Mean wall time of fn() over reps launches (HIP events on the current stream), microseconds."""
+    """Mean GPU time of fn() over reps back-to-back launches, microseconds:
+    HIP events on the current stream around the launches, which are queued
+    behind a GPU spin (torch.cuda._sleep) long enough for the host to
+    enqueue them all -- so the time is the kernels' and their launch gaps',
+    not the host's per-call overhead."""
+    global _SLEEP_CYCLES_PER_MS
     fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if _SLEEP_CYCLES_PER_MS is None:
+        e0.record()
+        torch.cuda._sleep(1 << 24)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = (1 << 24) / max(e0.elapsed_time(e1), 1e-3)
+    t0 = time.perf_counter()
+    for _ in range(min(reps, 20)):
+        fn()
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) / min(reps, 20) * 1e3
+    torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS * (2.0 * host_ms * reps + 2.0)))
     e0.record()
     for _ in range(reps):
         fn()
@@ -561,6 +581,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated matvec/attention lines")
+    ap.add_argument("--isolated-only", action="store_true", help="only the isolated matvec/attention lines")
     ap.add_argument("--no-q1g", action="store_true", help="skip the Q1_G 8192-context workload")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing plus a plain copy of known size (for PMC runs)")
@@ -634,6 +655,10 @@ def main() -> int:
                "positions": [p_first, pos - 1]}
         eng.close()
         print(json.dumps({"decode": rep}), flush=True)
+        return 0
+
+    if args.isolated_only:
+        print(json.dumps({"isolated": isolated_kernels(torch, np)}), flush=True)
         return 0
 
     if args.prefill_only:

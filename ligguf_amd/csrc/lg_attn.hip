@@ -22,6 +22,11 @@
  * per head and tile), then p.V by the position lanes.  The waves merge at
  * the end.
  *
+ * k_attn_unit (head_dim 64, 128, 256, up to 4096 positions): one query
+ * head per workgroup, K/V rows through registers, merged per head by
+ * k_attn_unit_merge -- NREP times the workgroups of k_attn_tile, which
+ * wins at longer contexts by reading each row once per KV head.
+ *
  * k_attn_split (head_dim 48, and position 0): three passes per chunk.
  * A K/V row of one head is HD fp16 = 2*HD bytes; LPP lanes split it (DPL
  * dims each), so a wave covers 64/LPP positions per step.
@@ -600,6 +605,217 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
     }
 }
 
+/* ------------------------------------------------------------------ */
+/* k_attn_unit (head_dim 64, 128, 256): one query head per workgroup.   */
+/* ------------------------------------------------------------------ */
+/* Contexts up to LG_ATTN_UNIT_CTX positions.  Unit (query head h, chunk c)
+ * takes positions [c*chunk, min((c+1)*chunk, pos+1)) in one pass: 4 waves,
+ * LPP = HD/8 lanes per position (8 dims each), PPB positions per workgroup
+ * step, the K and V pieces of H steps per register batch, two batches in
+ * flight; per position an online-softmax step of the lane group (log2
+ * units).  Lane groups merge by lane permutes, waves in LDS, and the unit's
+ * partial (m, l, o) goes to the workspace; k_attn_unit_merge merges each
+ * head's chunks.  NREP times as many workgroups as k_attn_tile's (at least
+ * 256 at 32 query heads); the NREP units of a (KV head, chunk) read the same
+ * rows, and their workgroup indices differ by multiples of 8, so they run
+ * together on one XCD and share its L2.  Past LG_ATTN_UNIT_CTX positions
+ * k_attn_tile, which reads each row once per KV head, is faster (measured:
+ * 8.3 / 14.6 / 61 us at 512 / 4096 / 32768 positions and 32 / 8 heads of
+ * 128, against 9.6 / 15.3 / 38.5 for k_attn_tile + k_attn_merge). */
+#define LG_ATTN_UNIT_MAX_NCH 16
+#define LG_ATTN_UNIT_CTX 4096
+#define LG_ATTN_UNIT_H 8   /* steps per register batch */
+
+__device__ __forceinline__ float attn_dpp_ror8(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));   /* row_ror:8 */
+}
+
+/* combine two online-softmax states (m in log2 units; m = -inf: empty) */
+__device__ __forceinline__ void attn_osm_merge(float& m, float& l, float* o, float m2, float l2, const float* o2)
+{
+    const float mn = fmaxf(m, m2);
+    const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+    const float b = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
+    l = lg_fma2(l, a, l2, b);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = lg_fma2(o[i], a, o2[i], b);
+    m = mn;
+}
+
+template <int HD, int NREP>
+__global__ __launch_bounds__(256) void k_attn_unit(const float* __restrict__ q, const float* __restrict__ kcur,
+                                                   const float* __restrict__ vcur, const uint16_t* __restrict__ kc,
+                                                   const uint16_t* __restrict__ vc, int n_kv, int pos, int chunk,
+                                                   int nch, float scale2, float* __restrict__ ws)
+{
+    constexpr int NW = 4, LPP = HD / 8, PPW = 64 / LPP, PPB = NW * PPW, H = LG_ATTN_UNIT_H;
+    __shared__ float s_o[NW][HD];
+    __shared__ float s_m[NW], s_l[NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gl = lane % LPP, grp = lane / LPP;
+    /* unit of this workgroup */
+    const int blk = blockIdx.x / (8 * NREP), rem = blockIdx.x % (8 * NREP);
+    const int r = rem / 8, gc = blk * 8 + rem % 8;
+    if (gc >= n_kv * nch) return;   /* padding of the last 8-block: no unit */
+    const int c = gc / n_kv, g = gc % n_kv, h = g * NREP + r;
+    const int kv_dim = n_kv * HD;
+    const int t0 = c * chunk, t1 = min(t0 + chunk, pos + 1);
+    const int nsteps = (t1 - t0 + PPB - 1) / PPB;
+    const int tcache = min(t1, pos);   /* positions [t0, tcache) come from the cache */
+
+    /* this lane's dims of q_h, and of this step's k and v (used at t == pos) */
+    const float4 q0 = *(const float4*)(q + (size_t)h * HD + gl * 8);
+    const float4 q1 = *(const float4*)(q + (size_t)h * HD + gl * 8 + 4);
+    const float4 k0 = *(const float4*)(kcur + (size_t)g * HD + gl * 8);
+    const float4 k1 = *(const float4*)(kcur + (size_t)g * HD + gl * 8 + 4);
+    const float4 v0 = *(const float4*)(vcur + (size_t)g * HD + gl * 8);
+    const float4 v1 = *(const float4*)(vcur + (size_t)g * HD + gl * 8 + 4);
+    uint4 kb[2][H], vb[2][H];
+    /* steps sb.. into batch b; rows outside [t0, tcache) load row t0 (unused) */
+    auto issue = [&](int b, int sb) {
+#pragma unroll
+        for (int st = 0; st < H; st++) {
+            int t = t0 + (sb + st) * PPB + wave * PPW + grp;
+            t = t < tcache ? t : t0;
+            const size_t o = (size_t)t * kv_dim + (size_t)g * HD + gl * 8;
+            kb[b][st] = *(const uint4*)(kc + o);
+            vb[b][st] = *(const uint4*)(vc + o);
+        }
+    };
+    issue(0, 0);
+    issue(1, H);
+    const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const float kn[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const float vn[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float m = -INFINITY, l = 0.0f, o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = 0.0f;
+    /* one online-softmax step of the lane group on the row (k, v) */
+    auto step = [&](const float* kf, const float* vf, bool use) {
+        float sc = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; d++) sc = __builtin_fmaf(kf[d], qv[d], sc);
+        sc = lg_group_sum<LPP>(sc) * scale2;
+        if (use) {
+            const float mn = fmaxf(m, sc);
+            const float a = __builtin_amdgcn_exp2f(m - mn);   /* 0 while m = -inf */
+            const float p = __builtin_amdgcn_exp2f(sc - mn);
+            l = __builtin_fmaf(l, a, p);
+#pragma unroll
+            for (int d = 0; d < 8; d++) o[d] = lg_fma2(o[d], a, p, vf[d]);
+            m = mn;
+        }
+    };
+    auto process = [&](int b, int sb) {
+#pragma unroll
+        for (int st = 0; st < H; st++) {
+            if (sb + st < nsteps) {   /* uniform over the wave */
+                const int t = t0 + (sb + st) * PPB + wave * PPW + grp;
+                AttnH8 kh, vh;
+                kh.set(kb[b][st]);
+                vh.set(vb[b][st]);
+                float kf[8], vf[8];
+#pragma unroll
+                for (int d = 0; d < 8; d++) { kf[d] = kh.f(d); vf[d] = vh.f(d); }
+                step(kf, vf, t < tcache);
+            }
+        }
+    };
+    /* the loads stay unconditional (past the chunk: row t0 again, unused),
+     * so the waits before each batch count only the batches issued before it */
+    for (int sb = 0; sb < nsteps; sb += 2 * H) {
+        process(0, sb);
+        issue(0, sb + 2 * H);
+        process(1, sb + H);
+        issue(1, sb + 3 * H);
+    }
+    /* position pos (in the last chunk): this step's fp32 k and v, on lane
+     * group 0 of wave 0 */
+    if (pos < t1 && wave == 0) step(kn, vn, grp == 0);
+    /* the wave's position groups (lanes with the same dims) merge */
+    if constexpr (LPP == 8) {
+        float o2[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o2[i] = attn_dpp_ror8(o[i]);
+        attn_osm_merge(m, l, o, attn_dpp_ror8(m), attn_dpp_ror8(l), o2);
+    }
+    if constexpr (LPP <= 16) {
+        float o2[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o2[i] = lg_partner<4>(o[i]);
+        attn_osm_merge(m, l, o, lg_partner<4>(m), lg_partner<4>(l), o2);
+    }
+    {
+        float o2[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o2[i] = lg_partner<5>(o[i]);
+        attn_osm_merge(m, l, o, lg_partner<5>(m), lg_partner<5>(l), o2);
+    }
+    if (grp == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) s_o[wave][gl * 8 + i] = o[i];
+        if (gl == 0) { s_m[wave] = m; s_l[wave] = l; }
+    }
+    attn_bar();
+    /* the unit's partial: [m, l, o[HD]] */
+    float* part = ws + ((size_t)h * nch + c) * (HD + 2);
+    for (int d = tid; d < HD; d += NW * 64) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, s_m[w]);
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float wt = s_m[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w] - M);
+            O = __builtin_fmaf(s_o[w][d], wt, O);
+            L = __builtin_fmaf(s_l[w], wt, L);
+        }
+        part[2 + d] = O;
+        if (d == 0) { part[0] = M; part[1] = L; }
+    }
+}
+
+/* one workgroup per query head: the unit partials [m, l, o[HD]] of its
+ * nch chunks merged (weights 2^(m_c - M), as k_attn_merge) */
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_unit_merge(const float* __restrict__ ws, int nch, float* __restrict__ out)
+{
+    __shared__ float s_cm[LG_ATTN_UNIT_MAX_NCH], s_cl[LG_ATTN_UNIT_MAX_NCH];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const float* base = ws + (size_t)h * nch * (HD + 2);
+    if (tid < nch) { s_cm[tid] = base[(size_t)tid * (HD + 2)]; s_cl[tid] = base[(size_t)tid * (HD + 2) + 1]; }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, s_cm[cc]);
+    float L = 0.0f;
+    for (int cc = 0; cc < nch; cc++) L = __builtin_fmaf(s_cl[cc], __builtin_amdgcn_exp2f(s_cm[cc] - M), L);
+    for (int d = tid; d < HD; d += 256) {
+        float O = 0.0f;
+        for (int c0 = 0; c0 < nch; c0 += 16) {
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = base[(size_t)min(c0 + k, nch - 1) * (HD + 2) + 2 + d];
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (c0 + k < nch) O = __builtin_fmaf(v[k], __builtin_amdgcn_exp2f(s_cm[c0 + k] - M), O);
+        }
+        out[(size_t)h * HD + d] = O / L;
+    }
+}
+
+/* chunking of the unit kernel: 8 chunks up to 512 positions (at least one
+ * step each), then a chunk per 256 positions (16 at LG_ATTN_UNIT_CTX) */
+static void attn_unit_split(int ctx, int ppb, int* chunk, int* nch)
+{
+    int n = ctx <= 512 ? 8 : (ctx + 255) / 256;
+    if (n > LG_ATTN_UNIT_MAX_NCH) n = LG_ATTN_UNIT_MAX_NCH;
+    int c = (ctx + n - 1) / n;
+    c = (c + ppb - 1) / ppb * ppb;
+    *chunk = c;
+    *nch = (ctx + c - 1) / c;
+}
+
 template <int HD, int NREP, int LPP>
 static void launch_attn(const float* q, const float* k, const float* v, const uint16_t* kc, const uint16_t* vc,
                         int n_kv_heads, int pos, float* out, float* ws, hipStream_t s)
@@ -608,6 +824,15 @@ static void launch_attn(const float* q, const float* k, const float* v, const ui
     const float scale = 1.0f / sqrtf((float)HD);
     int ch, nch;
     if constexpr (HD == 64 || HD == 128 || HD == 256) {
+        if (pos > 0 && ctx <= LG_ATTN_UNIT_CTX) {
+            constexpr int PPB = 4 * (64 / (HD / 8));
+            attn_unit_split(ctx, PPB, &ch, &nch);
+            const int grid = (n_kv_heads * nch + 7) / 8 * 8 * NREP;
+            hipLaunchKernelGGL((k_attn_unit<HD, NREP>), dim3(grid), dim3(256), 0, s, q, k, v, kc, vc, n_kv_heads, pos,
+                               ch, nch, scale * 1.44269504088896341f, ws);
+            hipLaunchKernelGGL((k_attn_unit_merge<HD>), dim3(n_kv_heads * NREP), dim3(256), 0, s, ws, nch, out);
+            return;
+        }
         if (attn_tiled(HD, pos)) {
             attn_tile_split(ctx, HD, NREP, &ch, &nch);
             hipLaunchKernelGGL((k_attn_tile<HD, NREP>), dim3(nch, n_kv_heads), dim3(LG_ATTN_TW * 64), 0, s, q, k, v, kc, vc,
