@@ -104,12 +104,15 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const P
  * nwg / n_kv workgroups (the V rows from L.v when VT is not 0, on the
  * activation the Q|K sweep left in LDS), then, once every workgroup of the
  * group has stored its rows (group_arrive / group_wait), attention unit b,
- * which belongs to group g by the units' order (kv head fastest).  The
- * group's K/V cache rows load before the wait.  With the workgroups of a
+ * which belongs to group g by the units' order (kv head fastest): a
+ * short-context unit (one query head, a fixed chunk) or (LONG) a
+ * long-context one (the group's query heads, chunk b / n_kv of
+ * pk_attn_split's).  The unit's K/V cache rows (its first register set)
+ * load before the wait.  With the workgroups of a
  * group on one XCD (workgroup b on XCD b % 8, n_kv = 8) the barrier stays in
  * that XCD's L2.  The same rows, units and arithmetic as k_f_qkv(2) +
  * k_f_attn, so the same bits. */
-template <int LT, int VT, class S, int HD, int NREP, bool EMB>
+template <int LT, int VT, class S, int HD, int NREP, bool EMB, bool LONG>
 __global__ __launch_bounds__(PK_THREADS) void k_f_qkva(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                        int l, uint8_t* atr)
 {
@@ -143,7 +146,8 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkva(const PkParams P, const P
     group_arrive(words + r, round);
     uint64_t* tr = f_tr(Sd, l, 1);
     stamp(tr, 0);
-    phase_attn<HD, NREP, 1, false>(P, L, l, pos, out, round, 0, tr, false, words, gsz);
+    if constexpr (LONG) phase_attn<HD, NREP, NREP, true, 1, true>(P, L, l, pos, out, round, 0, tr, false, words, gsz);
+    else phase_attn<HD, NREP, 1, false>(P, L, l, pos, out, round, 0, tr, false, words, gsz);
 }
 
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
@@ -300,20 +304,21 @@ static void f_launch_qkv(const PkParams& P, const PkLayer& L, PkStep* S, int l, 
  * the grid split evenly over the KV groups */
 static bool f_qkva_ok(const PkParams& P, int nwg, bool long_ctx)
 {
-    return P.qkva && !long_ctx && nwg % P.n_kv == 0 && nwg <= LG_MAX_GROUP_WORDS;
+    /* long contexts: at most one unit per workgroup (pk_att_max_nch) */
+    return P.qkva && nwg % P.n_kv == 0 && nwg <= LG_MAX_GROUP_WORDS && (!long_ctx || P.att_grid <= nwg);
 }
 
 /* phases 0 and 1 of layer l in one kernel (k_f_qkva) */
-template <int LT, class SH, int HD, int NREP>
-static void f_launch_qkva(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
-                          uint8_t* atr)
+template <int LT, class SH, int HD, int NREP, bool LONG>
+static void f_launch_qkva_n(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
+                            uint8_t* atr)
 {
     if constexpr (f_mixable<LT>()) {
         if (L.v) {
-#define QKVA2(VT)                                                                                                  \
-    do {                                                                                                           \
-        if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, true>), g, b, 0, st, P, L, S, l, atr);     \
-        else hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, false>), g, b, 0, st, P, L, S, l, atr);          \
+#define QKVA2(VT)                                                                                                    \
+    do {                                                                                                             \
+        if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, true, LONG>), g, b, 0, st, P, L, S, l, atr);  \
+        else hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, false, LONG>), g, b, 0, st, P, L, S, l, atr);       \
     } while (0)
             if (L.v_t == LG_Q6_K_R) QKVA2(LG_Q6_K_R);
             else if (L.v_t == LG_Q6_K) QKVA2(LG_Q6_K);
@@ -323,8 +328,16 @@ static void f_launch_qkva(const PkParams& P, const PkLayer& L, PkStep* S, int l,
             return;
         }
     }
-    if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, true>), g, b, 0, st, P, L, S, l, atr);
-    else hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, false>), g, b, 0, st, P, L, S, l, atr);
+    if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, true, LONG>), g, b, 0, st, P, L, S, l, atr);
+    else hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, false, LONG>), g, b, 0, st, P, L, S, l, atr);
+}
+
+template <int LT, class SH, int HD, int NREP>
+static void f_launch_qkva(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
+                          uint8_t* atr, bool long_ctx)
+{
+    if (long_ctx) f_launch_qkva_n<LT, SH, HD, NREP, true>(P, L, S, l, g, b, st, atr);
+    else f_launch_qkva_n<LT, SH, HD, NREP, false>(P, L, S, l, g, b, st, atr);
 }
 
 /* phase 4 of layer l: down rows of the layer's down type */
@@ -351,7 +364,7 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
     const bool qkva = f_qkva_ok(P, nwg, long_ctx);
     for (int l = 0; l < n_layers; l++) {
         if (qkva) {
-            f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, atr);
+            f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, atr, long_ctx);
         } else {
             f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
             if (long_ctx) hipLaunchKernelGGL((k_f_attn<HD, NREP, true>), dim3(P.att_grid), b, 0, st, P, Lh[l], S, l);
@@ -374,7 +387,7 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
     const dim3 g(nwg), b(PK_THREADS);
     switch (phase) {
     case 0:   /* with the fused QKV + attention kernel in use, that kernel */
-        if (f_qkva_ok(P, nwg, long_ctx)) f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, nullptr);
+        if (f_qkva_ok(P, nwg, long_ctx)) f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, nullptr, long_ctx);
         else f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr);
         break;
     case 1:

@@ -165,6 +165,28 @@ __device__ __forceinline__ void group_wait(const PkParams& P, const uint64_t* wo
     bar();
 }
 
+/* the online softmax moves its reference max only past this margin (log2
+ * units): the running sums are rescaled then, not at every new maximum */
+#define PK_ATT_LAZY 8.0f
+
+/* lg_group_sum of N values, each butterfly step over all of them in turn */
+template <int G, int N>
+__device__ __forceinline__ void lg_group_sum_n(float* v)
+{
+#pragma unroll
+    for (int r = 0; r < N; r++) if constexpr (G >= 2) v[r] += lg_partner<0>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; r++) if constexpr (G >= 4) v[r] += lg_partner<1>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; r++) if constexpr (G >= 8) v[r] += lg_partner<2>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; r++) if constexpr (G >= 16) v[r] += lg_partner<3>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; r++) if constexpr (G >= 32) v[r] += lg_partner<4>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; r++) if constexpr (G >= 64) v[r] += lg_partner<5>(v[r]);
+}
+
 /* 2^x (v_exp_f32): attention scores are kept in log2 units */
 __device__ __forceinline__ float lg_exp2(float x)
 {
@@ -763,7 +785,7 @@ __device__ __forceinline__ void osm_merge(float& m, float& l, float* o, float m2
  * the last unit of each group of pk_att_group chunks (atomic counter) merges
  * the group into one of the layer's PK_ATT_MERGE group slots.  The first unit of g's last chunk also writes the fp16 cache
  * row pos. */
-template <int HD, int NREP, int NQ, bool BATCHES, int WPC = 1>
+template <int HD, int NREP, int NQ, bool BATCHES, int WPC = 1, bool GMAJOR = false>
 __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, int layer, int pos_arg,
                                            const float* __restrict__ qkv, uint64_t wait_target, uint64_t sig,
                                            uint64_t* tr, bool stamp0 = true, const uint64_t* gwords = nullptr,
@@ -795,8 +817,10 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
     const int ngc = FIX ? 0 : P.n_kv * nch;   /* (kv head, chunk) pairs */
     const int nunits = FIX ? P.n_heads * PK_ATT_MERGE : ngc * NSUB;
     /* unit -> kv head, chunk, query-head subset */
-    auto unit_g = [&](int u) { return FIX ? u % P.n_kv : (u % ngc) / nch; };
-    auto unit_c = [&](int u) { return FIX ? u / P.n_heads : (u % ngc) % nch; };
+    /* (GMAJOR, long-context units of the fused QKV + attention kernel: kv
+     * head fastest, so unit u belongs to KV group u % n_kv like workgroup u) */
+    auto unit_g = [&](int u) { return FIX ? u % P.n_kv : GMAJOR ? (u % ngc) % P.n_kv : (u % ngc) / nch; };
+    auto unit_c = [&](int u) { return FIX ? u / P.n_heads : GMAJOR ? (u % ngc) / P.n_kv : (u % ngc) % nch; };
     auto unit_q = [&](int u) { return FIX ? (u / P.n_kv) % NREP : u / ngc; };
     const size_t loff = (size_t)layer * P.n_ctx * kvd;
     const float scale2 = 1.44269504088896341f / sqrtf((float)HD);   /* log2(e) / sqrt(head_dim) */
@@ -861,7 +885,9 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
      * unit's K/V rows -- cache rows of earlier steps, position-free -- load
      * before it, by waves 1.. (wave 0 polls: its loads would hold the poll
      * back), and the heads after it */
-    const bool pre = FIX && wait_target != 0;
+    /* (GMAJOR: the long unit's first register set likewise -- rows of
+     * earlier steps, its chunk fixed by the position known at launch) */
+    const bool pre = (FIX || GMAJOR) && wait_target != 0;
     if (pre && has && wave != 0) load_kv(0, blockIdx.x, 0);
     if (wait_target) {
         if (gwords) group_wait(P, gwords, gsz, wait_target);
@@ -881,7 +907,7 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
         const int t0 = c * chunk;
         load_heads(u);
         lg_issue_order();   /* heads first, then K/V */
-        if (!pre || wave == 0) load_kv(0, u, 0);
+        if (!pre || wave == 0 || u != (int)blockIdx.x) load_kv(0, u, 0);
         if (FIX) {
             /* the position from here on: an empty asm pins its first use
              * behind the loads above (it may still be in flight) */
@@ -966,22 +992,41 @@ __device__ __forceinline__ void phase_attn(const PkParams& P, const PkLayer& L, 
 #pragma unroll
                         for (int i = 0; i < 8; i++) { kf[i] = s_kv[gl * 8 + i]; vf[i] = s_kv[HDP + gl * 8 + i]; }
                     }
+                    /* the heads' scores, then their lane-group sums step by
+                     * step across the heads (independent permutes back to
+                     * back, no wait states between them) */
+                    float sc[NQ];
 #pragma unroll
                     for (int r = 0; r < NQ; r++) {
                         float qv[8];
 #pragma unroll
                         for (int i = 0; i < 8; i++) qv[i] = QIN ? qr[r < QREG ? r : 0][i] : s_q[r * HDP + gl * 8 + i];
-                        float sc = 0.0f;
+                        sc[r] = 0.0f;
 #pragma unroll
-                        for (int i = 0; i < 8; i++) sc += qv[i] * kf[i];
-                        sc = lg_group_sum<LPP>(sc) * scale2;
-                        const float mn = fmaxf(m[r], sc);
-                        const float a = lg_exp2(m[r] - mn);     /* 0 while m = -inf */
-                        const float pw = lg_exp2(sc - mn);
-                        l[r] = l[r] * a + pw;
+                        for (int i = 0; i < 8; i++) sc[r] += qv[i] * kf[i];
+                    }
+                    lg_group_sum_n<LPP, NQ>(sc);
+                    /* online softmax with a lazily moved reference: the sums
+                     * are kept relative to m, which moves (and rescales
+                     * them) only when a score passes m + PK_ATT_LAZY -- each
+                     * weight 2^(s - m) stays below 2^PK_ATT_LAZY, and the
+                     * state (m, l, o) stands for sum 2^(s - m) as before */
 #pragma unroll
-                        for (int i = 0; i < 8; i++) o[r][i] = lg_fma2(o[r][i], a, pw, vf[i]);
-                        m[r] = mn;
+                    for (int r = 0; r < NQ; r++) {
+                        const float s2 = sc[r] * scale2;
+                        const bool up = s2 > m[r] + PK_ATT_LAZY;   /* also while m = -inf */
+                        if (__builtin_amdgcn_ballot_w64(up)) {     /* wave-uniform, rare past the first rows */
+                            const float mn = up ? s2 : m[r];
+                            const float a = up ? lg_exp2(m[r] - mn) : 1.0f;   /* 0 while m = -inf */
+                            l[r] *= a;
+#pragma unroll
+                            for (int i = 0; i < 8; i++) o[r][i] *= a;
+                            m[r] = mn;
+                        }
+                        const float pw = lg_exp2(s2 - m[r]);
+                        l[r] += pw;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) o[r][i] = __builtin_fmaf(pw, vf[i], o[r][i]);
                     }
                 }
             }

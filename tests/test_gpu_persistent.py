@@ -477,3 +477,32 @@ def test_fused_qkva_equals_two_kernels(pk_model, mix, monkeypatch):
     (a, ta), (b, tb) = runs
     assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
     assert np.array_equal(ta, tb)
+
+
+def test_fused_qkva_long_context_equals_two_kernels(long_model, monkeypatch):
+    """The fused QKV + attention kernel with the long-context units (KV
+    groups' chunks on the group's workgroups, each unit's first K/V set
+    loaded before the group barrier) against QKV + k_f_attn<long>
+    (LG_NO_QKVA=1): the same logits bit for bit at 6000 and 9000 positions
+    from the same random fp16 cache."""
+    hm = long_model[0]
+    cfg = hm.cfg
+    rng = np.random.default_rng(9)
+    pos_max = 9000
+    k = rng.standard_normal(pos_max * cfg.kv_dim).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(pos_max * cfg.kv_dim).astype(np.float16).view(np.uint16)
+    runs = []
+    for env in ("0", "1"):
+        monkeypatch.setenv("LG_NO_QKVA", env)
+        eng = Engine(0)
+        try:
+            eng.load(hm)
+            eng.set_path(PATH_FUSED)
+            out = []
+            for pos in (6000, pos_max):
+                eng.kv_write(0, 1, 0, pos_max, k, v)
+                out.append(eng.decode(7, pos))
+            runs.append(out)
+        finally:
+            eng.close()
+    assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(*runs))
