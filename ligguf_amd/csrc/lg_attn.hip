@@ -64,7 +64,8 @@ static int attn_chunk(int ctx)
 #define LG_ATTN_TMAX 4096
 __host__ __device__ constexpr int attn_tpw(int hd, int nrep)
 {
-    return (2 * 64 * 8 / hd) < (64 / nrep) ? (2 * 64 * 8 / hd) : (64 / nrep);
+    /* a whole number of position steps (512 / hd positions per wave step) */
+    return ((2 * 64 * 8 / hd) < (64 / nrep) ? (2 * 64 * 8 / hd) : (64 / nrep)) / (512 / hd) * (512 / hd);
 }
 __host__ __device__ constexpr int attn_tp(int hd, int nrep) { return LG_ATTN_TW * attn_tpw(hd, nrep); }
 
@@ -857,7 +858,11 @@ static int attn_nrep(int nrep, const float* q, const float* k, const float* v, c
     case 2: launch_attn<HD, 2, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
     case 4: launch_attn<HD, 4, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
     case 8: launch_attn<HD, 8, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
-    default: lg_set_error("attention: %d query heads per KV head unsupported (1, 2, 4, 8)", nrep); return LG_ERR_ARG;
+    case 3: launch_attn<HD, 3, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
+    case 5: launch_attn<HD, 5, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
+    case 6: launch_attn<HD, 6, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
+    case 7: launch_attn<HD, 7, LPP>(q, k, v, kc, vc, n_kv_heads, pos, out, ws, s); return 0;
+    default: lg_set_error("attention: %d query heads per KV head unsupported (1 to 8)", nrep); return LG_ERR_ARG;
     }
 }
 

@@ -465,7 +465,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     const bool q8act = lt == LG_Q8_0 || lt == LG_Q1_0;
     bool ok = m->n_embed <= PK_MAX_EMBED && m->n_ff <= PK_MAX_FF && m->n_embed % (q8act ? 32 : 256) == 0 &&
               m->n_ff % (q8act ? 32 : 256) == 0 && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
-              m->n_kv_heads <= 32 && m->n_heads <= 32 && ctx->output.cols == m->n_embed;
+              m->n_kv_heads <= 32 && m->n_heads <= 64 && ctx->output.cols == m->n_embed;
     /* uniform: every layer matrix of type lt (the persistent kernel's and
      * the fused step's case); otherwise the fused step also takes layers
      * whose V (Q|K stacked) and down matrices are of a side type */

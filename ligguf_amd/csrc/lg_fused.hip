@@ -419,8 +419,9 @@ struct FusedVariant {
 /* one variant per (layer type, output type, head_dim, query heads per KV
  * head) and width class: n_embed 4096 / n_ff 12288 (the Qwen3-8B shape),
  * n_embed 4096 / n_ff 14336 (Llama-3-8B, Mistral-7B), n_embed 2560 / n_ff
- * 9728 (Qwen3-4B), n_embed 2048 / n_ff 5632 (TinyLlama-1.1B, head_dim 64),
- * and any width up to 2048 / 2048 (tiny models) */
+ * 9728 (Qwen3-4B), n_embed 5120 / n_ff 17408 (Qwen3-14B: 40 query heads on
+ * 8 KV heads), n_embed 2048 / n_ff 5632 (TinyLlama-1.1B, head_dim 64), and
+ * any width up to 2048 / 2048 (tiny models) */
 #define FVS(LT, OT, HD, NR, E, F)                                                                              \
     {LT, OT, HD, NR, f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F),                                \
      fused_enqueue<LT, OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,         \
@@ -434,9 +435,10 @@ static const FusedVariant f_variants[] = {
     FV(LG_Q1_G, LG_Q8_0, 128, 4), FV(LG_Q1_G, LG_Q6_K, 128, 4), FV(LG_Q3_K, LG_Q6_K, 128, 4),
     FV(LG_Q2_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q6_K, 128, 4), FV(LG_Q1_0, LG_Q8_0, 128, 4),
     FV(LG_Q4_K, LG_Q6_K, 128, 8), FV(LG_Q4_K, LG_Q6_K, 128, 1), FV(LG_Q5_K, LG_Q4_K, 128, 1),
+    FV(LG_Q5_K, LG_Q6_K, 128, 8),
     FV(LG_Q8_0, LG_Q8_0, 128, 1),
     FVS(LG_Q4_K, LG_Q6_K, 128, 4, 4096, 14336), FVS(LG_Q8_0, LG_Q8_0, 128, 4, 4096, 14336),
-    FVS(LG_Q4_K, LG_Q6_K, 128, 4, 2560, 9728),
+    FVS(LG_Q4_K, LG_Q6_K, 128, 4, 2560, 9728), FVS(LG_Q4_K, LG_Q6_K, 128, 5, 5120, 17408),
     FVS(LG_Q4_K, LG_Q6_K, 64, 8, 2048, 5632), FVS(LG_Q8_0, LG_Q8_0, 64, 8, 2048, 5632),
     FVS(LG_Q8_0, LG_Q8_0, 48, 1, 2048, 2048), FVS(LG_Q8_0, LG_Q8_0, 64, 1, 2048, 2048),
     FVS(LG_Q4_K, LG_Q6_K, 64, 1, 2048, 2048),

@@ -1316,7 +1316,7 @@ __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_h(const float* __
 
 int lg_prefill_attn_supported(int head_dim, int nrep)
 {
-    return (head_dim == 48 || head_dim == 64 || head_dim == 128) && (nrep == 1 || nrep == 2 || nrep == 4 || nrep == 8);
+    return (head_dim == 48 || head_dim == 64 || head_dim == 128) && nrep >= 1 && nrep <= 8;
 }
 
 static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_t* kc, const uint16_t* vc, int T,
@@ -1337,7 +1337,11 @@ static int launch_attn(const PfModel& M, const float* qkv, int qs, const uint16_
     switch (nrep) {                   \
     case 1: PFA(HD, 1); break;        \
     case 2: PFA(HD, 2); break;        \
+    case 3: PFA(HD, 3); break;        \
     case 4: PFA(HD, 4); break;        \
+    case 5: PFA(HD, 5); break;        \
+    case 6: PFA(HD, 6); break;        \
+    case 7: PFA(HD, 7); break;        \
     default: PFA(HD, 8); break;       \
     }
     switch (M.head_dim) {

@@ -110,6 +110,8 @@ BATCHED_MODELS = [
     # the other query-head ratios of the prefill attention kernel: 2 (16/8 heads) and 8 (32/4)
     ModelConfig("qwen3-w2048-q4k-nrep2", 1, 1, 2048, 16, 8, 128, 6144, 1024, 1024, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
     ModelConfig("llama-w4096-q4k-nrep8", 0, 1, 4096, 32, 4, 128, 12288, 1024, 1024, 1e4, 1e-5, Q4_K, Q4_K, Q6_K),
+    # Qwen3-14B widths: 5 query heads per KV head (40/8), FFN 17408
+    ModelConfig("qwen3-w5120-q4k-nrep5", 1, 1, 5120, 40, 8, 128, 17408, 1024, 1024, 1e6, 1e-6, Q4_K, Q4_K, Q6_K),
     # Q1_G layers (Q1_G x Q8_0 GEMM), Q8_0 embedding and output
     ModelConfig("qwen3-w4096-q1g", 1, 2, 4096, 32, 8, 128, 12288, 2048, 4096, 1e6, 1e-6, Q1_G, Q8_0, Q8_0),
     # the tiny parity config: Q8_0 throughout, width 288 (no multiple of 256), head_dim 48

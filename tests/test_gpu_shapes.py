@@ -42,6 +42,11 @@ SHAPES = [
     ModelConfig("qwen3-w4096-q1_0", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q1_0, Q8_0, Q8_0),
     # Q8_0 layers with a Q6_K output head
     ModelConfig("qwen3-w4096-q8_0-q6khead", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q8_0, Q4_K, Q6_K),
+    # Qwen3-14B widths: 40 query heads on 8 KV heads (5 per group), FFN 17408
+    ModelConfig("qwen3-w5120-ff17408-40x8-q4k", 1, 2, 5120, 40, 8, 128, 17408, 2048, 2048, 1e6, 1e-6, Q4_K, Q4_K,
+                Q6_K),
+    # Q5_K layers with 8 query heads per KV head
+    ModelConfig("qwen3-w4096-q5k-nrep8", 1, 2, 4096, 32, 4, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K),
     # Q5_K_M-style: Q5_K layers, Q6_K attn_v and ffn_down in layer 1
     ModelConfig("qwen3-w4096-q5k-mixed", 1, 2, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K,
                 overrides=(("attn_v.1", Q6_K), ("ffn_down.1", Q6_K))),
