@@ -20,7 +20,8 @@ BUILD = os.path.join(PKG, "_build")
 HIP_SO = os.path.join(PKG, "libligguf_hip.so")
 ENC_SO = os.path.join(PKG, "libligguf_encode.so")
 
-HIP_SOURCES = ["lg_kernels.hip", "lg_matvec.hip", "lg_attn.hip", "lg_persist.hip", "lg_fused.hip", "lg_prefill.hip", "lg_sample.hip", "lg_bert.hip", "lg_engine.hip"]
+HIP_SOURCES = ["lg_fused.hip", "lg_fused_p1.hip", "lg_fused_p2.hip", "lg_fused_p3.hip", "lg_prefill.hip", "lg_engine.hip",
+               "lg_persist.hip", "lg_attn.hip", "lg_bert.hip", "lg_sample.hip", "lg_kernels.hip", "lg_matvec.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

@@ -175,6 +175,7 @@ struct lg_ctx {
     bool use_graph = true;
     bool regroup = true;             /* fused kernels read regrouped copies of misaligned formats */
     bool qkva = true;                /* fused step: QKV and short-context attention in one kernel */
+    bool qkvao = true;               /* ... and att_out, split by KV group */
     hipGraphExec_t graph[2] = {nullptr, nullptr};   /* the step with short / long-context attention */
 };
 
@@ -238,6 +239,8 @@ extern "C" int lg_create(int device, lg_ctx** out)
     ctx->regroup = !(nr && nr[0] == '1');
     const char* nq = getenv("LG_NO_QKVA");
     ctx->qkva = !(nq && nq[0] == '1');
+    const char* no = getenv("LG_NO_QKVAO");
+    ctx->qkvao = !(no && no[0] == '1');
     const hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         lg_set_error("hipStreamCreate failed: %s", hipGetErrorString(e));
@@ -613,6 +616,9 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
         P.att_po = ws;
         P.att_pml = ws + L * slots * m->n_embed;
     }
+    /* att_out partials of the 8 KV groups (one layer at a time: the next
+     * layer's kernel writes them after this layer's up|gate read them) */
+    if ((rc = dalloc(ctx, (void**)&P.ao_part, 8 * (size_t)m->n_embed * sizeof(float)))) return rc;
     /* one zeroed block for the counters and flags; argmax partials for up
      * to LG_OUT_MAX_WGS output-head workgroups per CU */
     const int nwg = ctx->pk_nwg;
@@ -632,6 +638,7 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
     P.attn_cnt = (uint32_t*)(tail + 256);                          /* up to 32 heads x PK_ATT_MERGE groups */
     P.grp_cnt = (uint64_t*)(tail + 256 + 32 * PK_ATT_MERGE * 4);   /* LG_MAX_GROUP_WORDS x 8 B */
     P.qkva = ctx->qkva;
+    P.qkvao = ctx->qkvao;
     P.spin_cap = 1 << 20;
     P.act_stride = ctx->act_stride;
     /* fused path: device step record, prompt feed, pinned staging */

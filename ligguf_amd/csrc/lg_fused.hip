@@ -98,6 +98,95 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const P
         MergeSrc{nullptr, nullptr, 0, 0}, left ? nwv - left : 0);
 }
 
+/* att_out rows of this workgroup, KV group g's share of each (the fused
+ * QKV + attention + att_out kernel, after the group's attention units).
+ * The group's query heads are values 512g .. 512g+511 of the attention
+ * vector -- two Q8_K blocks (or 16 Q8_0 blocks) of their own, quantized by
+ * the group alone -- and slots 8g .. 8g+7 of every 4096-value att_out row.
+ * After a second group barrier (every unit of the group stored its
+ * partials), wave 0 merges the group's two 256-value chunks as the att_out
+ * build does (MergeAct, chunks in ascending order) and quantizes them into
+ * s_act; then lane 8q + j of each wave dots slot 8g + j of row q of a pass
+ * and the 8-lane sum -- the first three steps of lg_wave_sum -- is the
+ * row's group partial, stored to P.ao_part[g][row].  The next up|gate
+ * build adds the 8 partials in lg_wave_sum's order (PartSum), so xm is the
+ * att_out phase's bit for bit.  Rows of workgroup r: r * rpw .. (rpw =
+ * n_embed / group size, at most 64 * AO_NP), pass p of wave w rows
+ * 64p + 8w + q of them.  Waves 1.. issue their row loads before the
+ * barrier wait; wave 0 polls, then issues the merge loads and its rows. */
+#define AO_NP 2
+template <int LT, int HD, int NREP>
+__device__ __forceinline__ void phase_ao_group(const PkParams& P, const PkLayer& L, int l, int pos, int g, int r,
+                                               int gsz, const uint64_t* words, uint64_t* mine, uint64_t round2,
+                                               uint8_t* atr, uint64_t* tr)
+{
+    using F = Fmt<LT>;
+    constexpr int QT = lg_act_qt(LT);
+    static_assert(F::VALS == 64 && NREP * HD == 8 * 64, "a group's slice is 8 slots of 64 values");
+    const int lane = LG_TID & 63, wave = __builtin_amdgcn_readfirstlane(LG_TID >> 6);
+    const int ne = P.n_embed, rpw = ne / gsz, r0 = r * rpw;
+    const int j = lane & 7, q = lane >> 3, slot = 8 * g + j;
+    stamp(tr, 0);
+    typename F::W w[AO_NP];
+    auto load_rows = [&]() {
+#pragma unroll
+        for (int p = 0; p < AO_NP; p++) {
+            const int i = r0 + min(64 * p + 8 * wave + q, rpw - 1);
+            F::load_w(w[p], L.ao + (size_t)i * L.ao_rsz, slot);
+        }
+    };
+    /* this workgroup's attention partials are stored (and acknowledged by
+     * group_arrive) before its rows load: the acknowledgement wait would
+     * wait for the row loads too */
+    group_arrive(mine, round2);
+    if (wave != 0) load_rows();
+    group_wait(P, words, gsz, round2);
+    stamp(tr, 1);
+    if (wave == 0) {
+        const MergeSrc ms = att_partials<HD, NREP>(P, l, pos);
+        MergeAct<1> m0, m1;
+        m0.load_at(ms, P.n_heads, ne, (2 * g) * 256 + 4 * lane);
+        m1.load_at(ms, P.n_heads, ne, (2 * g + 1) * 256 + 4 * lane);
+        lg_issue_order();
+        load_rows();
+        ActSrc<1> a0, a1;
+        m0.merge(ms.nch, a0);
+        m1.merge(ms.nch, a1);
+        const float v0[4] = {a0.v[0].x, a0.v[0].y, a0.v[0].z, a0.v[0].w};
+        const float v1[4] = {a1.v[0].x, a1.v[0].y, a1.v[0].z, a1.v[0].w};
+        lg_emit(v0, QT, s_act, 2 * g, 256);
+        lg_emit(v1, QT, s_act, 2 * g + 1, 256);
+    }
+    bar();
+    stamp(tr, 2);
+    if (atr && r == 0) {
+        /* activation trace (tests): the group's two chunks as built */
+        constexpr int CB = QT == LG_Q8_K ? LG_BS_Q8_K : 8 * LG_BS_Q8_0;
+        uint32_t* dst = (uint32_t*)(atr + (size_t)(2 * g) * CB);
+        const uint32_t* src = (const uint32_t*)(s_act + (size_t)(2 * g) * CB);
+        for (int i = LG_TID; i < 2 * CB / 4; i += PK_THREADS) dst[i] = src[i];
+    }
+    typename F::Act act;
+    F::load_act(act, s_act, slot);
+    float pv[AO_NP];
+#pragma unroll
+    for (int p = 0; p < AO_NP; p++) {
+        float a = 0.0f;
+        a += F::dot(w[p], act, slot);
+        pv[p] = lg_group_sum<8>(a);
+    }
+    /* lanes 8p + q gather row q of pass p: one store of 8 consecutive
+     * values per pass */
+    float* out = P.ao_part + (size_t)g * ne;
+#pragma unroll
+    for (int p = 0; p < AO_NP; p++) {
+        const float v = __shfl(pv[p], 8 * (lane & 7), 64);
+        const int li = 64 * p + 8 * wave + (lane & 7);
+        if ((lane >> 3) == p && li < rpw) out[r0 + li] = v;
+    }
+    stamp(tr, 3);
+}
+
 /* Q|K|V rows and the short-context attention units of one KV group in one
  * kernel.  Workgroup b works for KV group g = b % n_kv: first the group's
  * rows -- q of its NREP heads, k and v of head g -- split over the group's
@@ -112,10 +201,11 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const P
  * group on one XCD (workgroup b on XCD b % 8, n_kv = 8) the barrier stays in
  * that XCD's L2.  The same rows, units and arithmetic as k_f_qkv(2) +
  * k_f_attn, so the same bits. */
-template <int LT, int VT, class S, int HD, int NREP, bool EMB, bool LONG>
+template <int LT, int VT, class S, int HD, int NREP, bool EMB, bool LONG, bool AO = false>
 __global__ __launch_bounds__(PK_THREADS) void k_f_qkva(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                        int l, uint8_t* atr)
 {
+    static_assert(!(AO && LONG), "att_out by KV group: short-context units");
     constexpr int NE = S::NE;
     const int ne = P.n_embed, kvd = P.kv_dim, qs = ne + 2 * kvd;
     const int nkv = P.n_kv, g = (int)blockIdx.x % nkv, gsz = (int)gridDim.x / nkv, r = (int)blockIdx.x / nkv;
@@ -148,6 +238,9 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkva(const PkParams P, const P
     stamp(tr, 0);
     if constexpr (LONG) phase_attn<HD, NREP, NREP, true, 1, true>(P, L, l, pos, out, round, 0, tr, false, words, gsz);
     else phase_attn<HD, NREP, 1, false>(P, L, l, pos, out, round, 0, tr, false, words, gsz);
+    if constexpr (AO)
+        phase_ao_group<LT, HD, NREP>(P, L, l, pos, g, r, gsz, words, words + r, round + 1, f_atr(atr, P, 4 * l + 1),
+                                     f_tr(Sd, l, 2));
 }
 
 /* LONG: the long-context units (the host picks by pk_att_long of the step's
@@ -192,15 +285,18 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkL
         f_tr(Sd, l, 2), f_atr(atr, P, 4 * l + 1), ne, att_partials<HD, NREP>(P, l, Sd->pos));
 }
 
-template <int LT, class S>
+/* RSUM: the input is x_l + the att_out group partials (k_f_qkva<..., AO>),
+ * stored by workgroup 0 as xm_l */
+template <int LT, class S, bool RSUM = false>
 __global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
                                                      uint8_t* atr)
 {
     constexpr int NE = S::NE;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, BLD_RMS, S::CE, LG_UG_R>(
-        P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, P.xm + (size_t)l * ne, nullptr, P.hb + (size_t)l * nff, nullptr, 0,
-        0, f_tr(Sd, l, 3), f_atr(atr, P, 4 * l + 2), ne);
+    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, RSUM ? BLD_RSUM : BLD_RMS, S::CE, LG_UG_R>(
+        P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, RSUM ? P.xs + (size_t)l * ne : P.xm + (size_t)l * ne, nullptr,
+        P.hb + (size_t)l * nff, RSUM ? P.xm + (size_t)l * ne : nullptr, 0, 0, f_tr(Sd, l, 3), f_atr(atr, P, 4 * l + 2),
+        ne);
 }
 
 template <int LT, class S>
@@ -271,10 +367,12 @@ static void f_launch_out(const PkParams& P, PkStep* S, int nwg, dim3 b, hipStrea
 template <int LT>
 static constexpr bool f_mixable() { return LT == LG_Q4_K || LT == LG_Q5_K; }
 
+#if LG_FUSED_PART == 0
 bool lg_fused_side_type(int lt, int t)
 {
     return t == lt || ((lt == LG_Q4_K || lt == LG_Q5_K) && (t == LG_Q5_K || t == LG_Q6_K));
 }
+#endif
 
 /* phase 0 of layer l: Q|K|V stacked, or Q|K and a V of its own type */
 template <int LT, class SH>
@@ -308,8 +406,24 @@ static bool f_qkva_ok(const PkParams& P, int nwg, bool long_ctx)
     return P.qkva && nwg % P.n_kv == 0 && nwg <= LG_MAX_GROUP_WORDS && (!long_ctx || P.att_grid <= nwg);
 }
 
-/* phases 0 and 1 of layer l in one kernel (k_f_qkva) */
-template <int LT, class SH, int HD, int NREP, bool LONG>
+/* att_out in the QKV + attention kernel, split by KV group: short-context
+ * units, 8 KV groups of 512 query values (8 slots of a 4096-value row of a
+ * 64-value-slot format, one slot per lane), at most 64 * AO_NP rows per
+ * workgroup */
+template <int LT, class SH, int HD, int NREP>
+static bool f_qkvao_ok(const PkParams& P, int nwg, bool long_ctx)
+{
+    if constexpr (Fmt<LT>::VALS != 64 || NREP * HD != 512 || SH::NE != 1) return false;
+    else {
+        if (!P.qkvao || !P.ao_part || long_ctx || !f_qkva_ok(P, nwg, false) || P.n_kv != 8 || P.n_embed != 4096)
+            return false;
+        const int gsz = nwg / P.n_kv;
+        return P.n_embed % gsz == 0 && P.n_embed / gsz <= 64 * AO_NP;
+    }
+}
+
+/* phases 0 and 1 of layer l in one kernel (k_f_qkva), with AO phase 2 too */
+template <int LT, class SH, int HD, int NREP, bool LONG, bool AO = false>
 static void f_launch_qkva_n(const PkParams& P, const PkLayer& L, PkStep* S, int l, dim3 g, dim3 b, hipStream_t st,
                             uint8_t* atr)
 {
@@ -317,8 +431,8 @@ static void f_launch_qkva_n(const PkParams& P, const PkLayer& L, PkStep* S, int 
         if (L.v) {
 #define QKVA2(VT)                                                                                                    \
     do {                                                                                                             \
-        if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, true, LONG>), g, b, 0, st, P, L, S, l, atr);  \
-        else hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, false, LONG>), g, b, 0, st, P, L, S, l, atr);       \
+        if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, true, LONG, AO>), g, b, 0, st, P, L, S, l, atr); \
+        else hipLaunchKernelGGL((k_f_qkva<LT, VT, SH, HD, NREP, false, LONG, AO>), g, b, 0, st, P, L, S, l, atr);  \
     } while (0)
             if (L.v_t == LG_Q6_K_R) QKVA2(LG_Q6_K_R);
             else if (L.v_t == LG_Q6_K) QKVA2(LG_Q6_K);
@@ -328,8 +442,8 @@ static void f_launch_qkva_n(const PkParams& P, const PkLayer& L, PkStep* S, int 
             return;
         }
     }
-    if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, true, LONG>), g, b, 0, st, P, L, S, l, atr);
-    else hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, false, LONG>), g, b, 0, st, P, L, S, l, atr);
+    if (l == 0) hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, true, LONG, AO>), g, b, 0, st, P, L, S, l, atr);
+    else hipLaunchKernelGGL((k_f_qkva<LT, 0, SH, HD, NREP, false, LONG, AO>), g, b, 0, st, P, L, S, l, atr);
 }
 
 template <int LT, class SH, int HD, int NREP>
@@ -362,6 +476,19 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
 {
     const dim3 g(nwg), b(PK_THREADS);
     const bool qkva = f_qkva_ok(P, nwg, long_ctx);
+    if constexpr (Fmt<LT>::VALS == 64 && NREP * HD == 512 && SH::NE == 1) {
+        if (f_qkvao_ok<LT, SH, HD, NREP>(P, nwg, long_ctx)) {
+            /* three kernels a layer: QKV + attention + att_out by KV group,
+             * up|gate on x + the partials, down */
+            for (int l = 0; l < n_layers; l++) {
+                f_launch_qkva_n<LT, SH, HD, NREP, false, true>(P, Lh[l], S, l, g, b, st, atr);
+                hipLaunchKernelGGL((k_f_ug<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, atr);
+                f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
+            }
+            f_launch_out<OT, SH>(P, S, nwg, b, st, atr);
+            return;
+        }
+    }
     for (int l = 0; l < n_layers; l++) {
         if (qkva) {
             f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, atr, long_ctx);
@@ -385,8 +512,13 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
                         hipStream_t st)
 {
     const dim3 g(nwg), b(PK_THREADS);
+    bool ao = false;
+    if constexpr (Fmt<LT>::VALS == 64 && NREP * HD == 512 && SH::NE == 1) ao = f_qkvao_ok<LT, SH, HD, NREP>(P, nwg, long_ctx);
     switch (phase) {
-    case 0:   /* with the fused QKV + attention kernel in use, that kernel */
+    case 0:   /* with the fused QKV + attention (+ att_out) kernel in use, that kernel */
+        if constexpr (Fmt<LT>::VALS == 64 && NREP * HD == 512 && SH::NE == 1) {
+            if (ao) { f_launch_qkva_n<LT, SH, HD, NREP, false, true>(P, Lh[l], S, l, g, b, st, nullptr); break; }
+        }
         if (f_qkva_ok(P, nwg, long_ctx)) f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, nullptr, long_ctx);
         else f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr);
         break;
@@ -395,7 +527,12 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
         else hipLaunchKernelGGL((k_f_attn<HD, NREP, false>), g, b, 0, st, P, Lh[l], S, l);
         break;
     case 2: hipLaunchKernelGGL((k_f_ao<LT, SH, HD, NREP>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
-    case 3: hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr); break;
+    case 3:   /* the up|gate kernel the step runs */
+        if constexpr (Fmt<LT>::VALS == 64 && NREP * HD == 512 && SH::NE == 1) {
+            if (ao) { hipLaunchKernelGGL((k_f_ug<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, nullptr); break; }
+        }
+        hipLaunchKernelGGL((k_f_ug<LT, SH>), g, b, 0, st, P, Lh[l], S, l, nullptr);
+        break;
     case 4: f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr); break;
     default: f_launch_out<OT, SH>(P, S, nwg, b, st, nullptr); break;
     }
@@ -429,39 +566,94 @@ struct FusedVariant {
      fused_enqueue<f_rep(LT), OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,  \
      fused_phase<f_rep(LT), OT, HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>}
 #define FV(LT, OT, HD, NR) FVS(LT, OT, HD, NR, 4096, 12288)
-static const FusedVariant f_variants[] = {
-    FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
-    FV(LG_Q5_K, LG_Q6_K, 128, 4), FV(LG_Q6_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q8_0, 128, 4),
-    FV(LG_Q1_G, LG_Q8_0, 128, 4), FV(LG_Q1_G, LG_Q6_K, 128, 4), FV(LG_Q3_K, LG_Q6_K, 128, 4),
-    FV(LG_Q2_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q6_K, 128, 4), FV(LG_Q1_0, LG_Q8_0, 128, 4),
-    FV(LG_Q4_K, LG_Q6_K, 128, 8), FV(LG_Q4_K, LG_Q6_K, 128, 1), FV(LG_Q5_K, LG_Q4_K, 128, 1),
-    FV(LG_Q5_K, LG_Q6_K, 128, 8),
-    FV(LG_Q8_0, LG_Q8_0, 128, 1),
-    FVS(LG_Q4_K, LG_Q6_K, 128, 4, 4096, 14336), FVS(LG_Q8_0, LG_Q8_0, 128, 4, 4096, 14336),
-    FVS(LG_Q4_K, LG_Q6_K, 128, 4, 2560, 9728), FVS(LG_Q4_K, LG_Q6_K, 128, 5, 5120, 17408),
-    FVS(LG_Q4_K, LG_Q6_K, 64, 8, 2048, 5632), FVS(LG_Q8_0, LG_Q8_0, 64, 8, 2048, 5632),
-    FVS(LG_Q8_0, LG_Q8_0, 48, 1, 2048, 2048), FVS(LG_Q8_0, LG_Q8_0, 64, 1, 2048, 2048),
-    FVS(LG_Q4_K, LG_Q6_K, 64, 1, 2048, 2048),
-};
+/* the table in four parts, one per translation unit (lg_fused.hip and
+ * lg_fused_p1..p3.hip, which include this file with LG_FUSED_PART set), so
+ * that the variants compile in parallel */
+#ifndef LG_FUSED_PART
+#define LG_FUSED_PART 0
+#endif
+#if LG_FUSED_PART == 0
+const FusedVariant* lg_fused_part_0(int* n)
+{
+    static const FusedVariant v[] = {
+        FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
+        FV(LG_Q5_K, LG_Q6_K, 128, 4), FV(LG_Q6_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q8_0, 128, 4),
+    };
+    *n = (int)(sizeof(v) / sizeof(v[0]));
+    return v;
+}
+#elif LG_FUSED_PART == 1
+const FusedVariant* lg_fused_part_1(int* n)
+{
+    static const FusedVariant v[] = {
+        FV(LG_Q1_G, LG_Q8_0, 128, 4), FV(LG_Q1_G, LG_Q6_K, 128, 4), FV(LG_Q3_K, LG_Q6_K, 128, 4),
+        FV(LG_Q2_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q6_K, 128, 4), FV(LG_Q1_0, LG_Q8_0, 128, 4),
+        FV(LG_Q8_0, LG_Q8_0, 128, 1),
+    };
+    *n = (int)(sizeof(v) / sizeof(v[0]));
+    return v;
+}
+#elif LG_FUSED_PART == 2
+const FusedVariant* lg_fused_part_2(int* n)
+{
+    static const FusedVariant v[] = {
+        FV(LG_Q4_K, LG_Q6_K, 128, 8), FV(LG_Q4_K, LG_Q6_K, 128, 1), FV(LG_Q5_K, LG_Q4_K, 128, 1),
+        FV(LG_Q5_K, LG_Q6_K, 128, 8),
+        FVS(LG_Q4_K, LG_Q6_K, 128, 4, 4096, 14336), FVS(LG_Q8_0, LG_Q8_0, 128, 4, 4096, 14336),
+    };
+    *n = (int)(sizeof(v) / sizeof(v[0]));
+    return v;
+}
+#else
+const FusedVariant* lg_fused_part_3(int* n)
+{
+    static const FusedVariant v[] = {
+        FVS(LG_Q4_K, LG_Q6_K, 128, 4, 2560, 9728), FVS(LG_Q4_K, LG_Q6_K, 128, 5, 5120, 17408),
+        FVS(LG_Q4_K, LG_Q6_K, 64, 8, 2048, 5632), FVS(LG_Q8_0, LG_Q8_0, 64, 8, 2048, 5632),
+        FVS(LG_Q8_0, LG_Q8_0, 48, 1, 2048, 2048), FVS(LG_Q8_0, LG_Q8_0, 64, 1, 2048, 2048),
+        FVS(LG_Q4_K, LG_Q6_K, 64, 1, 2048, 2048),
+    };
+    *n = (int)(sizeof(v) / sizeof(v[0]));
+    return v;
+}
+#endif
 #undef FV
 #undef FVS
 
+#if LG_FUSED_PART == 0
+const FusedVariant* lg_fused_part_1(int* n);
+const FusedVariant* lg_fused_part_2(int* n);
+const FusedVariant* lg_fused_part_3(int* n);
+struct FusedPart {
+    const FusedVariant* v;
+    int n;
+};
+
 const void* lg_fused_variant(int lt, int ot, int hd, int nrep, int ne, int nff)
 {
+    FusedPart f_parts[4];
+    f_parts[0].v = lg_fused_part_0(&f_parts[0].n);
+    f_parts[1].v = lg_fused_part_1(&f_parts[1].n);
+    f_parts[2].v = lg_fused_part_2(&f_parts[2].n);
+    f_parts[3].v = lg_fused_part_3(&f_parts[3].n);
     /* a variant serves the model when its slots and chunks hold the model's
      * widths (masked past them) and it wastes no more than its class does */
-    for (const FusedVariant& v : f_variants) {
-        if (v.lt != lt || v.ot != ot || v.hd != hd || v.nrep != nrep) continue;
-        if (f_ns(lt, ne) == v.ne && f_ns(ot, ne) == v.no && f_cpw(ne) == v.ce && f_ns(lt, nff) == v.nf &&
-            f_cpw(nff) == v.cf)
-            return (const void*)&v;
-    }
-    for (const FusedVariant& v : f_variants) {
-        if (v.lt != lt || v.ot != ot || v.hd != hd || v.nrep != nrep) continue;
-        if (f_ns(lt, ne) <= v.ne && f_ns(ot, ne) <= v.no && f_cpw(ne) <= v.ce && f_ns(lt, nff) <= v.nf &&
-            f_cpw(nff) <= v.cf && v.ce <= 1 && v.cf <= 1)
-            return (const void*)&v;
-    }
+    for (const FusedPart& fp : f_parts)
+        for (int k = 0; k < fp.n; k++) {
+            const FusedVariant& v = fp.v[k];
+            if (v.lt != lt || v.ot != ot || v.hd != hd || v.nrep != nrep) continue;
+            if (f_ns(lt, ne) == v.ne && f_ns(ot, ne) == v.no && f_cpw(ne) == v.ce && f_ns(lt, nff) == v.nf &&
+                f_cpw(nff) == v.cf)
+                return (const void*)&v;
+        }
+    for (const FusedPart& fp : f_parts)
+        for (int k = 0; k < fp.n; k++) {
+            const FusedVariant& v = fp.v[k];
+            if (v.lt != lt || v.ot != ot || v.hd != hd || v.nrep != nrep) continue;
+            if (f_ns(lt, ne) <= v.ne && f_ns(ot, ne) <= v.no && f_cpw(ne) <= v.ce && f_ns(lt, nff) <= v.nf &&
+                f_cpw(nff) <= v.cf && v.ce <= 1 && v.cf <= 1)
+                return (const void*)&v;
+        }
     return nullptr;
 }
 
@@ -480,3 +672,4 @@ int lg_fused_phase(const void* variant, const PkParams& P, const PkLayer* layers
     (P.layers_rep ? v->phase_r : v->phase)(P, layers, S_dev, phase, layer, nwg, long_ctx, s);
     return lg_check_launch("fused decode phase");
 }
+#endif   /* LG_FUSED_PART == 0 */

@@ -75,6 +75,8 @@ struct PkParams {
     uint32_t* attn_cnt;      /* [unit head sets (n_kv * NREP / NQ <= 32)][PK_ATT_MERGE groups], zero between launches */
     uint64_t* grp_cnt;       /* [LG_MAX_GROUP_WORDS] KV-group barrier words of the fused QKV + attention kernel (launch counts) */
     int qkva;                /* fused path: QKV and short-context attention in one kernel (LG_NO_QKVA=1: two) */
+    int qkvao;               /* fused path: att_out in that kernel too, split by KV group (LG_NO_QKVAO=1: its own kernel) */
+    float* ao_part;          /* [8][n_embed] att_out partials of the KV groups, summed by the next up|gate build */
     uint64_t* progress;      /* one word per workgroup */
     float* amax_v;           /* per-workgroup argmax partials */
     int* amax_i;

@@ -215,7 +215,17 @@ __device__ __forceinline__ void stamp(uint64_t* tr, int k)
  * row; BLD_PLAIN: the source vector as it is; BLD_MERGE: the attention
  * partials merged (MergeSrc); BLD_KEEP: the activation the previous sweep of
  * the same kernel left in LDS (a second matrix on the same input) */
-enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3, BLD_KEEP = 4 };
+/* BLD_RSUM: rmsnorm of x + the att_out group partials (PartSum), that sum
+ * stored by workgroup 0 as the residual stream xm */
+enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3, BLD_KEEP = 4, BLD_RSUM = 5 };
+
+/* the activation format a weight format's dot reads: Q8_0 blocks for
+ * Q8_0/Q1_0/Q1_G rows, Q8_K blocks for the K-quants */
+__host__ __device__ constexpr int lg_act_qt(int fmt)
+{
+    return (fmt == LG_Q8_0 || fmt == LG_Q8_0_R || fmt == LG_Q1_0 || fmt == LG_Q1_0_R || fmt == LG_Q1_G ||
+            fmt == LG_Q1_G_R) ? LG_Q8_0 : LG_Q8_K;
+}
 
 __device__ __forceinline__ int chunk_base(int c)
 {
@@ -255,6 +265,42 @@ struct ActSrc {
     }
 };
 
+/* The att_out rows split by KV group (the fused QKV + attention + att_out
+ * kernel): group g's partial of row i is the sum of the row's slots 8g ..
+ * 8g+7 -- lanes 8g .. 8g+7 of a whole-row dot, whose lg_wave_sum adds the
+ * aligned 8-lane groups g0..g7 as ((g6+g7)+(g4+g5)) + ((g2+g3)+(g0+g1)).
+ * The sum below adds the 8 partials of each value in that order and then
+ * the residual, as EPI_RESID adds res + the wave sum, so xm comes out bit
+ * for bit as the att_out phase computes it.  part: [8][n] */
+template <int CPW>
+struct PartSum {
+    float4 p[8][CPW];
+    __device__ __forceinline__ void load(const float* __restrict__ part, int n)
+    {
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int c = 0; c < CPW; c++) p[k][c] = *(const float4*)(part + (size_t)k * n + chunk_ld(c, n));
+    }
+    __device__ __forceinline__ static float tree(float a0, float a1, float a2, float a3, float a4, float a5, float a6,
+                                                 float a7)
+    {
+        return ((a6 + a7) + (a4 + a5)) + ((a2 + a3) + (a0 + a1));
+    }
+    /* x + the partials, in place */
+    __device__ __forceinline__ void add_to(ActSrc<CPW>& x) const
+    {
+#pragma unroll
+        for (int c = 0; c < CPW; c++) {
+            float4& v = x.v[c];
+            v.x = v.x + tree(p[0][c].x, p[1][c].x, p[2][c].x, p[3][c].x, p[4][c].x, p[5][c].x, p[6][c].x, p[7][c].x);
+            v.y = v.y + tree(p[0][c].y, p[1][c].y, p[2][c].y, p[3][c].y, p[4][c].y, p[5][c].y, p[6][c].y, p[7][c].y);
+            v.z = v.z + tree(p[0][c].z, p[1][c].z, p[2][c].z, p[3][c].z, p[4][c].z, p[5][c].z, p[6][c].z, p[7][c].z);
+            v.w = v.w + tree(p[0][c].w, p[1][c].w, p[2][c].w, p[3][c].w, p[4][c].w, p[5][c].w, p[6][c].w, p[7][c].w);
+        }
+    }
+};
+
 /* attention partials of one layer, merged by the att_out build (BLD_MERGE):
  * the source vector is sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c,
  * M = max_c m_c, over the nch chunks in ascending order */
@@ -281,6 +327,19 @@ struct MergeAct {
                 o[c][k] = *(const float4*)(ms.po + (size_t)cc * ne + b);
                 ml[c][k] = *(const float2*)(ms.pml + ((size_t)cc * nh + b / ms.head_dim) * 2);
             }
+        }
+    }
+
+    /* CPW = 1: the four values at b (b = chunk * 256 + 4 * lane) of an
+     * explicitly named chunk, loaded as load() loads the wave's own */
+    __device__ __forceinline__ void load_at(const MergeSrc& ms, int nh, int ne, int b)
+    {
+        static_assert(CPW == 1, "one chunk");
+#pragma unroll
+        for (int c = 0; c < PK_ATT_MERGE; c++) {
+            const int cc = min(c, ms.nch - 1);
+            o[c][0] = *(const float4*)(ms.po + (size_t)cc * ne + b);
+            ml[c][0] = *(const float2*)(ms.pml + ((size_t)cc * nh + b / ms.head_dim) * 2);
         }
     }
 
@@ -516,8 +575,7 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
                                          const RowMap& rm = LG_ROWS_ALL, const WaveSet& wset = LG_WAVES_ALL)
 {
     using F = Fmt<FMT>;
-    constexpr int QT = (FMT == LG_Q8_0 || FMT == LG_Q8_0_R || FMT == LG_Q1_0 || FMT == LG_Q1_0_R || FMT == LG_Q1_G ||
-                        FMT == LG_Q1_G_R) ? LG_Q8_0 : LG_Q8_K;
+    constexpr int QT = lg_act_qt(FMT);
     /* a row of n_act values is nslots slots; lane j takes slots j, j+64, ..
      * (NS of them, those past nslots unused) */
     const int nslots = n_act / F::VALS;
@@ -547,10 +605,12 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
     ActSrc<CPW> as;
     MergeAct<CPW> mg;
     constexpr bool from_embed = BLD == BLD_EMB;
-    constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB;
+    constexpr bool rms = BLD == BLD_RMS || BLD == BLD_EMB || BLD == BLD_RSUM;
+    PartSum<BLD == BLD_RSUM ? CPW : 1> ps;
     auto load_src = [&]() {
         if (BLD == BLD_MERGE) mg.load(ms, P.n_embed, P.n_heads);
         else if (!from_embed && BLD != BLD_KEEP) as.load(src, n_act);
+        if (BLD == BLD_RSUM) ps.load(P.ao_part, n_act);
     };
     auto load_res = [&](int c0) {
         if (EPI == EPI_RESID) resl = res_src[rm.row(min(i0 + (c0 + lane) * ist, wlast))];
@@ -576,6 +636,16 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         if (wave == 0) prefetch();
     }
     stamp(tr, 1);
+    if constexpr (BLD == BLD_RSUM) {
+        /* xm = x + the att_out group partials; workgroup 0 stores it (the
+         * down phase's residual) */
+        ps.add_to(as);
+        if (blockIdx.x == 0) {
+#pragma unroll
+            for (int c = 0; c < CPW; c++)
+                if (chunk_base(c) < n_act) *(float4*)(emb_out + chunk_base(c)) = as.v[c];
+        }
+    }
     if (rms) build_rms<QT, CPW>(P, tok, nw, as, from_embed, emb_out, n_act);
     else if (BLD != BLD_KEEP) {
         if (BLD == BLD_MERGE) mg.merge(ms.nch, as);
