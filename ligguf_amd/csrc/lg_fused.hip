@@ -104,16 +104,17 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_qkv2(const PkParams P, const P
  * vector -- two Q8_K blocks (or 16 Q8_0 blocks) of their own, quantized by
  * the group alone -- and slots 8g .. 8g+7 of every 4096-value att_out row.
  * After a second group barrier (every unit of the group stored its
- * partials), wave 0 merges the group's two 256-value chunks as the att_out
- * build does (MergeAct, chunks in ascending order) and quantizes them into
- * s_act; then lane 8q + j of each wave dots slot 8g + j of row q of a pass
+ * partials), waves 0 and 1 merge the group's two 256-value chunks as the
+ * att_out build does (MergeAct, chunks in ascending order) and quantize
+ * them into s_act; then lane 8q + j of each wave dots slot 8g + j of row q of a pass
  * and the 8-lane sum -- the first three steps of lg_wave_sum -- is the
  * row's group partial, stored to P.ao_part[g][row].  The next up|gate
  * build adds the 8 partials in lg_wave_sum's order (PartSum), so xm is the
  * att_out phase's bit for bit.  Rows of workgroup r: r * rpw .. (rpw =
  * n_embed / group size, at most 64 * AO_NP), pass p of wave w rows
  * 64p + 8w + q of them.  Waves 1.. issue their row loads before the
- * barrier wait; wave 0 polls, then issues the merge loads and its rows. */
+ * barrier wait (wave 1's merge loads go behind them); wave 0 polls, then
+ * issues the merge loads and its rows. */
 #define AO_NP 2
 template <int LT, int HD, int NREP>
 __device__ __forceinline__ void phase_ao_group(const PkParams& P, const PkLayer& L, int l, int pos, int g, int r,
@@ -142,20 +143,16 @@ __device__ __forceinline__ void phase_ao_group(const PkParams& P, const PkLayer&
     if (wave != 0) load_rows();
     group_wait(P, words, gsz, round2);
     stamp(tr, 1);
-    if (wave == 0) {
+    if (wave < 2) {   /* wave w: chunk 2g + w */
         const MergeSrc ms = att_partials<HD, NREP>(P, l, pos);
-        MergeAct<1> m0, m1;
-        m0.load_at(ms, P.n_heads, ne, (2 * g) * 256 + 4 * lane);
-        m1.load_at(ms, P.n_heads, ne, (2 * g + 1) * 256 + 4 * lane);
+        MergeAct<1> m0;
+        m0.load_at(ms, P.n_heads, ne, (2 * g + wave) * 256 + 4 * lane);
         lg_issue_order();
-        load_rows();
-        ActSrc<1> a0, a1;
+        if (wave == 0) load_rows();
+        ActSrc<1> a0;
         m0.merge(ms.nch, a0);
-        m1.merge(ms.nch, a1);
         const float v0[4] = {a0.v[0].x, a0.v[0].y, a0.v[0].z, a0.v[0].w};
-        const float v1[4] = {a1.v[0].x, a1.v[0].y, a1.v[0].z, a1.v[0].w};
-        lg_emit(v0, QT, s_act, 2 * g, 256);
-        lg_emit(v1, QT, s_act, 2 * g + 1, 256);
+        lg_emit(v0, QT, s_act, 2 * g + wave, 256);
     }
     bar();
     stamp(tr, 2);
@@ -286,14 +283,18 @@ __global__ __launch_bounds__(PK_THREADS) void k_f_ao(const PkParams P, const PkL
 }
 
 /* RSUM: the input is x_l + the att_out group partials (k_f_qkva<..., AO>),
- * stored by workgroup 0 as xm_l */
+ * stored by workgroup 0 as xm_l; its build loads 8 more vectors, so LG_UGS_R
+ * batches of rows (a deeper ring) are in flight while it runs */
+#ifndef LG_UGS_R
+#define LG_UGS_R 2
+#endif
 template <int LT, class S, bool RSUM = false>
 __global__ __launch_bounds__(PK_THREADS) void k_f_ug(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd, int l,
                                                      uint8_t* atr)
 {
     constexpr int NE = S::NE;
     const int ne = P.n_embed, nff = P.n_ff;
-    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, RSUM ? BLD_RSUM : BLD_RMS, S::CE, LG_UG_R>(
+    phase_mv<LT, NE, LG_UG_B, 2, EPI_SWIGLU, RSUM ? BLD_RSUM : BLD_RMS, S::CE, RSUM ? LG_UGS_R : LG_UG_R>(
         P, 0, L.ug, L.ug_rsz, nff, nff, L.ffn_norm, RSUM ? P.xs + (size_t)l * ne : P.xm + (size_t)l * ne, nullptr,
         P.hb + (size_t)l * nff, RSUM ? P.xm + (size_t)l * ne : nullptr, 0, 0, f_tr(Sd, l, 3), f_atr(atr, P, 4 * l + 2),
         ne);

@@ -365,6 +365,227 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(4))) void
     }
 }
 
+/* The same products on the 32 x 32 forms: v_mfma_i32_32x32x32_i8 takes 16
+ * bytes of a 32-row A and of a 32-column B per lane, twice the multiplies
+ * of a 16x16x64 product per operand byte, so each token fragment read from
+ * LDS feeds twice the work.  A workgroup of 4 waves computes 128 rows x 64
+ * tokens, a wave 32 rows x 64 tokens (two 32 x 32 tiles, token rows i,
+ * weight columns j): lane l holds row j = l % 32 of its wave's rows and the
+ * K bytes 16 (l / 32) .. +15 of a 32-value sub-block -- sub-block 2c is the
+ * low nibbles and 2c+1 the high nibbles of the same 16 bytes of qs --
+ * against the token's quants 32s + 16 (l / 32) .. +15, read from its LDS
+ * row as stored; C register r of lane l is token 8 (r / 4) + 4 (l / 32) +
+ * r % 4 of the tile, row l % 32.  Scales split sc = 8h + l as in
+ * k_pf_gemm_q4k (two products per sub-block, S = 8 S_h + S_l exactly).
+ * The mins term M = sum_s m_s (bsums_2s + bsums_2s+1) is one
+ * v_mfma_f32_32x32x16_f16 per tile: each pair sum p = 64 p_hi + p_lo is
+ * staged as two fp16 integers (p_hi in [-64, 63], p_lo in [0, 63]) against
+ * 64 m_s and m_s, so every product and partial sum is an integer below
+ * 2^24 and M is exact.  Then out += d_a (d_w S - dmin_w M) per block in the
+ * same fp32 operations as k_pf_gemm_q4k, so both give the same bits. */
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+#define PF2_NT 256
+#define PF2_RB 128    /* rows per workgroup */
+#define PF2_AST 272   /* LDS row stride of a token's 256 quants */
+/* KS = 2 (the 4096-row att_out and down products, whose 128 x 64 tiles
+ * alone would leave one wave per SIMD): 8 waves, waves 4..7 take the second
+ * half of K with LDS stages of their own, and their sums are added to the
+ * first half's through LDS at the end (acc0 + acc1, one fixed order) */
+template <int ACC, int KS>
+__global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_q4k32(
+    const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
+{
+    constexpr int TT = 64;   /* tokens per workgroup: two 32-token tiles per wave */
+    __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
+    __shared__ __attribute__((aligned(16))) _Float16 s_m[KS][2][TT * 16];   /* per token: p_hi[8], p_lo[8] */
+    __shared__ __attribute__((aligned(16))) float s_d[KS][2][TT];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kh = wave >> 2, tid = threadIdx.x & (PF2_NT - 1);   /* K half; thread within it */
+    const int h = lane >> 5, j = lane & 31;
+    const int nb = K >> 8;
+    /* this half's blocks b0 .. b0 + nbh - 1; every wave runs L steps */
+    const int nb0 = KS == 2 ? (nb + 1) / 2 : nb;
+    const int b0 = kh * nb0, nbh = kh ? nb - nb0 : nb0, L = nb0;
+    const int nt = (T + TT - 1) / TT;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int rb = (slot / nt) * 8 + xcd;
+    if (rb * PF2_RB >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
+    const int t0 = (slot % nt) * TT;
+    const int row = rb * PF2_RB + (wave & 3) * 32 + j;
+    const uint8_t* wr = W + (size_t)min(row, R - 1) * rsz;
+    int8_t(*sa_)[TT * PF2_AST] = s_a[kh];
+    _Float16(*sm_)[TT * 16] = s_m[kh];
+    float(*sd_)[TT] = s_d[kh];
+
+    /* staging, per block: quant chunk q = tid + 256 u (token q / 16, piece
+     * q % 16); thread tid also takes bsums 4 (tid % 4) .. +3 of token tid / 4
+     * (pair sums 2 (tid % 4), +1) and, tid < 64, the d of token tid */
+    struct Stg {   /* clang vectors, not HIP's uint4 structs: their copies stay in registers */
+        v4i a[4];
+        uint2 bs;
+        float d;
+    };
+    auto stage_load = [&](Stg& st, int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int q = tid + PF2_NT * u, tok = min(t0 + (q >> 4), T - 1);
+            st.a[u] = *(const v4i*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
+        }
+        const int tb = min(t0 + (tid >> 2), T - 1);
+        st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
+        st.d = x.d[(size_t)b * x.tld + min(t0 + (tid & 63), x.tld - 1)];
+    };
+    auto stage_store = [&](const Stg& st, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int q = tid + PF2_NT * u;
+            *(v4i*)(sa_[buf] + (q >> 4) * PF2_AST + (q & 15) * 16) = st.a[u];
+        }
+        const int tok = tid >> 2, s0 = 2 * (tid & 3);
+        const int p0 = (int)(int16_t)(st.bs.x & 0xffff) + (int)(int16_t)(st.bs.x >> 16);
+        const int p1 = (int)(int16_t)(st.bs.y & 0xffff) + (int)(int16_t)(st.bs.y >> 16);
+        _Float16* m = sm_[buf] + tok * 16;
+        m[s0] = (_Float16)(float)(p0 >> 6);
+        m[s0 + 1] = (_Float16)(float)(p1 >> 6);
+        m[8 + s0] = (_Float16)(float)(p0 & 63);
+        m[8 + s0 + 1] = (_Float16)(float)(p1 & 63);
+        if (tid < 64) sd_[buf][tid] = st.d;
+    };
+    /* the lane's weight bytes of one block: header and 4 x 16 B of qs */
+    struct Blk {
+        uint4 hdr;
+        uint4 q[4];
+    };
+    auto blk_load = [&](Blk& B, int b) __attribute__((always_inline)) {
+        const uint8_t* p = wr + (size_t)b * LG_BS_Q4_K;
+        B.hdr = *(const uint4*)p;
+#pragma unroll
+        for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 16 + 32 * c + 16 * h);
+    };
+
+    v16f acc[2];
+    acc[0] = (v16f){};
+    acc[1] = (v16f){};
+
+    auto compute = [&](int buf, const Blk& cur) __attribute__((always_inline)) {
+        const uint4 h4 = cur.hdr;
+        const uint32_t scq[2] = {h4.y & 0x3F3F3F3Fu, (h4.w & 0x0F0F0F0Fu) | ((h4.y >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {h4.z & 0x3F3F3F3Fu, ((h4.w >> 4) & 0x0F0F0F0Fu) | ((h4.z >> 2) & 0x30303030u)};
+        const float dw = lg_h2f((uint16_t)(h4.x & 0xffffu));
+        const float dmw = lg_h2f((uint16_t)(h4.x >> 16));
+        /* mins operand: 64 m_s (lanes 0..31) or m_s (32..63), s = 0..7 */
+        v8h bm;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int m = (int)((mn[s >> 2] >> (8 * (s & 3))) & 0xFFu);
+            bm[s] = (_Float16)(float)(h ? m : 64 * m);
+        }
+        v16i Sh[2], Sl[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) Sh[t] = Sl[t] = (v16i){};
+        const int8_t* sa = sa_[buf] + j * PF2_AST + 16 * h;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t qw[4] = {cur.q[c].x, cur.q[c].y, cur.q[c].z, cur.q[c].w};
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int s = 2 * c + e;
+                const uint32_t sc = (scq[s >> 2] >> (8 * (s & 3))) & 0x3Fu;
+                const v2u16 sh = (v2u16)(uint16_t)(sc >> 3), sl = (v2u16)(uint16_t)(sc & 7u);
+                v4i bh, bl;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t nib = e ? (qw[k] >> 4) & 0x0F0F0F0Fu : qw[k] & 0x0F0F0F0Fu;
+                    bh[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(nib) * sh);
+                    bl[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(nib) * sl);
+                }
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint4 a = *(const uint4*)(sa + 32 * t * PF2_AST + 32 * s);
+                    const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+                    Sh[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bh, Sh[t], 0, 0, 0);
+                    Sl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, Sl[t], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const v8h am = *(const v8h*)(sm_[buf] + (32 * t + j) * 16 + 8 * h);
+            const v16f M = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, (v16f){}, 0, 0, 0);
+            const v16i S = Sh[t] * 8 + Sl[t];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dx = *(const float4*)(sd_[buf] + 32 * t + 8 * g + 4 * h);
+                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * g + i;
+                    acc[t][r] = __builtin_fmaf(dxs[i], lg_fma2(dw, (float)S[r], -dmw, M[r]), acc[t][r]);
+                }
+            }
+        }
+    };
+
+    /* step i of this half: the token tile of block b0 + i + 2 loads into
+     * registers while block b0 + i computes, and goes to LDS after it (two
+     * blocks' compute for each staging load; one for the weights) */
+    auto blk = [&](int i) { return b0 + min(i, nbh - 1); };
+    Blk cur, nxt;
+    Stg st0, st1;
+    stage_load(st0, blk(0));
+    stage_load(st1, blk(1));
+    blk_load(cur, blk(0));
+    stage_store(st0, 0);
+    __syncthreads();
+#define PF2_STEP(ii, ST_LD, ST_ST)                \
+    do {                                          \
+        stage_load(ST_LD, blk((ii) + 2));         \
+        blk_load(nxt, blk((ii) + 1));             \
+        if ((ii) < nbh) compute((ii) & 1, cur);   \
+        stage_store(ST_ST, ((ii) + 1) & 1);       \
+        cur = nxt;                                \
+        __syncthreads();                          \
+    } while (0)
+    /* pairs of steps (an odd count ends on one that computes nothing; the
+     * second half may have one block fewer) */
+    for (int i = 0; i < L; i += 2) {
+        PF2_STEP(i, st0, st1);
+        PF2_STEP(i + 1, st1, st0);
+    }
+#undef PF2_STEP
+    if constexpr (KS == 2) {
+        /* the second half's sums through LDS (its stage buffers are done) */
+        float* red = (float*)s_a[1];
+        if (kh == 1) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) red[(t * 16 + r) * (PF2_NT) + tid] = acc[t][r];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][r] = acc[t][r] + red[(t * 16 + r) * (PF2_NT) + tid];
+    }
+    if (row < R) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tok = t0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (tok < T) {
+                    float* o = out + (size_t)tok * ldo + row;
+                    *o = ACC ? *o + acc[t][r] : acc[t][r];
+                }
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
@@ -376,9 +597,29 @@ static int gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const Pf
         lg_set_error("prefill gemm: bad arguments (rows %d, cols %d, T %d)", rows, cols, T);
         return LG_ERR_ARG;
     }
-    /* 64-token tiles: 128 VGPRs, so up to four workgroups share a CU (at
-     * 128 tokens a workgroup needs 220 and the 512-token up|gate GEMM ran 10%
-     * slower) */
+    static const bool k16 = [] {
+        const char* e = getenv("LG_PF_GEMM16");
+        return e && e[0] == '1';
+    }();
+    if (!k16) {
+        /* the 32 x 32 product kernel: 128 rows x 64 tokens per workgroup;
+         * two K halves in one workgroup where the tiles alone would give one
+         * workgroup per CU or fewer (the 4096-row products at 512 tokens,
+         * att_out and down: 68.0 -> 61.8 us on average; Q|K|V's 384 tiles
+         * ran faster unsplit, 48.7 against 55.2 us) */
+        const int nrb = (rows + PF2_RB - 1) / PF2_RB + 7 & ~7;
+        const int ntl = (T + 63) / 64;
+        const bool ks2 = nrb * ntl <= 256 && cols >= 4 * 256;
+        const dim3 grid((unsigned)(nrb * ntl)), blk(ks2 ? 2 * PF2_NT : PF2_NT);
+#define PF2_LAUNCH(A, N) hipLaunchKernelGGL((k_pf_gemm_q4k32<A, N>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo)
+        if (accumulate) { if (ks2) PF2_LAUNCH(1, 2); else PF2_LAUNCH(1, 1); }
+        else { if (ks2) PF2_LAUNCH(0, 2); else PF2_LAUNCH(0, 1); }
+#undef PF2_LAUNCH
+        return lg_check_launch("prefill gemm");
+    }
+    /* LG_PF_GEMM16=1: the 16 x 16 product kernel.  64-token tiles: 128
+     * VGPRs, so up to four workgroups share a CU (at 128 tokens a workgroup
+     * needs 220 and the 512-token up|gate GEMM ran 10% slower) */
     const int nrb8 = (rows + PF_RB - 1) / PF_RB + 7 & ~7;
 #ifndef LG_PF_MI
 #define LG_PF_MI 4
