@@ -202,7 +202,6 @@ template <int LT, int VT, class S, int HD, int NREP, bool EMB, bool LONG, bool A
 __global__ __launch_bounds__(PK_THREADS) void k_f_qkva(const PkParams P, const PkLayer L, const PkStep* __restrict__ Sd,
                                                        int l, uint8_t* atr)
 {
-    static_assert(!(AO && LONG), "att_out by KV group: short-context units");
     constexpr int NE = S::NE;
     const int ne = P.n_embed, kvd = P.kv_dim, qs = ne + 2 * kvd;
     const int nkv = P.n_kv, g = (int)blockIdx.x % nkv, gsz = (int)gridDim.x / nkv, r = (int)blockIdx.x / nkv;
@@ -407,16 +406,17 @@ static bool f_qkva_ok(const PkParams& P, int nwg, bool long_ctx)
     return P.qkva && nwg % P.n_kv == 0 && nwg <= LG_MAX_GROUP_WORDS && (!long_ctx || P.att_grid <= nwg);
 }
 
-/* att_out in the QKV + attention kernel, split by KV group: short-context
- * units, 8 KV groups of 512 query values (8 slots of a 4096-value row of a
- * 64-value-slot format, one slot per lane), at most 64 * AO_NP rows per
- * workgroup */
+/* att_out in the QKV + attention kernel, split by KV group: 8 KV groups
+ * of 512 query values (8 slots of a 4096-value row of a 64-value-slot
+ * format, one slot per lane), at most 64 * AO_NP rows per workgroup; the
+ * long-context units' chunk groups are merged into their slots before the
+ * group barrier, so the group merge reads those as the att_out build does */
 template <int LT, class SH, int HD, int NREP>
 static bool f_qkvao_ok(const PkParams& P, int nwg, bool long_ctx)
 {
     if constexpr (Fmt<LT>::VALS != 64 || NREP * HD != 512 || SH::NE != 1) return false;
     else {
-        if (!P.qkvao || !P.ao_part || long_ctx || !f_qkva_ok(P, nwg, false) || P.n_kv != 8 || P.n_embed != 4096)
+        if (!P.qkvao || !P.ao_part || !f_qkva_ok(P, nwg, long_ctx) || P.n_kv != 8 || P.n_embed != 4096)
             return false;
         const int gsz = nwg / P.n_kv;
         return P.n_embed % gsz == 0 && P.n_embed / gsz <= 64 * AO_NP;
@@ -482,7 +482,8 @@ static void fused_enqueue(const PkParams& P, const PkLayer* Lh, PkStep* S, int n
             /* three kernels a layer: QKV + attention + att_out by KV group,
              * up|gate on x + the partials, down */
             for (int l = 0; l < n_layers; l++) {
-                f_launch_qkva_n<LT, SH, HD, NREP, false, true>(P, Lh[l], S, l, g, b, st, atr);
+                if (long_ctx) f_launch_qkva_n<LT, SH, HD, NREP, true, true>(P, Lh[l], S, l, g, b, st, atr);
+                else f_launch_qkva_n<LT, SH, HD, NREP, false, true>(P, Lh[l], S, l, g, b, st, atr);
                 hipLaunchKernelGGL((k_f_ug<LT, SH, true>), g, b, 0, st, P, Lh[l], S, l, atr);
                 f_launch_down<LT, SH>(P, Lh[l], S, l, g, b, st, atr);
             }
@@ -518,7 +519,11 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
     switch (phase) {
     case 0:   /* with the fused QKV + attention (+ att_out) kernel in use, that kernel */
         if constexpr (Fmt<LT>::VALS == 64 && NREP * HD == 512 && SH::NE == 1) {
-            if (ao) { f_launch_qkva_n<LT, SH, HD, NREP, false, true>(P, Lh[l], S, l, g, b, st, nullptr); break; }
+            if (ao) {
+                if (long_ctx) f_launch_qkva_n<LT, SH, HD, NREP, true, true>(P, Lh[l], S, l, g, b, st, nullptr);
+                else f_launch_qkva_n<LT, SH, HD, NREP, false, true>(P, Lh[l], S, l, g, b, st, nullptr);
+                break;
+            }
         }
         if (f_qkva_ok(P, nwg, long_ctx)) f_launch_qkva<LT, SH, HD, NREP>(P, Lh[l], S, l, g, b, st, nullptr, long_ctx);
         else f_launch_qkv<LT, SH>(P, Lh[l], S, l, g, b, st, nullptr);
