@@ -48,19 +48,21 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-UG_KERNEL = "k_f_ug Q4_K (rmsnorm + up|gate 24576x4096 + SwiGLU)"
+UG_KERNEL = "k_f_ug Q4_K (x + att_out group partials, rmsnorm + up|gate 24576x4096 + SwiGLU)"
 
 
 def dominant_kernel_roofline(eng, cfg, passes: int = 5):
     """Mean duration of the fused up|gate kernel over `passes` sweeps of all
     layers (lg_time_fused_phase: HIP events on the engine's stream), against
-    its algorithmic bytes: the two Q4_K matrices, the fp32 input vector and
-    rmsnorm weights it reads and the fp32 SwiGLU output it writes."""
+    its algorithmic bytes: the two Q4_K matrices; the fp32 residual input, the
+    8 att_out partials of the KV groups (summed into xm by its build) and the
+    rmsnorm weights it reads; the fp32 SwiGLU output and xm it writes."""
     from ligguf_amd.lib import Q4_K, row_size
     iters = passes * cfg.n_layers
     eng.time_phase(3, 0, cfg.n_layers)             # warm-up sweep
     avg_us = eng.time_phase(3, 0, iters)
-    alg = 2 * cfg.n_ff * row_size(Q4_K, cfg.n_embed) + 2 * cfg.n_embed * 4 + cfg.n_ff * 4
+    alg = (2 * cfg.n_ff * row_size(Q4_K, cfg.n_embed) + (1 + 8 + 1) * cfg.n_embed * 4 + cfg.n_ff * 4 +
+           cfg.n_embed * 4)
     avg_s = avg_us * 1e-6
     return {"bound": "hbm", "achieved": round(alg / avg_s / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": round(alg / avg_s / HBM_PEAK, 4), "traffic": measured_traffic(UG_KERNEL),
