@@ -1,8 +1,10 @@
 /* lg_fused.hip -- the per-token step of inference()
- * (fast/ligguf_fast_qk.cpp:24-144) as five fused kernels per layer plus one
- * for the output head, meant to be replayed from a HIP graph.
+ * (fast/ligguf_fast_qk.cpp:24-144) as fused kernels -- by default three per
+ * layer (qkv + attn + ao in k_f_qkva, the ao rows split by KV group; ug;
+ * down) -- plus one for the output head, meant to be replayed from a HIP
+ * graph.
  *
- * Per layer l (one workgroup of 8 waves per CU in every kernel):
+ * The phases of layer l (one workgroup of 8 waves per CU in every kernel):
  *   qkv   rmsnorm(x)->Q8 in LDS (every workgroup), Q|K|V rows      -> qkv[l]
  *   attn  QK-norm + RoPE + fp16 KV write of row pos, one-pass online
  *         softmax over (kv head, chunk) units               -> partials
@@ -20,9 +22,10 @@
  * flat access would also count against lgkmcnt, and each LDS wait of a
  * build would then wait for all of the wave's outstanding weight loads.
  * Every kernel issues its weight loads first and builds its activation
- * while they are in flight; the kernel boundary is the only sync (a graph
- * replays 5*n_layers + 1 kernels at ~1.6 us of fixed cost each, cheaper than
- * a flag sync through memory).  The token and position come from device
+ * while they are in flight; the kernel boundary is the only grid-wide sync
+ * (a graph replays 3*n_layers + 1 kernels at ~1.6 us of fixed cost each,
+ * cheaper than a flag sync through memory), the KV groups' barriers inside
+ * k_f_qkva stay within one XCD each.  The token and position come from device
  * memory (PkStep), so one captured graph serves every step.  The phase code
  * is the persistent kernel's (lg_phase.h): same arithmetic, same bits.
  */
