@@ -37,6 +37,13 @@
 /* activation build area: fp32 staging of x (rmsnorm) + quantized blocks */
 __shared__ __attribute__((aligned(16))) float s_x[PK_MAX_EMBED];
 __shared__ __attribute__((aligned(16))) uint8_t s_act[(PK_MAX_FF / 256) * LG_BS_Q8_K + 64];
+/* the fp32 activation of F16 rows, each 32-value slot followed by 4 unused
+ * floats: lanes read consecutive slots, and a 144-byte slot stride puts
+ * their 16-byte reads on distinct banks (a 128-byte stride would put every
+ * lane on the same ones).  Kernels of other formats do not reference it, so
+ * it takes LDS in F16 kernels only. */
+#define PK_ACTF_SLOT 36
+__shared__ __attribute__((aligned(16))) float s_actf[PK_MAX_FF_F / 32 * PK_ACTF_SLOT];
 __shared__ float s_red[64];
 __shared__ int s_int[8];
 /* attention */
@@ -220,12 +227,62 @@ __device__ __forceinline__ void stamp(uint64_t* tr, int k)
 enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3, BLD_KEEP = 4, BLD_RSUM = 5 };
 
 /* the activation format a weight format's dot reads: Q8_0 blocks for
- * Q8_0/Q1_0/Q1_G rows, Q8_K blocks for the K-quants */
+ * Q8_0/Q1_0/Q1_G rows, Q8_K blocks for the K-quants, fp32 for F16 rows (the
+ * reference's matmul passes the float vector to dot_f16_f32,
+ * fast/lil_math.cpp:397-409) */
 __host__ __device__ constexpr int lg_act_qt(int fmt)
 {
-    return (fmt == LG_Q8_0 || fmt == LG_Q8_0_R || fmt == LG_Q1_0 || fmt == LG_Q1_0_R || fmt == LG_Q1_G ||
+    return fmt == LG_F16_L ? LG_F32
+         : (fmt == LG_Q8_0 || fmt == LG_Q8_0_R || fmt == LG_Q1_0 || fmt == LG_Q1_0_R || fmt == LG_Q1_G ||
             fmt == LG_Q1_G_R) ? LG_Q8_0 : LG_Q8_K;
 }
+
+/* the wave's 256 values of chunk ch as an activation of format QT: fp32
+ * into s_actf (slot-padded), quantized blocks into s_act */
+template <int QT>
+__device__ __forceinline__ void act_emit(const float v[4], int ch, int nvalid)
+{
+    if constexpr (QT == LG_F32) {
+        const int lane = LG_TID & 63;
+        if (4 * lane < nvalid)
+            *(float4*)(s_actf + ch * (8 * PK_ACTF_SLOT) + (lane >> 3) * PK_ACTF_SLOT + 4 * (lane & 7)) =
+                make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+        lg_emit(v, QT, s_act, ch, nvalid);
+    }
+}
+
+/* F16 rows against the fp32 activation in s_actf: the slot's 32 floats are
+ * read from LDS at each dot (held in registers they would take 32 VGPRs a
+ * slot, 192 for a 12288-value down row), the same products and order as
+ * Fmt<LG_F16> (dot_f16_f32, fast/arch_avx2.h:83-109) */
+template <>
+struct Fmt<LG_F16_L> {
+    static constexpr int VALS = 32;
+    struct Act {
+        int s;
+    };
+    using W = Fmt<LG_F16>::W;
+    static __device__ __forceinline__ void load_act(Act& A, const uint8_t*, int s) { A.s = s; }
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s) { Fmt<LG_F16>::load_w(w, row, s); }
+    static __device__ __forceinline__ float dot(const W& w, const Act& A, int)
+    {
+        const float4* a = (const float4*)(s_actf + A.s * PK_ACTF_SLOT);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 p = a[2 * i], q = a[2 * i + 1];
+            const float f[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+            const uint32_t u[4] = {w.v[i].x, w.v[i].y, w.v[i].z, w.v[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                acc += lg_h2f((uint16_t)(u[k] & 0xffffu)) * f[2 * k];
+                acc += lg_h2f((uint16_t)(u[k] >> 16)) * f[2 * k + 1];
+            }
+        }
+        return acc;
+    }
+};
 
 __device__ __forceinline__ int chunk_base(int c)
 {
@@ -448,12 +505,12 @@ __device__ __forceinline__ void build_rms(const PkParams& P, int tok, const Norm
         if (256 * ch >= n) break;   /* wave-uniform */
         const float4 t = xv[c], g = nw.g[c];
         const float v[4] = {t.x * scale * g.x, t.y * scale * g.y, t.z * scale * g.z, t.w * scale * g.w};
-        lg_emit(v, QT, s_act, ch, min(256, n - 256 * ch));
+        act_emit<QT>(v, ch, min(256, n - 256 * ch));
     }
     bar();
 }
 
-/* the source chunks quantized into s_act */
+/* the source chunks quantized into s_act (fp32 into s_actf) */
 template <int QT, int CPW>
 __device__ __forceinline__ void build_plain(const ActSrc<CPW>& a, int n)
 {
@@ -464,7 +521,7 @@ __device__ __forceinline__ void build_plain(const ActSrc<CPW>& a, int n)
         if (256 * ch >= n) break;   /* wave-uniform */
         const bool ok = chunk_base(c) < n;
         const float v[4] = {ok ? a.v[c].x : 0.f, ok ? a.v[c].y : 0.f, ok ? a.v[c].z : 0.f, ok ? a.v[c].w : 0.f};
-        lg_emit(v, QT, s_act, ch, min(256, n - 256 * ch));
+        act_emit<QT>(v, ch, min(256, n - 256 * ch));
     }
     bar();
 }
@@ -652,8 +709,9 @@ __device__ __forceinline__ void phase_mv(const PkParams& P, int tok, const uint8
         build_plain<QT, CPW>(as, n_act);
     }
     stamp(tr, 2);
-    if (atr && blockIdx.x == 0) {
-        /* activation trace (tests): the quantized blocks as built */
+    if (QT != LG_F32 && atr && blockIdx.x == 0) {
+        /* activation trace (tests): the quantized blocks as built (fp32
+         * activations are not compared: nothing is quantized there) */
         const int words = ((QT == LG_Q8_K ? n_act / 256 * LG_BS_Q8_K : n_act / 32 * LG_BS_Q8_0) + 3) / 4;
         for (int i = LG_TID; i < words; i += PK_THREADS) ((uint32_t*)atr)[i] = ((const uint32_t*)s_act)[i];
     }
