@@ -18,9 +18,11 @@
 #define LG_Q1_G_R 141
 #define LG_Q3_K_R 111
 #define LG_Q1_0_R 140
-/* internal form of F16 rows in the whole-step kernels: the fp32 activation
- * they multiply stays in LDS (Fmt<LG_F16_L> in lg_phase.h) */
+/* internal forms of F16 / F32 rows in the whole-step kernels: the fp32
+ * activation they multiply stays in LDS (Fmt<LG_F16_L>, Fmt<LG_F32_L> in
+ * lg_phase.h) */
 #define LG_F16_L 101
+#define LG_F32_L 102
 #define LG_BS_Q8_0 34
 #define LG_BS_Q1_0 6
 #define LG_BS_Q1_G 18

@@ -463,11 +463,12 @@ static int setup_persistent(lg_ctx* ctx, const lg_model_desc* m)
      * than n_context does (up to the clamped att_max, never more) */
     att_nch = std::max(std::min(std::max(att_max, PK_ATT_MERGE), PK_ATT_MAX_NCH), PK_ATT_MERGE);
     /* widths: any the activation builds hold (LDS staging of n_embed and of
-     * the quantized n_ff vector -- the fp32 one for F16 layers), in whole
+     * the quantized n_ff vector -- the fp32 one for F16 / F32 layers), in whole
      * 256-value Q8_K blocks for K-quant and Q1_G layers; which widths have
      * kernels is up to the variants */
-    const bool q8act = lt == LG_Q8_0 || lt == LG_Q1_0 || lt == LG_F16;
-    bool ok = m->n_embed <= PK_MAX_EMBED && m->n_ff <= (lt == LG_F16 ? PK_MAX_FF_F : PK_MAX_FF) &&
+    const bool fact = lt == LG_F16 || lt == LG_F32;
+    const bool q8act = lt == LG_Q8_0 || lt == LG_Q1_0 || fact;
+    bool ok = m->n_embed <= PK_MAX_EMBED && m->n_ff <= (fact ? PK_MAX_FF_F : PK_MAX_FF) &&
               m->n_embed % (q8act ? 32 : 256) == 0 &&
               m->n_ff % (q8act ? 32 : 256) == 0 && att_chunk > 0 && att_nch <= PK_ATT_MAX_NCH &&
               m->n_kv_heads <= 32 && m->n_heads <= 64 && ctx->output.cols == m->n_embed;

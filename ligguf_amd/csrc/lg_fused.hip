@@ -549,10 +549,10 @@ static void fused_phase(const PkParams& P, const PkLayer* Lh, PkStep* S, int pha
 
 /* slots per lane of a row of n values of type t, and 256-value chunks per
  * wave of an n-wide activation build */
-static constexpr int f_vps(int t) { return (t == LG_Q8_0 || t == LG_Q1_0 || t == LG_F16) ? 32 : 64; }
-/* the kernels' form of a file type: F16 rows dot an fp32 activation held in
- * LDS (Fmt<LG_F16_L>) */
-static constexpr int f_kt(int t) { return t == LG_F16 ? LG_F16_L : t; }
+static constexpr int f_vps(int t) { return (t == LG_Q8_0 || t == LG_Q1_0 || t == LG_F16 || t == LG_F32) ? 32 : 64; }
+/* the kernels' form of a file type: F16 / F32 rows dot an fp32 activation
+ * held in LDS (Fmt<LG_F16_L>, Fmt<LG_F32_L>) */
+static constexpr int f_kt(int t) { return t == LG_F16 ? LG_F16_L : t == LG_F32 ? LG_F32_L : t; }
 static constexpr int f_ns(int t, int n) { return (n / f_vps(t) + 63) / 64; }
 static constexpr int f_cpw(int n) { return (n + 256 * PK_WAVES - 1) / (256 * PK_WAVES); }
 
@@ -570,8 +570,8 @@ struct FusedVariant {
  * n_embed 4096 / n_ff 14336 (Llama-3-8B, Mistral-7B), n_embed 2560 / n_ff
  * 9728 (Qwen3-4B), n_embed 5120 / n_ff 17408 (Qwen3-14B: 40 query heads on
  * 8 KV heads), n_embed 2048 / n_ff 5632 (TinyLlama-1.1B, head_dim 64), and
- * any width up to 2048 / 2048 (tiny models); F16 layers (and head) at the
- * Qwen3-8B shape */
+ * any width up to 2048 / 2048 (tiny models); F16 and F32 layers (and head)
+ * at the Qwen3-8B shape */
 #define FVS(LT, OT, HD, NR, E, F)                                                                              \
     {LT, OT, HD, NR, f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F),                                \
      fused_enqueue<f_kt(LT), f_kt(OT), HD, NR, FShape<f_ns(LT, E), f_ns(OT, E), f_cpw(E), f_ns(LT, F), f_cpw(F)>>,  \
@@ -626,7 +626,7 @@ const FusedVariant* lg_fused_part_3(int* n)
         FVS(LG_Q4_K, LG_Q6_K, 128, 4, 2560, 9728), FVS(LG_Q4_K, LG_Q6_K, 128, 5, 5120, 17408),
         FVS(LG_Q4_K, LG_Q6_K, 64, 8, 2048, 5632), FVS(LG_Q8_0, LG_Q8_0, 64, 8, 2048, 5632),
         FVS(LG_Q8_0, LG_Q8_0, 48, 1, 2048, 2048), FVS(LG_Q8_0, LG_Q8_0, 64, 1, 2048, 2048),
-        FVS(LG_Q4_K, LG_Q6_K, 64, 1, 2048, 2048),
+        FVS(LG_Q4_K, LG_Q6_K, 64, 1, 2048, 2048), FV(LG_F32, LG_F32, 128, 4),
     };
     *n = (int)(sizeof(v) / sizeof(v[0]));
     return v;

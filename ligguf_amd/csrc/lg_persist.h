@@ -8,7 +8,7 @@
 #define PK_THREADS 512      /* 8 waves per workgroup, one workgroup per CU */
 #define PK_MAX_EMBED 8192   /* n_embed limit (fp32 staging of x in LDS) */
 #define PK_MAX_FF 20480     /* n_ff limit (quantized activation in LDS) */
-#define PK_MAX_FF_F 12288   /* n_ff limit of F16 layers (fp32 activation in LDS) */
+#define PK_MAX_FF_F 12288   /* n_ff limit of F16 / F32 layers (fp32 activation in LDS) */
 #define PK_MAX_NREP 8       /* query heads per KV head */
 #define PK_ATT_MERGE 8      /* attention partials per head merged by the att_out build */
 #define LG_MAX_GROUP_WORDS 1024 /* workgroups of the fused QKV + attention kernel, at most (one barrier word each) */

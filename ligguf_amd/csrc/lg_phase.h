@@ -37,7 +37,7 @@
 /* activation build area: fp32 staging of x (rmsnorm) + quantized blocks */
 __shared__ __attribute__((aligned(16))) float s_x[PK_MAX_EMBED];
 __shared__ __attribute__((aligned(16))) uint8_t s_act[(PK_MAX_FF / 256) * LG_BS_Q8_K + 64];
-/* the fp32 activation of F16 rows, each 32-value slot followed by 4 unused
+/* the fp32 activation of F16 / F32 rows, each 32-value slot followed by 4 unused
  * floats: lanes read consecutive slots, and a 144-byte slot stride puts
  * their 16-byte reads on distinct banks (a 128-byte stride would put every
  * lane on the same ones).  Kernels of other formats do not reference it, so
@@ -227,12 +227,12 @@ __device__ __forceinline__ void stamp(uint64_t* tr, int k)
 enum { BLD_RMS = 0, BLD_PLAIN = 1, BLD_MERGE = 2, BLD_EMB = 3, BLD_KEEP = 4, BLD_RSUM = 5 };
 
 /* the activation format a weight format's dot reads: Q8_0 blocks for
- * Q8_0/Q1_0/Q1_G rows, Q8_K blocks for the K-quants, fp32 for F16 rows (the
- * reference's matmul passes the float vector to dot_f16_f32,
+ * Q8_0/Q1_0/Q1_G rows, Q8_K blocks for the K-quants, fp32 for F16 / F32 rows
+ * (the reference's matmul passes the float vector to dot_f16_f32 / dot_f32,
  * fast/lil_math.cpp:397-409) */
 __host__ __device__ constexpr int lg_act_qt(int fmt)
 {
-    return fmt == LG_F16_L ? LG_F32
+    return (fmt == LG_F16_L || fmt == LG_F32_L) ? LG_F32
          : (fmt == LG_Q8_0 || fmt == LG_Q8_0_R || fmt == LG_Q1_0 || fmt == LG_Q1_0_R || fmt == LG_Q1_G ||
             fmt == LG_Q1_G_R) ? LG_Q8_0 : LG_Q8_K;
 }
@@ -279,6 +279,28 @@ struct Fmt<LG_F16_L> {
                 acc += lg_h2f((uint16_t)(u[k] & 0xffffu)) * f[2 * k];
                 acc += lg_h2f((uint16_t)(u[k] >> 16)) * f[2 * k + 1];
             }
+        }
+        return acc;
+    }
+};
+
+/* F32 rows against the same fp32 activation: the products and order of
+ * Fmt<LG_F32> (dot_f32, fast/arch_avx2.h:83-109) */
+template <>
+struct Fmt<LG_F32_L> {
+    static constexpr int VALS = 32;
+    using Act = Fmt<LG_F16_L>::Act;
+    using W = Fmt<LG_F32>::W;
+    static __device__ __forceinline__ void load_act(Act& A, const uint8_t*, int s) { A.s = s; }
+    static __device__ __forceinline__ void load_w(W& w, const uint8_t* row, int s) { Fmt<LG_F32>::load_w(w, row, s); }
+    static __device__ __forceinline__ float dot(const W& w, const Act& A, int)
+    {
+        const float4* a = (const float4*)(s_actf + A.s * PK_ACTF_SLOT);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 f = a[i];
+            acc += __builtin_fmaf(w.v[i].w, f.w, __builtin_fmaf(w.v[i].z, f.z, lg_fma2(w.v[i].x, f.x, w.v[i].y, f.y)));
         }
         return acc;
     }
@@ -1333,7 +1355,9 @@ struct Batch {
 #define LG_QKV_B (Batch<LT, NE, 1, 2, 512>::value)
 #endif
 #ifndef LG_QKV_R
-#define LG_QKV_R 2
+/* a second batch in flight while a batch takes at most 128 bytes a lane
+ * (all but F32 rows) */
+#define LG_QKV_R (Batch<LT, NE, 1, 2, 512>::bytes > 128 ? 1 : 2)
 #endif
 #ifndef LG_AO_B
 #define LG_AO_B (Batch<LT, NE, 1, 1, 512>::value)
@@ -1345,7 +1369,7 @@ struct Batch {
 #define LG_UG_B 1
 #endif
 #ifndef LG_UG_R
-#define LG_UG_R 2
+#define LG_UG_R (Batch<LT, NE, 2, 1, 512>::bytes > 256 ? 1 : 2)
 #endif
 #ifndef LG_DN_B
 #define LG_DN_B (Batch<LT, NF, 1, 1, 512>::value)

@@ -9,12 +9,12 @@ long-context units with their 8-lane position groups) against the oracle's
 exact attention over the same fp16 cache.  The tiny parity config T runs
 its own tests (tests/test_gpu_decode.py) on the path AUTO picks, which is
 this one.  A model mixing V and down types per layer (Q4_K_M-style) runs the
-same tests on the fused path's mixed-layer kernels, and an F16 model on the
-F16 kernels (fp32 activations held in LDS)."""
+same tests on the fused path's mixed-layer kernels, and F16 and F32 models
+on the kernels that hold the fp32 activations in LDS."""
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import (F16, PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q1_0, Q2_K, Q3_K,
+from ligguf_amd.lib import (F16, F32, PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q1_0, Q2_K, Q3_K,
                             Q4_K, Q5_K, Q6_K, Q8_0, LgError)
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
 from parity import step_flips
@@ -48,8 +48,9 @@ SHAPES = [
                 Q6_K),
     # Q5_K layers with 8 query heads per KV head
     ModelConfig("qwen3-w4096-q5k-nrep8", 1, 2, 4096, 32, 4, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K),
-    # F16 layers, embedding and output head: the fp32 activations stay in LDS, nothing is quantized
+    # F16 / F32 layers, embedding and output head: the fp32 activations stay in LDS, nothing is quantized
     ModelConfig("qwen3-w4096-f16", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, F16, F16, F16),
+    ModelConfig("qwen3-w4096-f32", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, F32, F32, F32),
     # Q5_K_M-style: Q5_K layers, Q6_K attn_v and ffn_down in layer 1
     ModelConfig("qwen3-w4096-q5k-mixed", 1, 2, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q5_K, Q4_K, Q6_K,
                 overrides=(("attn_v.1", Q6_K), ("ffn_down.1", Q6_K))),
