@@ -17,6 +17,7 @@
  * so every integer of the reference's decomposition is reproduced and only
  * the fp32 accumulation order differs from T sequential steps. */
 #include <math.h>
+#include <type_traits>
 
 #include "lg_common.h"
 #include "lg_fmt.h"
@@ -27,6 +28,7 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+typedef short v2i16 __attribute__((ext_vector_type(2)));
 
 template <typename To, typename From>
 __device__ __forceinline__ To lg_bits(From v)
@@ -382,10 +384,21 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(4))) void
  * staged as two fp16 integers (p_hi in [-64, 63], p_lo in [0, 63]) against
  * 64 m_s and m_s, so every product and partial sum is an integer below
  * 2^24 and M is exact.  Then out += d_a (d_w S - dmin_w M) per block in the
- * same fp32 operations as k_pf_gemm_q4k, so both give the same bits. */
+ * same fp32 operations as k_pf_gemm_q4k, so both give the same bits.
+ *
+ * Q6_K rows (WT = LG_Q6_K) on the same tile: lane l's 16 bytes of chunk s
+ * (values 32s + 16 (l / 32) ..) are the whole of 16-value sub-block
+ * 2s + l / 32, so the lane folds its scale into them: w = sc (q - 32) (sc
+ * the int8 scale, |w| <= 4096, one packed 16-bit multiply-add per two
+ * values) is split w = 64 w_h + w_l (w_h in [-64, 64], w_l in [0, 63]) and
+ * the two byte forms go through two products: S = 64 S_h + S_l =
+ * sum_i sc_i sum (q - 32) a, the integer of k_pf_gemm_kq's Q6_K dot,
+ * exactly; out += (d_w d_a) S as there, so the two kernels give the same
+ * bits. */
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 #define PF2_NT 256
 #define PF2_RB 128    /* rows per workgroup */
 #define PF2_AST 272   /* LDS row stride of a token's 256 quants */
@@ -393,13 +406,17 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
  * alone would leave one wave per SIMD): 8 waves, waves 4..7 take the second
  * half of K with LDS stages of their own, and their sums are added to the
  * first half's through LDS at the end (acc0 + acc1, one fixed order) */
-template <int ACC, int KS>
-__global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_q4k32(
+template <int WT, int ACC, int KS>
+__global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_k32(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
+    static_assert(WT == LG_Q4_K || WT == LG_Q6_K, "Q4_K or Q6_K rows");
+    constexpr int BSZ = WT == LG_Q4_K ? LG_BS_Q4_K : LG_BS_Q6_K;
     constexpr int TT = 64;   /* tokens per workgroup: two 32-token tiles per wave */
     __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
-    __shared__ __attribute__((aligned(16))) _Float16 s_m[KS][2][TT * 16];   /* per token: p_hi[8], p_lo[8] */
+    /* per token: p_hi[8], p_lo[8] (Q4_K mins) */
+    constexpr int MST = WT == LG_Q4_K ? TT * 16 : 8;
+    __shared__ __attribute__((aligned(16))) _Float16 s_m[KS][2][MST];
     __shared__ __attribute__((aligned(16))) float s_d[KS][2][TT];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kh = wave >> 2, tid = threadIdx.x & (PF2_NT - 1);   /* K half; thread within it */
@@ -416,7 +433,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
     const int row = rb * PF2_RB + (wave & 3) * 32 + j;
     const uint8_t* wr = W + (size_t)min(row, R - 1) * rsz;
     int8_t(*sa_)[TT * PF2_AST] = s_a[kh];
-    _Float16(*sm_)[TT * 16] = s_m[kh];
+    _Float16(*sm_)[MST] = s_m[kh];
     float(*sd_)[TT] = s_d[kh];
 
     /* staging, per block: quant chunk q = tid + 256 u (token q / 16, piece
@@ -433,8 +450,10 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             const int q = tid + PF2_NT * u, tok = min(t0 + (q >> 4), T - 1);
             st.a[u] = *(const v4i*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
         }
-        const int tb = min(t0 + (tid >> 2), T - 1);
-        st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
+        if constexpr (WT == LG_Q4_K) {   /* the bsums feed the mins term */
+            const int tb = min(t0 + (tid >> 2), T - 1);
+            st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
+        }
         st.d = x.d[(size_t)b * x.tld + min(t0 + (tid & 63), x.tld - 1)];
     };
     auto stage_store = [&](const Stg& st, int buf) __attribute__((always_inline)) {
@@ -443,33 +462,111 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             const int q = tid + PF2_NT * u;
             *(v4i*)(sa_[buf] + (q >> 4) * PF2_AST + (q & 15) * 16) = st.a[u];
         }
-        const int tok = tid >> 2, s0 = 2 * (tid & 3);
-        const int p0 = (int)(int16_t)(st.bs.x & 0xffff) + (int)(int16_t)(st.bs.x >> 16);
-        const int p1 = (int)(int16_t)(st.bs.y & 0xffff) + (int)(int16_t)(st.bs.y >> 16);
-        _Float16* m = sm_[buf] + tok * 16;
-        m[s0] = (_Float16)(float)(p0 >> 6);
-        m[s0 + 1] = (_Float16)(float)(p1 >> 6);
-        m[8 + s0] = (_Float16)(float)(p0 & 63);
-        m[8 + s0 + 1] = (_Float16)(float)(p1 & 63);
+        const int tok = tid >> 2;
+        (void)tok;
+        if constexpr (WT == LG_Q4_K) {
+            const int s0 = 2 * (tid & 3);
+            const int p0 = (int)(int16_t)(st.bs.x & 0xffff) + (int)(int16_t)(st.bs.x >> 16);
+            const int p1 = (int)(int16_t)(st.bs.y & 0xffff) + (int)(int16_t)(st.bs.y >> 16);
+            _Float16* m = sm_[buf] + tok * 16;
+            m[s0] = (_Float16)(float)(p0 >> 6);
+            m[s0 + 1] = (_Float16)(float)(p1 >> 6);
+            m[8 + s0] = (_Float16)(float)(p0 & 63);
+            m[8 + s0 + 1] = (_Float16)(float)(p1 & 63);
+        }
         if (tid < 64) sd_[buf][tid] = st.d;
     };
-    /* the lane's weight bytes of one block: header and 4 x 16 B of qs */
-    struct Blk {
+    /* the lane's weight bytes of one block: Q4_K the header and 4 x 16 B of
+     * qs; Q6_K 4 x 16 B of ql, 2 x 16 B of qh, the 16 scales and d */
+    struct Blk4 {
         uint4 hdr;
         uint4 q[4];
     };
+    struct Blk6 {
+        v4i ql[4], qh[2], sc;
+        uint32_t d;
+    };
+    using Blk = typename std::conditional<WT == LG_Q4_K, Blk4, Blk6>::type;
     auto blk_load = [&](Blk& B, int b) __attribute__((always_inline)) {
-        const uint8_t* p = wr + (size_t)b * LG_BS_Q4_K;
-        B.hdr = *(const uint4*)p;
+        const uint8_t* p = wr + (size_t)b * BSZ;
+        if constexpr (WT == LG_Q4_K) {
+            B.hdr = *(const uint4*)p;
 #pragma unroll
-        for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 16 + 32 * c + 16 * h);
+            for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 16 + 32 * c + 16 * h);
+        } else {
+            /* 210-byte blocks: 2-byte aligned (unaligned dword loads) */
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                B.ql[2 * n] = lg_ld<v4i>(p + 64 * n + 16 * h);
+                B.ql[2 * n + 1] = lg_ld<v4i>(p + 64 * n + 32 + 16 * h);
+                B.qh[n] = lg_ld<v4i>(p + 128 + 32 * n + 16 * h);
+            }
+            B.sc = lg_ld<v4i>(p + 192);
+            B.d = lg_ld16(p + 208);
+        }
     };
 
     v16f acc[2];
     acc[0] = (v16f){};
     acc[1] = (v16f){};
 
+    auto compute6 = [&](int buf, const Blk6& cur) __attribute__((always_inline)) {
+        const float dw = lg_h2f((uint16_t)cur.d);
+        v16i Sh[2], Sl[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) Sh[t] = Sl[t] = (v16i){};
+        const int8_t* sa = sa_[buf] + j * PF2_AST + 16 * h;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            /* chunk s = values 128 n + 64 c + 32 e + (0..31): nibble c of
+             * ql[64 n + 32 e + ..], bits 2 (2c + e) of qh[32 n + ..] */
+            const int n = s >> 2, c = (s >> 1) & 1, e = s & 1, sb = 2 * s + h;
+            const v4i ql = cur.ql[2 * n + e], qh = cur.qh[n];
+            const int sc = (int)(int8_t)(cur.sc[sb >> 2] >> (8 * (sb & 3)));
+            const v2i16 sc2 = (v2i16)(short)sc, off2 = (v2i16)(short)(-32 * sc);
+            v4i bh, bl;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t q = (((uint32_t)ql[k] >> (4 * c)) & 0x0F0F0F0Fu) |
+                                   ((((uint32_t)qh[k] >> (2 * (2 * c + e))) & 0x03030303u) << 4);
+                /* values 0, 2 and 1, 3 in 16-bit halves: w = sc q - 32 sc,
+                 * then w_h = w >> 6 and w_l = w & 63 back to bytes */
+                const v2i16 we = lg_bits<v2i16>(q & 0x00FF00FFu) * sc2 + off2;
+                const v2i16 wo = lg_bits<v2i16>(__builtin_amdgcn_perm(0u, q, 0x0C030C01u)) * sc2 + off2;   /* bytes 1, 3 */
+                const uint32_t he = lg_bits<uint32_t>((v2i16)(we >> (short)6)),
+                               ho = lg_bits<uint32_t>((v2i16)(wo >> (short)6));
+                /* v_perm_b32 selector 0x06020400: bytes 0, 2 of the second
+                 * operand interleaved with bytes 0, 2 of the first */
+                bh[k] = (int)__builtin_amdgcn_perm(ho, he, 0x06020400u);
+                bl[k] = (int)(__builtin_amdgcn_perm(lg_bits<uint32_t>(wo), lg_bits<uint32_t>(we), 0x06020400u) & 0x3F3F3F3Fu);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint4 a = *(const uint4*)(sa + 32 * t * PF2_AST + 32 * s);
+                const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+                Sh[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bh, Sh[t], 0, 0, 0);
+                Sl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, Sl[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const v16i S = Sh[t] * 64 + Sl[t];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dx = *(const float4*)(sd_[buf] + 32 * t + 8 * g + 4 * h);
+                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * g + i;
+                    acc[t][r] = __builtin_fmaf(dw * dxs[i], (float)S[r], acc[t][r]);
+                }
+            }
+        }
+    };
     auto compute = [&](int buf, const Blk& cur) __attribute__((always_inline)) {
+      if constexpr (WT == LG_Q6_K) {
+        compute6(buf, cur);
+      } else {
         const uint4 h4 = cur.hdr;
         const uint32_t scq[2] = {h4.y & 0x3F3F3F3Fu, (h4.w & 0x0F0F0F0Fu) | ((h4.y >> 2) & 0x30303030u)};
         const uint32_t mn[2] = {h4.z & 0x3F3F3F3Fu, ((h4.w >> 4) & 0x0F0F0F0Fu) | ((h4.z >> 2) & 0x30303030u)};
@@ -526,6 +623,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
                 }
             }
         }
+      }
     };
 
     /* step i of this half: the token tile of block b0 + i + 2 loads into
@@ -589,6 +687,36 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
+/* LG_PF_GEMM16=1: the 16 x 16 product kernels for Q4_K and Q6_K rows */
+static bool pf_gemm16()
+{
+    static const bool k16 = [] {
+        const char* e = getenv("LG_PF_GEMM16");
+        return e && e[0] == '1';
+    }();
+    return k16;
+}
+
+/* the 32 x 32 product kernel (Q4_K, Q6_K): 128 rows x 64 tokens per
+ * workgroup; two K halves in one workgroup where the tiles alone would give
+ * one workgroup per CU or fewer (the 4096-row products at 512 tokens,
+ * att_out and down: Q4_K 68.0 -> 61.8 us on average; Q|K|V's 384 tiles ran
+ * faster unsplit, 48.7 against 55.2 us) */
+template <int WT>
+static int gemm_k32(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                    int accumulate, hipStream_t s)
+{
+    const int nrb = (rows + PF2_RB - 1) / PF2_RB + 7 & ~7;
+    const int ntl = (T + 63) / 64;
+    const bool ks2 = nrb * ntl <= 256 && cols >= 4 * 256;
+    const dim3 grid((unsigned)(nrb * ntl)), blk(ks2 ? 2 * PF2_NT : PF2_NT);
+#define PF2_LAUNCH(A, N) hipLaunchKernelGGL((k_pf_gemm_k32<WT, A, N>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo)
+    if (accumulate) { if (ks2) PF2_LAUNCH(1, 2); else PF2_LAUNCH(1, 1); }
+    else { if (ks2) PF2_LAUNCH(0, 2); else PF2_LAUNCH(0, 1); }
+#undef PF2_LAUNCH
+    return lg_check_launch("prefill gemm");
+}
+
 static int gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
                     int accumulate, hipStream_t s)
 {
@@ -597,26 +725,7 @@ static int gemm_q4k(const uint8_t* W, uint32_t rsz, int rows, int cols, const Pf
         lg_set_error("prefill gemm: bad arguments (rows %d, cols %d, T %d)", rows, cols, T);
         return LG_ERR_ARG;
     }
-    static const bool k16 = [] {
-        const char* e = getenv("LG_PF_GEMM16");
-        return e && e[0] == '1';
-    }();
-    if (!k16) {
-        /* the 32 x 32 product kernel: 128 rows x 64 tokens per workgroup;
-         * two K halves in one workgroup where the tiles alone would give one
-         * workgroup per CU or fewer (the 4096-row products at 512 tokens,
-         * att_out and down: 68.0 -> 61.8 us on average; Q|K|V's 384 tiles
-         * ran faster unsplit, 48.7 against 55.2 us) */
-        const int nrb = (rows + PF2_RB - 1) / PF2_RB + 7 & ~7;
-        const int ntl = (T + 63) / 64;
-        const bool ks2 = nrb * ntl <= 256 && cols >= 4 * 256;
-        const dim3 grid((unsigned)(nrb * ntl)), blk(ks2 ? 2 * PF2_NT : PF2_NT);
-#define PF2_LAUNCH(A, N) hipLaunchKernelGGL((k_pf_gemm_q4k32<A, N>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo)
-        if (accumulate) { if (ks2) PF2_LAUNCH(1, 2); else PF2_LAUNCH(1, 1); }
-        else { if (ks2) PF2_LAUNCH(0, 2); else PF2_LAUNCH(0, 1); }
-#undef PF2_LAUNCH
-        return lg_check_launch("prefill gemm");
-    }
+    if (!pf_gemm16()) return gemm_k32<LG_Q4_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     /* LG_PF_GEMM16=1: the 16 x 16 product kernel.  64-token tiles: 128
      * VGPRs, so up to four workgroups share a CU (at 128 tokens a workgroup
      * needs 220 and the 512-token up|gate GEMM ran 10% slower) */
@@ -1318,7 +1427,9 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
     case LG_Q2_K: return gemm_kq<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q3_K: return gemm_kq<LG_Q3_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q5_K: return gemm_kq<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
-    case LG_Q6_K: return gemm_kq<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q6_K:
+        if (!pf_gemm16()) return gemm_k32<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+        return gemm_kq<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q8_0: return gemm_b32<LG_Q8_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     default: return gemm_b32<LG_Q1_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     }
@@ -1353,8 +1464,6 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
  * P^T is the D layout of S^T (lane (g, q) holds keys 4g..4g+3), so it feeds
  * the second product without a transpose.  Only fp32 rounding differs from
  * the token-sequential step (sum orders, ~2^-22 per operand). */
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-
 template <int HD, int NREP, int SPLIT>
 __global__ __launch_bounds__(64 * NREP * SPLIT) void k_pf_attn_h(const float* __restrict__ qkv, int qstride, int n_embed,
                                                          int kv_dim, const uint16_t* __restrict__ kc,
