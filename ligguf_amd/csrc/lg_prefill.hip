@@ -386,6 +386,12 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(4))) void
  * 2^24 and M is exact.  Then out += d_a (d_w S - dmin_w M) per block in the
  * same fp32 operations as k_pf_gemm_q4k, so both give the same bits.
  *
+ * Q5_K rows (WT = LG_Q5_K): the Q4_K layout of scales and mins with a
+ * fifth bit per value from qh; w = sc q < 2^11 is formed in 16-bit halves
+ * and split w = 64 w_h + w_l (w_h <= 30, w_l <= 63), S = 64 S_h + S_l, and
+ * the mins term and the fp32 operations are Q4_K's (k_pf_gemm_kq's Q5_K
+ * dot gives the same bits).
+ *
  * Q6_K rows (WT = LG_Q6_K) on the same tile: lane l's 16 bytes of chunk s
  * (values 32s + 16 (l / 32) ..) are the whole of 16-value sub-block
  * 2s + l / 32, so the lane folds its scale into them: w = sc (q - 32) (sc
@@ -410,12 +416,14 @@ template <int WT, int ACC, int KS>
 __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_k32(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    static_assert(WT == LG_Q4_K || WT == LG_Q6_K, "Q4_K or Q6_K rows");
-    constexpr int BSZ = WT == LG_Q4_K ? LG_BS_Q4_K : LG_BS_Q6_K;
+    static_assert(WT == LG_Q4_K || WT == LG_Q5_K || WT == LG_Q6_K, "Q4_K, Q5_K or Q6_K rows");
+    /* Q4_K and Q5_K: 32-value sub-blocks with 6-bit scales and mins */
+    constexpr bool MINS = WT != LG_Q6_K;
+    constexpr int BSZ = WT == LG_Q4_K ? LG_BS_Q4_K : WT == LG_Q5_K ? LG_BS_Q5_K : LG_BS_Q6_K;
     constexpr int TT = 64;   /* tokens per workgroup: two 32-token tiles per wave */
     __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
-    /* per token: p_hi[8], p_lo[8] (Q4_K mins) */
-    constexpr int MST = WT == LG_Q4_K ? TT * 16 : 8;
+    /* per token: p_hi[8], p_lo[8] (the mins term) */
+    constexpr int MST = MINS ? TT * 16 : 8;
     __shared__ __attribute__((aligned(16))) _Float16 s_m[KS][2][MST];
     __shared__ __attribute__((aligned(16))) float s_d[KS][2][TT];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -450,7 +458,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             const int q = tid + PF2_NT * u, tok = min(t0 + (q >> 4), T - 1);
             st.a[u] = *(const v4i*)(x.qs + (size_t)tok * K + (size_t)b * 256 + (q & 15) * 16);
         }
-        if constexpr (WT == LG_Q4_K) {   /* the bsums feed the mins term */
+        if constexpr (MINS) {   /* the bsums feed the mins term */
             const int tb = min(t0 + (tid >> 2), T - 1);
             st.bs = *(const uint2*)(x.bs + ((size_t)tb * nb + b) * 16 + (tid & 3) * 4);
         }
@@ -464,7 +472,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         }
         const int tok = tid >> 2;
         (void)tok;
-        if constexpr (WT == LG_Q4_K) {
+        if constexpr (MINS) {
             const int s0 = 2 * (tid & 3);
             const int p0 = (int)(int16_t)(st.bs.x & 0xffff) + (int)(int16_t)(st.bs.x >> 16);
             const int p1 = (int)(int16_t)(st.bs.y & 0xffff) + (int)(int16_t)(st.bs.y >> 16);
@@ -482,17 +490,29 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         uint4 hdr;
         uint4 q[4];
     };
+    struct Blk5 {
+        uint4 hdr;
+        uint4 q[4];
+        v4i qh;
+    };
     struct Blk6 {
         v4i ql[4], qh[2], sc;
         uint32_t d;
     };
-    using Blk = typename std::conditional<WT == LG_Q4_K, Blk4, Blk6>::type;
+    using Blk = typename std::conditional<WT == LG_Q4_K, Blk4,
+                                          typename std::conditional<WT == LG_Q5_K, Blk5, Blk6>::type>::type;
     auto blk_load = [&](Blk& B, int b) __attribute__((always_inline)) {
         const uint8_t* p = wr + (size_t)b * BSZ;
         if constexpr (WT == LG_Q4_K) {
             B.hdr = *(const uint4*)p;
 #pragma unroll
             for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 16 + 32 * c + 16 * h);
+        } else if constexpr (WT == LG_Q5_K) {
+            /* 176-byte blocks: 16-byte aligned */
+            B.hdr = *(const uint4*)p;
+            B.qh = *(const v4i*)(p + 16 + 16 * h);
+#pragma unroll
+            for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 48 + 32 * c + 16 * h);
         } else {
             /* 210-byte blocks: 2-byte aligned (unaligned dword loads) */
 #pragma unroll
@@ -590,13 +610,31 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             for (int e = 0; e < 2; e++) {
                 const int s = 2 * c + e;
                 const uint32_t sc = (scq[s >> 2] >> (8 * (s & 3))) & 0x3Fu;
-                const v2u16 sh = (v2u16)(uint16_t)(sc >> 3), sl = (v2u16)(uint16_t)(sc & 7u);
                 v4i bh, bl;
+                if constexpr (WT == LG_Q4_K) {
+                    const v2u16 sh = (v2u16)(uint16_t)(sc >> 3), sl = (v2u16)(uint16_t)(sc & 7u);
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const uint32_t nib = e ? (qw[k] >> 4) & 0x0F0F0F0Fu : qw[k] & 0x0F0F0F0Fu;
-                    bh[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(nib) * sh);
-                    bl[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(nib) * sl);
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t nib = e ? (qw[k] >> 4) & 0x0F0F0F0Fu : qw[k] & 0x0F0F0F0Fu;
+                        bh[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(nib) * sh);
+                        bl[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(nib) * sl);
+                    }
+                } else {
+                    /* Q5_K: q = nibble e of qs | bit s of qh << 4 (0..31);
+                     * w = sc q < 2^11 in 16-bit halves, w = 64 w_h + w_l */
+                    const v2u16 sc2 = (v2u16)(uint16_t)sc;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t q = ((e ? qw[k] >> 4 : qw[k]) & 0x0F0F0F0Fu) |
+                                           ((((uint32_t)cur.qh[k] >> s) & 0x01010101u) << 4);
+                        const v2u16 we = lg_bits<v2u16>(q & 0x00FF00FFu) * sc2;
+                        const v2u16 wo = lg_bits<v2u16>(__builtin_amdgcn_perm(0u, q, 0x0C030C01u)) * sc2;
+                        const uint32_t he = lg_bits<uint32_t>((v2u16)(we >> (unsigned short)6)),
+                                       ho = lg_bits<uint32_t>((v2u16)(wo >> (unsigned short)6));
+                        bh[k] = (int)__builtin_amdgcn_perm(ho, he, 0x06020400u);
+                        bl[k] = (int)(__builtin_amdgcn_perm(lg_bits<uint32_t>(wo), lg_bits<uint32_t>(we), 0x06020400u) &
+                                      0x3F3F3F3Fu);
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
@@ -611,7 +649,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         for (int t = 0; t < 2; t++) {
             const v8h am = *(const v8h*)(sm_[buf] + (32 * t + j) * 16 + 8 * h);
             const v16f M = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, (v16f){}, 0, 0, 0);
-            const v16i S = Sh[t] * 8 + Sl[t];
+            const v16i S = Sh[t] * (WT == LG_Q4_K ? 8 : 64) + Sl[t];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const float4 dx = *(const float4*)(sd_[buf] + 32 * t + 8 * g + 4 * h);
@@ -687,7 +725,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-/* LG_PF_GEMM16=1: the 16 x 16 product kernels for Q4_K and Q6_K rows */
+/* LG_PF_GEMM16=1: the 16 x 16 product kernels for Q4_K, Q5_K and Q6_K rows */
 static bool pf_gemm16()
 {
     static const bool k16 = [] {
@@ -1426,7 +1464,9 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
     case LG_Q1_G: return gemm_q1g(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q2_K: return gemm_kq<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q3_K: return gemm_kq<LG_Q3_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
-    case LG_Q5_K: return gemm_kq<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q5_K:
+        if (!pf_gemm16()) return gemm_k32<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+        return gemm_kq<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q6_K:
         if (!pf_gemm16()) return gemm_k32<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
         return gemm_kq<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
