@@ -416,13 +416,16 @@ template <int WT, int ACC, int KS>
 __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_k32(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    static_assert(WT == LG_Q4_K || WT == LG_Q5_K || WT == LG_Q6_K, "Q4_K, Q5_K or Q6_K rows");
-    /* Q4_K and Q5_K: 32-value sub-blocks with 6-bit scales and mins */
-    constexpr bool MINS = WT != LG_Q6_K;
-    constexpr int BSZ = WT == LG_Q4_K ? LG_BS_Q4_K : WT == LG_Q5_K ? LG_BS_Q5_K : LG_BS_Q6_K;
+    static_assert(WT == LG_Q2_K || WT == LG_Q3_K || WT == LG_Q4_K || WT == LG_Q5_K || WT == LG_Q6_K, "K-quant rows");
+    /* the mins term: Q4_K and Q5_K (32-value sub-blocks: pair sums of the
+     * bsums, split 64 p_hi + p_lo) or Q2_K (16-value sub-blocks: the bsums) */
+    constexpr int MK = (WT == LG_Q4_K || WT == LG_Q5_K) ? 1 : WT == LG_Q2_K ? 2 : 0;
+    constexpr bool MINS = MK != 0;
+    constexpr int BSZ = WT == LG_Q2_K ? LG_BS_Q2_K : WT == LG_Q3_K ? LG_BS_Q3_K : WT == LG_Q4_K ? LG_BS_Q4_K
+                      : WT == LG_Q5_K ? LG_BS_Q5_K : LG_BS_Q6_K;
     constexpr int TT = 64;   /* tokens per workgroup: two 32-token tiles per wave */
     __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
-    /* per token: p_hi[8], p_lo[8] (the mins term) */
+    /* per token: p_hi[8], p_lo[8] or the 16 bsums (the mins term) */
     constexpr int MST = MINS ? TT * 16 : 8;
     __shared__ __attribute__((aligned(16))) _Float16 s_m[KS][2][MST];
     __shared__ __attribute__((aligned(16))) float s_d[KS][2][TT];
@@ -472,7 +475,11 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         }
         const int tok = tid >> 2;
         (void)tok;
-        if constexpr (MINS) {
+        if constexpr (MK == 2) {
+            const v4h m = {(_Float16)(float)(int16_t)(st.bs.x & 0xffff), (_Float16)(float)(int16_t)(st.bs.x >> 16),
+                           (_Float16)(float)(int16_t)(st.bs.y & 0xffff), (_Float16)(float)(int16_t)(st.bs.y >> 16)};
+            *(v4h*)(sm_[buf] + tok * 16 + 4 * (tid & 3)) = m;
+        } else if constexpr (MINS) {
             const int s0 = 2 * (tid & 3);
             const int p0 = (int)(int16_t)(st.bs.x & 0xffff) + (int)(int16_t)(st.bs.x >> 16);
             const int p1 = (int)(int16_t)(st.bs.y & 0xffff) + (int)(int16_t)(st.bs.y >> 16);
@@ -499,14 +506,41 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         v4i ql[4], qh[2], sc;
         uint32_t d;
     };
-    using Blk = typename std::conditional<WT == LG_Q4_K, Blk4,
-                                          typename std::conditional<WT == LG_Q5_K, Blk5, Blk6>::type>::type;
+    struct Blk2 {
+        v4i qs[2], sc;
+        uint32_t dd;
+    };
+    struct Blk3 {
+        v4i hm, qs[2];
+        uint32_t s0, s1, s2, d;
+    };
+    using Blk = typename std::conditional<
+        WT == LG_Q4_K, Blk4,
+        typename std::conditional<
+            WT == LG_Q5_K, Blk5,
+            typename std::conditional<WT == LG_Q6_K, Blk6,
+                                      typename std::conditional<WT == LG_Q2_K, Blk2, Blk3>::type>::type>::type>::type;
     auto blk_load = [&](Blk& B, int b) __attribute__((always_inline)) {
         const uint8_t* p = wr + (size_t)b * BSZ;
         if constexpr (WT == LG_Q4_K) {
             B.hdr = *(const uint4*)p;
 #pragma unroll
             for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 16 + 32 * c + 16 * h);
+        } else if constexpr (WT == LG_Q2_K) {
+            /* 84-byte blocks: scales[16], qs[64], d, dmin */
+            B.sc = lg_ld<v4i>(p);
+            B.qs[0] = lg_ld<v4i>(p + 16 + 16 * h);
+            B.qs[1] = lg_ld<v4i>(p + 48 + 16 * h);
+            B.dd = lg_ld<uint32_t>(p + 80);
+        } else if constexpr (WT == LG_Q3_K) {
+            /* 110-byte blocks: hmask[32], qs[64], scales[12], d */
+            B.hm = lg_ld<v4i>(p + 16 * h);
+            B.qs[0] = lg_ld<v4i>(p + 32 + 16 * h);
+            B.qs[1] = lg_ld<v4i>(p + 64 + 16 * h);
+            B.s0 = lg_ld<uint32_t>(p + 96);
+            B.s1 = lg_ld<uint32_t>(p + 100);
+            B.s2 = lg_ld<uint32_t>(p + 104);
+            B.d = lg_ld16(p + 108);
         } else if constexpr (WT == LG_Q5_K) {
             /* 176-byte blocks: 16-byte aligned */
             B.hdr = *(const uint4*)p;
@@ -583,9 +617,107 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             }
         }
     };
+    /* Q2_K: w = sc q <= 45 (bytes, two to a 16-bit multiply), one product
+     * per chunk; the mins term sum_i m_i bsums_i is one
+     * v_mfma_f32_32x32x16_f16 per tile (|bsum| <= 2048, m <= 15: exact) */
+    auto compute2 = [&](int buf, const Blk2& cur) __attribute__((always_inline)) {
+        const float dw = lg_h2f((uint16_t)(cur.dd & 0xffffu)), dmw = lg_h2f((uint16_t)(cur.dd >> 16));
+        v8h bm;   /* mins of sub-blocks 8h .. 8h + 7 */
+#pragma unroll
+        for (int k = 0; k < 8; k++) bm[k] = (_Float16)(float)(((uint32_t)cur.sc[2 * h + (k >> 2)] >> (8 * (k & 3) + 4)) & 15u);
+        v16i S[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) S[t] = (v16i){};
+        const int8_t* sa = sa_[buf] + j * PF2_AST + 16 * h;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            /* chunk s = values 128 n + 32 jj + (0..31): bits 2 jj of qs[32 n + ..] */
+            const int n = s >> 2, jj = s & 3, sb = 2 * s + h;
+            const v2u16 sc2 = (v2u16)(uint16_t)(((uint32_t)cur.sc[sb >> 2] >> (8 * (sb & 3))) & 15u);
+            v4i bw;
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                bw[k] = (int)lg_bits<uint32_t>(lg_bits<v2u16>(((uint32_t)cur.qs[n][k] >> (2 * jj)) & 0x03030303u) * sc2);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint4 a = *(const uint4*)(sa + 32 * t * PF2_AST + 32 * s);
+                const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+                S[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bw, S[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const v8h am = *(const v8h*)(sm_[buf] + (32 * t + j) * 16 + 8 * h);
+            const v16f M = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, (v16f){}, 0, 0, 0);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dx = *(const float4*)(sd_[buf] + 32 * t + 8 * g + 4 * h);
+                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * g + i;
+                    acc[t][r] = __builtin_fmaf(dxs[i], lg_fma2(dw, (float)S[t][r], -dmw, M[r]), acc[t][r]);
+                }
+            }
+        }
+    };
+    /* Q3_K: u = 2 bits of qs | the hmask bit << 2, value u - 4, scale sc =
+     * 6 bits - 32; w = -sc (u - 4) in [-128, 124] fits a byte (sc (u - 4)
+     * reaches 128), one product per chunk and S = -S' */
+    auto compute3 = [&](int buf, const Blk3& cur) __attribute__((always_inline)) {
+        const float dw = lg_h2f((uint16_t)cur.d);
+        v16i S[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) S[t] = (v16i){};
+        const int8_t* sa = sa_[buf] + j * PF2_AST + 16 * h;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int n = s >> 2, jj = s & 3, sb = 2 * s + h;
+            /* scale sb: low nibble of byte sb (sb < 8) or high nibble of
+             * byte sb - 8 of the first 8, two high bits from byte 8 + sb % 4
+             * at 2 (sb / 4) */
+            const uint32_t lw = (sb & 7) < 4 ? cur.s0 : cur.s1;
+            const int lo = (int)((lw >> (8 * (sb & 3) + (sb < 8 ? 0 : 4))) & 15u);
+            const int hi = (int)((cur.s2 >> (8 * (sb & 3) + 2 * (sb >> 2))) & 3u);
+            const int sc = (lo | (hi << 4)) - 32;
+            const v2i16 ws2 = (v2i16)(short)(-sc), off2 = (v2i16)(short)(4 * sc);
+            v4i bw;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t u = (((uint32_t)cur.qs[n][k] >> (2 * jj)) & 0x03030303u) |
+                                   ((((uint32_t)cur.hm[k] >> (4 * n + jj)) & 0x01010101u) << 2);
+                const v2i16 we = lg_bits<v2i16>(u & 0x00FF00FFu) * ws2 + off2;
+                const v2i16 wo = lg_bits<v2i16>(__builtin_amdgcn_perm(0u, u, 0x0C030C01u)) * ws2 + off2;
+                bw[k] = (int)__builtin_amdgcn_perm(lg_bits<uint32_t>(wo), lg_bits<uint32_t>(we), 0x06020400u);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint4 a = *(const uint4*)(sa + 32 * t * PF2_AST + 32 * s);
+                const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+                S[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bw, S[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dx = *(const float4*)(sd_[buf] + 32 * t + 8 * g + 4 * h);
+                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * g + i;
+                    acc[t][r] = __builtin_fmaf(dw * dxs[i], (float)(-S[t][r]), acc[t][r]);
+                }
+            }
+        }
+    };
     auto compute = [&](int buf, const Blk& cur) __attribute__((always_inline)) {
       if constexpr (WT == LG_Q6_K) {
         compute6(buf, cur);
+      } else if constexpr (WT == LG_Q2_K) {
+        compute2(buf, cur);
+      } else if constexpr (WT == LG_Q3_K) {
+        compute3(buf, cur);
       } else {
         const uint4 h4 = cur.hdr;
         const uint32_t scq[2] = {h4.y & 0x3F3F3F3Fu, (h4.w & 0x0F0F0F0Fu) | ((h4.y >> 2) & 0x30303030u)};
@@ -725,7 +857,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-/* LG_PF_GEMM16=1: the 16 x 16 product kernels for Q4_K, Q5_K and Q6_K rows */
+/* LG_PF_GEMM16=1: the 16 x 16 product kernels for the K-quant rows */
 static bool pf_gemm16()
 {
     static const bool k16 = [] {
@@ -1462,8 +1594,12 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
     switch (wtype) {
     case LG_Q4_K: return gemm_q4k(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q1_G: return gemm_q1g(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
-    case LG_Q2_K: return gemm_kq<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
-    case LG_Q3_K: return gemm_kq<LG_Q3_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q2_K:
+        if (!pf_gemm16()) return gemm_k32<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+        return gemm_kq<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q3_K:
+        if (!pf_gemm16()) return gemm_k32<LG_Q3_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+        return gemm_kq<LG_Q3_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q5_K:
         if (!pf_gemm16()) return gemm_k32<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
         return gemm_kq<LG_Q5_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
