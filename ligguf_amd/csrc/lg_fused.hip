@@ -592,6 +592,7 @@ const FusedVariant* lg_fused_part_0(int* n)
     static const FusedVariant v[] = {
         FV(LG_Q4_K, LG_Q6_K, 128, 4), FV(LG_Q4_K, LG_Q4_K, 128, 4), FV(LG_Q4_K, LG_Q8_0, 128, 4),
         FV(LG_Q5_K, LG_Q6_K, 128, 4), FV(LG_Q6_K, LG_Q6_K, 128, 4), FV(LG_Q8_0, LG_Q8_0, 128, 4),
+        FV(LG_F16, LG_Q6_K, 128, 4),
     };
     *n = (int)(sizeof(v) / sizeof(v[0]));
     return v;
