@@ -958,6 +958,19 @@ static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
         if (D.ug_fused) L.ug = pf_mat(D.ug);
         else { L.up = pf_mat(D.up); L.gate = pf_mat(D.gate); }
         L.down = pf_mat(D.down);
+        if (ctx->pk_ok && ctx->pk.layers_rep && l < (int)ctx->pk_layers.size()) {
+            /* uniform Q8_0 / Q1_0 layers: the regrouped copies the fused step
+             * reads (aligned 16-byte loads, the same values) */
+            const PkLayer& K = ctx->pk_layers[l];
+            auto rep = [](PfMat& M, const uint8_t* w) {
+                if (M.type == LG_Q8_0) { M.w = w; M.type = LG_Q8_0_R; }
+                else if (M.type == LG_Q1_0) { M.w = w; M.type = LG_Q1_0_R; }
+            };
+            if (D.qkv_fused) rep(L.qkv, K.qkv);
+            rep(L.ao, K.ao);
+            if (D.ug_fused) rep(L.ug, K.ug);
+            rep(L.down, K.down);
+        }
         L.att_norm = D.att_norm; L.ffn_norm = D.ffn_norm; L.q_norm = D.q_norm; L.k_norm = D.k_norm;
     }
     PfModel& M = ctx->pf_model;

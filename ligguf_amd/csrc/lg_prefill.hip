@@ -857,7 +857,8 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 /* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
-/* LG_PF_GEMM16=1: the 16 x 16 product kernels for the K-quant rows */
+/* LG_PF_GEMM16=1: the 16 x 16 product kernels for the K-quant, Q8_0 and
+ * Q1_0 rows */
 static bool pf_gemm16()
 {
     static const bool k16 = [] {
@@ -1426,11 +1427,32 @@ static int gemm_kq(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ
  * tile's quants in groups of 4 blocks (128 values) in LDS with their
  * scales, double-buffered.  The width need only be a multiple of 32: a
  * last group of fewer than 4 blocks stages clamped bytes it never uses. */
+/* where block `blk` of a row keeps its d and its quants (Q8_0) or sign
+ * bits (Q1_0): GGUF blocks, or the regrouped rows of the fused decode step
+ * (LG_Q8_0_R / LG_Q1_0_R: per run of 8 blocks, the 8 blocks' quants or
+ * bits, then their 8 d) */
+template <int WT>
+struct PfB32 {
+    static constexpr bool Q8 = WT == LG_Q8_0 || WT == LG_Q8_0_R;
+    static constexpr bool REP = WT == LG_Q8_0_R || WT == LG_Q1_0_R;
+    static constexpr int BSZ = Q8 ? LG_BS_Q8_0 : LG_BS_Q1_0;
+    static constexpr int QB = Q8 ? 32 : 4;   /* quant / bit bytes per block */
+    static __device__ __forceinline__ const uint8_t* d(const uint8_t* row, int blk)
+    {
+        return REP ? row + (size_t)(blk >> 3) * 8 * BSZ + 8 * QB + 2 * (blk & 7) : row + (size_t)blk * BSZ;
+    }
+    static __device__ __forceinline__ const uint8_t* q(const uint8_t* row, int blk)
+    {
+        return REP ? row + (size_t)(blk >> 3) * 8 * BSZ + QB * (blk & 7) : row + (size_t)blk * BSZ + 2;
+    }
+};
+
 template <int WT, int ACC>
 __global__ __launch_bounds__(512) void k_pf_gemm_b32(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    constexpr int MI = 4, BSZ = WT == LG_Q8_0 ? LG_BS_Q8_0 : LG_BS_Q1_0;
+    using B32 = PfB32<WT>;
+    constexpr int MI = 4;
     __shared__ __attribute__((aligned(16))) int8_t s_a[2][64 * PF1_AST];
     __shared__ __attribute__((aligned(16))) float s_d[2][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1465,12 +1487,12 @@ __global__ __launch_bounds__(512) void k_pf_gemm_b32(
     auto blk_load = [&](Blk& B, int gi) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint8_t* p = wr + (size_t)min(4 * gi + j, nbk - 1) * BSZ;
-            B.d[j] = lg_ld16(p);
-            if constexpr (WT == LG_Q8_0) {
-                B.q[j] = lg_ld<uint2>(p + 2 + 8 * g);
+            const int bk = min(4 * gi + j, nbk - 1);
+            B.d[j] = lg_ld16(B32::d(wr, bk));
+            if constexpr (B32::Q8) {
+                B.q[j] = lg_ld<uint2>(B32::q(wr, bk) + 8 * g);
             } else {
-                const uint32_t b8 = p[2 + g];
+                const uint32_t b8 = B32::q(wr, bk)[g];
                 /* bit i -> byte i: +1 where set, -1 (0xFF) where clear */
                 B.q[j] = make_uint2(0xFFFFFFFFu ^ ((uint32_t)bits4_to_bytes(b8 & 15u) * 0xFEu),
                                     0xFFFFFFFFu ^ ((uint32_t)bits4_to_bytes(b8 >> 4) * 0xFEu));
@@ -1531,10 +1553,195 @@ __global__ __launch_bounds__(512) void k_pf_gemm_b32(
     }
 }
 
+/* The same products on the 32 x 32 forms (k_pf_gemm_k32's tile: 128 rows
+ * x 64 tokens per workgroup of 4 waves, a wave 32 rows x two 32-token C
+ * tiles, the token tile of 8 blocks (256 values) a step staged two steps
+ * ahead, K in two halves where the tiles alone would leave one workgroup
+ * per CU).  Per 32-value block: the integer sum is one
+ * v_mfma_i32_32x32x32_i8 (lane l: row l % 32's bytes 16 (l / 32) .. +15 of
+ * the block -- Q8_0 quants, or Q1_0 bits as +-1 bytes -- against the
+ * token's), and the scale d_w d_a of every (token, row) pair of the tile is
+ * one v_mfma_f32_32x32x16_f16 whose only nonzero K term is d_a (the
+ * token's, fp16 as quantized) times d_w (the row's fp16): exact, and laid
+ * out as the sums are, so each pair takes one convert and one fma, with no
+ * per-token scale read from LDS.  out += (d_w d_a) s as k_pf_gemm_b32
+ * (the same bits where K is not split).  Widths any multiple of 32: blocks
+ * past the last of a step are not computed (their staged bytes are clamped
+ * copies). */
+template <int WT, int ACC, int KS>
+__global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_b32x(
+    const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
+{
+    using B32 = PfB32<WT>;
+    constexpr int TT = 64;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
+    __shared__ __attribute__((aligned(16))) _Float16 s_d[KS][2][8][TT];   /* d_a per block of the step, per token */
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kh = wave >> 2, tid = threadIdx.x & (PF2_NT - 1);
+    const int h = lane >> 5, j = lane & 31;
+    const int nbk = K >> 5, nst = (nbk + 7) >> 3;
+    const int ns0 = KS == 2 ? (nst + 1) / 2 : nst;
+    const int s0 = kh * ns0, nsh = kh ? nst - ns0 : ns0, L = ns0;
+    const int nt = (T + TT - 1) / TT;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int rb = (slot / nt) * 8 + xcd;
+    if (rb * PF2_RB >= R) return;   /* padding of the row blocks to a multiple of 8 (whole workgroup) */
+    const int t0 = (slot % nt) * TT;
+    const int row = rb * PF2_RB + (wave & 3) * 32 + j;
+    const uint8_t* wr = W + (size_t)min(row, R - 1) * rsz;
+    int8_t(*sa_)[TT * PF2_AST] = s_a[kh];
+    _Float16(*sd_)[8][TT] = s_d[kh];
+
+    /* staging, per step: quant piece q = tid + 256 u (token q / 16, 16-byte
+     * piece q % 16 of the step's 256 values, clamped to the row's end), and
+     * d_a of blocks tid / 64 and tid / 64 + 4 of token tid % 64 */
+    struct Stg {
+        v4i a[4];
+        float d[2];
+    };
+    auto stage_load = [&](Stg& st, int sp) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int q = tid + PF2_NT * u, tok = min(t0 + (q >> 4), T - 1);
+            st.a[u] = *(const v4i*)(x.qs + (size_t)tok * K + min(sp * 256 + (q & 15) * 16, K - 16));
+        }
+        const int tok = min(t0 + (tid & 63), T - 1);
+#pragma unroll
+        for (int e = 0; e < 2; e++) st.d[e] = x.d[(size_t)min(8 * sp + (tid >> 6) + 4 * e, nbk - 1) * x.tld + tok];
+    };
+    auto stage_store = [&](const Stg& st, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int q = tid + PF2_NT * u;
+            *(v4i*)(sa_[buf] + (q >> 4) * PF2_AST + (q & 15) * 16) = st.a[u];
+        }
+#pragma unroll
+        for (int e = 0; e < 2; e++) sd_[buf][(tid >> 6) + 4 * e][tid & 63] = (_Float16)st.d[e];
+    };
+    /* the lane's bytes of the step's 8 blocks and their d_w */
+    struct Blk {
+        v4i q[8];
+        uint32_t d[4];
+    };
+    auto blk_load = [&](Blk& B, int sp) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int bk = min(8 * sp + e, nbk - 1);
+            if constexpr (B32::Q8) {
+                B.q[e] = lg_ld<v4i>(B32::q(wr, bk) + 16 * h);   /* 16-byte aligned when regrouped */
+            } else {
+                /* bits 16h .. 16h + 15: bit i -> byte i, +1 where set, -1 where clear */
+                const uint32_t b16 = lg_ld16(B32::q(wr, bk) + 2 * h);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    B.q[e][k] = (int)(0xFFFFFFFFu ^ ((uint32_t)bits4_to_bytes((b16 >> (4 * k)) & 15u) * 0xFEu));
+            }
+            if constexpr (!B32::REP) {
+                const uint32_t dh = lg_ld16(B32::d(wr, bk));
+                B.d[e >> 1] = (e & 1) ? (B.d[e >> 1] | (dh << 16)) : dh;
+            }
+        }
+        if constexpr (B32::REP) {
+            /* the step is one regrouped run: its 8 d in one load */
+            const v4i dd = *(const v4i*)B32::d(wr, 8 * sp);
+#pragma unroll
+            for (int k = 0; k < 4; k++) B.d[k] = (uint32_t)dd[k];
+        }
+    };
+
+    v16f acc[2];
+    acc[0] = (v16f){};
+    acc[1] = (v16f){};
+
+    auto compute = [&](int buf, const Blk& cur, int sp) __attribute__((always_inline)) {
+        const int8_t* sa = sa_[buf] + j * PF2_AST + 16 * h;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (8 * sp + e >= nbk) break;   /* past the last block (uniform) */
+            /* scale operands: K term 0 only (lanes 0..31) */
+            v8h bd = (v8h){};
+            bd[0] = h ? (_Float16)0.0f : __builtin_bit_cast(_Float16, (uint16_t)(cur.d[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint4 a = *(const uint4*)(sa + 32 * t * PF2_AST + 32 * e);
+                const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+                const v16i is = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, cur.q[e], (v16i){}, 0, 0, 0);
+                v8h ad = (v8h){};
+                ad[0] = h ? (_Float16)0.0f : sd_[buf][e][32 * t + j];
+                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ad, bd, (v16f){}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[t][r] = __builtin_fmaf(sc[r], (float)is[r], acc[t][r]);
+            }
+        }
+    };
+
+    auto stp = [&](int i) { return s0 + min(i, nsh - 1); };
+    Blk cur, nxt;
+    Stg st0, st1;
+    stage_load(st0, stp(0));
+    stage_load(st1, stp(1));
+    blk_load(cur, stp(0));
+    stage_store(st0, 0);
+    __syncthreads();
+#define PF3_STEP(ii, ST_LD, ST_ST)                           \
+    do {                                                     \
+        stage_load(ST_LD, stp((ii) + 2));                    \
+        blk_load(nxt, stp((ii) + 1));                        \
+        if ((ii) < nsh) compute((ii) & 1, cur, s0 + (ii));   \
+        stage_store(ST_ST, ((ii) + 1) & 1);                  \
+        cur = nxt;                                           \
+        __syncthreads();                                     \
+    } while (0)
+    for (int i = 0; i < L; i += 2) {
+        PF3_STEP(i, st0, st1);
+        PF3_STEP(i + 1, st1, st0);
+    }
+#undef PF3_STEP
+    if constexpr (KS == 2) {
+        float* red = (float*)s_a[1];
+        if (kh == 1) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) red[(t * 16 + r) * (PF2_NT) + tid] = acc[t][r];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][r] = acc[t][r] + red[(t * 16 + r) * (PF2_NT) + tid];
+    }
+    if (row < R) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tok = t0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (tok < T) {
+                    float* o = out + (size_t)tok * ldo + row;
+                    *o = ACC ? *o + acc[t][r] : acc[t][r];
+                }
+            }
+        }
+    }
+}
+
 template <int WT>
 static int gemm_b32(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
                     int accumulate, hipStream_t s)
 {
+    if (!pf_gemm16()) {
+        const int nrb = (rows + PF2_RB - 1) / PF2_RB + 7 & ~7;
+        const int ntl = (T + 63) / 64;
+        const bool ks2 = nrb * ntl <= 256 && cols >= 4 * 256;
+        const dim3 grid((unsigned)(nrb * ntl)), blk(ks2 ? 2 * PF2_NT : PF2_NT);
+#define PF3_LAUNCH(A, N) hipLaunchKernelGGL((k_pf_gemm_b32x<WT, A, N>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo)
+        if (accumulate) { if (ks2) PF3_LAUNCH(1, 2); else PF3_LAUNCH(1, 1); }
+        else { if (ks2) PF3_LAUNCH(0, 2); else PF3_LAUNCH(0, 1); }
+#undef PF3_LAUNCH
+        return lg_check_launch("prefill gemm (32-value blocks)");
+    }
     const int nrb8 = (rows + 127) / 128 + 7 & ~7;
     const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
     if (accumulate) hipLaunchKernelGGL((k_pf_gemm_b32<WT, 1>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
@@ -1546,7 +1753,7 @@ int lg_prefill_act_type(int wtype)
 {
     switch (wtype) {
     case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: return LG_Q8_K;
-    case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: return LG_Q8_0;
+    case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: case LG_Q8_0_R: case LG_Q1_0_R: return LG_Q8_0;
     case LG_F32: case LG_F16: return LG_F32;
     default: return -1;
     }
@@ -1562,6 +1769,9 @@ static int64_t pf_row_bytes(int wtype, int cols)
     case LG_Q6_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q6_K;
     case LG_Q8_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q8_0;
     case LG_Q1_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q1_0;
+    /* regrouped rows: whole runs of 8 blocks */
+    case LG_Q8_0_R: return cols % 256 ? -1 : (int64_t)cols / 32 * LG_BS_Q8_0;
+    case LG_Q1_0_R: return cols % 256 ? -1 : (int64_t)cols / 32 * LG_BS_Q1_0;
     case LG_Q1_G: return cols % 256 ? -1 : (int64_t)cols / 128 * LG_BS_Q1_G;   /* the Q1_G GEMM steps 256 values */
     case LG_F32: return cols % 32 ? -1 : (int64_t)cols * 4;
     case LG_F16: return cols % 32 ? -1 : (int64_t)cols * 2;
@@ -1607,6 +1817,8 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
         if (!pf_gemm16()) return gemm_k32<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
         return gemm_kq<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q8_0: return gemm_b32<LG_Q8_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q8_0_R: return gemm_b32<LG_Q8_0_R>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q1_0_R: return gemm_b32<LG_Q1_0_R>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     default: return gemm_b32<LG_Q1_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     }
 }

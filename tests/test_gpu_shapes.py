@@ -161,19 +161,25 @@ def test_attention_past_the_short_split(shape_model, oracle, want_pos):
 
 
 def test_regrouped_copies_equal_gguf_rows(shape_model, monkeypatch):
-    """Where the fused step reads regrouped copies (Q8_0, Q6_K, Q1_G, Q3_K
-    matrices in whole 8-block groups), LG_NO_REGROUP=1 reads the GGUF rows:
+    """Where the fused step reads regrouped copies (Q8_0, Q6_K, Q1_G, Q3_K,
+    Q1_0 matrices in whole 8-block groups) -- and the batched prefill those
+    of uniform Q8_0 / Q1_0 layers --, LG_NO_REGROUP=1 reads the GGUF rows:
     the same logits bit for bit."""
     hm, eng = shape_model
     toks = np.random.default_rng(17).integers(1, hm.cfg.vocab, 3)
+    prompt = np.random.default_rng(18).integers(1, hm.cfg.vocab, 40)
     eng.set_path(PATH_FUSED)
     a = [eng.decode(int(t), i) for i, t in enumerate(toks)]
+    eng.set_prefill_path(PREFILL_AUTO)
+    pa = eng.prefill(prompt, 0)
     monkeypatch.setenv("LG_NO_REGROUP", "1")
     other = Engine(0)
     try:
         other.load(hm)
         other.set_path(PATH_FUSED)
         b = [other.decode(int(t), i) for i, t in enumerate(toks)]
+        pb = other.prefill(prompt, 0)
     finally:
         other.close()
     assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
+    assert np.array_equal(pa.view(np.uint32), pb.view(np.uint32))
