@@ -958,18 +958,25 @@ static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
         if (D.ug_fused) L.ug = pf_mat(D.ug);
         else { L.up = pf_mat(D.up); L.gate = pf_mat(D.gate); }
         L.down = pf_mat(D.down);
-        if (ctx->pk_ok && ctx->pk.layers_rep && l < (int)ctx->pk_layers.size()) {
-            /* uniform Q8_0 / Q1_0 layers: the regrouped copies the fused step
-             * reads (aligned 16-byte loads, the same values) */
+        if (ctx->pk_ok && l < (int)ctx->pk_layers.size()) {
+            /* matrices the fused step reads from regrouped copies (uniform
+             * Q8_0 / Q1_0 / Q6_K layers, a mixed layer's Q6_K V and down):
+             * the batched GEMMs read those too (aligned 16-byte loads, the
+             * same values) */
             const PkLayer& K = ctx->pk_layers[l];
-            auto rep = [](PfMat& M, const uint8_t* w) {
-                if (M.type == LG_Q8_0) { M.w = w; M.type = LG_Q8_0_R; }
-                else if (M.type == LG_Q1_0) { M.w = w; M.type = LG_Q1_0_R; }
+            const bool q6r = !lg_prefill_gemm16();   /* the 16 x 16 Q6_K kernel reads GGUF rows only */
+            auto rep = [&](PfMat& M, const uint8_t* w, int t) {
+                if ((M.type == LG_Q8_0 && t == LG_Q8_0_R) || (M.type == LG_Q1_0 && t == LG_Q1_0_R) ||
+                    (q6r && M.type == LG_Q6_K && t == LG_Q6_K_R)) {
+                    M.w = w;
+                    M.type = t;
+                }
             };
-            if (D.qkv_fused) rep(L.qkv, K.qkv);
-            rep(L.ao, K.ao);
-            if (D.ug_fused) rep(L.ug, K.ug);
-            rep(L.down, K.down);
+            if (D.qkv_fused) rep(L.qkv, K.qkv, K.qkv_t);
+            else if (D.qk_fused && K.v) rep(L.v, K.v, K.v_t);
+            rep(L.ao, K.ao, K.ao_t);
+            if (D.ug_fused) rep(L.ug, K.ug, K.ug_t);
+            rep(L.down, K.down, K.down_t);
         }
         L.att_norm = D.att_norm; L.ffn_norm = D.ffn_norm; L.q_norm = D.q_norm; L.k_norm = D.k_norm;
     }

@@ -416,13 +416,18 @@ template <int WT, int ACC, int KS>
 __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_k32(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    static_assert(WT == LG_Q2_K || WT == LG_Q3_K || WT == LG_Q4_K || WT == LG_Q5_K || WT == LG_Q6_K, "K-quant rows");
+    static_assert(WT == LG_Q2_K || WT == LG_Q3_K || WT == LG_Q4_K || WT == LG_Q5_K || WT == LG_Q6_K || WT == LG_Q6_K_R,
+                  "K-quant rows");
+    /* LG_Q6_K_R: the fused decode step's regrouped Q6_K rows (per run of 8
+     * blocks: their ql, qh, scales, d), the same values at aligned offsets */
+    constexpr bool Q6R = WT == LG_Q6_K_R;
     /* the mins term: Q4_K and Q5_K (32-value sub-blocks: pair sums of the
      * bsums, split 64 p_hi + p_lo) or Q2_K (16-value sub-blocks: the bsums) */
     constexpr int MK = (WT == LG_Q4_K || WT == LG_Q5_K) ? 1 : WT == LG_Q2_K ? 2 : 0;
     constexpr bool MINS = MK != 0;
     constexpr int BSZ = WT == LG_Q2_K ? LG_BS_Q2_K : WT == LG_Q3_K ? LG_BS_Q3_K : WT == LG_Q4_K ? LG_BS_Q4_K
                       : WT == LG_Q5_K ? LG_BS_Q5_K : LG_BS_Q6_K;
+    (void)Q6R;
     constexpr int TT = 64;   /* tokens per workgroup: two 32-token tiles per wave */
     __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
     /* per token: p_hi[8], p_lo[8] or the 16 bsums (the mins term) */
@@ -518,7 +523,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         WT == LG_Q4_K, Blk4,
         typename std::conditional<
             WT == LG_Q5_K, Blk5,
-            typename std::conditional<WT == LG_Q6_K, Blk6,
+            typename std::conditional<WT == LG_Q6_K || WT == LG_Q6_K_R, Blk6,
                                       typename std::conditional<WT == LG_Q2_K, Blk2, Blk3>::type>::type>::type>::type;
     auto blk_load = [&](Blk& B, int b) __attribute__((always_inline)) {
         const uint8_t* p = wr + (size_t)b * BSZ;
@@ -547,6 +552,17 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             B.qh = *(const v4i*)(p + 16 + 16 * h);
 #pragma unroll
             for (int c = 0; c < 4; c++) B.q[c] = *(const uint4*)(p + 48 + 32 * c + 16 * h);
+        } else if constexpr (WT == LG_Q6_K_R) {
+            const uint8_t* g = wr + (size_t)(b >> 3) * 8 * LG_BS_Q6_K;
+            const int e = b & 7;
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                B.ql[2 * n] = *(const v4i*)(g + 128 * e + 64 * n + 16 * h);
+                B.ql[2 * n + 1] = *(const v4i*)(g + 128 * e + 64 * n + 32 + 16 * h);
+                B.qh[n] = *(const v4i*)(g + 1024 + 64 * e + 32 * n + 16 * h);
+            }
+            B.sc = *(const v4i*)(g + 1536 + 16 * e);
+            B.d = lg_ld16(g + 1664 + 2 * e);
         } else {
             /* 210-byte blocks: 2-byte aligned (unaligned dword loads) */
 #pragma unroll
@@ -712,7 +728,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         }
     };
     auto compute = [&](int buf, const Blk& cur) __attribute__((always_inline)) {
-      if constexpr (WT == LG_Q6_K) {
+      if constexpr (WT == LG_Q6_K || WT == LG_Q6_K_R) {
         compute6(buf, cur);
       } else if constexpr (WT == LG_Q2_K) {
         compute2(buf, cur);
@@ -867,6 +883,8 @@ static bool pf_gemm16()
     }();
     return k16;
 }
+
+bool lg_prefill_gemm16() { return pf_gemm16(); }
 
 /* the 32 x 32 product kernel (Q4_K, Q6_K): 128 rows x 64 tokens per
  * workgroup; two K halves in one workgroup where the tiles alone would give
@@ -1752,7 +1770,7 @@ static int gemm_b32(const uint8_t* W, uint32_t rsz, int rows, int cols, const Pf
 int lg_prefill_act_type(int wtype)
 {
     switch (wtype) {
-    case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: return LG_Q8_K;
+    case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: case LG_Q6_K_R: return LG_Q8_K;
     case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: case LG_Q8_0_R: case LG_Q1_0_R: return LG_Q8_0;
     case LG_F32: case LG_F16: return LG_F32;
     default: return -1;
@@ -1767,6 +1785,7 @@ static int64_t pf_row_bytes(int wtype, int cols)
     case LG_Q4_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q4_K;
     case LG_Q5_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q5_K;
     case LG_Q6_K: return cols % 256 ? -1 : (int64_t)cols / 256 * LG_BS_Q6_K;
+    case LG_Q6_K_R: return cols % 2048 ? -1 : (int64_t)cols / 256 * LG_BS_Q6_K;
     case LG_Q8_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q8_0;
     case LG_Q1_0: return cols % 32 ? -1 : (int64_t)cols / 32 * LG_BS_Q1_0;
     /* regrouped rows: whole runs of 8 blocks */
@@ -1816,6 +1835,12 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
     case LG_Q6_K:
         if (!pf_gemm16()) return gemm_k32<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
         return gemm_kq<LG_Q6_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q6_K_R:
+        if (pf_gemm16()) {
+            lg_set_error("prefill gemm: regrouped Q6_K rows take the 32 x 32 kernel");
+            return LG_ERR_ARG;
+        }
+        return gemm_k32<LG_Q6_K_R>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q8_0: return gemm_b32<LG_Q8_0>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q8_0_R: return gemm_b32<LG_Q8_0_R>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q1_0_R: return gemm_b32<LG_Q1_0_R>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
