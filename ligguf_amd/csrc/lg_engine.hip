@@ -964,10 +964,10 @@ static void setup_prefill(lg_ctx* ctx, const lg_model_desc* m)
              * the batched GEMMs read those too (aligned 16-byte loads, the
              * same values) */
             const PkLayer& K = ctx->pk_layers[l];
-            const bool q6r = !lg_prefill_gemm16();   /* the 16 x 16 Q6_K kernel reads GGUF rows only */
+            const bool k32 = !lg_prefill_gemm16();   /* the 16 x 16 Q6_K and Q1_G kernels read GGUF rows only */
             auto rep = [&](PfMat& M, const uint8_t* w, int t) {
                 if ((M.type == LG_Q8_0 && t == LG_Q8_0_R) || (M.type == LG_Q1_0 && t == LG_Q1_0_R) ||
-                    (q6r && M.type == LG_Q6_K && t == LG_Q6_K_R)) {
+                    (k32 && M.type == LG_Q6_K && t == LG_Q6_K_R) || (k32 && M.type == LG_Q1_G && t == LG_Q1_G_R)) {
                     M.w = w;
                     M.type = t;
                 }

@@ -83,7 +83,7 @@ int lg_prefill_layers(const PfModel& M, PfBuffers& B, int T, int pos0, hipStream
 int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out,
                     int ldo, int accumulate, hipStream_t s);
 /* LG_PF_GEMM16=1 in the environment: the 16 x 16 int8-MFMA kernels (they
- * read regrouped Q8_0 / Q1_0 rows, Q6_K from the GGUF rows only) */
+ * read regrouped Q8_0 / Q1_0 rows, Q6_K and Q1_G from the GGUF rows only) */
 bool lg_prefill_gemm16();
 /* rmsnorm (norm_w != NULL) and the activation quantizer of qtype (LG_Q8_K,
  * n a multiple of 256, or LG_Q8_0, n a multiple of 32; LG_F32: the fp32

@@ -1585,12 +1585,19 @@ __global__ __launch_bounds__(512) void k_pf_gemm_b32(
  * per-token scale read from LDS.  out += (d_w d_a) s as k_pf_gemm_b32
  * (the same bits where K is not split).  Widths any multiple of 32: blocks
  * past the last of a step are not computed (their staged bytes are clamped
- * copies). */
+ * copies).
+ *
+ * Q1_G rows (WT = LG_Q1_G, LG_Q1_G_R): a 128-value block of sign bits with
+ * one fp16 d_w meets four activation blocks; with the bits as +-1 bytes s is
+ * dot_q8_0_q1_G's 2 s1 - asum, the scale MFMA puts d_a alone in place (B =
+ * 1), and out += d_w sum_j d_a,j s_j per 128 values in k_pf_gemm_q1g's fp32
+ * operations (the same bits where K is not split). */
 template <int WT, int ACC, int KS>
 __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm_b32x(
     const uint8_t* __restrict__ W, uint32_t rsz, int R, int K, PfQ8K x, int T, float* __restrict__ out, int ldo)
 {
-    using B32 = PfB32<WT>;
+    constexpr bool G = WT == LG_Q1_G || WT == LG_Q1_G_R;   /* 128-value sign blocks */
+    using B32 = PfB32<G ? LG_Q1_0 : WT>;
     constexpr int TT = 64;
     __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
     __shared__ __attribute__((aligned(16))) _Float16 s_d[KS][2][8][TT];   /* d_a per block of the step, per token */
@@ -1642,6 +1649,26 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
         uint32_t d[4];
     };
     auto blk_load = [&](Blk& B, int sp) __attribute__((always_inline)) {
+        if constexpr (G) {
+            /* the step's two Q1_G blocks 2 sp, 2 sp + 1 (K is a multiple of 256):
+             * bits 32 (e % 4) + 16h .. of block e / 4, and the two d_w */
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int qb = 2 * sp + (e >> 2);
+                const uint8_t* bits = WT == LG_Q1_G_R ? wr + (size_t)(qb >> 3) * 8 * LG_BS_Q1_G + 16 * (qb & 7)
+                                                      : wr + (size_t)qb * LG_BS_Q1_G + 2;
+                const uint32_t b16 = lg_ld16(bits + 4 * (e & 3) + 2 * h);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    B.q[e][k] = (int)(0xFFFFFFFFu ^ ((uint32_t)bits4_to_bytes((b16 >> (4 * k)) & 15u) * 0xFEu));
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int qb = 2 * sp + u;
+                B.d[u] = lg_ld16(WT == LG_Q1_G_R ? wr + (size_t)(qb >> 3) * 8 * LG_BS_Q1_G + 128 + 2 * (qb & 7)
+                                                 : wr + (size_t)qb * LG_BS_Q1_G);
+            }
+        } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int bk = min(8 * sp + e, nbk - 1);
@@ -1665,6 +1692,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
             for (int k = 0; k < 4; k++) B.d[k] = (uint32_t)dd[k];
         }
+        }
     };
 
     v16f acc[2];
@@ -1673,6 +1701,38 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 
     auto compute = [&](int buf, const Blk& cur, int sp) __attribute__((always_inline)) {
         const int8_t* sa = sa_[buf] + j * PF2_AST + 16 * h;
+        if constexpr (G) {
+            v8h one = (v8h){};
+            one[0] = h ? (_Float16)0.0f : (_Float16)1.0f;
+            /* per Q1_G block u and tile t: g = sum_j d_a,j s_j over its four
+             * activation blocks, then acc += d_w g */
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float dw = lg_h2f((uint16_t)cur.d[u]);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    v16f g = (v16f){};
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const int e = 4 * u + jj;
+                        /* never taken (K is a multiple of 256), but a branch per
+                         * block keeps the compiler from hoisting every block's
+                         * products at once: fully unrolled, they spilled */
+                        if (8 * sp + e >= nbk) break;
+                        const uint4 a = *(const uint4*)(sa + 32 * t * PF2_AST + 32 * e);
+                        const v4i af = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+                        const v16i is = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, cur.q[e], (v16i){}, 0, 0, 0);
+                        v8h ad = (v8h){};
+                        ad[0] = h ? (_Float16)0.0f : sd_[buf][e][32 * t + j];
+                        const v16f da = __builtin_amdgcn_mfma_f32_32x32x16_f16(ad, one, (v16f){}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) g[r] = __builtin_fmaf(da[r], (float)is[r], g[r]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[t][r] = __builtin_fmaf(dw, g[r], acc[t][r]);
+                }
+            }
+        } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             if (8 * sp + e >= nbk) break;   /* past the last block (uniform) */
@@ -1690,6 +1750,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[t][r] = __builtin_fmaf(sc[r], (float)is[r], acc[t][r]);
             }
+        }
         }
     };
 
@@ -1746,20 +1807,25 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
 }
 
 template <int WT>
+static int gemm_b32x(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
+                     int accumulate, hipStream_t s)
+{
+    const int nrb = (rows + PF2_RB - 1) / PF2_RB + 7 & ~7;
+    const int ntl = (T + 63) / 64;
+    const bool ks2 = nrb * ntl <= 256 && cols >= 4 * 256;
+    const dim3 grid((unsigned)(nrb * ntl)), blk(ks2 ? 2 * PF2_NT : PF2_NT);
+#define PF3_LAUNCH(A, N) hipLaunchKernelGGL((k_pf_gemm_b32x<WT, A, N>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo)
+    if (accumulate) { if (ks2) PF3_LAUNCH(1, 2); else PF3_LAUNCH(1, 1); }
+    else { if (ks2) PF3_LAUNCH(0, 2); else PF3_LAUNCH(0, 1); }
+#undef PF3_LAUNCH
+    return lg_check_launch("prefill gemm (32-value blocks)");
+}
+
+template <int WT>
 static int gemm_b32(const uint8_t* W, uint32_t rsz, int rows, int cols, const PfQ8K& x, int T, float* out, int ldo,
                     int accumulate, hipStream_t s)
 {
-    if (!pf_gemm16()) {
-        const int nrb = (rows + PF2_RB - 1) / PF2_RB + 7 & ~7;
-        const int ntl = (T + 63) / 64;
-        const bool ks2 = nrb * ntl <= 256 && cols >= 4 * 256;
-        const dim3 grid((unsigned)(nrb * ntl)), blk(ks2 ? 2 * PF2_NT : PF2_NT);
-#define PF3_LAUNCH(A, N) hipLaunchKernelGGL((k_pf_gemm_b32x<WT, A, N>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo)
-        if (accumulate) { if (ks2) PF3_LAUNCH(1, 2); else PF3_LAUNCH(1, 1); }
-        else { if (ks2) PF3_LAUNCH(0, 2); else PF3_LAUNCH(0, 1); }
-#undef PF3_LAUNCH
-        return lg_check_launch("prefill gemm (32-value blocks)");
-    }
+    if (!pf_gemm16()) return gemm_b32x<WT>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     const int nrb8 = (rows + 127) / 128 + 7 & ~7;
     const dim3 grid((unsigned)(nrb8 * ((T + 63) / 64))), blk(512);
     if (accumulate) hipLaunchKernelGGL((k_pf_gemm_b32<WT, 1>), grid, blk, 0, s, W, rsz, rows, cols, x, T, out, ldo);
@@ -1771,7 +1837,7 @@ int lg_prefill_act_type(int wtype)
 {
     switch (wtype) {
     case LG_Q2_K: case LG_Q3_K: case LG_Q4_K: case LG_Q5_K: case LG_Q6_K: case LG_Q6_K_R: return LG_Q8_K;
-    case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: case LG_Q8_0_R: case LG_Q1_0_R: return LG_Q8_0;
+    case LG_Q8_0: case LG_Q1_0: case LG_Q1_G: case LG_Q8_0_R: case LG_Q1_0_R: case LG_Q1_G_R: return LG_Q8_0;
     case LG_F32: case LG_F16: return LG_F32;
     default: return -1;
     }
@@ -1792,6 +1858,7 @@ static int64_t pf_row_bytes(int wtype, int cols)
     case LG_Q8_0_R: return cols % 256 ? -1 : (int64_t)cols / 32 * LG_BS_Q8_0;
     case LG_Q1_0_R: return cols % 256 ? -1 : (int64_t)cols / 32 * LG_BS_Q1_0;
     case LG_Q1_G: return cols % 256 ? -1 : (int64_t)cols / 128 * LG_BS_Q1_G;   /* the Q1_G GEMM steps 256 values */
+    case LG_Q1_G_R: return cols % 1024 ? -1 : (int64_t)cols / 128 * LG_BS_Q1_G;
     case LG_F32: return cols % 32 ? -1 : (int64_t)cols * 4;
     case LG_F16: return cols % 32 ? -1 : (int64_t)cols * 2;
     default: return -1;
@@ -1822,7 +1889,15 @@ int lg_prefill_gemm(int wtype, const uint8_t* W, uint32_t rsz, int rows, int col
     }
     switch (wtype) {
     case LG_Q4_K: return gemm_q4k(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
-    case LG_Q1_G: return gemm_q1g(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q1_G:
+        if (!pf_gemm16()) return gemm_b32x<LG_Q1_G>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+        return gemm_q1g(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
+    case LG_Q1_G_R:
+        if (pf_gemm16()) {
+            lg_set_error("prefill gemm: regrouped Q1_G rows take the 32 x 32 kernel");
+            return LG_ERR_ARG;
+        }
+        return gemm_b32x<LG_Q1_G_R>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
     case LG_Q2_K:
         if (!pf_gemm16()) return gemm_k32<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
         return gemm_kq<LG_Q2_K>(W, rsz, rows, cols, x, T, out, ldo, accumulate, s);
