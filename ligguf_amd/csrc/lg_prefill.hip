@@ -420,14 +420,12 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
                   "K-quant rows");
     /* LG_Q6_K_R: the fused decode step's regrouped Q6_K rows (per run of 8
      * blocks: their ql, qh, scales, d), the same values at aligned offsets */
-    constexpr bool Q6R = WT == LG_Q6_K_R;
     /* the mins term: Q4_K and Q5_K (32-value sub-blocks: pair sums of the
      * bsums, split 64 p_hi + p_lo) or Q2_K (16-value sub-blocks: the bsums) */
     constexpr int MK = (WT == LG_Q4_K || WT == LG_Q5_K) ? 1 : WT == LG_Q2_K ? 2 : 0;
     constexpr bool MINS = MK != 0;
     constexpr int BSZ = WT == LG_Q2_K ? LG_BS_Q2_K : WT == LG_Q3_K ? LG_BS_Q3_K : WT == LG_Q4_K ? LG_BS_Q4_K
                       : WT == LG_Q5_K ? LG_BS_Q5_K : LG_BS_Q6_K;
-    (void)Q6R;
     constexpr int TT = 64;   /* tokens per workgroup: two 32-token tiles per wave */
     __shared__ __attribute__((aligned(16))) int8_t s_a[KS][2][TT * PF2_AST];
     /* per token: p_hi[8], p_lo[8] or the 16 bsums (the mins term) */
@@ -478,8 +476,7 @@ __global__ __launch_bounds__(PF2_NT * KS) __attribute__((amdgpu_waves_per_eu(2))
             const int q = tid + PF2_NT * u;
             *(v4i*)(sa_[buf] + (q >> 4) * PF2_AST + (q & 15) * 16) = st.a[u];
         }
-        const int tok = tid >> 2;
-        (void)tok;
+        const int tok = tid >> 2;   /* bsums / mins of token tid / 4 */
         if constexpr (MK == 2) {
             const v4h m = {(_Float16)(float)(int16_t)(st.bs.x & 0xffff), (_Float16)(float)(int16_t)(st.bs.x >> 16),
                            (_Float16)(float)(int16_t)(st.bs.y & 0xffff), (_Float16)(float)(int16_t)(st.bs.y >> 16)};
